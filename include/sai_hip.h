@@ -1,0 +1,189 @@
+/*
+ * libsai_hip -- C ABI of the MI355X (gfx950) compressed-KV
+ * GroupQueryAttention path.
+ *
+ * This is the drop-in boundary for SmallAIOS onnx-rt's
+ * com.microsoft.GroupQueryAttention with fused rotary embedding over a
+ * quantised, paged KV cache. Plain C: integers, floats and raw pointers only.
+ * Every device pointer is caller-owned unless a function says otherwise; no
+ * C++ exception crosses the boundary; every call is asynchronous on the given
+ * HIP stream (void* = hipStream_t, NULL = the null stream) unless documented
+ * as synchronous.
+ *
+ * Each entry point names the reference interface it replaces
+ * (paths relative to the SmallAIOS workspace root).
+ *
+ * Threading: a sai_ctx and the caches created from it are thread-compatible,
+ * not thread-safe. The reference holds its cache behind Arc<Mutex<_>>
+ * (onnx-rt/src/session.rs:377); callers do the same.
+ */
+#ifndef SAI_HIP_H
+#define SAI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. The negative codes mirror the reference's error variants:
+ * OpError::{InvalidAttribute, ShapeMismatch, UnsupportedOp}
+ * (onnx-rt/src/operators.rs:26-37) and CudaError::{RuntimeError, AllocFailed}
+ * plus the cache's "position_overflow" (onnx-rt/src/cuda/kv_cache.rs:245-250). */
+typedef int32_t sai_status;
+#define SAI_OK 0
+#define SAI_ERR_INVALID_ATTRIBUTE (-1)
+#define SAI_ERR_SHAPE_MISMATCH (-2)
+#define SAI_ERR_UNSUPPORTED (-3)
+#define SAI_ERR_HIP (-4)
+#define SAI_ERR_ALLOC (-5)
+#define SAI_ERR_OVERFLOW (-6)
+#define SAI_ERR_NULL (-7)
+
+/* Element types, numbered as the reference's DataType / ONNX TensorProto
+ * (onnx-rt/src/tensor.rs). */
+#define SAI_DTYPE_F32 1
+#define SAI_DTYPE_F16 10
+#define SAI_DTYPE_BF16 16
+
+/* KV quantisation schemes.
+ * INT8: symmetric, one f32 scale per (token, kv head): s = amax/127 (1.0 when
+ *       amax == 0), code = clamp(round_half_even(x/s), -128, 127)
+ *       (QuantizeLinear semantics, onnx-rt/src/ops/quantized.rs:115-164).
+ * INT4: asymmetric per (token, kv head, group of 32 along head_dim): min/max
+ *       quantiser of onnx-rt/src/kv_compression.rs:223-253 with levels 15,
+ *       scale and zero point stored as IEEE binary16, codes packed LSB-first
+ *       (kv_compression.rs:294-312). */
+#define SAI_KV_INT8 1
+#define SAI_KV_INT4 2
+
+/* Tokens per cache page. */
+#define SAI_PAGE_TOKENS 16
+
+typedef struct sai_ctx sai_ctx;
+typedef struct sai_kvcache sai_kvcache;
+
+/* ---- runtime --------------------------------------------------------------
+ * Replaces CudaRuntime::new / drop (onnx-rt/src/cuda/mod.rs:619-700). */
+sai_status sai_init(int device, sai_ctx** out);
+void sai_destroy(sai_ctx* ctx);
+/* Message of the last failed call on ctx ("" if none). Valid until the next
+ * call on ctx. Replaces the Display of CudaError/OpError. */
+const char* sai_last_error(const sai_ctx* ctx);
+/* 1 / sqrt(head_dim) computed exactly as the reference's default GQA scale
+ * (Newton sqrt_f32, onnx-rt/src/ops/microsoft.rs:54-63 and :1153). */
+float sai_default_scale(int32_t head_dim);
+/* Device kernels are compiled for gfx950 only; returns 1 when `device` is one. */
+int32_t sai_device_supported(int device);
+
+/* ---- paged quantised KV cache ---------------------------------------------
+ * Replaces GpuKvCache (onnx-rt/src/cuda/kv_cache.rs:111-390). Differences by
+ * design: pages of SAI_PAGE_TOKENS tokens behind a per-sequence page table
+ * instead of one linear [max_seq, Hkv, D] buffer, a committed length per
+ * sequence instead of one current_position, and int8/int4 codes instead of
+ * bf16. Lifecycle is the reference's: append (pending, not committed) ->
+ * attention sees committed + pending tokens (view_pending, kv_cache.rs:320) ->
+ * advance once per forward pass (advance_position, kv_cache.rs:295). */
+typedef struct sai_kvcache_desc {
+  int32_t num_layers;
+  int32_t num_kv_heads;
+  int32_t head_dim;          /* 64 or 128 */
+  int32_t num_pages;         /* physical pages per layer */
+  int32_t max_batch;         /* sequences */
+  int32_t max_pages_per_seq; /* page-table width */
+  int32_t quant;             /* SAI_KV_INT8 or SAI_KV_INT4 */
+} sai_kvcache_desc;
+
+/* Allocates num_layers pools of num_pages pages (zero-filled, as
+ * GpuKvCache::allocate zero-fills, kv_cache.rs:176-179). Synchronous.
+ * Errors: SHAPE_MISMATCH for zero/unsupported dims (kv_cache_allocate:zero_dim),
+ * ALLOC when device memory runs out. */
+sai_status sai_kvcache_create(sai_ctx* ctx, const sai_kvcache_desc* desc, sai_kvcache** out);
+void sai_kvcache_destroy(sai_kvcache* cache);
+
+/* Page table for `batch` sequences, host array [batch][max_pages_per_seq] of
+ * physical page ids in [0, num_pages), or -1 for an unmapped slot. Every entry
+ * is validated on the host. Synchronous. Resets all lengths to 0. */
+sai_status sai_kvcache_set_page_table(sai_ctx* ctx, sai_kvcache* cache, const int32_t* page_table,
+                                      int32_t batch);
+/* Committed lengths (host array [batch]); clears pending tokens. Synchronous. */
+sai_status sai_kvcache_set_seq_lens(sai_ctx* ctx, sai_kvcache* cache, const int32_t* seq_lens,
+                                    int32_t batch);
+/* Commit the pending tokens of the current forward pass: every committed
+ * length grows by the pending count. Stream-ordered. Replaces
+ * GpuKvCache::advance_position (kv_cache.rs:295-304). */
+sai_status sai_kvcache_advance(sai_ctx* ctx, sai_kvcache* cache, void* stream);
+/* All lengths back to 0, buffers kept (GpuKvCache::reset, kv_cache.rs:386-388). */
+sai_status sai_kvcache_reset(sai_ctx* ctx, sai_kvcache* cache);
+/* Host view of the lengths: seq_lens_out[batch] (committed), *pending_out. */
+sai_status sai_kvcache_lengths(const sai_kvcache* cache, int32_t* seq_lens_out,
+                               int32_t* pending_out, int32_t* batch_out);
+/* Copy n_tokens tokens [t0, t0+n_tokens) of (sequence b, kv head h, layer) out
+ * of the pages into host buffers in logical order. Synchronous (debug,
+ * checkpoint and tests). INT8: k/v_codes int8 [n][D], k/v_params f32 [n]
+ * scales. INT4: k/v_codes u8 [n][D/2] packed LSB-first along D, k/v_params
+ * u16 [n][D/32][2] binary16 (scale, zero). */
+sai_status sai_kvcache_read(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, int32_t b,
+                            int32_t kv_head, int32_t t0, int32_t n_tokens, void* k_codes,
+                            void* v_codes, void* k_params, void* v_params);
+/* Raw pool of one layer (device pointer and size in bytes) and the bytes of
+ * one (page, kv head) block; the block layout is documented in DESIGN.md. */
+sai_status sai_kvcache_pool(const sai_kvcache* cache, int32_t layer, void** dev_ptr,
+                            size_t* bytes, size_t* block_bytes);
+
+/* ---- kernel 1: RoPE + quantise + pack append --------------------------------
+ * Replaces GpuKvCache::append (kv_cache.rs:233-278) fused with the K half of
+ * gqa_apply_rotary (onnx-rt/src/ops/microsoft.rs:1004-1052) and the
+ * QuantizeLinear of the KV scheme. k, v: device [batch, s_new, Hkv*D] of
+ * `dtype` (F32 or BF16), pre-RoPE K. Token s of sequence b goes to position
+ * seq_len[b] + s; RoPE (when do_rotary) uses that position in cos/sin
+ * ([cache_rows, D/2] f32, device). Leaves s_new tokens pending; the same
+ * s_new must be used for every layer of a forward pass, and appending a layer
+ * twice before advance rewrites the same slots.
+ * Errors: SHAPE_MISMATCH (dims, unmapped page, position >= cache_rows),
+ * OVERFLOW (past the page table), UNSUPPORTED (dtype/head_dim). */
+sai_status sai_kv_append(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* k,
+                         const void* v, int32_t dtype, int32_t batch, int32_t s_new,
+                         const float* cos_cache, const float* sin_cache, int32_t cache_rows,
+                         int32_t do_rotary, int32_t rotary_interleaved, void* stream);
+
+/* ---- kernel 2: split-K flash decode -----------------------------------------
+ * Replaces gpu_gqa_with_cache (onnx-rt/src/cuda/kernels/attention.rs:1260-1295)
+ * and, for Sq == 1, op_group_query_attention's attention half
+ * (onnx-rt/src/ops/microsoft.rs:1082-1190): RoPE on Q at position
+ * seq_len[b] + pending - 1, causal attention over the committed + pending
+ * tokens of each sequence (ragged lengths allowed), GQA head grouping
+ * kh = qh / (Hq/Hkv). Requires pending == 1.
+ * q: device [batch, 1, num_heads*D] of `dtype` (F32 or BF16);
+ * out: device [batch, 1, num_heads*D] f32. scale: used when has_scale != 0,
+ * else sai_default_scale(D). */
+sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
+                          int32_t dtype, int32_t batch, int32_t num_heads,
+                          const float* cos_cache, const float* sin_cache, int32_t cache_rows,
+                          int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
+                          float scale, float* out, void* stream);
+
+/* ---- kernel 3: prefill chunk (bf16/f16 MFMA) ---------------------------------
+ * Same contract as sai_gqa_decode for a chunk of sq == pending query tokens per
+ * sequence (the reference's op_group_query_attention with Sq > 1, causal with
+ * past_sk = seq_len[b], microsoft.rs:1156 and :331-337).
+ * q: device [batch, sq, num_heads*D]; out: device [batch, sq, num_heads*D] f32. */
+sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
+                           int32_t dtype, int32_t batch, int32_t sq, int32_t num_heads,
+                           const float* cos_cache, const float* sin_cache, int32_t cache_rows,
+                           int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
+                           float scale, float* out, void* stream);
+
+/* ---- tuning / introspection ------------------------------------------------- */
+/* Tokens per split-K work item of the decode kernel (0 = automatic, else a
+ * multiple of 64). Returns the previous value. */
+int32_t sai_set_decode_split(sai_ctx* ctx, int32_t tokens);
+/* Number of workgroups and split size of the last decode launch on ctx. */
+sai_status sai_last_decode_shape(const sai_ctx* ctx, int32_t* workgroups, int32_t* split_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAI_HIP_H */

@@ -1,0 +1,123 @@
+/*
+ * CPU oracle for the compressed-KV GroupQueryAttention path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker: tests/, the smoke
+ * entry and the CPU-baseline leg of bench.py load it. The product library
+ * (smallaios_amd/libsai_hip.so) never links, loads or calls it.
+ *
+ * It restates, op for op, the reference's Rust CPU semantics
+ * (SmallAIOS onnx-rt, workspace 0.2.1). Every function cites the file:line
+ * it follows. Arithmetic is plain IEEE f32 without contraction
+ * (built with -ffp-contract=off -fno-fast-math), matching Rust, which never
+ * fuses multiply-add on its own.
+ *
+ * Layout conventions (all little-endian, row-major):
+ *   Q   [B, Sq, Hq*D]   K/V new [B, Sq, Hkv*D]   (ORT "BSH")
+ *   past/present K/V [B, Hkv, S, D]               (ORT "BHSD")
+ *   int8 cache codes [B, Hkv, T, D] int8, scales [B, Hkv, T] f32
+ *   int4 cache codes [B, Hkv, T, D/2] u8 (pack_bits LSB-first along D),
+ *        scale/zero [B, Hkv, T, D/32] f16 bits
+ *
+ * Return codes of the int functions: 0 ok, -1 InvalidAttribute,
+ * -2 ShapeMismatch (the reference's OpError variants, operators.rs:26-37).
+ */
+#ifndef SAI_ORACLE_H
+#define SAI_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* --- scalar numerics --------------------------------------------------- */
+float sai_or_expf_approx(float x);
+float sai_or_sqrt_f32(float x);
+float sai_or_sqrt_approx(float x);
+float sai_or_round_half_even(float x);
+float sai_or_round_f32_kv(float x);
+int32_t sai_or_sat_i32(float x);
+uint32_t sai_or_sat_u32(float x);
+int64_t sai_or_sat_i64(float x);
+uint16_t sai_or_f32_to_bf16(float x);
+float sai_or_bf16_to_f32(uint16_t b);
+uint16_t sai_or_f32_to_f16(float x);
+float sai_or_f16_to_f32(uint16_t h);
+void sai_or_f32_to_f16_array(const float* x, size_t n, uint16_t* out);
+void sai_or_round_half_even_array(const float* x, size_t n, float* out);
+void sai_or_expf_approx_array(const float* x, size_t n, float* out);
+float sai_or_default_scale(int head_dim);
+
+/* --- bit packing ------------------------------------------------------- */
+void sai_or_pack_bits(const uint32_t* values, size_t n, int bits, uint8_t* out);
+void sai_or_unpack_bits(const uint8_t* data, size_t nbytes, size_t count, int bits,
+                        uint32_t* out);
+
+/* --- RoPE / SDPA / GQA (f32 reference op) ------------------------------ */
+int sai_or_apply_rope(float* x, int b, int heads, int sq, int head_dim, const float* cos_cache,
+                      const float* sin_cache, int cache_rows, int cache_cols,
+                      const int64_t* position_ids, int n_pos, int interleaved, int rotary_dim);
+
+int sai_or_sdpa(const float* q, const float* k, const float* v, int batch, int num_q_heads,
+                int num_kv_heads, int sq, int sk, int head_dim, int past_sk, float scale,
+                int causal, float* out);
+
+/* op_group_query_attention. past_k/past_v may be NULL (past_sk must then be 0).
+ * scale_attr: used when has_scale != 0. Outputs: attn [B,Sq,Hq*D],
+ * present_k/present_v [B,Hkv,past_sk+Sq,D]. */
+int sai_or_gqa(const float* query, const float* key, const float* value, int b, int sq,
+               int q_hidden, int kv_hidden, const float* past_k, const float* past_v,
+               int past_sk, const float* cos_cache, const float* sin_cache, int cache_rows,
+               int cache_cols, int num_heads, int kv_num_heads, int has_scale, float scale_attr,
+               int local_window_size, int do_rotary, int rotary_interleaved, float* attn_out,
+               float* present_k, float* present_v);
+
+/* --- composed KV quantisation spec ------------------------------------- */
+void sai_or_quant_int8_row(const float* x, int d, int8_t* codes, float* scale);
+void sai_or_dequant_int8_row(const int8_t* codes, float scale, int d, float* out);
+void sai_or_quant_int4_row(const float* x, int d, uint8_t* packed, uint16_t* scale_f16,
+                           uint16_t* zero_f16);
+void sai_or_dequant_int4_row(const uint8_t* packed, const uint16_t* scale_f16,
+                             const uint16_t* zero_f16, int d, float* out);
+
+/* --- composed quantized-cache step (the oracle of the HIP path) --------- */
+/* KV append: for every (b, s, kvh) row of the new K/V ([B,S_new,Hkv*D] f32),
+ * apply RoPE to K at position start_pos[b]+s (when do_rotary), quantize K and V
+ * with the chosen spec and write codes/params at token index start_pos[b]+s of
+ * the logical cache (capacity t_cap tokens per (b, kvh)).
+ * quant: 1 = int8 sym per (token, head), 2 = int4 asym per group of 32. */
+int sai_or_kv_append(const float* k_new, const float* v_new, int b, int s_new, int kv_heads,
+                     int head_dim, const int32_t* start_pos, const float* cos_cache,
+                     const float* sin_cache, int cache_rows, int do_rotary, int interleaved,
+                     int quant, int t_cap, void* k_codes, void* v_codes, float* k_scale,
+                     float* v_scale, uint16_t* k_sz, uint16_t* v_sz);
+
+/* Dequantise the first seq_len[b] tokens of every (b, kvh) into f32
+ * [B, Hkv, t_cap, D] (rows beyond seq_len are left untouched). */
+int sai_or_kv_dequant(int b, int kv_heads, int head_dim, int quant, int t_cap,
+                      const int32_t* seq_len, const void* k_codes, const void* v_codes,
+                      const float* k_scale, const float* v_scale, const uint16_t* k_sz,
+                      const uint16_t* v_sz, float* k_out, float* v_out);
+
+/* Attention over the dequantised cache (new tokens already appended):
+ * query [B, Sq, Hq*D] f32 (pre-RoPE), seq_len[b] = total keys for batch b
+ * (past + Sq). Q is rotated at positions seq_len[b]-Sq+i, then causal SDPA
+ * with past_sk = seq_len[b]-Sq. Per-batch, because ragged batches have a
+ * different past_sk per sequence. out [B, Sq, Hq*D] f32. */
+int sai_or_gqa_cached(const float* query, int b, int sq, int num_heads, int kv_heads,
+                      int head_dim, const int32_t* seq_len, int t_cap, const float* k_deq,
+                      const float* v_deq, const float* cos_cache, const float* sin_cache,
+                      int cache_rows, int do_rotary, int interleaved, int has_scale,
+                      float scale_attr, float* out);
+
+/* Exhaustive check that the int8 code rule built on round_half_even equals
+ * the same rule built on IEEE roundTiesToEven (rintf) for every f32 bit
+ * pattern u in [lo, hi) (hi <= 2^32). Returns the number of mismatches. */
+uint64_t sai_or_check_rhe_vs_rint(uint64_t lo, uint64_t hi);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

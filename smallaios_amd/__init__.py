@@ -1,0 +1,299 @@
+"""smallaios_amd -- MI355X (gfx950) compressed-KV GroupQueryAttention path.
+
+Python binding (ctypes) of ``libsai_hip.so``, the C ABI declared in
+``include/sai_hip.h``. Device buffers are passed as raw pointers; torch
+tensors on ``cuda`` are accepted for convenience (torch is only used for
+device memory and streams). Importing this package never falls back to a CPU
+implementation: if the library is missing every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsai_hip.so")
+
+SAI_OK = 0
+STATUS_NAMES = {
+    -1: "InvalidAttribute", -2: "ShapeMismatch", -3: "Unsupported", -4: "HipError",
+    -5: "AllocFailed", -6: "PositionOverflow", -7: "NullArgument",
+}
+DTYPE_F32 = 1
+DTYPE_F16 = 10
+DTYPE_BF16 = 16
+KV_INT8 = 1
+KV_INT4 = 2
+PAGE_TOKENS = 16
+
+_lib = None
+
+
+class SaiError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.kind = STATUS_NAMES.get(status, f"status {status}")
+        super().__init__(f"{self.kind}: {message}")
+
+
+class _Desc(C.Structure):
+    _fields_ = [
+        ("num_layers", C.c_int32), ("num_kv_heads", C.c_int32), ("head_dim", C.c_int32),
+        ("num_pages", C.c_int32), ("max_batch", C.c_int32), ("max_pages_per_seq", C.c_int32),
+        ("quant", C.c_int32),
+    ]
+
+
+def lib() -> C.CDLL:
+    """Load libsai_hip.so (built in-tree by smallaios_amd/build.py)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python smallaios_amd/build.py` "
+                "(or __graft_entry__.build()); there is no CPU fallback")
+        L = C.CDLL(LIB_PATH)
+        _declare(L)
+        _lib = L
+    return _lib
+
+
+EXPORTS = [
+    "sai_init", "sai_destroy", "sai_last_error", "sai_default_scale", "sai_device_supported",
+    "sai_kvcache_create", "sai_kvcache_destroy", "sai_kvcache_set_page_table",
+    "sai_kvcache_set_seq_lens", "sai_kvcache_advance", "sai_kvcache_reset",
+    "sai_kvcache_lengths", "sai_kvcache_read", "sai_kvcache_pool", "sai_kv_append",
+    "sai_gqa_decode", "sai_gqa_prefill", "sai_set_decode_split", "sai_last_decode_shape",
+]
+
+
+def _declare(L: C.CDLL) -> None:
+    p, i32, f = C.c_void_p, C.c_int32, C.c_float
+    pp = C.POINTER(C.c_void_p)
+    sig = {
+        "sai_init": (i32, [C.c_int, pp]),
+        "sai_destroy": (None, [p]),
+        "sai_last_error": (C.c_char_p, [p]),
+        "sai_default_scale": (f, [i32]),
+        "sai_device_supported": (i32, [C.c_int]),
+        "sai_kvcache_create": (i32, [p, C.POINTER(_Desc), pp]),
+        "sai_kvcache_destroy": (None, [p]),
+        "sai_kvcache_set_page_table": (i32, [p, p, p, i32]),
+        "sai_kvcache_set_seq_lens": (i32, [p, p, p, i32]),
+        "sai_kvcache_advance": (i32, [p, p, p]),
+        "sai_kvcache_reset": (i32, [p, p]),
+        "sai_kvcache_lengths": (i32, [p, p, p, p]),
+        "sai_kvcache_read": (i32, [p, p, i32, i32, i32, i32, i32, p, p, p, p]),
+        "sai_kvcache_pool": (i32, [p, i32, pp, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+        "sai_kv_append": (i32, [p, p, i32, p, p, i32, i32, i32, p, p, i32, i32, i32, p]),
+        "sai_gqa_decode": (i32, [p, p, i32, p, i32, i32, i32, p, p, i32, i32, i32, i32, f, p,
+                                 p]),
+        "sai_gqa_prefill": (i32, [p, p, i32, p, i32, i32, i32, i32, p, p, i32, i32, i32, i32,
+                                  f, p, p]),
+        "sai_set_decode_split": (i32, [p, i32]),
+        "sai_last_decode_shape": (i32, [p, C.POINTER(i32), C.POINTER(i32)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def default_scale(head_dim: int) -> float:
+    return float(lib().sai_default_scale(head_dim))
+
+
+def rope_tables(max_seq: int, head_dim: int, theta: float):
+    """cos/sin caches [max_seq, head_dim/2] f32 (the op's cos_cache/sin_cache
+    inputs): theta^(-2i/D) and cos/sin of pos * inv_freq in f64, rounded once."""
+    half = head_dim // 2
+    inv = theta ** (-(2.0 * np.arange(half, dtype=np.float64)) / head_dim)
+    ang = np.arange(max_seq, dtype=np.float64)[:, None] * inv[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def _dev_ptr(x):
+    """Raw device pointer of a torch tensor / int / None."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def _dtype_code(x, default=DTYPE_F32):
+    try:
+        import torch
+        if isinstance(x, torch.Tensor):
+            return {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16,
+                    torch.float16: DTYPE_F16}[x.dtype]
+    except ImportError:  # pragma: no cover
+        pass
+    return default
+
+
+def _stream(stream):
+    if stream is None:
+        try:
+            import torch
+            return torch.cuda.current_stream().cuda_stream
+        except Exception:  # pragma: no cover
+            return None
+    return stream if isinstance(stream, int) else stream.cuda_stream
+
+
+class Runtime:
+    """sai_ctx: one per device."""
+
+    def __init__(self, device: int = 0):
+        self._L = lib()
+        h = C.c_void_p()
+        st = self._L.sai_init(device, C.byref(h))
+        if st != SAI_OK:
+            raise SaiError(st, f"sai_init({device})")
+        self.handle = h
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            self._L.sai_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def last_error(self) -> str:
+        return self._L.sai_last_error(self.handle).decode()
+
+    def check(self, st: int, what: str):
+        if st != SAI_OK:
+            raise SaiError(st, f"{what}: {self.last_error()}")
+
+    def set_decode_split(self, tokens: int) -> int:
+        return int(self._L.sai_set_decode_split(self.handle, tokens))
+
+    def last_decode_shape(self):
+        wg, sp = C.c_int32(), C.c_int32()
+        self._L.sai_last_decode_shape(self.handle, C.byref(wg), C.byref(sp))
+        return wg.value, sp.value
+
+
+class KvCache:
+    """sai_kvcache: paged int8/int4 KV cache (mirror of the reference's GpuKvCache)."""
+
+    def __init__(self, rt: Runtime, num_layers, num_kv_heads, head_dim, num_pages, max_batch,
+                 max_pages_per_seq, quant=KV_INT8):
+        self.rt = rt
+        self._L = rt._L
+        self.desc = _Desc(num_layers, num_kv_heads, head_dim, num_pages, max_batch,
+                          max_pages_per_seq, quant)
+        h = C.c_void_p()
+        rt.check(self._L.sai_kvcache_create(rt.handle, C.byref(self.desc), C.byref(h)),
+                 "kvcache_create")
+        self.handle = h
+        self.num_layers, self.kv_heads, self.head_dim = num_layers, num_kv_heads, head_dim
+        self.quant = quant
+        self.max_pages_per_seq = max_pages_per_seq
+
+    def close(self):
+        if self.handle:
+            self._L.sai_kvcache_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_page_table(self, table):
+        t = np.ascontiguousarray(table, dtype=np.int32)
+        assert t.ndim == 2 and t.shape[1] == self.max_pages_per_seq
+        self.rt.check(self._L.sai_kvcache_set_page_table(
+            self.rt.handle, self.handle, t.ctypes.data_as(C.c_void_p), t.shape[0]),
+            "set_page_table")
+        self.batch = t.shape[0]
+
+    def set_seq_lens(self, lens):
+        a = np.ascontiguousarray(lens, dtype=np.int32)
+        self.rt.check(self._L.sai_kvcache_set_seq_lens(
+            self.rt.handle, self.handle, a.ctypes.data_as(C.c_void_p), a.size), "set_seq_lens")
+
+    def advance(self, stream=None):
+        self.rt.check(self._L.sai_kvcache_advance(self.rt.handle, self.handle, _stream(stream)),
+                      "advance")
+
+    def reset(self):
+        self.rt.check(self._L.sai_kvcache_reset(self.rt.handle, self.handle), "reset")
+
+    def lengths(self):
+        b = C.c_int32()
+        pend = C.c_int32()
+        self._L.sai_kvcache_lengths(self.handle, None, C.byref(pend), C.byref(b))
+        out = np.zeros(max(b.value, 1), dtype=np.int32)
+        self._L.sai_kvcache_lengths(self.handle, out.ctypes.data_as(C.c_void_p), None, None)
+        return out[: b.value], pend.value
+
+    def pool(self, layer: int):
+        ptr, nbytes, bb = C.c_void_p(), C.c_size_t(), C.c_size_t()
+        st = self._L.sai_kvcache_pool(self.handle, layer, C.byref(ptr), C.byref(nbytes),
+                                      C.byref(bb))
+        if st != SAI_OK:
+            raise SaiError(st, "kvcache_pool")
+        return ptr.value, nbytes.value, bb.value
+
+    def read(self, layer, b, kv_head, t0, n):
+        """Codes/params of tokens [t0, t0+n) in logical order (synchronous)."""
+        D = self.head_dim
+        if self.quant == KV_INT8:
+            kc = np.zeros((n, D), np.int8)
+            vc = np.zeros((n, D), np.int8)
+            kp = np.zeros(n, np.float32)
+            vp = np.zeros(n, np.float32)
+        else:
+            kc = np.zeros((n, D // 2), np.uint8)
+            vc = np.zeros((n, D // 2), np.uint8)
+            kp = np.zeros((n, D // 32, 2), np.uint16)
+            vp = np.zeros((n, D // 32, 2), np.uint16)
+        ptr = lambda a: a.ctypes.data_as(C.c_void_p)
+        self.rt.check(self._L.sai_kvcache_read(self.rt.handle, self.handle, layer, b, kv_head, t0,
+                                               n, ptr(kc), ptr(vc), ptr(kp), ptr(vp)),
+                      "kvcache_read")
+        return kc, vc, kp, vp
+
+    # ---- kernels ----------------------------------------------------------
+    def append(self, layer, k, v, batch, s_new, cos=None, sin=None, cache_rows=0,
+               do_rotary=True, interleaved=False, stream=None, dtype=None):
+        dt = dtype if dtype is not None else _dtype_code(k)
+        self.rt.check(self._L.sai_kv_append(
+            self.rt.handle, self.handle, layer, _dev_ptr(k), _dev_ptr(v), dt, batch, s_new,
+            _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary), int(interleaved),
+            _stream(stream)), "kv_append")
+
+    def decode(self, layer, q, out, batch, num_heads, cos=None, sin=None, cache_rows=0,
+               do_rotary=True, interleaved=False, scale=None, stream=None, dtype=None):
+        dt = dtype if dtype is not None else _dtype_code(q)
+        self.rt.check(self._L.sai_gqa_decode(
+            self.rt.handle, self.handle, layer, _dev_ptr(q), dt, batch, num_heads, _dev_ptr(cos),
+            _dev_ptr(sin), cache_rows, int(do_rotary), int(interleaved), int(scale is not None),
+            0.0 if scale is None else float(scale), _dev_ptr(out), _stream(stream)),
+            "gqa_decode")
+
+    def prefill(self, layer, q, out, batch, sq, num_heads, cos=None, sin=None, cache_rows=0,
+                do_rotary=True, interleaved=False, scale=None, stream=None, dtype=None):
+        dt = dtype if dtype is not None else _dtype_code(q)
+        self.rt.check(self._L.sai_gqa_prefill(
+            self.rt.handle, self.handle, layer, _dev_ptr(q), dt, batch, sq, num_heads,
+            _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary), int(interleaved),
+            int(scale is not None), 0.0 if scale is None else float(scale), _dev_ptr(out),
+            _stream(stream)), "gqa_prefill")
+
+
+def identity_page_table(batch: int, pages_per_seq: int):
+    """Sequence b owns pages [b*pages_per_seq, (b+1)*pages_per_seq)."""
+    return np.arange(batch * pages_per_seq, dtype=np.int32).reshape(batch, pages_per_seq)

@@ -1,0 +1,605 @@
+// C ABI of libsai_hip (declared in include/sai_hip.h).
+//
+// Host-side responsibilities: argument and shape validation with the
+// reference's error kinds, the host mirror of page table and lengths (every
+// page id and position a kernel will touch is checked here before launch),
+// workspace management and kernel dispatch. No exception leaves this file.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/sai_hip.h"
+#include "sai_internal.h"
+
+#define SAI_API extern "C" __attribute__((visibility("default")))
+
+struct sai_ctx {
+  int device = 0;
+  int num_cus = 0;
+  std::string err;
+  float* partials = nullptr;
+  size_t partial_floats = 0;
+  int32_t* counters = nullptr;
+  size_t counter_n = 0;
+  int32_t decode_split = 0;  // 0 = automatic
+  int32_t last_wg = 0;
+  int32_t last_split = 0;
+};
+
+struct sai_kvcache {
+  sai_kvcache_desc desc{};
+  size_t block_bytes = 0;
+  size_t pool_bytes = 0;
+  std::vector<uint8_t*> pools;
+  int32_t* d_page_table = nullptr;
+  int32_t* d_seq_lens = nullptr;
+  std::vector<int32_t> h_page_table;  // [max_batch][max_pages_per_seq]
+  std::vector<int32_t> h_mapped;      // leading mapped pages per sequence
+  std::vector<int32_t> h_seq_lens;    // committed
+  int32_t batch = 0;
+  int32_t pending = 0;
+};
+
+namespace {
+
+sai_status fail(sai_ctx* ctx, sai_status code, const char* fmt, ...) {
+  if (ctx) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    ctx->err = buf;
+  }
+  return code;
+}
+
+sai_status hip_fail(sai_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, SAI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Newton square root of the reference (onnx-rt/src/ops/microsoft.rs:54-63);
+// the default GQA scale is 1 / sqrt_f32(head_dim) (microsoft.rs:1153).
+float sqrt_f32_newton(float x) {
+  if (x <= 0.0f) return 0.0f;
+  volatile float guess = x;  // keep every step in f32, unfused
+  for (int i = 0; i < 16; ++i) {
+    volatile float q = x / guess;
+    volatile float s = guess + q;
+    guess = 0.5f * s;
+  }
+  return guess;
+}
+
+bool supported_dims(int head_dim, int quant) {
+  if (head_dim != 64 && head_dim != 128) return false;
+  return quant == SAI_KV_INT8 || quant == SAI_KV_INT4;
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) == hipSuccess && prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+// Common checks before a kernel touches the pages of positions [0, len_b).
+sai_status check_lengths(sai_ctx* ctx, const sai_kvcache* c, int32_t batch, int32_t extra,
+                         const char* op) {
+  if (batch <= 0 || batch != c->batch)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                "%s: batch %d does not match the cache's page table batch %d", op, batch,
+                c->batch);
+  const int64_t cap = (int64_t)c->desc.max_pages_per_seq * SAI_PAGE_TOKENS;
+  for (int i = 0; i < batch; ++i) {
+    const int64_t len = (int64_t)c->h_seq_lens[i] + extra;
+    if (len > cap)
+      return fail(ctx, SAI_ERR_OVERFLOW, "%s: position_overflow (sequence %d needs %lld > %lld)",
+                  op, i, (long long)len, (long long)cap);
+    const int64_t pages = (len + SAI_PAGE_TOKENS - 1) / SAI_PAGE_TOKENS;
+    if (pages > c->h_mapped[i])
+      return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                  "%s: sequence %d needs %lld pages but only %d leading pages are mapped", op, i,
+                  (long long)pages, c->h_mapped[i]);
+  }
+  return SAI_OK;
+}
+
+sai_status check_rope(sai_ctx* ctx, const sai_kvcache* c, int32_t batch, int32_t extra,
+                      const float* cos_cache, const float* sin_cache, int32_t cache_rows,
+                      int32_t do_rotary, const char* op) {
+  if (!do_rotary) return SAI_OK;
+  if (!cos_cache || !sin_cache)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: do_rotary=1 but cos_cache/sin_cache is missing",
+                op);
+  int32_t maxlen = 0;
+  for (int i = 0; i < batch; ++i) maxlen = std::max(maxlen, c->h_seq_lens[i] + extra);
+  if (maxlen > cache_rows)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: position %d out of cache range %d", op,
+                maxlen - 1, cache_rows);
+  return SAI_OK;
+}
+
+sai_status ensure_workspace(sai_ctx* ctx, size_t partial_floats, size_t counters) {
+  if (partial_floats > ctx->partial_floats) {
+    if (ctx->partials) (void)hipFree(ctx->partials);
+    ctx->partials = nullptr;
+    ctx->partial_floats = 0;
+    size_t n = std::max(partial_floats, (size_t)1 << 20);
+    hipError_t e = hipMalloc(&ctx->partials, n * sizeof(float));
+    if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "decode workspace: %s", hipGetErrorString(e));
+    ctx->partial_floats = n;
+  }
+  if (counters > ctx->counter_n) {
+    if (ctx->counters) (void)hipFree(ctx->counters);
+    ctx->counters = nullptr;
+    ctx->counter_n = 0;
+    size_t n = std::max(counters, (size_t)4096);
+    hipError_t e = hipMalloc(&ctx->counters, n * sizeof(int32_t));
+    if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "decode counters: %s", hipGetErrorString(e));
+    e = hipMemset(ctx->counters, 0, n * sizeof(int32_t));
+    if (e != hipSuccess) return hip_fail(ctx, e, "decode counters memset");
+    ctx->counter_n = n;
+  }
+  return SAI_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- runtime ---
+SAI_API sai_status sai_init(int device, sai_ctx** out) {
+  if (!out) return SAI_ERR_NULL;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return SAI_ERR_HIP;
+  sai_ctx* ctx = new (std::nothrow) sai_ctx();
+  if (!ctx) return SAI_ERR_ALLOC;
+  ctx->device = device;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) ctx->num_cus = prop.multiProcessorCount;
+  if (ctx->num_cus <= 0) ctx->num_cus = 256;
+  *out = ctx;
+  return SAI_OK;
+}
+
+SAI_API void sai_destroy(sai_ctx* ctx) {
+  if (!ctx) return;
+  DeviceGuard dg(ctx->device);
+  if (ctx->partials) (void)hipFree(ctx->partials);
+  if (ctx->counters) (void)hipFree(ctx->counters);
+  delete ctx;
+}
+
+SAI_API const char* sai_last_error(const sai_ctx* ctx) { return ctx ? ctx->err.c_str() : ""; }
+
+SAI_API float sai_default_scale(int32_t head_dim) {
+  return 1.0f / sqrt_f32_newton((float)head_dim);
+}
+
+SAI_API int32_t sai_device_supported(int device) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return 0;
+  return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+SAI_API int32_t sai_set_decode_split(sai_ctx* ctx, int32_t tokens) {
+  if (!ctx) return 0;
+  int32_t prev = ctx->decode_split;
+  if (tokens >= 0 && tokens % 64 == 0) ctx->decode_split = tokens;
+  return prev;
+}
+
+SAI_API sai_status sai_last_decode_shape(const sai_ctx* ctx, int32_t* workgroups,
+                                         int32_t* split_tokens) {
+  if (!ctx) return SAI_ERR_NULL;
+  if (workgroups) *workgroups = ctx->last_wg;
+  if (split_tokens) *split_tokens = ctx->last_split;
+  return SAI_OK;
+}
+
+// ------------------------------------------------------------------ cache ---
+SAI_API sai_status sai_kvcache_create(sai_ctx* ctx, const sai_kvcache_desc* desc,
+                                      sai_kvcache** out) {
+  if (!ctx || !desc || !out) return SAI_ERR_NULL;
+  *out = nullptr;
+  const sai_kvcache_desc& d = *desc;
+  if (d.num_layers <= 0 || d.num_kv_heads <= 0 || d.head_dim <= 0 || d.num_pages <= 0 ||
+      d.max_batch <= 0 || d.max_pages_per_seq <= 0)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "kv_cache_allocate: zero_dim");
+  if (!supported_dims(d.head_dim, d.quant))
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "kv_cache_allocate: head_dim %d / quant %d unsupported",
+                d.head_dim, d.quant);
+  DeviceGuard dg(ctx->device);
+  sai_kvcache* c = new (std::nothrow) sai_kvcache();
+  if (!c) return fail(ctx, SAI_ERR_ALLOC, "kv_cache_allocate: host");
+  c->desc = d;
+  c->block_bytes = d.quant == SAI_KV_INT8 ? sai::block_bytes_int8(d.head_dim)
+                                          : sai::block_bytes_int4(d.head_dim);
+  c->pool_bytes = (size_t)d.num_pages * d.num_kv_heads * c->block_bytes;
+  c->pools.assign(d.num_layers, nullptr);
+  hipError_t e = hipSuccess;
+  for (int l = 0; l < d.num_layers && e == hipSuccess; ++l) {
+    e = hipMalloc(&c->pools[l], c->pool_bytes);
+    if (e == hipSuccess) e = hipMemset(c->pools[l], 0, c->pool_bytes);
+  }
+  const size_t pt_n = (size_t)d.max_batch * d.max_pages_per_seq;
+  if (e == hipSuccess) e = hipMalloc(&c->d_page_table, pt_n * sizeof(int32_t));
+  if (e == hipSuccess) e = hipMemset(c->d_page_table, 0, pt_n * sizeof(int32_t));
+  if (e == hipSuccess) e = hipMalloc(&c->d_seq_lens, (size_t)d.max_batch * sizeof(int32_t));
+  if (e == hipSuccess) e = hipMemset(c->d_seq_lens, 0, (size_t)d.max_batch * sizeof(int32_t));
+  if (e != hipSuccess) {
+    sai_kvcache_destroy(c);
+    return fail(ctx, SAI_ERR_ALLOC, "kv_cache_allocate: %s", hipGetErrorString(e));
+  }
+  c->h_page_table.assign(pt_n, -1);
+  c->h_mapped.assign(d.max_batch, 0);
+  c->h_seq_lens.assign(d.max_batch, 0);
+  *out = c;
+  return SAI_OK;
+}
+
+SAI_API void sai_kvcache_destroy(sai_kvcache* c) {
+  if (!c) return;
+  for (uint8_t* p : c->pools)
+    if (p) (void)hipFree(p);
+  if (c->d_page_table) (void)hipFree(c->d_page_table);
+  if (c->d_seq_lens) (void)hipFree(c->d_seq_lens);
+  delete c;
+}
+
+SAI_API sai_status sai_kvcache_set_page_table(sai_ctx* ctx, sai_kvcache* c,
+                                              const int32_t* page_table, int32_t batch) {
+  if (!ctx || !c || !page_table) return SAI_ERR_NULL;
+  const sai_kvcache_desc& d = c->desc;
+  if (batch <= 0 || batch > d.max_batch)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "set_page_table: batch %d not in 1..%d", batch,
+                d.max_batch);
+  const int w = d.max_pages_per_seq;
+  std::vector<int32_t> mapped(d.max_batch, 0);
+  for (int b = 0; b < batch; ++b) {
+    int lead = 0;
+    bool gap = false;
+    for (int i = 0; i < w; ++i) {
+      const int32_t pid = page_table[(size_t)b * w + i];
+      if (pid < -1 || pid >= d.num_pages)
+        return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                    "set_page_table: page id %d of sequence %d slot %d outside [0, %d)", pid, b, i,
+                    d.num_pages);
+      if (pid == -1) gap = true;
+      if (!gap) lead = i + 1;
+    }
+    mapped[b] = lead;
+  }
+  DeviceGuard dg(ctx->device);
+  // setup call: order after all work that may still read the table
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(ctx, e, "set_page_table: sync");
+  std::vector<int32_t> dev_copy((size_t)batch * w);
+  for (size_t i = 0; i < dev_copy.size(); ++i) dev_copy[i] = std::max(page_table[i], 0);
+  e = hipMemcpy(c->d_page_table, dev_copy.data(), dev_copy.size() * sizeof(int32_t),
+                hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(ctx, e, "set_page_table");
+  std::fill(c->h_page_table.begin(), c->h_page_table.end(), -1);
+  std::copy(page_table, page_table + (size_t)batch * w, c->h_page_table.begin());
+  c->h_mapped = mapped;
+  c->batch = batch;
+  std::fill(c->h_seq_lens.begin(), c->h_seq_lens.end(), 0);
+  c->pending = 0;
+  e = hipMemset(c->d_seq_lens, 0, (size_t)d.max_batch * sizeof(int32_t));
+  if (e != hipSuccess) return hip_fail(ctx, e, "set_page_table: lengths");
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_kvcache_set_seq_lens(sai_ctx* ctx, sai_kvcache* c, const int32_t* seq_lens,
+                                            int32_t batch) {
+  if (!ctx || !c || !seq_lens) return SAI_ERR_NULL;
+  if (batch != c->batch)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "set_seq_lens: batch %d != page table batch %d",
+                batch, c->batch);
+  for (int b = 0; b < batch; ++b) {
+    if (seq_lens[b] < 0 || (int64_t)seq_lens[b] > (int64_t)c->h_mapped[b] * SAI_PAGE_TOKENS)
+      return fail(ctx, SAI_ERR_OVERFLOW, "set_seq_lens: length %d of sequence %d exceeds %d mapped pages",
+                  seq_lens[b], b, c->h_mapped[b]);
+  }
+  DeviceGuard dg(ctx->device);
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(ctx, e, "set_seq_lens: sync");
+  e = hipMemcpy(c->d_seq_lens, seq_lens, (size_t)batch * sizeof(int32_t),
+                           hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(ctx, e, "set_seq_lens");
+  std::copy(seq_lens, seq_lens + batch, c->h_seq_lens.begin());
+  c->pending = 0;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_kvcache_advance(sai_ctx* ctx, sai_kvcache* c, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  if (c->pending == 0) return SAI_OK;
+  for (int b = 0; b < c->batch; ++b)
+    if ((int64_t)c->h_seq_lens[b] + c->pending > (int64_t)c->desc.max_pages_per_seq * SAI_PAGE_TOKENS)
+      return fail(ctx, SAI_ERR_OVERFLOW, "kv_cache_advance:position_overflow");
+  DeviceGuard dg(ctx->device);
+  hipError_t e = sai::launch_seq_advance(c->d_seq_lens, c->batch, c->pending, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "kv_cache_advance");
+  for (int b = 0; b < c->batch; ++b) c->h_seq_lens[b] += c->pending;
+  c->pending = 0;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_kvcache_reset(sai_ctx* ctx, sai_kvcache* c) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  DeviceGuard dg(ctx->device);
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemset(c->d_seq_lens, 0, (size_t)c->desc.max_batch * sizeof(int32_t));
+  if (e != hipSuccess) return hip_fail(ctx, e, "kv_cache_reset");
+  std::fill(c->h_seq_lens.begin(), c->h_seq_lens.end(), 0);
+  c->pending = 0;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_kvcache_lengths(const sai_kvcache* c, int32_t* seq_lens_out,
+                                       int32_t* pending_out, int32_t* batch_out) {
+  if (!c) return SAI_ERR_NULL;
+  if (seq_lens_out) std::copy(c->h_seq_lens.begin(), c->h_seq_lens.begin() + c->batch, seq_lens_out);
+  if (pending_out) *pending_out = c->pending;
+  if (batch_out) *batch_out = c->batch;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_kvcache_pool(const sai_kvcache* c, int32_t layer, void** dev_ptr,
+                                    size_t* bytes, size_t* block_bytes) {
+  if (!c) return SAI_ERR_NULL;
+  if (layer < 0 || layer >= c->desc.num_layers) return SAI_ERR_SHAPE_MISMATCH;
+  if (dev_ptr) *dev_ptr = c->pools[layer];
+  if (bytes) *bytes = c->pool_bytes;
+  if (block_bytes) *block_bytes = c->block_bytes;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_kvcache_read(sai_ctx* ctx, sai_kvcache* c, int32_t layer, int32_t b,
+                                    int32_t kv_head, int32_t t0, int32_t n_tokens, void* k_codes,
+                                    void* v_codes, void* k_params, void* v_params) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const sai_kvcache_desc& d = c->desc;
+  if (layer < 0 || layer >= d.num_layers || b < 0 || b >= c->batch || kv_head < 0 ||
+      kv_head >= d.num_kv_heads || t0 < 0 || n_tokens < 0)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "kvcache_read: index out of range");
+  if ((int64_t)t0 + n_tokens > (int64_t)c->h_mapped[b] * SAI_PAGE_TOKENS)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "kvcache_read: tokens beyond the mapped pages");
+  DeviceGuard dg(ctx->device);
+  const int D = d.head_dim;
+  std::vector<uint8_t> blk(c->block_bytes);
+  const int NG = D / 32;
+  for (int t = t0; t < t0 + n_tokens; ++t) {
+    const int page = c->h_page_table[(size_t)b * d.max_pages_per_seq + t / SAI_PAGE_TOKENS];
+    const int slot = t % SAI_PAGE_TOKENS;
+    const int i = t - t0;
+    // one block copy per page (re-used while t stays in the page)
+    if (i == 0 || slot == 0) {
+      hipError_t e = hipMemcpy(blk.data(),
+                               c->pools[layer] + ((size_t)page * d.num_kv_heads + kv_head) * c->block_bytes,
+                               c->block_bytes, hipMemcpyDeviceToHost);
+      if (e != hipSuccess) return hip_fail(ctx, e, "kvcache_read");
+    }
+    if (d.quant == SAI_KV_INT8) {
+      if (k_codes) std::memcpy((int8_t*)k_codes + (size_t)i * D, blk.data() + (size_t)slot * D, D);
+      if (v_codes)
+        for (int e = 0; e < D; ++e) ((int8_t*)v_codes)[(size_t)i * D + e] = (int8_t)blk[16 * D + e * 16 + slot];
+      if (k_params) std::memcpy((float*)k_params + i, blk.data() + 32 * D + 4 * slot, 4);
+      if (v_params) std::memcpy((float*)v_params + i, blk.data() + 32 * D + 64 + 4 * slot, 4);
+    } else {
+      if (k_codes) std::memcpy((uint8_t*)k_codes + (size_t)i * (D / 2), blk.data() + (size_t)slot * (D / 2), D / 2);
+      if (v_codes) {
+        uint8_t* dst = (uint8_t*)v_codes + (size_t)i * (D / 2);
+        for (int e = 0; e < D; e += 2) {
+          const uint8_t b0 = blk[8 * D + e * 8 + slot / 2];
+          const uint8_t b1 = blk[8 * D + (e + 1) * 8 + slot / 2];
+          const uint8_t n0 = (slot & 1) ? (b0 >> 4) : (b0 & 0xF);
+          const uint8_t n1 = (slot & 1) ? (b1 >> 4) : (b1 & 0xF);
+          dst[e / 2] = (uint8_t)(n0 | (n1 << 4));
+        }
+      }
+      if (k_params)
+        std::memcpy((uint16_t*)k_params + (size_t)i * NG * 2, blk.data() + 16 * D + (size_t)slot * NG * 4, NG * 4);
+      if (v_params)
+        std::memcpy((uint16_t*)v_params + (size_t)i * NG * 2,
+                    blk.data() + 16 * D + 64 * NG + (size_t)slot * NG * 4, NG * 4);
+    }
+  }
+  return SAI_OK;
+}
+
+// ---------------------------------------------------------------- kernels ---
+SAI_API sai_status sai_kv_append(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* k,
+                                 const void* v, int32_t dtype, int32_t batch, int32_t s_new,
+                                 const float* cos_cache, const float* sin_cache, int32_t cache_rows,
+                                 int32_t do_rotary, int32_t rotary_interleaved, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "kv_append";
+  if (!k || !v) return fail(ctx, SAI_ERR_NULL, "%s: missing key/value", op);
+  if (layer < 0 || layer >= c->desc.num_layers)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "kv_cache_append:layer_idx %d", layer);
+  if (dtype != SAI_DTYPE_F32 && dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (want f32 or bf16)", op, dtype);
+  if (s_new <= 0) return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: s_new must be > 0", op);
+  if (c->pending != 0 && c->pending != s_new)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                "%s: %d tokens pending from another layer of this pass, got %d", op, c->pending,
+                s_new);
+  sai_status st = check_lengths(ctx, c, batch, s_new, op);
+  if (st != SAI_OK) return st;
+  st = check_rope(ctx, c, batch, s_new, cos_cache, sin_cache, cache_rows, do_rotary, op);
+  if (st != SAI_OK) return st;
+  DeviceGuard dg(ctx->device);
+  sai::AppendParams p{};
+  p.k = k;
+  p.v = v;
+  p.dtype = dtype;
+  p.batch = batch;
+  p.s_new = s_new;
+  p.kv_heads = c->desc.num_kv_heads;
+  p.cos_cache = cos_cache;
+  p.sin_cache = sin_cache;
+  p.cache_rows = cache_rows;
+  p.do_rotary = do_rotary ? 1 : 0;
+  p.interleaved = rotary_interleaved ? 1 : 0;
+  p.seq_lens = c->d_seq_lens;
+  p.page_table = c->d_page_table;
+  p.max_pages = c->desc.max_pages_per_seq;
+  p.pool = c->pools[layer];
+  p.num_pages = c->desc.num_pages;
+  hipError_t e = sai::launch_kv_append(p, c->desc.head_dim, c->desc.quant, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "kv_append launch");
+  c->pending = s_new;
+  return SAI_OK;
+}
+
+namespace {
+
+sai_status attention_common(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
+                            int32_t dtype, int32_t batch, int32_t sq, int32_t num_heads,
+                            const float* cos_cache, const float* sin_cache, int32_t cache_rows,
+                            int32_t do_rotary, float* out, const char* op, int32_t* group) {
+  if (!q || !out) return fail(ctx, SAI_ERR_NULL, "%s: missing query/output", op);
+  if (layer < 0 || layer >= c->desc.num_layers)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: layer_idx %d", op, layer);
+  if (dtype != SAI_DTYPE_F32 && dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (want f32 or bf16)", op, dtype);
+  const int kvh = c->desc.num_kv_heads;
+  if (num_heads <= 0)
+    return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE, "GroupQueryAttention: num_heads and kv_num_heads must be > 0");
+  if (num_heads % kvh != 0)
+    return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE,
+                "GroupQueryAttention: num_heads must be a multiple of kv_num_heads");
+  const int G = num_heads / kvh;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: group size %d (supported 1, 2, 4, 8)", op, G);
+  if (c->pending != sq)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                "%s: %d query tokens but %d tokens pending in the cache (append first)", op, sq,
+                c->pending);
+  sai_status st = check_lengths(ctx, c, batch, sq, op);
+  if (st != SAI_OK) return st;
+  st = check_rope(ctx, c, batch, sq, cos_cache, sin_cache, cache_rows, do_rotary, op);
+  if (st != SAI_OK) return st;
+  *group = G;
+  return SAI_OK;
+}
+
+}  // namespace
+
+SAI_API sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
+                                  int32_t dtype, int32_t batch, int32_t num_heads,
+                                  const float* cos_cache, const float* sin_cache,
+                                  int32_t cache_rows, int32_t do_rotary,
+                                  int32_t rotary_interleaved, int32_t has_scale, float scale,
+                                  float* out, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "gqa_decode";
+  int32_t G = 0;
+  sai_status st = attention_common(ctx, c, layer, q, dtype, batch, 1, num_heads, cos_cache,
+                                   sin_cache, cache_rows, do_rotary, out, op, &G);
+  if (st != SAI_OK) return st;
+  if (c->desc.quant != SAI_KV_INT8)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: int4 decode is not built yet", op);
+  const int D = c->desc.head_dim;
+  const int kvh = c->desc.num_kv_heads;
+
+  // split size: about 4 workgroups per CU over the whole batch
+  int64_t tok_heads = 0;
+  for (int b = 0; b < batch; ++b) tok_heads += (int64_t)(c->h_seq_lens[b] + 1) * kvh;
+  int32_t split = ctx->decode_split;
+  if (split <= 0) {
+    const int64_t target_wg = (int64_t)ctx->num_cus * 4;
+    int64_t s = (tok_heads + target_wg - 1) / target_wg;
+    s = ((s + 63) / 64) * 64;
+    split = (int32_t)std::max<int64_t>(256, std::min<int64_t>(s, 1 << 20));
+  }
+  int64_t work = 0;
+  for (int b = 0; b < batch; ++b) work += (c->h_seq_lens[b] + 1 + split - 1) / split;
+  if (work <= 0 || work > 0x7FFFFFFF)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: bad work size", op);
+  DeviceGuard dg(ctx->device);
+  st = ensure_workspace(ctx, (size_t)work * kvh * G * (D + 2), (size_t)batch * kvh);
+  if (st != SAI_OK) return st;
+
+  sai::DecodeParams p{};
+  p.q = q;
+  p.q_dtype = dtype;
+  p.out = out;
+  p.pool = c->pools[layer];
+  p.kv_heads = kvh;
+  p.num_pages = c->desc.num_pages;
+  p.seq_lens = c->d_seq_lens;
+  p.pending = 1;
+  p.page_table = c->d_page_table;
+  p.max_pages = c->desc.max_pages_per_seq;
+  p.batch = batch;
+  p.cos_cache = cos_cache;
+  p.sin_cache = sin_cache;
+  p.cache_rows = cache_rows;
+  p.do_rotary = do_rotary ? 1 : 0;
+  p.interleaved = rotary_interleaved ? 1 : 0;
+  const float sc = has_scale ? scale : sai_default_scale(D);
+  p.scale_log2 = sc * 1.4426950408889634f;
+  p.split_tokens = split;
+  p.partials = ctx->partials;
+  p.counters = ctx->counters;
+  hipError_t e = sai::launch_gqa_decode(p, D, G, c->desc.quant, (int)work, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "gqa_decode launch");
+  ctx->last_wg = (int32_t)(work * kvh);
+  ctx->last_split = split;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
+                                   int32_t dtype, int32_t batch, int32_t sq, int32_t num_heads,
+                                   const float* cos_cache, const float* sin_cache,
+                                   int32_t cache_rows, int32_t do_rotary,
+                                   int32_t rotary_interleaved, int32_t has_scale, float scale,
+                                   float* out, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "gqa_prefill";
+  if (sq <= 0) return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: sq must be > 0", op);
+  int32_t G = 0;
+  sai_status st = attention_common(ctx, c, layer, q, dtype, batch, sq, num_heads, cos_cache,
+                                   sin_cache, cache_rows, do_rotary, out, op, &G);
+  if (st != SAI_OK) return st;
+  if (c->desc.quant != SAI_KV_INT8)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: int4 prefill is not built yet", op);
+  const int D = c->desc.head_dim;
+  DeviceGuard dg(ctx->device);
+  sai::PrefillParams p{};
+  p.q = q;
+  p.q_dtype = dtype;
+  p.out = out;
+  p.pool = c->pools[layer];
+  p.kv_heads = c->desc.num_kv_heads;
+  p.num_pages = c->desc.num_pages;
+  p.seq_lens = c->d_seq_lens;
+  p.sq = sq;
+  p.page_table = c->d_page_table;
+  p.max_pages = c->desc.max_pages_per_seq;
+  p.batch = batch;
+  p.cos_cache = cos_cache;
+  p.sin_cache = sin_cache;
+  p.cache_rows = cache_rows;
+  p.do_rotary = do_rotary ? 1 : 0;
+  p.interleaved = rotary_interleaved ? 1 : 0;
+  const float sc = has_scale ? scale : sai_default_scale(D);
+  p.scale_log2 = sc * 1.4426950408889634f;
+  hipError_t e = sai::launch_gqa_prefill(p, D, G, c->desc.quant, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "gqa_prefill launch");
+  return SAI_OK;
+}

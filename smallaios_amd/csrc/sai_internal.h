@@ -1,0 +1,143 @@
+// Internal definitions shared by the gfx950 kernels and the C ABI.
+//
+// Paged cache layout (one pool per layer, page p, kv head h):
+//   block(p, h) = pool + (p * Hkv + h) * block_bytes
+//
+// INT8 block, D = head_dim, 16 tokens:
+//   [0,        16*D)        K codes, row-major [slot][D]        (int8)
+//   [16*D,     32*D)        V codes, transposed [D][slot]       (int8)
+//   [32*D,     32*D+64)     K scales [slot]                     (f32)
+//   [32*D+64,  32*D+128)    V scales [slot]                     (f32)
+//   block_bytes = 32*D + 128
+// INT4 block (G = D/32 groups):
+//   [0,      8*D)           K codes [slot][D/2], LSB-first along D
+//   [8*D,    16*D)          V codes [D][8], LSB-first along slots
+//   [16*D,   16*D+64*G)     K (scale, zero) binary16 [slot][G][2]
+//   [.. ,    16*D+128*G)    V (scale, zero) binary16 [slot][G][2]
+//   block_bytes = 16*D + 128*G = 20*D
+//
+// K is stored token-major so that a decode lane's 16-byte load is 16
+// consecutive head_dim codes of one token (the k operand of the QK MFMA);
+// V is stored dim-major so that a lane's 16-byte load is 16 consecutive
+// tokens of one dim (the k operand of the PV MFMA).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sai {
+
+constexpr int kPageTokens = 16;
+constexpr int kQuantInt8 = 1;
+constexpr int kQuantInt4 = 2;
+constexpr int kDtypeF32 = 1;
+constexpr int kDtypeF16 = 10;
+constexpr int kDtypeBf16 = 16;
+
+__host__ __device__ constexpr size_t block_bytes_int8(int d) { return (size_t)32 * d + 128; }
+__host__ __device__ constexpr size_t block_bytes_int4(int d) { return (size_t)20 * d; }
+
+// ---- device helpers ---------------------------------------------------------
+
+// Rust `as i32` from f32: NaN -> 0, saturating, truncating.
+__device__ __forceinline__ int32_t sat_i32(float x) {
+  if (x != x) return 0;
+  if (x >= 2147483648.0f) return INT32_MAX;
+  if (x <= -2147483648.0f) return INT32_MIN;
+  return (int32_t)x;
+}
+
+// Rust `as u32` from f32: NaN -> 0, negative -> 0, saturating, truncating.
+__device__ __forceinline__ uint32_t sat_u32(float x) {
+  if (x != x) return 0u;
+  if (x <= 0.0f) return 0u;
+  if (x >= 4294967296.0f) return 0xFFFFFFFFu;
+  return (uint32_t)x;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+
+// Element i of a row stored as f32 or bf16.
+__device__ __forceinline__ float load_elem(const void* base, size_t i, int dtype) {
+  if (dtype == kDtypeBf16) return bf16_bits_to_f32(((const uint16_t*)base)[i]);
+  return ((const float*)base)[i];
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// ---- launch parameters --------------------------------------------------------
+
+struct AppendParams {
+  const void* k;  // [batch, s_new, Hkv*D]
+  const void* v;
+  int dtype;
+  int batch, s_new, kv_heads;
+  const float* cos_cache;
+  const float* sin_cache;
+  int cache_rows;
+  int do_rotary, interleaved;
+  const int32_t* seq_lens;    // device [batch] committed lengths
+  const int32_t* page_table;  // device [batch][max_pages]
+  int max_pages;
+  uint8_t* pool;
+  int num_pages;
+};
+
+struct DecodeParams {
+  const void* q;  // [batch, 1, Hq*D]
+  int q_dtype;
+  float* out;  // [batch, 1, Hq*D]
+  const uint8_t* pool;
+  int kv_heads, num_pages;
+  const int32_t* seq_lens;  // device [batch] committed
+  int pending;              // attention length = seq_lens[b] + pending
+  const int32_t* page_table;
+  int max_pages;
+  int batch;
+  const float* cos_cache;
+  const float* sin_cache;
+  int cache_rows, do_rotary, interleaved;
+  float scale_log2;   // softmax scale * log2(e)
+  int split_tokens;   // tokens per workgroup, multiple of 64
+  float* partials;    // [work_items * Hkv][G][D + 2]
+  int32_t* counters;  // [batch * Hkv], zero between launches
+};
+
+struct PrefillParams {
+  const void* q;  // [batch, sq, Hq*D]
+  int q_dtype;
+  float* out;  // [batch, sq, Hq*D]
+  const uint8_t* pool;
+  int kv_heads, num_pages;
+  const int32_t* seq_lens;  // committed; total = seq_lens[b] + sq, queries at seq_lens[b] + i
+  int sq;
+  const int32_t* page_table;
+  int max_pages;
+  int batch;
+  const float* cos_cache;
+  const float* sin_cache;
+  int cache_rows, do_rotary, interleaved;
+  float scale_log2;
+};
+
+// Launchers (return hipError_t of the launch).
+hipError_t launch_kv_append(const AppendParams& p, int head_dim, int quant, hipStream_t s);
+hipError_t launch_gqa_decode(const DecodeParams& p, int head_dim, int group, int quant,
+                             int work_items, hipStream_t s);
+hipError_t launch_gqa_prefill(const PrefillParams& p, int head_dim, int group, int quant,
+                              hipStream_t s);
+hipError_t launch_seq_advance(int32_t* seq_lens, int batch, int pending, hipStream_t s);
+
+}  // namespace sai

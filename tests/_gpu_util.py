@@ -1,0 +1,158 @@
+"""Shared helpers of the GPU parity tests: build the same quantised cache on
+the GPU (through the C ABI) and in the oracle, then compare."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+
+import oracle as O
+import smallaios_amd as S
+
+ATOL = 2e-3  # attention outputs: |gpu - ref| <= ATOL + RTOL * |ref|
+RTOL = 1e-2
+
+
+def log(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def to_bf16_f32(x: np.ndarray) -> np.ndarray:
+    """Round f32 -> bf16 (RNE, as the reference's f32_to_bf16) and back to f32."""
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def dev(x: np.ndarray, dtype="f32"):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    if dtype == "bf16":
+        t = t.to(torch.bfloat16)
+    return t.contiguous()
+
+
+class Case:
+    """One cache (GPU + oracle) with `batch` sequences.
+
+    past_lens: committed lengths before the step under test; the past K/V is
+    appended by the HIP append kernel in one prefill-style call (max(past)
+    tokens per sequence) and then truncated per sequence with set_seq_lens.
+    """
+
+    def __init__(self, rt, seed, batch, hq, hkv, d, past_lens, new_tokens, theta=10000.0,
+                 quant=S.KV_INT8, kv_dtype="f32", permute_pages=False, do_rotary=True,
+                 interleaved=False, k_transform=None, extra_pages=3, max_pages_per_seq=None,
+                 extra_tokens=0):
+        self.rng = np.random.default_rng(seed)
+        self.rt = rt
+        self.batch, self.hq, self.hkv, self.d = batch, hq, hkv, d
+        self.past_lens = np.asarray(past_lens, dtype=np.int32)
+        self.new_tokens = new_tokens
+        self.quant = quant
+        self.kv_dtype = kv_dtype
+        self.do_rotary, self.interleaved = do_rotary, interleaved
+        self.k_transform = k_transform
+        total = int(self.past_lens.max()) + new_tokens + extra_tokens
+        self.t_cap = total
+        self.max_pages = max_pages_per_seq or (total + S.PAGE_TOKENS - 1) // S.PAGE_TOKENS
+        num_pages = batch * self.max_pages + extra_pages
+        self.cos, self.sin = S.rope_tables(total + 8, d, theta)
+        self.cos_d, self.sin_d = dev(self.cos), dev(self.sin)
+        self.cache = S.KvCache(rt, 1, hkv, d, num_pages, batch, self.max_pages, quant)
+        if permute_pages:
+            ids = self.rng.permutation(num_pages)[: batch * self.max_pages]
+        else:
+            ids = np.arange(batch * self.max_pages)
+        self.page_table = ids.astype(np.int32).reshape(batch, self.max_pages)
+        self.cache.set_page_table(self.page_table)
+        self.ocache = O.LogicalCache(batch, hkv, d, self.t_cap, quant)
+        pmax = int(self.past_lens.max())
+        if pmax > 0:
+            k, v = self.kv(pmax)
+            self.append_both(k, v)
+            self.cache.advance()
+            self.cache.set_seq_lens(self.past_lens)
+            self.ocache.seq_len = self.past_lens.copy()
+
+    def kv(self, n):
+        shape = (self.batch, n, self.hkv * self.d)
+        k = self.rng.standard_normal(shape, dtype=np.float32)
+        v = self.rng.standard_normal(shape, dtype=np.float32)
+        if self.k_transform is not None:
+            k = self.k_transform(self.rng, k)
+        if self.kv_dtype == "bf16":
+            k, v = to_bf16_f32(k), to_bf16_f32(v)
+        return k, v
+
+    def append_both(self, k, v):
+        n = k.shape[1]
+        self.cache.append(0, dev(k, self.kv_dtype), dev(v, self.kv_dtype), self.batch, n,
+                          self.cos_d, self.sin_d, self.cos.shape[0], self.do_rotary,
+                          self.interleaved)
+        self.ocache.append(k, v, self.cos, self.sin, self.do_rotary, self.interleaved)
+
+    def step_kv(self):
+        """Append the step's new tokens (pending on the GPU)."""
+        k, v = self.kv(self.new_tokens)
+        self.append_both(k, v)
+
+    def query(self, q_dtype="f32"):
+        q = self.rng.standard_normal((self.batch, self.new_tokens, self.hq * self.d),
+                                     dtype=np.float32)
+        if q_dtype == "bf16":
+            q = to_bf16_f32(q)
+        return q
+
+    def check_codes(self, seqs=None):
+        """Bit-exact comparison of every stored code and scale."""
+        lens = self.ocache.seq_len
+        for b in (range(self.batch) if seqs is None else seqs):
+            n = int(lens[b])
+            for h in range(self.hkv):
+                kc, vc, kp, vp = self.cache.read(0, b, h, 0, n)
+                oc = self.ocache
+                np.testing.assert_array_equal(kc, oc.k_codes[b, h, :n], err_msg=f"K codes b={b} h={h}")
+                np.testing.assert_array_equal(vc, oc.v_codes[b, h, :n], err_msg=f"V codes b={b} h={h}")
+                if self.quant == S.KV_INT8:
+                    np.testing.assert_array_equal(kp.view(np.uint32), oc.k_scale[b, h, :n].view(np.uint32),
+                                                  err_msg=f"K scales b={b} h={h}")
+                    np.testing.assert_array_equal(vp.view(np.uint32), oc.v_scale[b, h, :n].view(np.uint32),
+                                                  err_msg=f"V scales b={b} h={h}")
+                else:
+                    np.testing.assert_array_equal(kp, oc.k_sz[b, h, :n], err_msg=f"K params b={b} h={h}")
+                    np.testing.assert_array_equal(vp, oc.v_sz[b, h, :n], err_msg=f"V params b={b} h={h}")
+
+    def gpu_decode(self, q, q_dtype="f32", scale=None):
+        import torch
+        out = torch.zeros((self.batch, 1, self.hq * self.d), dtype=torch.float32, device="cuda")
+        self.cache.decode(0, dev(q, q_dtype), out, self.batch, self.hq, self.cos_d, self.sin_d,
+                          self.cos.shape[0], self.do_rotary, self.interleaved, scale)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    def gpu_prefill(self, q, q_dtype="f32", scale=None):
+        import torch
+        out = torch.zeros((self.batch, self.new_tokens, self.hq * self.d), dtype=torch.float32,
+                          device="cuda")
+        self.cache.prefill(0, dev(q, q_dtype), out, self.batch, self.new_tokens, self.hq,
+                           self.cos_d, self.sin_d, self.cos.shape[0], self.do_rotary,
+                           self.interleaved, scale)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    def oracle_attend(self, q, scale=None):
+        return self.ocache.attend(q, self.hq, self.cos, self.sin, self.do_rotary,
+                                  self.interleaved, scale)
+
+
+def assert_close(got, ref, what=""):
+    err = np.abs(got - ref)
+    tol = ATOL + RTOL * np.abs(ref)
+    bad = err > tol
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - tol), err.shape)
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {bad.size} outside {ATOL} abs / {RTOL} rel; "
+            f"worst at {i}: got {got[i]}, ref {ref[i]}, max abs err {err.max():.3e}")
+    return float(err.max())

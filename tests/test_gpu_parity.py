@@ -1,0 +1,225 @@
+"""GPU parity of the three HIP kernels against the CPU oracle, through the C ABI.
+
+Bar: KV codes and scales bit-exact; attention outputs within 2e-3 abs + 1e-2 rel
+of the oracle (the reference's f32 CPU semantics over the dequantised cache).
+Shapes follow the five workloads of the path (decode batch 1 / Llama-3-8B layer
+/ int4 long context / ragged paged batch / prefill chunk), at full size where
+the oracle finishes in seconds and at reduced length otherwise.
+"""
+import numpy as np
+import pytest
+
+import smallaios_amd as S
+from _gpu_util import Case, assert_close, log
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def rt():
+    import torch
+    assert torch.cuda.is_available()
+    assert S.lib().sai_device_supported(0) == 1, "device 0 is not gfx950"
+    r = S.Runtime(0)
+    yield r
+    r.close()
+
+
+# ----------------------------------------------------------------- append ---
+def test_append_c1_int8_bit_exact(rt):
+    log("append c1: B=1 Hkv=2 D=64 past=511 +1, f32, theta 1e4")
+    c = Case(rt, 0x5A1A0000, 1, 8, 2, 64, [511], 1, theta=1e4)
+    c.step_kv()
+    c.check_codes()
+
+
+@pytest.mark.parametrize("d,interleaved,rot,kv_dtype", [
+    (128, False, True, "bf16"), (128, True, True, "f32"), (64, True, True, "f32"),
+    (128, False, False, "f32")])
+def test_append_variants_bit_exact(rt, d, interleaved, rot, kv_dtype):
+    log(f"append variants d={d} interleaved={interleaved} rotary={rot} {kv_dtype}")
+    c = Case(rt, 7 + d, 3, 8, 4, d, [40, 5, 17], 9, theta=5e5, kv_dtype=kv_dtype,
+             permute_pages=True, interleaved=interleaved, do_rotary=rot)
+    c.step_kv()
+    c.check_codes()
+
+
+def test_append_special_values(rt):
+    """Zero rows, huge/tiny magnitudes, inf and NaN keep the codes bit-exact."""
+    log("append special values")
+
+    def poison(rng, k):
+        k = k.copy()
+        k[0, 0, :64] = 0.0                      # zero row -> scale 1.0
+        k[0, 1, :64] = np.float32(3.0e38)       # huge
+        k[0, 2, :64] *= np.float32(1e-30)       # tiny
+        k[0, 3, 5] = np.inf
+        k[0, 4, 7] = np.nan
+        k[0, 5, :64] = np.nan                   # all-NaN row
+        k[0, 6, 64:128] = np.float32(-np.inf)
+        return k
+
+    c = Case(rt, 11, 1, 4, 2, 64, [0], 8, k_transform=poison, do_rotary=False)
+    c.step_kv()
+    c.check_codes()
+
+
+def test_append_int4_bit_exact(rt):
+    """int4 asym g32 codes and f16 params, K with x20 outlier channels."""
+    log("append int4: outlier channels, student-t, odd start positions")
+
+    def heavy(rng, k):
+        b, n, hd = k.shape
+        t = rng.standard_normal(k.shape).astype(np.float32) / np.sqrt(
+            rng.chisquare(3, size=k.shape) / 3).astype(np.float32)
+        t = t.reshape(b, n, hd // 128, 128)
+        t[..., [7, 31, 64, 100]] *= 20.0
+        return t.reshape(b, n, hd).astype(np.float32)
+
+    c = Case(rt, 0x5A1A0002, 2, 8, 2, 128, [33, 6], 5, theta=5e5, quant=S.KV_INT4,
+             k_transform=heavy, permute_pages=True, extra_tokens=1)
+    c.step_kv()
+    c.check_codes()
+    c.cache.advance()
+    # a single-token append at an odd position must keep the neighbour's nibble
+    k, v = c.kv(1)
+    c.append_both(k, v)
+    c.check_codes()
+
+
+# ----------------------------------------------------------------- decode ---
+def test_decode_c1(rt):
+    log("decode c1: 8Q/2KV D=64 ctx 512 B=1 f32 theta 1e4")
+    c = Case(rt, 0x5A1A0000, 1, 8, 2, 64, [511], 1, theta=1e4)
+    c.step_kv()
+    q = c.query()
+    got = c.gpu_decode(q)
+    ref = c.oracle_attend(q)
+    err = assert_close(got, ref, "c1 decode")
+    log(f"  max abs err {err:.2e}")
+
+
+def test_decode_llama_shape_ragged_bf16(rt):
+    log("decode 32Q/8KV D=128 B=4 ragged, bf16, permuted pages, theta 5e5")
+    c = Case(rt, 21, 4, 32, 8, 128, [1000, 77, 513, 2047], 1, theta=5e5, kv_dtype="bf16",
+             permute_pages=True)
+    c.step_kv()
+    q = c.query("bf16")
+    got = c.gpu_decode(q, "bf16")
+    ref = c.oracle_attend(q)
+    assert_close(got, ref, "llama-shape decode")
+    c.check_codes(seqs=[1])
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(4, 4, 128), (8, 4, 64), (32, 4, 128), (16, 2, 64)])
+def test_decode_groups(rt, hq, hkv, d):
+    log(f"decode group {hq // hkv}: hq={hq} hkv={hkv} d={d}")
+    c = Case(rt, 31 + hq, 2, hq, hkv, d, [300, 129], 1, permute_pages=True)
+    c.step_kv()
+    q = c.query()
+    assert_close(c.gpu_decode(q), c.oracle_attend(q), f"group {hq // hkv}")
+
+
+@pytest.mark.parametrize("split", [64, 256, 1024])
+def test_decode_split_merge(rt, split):
+    """Many split-K partials merged by the last workgroup; repeated launches
+    reuse the self-resetting counters."""
+    log(f"decode split merge split={split}")
+    c = Case(rt, 41, 3, 32, 8, 128, [3000, 1, 640], 1, permute_pages=True)
+    prev = rt.set_decode_split(split)
+    try:
+        c.step_kv()
+        q = c.query()
+        ref = c.oracle_attend(q)
+        for _ in range(3):
+            assert_close(c.gpu_decode(q), ref, f"split {split}")
+        wg, sp = rt.last_decode_shape()
+        assert sp == split and wg >= 8
+    finally:
+        rt.set_decode_split(prev)
+
+
+def test_decode_first_token_equals_v(rt):
+    """One visible key: the output is that key's dequantised V (cf. the
+    reference's test_gpu_gqa_first_token_no_history)."""
+    log("decode first token")
+    c = Case(rt, 51, 2, 8, 2, 128, [0, 0], 1)
+    c.step_kv()
+    q = c.query()
+    got = c.gpu_decode(q)
+    _, vd = c.ocache.dequant()
+    for b in range(2):
+        for hq in range(8):
+            np.testing.assert_allclose(got[b, 0, hq * 128:(hq + 1) * 128], vd[b, hq // 4, 0],
+                                       atol=1e-5, rtol=1e-5)
+
+
+def test_decode_options(rt):
+    log("decode: no rotary / interleaved / explicit scale")
+    for rot, inter, scale in [(False, False, None), (True, True, None), (True, False, 0.05)]:
+        c = Case(rt, 61, 2, 16, 4, 64, [200, 90], 1, do_rotary=rot, interleaved=inter)
+        c.step_kv()
+        q = c.query()
+        assert_close(c.gpu_decode(q, scale=scale), c.oracle_attend(q, scale), f"{rot} {inter} {scale}")
+
+
+def test_decode_ragged_paged_batch(rt):
+    """64 sequences, seeded uniform lengths, 16-token pages, permuted page table."""
+    log("decode ragged: 64 seqs, lengths U[16,1500], permuted pages")
+    rng = np.random.default_rng(0x5A1A0003)
+    lens = rng.integers(16, 1500, size=64).astype(np.int32)
+    c = Case(rt, 71, 64, 32, 8, 128, lens, 1, theta=5e5, permute_pages=True)
+    c.step_kv()
+    q = c.query()
+    assert_close(c.gpu_decode(q), c.oracle_attend(q), "ragged decode")
+
+
+def test_decode_llama_layer_full_size(rt):
+    """Full Llama-3-8B decode layer: B=16, 8k context, bf16 Q, int8 KV."""
+    log("decode full size: B=16 ctx 8192 32Q/8KV D=128")
+    c = Case(rt, 0x5A1A0001, 16, 32, 8, 128, [8191] * 16, 1, theta=5e5)
+    c.step_kv()
+    q = c.query("bf16")
+    got = c.gpu_decode(q, "bf16")
+    ref = c.oracle_attend(q)
+    err = assert_close(got, ref, "c2 decode")
+    log(f"  max abs err {err:.2e}")
+    c.check_codes(seqs=[0, 15])
+
+
+# ---------------------------------------------------------------- prefill ---
+@pytest.mark.parametrize("hq,hkv,d,past,new,qd", [
+    (8, 2, 64, [100, 37], 70, "f32"),
+    (32, 8, 128, [300, 0], 200, "bf16"),
+    (8, 8, 128, [64, 17], 130, "f32"),
+    (16, 2, 128, [5, 250], 33, "f32"),
+])
+def test_prefill_small(rt, hq, hkv, d, past, new, qd):
+    log(f"prefill hq={hq} hkv={hkv} d={d} past={past} new={new} {qd}")
+    c = Case(rt, 81 + new, len(past), hq, hkv, d, past, new, theta=5e5, permute_pages=True,
+             kv_dtype=qd)
+    c.step_kv()
+    c.check_codes()
+    q = c.query(qd)
+    got = c.gpu_prefill(q, qd)
+    ref = c.oracle_attend(q)
+    assert_close(got, ref, "prefill")
+
+
+def test_prefill_chunk_full_size_sampled(rt):
+    """B=2, 2048 new tokens over 6144 cached, 32Q/8KV: append + prefill at full
+    size; outputs checked on sampled query rows (oracle per row)."""
+    import copy
+
+    log("prefill full size: B=2 past 6144 new 2048")
+    c = Case(rt, 0x5A1A0004, 2, 32, 8, 128, [6144, 6144], 2048, theta=5e5, kv_dtype="bf16")
+    c.step_kv()
+    q = c.query("bf16")
+    got = c.gpu_prefill(q, "bf16")
+    c.check_codes(seqs=[1])
+    deq = c.ocache.dequant()
+    for i in [0, 1, 63, 64, 777, 1500, 2046, 2047]:
+        oc = copy.copy(c.ocache)
+        oc.seq_len = np.array([6144 + i + 1] * 2, dtype=np.int32)
+        ref = oc.attend(q[:, i:i + 1], 32, c.cos, c.sin, deq=deq)
+        assert_close(got[:, i:i + 1], ref, f"prefill row {i}")
