@@ -150,6 +150,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--split", type=int, default=0, help="decode split size (0 = automatic)")
+    ap.add_argument("--waves", type=int, default=0, help="waves per decode workgroup (4 or 8)")
+    ap.add_argument("--unfused", action="store_true",
+                    help="two launches per step (sai_kv_append + sai_gqa_decode) instead of the "
+                         "fused sai_gqa_with_cache")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay the step from a captured HIP graph (one graph launch per step)")
+    ap.add_argument("--merge", choices=["auto", "combine", "inkernel"], default="auto",
+                    help="split merge: separate combine kernel or last-workgroup merge")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this path is "
@@ -164,6 +172,10 @@ def main():
     rt = S.Runtime(0)
     if args.split:
         rt.set_decode_split(args.split)
+    if args.waves:
+        rt.set_decode_waves(args.waves)
+    if args.merge != "auto":
+        rt.set_decode_merge(args.merge == "inkernel")
     cos, sin = S.rope_tables(CTX, D, THETA)
     cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
     cache, g = build_cache(S, torch, rt, cos_d, sin_d)
@@ -172,14 +184,19 @@ def main():
     k_new = torch.randn((B, 1, HKV * D), generator=g, device="cuda")
     v_new = torch.randn((B, 1, HKV * D), generator=g, device="cuda")
     out = torch.empty((B, 1, HQ * D), device="cuda", dtype=torch.float32)
-    stream = torch.cuda.current_stream()
+    stream = torch.cuda.Stream()  # default priority; graph capture needs a non-default stream
     rows = cos_d.shape[0]
 
     def step(ev=None):
-        cache.append(0, k_new, v_new, B, 1, cos_d, sin_d, rows, stream=stream)
+        if args.unfused:
+            cache.append(0, k_new, v_new, B, 1, cos_d, sin_d, rows, stream=stream)
         if ev is not None:
             ev[0].record(stream)
-        cache.decode(0, q, out, B, HQ, cos_d, sin_d, rows, stream=stream)
+        if args.unfused:
+            cache.decode(0, q, out, B, HQ, cos_d, sin_d, rows, stream=stream)
+        else:
+            cache.decode_with_cache(0, q, k_new, v_new, out, B, HQ, cos_d, sin_d, rows,
+                                    stream=stream)
         if ev is not None:
             ev[1].record(stream)
 
@@ -187,10 +204,21 @@ def main():
         step()
     torch.cuda.synchronize()
 
+    run = step
+    if args.graph:
+        # the step's launches (no allocation, no memset) recorded once, replayed
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        run = graph.replay
+
     # timed region 1: whole steps, wall clock
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        run()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall / args.steps * 1e3
@@ -226,7 +254,10 @@ def main():
         "config": {"workload": "llama3-8b-layer-gqa-decode", "batch": B, "context": CTX,
                    "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "q_dtype": "bf16",
                    "kv_cache": "int8 per-token-head f32 scale, 16-token pages",
-                   "rope_theta": THETA, "step": "kv_append + gqa_decode"},
+                   "rope_theta": THETA,
+                   "step": ("kv_append + gqa_decode" if args.unfused
+                            else "gqa_with_cache (append fused into decode)")
+                           + (", hip graph replay" if args.graph else "")},
         "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
         "tokens_per_s": round(B / (ms_step * 1e-3), 1),
         "tokens_per_s_32_layers": round(B / (32 * ms_step * 1e-3), 1),

@@ -164,6 +164,21 @@ sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const
                           int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
                           float scale, float* out, void* stream);
 
+/* ---- kernels 1 + 2 fused: one decode step in one launch ----------------------
+ * Replaces gpu_gqa_with_cache (onnx-rt/src/cuda/kernels/attention.rs:1260-1295),
+ * which appends the step's K/V to the cache (GpuKvCache::append) and attends
+ * over view_pending: here the decode kernel's workgroup that owns a sequence's
+ * last split writes the new token (same RoPE/quantise arithmetic as
+ * sai_kv_append, bit for bit) before streaming its tiles. k_new, v_new: device
+ * [batch, 1, Hkv*D] of kv_dtype (F32 or BF16). Leaves 1 token pending, exactly
+ * like sai_kv_append with s_new = 1 followed by sai_gqa_decode. */
+sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
+                              int32_t q_dtype, const void* k_new, const void* v_new,
+                              int32_t kv_dtype, int32_t batch, int32_t num_heads,
+                              const float* cos_cache, const float* sin_cache, int32_t cache_rows,
+                              int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
+                              float scale, float* out, void* stream);
+
 /* ---- kernel 3: prefill chunk (bf16/f16 MFMA) ---------------------------------
  * Same contract as sai_gqa_decode for a chunk of sq == pending query tokens per
  * sequence (the reference's op_group_query_attention with Sq > 1, causal with
@@ -179,6 +194,11 @@ sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, cons
 /* Tokens per split-K work item of the decode kernel (0 = automatic, else a
  * multiple of 64). Returns the previous value. */
 int32_t sai_set_decode_split(sai_ctx* ctx, int32_t tokens);
+/* Waves per decode workgroup (4 or 8). Returns the previous value. */
+int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves);
+/* Split merge of the decode kernel: 0 = separate combine kernel, 1 = the last
+ * workgroup of a sequence merges in-kernel. Returns the previous value. */
+int32_t sai_set_decode_merge(sai_ctx* ctx, int32_t in_kernel);
 /* Number of workgroups and split size of the last decode launch on ctx. */
 sai_status sai_last_decode_shape(const sai_ctx* ctx, int32_t* workgroups, int32_t* split_tokens);
 

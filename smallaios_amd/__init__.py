@@ -65,7 +65,8 @@ EXPORTS = [
     "sai_kvcache_create", "sai_kvcache_destroy", "sai_kvcache_set_page_table",
     "sai_kvcache_set_seq_lens", "sai_kvcache_advance", "sai_kvcache_reset",
     "sai_kvcache_lengths", "sai_kvcache_read", "sai_kvcache_pool", "sai_kv_append",
-    "sai_gqa_decode", "sai_gqa_prefill", "sai_set_decode_split", "sai_last_decode_shape",
+    "sai_gqa_decode", "sai_gqa_with_cache", "sai_gqa_prefill", "sai_set_decode_split",
+    "sai_set_decode_waves", "sai_set_decode_merge", "sai_last_decode_shape",
 ]
 
 
@@ -90,9 +91,13 @@ def _declare(L: C.CDLL) -> None:
         "sai_kv_append": (i32, [p, p, i32, p, p, i32, i32, i32, p, p, i32, i32, i32, p]),
         "sai_gqa_decode": (i32, [p, p, i32, p, i32, i32, i32, p, p, i32, i32, i32, i32, f, p,
                                  p]),
+        "sai_gqa_with_cache": (i32, [p, p, i32, p, i32, p, p, i32, i32, i32, p, p, i32, i32,
+                                     i32, i32, f, p, p]),
         "sai_gqa_prefill": (i32, [p, p, i32, p, i32, i32, i32, i32, p, p, i32, i32, i32, i32,
                                   f, p, p]),
         "sai_set_decode_split": (i32, [p, i32]),
+        "sai_set_decode_waves": (i32, [p, i32]),
+        "sai_set_decode_merge": (i32, [p, i32]),
         "sai_last_decode_shape": (i32, [p, C.POINTER(i32), C.POINTER(i32)]),
     }
     for name, (res, args) in sig.items():
@@ -176,6 +181,12 @@ class Runtime:
 
     def set_decode_split(self, tokens: int) -> int:
         return int(self._L.sai_set_decode_split(self.handle, tokens))
+
+    def set_decode_waves(self, waves: int) -> int:
+        return int(self._L.sai_set_decode_waves(self.handle, waves))
+
+    def set_decode_merge(self, in_kernel: bool) -> int:
+        return int(self._L.sai_set_decode_merge(self.handle, int(in_kernel)))
 
     def last_decode_shape(self):
         wg, sp = C.c_int32(), C.c_int32()
@@ -283,6 +294,18 @@ class KvCache:
             _dev_ptr(sin), cache_rows, int(do_rotary), int(interleaved), int(scale is not None),
             0.0 if scale is None else float(scale), _dev_ptr(out), _stream(stream)),
             "gqa_decode")
+
+    def decode_with_cache(self, layer, q, k_new, v_new, out, batch, num_heads, cos=None,
+                          sin=None, cache_rows=0, do_rotary=True, interleaved=False, scale=None,
+                          stream=None, q_dtype=None, kv_dtype=None):
+        """Fused step: append the token (k_new/v_new [B,1,Hkv*D]) and attend."""
+        qd = q_dtype if q_dtype is not None else _dtype_code(q)
+        kd = kv_dtype if kv_dtype is not None else _dtype_code(k_new)
+        self.rt.check(self._L.sai_gqa_with_cache(
+            self.rt.handle, self.handle, layer, _dev_ptr(q), qd, _dev_ptr(k_new), _dev_ptr(v_new),
+            kd, batch, num_heads, _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary),
+            int(interleaved), int(scale is not None), 0.0 if scale is None else float(scale),
+            _dev_ptr(out), _stream(stream)), "gqa_with_cache")
 
     def prefill(self, layer, q, out, batch, sq, num_heads, cos=None, sin=None, cache_rows=0,
                 do_rotary=True, interleaved=False, scale=None, stream=None, dtype=None):

@@ -5,33 +5,40 @@
 // reads 264 B per (token, kv head) and does 4 * 128 * 2 multiply-adds on them.
 // Dequantising every code to f32 and doing those multiply-adds on the VALU
 // costs more vector cycles than the HBM stream leaves (~90 SIMD cycles per
-// token-head at 80 % of 8 TB/s); the VALU would be the bound. Instead the int8
-// codes go straight from HBM into v_mfma_i32_16x16x64_i8 operands and the
-// per-token scales are applied to the 32-bit dot products:
+// token-head at 80 % of 8 TB/s). Instead the int8 codes go straight from HBM
+// into v_mfma_i32_16x16x64_i8 operands and the per-token scales are applied to
+// the 32-bit dot products:
 //   score(t, h) = s_k[t] * (sq_hi[h] * <k_t, qhi_h> + sq_lo[h] * <k_t, qlo_h>)
 //   out(h, :)   = sum_t p'(t, h) * v_t,   p' = p * s_v[t] = sp[h]*(phi + plo/254)
-// Q (after RoPE) and P' are split into two int8 terms (hi + residual/254) so
-// their representation error is ~1/64516 of the row maximum; both terms ride in
-// spare MFMA rows/columns, so the split costs no extra MFMA issue.
+// Q (after RoPE) and P' are split into two int8 terms (hi + residual/254), so
+// their representation error is ~1/64516 of the row maximum; both terms ride
+// in spare MFMA rows/columns, so the split costs no extra MFMA issue.
 //
 // Wave layout (lane = r + 16 g, r = lane & 15, g = lane >> 4). A tile is 64
-// tokens = 4 pages; "group" g of a tile is page g.
+// tokens = 4 pages; lane group g of a tile works on page g.
 //   QK  : S^T = K * Q^T.  A = K codes, row i of MFMA #blk is token
 //         (page i>>2, slot 4*blk + (i&3)); B = Q terms, column j = head-term
 //         (head j>>1, term j&1: 0 = hi, 1 = lo). The result lands with lane
 //         (j, g) holding head-term j for all 16 slots of page g -- exactly the
 //         A-operand layout the PV product needs, so no LDS transpose.
+//         k index: lane group g, k step ks <-> dims (D/4)*g + 16*ks + [0,16),
+//         so one row's 4 lane groups read one contiguous 128-byte line.
 //   PV  : O = P' * V.  A = P' codes (row = head-term, k = slots of page g),
 //         B = V codes read dim-major from the page (column = dim).
 //   Online softmax in the log2 domain; cross-page reductions are two
-//   shuffles (lanes j, j+16, j+32, j+48), the hi/lo pairing one DPP swap.
+//   permlane swaps (VALU), the hi/lo pairing one DPP quad swap.
 //
-// Work split: grid.x enumerates (sequence, split) pairs for ragged lengths
+// Memory pipeline: the split's page ids are staged in LDS once, and every
+// wave double-buffers its tiles in registers (the loads of tile i+NW are in
+// flight while tile i is computed).
+//
+// Work split: grid.x enumerates (sequence, split) pairs over ragged lengths
 // (each wave finds its pair by a prefix scan over seq_lens), grid.y is the kv
 // head. NW waves of a workgroup take interleaved tiles of the split and merge
-// through LDS; when a sequence has several splits, every workgroup writes a
-// partial (m, l, o) and the last one to finish (atomic counter, no waiting)
-// merges them and resets the counter.
+// through LDS. A sequence with one split writes its output directly; with
+// several, every workgroup writes a partial (m, l, o) and the combine kernel
+// (a second launch, so no cross-workgroup fences) merges them.
+#include "append_row.h"
 #include "sai_internal.h"
 
 namespace sai {
@@ -40,8 +47,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// RoPE of one element, unfused like rotate_rope_block
-// (onnx-rt/src/ops/microsoft.rs:137-160).
+constexpr int kMaxSplitPages = 1024;  // split_tokens <= 16384
+
 __device__ __forceinline__ float rope_elem(float c, float s, float own, float partner,
                                            bool first) {
 #pragma clang fp contract(off)
@@ -52,30 +59,204 @@ __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
   return (a & 0xFF) | ((b & 0xFF) << 8) | ((c & 0xFF) << 16) | ((int)((unsigned)d << 24));
 }
 
+// exchange with the neighbouring lane: quad_perm(1,0,3,2)
 __device__ __forceinline__ int swap_pair(int v) {
-  // quad_perm(1,0,3,2): exchange with the neighbouring lane
   return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
 }
 
+// max / sum over the four lane groups (lanes r, r+16, r+32, r+48)
 __device__ __forceinline__ float xgroup_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
-
 __device__ __forceinline__ float xgroup_sum(float v) {
-  v += __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// 16 consecutive elements (f32 or bf16) starting at element `off`; the
+// offset is a multiple of 16 and the row 32-byte aligned.
+__device__ __forceinline__ void load16(const void* base, size_t off, int dtype, float (&x)[16]) {
+  if (dtype == kDtypeBf16) {
+    const uint4* p = (const uint4*)((const uint16_t*)base + off);
+    const uint4 a = p[0], b = p[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  } else {
+    const float4* p = (const float4*)((const float*)base + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 v = p[i];
+      x[4 * i] = v.x, x[4 * i + 1] = v.y, x[4 * i + 2] = v.z, x[4 * i + 3] = v.w;
+    }
+  }
+}
+
+template <int D>
+struct TileRegs {
+  static constexpr int KS = D / 64;
+  static constexpr int JB = D / 16;
+  v4i ka[4][KS];  // K codes, QK A operand per 16-row block
+  v4i vb[JB];     // V codes (dim-major), PV B operand per 16-dim block
+  float sk, sv;   // K / V scale of (page g, slot r); shared through LDS
+};
+
+template <int D>
+__device__ __forceinline__ void load_tile(TileRegs<D>& T, const uint8_t* __restrict__ pool,
+                                          const int* sm_pg, int tile, int num_pages, int kvh,
+                                          int r, int g, int n_pages_split) {
+  constexpr size_t BB = block_bytes_int8(D);
+  const int lp = n_pages_split - 1;
+  const int pg_g = sm_pg[min(tile * 4 + g, lp)];
+  const int pg_k = sm_pg[min(tile * 4 + (r >> 2), lp)];
+  const uint8_t* blk_g = pool + block_offset(pg_g, kvh, num_pages, BB);
+  const uint8_t* blk_k = pool + block_offset(pg_k, kvh, num_pages, BB);
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+    for (int ks = 0; ks < TileRegs<D>::KS; ++ks)
+      T.ka[blk][ks] = __builtin_nontemporal_load(
+          (const v4i*)(blk_k + (size_t)(4 * blk + (r & 3)) * D + (D / 4) * g + 16 * ks));
+#pragma unroll
+  for (int jb = 0; jb < TileRegs<D>::JB; ++jb)
+    T.vb[jb] = __builtin_nontemporal_load((const v4i*)(blk_g + 16 * D + (16 * jb + r) * 16));
+  T.sk = ((const float*)(blk_g + 32 * D))[r];
+  T.sv = ((const float*)(blk_g + 32 * D + 64))[r];
+}
+
+template <int D, int G>
+struct WaveState {
+  float m_run, l_run;   // per head (lanes of head-term j), log2 domain
+  float acc[D / 16][2]; // lane (dim 16*jb + r, group g): heads 2g, 2g+1
+};
+
+template <int D, int G>
+__device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, G>& st,
+                                             const v4i (&qB)[D / 64], float q_own, float q_oth,
+                                             int tok0, int t_end, bool is_hi, bool live, int g,
+                                             float* sm_sc) {
+  constexpr int KS = D / 64;
+  constexpr int JB = D / 16;
+  // QK^T on the matrix cores
+  v4i cs[4];
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    cs[blk] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      cs[blk] = __builtin_amdgcn_mfma_i32_16x16x64_i8(T.ka[blk][ks], qB[ks], cs[blk], 0, 0, 0);
+  }
+  // scales of page g, slots 0..15 (this wave's LDS slot; lane 16g + r wrote slot r)
+  const int lane = threadIdx.x & 63;
+  sm_sc[lane] = T.sk;
+  sm_sc[64 + lane] = T.sv;
+  __builtin_amdgcn_wave_barrier();  // LDS ops of a wave run in order; keep the compiler from hoisting
+  float skv[16], svv[16];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float4 a = *(const float4*)(sm_sc + 16 * g + 4 * w);
+    const float4 c = *(const float4*)(sm_sc + 64 + 16 * g + 4 * w);
+    skv[4 * w] = a.x, skv[4 * w + 1] = a.y, skv[4 * w + 2] = a.z, skv[4 * w + 3] = a.w;
+    svv[4 * w] = c.x, svv[4 * w + 1] = c.y, svv[4 * w + 2] = c.z, svv[4 * w + 3] = c.w;
+  }
+  const int nvalid = t_end - tok0;  // slots [0, nvalid) of page g are visible
+  const bool full = __builtin_amdgcn_readfirstlane(t_end - (tok0 - 16 * g) >= 64);
+  float s[16];
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int slot = 4 * blk + e;
+      const int own = cs[blk][e];
+      const int oth = swap_pair(own);
+      s[slot] = (q_own * (float)own + q_oth * (float)oth) * skv[slot];
+    }
+  if (!full) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s[i] = (i < nvalid) ? s[i] : -INFINITY;
+      svv[i] = (i < nvalid) ? svv[i] : 0.0f;
+    }
+  }
+  float mt = s[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) mt = fmaxf(mt, s[i]);
+  mt = xgroup_max(mt);
+  const float m_new = fmaxf(st.m_run, mt);
+  const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+  const float alpha = fast_exp2(st.m_run - m_use);
+  float psum = 0.0f, pmax = 0.0f;
+  float pv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float pe = fast_exp2(s[i] - m_use);
+    psum += pe;
+    pv[i] = pe * svv[i];
+    pmax = fmaxf(pmax, pv[i]);
+  }
+  psum = xgroup_sum(psum);
+  pmax = xgroup_max(pmax);
+  st.l_run = st.l_run * alpha + psum;
+  st.m_run = m_new;
+
+  // P' -> int8 (hi, lo) terms; this lane's term is its row of the PV A operand
+  const float sp = pmax * (1.0f / 127.0f);
+  const float inv_sp = pmax > 0.0f ? 127.0f / pmax : 0.0f;
+  int pc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float hi = rintf(pv[i] * inv_sp);
+    const float lo = fminf(fmaxf(rintf((pv[i] - hi * sp) * (254.0f * inv_sp)), -127.0f), 127.0f);
+    pc[i] = live ? (int)(is_hi ? hi : lo) : 0;
+  }
+  v4i pa;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) pa[w] = pack4(pc[4 * w], pc[4 * w + 1], pc[4 * w + 2], pc[4 * w + 3]);
+
+  // rescale factors of the heads this lane accumulates (2g, 2g+1); head h's
+  // softmax state sits in lanes with head-term 2h (read from lane 2h)
+  float a0 = 0.0f, a1 = 0.0f, s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int h2 = 0; h2 < (G + 1) / 2; ++h2) {
+    const int ah0 = __builtin_amdgcn_readlane(__float_as_int(alpha), 4 * h2);
+    const int sh0 = __builtin_amdgcn_readlane(__float_as_int(sp), 4 * h2);
+    const int ah1 = G > 2 * h2 + 1 ? __builtin_amdgcn_readlane(__float_as_int(alpha), 4 * h2 + 2) : 0;
+    const int sh1 = G > 2 * h2 + 1 ? __builtin_amdgcn_readlane(__float_as_int(sp), 4 * h2 + 2) : 0;
+    if (g == h2) {
+      a0 = __int_as_float(ah0);
+      s0 = __int_as_float(sh0);
+      a1 = __int_as_float(ah1);
+      s1 = __int_as_float(sh1);
+    }
+  }
+  const float s0l = s0 * (1.0f / 254.0f);
+  const float s1l = s1 * (1.0f / 254.0f);
+
+  // P' V on the matrix cores
+#pragma unroll
+  for (int jb = 0; jb < JB; ++jb) {
+    const v4i co = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, T.vb[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+    st.acc[jb][0] = st.acc[jb][0] * a0 + ((float)co[0] * s0 + (float)co[1] * s0l);
+    st.acc[jb][1] = st.acc[jb][1] * a1 + ((float)co[2] * s1 + (float)co[3] * s1l);
+  }
+}
+
 template <int D, int G, int NW>
-__global__ __launch_bounds__(64 * NW) void gqa_decode_int8_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   static_assert(G >= 1 && G <= 8, "group");
-  constexpr int KS = D / 64;  // 64-dim k steps of the QK product
-  constexpr int JB = D / 16;  // 16-dim column blocks of the PV product
-  constexpr size_t BB = block_bytes_int8(D);
+  constexpr int KS = D / 64;
+  constexpr int JB = D / 16;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -116,186 +297,134 @@ __global__ __launch_bounds__(64 * NW) void gqa_decode_int8_kernel(DecodeParams p
   const int L = p.seq_lens[b] + p.pending;
   const int t_begin = split * p.split_tokens;
   const int t_end = min(L, t_begin + p.split_tokens);
-  const int last_page = (L - 1) / kPageTokens;
-  const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
-  const uint8_t* pool = p.pool;
   const int Hq = p.kv_heads * G;
+  const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
+
+  // ---- fused append: the split holding the new token writes it first ----------
+  if (p.k_new != nullptr && split == nsplit - 1 && wave == 0) {
+    const int pos = L - 1;
+    uint8_t* blk = (uint8_t*)p.pool +
+                   block_offset(pt[pos / kPageTokens], kvh, p.num_pages, block_bytes_int8(D));
+    const size_t row = ((size_t)b * p.kv_heads + kvh) * D * (p.kv_dtype == kDtypeBf16 ? 2 : 4);
+    append_row_int8<D>((const uint8_t*)p.k_new + row, (const uint8_t*)p.v_new + row, p.kv_dtype,
+                       lane, pos, blk, pos % kPageTokens, p.do_rotary, p.interleaved != 0,
+                       p.cos_cache, p.sin_cache);
+    __threadfence_block();
+  }
+
+  // ---- page ids of the split -> LDS --------------------------------------------
+  __shared__ int sm_pg[kMaxSplitPages];
+  const int first_page = t_begin / kPageTokens;
+  const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
+  for (int i = threadIdx.x; i < n_pages_split; i += 64 * NW) sm_pg[i] = pt[first_page + i];
+  __syncthreads();
+
+  // ---- first tile in flight while Q is prepared ----------------------------------
+  const int n_tiles = (t_end - t_begin + 63) / 64;
+  const int tile_off = 0;  // splits start on a tile (64-token) boundary
+  TileRegs<D> TA;
+  int tile = wave;
+  if (tile < n_tiles) load_tile<D>(TA, p.pool, sm_pg + tile_off, tile, p.num_pages, kvh, r, g, n_pages_split);
 
   // ---- Q: RoPE at position L-1, split into int8 (hi, lo) terms -------------
   const int hterm = r;  // column j of the QK product
   const int h = hterm >> 1;
   const bool is_hi = (hterm & 1) == 0;
   const bool live = h < G;
-  float qv[KS][16];
-  float amax = 0.0f;
+  v4i qB[KS];
+  float sq_hi;
   {
+    constexpr int HALF = D / 2;
     const int pos = L - 1;
     const int hq = kvh * G + (live ? h : 0);
     const size_t qbase = ((size_t)b * Hq + hq) * D;
-    constexpr int HALF = D / 2;
+    float qv[KS][16];
+    float amax = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
+      const int c0 = (D / 4) * g + 16 * ks;  // first dim of this lane's chunk
+      float x[16];
+      load16(p.q, qbase + c0, p.q_dtype, x);
+      if (p.do_rotary) {
+        const float* cr = p.cos_cache + (size_t)pos * HALF;
+        const float* sr = p.sin_cache + (size_t)pos * HALF;
+        if (p.interleaved) {
+          const float4 c0v = *(const float4*)(cr + c0 / 2), c1v = *(const float4*)(cr + c0 / 2 + 4);
+          const float4 s0v = *(const float4*)(sr + c0 / 2), s1v = *(const float4*)(sr + c0 / 2 + 4);
+          const float cc[8] = {c0v.x, c0v.y, c0v.z, c0v.w, c1v.x, c1v.y, c1v.z, c1v.w};
+          const float ss[8] = {s0v.x, s0v.y, s0v.z, s0v.w, s1v.x, s1v.y, s1v.z, s1v.w};
+          float y[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) y[i] = rope_elem(cc[i >> 1], ss[i >> 1], x[i], x[i ^ 1], (i & 1) == 0);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) x[i] = y[i];
+        } else {
+          const bool first = c0 < HALF;
+          const int pc0 = first ? c0 : c0 - HALF;  // pair index of element 0
+          float xp[16];
+          load16(p.q, qbase + (first ? c0 + HALF : c0 - HALF), p.q_dtype, xp);
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) {
+            const float4 cv = *(const float4*)(cr + pc0 + 4 * i4);
+            const float4 sv = *(const float4*)(sr + pc0 + 4 * i4);
+            const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
+            const float ss[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              x[4 * i4 + e] = rope_elem(cc[e], ss[e], x[4 * i4 + e], xp[4 * i4 + e], first);
+          }
+        }
+      }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int d = 16 * g + 64 * ks + i;
-        float x = load_elem(p.q, qbase + d, p.q_dtype);
-        if (p.do_rotary) {
-          int dp, pi;
-          bool first;
-          if (p.interleaved) {
-            dp = d ^ 1;
-            pi = d >> 1;
-            first = (d & 1) == 0;
-          } else {
-            first = d < HALF;
-            dp = first ? d + HALF : d - HALF;
-            pi = first ? d : d - HALF;
-          }
-          const float xp = load_elem(p.q, qbase + dp, p.q_dtype);
-          x = rope_elem(p.cos_cache[(size_t)pos * HALF + pi], p.sin_cache[(size_t)pos * HALF + pi],
-                        x, xp, first);
-        }
-        qv[ks][i] = live ? x : 0.0f;
+        qv[ks][i] = live ? x[i] : 0.0f;
         amax = fmaxf(amax, fabsf(qv[ks][i]));
       }
     }
-  }
-  amax = xgroup_max(amax);
-  const float sq_hi = amax > 0.0f ? amax * (1.0f / 127.0f) : 1.0f;
-  const float inv_sq = 1.0f / sq_hi;
-  const float sq_lo = sq_hi * (1.0f / 254.0f);
-  v4i qB[KS];
+    amax = xgroup_max(amax);
+    sq_hi = amax > 0.0f ? amax * (1.0f / 127.0f) : 1.0f;
+    const float inv_sq = 1.0f / sq_hi;
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    int c[16];
+    for (int ks = 0; ks < KS; ++ks) {
+      int c[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float y = qv[ks][i];
-      float hi = rintf(y * inv_sq);
-      hi = fminf(fmaxf(hi, -127.0f), 127.0f);
-      const float res = y - hi * sq_hi;
-      float lo = rintf(res * (254.0f * inv_sq));
-      lo = fminf(fmaxf(lo, -127.0f), 127.0f);
-      c[i] = live ? (int)(is_hi ? hi : lo) : 0;
-    }
-#pragma unroll
-    for (int w = 0; w < 4; ++w) qB[ks][w] = pack4(c[4 * w], c[4 * w + 1], c[4 * w + 2], c[4 * w + 3]);
-  }
-  const float q_own = is_hi ? sq_hi : sq_lo;
-  const float q_oth = is_hi ? sq_lo : sq_hi;
-
-  // ---- stream the split's tiles ---------------------------------------------
-  float m_run = -INFINITY;  // per head (lanes of head-term j), log2 domain
-  float l_run = 0.0f;
-  float acc[JB][2];  // lane (dim 16*jb + r, group g): heads 2g, 2g+1
-#pragma unroll
-  for (int jb = 0; jb < JB; ++jb) acc[jb][0] = acc[jb][1] = 0.0f;
-
-  const int n_tiles = (t_end - t_begin + 63) / 64;
-  for (int tile = wave; tile < n_tiles; tile += NW) {
-    const int t0 = t_begin + tile * 64;
-    const int pg_g = min(t0 / kPageTokens + g, last_page);
-    const int pg_k = min(t0 / kPageTokens + (r >> 2), last_page);
-    const uint8_t* blk_g = pool + ((size_t)pt[pg_g] * p.kv_heads + kvh) * BB;
-    const uint8_t* blk_k = pool + ((size_t)pt[pg_k] * p.kv_heads + kvh) * BB;
-
-    v4i ka[4][KS];
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        ka[blk][ks] =
-            *(const v4i*)(blk_k + (size_t)(4 * blk + (r & 3)) * D + 16 * g + 64 * ks);
-    v4i vb[JB];
-#pragma unroll
-    for (int jb = 0; jb < JB; ++jb) vb[jb] = *(const v4i*)(blk_g + 16 * D + (16 * jb + r) * 16);
-    float sk[16], sv[16];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float4 a = *(const float4*)(blk_g + 32 * D + 16 * w);
-      const float4 c = *(const float4*)(blk_g + 32 * D + 64 + 16 * w);
-      sk[4 * w] = a.x, sk[4 * w + 1] = a.y, sk[4 * w + 2] = a.z, sk[4 * w + 3] = a.w;
-      sv[4 * w] = c.x, sv[4 * w + 1] = c.y, sv[4 * w + 2] = c.z, sv[4 * w + 3] = c.w;
-    }
-
-    // QK^T on the matrix cores
-    v4i cs[4];
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
-      cs[blk] = v4i{0, 0, 0, 0};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        cs[blk] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka[blk][ks], qB[ks], cs[blk], 0, 0, 0);
-    }
-
-    // scores of page g, slots 0..15 (slot = 4*blk + e)
-    float s[16];
-    const int tok0 = t0 + 16 * g;
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int slot = 4 * blk + e;
-        const int own = cs[blk][e];
-        const int oth = swap_pair(own);
-        const float raw = q_own * (float)own + q_oth * (float)oth;
-        const float sc = raw * sk[slot] * p.scale_log2;
-        s[slot] = (tok0 + slot < t_end) ? sc : -INFINITY;
+      for (int i = 0; i < 16; ++i) {
+        const float y = qv[ks][i];
+        const float hi = fminf(fmaxf(rintf(y * inv_sq), -127.0f), 127.0f);
+        const float lo = fminf(fmaxf(rintf((y - hi * sq_hi) * (254.0f * inv_sq)), -127.0f), 127.0f);
+        c[i] = live ? (int)(is_hi ? hi : lo) : 0;
       }
-    }
-    float mt = s[0];
 #pragma unroll
-    for (int i = 1; i < 16; ++i) mt = fmaxf(mt, s[i]);
-    mt = xgroup_max(mt);
-    const float m_new = fmaxf(m_run, mt);
-    const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
-    float psum = 0.0f, pmax = 0.0f;
-    float pv[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float pe = fast_exp2(s[i] - m_use);
-      psum += pe;
-      pv[i] = (tok0 + i < t_end) ? pe * sv[i] : 0.0f;
-      pmax = fmaxf(pmax, pv[i]);
+      for (int w = 0; w < 4; ++w) qB[ks][w] = pack4(c[4 * w], c[4 * w + 1], c[4 * w + 2], c[4 * w + 3]);
     }
-    psum = xgroup_sum(psum);
-    pmax = xgroup_max(pmax);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+  }
+  // the softmax scale (log2 domain) rides on the Q term scales
+  const float sq_hi_s = sq_hi * p.scale_log2;
+  const float sq_lo_s = sq_hi_s * (1.0f / 254.0f);
+  const float q_own = is_hi ? sq_hi_s : sq_lo_s;
+  const float q_oth = is_hi ? sq_lo_s : sq_hi_s;
+  __shared__ float sm_sc[NW][128];
 
-    // P' -> int8 (hi, lo) terms; this lane's term is its row of the PV A operand
-    const float sp = pmax * (1.0f / 127.0f);
-    const float inv_sp = pmax > 0.0f ? 127.0f / pmax : 0.0f;
-    int pc[16];
+  // ---- stream the split's tiles, double-buffered --------------------------------
+  WaveState<D, G> st;
+  st.m_run = -INFINITY;
+  st.l_run = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float hi = rintf(pv[i] * inv_sp);
-      const float res = pv[i] - hi * sp;
-      float lo = rintf(res * (254.0f * inv_sp));
-      lo = fminf(fmaxf(lo, -127.0f), 127.0f);
-      pc[i] = live ? (int)(is_hi ? hi : lo) : 0;
-    }
-    v4i pa;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) pa[w] = pack4(pc[4 * w], pc[4 * w + 1], pc[4 * w + 2], pc[4 * w + 3]);
+  for (int jb = 0; jb < JB; ++jb) st.acc[jb][0] = st.acc[jb][1] = 0.0f;
 
-    // rescale factors of the two heads this lane accumulates (2g, 2g+1):
-    // held by lanes with head-term 4g + 2hh, i.e. lane 20g + 2hh
-    const float a0 = __shfl(alpha, 20 * g, 64);
-    const float a1 = __shfl(alpha, 20 * g + 2, 64);
-    const float s0 = __shfl(sp, 20 * g, 64);
-    const float s1 = __shfl(sp, 20 * g + 2, 64);
-    const float s0l = s0 * (1.0f / 254.0f);
-    const float s1l = s1 * (1.0f / 254.0f);
-
-    // P' V on the matrix cores
-#pragma unroll
-    for (int jb = 0; jb < JB; ++jb) {
-      const v4i co = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
-      acc[jb][0] = acc[jb][0] * a0 + (float)co[0] * s0 + (float)co[1] * s0l;
-      acc[jb][1] = acc[jb][1] * a1 + (float)co[2] * s1 + (float)co[3] * s1l;
-    }
+  TileRegs<D> TB;
+  while (tile < n_tiles) {
+    int nxt = tile + NW;
+    if (nxt < n_tiles) load_tile<D>(TB, p.pool, sm_pg + tile_off, nxt, p.num_pages, kvh, r, g, n_pages_split);
+    compute_tile<D, G>(TA, st, qB, q_own, q_oth, t_begin + tile * 64 + 16 * g, t_end, is_hi,
+                       live, g, sm_sc[wave]);
+    tile = nxt;
+    if (tile >= n_tiles) break;
+    nxt = tile + NW;
+    if (nxt < n_tiles) load_tile<D>(TA, p.pool, sm_pg + tile_off, nxt, p.num_pages, kvh, r, g, n_pages_split);
+    compute_tile<D, G>(TB, st, qB, q_own, q_oth, t_begin + tile * 64 + 16 * g, t_end, is_hi,
+                       live, g, sm_sc[wave]);
+    tile = nxt;
   }
 
   // ---- merge the NW waves of the workgroup --------------------------------------
@@ -303,15 +432,15 @@ __global__ __launch_bounds__(64 * NW) void gqa_decode_int8_kernel(DecodeParams p
   __shared__ float sm_l[NW][G];
   __shared__ float sm_o[NW][G][D];
   if (g == 0 && is_hi && live) {
-    sm_m[wave][h] = m_run;
-    sm_l[wave][h] = l_run;
+    sm_m[wave][h] = st.m_run;
+    sm_l[wave][h] = st.l_run;
   }
 #pragma unroll
   for (int jb = 0; jb < JB; ++jb)
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int hd = 2 * g + hh;
-      if (hd < G) sm_o[wave][hd][16 * jb + r] = acc[jb][hh];
+      if (hd < G) sm_o[wave][hd][16 * jb + r] = st.acc[jb][hh];
     }
   __syncthreads();
 
@@ -339,19 +468,30 @@ __global__ __launch_bounds__(64 * NW) void gqa_decode_int8_kernel(DecodeParams p
       }
     }
   }
+  if (!p.merge_in_kernel) {
+    // every sequence records its split range, single-split ones included, so
+    // the combine kernel never reads a previous launch's entry
+    if (split == 0 && threadIdx.x == 0 && kvh == 0) {
+      p.seq_info[2 * b] = split_base;
+      p.seq_info[2 * b + 1] = nsplit;
+    }
+    return;
+  }
   if (nsplit == 1) return;
 
-  // ---- last workgroup of this (sequence, kv head) merges the splits -----------
+  // ---- in-kernel merge: the last workgroup of (b, kvh) to finish merges -------
+  // One agent-scope release (thread 0, after the barrier has made every
+  // wave's partial stores complete) and one acquire; the counter resets itself.
   __shared__ int sm_last;
-  __threadfence();
   __syncthreads();
   if (threadIdx.x == 0) {
+    __threadfence();
     const int prev = atomicAdd(&p.counters[b * p.kv_heads + kvh], 1);
     sm_last = (prev == nsplit - 1);
+    if (sm_last) __threadfence();
   }
   __syncthreads();
   if (!sm_last) return;
-  __threadfence();
   const size_t stride = (size_t)p.kv_heads * (G * (D + 2));
   const float* p0 = p.partials + ((size_t)split_base * p.kv_heads + kvh) * (G * (D + 2));
   for (int t = threadIdx.x; t < G * D; t += 64 * NW) {
@@ -371,21 +511,56 @@ __global__ __launch_bounds__(64 * NW) void gqa_decode_int8_kernel(DecodeParams p
   if (threadIdx.x == 0) atomicExch(&p.counters[b * p.kv_heads + kvh], 0);
 }
 
+// Merge of the split partials of one (sequence, kv head): grid (batch, Hkv).
 template <int D, int G>
-hipError_t launch_dg(const DecodeParams& p, int work_items, hipStream_t st) {
-  constexpr int NW = 4;
-  hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, NW>), dim3(work_items, p.kv_heads),
-                     dim3(64 * NW), 0, st, p);
+__global__ __launch_bounds__(256) void gqa_decode_combine_kernel(DecodeParams p) {
+  const int b = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int split_base = p.seq_info[2 * b];
+  const int nsplit = p.seq_info[2 * b + 1];
+  if (nsplit <= 1) return;
+  const int Hq = p.kv_heads * G;
+  const size_t stride = (size_t)p.kv_heads * (G * (D + 2));
+  const float* p0 = p.partials + ((size_t)split_base * p.kv_heads + kvh) * (G * (D + 2));
+  for (int t = threadIdx.x; t < G * D; t += 256) {
+    const int hd = t / D, d = t % D;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p0[s * stride + hd * (D + 2)]);
+    float Ls = 0.0f, O = 0.0f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float* ps = p0 + s * stride + hd * (D + 2);
+      if (ps[0] == -INFINITY) continue;
+      const float f = fast_exp2(ps[0] - M);
+      Ls += ps[1] * f;
+      O += ps[2 + d] * f;
+    }
+    p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+  }
+}
+
+template <int D, int G>
+hipError_t launch_dg(const DecodeParams& p, int work_items, bool combine, hipStream_t st) {
+  if (p.waves == 8)
+    hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, 8>), dim3(work_items, p.kv_heads), dim3(512),
+                       0, st, p);
+  else
+    hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, 4>), dim3(work_items, p.kv_heads), dim3(256),
+                       0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !combine || p.merge_in_kernel) return e;
+  hipLaunchKernelGGL((gqa_decode_combine_kernel<D, G>), dim3(p.batch, p.kv_heads), dim3(256), 0,
+                     st, p);
   return hipGetLastError();
 }
 
 template <int D>
-hipError_t launch_d(const DecodeParams& p, int group, int work_items, hipStream_t st) {
+hipError_t launch_d(const DecodeParams& p, int group, int work_items, bool combine,
+                    hipStream_t st) {
   switch (group) {
-    case 1: return launch_dg<D, 1>(p, work_items, st);
-    case 2: return launch_dg<D, 2>(p, work_items, st);
-    case 4: return launch_dg<D, 4>(p, work_items, st);
-    case 8: return launch_dg<D, 8>(p, work_items, st);
+    case 1: return launch_dg<D, 1>(p, work_items, combine, st);
+    case 2: return launch_dg<D, 2>(p, work_items, combine, st);
+    case 4: return launch_dg<D, 4>(p, work_items, combine, st);
+    case 8: return launch_dg<D, 8>(p, work_items, combine, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -393,10 +568,13 @@ hipError_t launch_d(const DecodeParams& p, int group, int work_items, hipStream_
 }  // namespace
 
 hipError_t launch_gqa_decode(const DecodeParams& p, int head_dim, int group, int quant,
-                             int work_items, hipStream_t st) {
+                             int work_items, bool combine, hipStream_t st) {
   if (quant != kQuantInt8) return hipErrorInvalidValue;
-  if (head_dim == 64) return launch_d<64>(p, group, work_items, st);
-  if (head_dim == 128) return launch_d<128>(p, group, work_items, st);
+  if (p.split_tokens <= 0 || p.split_tokens % 64 != 0 ||
+      p.split_tokens > kMaxSplitPages * kPageTokens)
+    return hipErrorInvalidValue;
+  if (head_dim == 64) return launch_d<64>(p, group, work_items, combine, st);
+  if (head_dim == 128) return launch_d<128>(p, group, work_items, combine, st);
   return hipErrorInvalidValue;
 }
 

@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256) void gqa_prefill_int8_kernel(PrefillParams p) 
       const int tok = c / (D / 16);
       const int dp = c % (D / 16);
       const int pg = min((t0 + tok) / kPageTokens, last_page);
-      const uint8_t* blk = p.pool + ((size_t)pt[pg] * p.kv_heads + kvh) * BB;
+      const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
       const uint4 w = *(const uint4*)(blk + (size_t)((t0 + tok) % kPageTokens) * D + 16 * dp);
       uint32_t h[8];
       codes4_to_f16(w.x, h[0], h[1]);
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(256) void gqa_prefill_int8_kernel(PrefillParams p) 
       const int cb = c / D;
       const int d = c % D;
       const int pg = min(t0 / kPageTokens + cb, last_page);
-      const uint8_t* blk = p.pool + ((size_t)pt[pg] * p.kv_heads + kvh) * BB;
+      const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
       const uint4 w = *(const uint4*)(blk + 16 * D + (size_t)d * 16);
       const int kst = cb >> 1;
       const int half = (cb & 1) * 4;
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256) void gqa_prefill_int8_kernel(PrefillParams p) 
       const int which = tid >> 6;
       const int tok = tid & 63;
       const int pg = min((t0 + tok) / kPageTokens, last_page);
-      const uint8_t* blk = p.pool + ((size_t)pt[pg] * p.kv_heads + kvh) * BB;
+      const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
       const float v = ((const float*)(blk + 32 * D + 64 * which))[(t0 + tok) % kPageTokens];
       const bool ok = t0 + tok < total;
       if (which == 0)

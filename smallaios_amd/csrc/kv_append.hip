@@ -8,15 +8,10 @@
 // absolute maximum (int8) or the group's min/max (int4, 32 lanes per group) are
 // wave reductions; max/min are exact, so the reduction order cannot change the
 // scale.
-//
-// Bit-exactness with the reference's Rust f32 semantics:
-//   * RoPE is `c*x0 - s*x1`, `s*x0 + c*x1` with every product rounded on its
-//     own (this file is built with -ffp-contract=off and the pragma below);
-//   * x / s is the IEEE correctly rounded division (hipcc default
-//     -fhip-fp32-correctly-rounded-divide-sqrt);
-//   * round_half_even(x) == rintf(x) for every f32 once clamped to the int8
-//     code range (checked exhaustively on the CPU by the test suite);
-//   * float -> int conversions restate Rust's saturating `as` casts.
+// The row arithmetic (and why it is bit-exact with the reference's f32
+// semantics) is in append_row.h; this file is also built with
+// -ffp-contract=off.
+#include "append_row.h"
 #include "sai_internal.h"
 
 #pragma clang fp contract(off)
@@ -24,48 +19,6 @@
 namespace sai {
 
 namespace {
-
-// RoPE of one element. `first` = this element is x0 of its pair.
-// Reference: rotate_rope_block, onnx-rt/src/ops/microsoft.rs:137-160.
-__device__ __forceinline__ float rope_elem(float c, float s, float own, float partner,
-                                           bool first) {
-#pragma clang fp contract(off)
-  return first ? (c * own - s * partner) : (s * partner + c * own);
-}
-
-template <int D>
-__device__ __forceinline__ void rope_row(float (&x)[D / 64], int lane, int pos,
-                                         const AppendParams& p) {
-  constexpr int J = D / 64;
-  constexpr int HALF = D / 2;
-  float xp[J];
-  if (p.interleaved) {
-#pragma unroll
-    for (int j = 0; j < J; ++j) xp[j] = __shfl_xor(x[j], 1, 64);
-  } else if constexpr (HALF >= 64) {
-#pragma unroll
-    for (int j = 0; j < J; ++j) xp[j] = x[j ^ (HALF / 64)];
-  } else {
-#pragma unroll
-    for (int j = 0; j < J; ++j) xp[j] = __shfl_xor(x[j], HALF, 64);
-  }
-  const float* cr = p.cos_cache + (size_t)pos * HALF;
-  const float* sr = p.sin_cache + (size_t)pos * HALF;
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int e = lane + 64 * j;
-    int i;
-    bool first;
-    if (p.interleaved) {
-      i = e >> 1;
-      first = (e & 1) == 0;
-    } else {
-      first = e < HALF;
-      i = first ? e : e - HALF;
-    }
-    x[j] = rope_elem(cr[i], sr[i], x[j], xp[j], first);
-  }
-}
 
 template <int D>
 __device__ __forceinline__ void decode_row(const AppendParams& p, long row, int& b, int& s,
@@ -79,7 +32,6 @@ __device__ __forceinline__ void decode_row(const AppendParams& p, long row, int&
 // ---------------------------------------------------------------- int8 ----
 template <int D>
 __global__ __launch_bounds__(256) void kv_append_int8_kernel(AppendParams p) {
-  constexpr int J = D / 64;
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   const long rows = (long)p.batch * p.s_new * p.kv_heads;
@@ -88,35 +40,12 @@ __global__ __launch_bounds__(256) void kv_append_int8_kernel(AppendParams p) {
   decode_row<D>(p, row, b, s, h);
   const int pos = p.seq_lens[b] + s;
   const int page = p.page_table[(size_t)b * p.max_pages + pos / kPageTokens];
-  const int slot = pos % kPageTokens;
-  uint8_t* blk = p.pool + ((size_t)page * p.kv_heads + h) * block_bytes_int8(D);
+  uint8_t* blk = p.pool + block_offset(page, h, p.num_pages, block_bytes_int8(D));
   const size_t src = (size_t)row * D;  // [b][s][h][D] == row * D
-
-#pragma unroll
-  for (int which = 0; which < 2; ++which) {
-    float x[J];
-    const void* in = which == 0 ? p.k : p.v;
-#pragma unroll
-    for (int j = 0; j < J; ++j) x[j] = load_elem(in, src + lane + 64 * j, p.dtype);
-    if (which == 0 && p.do_rotary) rope_row<D>(x, lane, pos, p);
-
-    float a = 0.0f;
-#pragma unroll
-    for (int j = 0; j < J; ++j) a = fmaxf(a, fabsf(x[j]));
-    a = wave_max(a);
-    const float sc = (a > 0.0f) ? a / 127.0f : 1.0f;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      int32_t q = sat_i32(rintf(x[j] / sc));
-      q = q < -128 ? -128 : (q > 127 ? 127 : q);
-      const int e = lane + 64 * j;
-      if (which == 0)
-        blk[(size_t)slot * D + e] = (uint8_t)(int8_t)q;
-      else
-        blk[(size_t)16 * D + (size_t)e * 16 + slot] = (uint8_t)(int8_t)q;
-    }
-    if (lane == 0) ((float*)(blk + 32 * D + 64 * which))[slot] = sc;
-  }
+  const size_t esz = p.dtype == kDtypeBf16 ? 2 : 4;
+  append_row_int8<D>((const uint8_t*)p.k + src * esz, (const uint8_t*)p.v + src * esz, p.dtype,
+                     lane, pos, blk, pos % kPageTokens, p.do_rotary, p.interleaved != 0,
+                     p.cos_cache, p.sin_cache);
 }
 
 // ---------------------------------------------------------------- int4 ----
@@ -183,7 +112,7 @@ __global__ __launch_bounds__(256) void kv_append_int4_kernel(AppendParams p, int
   if (!fresh[0] && !fresh[1]) return;  // pair past the new tokens: nothing to write
   const int page = p.page_table[(size_t)b * p.max_pages + pos0 / kPageTokens];
   const int slot0 = pos0 % kPageTokens;
-  uint8_t* blk = p.pool + ((size_t)page * p.kv_heads + h) * block_bytes_int4(D);
+  uint8_t* blk = p.pool + block_offset(page, h, p.num_pages, block_bytes_int4(D));
 
   // new nibble codes of V for (token 0/1 of the pair, element lane + 64j)
   uint32_t vq[2][J];
@@ -203,8 +132,7 @@ __global__ __launch_bounds__(256) void kv_append_int4_kernel(AppendParams p, int
 #pragma unroll
       for (int j = 0; j < J; ++j) x[j] = load_elem(in, src + lane + 64 * j, p.dtype);
       if (which == 0 && p.do_rotary) {
-        // rope_row reads p.cos/sin at `pos`
-        rope_row<D>(x, lane, pos, p);
+        rope_row_wave<D>(x, lane, pos, p.cos_cache, p.sin_cache, p.interleaved != 0);
       }
       uint16_t* sz = (uint16_t*)(blk + 16 * D + 64 * NG * which) + (size_t)slot * NG * 2;
 #pragma unroll

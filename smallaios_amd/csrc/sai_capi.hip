@@ -26,9 +26,13 @@ struct sai_ctx {
   std::string err;
   float* partials = nullptr;
   size_t partial_floats = 0;
+  int32_t* seq_info = nullptr;
+  size_t seq_info_n = 0;
   int32_t* counters = nullptr;
   size_t counter_n = 0;
   int32_t decode_split = 0;  // 0 = automatic
+  int32_t decode_waves = 4;
+  int32_t decode_merge = 0;  // 0: combine kernel, 1: in-kernel merge
   int32_t last_wg = 0;
   int32_t last_split = 0;
 };
@@ -77,6 +81,9 @@ float sqrt_f32_newton(float x) {
   }
   return guess;
 }
+
+// Largest decode split (the kernel stages a split's page ids in LDS).
+constexpr int32_t kMaxDecodeSplit = 16384;
 
 bool supported_dims(int head_dim, int quant) {
   if (head_dim != 64 && head_dim != 128) return false;
@@ -131,16 +138,8 @@ sai_status check_rope(sai_ctx* ctx, const sai_kvcache* c, int32_t batch, int32_t
   return SAI_OK;
 }
 
-sai_status ensure_workspace(sai_ctx* ctx, size_t partial_floats, size_t counters) {
-  if (partial_floats > ctx->partial_floats) {
-    if (ctx->partials) (void)hipFree(ctx->partials);
-    ctx->partials = nullptr;
-    ctx->partial_floats = 0;
-    size_t n = std::max(partial_floats, (size_t)1 << 20);
-    hipError_t e = hipMalloc(&ctx->partials, n * sizeof(float));
-    if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "decode workspace: %s", hipGetErrorString(e));
-    ctx->partial_floats = n;
-  }
+sai_status ensure_workspace(sai_ctx* ctx, size_t partial_floats, size_t seq_info,
+                            size_t counters) {
   if (counters > ctx->counter_n) {
     if (ctx->counters) (void)hipFree(ctx->counters);
     ctx->counters = nullptr;
@@ -151,6 +150,24 @@ sai_status ensure_workspace(sai_ctx* ctx, size_t partial_floats, size_t counters
     e = hipMemset(ctx->counters, 0, n * sizeof(int32_t));
     if (e != hipSuccess) return hip_fail(ctx, e, "decode counters memset");
     ctx->counter_n = n;
+  }
+  if (partial_floats > ctx->partial_floats) {
+    if (ctx->partials) (void)hipFree(ctx->partials);
+    ctx->partials = nullptr;
+    ctx->partial_floats = 0;
+    size_t n = std::max(partial_floats, (size_t)1 << 20);
+    hipError_t e = hipMalloc(&ctx->partials, n * sizeof(float));
+    if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "decode workspace: %s", hipGetErrorString(e));
+    ctx->partial_floats = n;
+  }
+  if (seq_info > ctx->seq_info_n) {
+    if (ctx->seq_info) (void)hipFree(ctx->seq_info);
+    ctx->seq_info = nullptr;
+    ctx->seq_info_n = 0;
+    size_t n = std::max(seq_info, (size_t)4096);
+    hipError_t e = hipMalloc(&ctx->seq_info, n * sizeof(int32_t));
+    if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "decode sequence info: %s", hipGetErrorString(e));
+    ctx->seq_info_n = n;
   }
   return SAI_OK;
 }
@@ -177,6 +194,7 @@ SAI_API void sai_destroy(sai_ctx* ctx) {
   if (!ctx) return;
   DeviceGuard dg(ctx->device);
   if (ctx->partials) (void)hipFree(ctx->partials);
+  if (ctx->seq_info) (void)hipFree(ctx->seq_info);
   if (ctx->counters) (void)hipFree(ctx->counters);
   delete ctx;
 }
@@ -196,7 +214,21 @@ SAI_API int32_t sai_device_supported(int device) {
 SAI_API int32_t sai_set_decode_split(sai_ctx* ctx, int32_t tokens) {
   if (!ctx) return 0;
   int32_t prev = ctx->decode_split;
-  if (tokens >= 0 && tokens % 64 == 0) ctx->decode_split = tokens;
+  if (tokens >= 0 && tokens % 64 == 0 && tokens <= kMaxDecodeSplit) ctx->decode_split = tokens;
+  return prev;
+}
+
+SAI_API int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves) {
+  if (!ctx) return 0;
+  int32_t prev = ctx->decode_waves;
+  if (waves == 4 || waves == 8) ctx->decode_waves = waves;
+  return prev;
+}
+
+SAI_API int32_t sai_set_decode_merge(sai_ctx* ctx, int32_t in_kernel) {
+  if (!ctx) return 0;
+  int32_t prev = ctx->decode_merge;
+  ctx->decode_merge = in_kernel ? 1 : 0;
   return prev;
 }
 
@@ -388,7 +420,7 @@ SAI_API sai_status sai_kvcache_read(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
     // one block copy per page (re-used while t stays in the page)
     if (i == 0 || slot == 0) {
       hipError_t e = hipMemcpy(blk.data(),
-                               c->pools[layer] + ((size_t)page * d.num_kv_heads + kv_head) * c->block_bytes,
+                               c->pools[layer] + sai::block_offset(page, kv_head, d.num_pages, c->block_bytes),
                                c->block_bytes, hipMemcpyDeviceToHost);
       if (e != hipSuccess) return hip_fail(ctx, e, "kvcache_read");
     }
@@ -499,18 +531,16 @@ sai_status attention_common(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const v
 
 }  // namespace
 
-SAI_API sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
-                                  int32_t dtype, int32_t batch, int32_t num_heads,
-                                  const float* cos_cache, const float* sin_cache,
-                                  int32_t cache_rows, int32_t do_rotary,
-                                  int32_t rotary_interleaved, int32_t has_scale, float scale,
-                                  float* out, void* stream) {
-  if (!ctx || !c) return SAI_ERR_NULL;
+namespace {
+
+// Shared by sai_gqa_decode and sai_gqa_with_cache (k_new/v_new non-null: the
+// decode kernel appends the step's token itself).
+sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
+                         int32_t dtype, int32_t batch, int32_t G, const float* cos_cache,
+                         const float* sin_cache, int32_t cache_rows, int32_t do_rotary,
+                         int32_t rotary_interleaved, int32_t has_scale, float scale, float* out,
+                         const void* k_new, const void* v_new, int32_t kv_dtype, void* stream) {
   const char* op = "gqa_decode";
-  int32_t G = 0;
-  sai_status st = attention_common(ctx, c, layer, q, dtype, batch, 1, num_heads, cos_cache,
-                                   sin_cache, cache_rows, do_rotary, out, op, &G);
-  if (st != SAI_OK) return st;
   if (c->desc.quant != SAI_KV_INT8)
     return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: int4 decode is not built yet", op);
   const int D = c->desc.head_dim;
@@ -524,14 +554,21 @@ SAI_API sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, c
     const int64_t target_wg = (int64_t)ctx->num_cus * 4;
     int64_t s = (tok_heads + target_wg - 1) / target_wg;
     s = ((s + 63) / 64) * 64;
-    split = (int32_t)std::max<int64_t>(256, std::min<int64_t>(s, 1 << 20));
+    split = (int32_t)std::max<int64_t>(256, std::min<int64_t>(s, kMaxDecodeSplit));
   }
+  split = std::min(split, kMaxDecodeSplit);
   int64_t work = 0;
-  for (int b = 0; b < batch; ++b) work += (c->h_seq_lens[b] + 1 + split - 1) / split;
+  bool multi = false;
+  for (int b = 0; b < batch; ++b) {
+    const int64_t n = (c->h_seq_lens[b] + 1 + split - 1) / split;
+    work += n;
+    multi = multi || n > 1;
+  }
   if (work <= 0 || work > 0x7FFFFFFF)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: bad work size", op);
   DeviceGuard dg(ctx->device);
-  st = ensure_workspace(ctx, (size_t)work * kvh * G * (D + 2), (size_t)batch * kvh);
+  sai_status st = ensure_workspace(ctx, (size_t)work * kvh * G * (D + 2), (size_t)batch * 2,
+                                   (size_t)batch * kvh);
   if (st != SAI_OK) return st;
 
   sai::DecodeParams p{};
@@ -554,13 +591,67 @@ SAI_API sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, c
   const float sc = has_scale ? scale : sai_default_scale(D);
   p.scale_log2 = sc * 1.4426950408889634f;
   p.split_tokens = split;
+  p.waves = ctx->decode_waves;
   p.partials = ctx->partials;
+  p.seq_info = ctx->seq_info;
+  p.merge_in_kernel = ctx->decode_merge;
   p.counters = ctx->counters;
-  hipError_t e = sai::launch_gqa_decode(p, D, G, c->desc.quant, (int)work, (hipStream_t)stream);
+  p.k_new = k_new;
+  p.v_new = v_new;
+  p.kv_dtype = kv_dtype;
+  hipError_t e =
+      sai::launch_gqa_decode(p, D, G, c->desc.quant, (int)work, multi, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gqa_decode launch");
   ctx->last_wg = (int32_t)(work * kvh);
   ctx->last_split = split;
   return SAI_OK;
+}
+
+}  // namespace
+
+SAI_API sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
+                                  int32_t dtype, int32_t batch, int32_t num_heads,
+                                  const float* cos_cache, const float* sin_cache,
+                                  int32_t cache_rows, int32_t do_rotary,
+                                  int32_t rotary_interleaved, int32_t has_scale, float scale,
+                                  float* out, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  int32_t G = 0;
+  sai_status st = attention_common(ctx, c, layer, q, dtype, batch, 1, num_heads, cos_cache,
+                                   sin_cache, cache_rows, do_rotary, out, "gqa_decode", &G);
+  if (st != SAI_OK) return st;
+  return launch_decode(ctx, c, layer, q, dtype, batch, G, cos_cache, sin_cache, cache_rows,
+                       do_rotary, rotary_interleaved, has_scale, scale, out, nullptr, nullptr,
+                       SAI_DTYPE_F32, stream);
+}
+
+SAI_API sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
+                                      const void* q, int32_t q_dtype, const void* k_new,
+                                      const void* v_new, int32_t kv_dtype, int32_t batch,
+                                      int32_t num_heads, const float* cos_cache,
+                                      const float* sin_cache, int32_t cache_rows,
+                                      int32_t do_rotary, int32_t rotary_interleaved,
+                                      int32_t has_scale, float scale, float* out, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "gqa_with_cache";
+  if (!k_new || !v_new) return fail(ctx, SAI_ERR_NULL, "%s: missing key/value", op);
+  if (kv_dtype != SAI_DTYPE_F32 && kv_dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (want f32 or bf16)", op, kv_dtype);
+  if (c->pending != 0 && c->pending != 1)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                "%s: %d tokens pending from another layer of this pass, got 1", op, c->pending);
+  // the token appended here is the pending one the attention sees
+  const int32_t prev_pending = c->pending;
+  c->pending = 1;
+  int32_t G = 0;
+  sai_status st = attention_common(ctx, c, layer, q, q_dtype, batch, 1, num_heads, cos_cache,
+                                   sin_cache, cache_rows, do_rotary, out, op, &G);
+  if (st == SAI_OK)
+    st = launch_decode(ctx, c, layer, q, q_dtype, batch, G, cos_cache, sin_cache, cache_rows,
+                       do_rotary, rotary_interleaved, has_scale, scale, out, k_new, v_new,
+                       kv_dtype, stream);
+  if (st != SAI_OK) c->pending = prev_pending;
+  return st;
 }
 
 SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,

@@ -1,7 +1,9 @@
 // Internal definitions shared by the gfx950 kernels and the C ABI.
 //
-// Paged cache layout (one pool per layer, page p, kv head h):
-//   block(p, h) = pool + (p * Hkv + h) * block_bytes
+// Paged cache layout (one pool per layer, page p, kv head h), kv-head major so
+// that the pages of one sequence and head (identity or clustered page tables)
+// form one contiguous stream for the decode workgroup that reads them:
+//   block(p, h) = pool + (h * num_pages + p) * block_bytes
 //
 // INT8 block, D = head_dim, 16 tokens:
 //   [0,        16*D)        K codes, row-major [slot][D]        (int8)
@@ -36,6 +38,9 @@ constexpr int kDtypeBf16 = 16;
 
 __host__ __device__ constexpr size_t block_bytes_int8(int d) { return (size_t)32 * d + 128; }
 __host__ __device__ constexpr size_t block_bytes_int4(int d) { return (size_t)20 * d; }
+__host__ __device__ inline size_t block_offset(int page, int head, int num_pages, size_t bb) {
+  return ((size_t)head * num_pages + page) * bb;
+}
 
 // ---- device helpers ---------------------------------------------------------
 
@@ -111,8 +116,14 @@ struct DecodeParams {
   int cache_rows, do_rotary, interleaved;
   float scale_log2;   // softmax scale * log2(e)
   int split_tokens;   // tokens per workgroup, multiple of 64
+  int waves;          // waves per workgroup (4 or 8)
   float* partials;    // [work_items * Hkv][G][D + 2]
-  int32_t* counters;  // [batch * Hkv], zero between launches
+  int32_t* seq_info;  // [batch][2]: first work item, number of splits
+  int merge_in_kernel;  // 1: last workgroup merges the splits (counters)
+  int32_t* counters;    // [batch * Hkv], zero between launches
+  const void* k_new;    // fused append: [batch, 1, Hkv*D] pre-RoPE K, or null
+  const void* v_new;
+  int kv_dtype;
 };
 
 struct PrefillParams {
@@ -135,7 +146,7 @@ struct PrefillParams {
 // Launchers (return hipError_t of the launch).
 hipError_t launch_kv_append(const AppendParams& p, int head_dim, int quant, hipStream_t s);
 hipError_t launch_gqa_decode(const DecodeParams& p, int head_dim, int group, int quant,
-                             int work_items, hipStream_t s);
+                             int work_items, bool combine, hipStream_t s);
 hipError_t launch_gqa_prefill(const PrefillParams& p, int head_dim, int group, int quant,
                               hipStream_t s);
 hipError_t launch_seq_advance(int32_t* seq_lens, int batch, int pending, hipStream_t s);

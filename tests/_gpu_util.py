@@ -131,6 +131,19 @@ class Case:
         torch.cuda.synchronize()
         return out.cpu().numpy()
 
+    def step_fused(self, q, q_dtype="f32", scale=None):
+        """Append the step's token and attend in one launch (sai_gqa_with_cache)."""
+        import torch
+        k, v = self.kv(1)
+        self.ocache.append(k, v, self.cos, self.sin, self.do_rotary, self.interleaved)
+        out = torch.zeros((self.batch, 1, self.hq * self.d), dtype=torch.float32, device="cuda")
+        self.cache.decode_with_cache(0, dev(q, q_dtype), dev(k, self.kv_dtype),
+                                     dev(v, self.kv_dtype), out, self.batch, self.hq, self.cos_d,
+                                     self.sin_d, self.cos.shape[0], self.do_rotary,
+                                     self.interleaved, scale)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
     def gpu_prefill(self, q, q_dtype="f32", scale=None):
         import torch
         out = torch.zeros((self.batch, self.new_tokens, self.hq * self.d), dtype=torch.float32,

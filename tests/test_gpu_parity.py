@@ -139,6 +139,29 @@ def test_decode_split_merge(rt, split):
         rt.set_decode_split(prev)
 
 
+@pytest.mark.parametrize("merge_in_kernel", [False, True])
+@pytest.mark.parametrize("split", [64, 4096])
+def test_decode_fused_step(rt, merge_in_kernel, split):
+    """sai_gqa_with_cache: the decode kernel appends the token itself (codes
+    bit-exact with the standalone append) and merges splits in-kernel or in the
+    combine kernel; repeated steps advance the cache."""
+    log(f"fused decode step merge_in_kernel={merge_in_kernel} split={split}")
+    prev_m = rt.set_decode_merge(merge_in_kernel)
+    prev_s = rt.set_decode_split(split)
+    try:
+        c = Case(rt, 91, 3, 32, 8, 128, [700, 5, 4100], 1, theta=5e5, kv_dtype="bf16",
+                 permute_pages=True, extra_tokens=2)
+        for step in range(3):
+            q = c.query("bf16")
+            got = c.step_fused(q, "bf16")
+            assert_close(got, c.oracle_attend(q), f"fused step {step}")
+            c.check_codes(seqs=[1])
+            c.cache.advance()
+    finally:
+        rt.set_decode_merge(prev_m)
+        rt.set_decode_split(prev_s)
+
+
 def test_decode_first_token_equals_v(rt):
     """One visible key: the output is that key's dequantised V (cf. the
     reference's test_gpu_gqa_first_token_no_history)."""
