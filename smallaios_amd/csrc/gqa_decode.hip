@@ -265,14 +265,21 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   const int kvh = blockIdx.y;
   const int work = blockIdx.x;
 
-  // ---- (sequence, split) of this workgroup: prefix scan over split counts ----
+  // ---- (sequence, split) of this workgroup ------------------------------------
+  // Uniform split count (every sequence has p.uniform_nsplit splits): direct
+  // mapping. Ragged: prefix scan over the per-sequence split counts.
   int b = -1, split = 0, nsplit = 0, split_base = 0;
-  {
+  if (p.uniform_nsplit > 0) {
+    nsplit = p.uniform_nsplit;
+    b = work / nsplit;
+    split = work - b * nsplit;
+    split_base = b * nsplit;
+  } else {
     int base = 0;
     for (int c0 = 0; c0 < p.batch; c0 += 64) {
       const int bi = c0 + lane;
-      const int L = bi < p.batch ? p.seq_lens[bi] + p.pending : 0;
-      const int n = (L + p.split_tokens - 1) / p.split_tokens;
+      const int Lb = bi < p.batch ? p.seq_lens[bi] + p.pending : 0;
+      const int n = (Lb + p.split_tokens - 1) / p.split_tokens;
       int incl = n;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
@@ -292,35 +299,42 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
       base += total;
     }
   }
-  if (b < 0) return;  // uniform over the workgroup
+  if (b < 0 || b >= p.batch) return;  // uniform over the workgroup
+
+  // page ids of the split, loaded before the length is known (the page-table
+  // row has max_pages entries; the split's range is clamped to it)
+  const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
+  const int first_page = split * (p.split_tokens / kPageTokens);
+  __shared__ int sm_pg[kMaxSplitPages];
+  const int split_pages = p.split_tokens / kPageTokens;
+  for (int i = threadIdx.x; i < split_pages; i += 64 * NW)
+    sm_pg[i] = pt[min(first_page + i, p.max_pages - 1)];
 
   const int L = p.seq_lens[b] + p.pending;
   const int t_begin = split * p.split_tokens;
   const int t_end = min(L, t_begin + p.split_tokens);
   const int Hq = p.kv_heads * G;
-  const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
+  const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
+  const int n_tiles = (t_end - t_begin + 63) / 64;
+  // the wave that streams the split's last tile (it holds the newest token)
+  const int last_owner = (n_tiles - 1) % NW;
+  __syncthreads();
 
-  // ---- fused append: the split holding the new token writes it first ----------
-  if (p.k_new != nullptr && split == nsplit - 1 && wave == 0) {
+  // ---- fused append: the last tile's owner writes the new token first ---------
+  if (p.k_new != nullptr && split == nsplit - 1 && wave == last_owner) {
     const int pos = L - 1;
     uint8_t* blk = (uint8_t*)p.pool +
-                   block_offset(pt[pos / kPageTokens], kvh, p.num_pages, block_bytes_int8(D));
+                   block_offset(sm_pg[pos / kPageTokens - first_page], kvh, p.num_pages,
+                                block_bytes_int8(D));
     const size_t row = ((size_t)b * p.kv_heads + kvh) * D * (p.kv_dtype == kDtypeBf16 ? 2 : 4);
     append_row_int8<D>((const uint8_t*)p.k_new + row, (const uint8_t*)p.v_new + row, p.kv_dtype,
                        lane, pos, blk, pos % kPageTokens, p.do_rotary, p.interleaved != 0,
                        p.cos_cache, p.sin_cache);
+    // this wave reads the page back in its last tile: order the stores first
     __threadfence_block();
   }
 
-  // ---- page ids of the split -> LDS --------------------------------------------
-  __shared__ int sm_pg[kMaxSplitPages];
-  const int first_page = t_begin / kPageTokens;
-  const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
-  for (int i = threadIdx.x; i < n_pages_split; i += 64 * NW) sm_pg[i] = pt[first_page + i];
-  __syncthreads();
-
   // ---- first tile in flight while Q is prepared ----------------------------------
-  const int n_tiles = (t_end - t_begin + 63) / 64;
   const int tile_off = 0;  // splits start on a tile (64-token) boundary
   TileRegs<D> TA;
   int tile = wave;
@@ -412,19 +426,29 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
 #pragma unroll
   for (int jb = 0; jb < JB; ++jb) st.acc[jb][0] = st.acc[jb][1] = 0.0f;
 
+  // Ping-pong over this wave's tiles wave, wave+NW, ... Every prefetch inside
+  // the loop is unconditional (straight-line code), so the compiler's wait
+  // counts only cover the tile being computed, never the one in flight.
   TileRegs<D> TB;
-  while (tile < n_tiles) {
-    int nxt = tile + NW;
-    if (nxt < n_tiles) load_tile<D>(TB, p.pool, sm_pg + tile_off, nxt, p.num_pages, kvh, r, g, n_pages_split);
-    compute_tile<D, G>(TA, st, qB, q_own, q_oth, t_begin + tile * 64 + 16 * g, t_end, is_hi,
-                       live, g, sm_sc[wave]);
-    tile = nxt;
-    if (tile >= n_tiles) break;
-    nxt = tile + NW;
-    if (nxt < n_tiles) load_tile<D>(TA, p.pool, sm_pg + tile_off, nxt, p.num_pages, kvh, r, g, n_pages_split);
-    compute_tile<D, G>(TB, st, qB, q_own, q_oth, t_begin + tile * 64 + 16 * g, t_end, is_hi,
-                       live, g, sm_sc[wave]);
-    tile = nxt;
+  const int my_tiles = tile < n_tiles ? (n_tiles - 1 - tile) / NW + 1 : 0;
+  auto tok0 = [&](int k) { return t_begin + (wave + k * NW) * 64 + 16 * g; };
+  auto ld = [&](TileRegs<D>& T, int k) {
+    load_tile<D>(T, p.pool, sm_pg + tile_off, wave + k * NW, p.num_pages, kvh, r, g,
+                 n_pages_split);
+  };
+  int k = 0;
+  for (; k + 2 < my_tiles; k += 2) {
+    ld(TB, k + 1);
+    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), t_end, is_hi, live, g, sm_sc[wave]);
+    ld(TA, k + 2);
+    compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), t_end, is_hi, live, g, sm_sc[wave]);
+  }
+  if (k + 1 < my_tiles) {  // two left
+    ld(TB, k + 1);
+    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), t_end, is_hi, live, g, sm_sc[wave]);
+    compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), t_end, is_hi, live, g, sm_sc[wave]);
+  } else if (k < my_tiles) {  // one left
+    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), t_end, is_hi, live, g, sm_sc[wave]);
   }
 
   // ---- merge the NW waves of the workgroup --------------------------------------
