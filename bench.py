@@ -1,21 +1,26 @@
-"""Benchmark of the compressed-KV GQA decode step on one MI355X.
+"""Benchmark of the compressed-KV GQA path on one MI355X.
 
-Workload (the Llama-3-8B layer decode the metric is quoted on): 16 sequences,
-32 query / 8 kv heads, head_dim 128, uniform context 8192 (8191 cached tokens
-+ the step's token), Q bf16 ~ N(0,1), pre-RoPE K and V ~ N(0,1), RoPE theta
-500000, int8 KV with one f32 scale per (token, kv head), 16-token pages.
+Default workload (the one the headline metric is quoted on): Llama-3-8B layer
+decode -- 16 sequences, 32 query / 8 kv heads, head_dim 128, uniform context
+8192 (8191 cached tokens + the step's token), Q bf16 ~ N(0,1), pre-RoPE K and
+V ~ N(0,1), RoPE theta 500000, int8 KV with one f32 scale per (token, kv
+head), 16-token pages.
 
-One step = kernel 1 (RoPE + quantise + append the step's token for all 16x8
-(sequence, kv head) rows) + kernel 2 (split-K flash decode over the 8192
-tokens), i.e. one layer's attention for one generated token. The step's token
-goes to the same slot every step (append without advance), so the context
-stays at 8192.
+One decode step = one layer's attention for one generated token per
+sequence: RoPE + quantise + append the step's K/V and split-K flash decode
+over the whole context (sai_gqa_with_cache: one decode launch that also
+appends, plus the split-merge kernel). The step's token goes to the same slot
+every step (append without advance), so the context stays fixed.
 
-Printed (one JSON line): whole-step algorithmic HBM throughput of the decode
-attention (GB/s, `value`), % of the 8 TB/s peak, tokens/s, the decode
-kernel's own roofline from HIP events on its stream, and the oracle (the C
-restatement of the reference's single-threaded CPU path) timed on a bounded
-sample on the host cores.
+Other workloads (--workload, for the per-configuration table): `batch1`
+(8Q/2KV, head_dim 64, context 512), `ragged` (64 sequences with seeded
+lengths U[128, 16384], randomly permuted page table) and `prefill` (2 x 2048
+new tokens appended to a 6144-token cache, then causal MFMA attention).
+
+Printed: one JSON line with whole-step algorithmic throughput (`value`), % of
+peak, tokens/s, the dominant kernel's roofline from HIP events on its stream,
+and (default workload) the oracle -- the C restatement of the reference's
+single-threaded CPU path -- timed on a bounded sample on the host cores.
 """
 from __future__ import annotations
 
@@ -32,24 +37,47 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "decode attention HBM GB/s (% of peak) + tokens/s, 8k ctx int8 KV, 1 MI355X"
-PEAK_GBPS = 8000.0
-B, HQ, HKV, D, CTX, THETA = 16, 32, 8, 128, 8192, 500000.0
+HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E spec
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16/bf16 matrix peak
 PAGE = 16
 
+WORKLOADS = {
+    "llama8k": dict(kind="decode", batch=16, hq=32, hkv=8, d=128, lens=("uniform", 8192),
+                    theta=500000.0, q_dtype="bf16", permute=False),
+    "batch1": dict(kind="decode", batch=1, hq=8, hkv=2, d=64, lens=("uniform", 512),
+                   theta=10000.0, q_dtype="f32", permute=False),
+    "ragged": dict(kind="decode", batch=64, hq=32, hkv=8, d=128, lens=("uniform_rand", 128, 16384),
+                   theta=500000.0, q_dtype="bf16", permute=True),
+    "prefill": dict(kind="prefill", batch=2, hq=32, hkv=8, d=128, past=6144, new=2048,
+                    theta=500000.0, q_dtype="bf16", permute=False),
+}
 
-def algorithmic_bytes(b=B, hq=HQ, hkv=HKV, d=D, ctx=CTX):
-    """Bytes one decode step must move at minimum: int8 K+V codes, f32 K+V
-    scales, the bf16 query and the f32 output."""
-    codes = b * hkv * ctx * 2 * d
-    scales = b * hkv * ctx * 2 * 4
-    q = b * hq * d * 2
-    out = b * hq * d * 4
-    return codes + scales + q + out
+
+def decode_lengths(w, seed=0x5A1A0003):
+    kind = w["lens"][0]
+    if kind == "uniform":
+        return np.full(w["batch"], w["lens"][1], dtype=np.int64)
+    rng = np.random.default_rng(seed)
+    return rng.integers(w["lens"][1], w["lens"][2] + 1, size=w["batch"]).astype(np.int64)
+
+
+def decode_bytes(lens, hq, hkv, d, q_bytes):
+    """Algorithmic bytes of one decode step: int8 K+V codes and f32 K+V scales
+    of every visible token, the query and the f32 output."""
+    kv = int(lens.sum()) * hkv * (2 * d + 2 * 4)
+    return kv + len(lens) * hq * d * q_bytes + len(lens) * hq * d * 4
+
+
+def prefill_flops(batch, hq, d, past, new):
+    """QK^T + PV multiply-adds x2 over every (query, visible key) pair."""
+    keys = sum(past + i + 1 for i in range(new))
+    return 4 * d * hq * keys * batch
 
 
 def traffic_from_profile():
     """HBM bytes per decode launch measured with rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, calibrated against a copy kernel), if the summary is present."""
+    WRITE_SIZE, calibrated against a copy of known size), if the summary is
+    present."""
     path = os.path.join(ROOT, "profiles", "gqa_decode_llama8k_pmc.txt")
     try:
         with open(path) as f:
@@ -59,22 +87,28 @@ def traffic_from_profile():
         return None
 
 
-def build_cache(S, torch, rt, cos_d, sin_d):
-    pages = (CTX + PAGE - 1) // PAGE
-    cache = S.KvCache(rt, 1, HKV, D, B * pages, B, pages, S.KV_INT8)
-    cache.set_page_table(S.identity_page_table(B, pages))
+def build_cache(S, torch, rt, w, past_lens, extra_tokens, cos_d, sin_d, seed):
+    """Cache holding past_lens[b] tokens per sequence, appended by the HIP
+    append kernel in chunks (all sequences to max(past), then truncated)."""
+    b, hkv, d = w["batch"], w["hkv"], w["d"]
+    cap = int(past_lens.max()) + extra_tokens
+    pages = (cap + PAGE - 1) // PAGE
+    cache = S.KvCache(rt, 1, hkv, d, b * pages, b, pages, S.KV_INT8)
+    ids = np.arange(b * pages, dtype=np.int32)
+    if w["permute"]:
+        ids = np.random.default_rng(seed).permutation(ids).astype(np.int32)
+    cache.set_page_table(ids.reshape(b, pages))
     g = torch.Generator(device="cuda")
-    g.manual_seed(0x5A1A0001)
-    past = CTX - 1
-    chunk = 1024
-    done = 0
+    g.manual_seed(seed)
+    past, done, chunk = int(past_lens.max()), 0, 1024
     while done < past:
         n = min(chunk, past - done)
-        k = torch.randn((B, n, HKV * D), generator=g, device="cuda", dtype=torch.float32)
-        v = torch.randn((B, n, HKV * D), generator=g, device="cuda", dtype=torch.float32)
-        cache.append(0, k, v, B, n, cos_d, sin_d, cos_d.shape[0])
+        k = torch.randn((b, n, hkv * d), generator=g, device="cuda")
+        v = torch.randn((b, n, hkv * d), generator=g, device="cuda")
+        cache.append(0, k, v, b, n, cos_d, sin_d, cos_d.shape[0])
         cache.advance()
         done += n
+    cache.set_seq_lens(past_lens.astype(np.int32))
     torch.cuda.synchronize()
     return cache, g
 
@@ -100,16 +134,17 @@ def copy_bandwidth(torch):
     return 2 * n * 4 / (ms * 1e-3) / 1e9
 
 
-def cpu_baseline(seconds_target=12.0):
+def cpu_baseline(w, seconds_target=12.0):
     """The oracle (C restatement of the reference's CPU path, one thread) on a
-    bounded sample of the same workload: for each sampled sequence, quantise
-    the appended token, dequantise its 8192-token int8 cache, RoPE Q, copy the
-    present K/V and run the scalar f32 SDPA with expf_approx."""
+    bounded sample of the default workload: per sampled sequence, quantise the
+    appended token, dequantise its int8 cache, RoPE Q, copy the present K/V and
+    run the scalar f32 SDPA with expf_approx."""
     import oracle as O
     import smallaios_amd as S
+    hq, hkv, d, ctx, theta = w["hq"], w["hkv"], w["d"], w["lens"][1], w["theta"]
     rng = np.random.default_rng(7)
-    cos, sin = S.rope_tables(CTX, D, THETA)
-    oc = O.LogicalCache(1, HKV, D, CTX, O.INT8)
+    cos, sin = S.rope_tables(ctx, d, theta)
+    oc = O.LogicalCache(1, hkv, d, ctx, O.INT8)
     oc.k_codes[:] = rng.integers(-127, 128, oc.k_codes.shape, dtype=np.int8)
     oc.v_codes[:] = rng.integers(-127, 128, oc.v_codes.shape, dtype=np.int8)
     oc.k_scale[:] = rng.uniform(0.015, 0.035, oc.k_scale.shape).astype(np.float32)
@@ -117,30 +152,53 @@ def cpu_baseline(seconds_target=12.0):
     seqs = 0
     t0 = time.perf_counter()
     while True:
-        oc.seq_len[:] = CTX - 1
-        k = rng.standard_normal((1, 1, HKV * D), dtype=np.float32)
-        v = rng.standard_normal((1, 1, HKV * D), dtype=np.float32)
+        oc.seq_len[:] = ctx - 1
+        k = rng.standard_normal((1, 1, hkv * d), dtype=np.float32)
+        v = rng.standard_normal((1, 1, hkv * d), dtype=np.float32)
         q = O.bf16_bits_to_f32(O.f32_to_bf16_bits(
-            rng.standard_normal(HQ * D, dtype=np.float32))).reshape(1, 1, HQ * D)
+            rng.standard_normal(hq * d, dtype=np.float32))).reshape(1, 1, hq * d)
         oc.append(k, v, cos, sin)
-        oc.attend(q, HQ, cos, sin)
+        oc.attend(q, hq, cos, sin)
         seqs += 1
         el = time.perf_counter() - t0
-        if el >= seconds_target and seqs % B == 0:
+        if el >= seconds_target and seqs % w["batch"] == 0:
             break
-    per_seq = el / seqs
-    step_s = per_seq * B
+    step_s = el / seqs * w["batch"]
+    lens = decode_lengths(w)
     return {
-        "value": round(algorithmic_bytes() / step_s / 1e9, 4),
+        "value": round(decode_bytes(lens, hq, hkv, d, 2) / step_s / 1e9, 4),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"{seqs} sequences ({seqs // B} full steps of {B}) of the 8192-context "
-                   f"32Q/8KV int8 decode, one thread: {step_s * 1e3:.0f} ms per step, "
-                   f"{B / step_s:.2f} tokens/s"),
+        "sample": (f"{seqs} sequences ({seqs // w['batch']} full steps of {w['batch']}) of the "
+                   f"{ctx}-context {hq}Q/{hkv}KV int8 decode, one thread: "
+                   f"{step_s * 1e3:.0f} ms per step, {w['batch'] / step_s:.2f} tokens/s"),
         "ms_per_step": round(step_s * 1e3, 2),
-        "tokens_per_s": round(B / step_s, 3),
+        "tokens_per_s": round(w["batch"] / step_s, 3),
     }
+
+
+def time_steps(torch, run, steps):
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
+def event_times(torch, stream, pre, kernel, steps):
+    """Per-launch duration of `kernel` from HIP events recorded on its stream
+    around it (the rest of the step, `pre`, runs outside the bracket)."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for a, b in evs:
+        pre()
+        a.record(stream)
+        kernel()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return np.array([a.elapsed_time(b) for a, b in evs]) * 1e3  # us
 
 
 def main():
@@ -148,16 +206,14 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="llama8k")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--split", type=int, default=0, help="decode split size (0 = automatic)")
     ap.add_argument("--waves", type=int, default=0, help="waves per decode workgroup (4 or 8)")
     ap.add_argument("--unfused", action="store_true",
-                    help="two launches per step (sai_kv_append + sai_gqa_decode) instead of the "
-                         "fused sai_gqa_with_cache")
-    ap.add_argument("--graph", action="store_true",
-                    help="replay the step from a captured HIP graph (one graph launch per step)")
+                    help="decode: sai_kv_append + sai_gqa_decode instead of sai_gqa_with_cache")
     ap.add_argument("--merge", choices=["auto", "combine", "inkernel"], default="auto",
-                    help="split merge: separate combine kernel or last-workgroup merge")
+                    help="decode split merge: combine kernel or last-workgroup merge")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this path is "
@@ -169,6 +225,7 @@ def main():
 
     assert torch.cuda.is_available(), "needs an MI355X"
     torch.cuda.set_device(0)
+    w = WORKLOADS[args.workload]
     rt = S.Runtime(0)
     if args.split:
         rt.set_decode_split(args.split)
@@ -176,103 +233,123 @@ def main():
         rt.set_decode_waves(args.waves)
     if args.merge != "auto":
         rt.set_decode_merge(args.merge == "inkernel")
-    cos, sin = S.rope_tables(CTX, D, THETA)
-    cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
-    cache, g = build_cache(S, torch, rt, cos_d, sin_d)
+    b, hq, hkv, d = w["batch"], w["hq"], w["hkv"], w["d"]
+    qdt = torch.bfloat16 if w["q_dtype"] == "bf16" else torch.float32
+    stream = torch.cuda.Stream()  # default priority
+    seed = 0x5A1A0001
 
-    q = torch.randn((B, 1, HQ * D), generator=g, device="cuda").to(torch.bfloat16)
-    k_new = torch.randn((B, 1, HKV * D), generator=g, device="cuda")
-    v_new = torch.randn((B, 1, HKV * D), generator=g, device="cuda")
-    out = torch.empty((B, 1, HQ * D), device="cuda", dtype=torch.float32)
-    stream = torch.cuda.Stream()  # default priority; graph capture needs a non-default stream
-    rows = cos_d.shape[0]
+    if w["kind"] == "decode":
+        lens = decode_lengths(w)
+        cos, sin = S.rope_tables(int(lens.max()) + 1, d, w["theta"])
+        cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+        cache, g = build_cache(S, torch, rt, w, lens - 1, 1, cos_d, sin_d, seed)
+        q = torch.randn((b, 1, hq * d), generator=g, device="cuda").to(qdt)
+        k_new = torch.randn((b, 1, hkv * d), generator=g, device="cuda")
+        v_new = torch.randn((b, 1, hkv * d), generator=g, device="cuda")
+        out = torch.empty((b, 1, hq * d), device="cuda", dtype=torch.float32)
+        rows = cos_d.shape[0]
 
-    def step(ev=None):
-        if args.unfused:
-            cache.append(0, k_new, v_new, B, 1, cos_d, sin_d, rows, stream=stream)
-        if ev is not None:
-            ev[0].record(stream)
-        if args.unfused:
-            cache.decode(0, q, out, B, HQ, cos_d, sin_d, rows, stream=stream)
-        else:
-            cache.decode_with_cache(0, q, k_new, v_new, out, B, HQ, cos_d, sin_d, rows,
-                                    stream=stream)
-        if ev is not None:
-            ev[1].record(stream)
+        def pre():
+            if args.unfused:
+                cache.append(0, k_new, v_new, b, 1, cos_d, sin_d, rows, stream=stream)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+        def kern():
+            if args.unfused:
+                cache.decode(0, q, out, b, hq, cos_d, sin_d, rows, stream=stream)
+            else:
+                cache.decode_with_cache(0, q, k_new, v_new, out, b, hq, cos_d, sin_d, rows,
+                                        stream=stream)
 
-    run = step
-    if args.graph:
-        # the step's launches (no allocation, no memset) recorded once, replayed
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            step()
+        def step():
+            pre()
+            kern()
+
         for _ in range(args.warmup):
-            graph.replay()
-        torch.cuda.synchronize()
-        run = graph.replay
+            step()
+        ms_step = time_steps(torch, step, args.steps)
+        kus = event_times(torch, stream, pre, kern, args.steps)
+        alg = decode_bytes(lens, hq, hkv, d, 2 if qdt == torch.bfloat16 else 4)
+        k_us = float(np.median(kus))
+        wg, split = rt.last_decode_shape()
+        value = alg / (ms_step * 1e-3) / 1e9
+        achieved = alg / (k_us * 1e-6) / 1e9
+        result = {
+            "metric": METRIC if args.workload == "llama8k" else
+            f"{args.workload} decode attention HBM GB/s, int8 KV, 1 MI355X",
+            "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+            "data": "synthetic (seeded N(0,1) Q/K/V; no checkpoint)",
+            "config": {"workload": args.workload, "batch": b, "q_heads": hq, "kv_heads": hkv,
+                       "head_dim": d, "context": (int(lens[0]) if w["lens"][0] == "uniform"
+                                                  else f"U[{w['lens'][1]},{w['lens'][2]}]"),
+                       "total_tokens": int(lens.sum()), "q_dtype": w["q_dtype"],
+                       "kv_cache": "int8 per-token-head f32 scale, 16-token pages"
+                                   + (", permuted page table" if w["permute"] else ""),
+                       "rope_theta": w["theta"],
+                       "step": ("kv_append + gqa_decode (+ merge)" if args.unfused
+                                else "gqa_with_cache: append fused into decode (+ merge)")},
+            "pct_of_peak": round(100 * value / HBM_PEAK_GBPS, 2),
+            "tokens_per_s": round(b / (ms_step * 1e-3), 1),
+            "tokens_per_s_32_layers": round(b / (32 * ms_step * 1e-3), 1),
+            "algorithmic_bytes_per_step": alg,
+            "decode_kernel": {"median_us": round(k_us, 3), "mean_us": round(float(kus.mean()), 3),
+                              "workgroups": wg, "split_tokens": split},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                         "traffic": traffic_from_profile() if args.workload == "llama8k" else None},
+        }
+    else:  # prefill
+        past, new = w["past"], w["new"]
+        cos, sin = S.rope_tables(past + new, d, w["theta"])
+        cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+        cache, g = build_cache(S, torch, rt, w, np.full(b, past), new, cos_d, sin_d, seed)
+        q = torch.randn((b, new, hq * d), generator=g, device="cuda").to(qdt)
+        k_new = torch.randn((b, new, hkv * d), generator=g, device="cuda").to(torch.bfloat16)
+        v_new = torch.randn((b, new, hkv * d), generator=g, device="cuda").to(torch.bfloat16)
+        out = torch.empty((b, new, hq * d), device="cuda", dtype=torch.float32)
+        rows = cos_d.shape[0]
 
-    # timed region 1: whole steps, wall clock
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        run()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = wall / args.steps * 1e3
+        def pre():
+            cache.append(0, k_new, v_new, b, new, cos_d, sin_d, rows, stream=stream)
 
-    # timed region 2: the decode kernel alone, HIP events on its stream
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    for i in range(args.steps):
-        step(evs[i])
-    torch.cuda.synchronize()
-    kms = np.array([a.elapsed_time(b) for a, b in evs])
-    k_us = float(np.median(kms)) * 1e3
-    k_mean_us = float(kms.mean()) * 1e3
-    wg, split = rt.last_decode_shape()
+        def kern():
+            cache.prefill(0, q, out, b, new, hq, cos_d, sin_d, rows, stream=stream)
 
-    alg = algorithmic_bytes()
-    value = alg / (ms_step * 1e-3) / 1e9
-    achieved = alg / (k_us * 1e-6) / 1e9
-    copy_gbps = copy_bandwidth(torch)
-    result = {
-        "metric": METRIC,
-        "value": round(value, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic (seeded N(0,1) Q/K/V, random-init; no checkpoint)",
-        "config": {"workload": "llama3-8b-layer-gqa-decode", "batch": B, "context": CTX,
-                   "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "q_dtype": "bf16",
-                   "kv_cache": "int8 per-token-head f32 scale, 16-token pages",
-                   "rope_theta": THETA,
-                   "step": ("kv_append + gqa_decode" if args.unfused
-                            else "gqa_with_cache (append fused into decode)")
-                           + (", hip graph replay" if args.graph else "")},
-        "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
-        "tokens_per_s": round(B / (ms_step * 1e-3), 1),
-        "tokens_per_s_32_layers": round(B / (32 * ms_step * 1e-3), 1),
-        "algorithmic_bytes_per_step": alg,
-        "decode_kernel": {"median_us": round(k_us, 3), "mean_us": round(k_mean_us, 3),
-                          "workgroups": wg, "split_tokens": split},
-        "measured_copy_gbps": round(copy_gbps, 1),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": traffic_from_profile()},
-    }
+        def step():
+            pre()
+            kern()
+
+        for _ in range(args.warmup):
+            step()
+        ms_step = time_steps(torch, step, args.steps)
+        kus = event_times(torch, stream, pre, kern, args.steps)
+        aus = event_times(torch, stream, lambda: None, pre, max(10, args.steps // 4))
+        flops = prefill_flops(b, hq, d, past, new)
+        k_us = float(np.median(kus))
+        tflops = flops / (k_us * 1e-6) / 1e12
+        result = {
+            "metric": "prefill chunk attention TFLOP/s (MFMA), int8 KV, 1 MI355X",
+            "value": round(flops / (ms_step * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+            "data": "synthetic (seeded N(0,1) Q/K/V; no checkpoint)",
+            "config": {"workload": "prefill", "batch": b, "q_heads": hq, "kv_heads": hkv,
+                       "head_dim": d, "past": past, "new_tokens": new, "q_dtype": "bf16",
+                       "kv_cache": "int8 per-token-head f32 scale, 16-token pages",
+                       "step": "kv_append (2048 tokens) + gqa_prefill"},
+            "tokens_per_s": round(b * new / (ms_step * 1e-3), 1),
+            "prefill_kernel": {"median_us": round(k_us, 2), "flops": flops},
+            "append_kernel": {"median_us": round(float(np.median(aus)), 2)},
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
+                         "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
+        }
+    result["measured_copy_gbps"] = round(copy_bandwidth(torch), 1)
     cache.close()
     rt.close()
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline()
+    if args.workload == "llama8k" and not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
 
 
