@@ -13,9 +13,11 @@ appends, plus the split-merge kernel). The step's token goes to the same slot
 every step (append without advance), so the context stays fixed.
 
 Other workloads (--workload, for the per-configuration table): `batch1`
-(8Q/2KV, head_dim 64, context 512), `ragged` (64 sequences with seeded
-lengths U[128, 16384], randomly permuted page table) and `prefill` (2 x 2048
-new tokens appended to a 6144-token cache, then causal MFMA attention).
+(8Q/2KV, head_dim 64, context 512), `int4long` (4 sequences of 32768 tokens,
+int4 KV with f16 (scale, zero) per group of 32 dims, K Student-t df 3 with
+four x20 outlier channels), `ragged` (64 sequences with seeded lengths
+U[128, 16384], randomly permuted page table) and `prefill` (2 x 2048 new
+tokens appended to a 6144-token cache, then causal MFMA attention).
 
 Printed: one JSON line with whole-step algorithmic throughput (`value`), % of
 peak, tokens/s, the dominant kernel's roofline from HIP events on its stream,
@@ -46,6 +48,9 @@ WORKLOADS = {
                     theta=500000.0, q_dtype="bf16", permute=False),
     "batch1": dict(kind="decode", batch=1, hq=8, hkv=2, d=64, lens=("uniform", 512),
                    theta=10000.0, q_dtype="f32", permute=False),
+    "int4long": dict(kind="decode", batch=4, hq=32, hkv=8, d=128, lens=("uniform", 32768),
+                     theta=500000.0, q_dtype="bf16", permute=False, quant="int4",
+                     k_dist="outlier_t3"),
     "ragged": dict(kind="decode", batch=64, hq=32, hkv=8, d=128, lens=("uniform_rand", 128, 16384),
                    theta=500000.0, q_dtype="bf16", permute=True),
     "prefill": dict(kind="prefill", batch=2, hq=32, hkv=8, d=128, past=6144, new=2048,
@@ -61,10 +66,16 @@ def decode_lengths(w, seed=0x5A1A0003):
     return rng.integers(w["lens"][1], w["lens"][2] + 1, size=w["batch"]).astype(np.int64)
 
 
-def decode_bytes(lens, hq, hkv, d, q_bytes):
-    """Algorithmic bytes of one decode step: int8 K+V codes and f32 K+V scales
-    of every visible token, the query and the f32 output."""
-    kv = int(lens.sum()) * hkv * (2 * d + 2 * 4)
+def kv_bytes_per_token_head(d, quant):
+    """int8: K+V codes (2d) and two f32 scales; int4: K+V nibbles (d) and an
+    f16 (scale, zero) per group of 32 dims for K and for V (d/4)."""
+    return 2 * d + 8 if quant == "int8" else d + d // 4
+
+
+def decode_bytes(lens, hq, hkv, d, q_bytes, quant="int8"):
+    """Algorithmic bytes of one decode step: the K+V codes and quantisation
+    parameters of every visible token, the query and the f32 output."""
+    kv = int(lens.sum()) * hkv * kv_bytes_per_token_head(d, quant)
     return kv + len(lens) * hq * d * q_bytes + len(lens) * hq * d * 4
 
 
@@ -93,7 +104,8 @@ def build_cache(S, torch, rt, w, past_lens, extra_tokens, cos_d, sin_d, seed):
     b, hkv, d = w["batch"], w["hkv"], w["d"]
     cap = int(past_lens.max()) + extra_tokens
     pages = (cap + PAGE - 1) // PAGE
-    cache = S.KvCache(rt, 1, hkv, d, b * pages, b, pages, S.KV_INT8)
+    quant = S.KV_INT4 if w.get("quant") == "int4" else S.KV_INT8
+    cache = S.KvCache(rt, 1, hkv, d, b * pages, b, pages, quant)
     ids = np.arange(b * pages, dtype=np.int32)
     if w["permute"]:
         ids = np.random.default_rng(seed).permutation(ids).astype(np.int32)
@@ -105,6 +117,12 @@ def build_cache(S, torch, rt, w, past_lens, extra_tokens, cos_d, sin_d, seed):
         n = min(chunk, past - done)
         k = torch.randn((b, n, hkv * d), generator=g, device="cuda")
         v = torch.randn((b, n, hkv * d), generator=g, device="cuda")
+        if w.get("k_dist") == "outlier_t3":
+            # Student-t df 3 (normal / sqrt(chi2_3 / 3)), four x20 channels per head
+            chi = torch.randn((3, b, n, hkv * d), generator=g, device="cuda").square().sum(0)
+            k = (k / torch.sqrt(chi / 3)).view(b, n, hkv, d)
+            k[..., [7, 31, 64, 100]] *= 20.0
+            k = k.reshape(b, n, hkv * d).contiguous()
         cache.append(0, k, v, b, n, cos_d, sin_d, cos_d.shape[0])
         cache.advance()
         done += n
@@ -268,23 +286,29 @@ def main():
             step()
         ms_step = time_steps(torch, step, args.steps)
         kus = event_times(torch, stream, pre, kern, args.steps)
-        alg = decode_bytes(lens, hq, hkv, d, 2 if qdt == torch.bfloat16 else 4)
+        quant = w.get("quant", "int8")
+        alg = decode_bytes(lens, hq, hkv, d, 2 if qdt == torch.bfloat16 else 4, quant)
         k_us = float(np.median(kus))
         wg, split = rt.last_decode_shape()
         value = alg / (ms_step * 1e-3) / 1e9
         achieved = alg / (k_us * 1e-6) / 1e9
         result = {
             "metric": METRIC if args.workload == "llama8k" else
-            f"{args.workload} decode attention HBM GB/s, int8 KV, 1 MI355X",
+            f"{args.workload} decode attention HBM GB/s, {quant} KV, 1 MI355X",
             "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "int8",
-            "data": "synthetic (seeded N(0,1) Q/K/V; no checkpoint)",
+            "scaling": "weak", "vs_baseline": None,
+            "dtype": "int8" if quant == "int8" else "int8 QK / f16 PV",
+            "data": ("synthetic (seeded N(0,1) Q/V, K "
+                     + ("Student-t df 3 with x20 outlier channels" if w.get("k_dist") else "N(0,1)")
+                     + "; no checkpoint)"),
             "config": {"workload": args.workload, "batch": b, "q_heads": hq, "kv_heads": hkv,
                        "head_dim": d, "context": (int(lens[0]) if w["lens"][0] == "uniform"
                                                   else f"U[{w['lens'][1]},{w['lens'][2]}]"),
                        "total_tokens": int(lens.sum()), "q_dtype": w["q_dtype"],
-                       "kv_cache": "int8 per-token-head f32 scale, 16-token pages"
+                       "kv_cache": ("int8 per-token-head f32 scale" if quant == "int8" else
+                                    "int4 asymmetric, f16 (scale, zero) per group of 32 dims")
+                                   + ", 16-token pages"
                                    + (", permuted page table" if w["permute"] else ""),
                        "rope_theta": w["theta"],
                        "step": ("kv_append + gqa_decode (+ merge)" if args.unfused

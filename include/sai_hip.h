@@ -194,7 +194,8 @@ sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, cons
 /* Tokens per split-K work item of the decode kernel (0 = automatic, else a
  * multiple of 64). Returns the previous value. */
 int32_t sai_set_decode_split(sai_ctx* ctx, int32_t tokens);
-/* Waves per decode workgroup (4 or 8). Returns the previous value. */
+/* Waves per decode workgroup: 4 or 8, or 0 = automatic (4 for an int8
+ * cache, 8 for int4). Returns the previous value. */
 int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves);
 /* Split merge of the decode kernel: 0 = separate combine kernel, 1 = the last
  * workgroup of a sequence merges in-kernel. Returns the previous value. */

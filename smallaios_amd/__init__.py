@@ -54,6 +54,13 @@ def lib() -> C.CDLL:
             raise ImportError(
                 f"{LIB_PATH} is missing: build it with `python smallaios_amd/build.py` "
                 "(or __graft_entry__.build()); there is no CPU fallback")
+        try:
+            # torch bundles its own HIP runtime under the same soname
+            # (libamdhip64.so.7); loading it first makes the process use one
+            # runtime for torch tensors and this library alike
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(LIB_PATH)
         _declare(L)
         _lib = L

@@ -26,7 +26,7 @@ EXTRA = {
     "kv_append.hip": ["-ffp-contract=off"],
     "sai_capi.hip": ["-ffp-contract=off"],
 }
-SOURCES = ["kv_append.hip", "gqa_decode.hip", "gqa_prefill.hip", "sai_capi.hip"]
+SOURCES = ["kv_append.hip", "gqa_decode.hip", "gqa_decode_int4.hip", "gqa_prefill.hip", "sai_capi.hip"]
 
 
 def _run(cmd):

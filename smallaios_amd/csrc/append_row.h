@@ -106,4 +106,84 @@ __device__ __forceinline__ void append_row_int8(const void* k_row, const void* v
   }
 }
 
+// int4 code of element x of a group of 32 = one half-wave (lanes 0-31 /
+// 32-63): min/max over the group, scale (max-min)/15 (1.0 for an empty range)
+// and zero point min stored as binary16 and used as stored, code =
+// min(round_half_away((x - z)/s) as u32, 15) (onnx-rt/src/kv_compression.rs:223-253).
+__device__ __forceinline__ void quant_int4_elem(float x, uint32_t& q, uint16_t& s16,
+                                                uint16_t& z16) {
+#pragma clang fp contract(off)
+  // group of 32 = one half-wave (lanes 0-31 / 32-63) for each j
+  // NaN never wins a `<` / `>` comparison in the reference loop
+  float mn = (x != x) ? INFINITY : x;
+  float mx = (x != x) ? -INFINITY : x;
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) {
+    const float omn = __shfl_xor(mn, off, 64);
+    const float omx = __shfl_xor(mx, off, 64);
+    // `if v < min { min = v }` ignores NaN, like fminf/fmaxf
+    mn = fminf(mn, omn);
+    mx = fmaxf(mx, omx);
+  }
+  const float range = mx - mn;
+  const float scale = (range > 0.0f) ? range / 15.0f : 1.0f;
+  const _Float16 hs = (_Float16)scale;  // v_cvt_f16_f32, round to nearest even
+  const _Float16 hz = (_Float16)mn;
+  const float sf = (float)hs;
+  const float zf = (float)hz;
+  uint32_t v = 0u;
+  if (sf > 0.0f) {
+    // round_f32 of onnx-rt/src/kv_compression.rs:27-37, then `as u32`
+    const float t = (x - zf) / sf;
+    const float tr = (float)sat_i32(t);
+    const float fr = t - tr;
+    const float rr = (fr >= 0.5f) ? tr + 1.0f : ((fr <= -0.5f) ? tr - 1.0f : tr);
+    v = sat_u32(rr);
+  }
+  q = v < 15u ? v : 15u;
+  s16 = __builtin_bit_cast(uint16_t, hs);
+  z16 = __builtin_bit_cast(uint16_t, hz);
+}
+
+// Full K+V append of one (token, kv head) row into an int4 page block, one
+// wave. K is packed LSB-first along D; V is dim-major and shares each byte
+// with the neighbouring slot, whose nibble is kept (read-modify-write; the
+// caller guarantees no other wave writes that byte concurrently).
+__device__ __forceinline__ void append_row_int4_d128(const void* k_row, const void* v_row,
+                                                     int dtype, int lane, int pos, uint8_t* blk,
+                                                     int slot, int do_rotary, bool interleaved,
+                                                     const float* cos_cache,
+                                                     const float* sin_cache) {
+  constexpr int D = 128;
+  constexpr int NG = D / 32;
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+    float x[2];
+    const void* in = which == 0 ? k_row : v_row;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) x[j] = load_elem(in, lane + 64 * j, dtype);
+    if (which == 0 && do_rotary) rope_row_wave<D>(x, lane, pos, cos_cache, sin_cache, interleaved);
+    uint16_t* sz = (uint16_t*)(blk + 16 * D + 64 * NG * which) + (size_t)slot * NG * 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint32_t q;
+      uint16_t s16, z16;
+      quant_int4_elem(x[j], q, s16, z16);
+      const int e = lane + 64 * j;
+      if ((lane & 31) == 0) {
+        sz[(e / 32) * 2 + 0] = s16;
+        sz[(e / 32) * 2 + 1] = z16;
+      }
+      if (which == 0) {
+        const uint32_t other = (uint32_t)__shfl_xor((int)q, 1, 64);
+        if ((lane & 1) == 0) blk[(size_t)slot * (D / 2) + e / 2] = (uint8_t)(q | (other << 4));
+      } else {
+        uint8_t* dst = blk + (size_t)8 * D + (size_t)e * 8 + (slot >> 1);
+        const uint8_t cur = *dst;
+        *dst = (slot & 1) ? (uint8_t)((cur & 0x0F) | (q << 4)) : (uint8_t)((cur & 0xF0) | q);
+      }
+    }
+  }
+}
+
 }  // namespace sai

@@ -38,69 +38,15 @@
 // through LDS. A sequence with one split writes its output directly; with
 // several, every workgroup writes a partial (m, l, o) and the combine kernel
 // (a second launch, so no cross-workgroup fences) merges them.
+#include <type_traits>
+
 #include "append_row.h"
+#include "decode_common.h"
 #include "sai_internal.h"
 
 namespace sai {
 
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-constexpr int kMaxSplitPages = 1024;  // split_tokens <= 16384
-
-__device__ __forceinline__ float rope_elem(float c, float s, float own, float partner,
-                                           bool first) {
-#pragma clang fp contract(off)
-  return first ? (c * own - s * partner) : (s * partner + c * own);
-}
-
-__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
-  return (a & 0xFF) | ((b & 0xFF) << 8) | ((c & 0xFF) << 16) | ((int)((unsigned)d << 24));
-}
-
-// exchange with the neighbouring lane: quad_perm(1,0,3,2)
-__device__ __forceinline__ int swap_pair(int v) {
-  return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
-}
-
-// max / sum over the four lane groups (lanes r, r+16, r+32, r+48)
-__device__ __forceinline__ float xgroup_max(float v) {
-  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float xgroup_sum(float v) {
-  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// 16 consecutive elements (f32 or bf16) starting at element `off`; the
-// offset is a multiple of 16 and the row 32-byte aligned.
-__device__ __forceinline__ void load16(const void* base, size_t off, int dtype, float (&x)[16]) {
-  if (dtype == kDtypeBf16) {
-    const uint4* p = (const uint4*)((const uint16_t*)base + off);
-    const uint4 a = p[0], b = p[1];
-    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      x[2 * i] = __uint_as_float(w[i] << 16);
-      x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-    }
-  } else {
-    const float4* p = (const float4*)((const float*)base + off);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 v = p[i];
-      x[4 * i] = v.x, x[4 * i + 1] = v.y, x[4 * i + 2] = v.z, x[4 * i + 3] = v.w;
-    }
-  }
-}
 
 template <int D>
 struct TileRegs {
@@ -266,39 +212,8 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   const int work = blockIdx.x;
 
   // ---- (sequence, split) of this workgroup ------------------------------------
-  // Uniform split count (every sequence has p.uniform_nsplit splits): direct
-  // mapping. Ragged: prefix scan over the per-sequence split counts.
-  int b = -1, split = 0, nsplit = 0, split_base = 0;
-  if (p.uniform_nsplit > 0) {
-    nsplit = p.uniform_nsplit;
-    b = work / nsplit;
-    split = work - b * nsplit;
-    split_base = b * nsplit;
-  } else {
-    int base = 0;
-    for (int c0 = 0; c0 < p.batch; c0 += 64) {
-      const int bi = c0 + lane;
-      const int Lb = bi < p.batch ? p.seq_lens[bi] + p.pending : 0;
-      const int n = (Lb + p.split_tokens - 1) / p.split_tokens;
-      int incl = n;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += t;
-      }
-      const int total = __shfl(incl, 63, 64);
-      if (work < base + total) {
-        const unsigned long long m = __ballot(base + incl > work);
-        const int first = __ffsll((long long)m) - 1;
-        b = c0 + first;
-        split_base = base + __shfl(incl - n, first, 64);
-        nsplit = __shfl(n, first, 64);
-        split = work - split_base;
-        break;
-      }
-      base += total;
-    }
-  }
+  int b, split, nsplit, split_base;
+  decode_work_item(p, work, lane, b, split, nsplit, split_base);
   if (b < 0 || b >= p.batch) return;  // uniform over the workgroup
 
   // page ids of the split, loaded before the length is known (the page-table
@@ -563,6 +478,13 @@ __global__ __launch_bounds__(256) void gqa_decode_combine_kernel(DecodeParams p)
 }
 
 template <int D, int G>
+hipError_t launch_combine_dg(const DecodeParams& p, hipStream_t st) {
+  hipLaunchKernelGGL((gqa_decode_combine_kernel<D, G>), dim3(p.batch, p.kv_heads), dim3(256), 0,
+                     st, p);
+  return hipGetLastError();
+}
+
+template <int D, int G>
 hipError_t launch_dg(const DecodeParams& p, int work_items, bool combine, hipStream_t st) {
   if (p.waves == 8)
     hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, 8>), dim3(work_items, p.kv_heads), dim3(512),
@@ -572,9 +494,7 @@ hipError_t launch_dg(const DecodeParams& p, int work_items, bool combine, hipStr
                        0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !combine || p.merge_in_kernel) return e;
-  hipLaunchKernelGGL((gqa_decode_combine_kernel<D, G>), dim3(p.batch, p.kv_heads), dim3(256), 0,
-                     st, p);
-  return hipGetLastError();
+  return launch_combine_dg<D, G>(p, st);
 }
 
 template <int D>
@@ -591,8 +511,25 @@ hipError_t launch_d(const DecodeParams& p, int group, int work_items, bool combi
 
 }  // namespace
 
+hipError_t launch_decode_combine(const DecodeParams& p, int head_dim, int group, hipStream_t st) {
+  auto by_group = [&](auto d) -> hipError_t {
+    constexpr int D = decltype(d)::value;
+    switch (group) {
+      case 1: return launch_combine_dg<D, 1>(p, st);
+      case 2: return launch_combine_dg<D, 2>(p, st);
+      case 4: return launch_combine_dg<D, 4>(p, st);
+      case 8: return launch_combine_dg<D, 8>(p, st);
+      default: return hipErrorInvalidValue;
+    }
+  };
+  if (head_dim == 64) return by_group(std::integral_constant<int, 64>{});
+  if (head_dim == 128) return by_group(std::integral_constant<int, 128>{});
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_gqa_decode(const DecodeParams& p, int head_dim, int group, int quant,
                              int work_items, bool combine, hipStream_t st) {
+  if (quant == kQuantInt4) return launch_gqa_decode_int4(p, head_dim, group, work_items, combine, st);
   if (quant != kQuantInt8) return hipErrorInvalidValue;
   if (p.split_tokens <= 0 || p.split_tokens % 64 != 0 ||
       p.split_tokens > kMaxSplitPages * kPageTokens)

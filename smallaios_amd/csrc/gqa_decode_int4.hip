@@ -1,0 +1,505 @@
+// Kernel 2, int4 cache: split-K flash decode over pages of 4-bit asymmetric
+// codes with a binary16 (scale, zero) per (token, kv head, group of 32 dims).
+// head_dim 128 (4 groups), GQA group G <= 8.
+//
+// Same work split, prologue, double-buffered tile stream and split merge as
+// the int8 kernel (gqa_decode.hip); what changes is the math:
+//   score(t,h) = sum_G s_tG * <c_t,G , q_h,G> + sum_G z_tG * sum(q_h,G)
+//   out(h,d)   = sum_t (p_t * s_tG(d)) * c_td + sum_t p_t * z_tG(d)
+//
+// Column layout ("block-diagonal"): MFMA column j = 4*hh + G' stands for
+// (head hh of a quad of heads, dim group G'). Lane (r, g) of the QK A
+// operand holds token r's dims of group g (one 16-byte load); the B operand
+// of lane (j, g) is q_hh on those dims if g == G' and zero otherwise, so the
+// accumulation over the four 8-dim chunks leaves <c_t,G', q_hh,G'> in column
+// j. The lane scales it by its own group's s_tG', adds z_tG' * sum(q_hh,G'),
+// and a quad reduction over G' gives the score. All 16 columns are useful for
+// G = 4; G = 8 runs two quads.
+//
+// Codes as f16 subnormals: the mask (w & 0x000F000F) turns two nibbles into
+// the exact binary16 values c * 2^-24, and (w & 0x00F000F0) gives c * 2^-20,
+// so a dword of 8 nibbles unpacks with one shift and four masks. The factor
+// 16 between the two is folded into the other operand (Q x16 on the 2^-24
+// dims; p / 16 on the 2^-20 slots, taken in the exponent), and the powers of
+// two into the score scale and the merge. v_mfma_f32_16x16x32_f16 multiplies
+// subnormal inputs exactly.
+//
+// QK: Q / max|Q| is split into f16 hi + lo summed along k (22 significant
+// bits, so keys with large outlier channels do not amplify the query's
+// rounding). PV: A row j = p_t(hh) * s_v,tG' (f16), B = V nibbles; output row
+// (hh, G') is read for the dims of group G'. The zero-point term
+// sum_t p_t z_v,tG' is accumulated per lane next to the softmax state and
+// added at the merge.
+#include <type_traits>
+
+#include "append_row.h"
+#include "decode_common.h"
+#include "sai_internal.h"
+
+namespace sai {
+
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 128;
+constexpr int kNG = kD / 32;  // groups of 32 along head_dim
+constexpr int kJB = kD / 16;  // 16-dim column blocks of PV
+constexpr size_t kBB = block_bytes_int4(kD);
+constexpr float kTwo20 = 1048576.0f;          // 2^20
+constexpr float kTwo24 = 16777216.0f;         // 2^24
+
+struct Tile4 {
+  v4u ka[4];     // K: token (page r>>2, slot 4*blk + (r&3)), dims 32g .. 32g+31
+  v2u vb[kJB];   // V: slots 0..15 of dim 16*jb + r in page g
+  uint4 kp, vp;  // (scale, zero) x 4 groups, f16, of (page g, slot r)
+};
+
+__device__ __forceinline__ void load_tile4(Tile4& T, const uint8_t* __restrict__ pool,
+                                           const int* sm_pg, int tile, int num_pages, int kvh,
+                                           int r, int g, int n_pages_split) {
+  const int lp = n_pages_split - 1;
+  const int pg_g = sm_pg[min(tile * 4 + g, lp)];
+  const int pg_k = sm_pg[min(tile * 4 + (r >> 2), lp)];
+  const uint8_t* blk_g = pool + block_offset(pg_g, kvh, num_pages, kBB);
+  const uint8_t* blk_k = pool + block_offset(pg_k, kvh, num_pages, kBB);
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk)
+    T.ka[blk] = __builtin_nontemporal_load(
+        (const v4u*)(blk_k + (size_t)(4 * blk + (r & 3)) * (kD / 2) + 16 * g));
+#pragma unroll
+  for (int jb = 0; jb < kJB; ++jb)
+    T.vb[jb] = __builtin_nontemporal_load((const v2u*)(blk_g + 8 * kD + (16 * jb + r) * 8));
+  T.kp = *(const uint4*)(blk_g + 16 * kD + 16 * r);
+  T.vp = *(const uint4*)(blk_g + 16 * kD + 64 * kNG + 16 * r);
+}
+
+// 8 nibbles (one dword, element k at bits 4k..4k+3) -> f16 subnormals in the
+// order k = 0,4,1,5,2,6,3,7 with scales 2^-24, 2^-24, 2^-20, 2^-20, 2^-24,
+// 2^-24, 2^-20, 2^-20.
+__device__ __forceinline__ v8h unpack_sub(uint32_t w) {
+  const uint32_t t = w >> 8;
+  const v4u u = v4u{w & 0x000F000Fu, w & 0x00F000F0u, t & 0x000F000Fu, t & 0x00F000F0u};
+  return __builtin_bit_cast(v8h, u);
+}
+// element of the chunk at k position i of that order, and whether its scale
+// is 2^-24 (true) or 2^-20
+__device__ __forceinline__ constexpr int sub_elem(int i) { return (i >> 1) + ((i & 1) ? 4 : 0); }
+__device__ __forceinline__ constexpr bool sub_small(int i) { return ((i >> 1) & 1) == 0; }
+
+// float add of the lane xor 1 / xor 2 neighbour inside a quad
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
+  return v;
+}
+
+template <int G>
+struct State4 {
+  static constexpr int HT = (G + 3) / 4;  // quads of heads
+  float m_run[HT], l_run[HT];  // per lane (j, g): head 4*qd + j/4, log2 domain
+  float zacc[HT];              // sum_t p_t z_v,tG' of (head 4*qd + j/4, G' = j&3)
+  float acc[HT][kJB];          // lane (dim 16*jb + r, g): head 4*qd + g, x 2^-24
+};
+
+// One 64-token tile: lane (r, g) owns page g of the tile (slots 0..15) for
+// column j = r. MASK: the tile crosses the end of the split (t_end).
+template <int G, bool MASK>
+__device__ __forceinline__ void compute_tile4(const Tile4& T, State4<G>& st,
+                                              const v8h (&Bh)[State4<G>::HT][kNG],
+                                              const v8h (&Bl)[State4<G>::HT][kNG],
+                                              const float (&qsn)[State4<G>::HT],
+                                              const float (&q_scale)[State4<G>::HT], int tok0,
+                                              int t_end, int r, int g, uint4* sm_p) {
+  constexpr int HT = State4<G>::HT;
+  const int lane = threadIdx.x & 63;
+  const int gp = r & 3;
+  // (scale, zero) of every slot of the tile through this wave's LDS slot
+  sm_p[lane] = T.kp;
+  sm_p[64 + lane] = T.vp;
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t* sm_w = (const uint32_t*)sm_p;
+
+  // QK^T: per 16-token block, accumulate the four 8-dim chunks (hi and lo)
+  v4f cs[HT][4];
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    v8h ka[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ka[c] = unpack_sub(T.ka[blk][c]);
+#pragma unroll
+    for (int qd = 0; qd < HT; ++qd) {
+      v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[c], Bh[qd][c], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[c], Bl[qd][c], acc, 0, 0, 0);
+      }
+      cs[qd][blk] = acc;
+    }
+  }
+  const int nvalid = t_end - tok0;
+  // u = sum_G' (s_G' * dot_G' + z_G' * qsn); score (log2) = q_scale * u
+  float u[HT][16];
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int slot = 4 * blk + e;
+      const v2h sz = __builtin_bit_cast(v2h, sm_w[(16 * g + slot) * 4 + gp]);
+#pragma unroll
+      for (int qd = 0; qd < HT; ++qd)
+        u[qd][slot] = quad_sum(fmaf((float)sz[0], cs[qd][blk][e], (float)sz[1] * qsn[qd]));
+    }
+  if (MASK) {
+#pragma unroll
+    for (int qd = 0; qd < HT; ++qd)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) u[qd][i] = (i < nvalid) ? u[qd][i] : -INFINITY;
+  }
+  // p of even slots; odd slots hold p / 16 (their V codes carry 2^-20)
+  float p[HT][16];
+  float alpha[HT];
+#pragma unroll
+  for (int qd = 0; qd < HT; ++qd) {
+    float mt = u[qd][0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mt = fmaxf(mt, u[qd][i]);
+    mt = xgroup_max(mt) * q_scale[qd];
+    const float m_new = fmaxf(st.m_run[qd], mt);
+    const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+    alpha[qd] = fast_exp2(st.m_run[qd] - m_use);
+    float se = 0.0f, so = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      p[qd][i] = fast_exp2(fmaf(u[qd][i], q_scale[qd], (i & 1) ? -m_use - 4.0f : -m_use));
+      if (i & 1)
+        so += p[qd][i];
+      else
+        se += p[qd][i];
+    }
+    const float psum = xgroup_sum(fmaf(so, 16.0f, se));
+    st.l_run[qd] = st.l_run[qd] * alpha[qd] + psum;
+    st.m_run[qd] = m_new;
+  }
+
+  // A operand of P V: row j = p(head) * s_v of group G' = j&3, slots of each
+  // half in the V unpack order; zero-point sums of the same (head, G')
+  v8h pa[HT][2];
+  float ze[HT], zo[HT];
+#pragma unroll
+  for (int qd = 0; qd < HT; ++qd) ze[qd] = zo[qd] = 0.0f;
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int slot = 8 * half + sub_elem(i);
+      const v2h sz = __builtin_bit_cast(v2h, sm_w[(64 + 16 * g + slot) * 4 + gp]);
+#pragma unroll
+      for (int qd = 0; qd < HT; ++qd) {
+        float a = p[qd][slot] * (float)sz[0];
+        float z = p[qd][slot] * (float)sz[1];
+        if (MASK) {
+          // masked slots may hold stale parameters: select, do not multiply
+          a = (slot < nvalid) ? a : 0.0f;
+          z = (slot < nvalid) ? z : 0.0f;
+        }
+        pa[qd][half][i] = (_Float16)a;
+        if (slot & 1)
+          zo[qd] += z;
+        else
+          ze[qd] += z;
+      }
+    }
+#pragma unroll
+  for (int qd = 0; qd < HT; ++qd)
+    st.zacc[qd] = st.zacc[qd] * alpha[qd] + xgroup_sum(fmaf(zo[qd], 16.0f, ze[qd]));
+
+  // rescale factor of the head this lane accumulates in P V (4*qd + g)
+  float apv[HT];
+#pragma unroll
+  for (int qd = 0; qd < HT; ++qd) {
+    const int a0 = __builtin_amdgcn_readlane(__float_as_int(alpha[qd]), 0);
+    const int a1 = __builtin_amdgcn_readlane(__float_as_int(alpha[qd]), 4);
+    const int a2 = __builtin_amdgcn_readlane(__float_as_int(alpha[qd]), 8);
+    const int a3 = __builtin_amdgcn_readlane(__float_as_int(alpha[qd]), 12);
+    apv[qd] = __int_as_float(g == 0 ? a0 : (g == 1 ? a1 : (g == 2 ? a2 : a3)));
+  }
+  // P V on the matrix cores; lane (dim, g) reads row (head g, group of dim)
+#pragma unroll
+  for (int jb = 0; jb < kJB; ++jb) {
+    const v8h b0 = unpack_sub(T.vb[jb].x);
+    const v8h b1 = unpack_sub(T.vb[jb].y);
+#pragma unroll
+    for (int qd = 0; qd < HT; ++qd) {
+      v4f co = v4f{0.f, 0.f, 0.f, 0.f};
+      co = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[qd][0], b0, co, 0, 0, 0);
+      co = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[qd][1], b1, co, 0, 0, 0);
+      st.acc[qd][jb] = st.acc[qd][jb] * apv[qd] + co[jb >> 1];
+    }
+  }
+}
+
+template <int G, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(DecodeParams p) {
+  constexpr int HT = State4<G>::HT;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int kvh = blockIdx.y;
+  const int work = blockIdx.x;
+
+  int b, split, nsplit, split_base;
+  decode_work_item(p, work, lane, b, split, nsplit, split_base);
+  if (b < 0 || b >= p.batch) return;  // uniform over the workgroup
+
+  const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
+  const int first_page = split * (p.split_tokens / kPageTokens);
+  __shared__ int sm_pg[kMaxSplitPages];
+  const int split_pages = p.split_tokens / kPageTokens;
+  for (int i = threadIdx.x; i < split_pages; i += 64 * NW)
+    sm_pg[i] = pt[min(first_page + i, p.max_pages - 1)];
+
+  const int L = p.seq_lens[b] + p.pending;
+  const int t_begin = split * p.split_tokens;
+  const int t_end = min(L, t_begin + p.split_tokens);
+  const int Hq = p.kv_heads * G;
+  const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
+  const int n_tiles = (t_end - t_begin + 63) / 64;
+  const int last_owner = (n_tiles - 1) % NW;
+  __syncthreads();
+
+  // fused append: the last tile's owner writes the new token first
+  if (p.k_new != nullptr && split == nsplit - 1 && wave == last_owner) {
+    const int pos = L - 1;
+    uint8_t* blk = (uint8_t*)p.pool +
+                   block_offset(sm_pg[pos / kPageTokens - first_page], kvh, p.num_pages, kBB);
+    const size_t row = ((size_t)b * p.kv_heads + kvh) * kD * (p.kv_dtype == kDtypeBf16 ? 2 : 4);
+    append_row_int4_d128((const uint8_t*)p.k_new + row, (const uint8_t*)p.v_new + row,
+                         p.kv_dtype, lane, pos, blk, pos % kPageTokens, p.do_rotary,
+                         p.interleaved != 0, p.cos_cache, p.sin_cache);
+    __threadfence_block();
+  }
+
+  // first tile in flight while Q is prepared
+  Tile4 TA;
+  int tile = wave;
+  if (tile < n_tiles) load_tile4(TA, p.pool, sm_pg, tile, p.num_pages, kvh, r, g, n_pages_split);
+
+  // ---- Q: lane (j = 4*hh + G', g) holds the 32 dims of group g of head
+  // 4*qd + hh, RoPE'd at position L-1, normalised by the head's max|Q| ----
+  const int gp = r & 3;
+  const int hh = r >> 2;
+  v8h Bh[HT][kNG], Bl[HT][kNG];
+  float qsn[HT], q_scale[HT];
+#pragma unroll
+  for (int qd = 0; qd < HT; ++qd) {
+    const int h = 4 * qd + hh;
+    const bool live = h < G;
+    const int pos = L - 1;
+    const size_t qbase = ((size_t)b * Hq + kvh * G + (live ? h : 0)) * kD;
+    float x[32];
+    if (live) {
+      float t[16];
+      load16(p.q, qbase + 32 * g, p.q_dtype, t);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = t[i];
+      load16(p.q, qbase + 32 * g + 16, p.q_dtype, t);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[16 + i] = t[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[i] = 0.0f;
+    }
+    if (p.do_rotary) {
+      const float* cr = p.cos_cache + (size_t)pos * (kD / 2);
+      const float* sr = p.sin_cache + (size_t)pos * (kD / 2);
+      float y[32];
+      if (p.interleaved) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const int d = 32 * g + i;
+          y[i] = rope_elem(cr[d >> 1], sr[d >> 1], x[i], x[i ^ 1], (i & 1) == 0);
+        }
+      } else {
+        // partner d +- 64: group g ^ 2, the lane 32 away
+        const bool first = g < 2;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          // permlane32_swap(x, x): [0] = lanes 0-31's x on both halves, [1] =
+          // lanes 32-63's x on both halves
+          auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i]), __float_as_uint(x[i]),
+                                                     false, false);
+          const float xp = __uint_as_float(first ? sw[1] : sw[0]);
+          const int pi = (first ? 32 * g : 32 * g - kD / 2) + i;
+          y[i] = rope_elem(cr[pi], sr[pi], x[i], xp, first);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[i] = y[i];
+    }
+    float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      amax = fmaxf(amax, fabsf(x[i]));
+      sum += x[i];
+    }
+    amax = xgroup_max(amax);
+    const float norm = amax > 0.0f ? amax : 1.0f;
+    const float inv = 1.0f / norm;
+    // dots come out x 2^-20 (see the unpack), folded into the score scale
+    q_scale[qd] = norm * p.scale_log2 * kTwo20;
+    // sum over group G' = j&3 of this head: held by lane (j, G')
+    const float gsum = __shfl(sum, r + 16 * gp, 64);
+    qsn[qd] = gsum * inv * (1.0f / kTwo20);
+    const v8h zero = v8h{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      v8h qh, ql;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float yv = x[8 * c + sub_elem(i)] * inv * (sub_small(i) ? 16.0f : 1.0f);
+        // hi and lo must split one f32 value; without this barrier the
+        // backend may fold the product into one of the two f16 conversions
+        // only (v_fma_mixlo_f16, a single rounding) and hi + lo drifts
+        __asm__("" : "+v"(yv));
+        const _Float16 hi = (_Float16)yv;
+        qh[i] = hi;
+        ql[i] = (_Float16)(yv - (float)hi);
+      }
+      Bh[qd][c] = g == gp ? qh : zero;
+      Bl[qd][c] = g == gp ? ql : zero;
+    }
+  }
+  __shared__ uint4 sm_par[NW][128];
+
+  // ---- stream the split's tiles, ping-pong; the last one may be partial ----
+  State4<G> st;
+#pragma unroll
+  for (int qd = 0; qd < HT; ++qd) {
+    st.m_run[qd] = -INFINITY;
+    st.l_run[qd] = 0.0f;
+    st.zacc[qd] = 0.0f;
+#pragma unroll
+    for (int jb = 0; jb < kJB; ++jb) st.acc[qd][jb] = 0.0f;
+  }
+
+  Tile4 TB;
+  const int my_tiles = tile < n_tiles ? (n_tiles - 1 - tile) / NW + 1 : 0;
+  auto tok0 = [&](int k) { return t_begin + (wave + k * NW) * 64 + 16 * g; };
+  auto ld = [&](Tile4& T, int k) {
+    load_tile4(T, p.pool, sm_pg, wave + k * NW, p.num_pages, kvh, r, g, n_pages_split);
+  };
+  // tiles before the split's last one are full
+  const bool last_partial = (t_end - t_begin) % 64 != 0;
+  auto run = [&](const Tile4& T, int k) {
+    const bool partial = last_partial && wave + k * NW == n_tiles - 1;
+    if (__builtin_amdgcn_readfirstlane(partial))
+      compute_tile4<G, true>(T, st, Bh, Bl, qsn, q_scale, tok0(k), t_end, r, g, sm_par[wave]);
+    else
+      compute_tile4<G, false>(T, st, Bh, Bl, qsn, q_scale, tok0(k), t_end, r, g, sm_par[wave]);
+  };
+  int k = 0;
+  for (; k + 2 < my_tiles; k += 2) {
+    ld(TB, k + 1);
+    compute_tile4<G, false>(TA, st, Bh, Bl, qsn, q_scale, tok0(k), t_end, r, g, sm_par[wave]);
+    ld(TA, k + 2);
+    compute_tile4<G, false>(TB, st, Bh, Bl, qsn, q_scale, tok0(k + 1), t_end, r, g, sm_par[wave]);
+  }
+  if (k + 1 < my_tiles) {
+    ld(TB, k + 1);
+    compute_tile4<G, false>(TA, st, Bh, Bl, qsn, q_scale, tok0(k), t_end, r, g, sm_par[wave]);
+    run(TB, k + 1);
+  } else if (k < my_tiles) {
+    run(TA, k);
+  }
+
+  // ---- merge the NW waves; zero-point sums join per (head, dim group) ----
+  __shared__ float sm_m[NW][G];
+  __shared__ float sm_l[NW][G];
+  __shared__ float sm_z[NW][G][kNG];
+  __shared__ float sm_o[NW][G][kD];
+#pragma unroll
+  for (int qd = 0; qd < HT; ++qd) {
+    const int h = 4 * qd + hh;
+    if (g == 0 && h < G) {
+      sm_z[wave][h][gp] = st.zacc[qd];
+      if (gp == 0) {
+        sm_m[wave][h] = st.m_run[qd];
+        sm_l[wave][h] = st.l_run[qd];
+      }
+    }
+    const int hd = 4 * qd + g;
+    if (hd < G) {
+#pragma unroll
+      for (int jb = 0; jb < kJB; ++jb) sm_o[wave][hd][16 * jb + r] = st.acc[qd][jb] * kTwo24;
+    }
+  }
+  __syncthreads();
+
+  float* part = p.partials + ((size_t)(split_base + split) * p.kv_heads + kvh) * (G * (kD + 2));
+  for (int t = threadIdx.x; t < G * kD; t += 64 * NW) {
+    const int hd = t / kD, d = t % kD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm_m[w][hd]);
+    float Ls = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      if (sm_m[w][hd] == -INFINITY) continue;
+      const float f = fast_exp2(sm_m[w][hd] - M);
+      Ls += sm_l[w][hd] * f;
+      O += (sm_o[w][hd][d] + sm_z[w][hd][d >> 5]) * f;
+    }
+    if (nsplit == 1) {
+      p.out[((size_t)b * Hq + kvh * G + hd) * kD + d] = Ls > 0.0f ? O / Ls : 0.0f;
+    } else {
+      part[hd * (kD + 2) + 2 + d] = O;
+      if (d == 0) {
+        part[hd * (kD + 2)] = M;
+        part[hd * (kD + 2) + 1] = Ls;
+      }
+    }
+  }
+  if (split == 0 && threadIdx.x == 0 && kvh == 0) {
+    p.seq_info[2 * b] = split_base;
+    p.seq_info[2 * b + 1] = nsplit;
+  }
+}
+
+template <int G>
+hipError_t launch_g(const DecodeParams& p, int work_items, bool combine, hipStream_t st) {
+  if (p.waves == 8)
+    hipLaunchKernelGGL((gqa_decode_int4_kernel<G, 8>), dim3(work_items, p.kv_heads), dim3(512), 0,
+                       st, p);
+  else
+    hipLaunchKernelGGL((gqa_decode_int4_kernel<G, 4>), dim3(work_items, p.kv_heads), dim3(256), 0,
+                       st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !combine) return e;
+  return launch_decode_combine(p, kD, G, st);
+}
+
+}  // namespace
+
+hipError_t launch_gqa_decode_int4(const DecodeParams& p, int head_dim, int group, int work_items,
+                                  bool combine, hipStream_t st) {
+  if (head_dim != kD) return hipErrorInvalidValue;
+  if (p.split_tokens <= 0 || p.split_tokens % 64 != 0 ||
+      p.split_tokens > kMaxSplitPages * kPageTokens)
+    return hipErrorInvalidValue;
+  switch (group) {
+    case 1: return launch_g<1>(p, work_items, combine, st);
+    case 2: return launch_g<2>(p, work_items, combine, st);
+    case 4: return launch_g<4>(p, work_items, combine, st);
+    case 8: return launch_g<8>(p, work_items, combine, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace sai

@@ -54,41 +54,6 @@ __global__ __launch_bounds__(256) void kv_append_int8_kernel(AppendParams p) {
 // writes. Tokens of the pair outside [seq_len, seq_len + s_new) keep their
 // stored nibbles.
 template <int D>
-__device__ __forceinline__ void quant_int4_elem(float x, int lane, uint32_t& q, uint16_t& s16,
-                                                uint16_t& z16) {
-  // group of 32 = one half-wave (lanes 0-31 / 32-63) for each j
-  // NaN never wins a `<` / `>` comparison in the reference loop
-  float mn = (x != x) ? INFINITY : x;
-  float mx = (x != x) ? -INFINITY : x;
-#pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) {
-    const float omn = __shfl_xor(mn, off, 64);
-    const float omx = __shfl_xor(mx, off, 64);
-    // `if v < min { min = v }` ignores NaN, like fminf/fmaxf
-    mn = fminf(mn, omn);
-    mx = fmaxf(mx, omx);
-  }
-  const float range = mx - mn;
-  const float scale = (range > 0.0f) ? range / 15.0f : 1.0f;
-  const _Float16 hs = (_Float16)scale;  // v_cvt_f16_f32, round to nearest even
-  const _Float16 hz = (_Float16)mn;
-  const float sf = (float)hs;
-  const float zf = (float)hz;
-  uint32_t v = 0u;
-  if (sf > 0.0f) {
-    // round_f32 of onnx-rt/src/kv_compression.rs:27-37, then `as u32`
-    const float t = (x - zf) / sf;
-    const float tr = (float)sat_i32(t);
-    const float fr = t - tr;
-    const float rr = (fr >= 0.5f) ? tr + 1.0f : ((fr <= -0.5f) ? tr - 1.0f : tr);
-    v = sat_u32(rr);
-  }
-  q = v < 15u ? v : 15u;
-  s16 = __builtin_bit_cast(uint16_t, hs);
-  z16 = __builtin_bit_cast(uint16_t, hz);
-}
-
-template <int D>
 __global__ __launch_bounds__(256) void kv_append_int4_kernel(AppendParams p, int pairs_per_seq) {
   constexpr int J = D / 64;
   constexpr int NG = D / 32;
@@ -139,7 +104,7 @@ __global__ __launch_bounds__(256) void kv_append_int4_kernel(AppendParams p, int
       for (int j = 0; j < J; ++j) {
         uint32_t q;
         uint16_t s16, z16;
-        quant_int4_elem<D>(x[j], lane, q, s16, z16);
+        quant_int4_elem(x[j], q, s16, z16);
         const int e = lane + 64 * j;
         if ((lane & 31) == 0) {
           const int gidx = e / 32;

@@ -31,7 +31,7 @@ struct sai_ctx {
   int32_t* counters = nullptr;
   size_t counter_n = 0;
   int32_t decode_split = 0;  // 0 = automatic
-  int32_t decode_waves = 4;
+  int32_t decode_waves = 0;  // 0: automatic
   int32_t decode_merge = 0;  // 0: combine kernel, 1: in-kernel merge
   int32_t last_wg = 0;
   int32_t last_split = 0;
@@ -221,7 +221,7 @@ SAI_API int32_t sai_set_decode_split(sai_ctx* ctx, int32_t tokens) {
 SAI_API int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves) {
   if (!ctx) return 0;
   int32_t prev = ctx->decode_waves;
-  if (waves == 4 || waves == 8) ctx->decode_waves = waves;
+  if (waves == 0 || waves == 4 || waves == 8) ctx->decode_waves = waves;
   return prev;
 }
 
@@ -541,9 +541,9 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
                          int32_t rotary_interleaved, int32_t has_scale, float scale, float* out,
                          const void* k_new, const void* v_new, int32_t kv_dtype, void* stream) {
   const char* op = "gqa_decode";
-  if (c->desc.quant != SAI_KV_INT8)
-    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: int4 decode is not built yet", op);
   const int D = c->desc.head_dim;
+  if (c->desc.quant == SAI_KV_INT4 && D != 128)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: int4 decode needs head_dim 128 (got %d)", op, D);
   const int kvh = c->desc.num_kv_heads;
 
   // Split size. Uniform lengths: one round of about one workgroup per CU
@@ -603,7 +603,8 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   const float sc = has_scale ? scale : sai_default_scale(D);
   p.scale_log2 = sc * 1.4426950408889634f;
   p.split_tokens = split;
-  p.waves = ctx->decode_waves;
+  // int4 tiles are compute-heavier: two waves per SIMD from one workgroup
+  p.waves = ctx->decode_waves ? ctx->decode_waves : (c->desc.quant == SAI_KV_INT4 ? 8 : 4);
   p.uniform_nsplit = uniform ? (int)n_first : 0;
   p.partials = ctx->partials;
   p.seq_info = ctx->seq_info;

@@ -32,6 +32,17 @@ def dev(x: np.ndarray, dtype="f32"):
     return t.contiguous()
 
 
+def outlier_student_t(rng, k):
+    """K of the long-context int4 workload: Student-t (df 3) with four fixed
+    outlier channels per head scaled x20."""
+    b, n, hd = k.shape
+    t = rng.standard_normal(k.shape).astype(np.float32) / np.sqrt(
+        rng.chisquare(3, size=k.shape) / 3).astype(np.float32)
+    t = t.reshape(b, n, hd // 128, 128)
+    t[..., [7, 31, 64, 100]] *= 20.0
+    return t.reshape(b, n, hd).astype(np.float32)
+
+
 class Case:
     """One cache (GPU + oracle) with `batch` sequences.
 

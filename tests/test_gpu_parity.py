@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import smallaios_amd as S
-from _gpu_util import Case, assert_close, log
+from _gpu_util import Case, assert_close, log, outlier_student_t
 
 pytestmark = pytest.mark.gpu
 
@@ -68,16 +68,8 @@ def test_append_int4_bit_exact(rt):
     """int4 asym g32 codes and f16 params, K with x20 outlier channels."""
     log("append int4: outlier channels, student-t, odd start positions")
 
-    def heavy(rng, k):
-        b, n, hd = k.shape
-        t = rng.standard_normal(k.shape).astype(np.float32) / np.sqrt(
-            rng.chisquare(3, size=k.shape) / 3).astype(np.float32)
-        t = t.reshape(b, n, hd // 128, 128)
-        t[..., [7, 31, 64, 100]] *= 20.0
-        return t.reshape(b, n, hd).astype(np.float32)
-
     c = Case(rt, 0x5A1A0002, 2, 8, 2, 128, [33, 6], 5, theta=5e5, quant=S.KV_INT4,
-             k_transform=heavy, permute_pages=True, extra_tokens=1)
+             k_transform=outlier_student_t, permute_pages=True, extra_tokens=1)
     c.step_kv()
     c.check_codes()
     c.cache.advance()
@@ -208,6 +200,93 @@ def test_decode_llama_layer_full_size(rt):
     err = assert_close(got, ref, "c2 decode")
     log(f"  max abs err {err:.2e}")
     c.check_codes(seqs=[0, 15])
+
+
+# ------------------------------------------------------------ int4 decode ---
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (16, 2)])
+def test_decode_int4_groups(rt, hq, hkv):
+    log(f"decode int4 group {hq // hkv}: hq={hq} hkv={hkv}, outlier K, permuted pages")
+    c = Case(rt, 0x1400 + hq, 3, hq, hkv, 128, [300, 129, 17], 1, theta=5e5, quant=S.KV_INT4,
+             k_transform=outlier_student_t, permute_pages=True)
+    c.step_kv()
+    q = c.query()
+    assert_close(c.gpu_decode(q), c.oracle_attend(q), f"int4 group {hq // hkv}")
+
+
+def test_decode_int4_options(rt):
+    log("decode int4: no rotary / interleaved / explicit scale / bf16")
+    for rot, inter, scale, dt in [(False, False, None, "f32"), (True, True, None, "bf16"),
+                                  (True, False, 0.05, "f32")]:
+        c = Case(rt, 0x1410, 2, 16, 4, 128, [200, 90], 1, quant=S.KV_INT4, do_rotary=rot,
+                 interleaved=inter, kv_dtype=dt)
+        c.step_kv()
+        q = c.query(dt)
+        assert_close(c.gpu_decode(q, dt, scale=scale), c.oracle_attend(q, scale),
+                     f"int4 {rot} {inter} {scale} {dt}")
+
+
+def test_decode_int4_first_token_equals_v(rt):
+    log("decode int4 first token")
+    c = Case(rt, 0x1420, 2, 8, 2, 128, [0, 0], 1, quant=S.KV_INT4)
+    c.step_kv()
+    q = c.query()
+    got = c.gpu_decode(q)
+    _, vd = c.ocache.dequant()
+    for b in range(2):
+        for hq in range(8):
+            np.testing.assert_allclose(got[b, 0, hq * 128:(hq + 1) * 128], vd[b, hq // 4, 0],
+                                       atol=2e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("split", [64, 1024])
+def test_decode_int4_split_merge(rt, split):
+    log(f"decode int4 split merge split={split}")
+    c = Case(rt, 0x1430, 3, 32, 8, 128, [3000, 1, 640], 1, quant=S.KV_INT4,
+             k_transform=outlier_student_t, permute_pages=True)
+    prev = rt.set_decode_split(split)
+    try:
+        c.step_kv()
+        q = c.query()
+        ref = c.oracle_attend(q)
+        for _ in range(2):
+            assert_close(c.gpu_decode(q), ref, f"int4 split {split}")
+    finally:
+        rt.set_decode_split(prev)
+
+
+@pytest.mark.parametrize("split", [64, 4096])
+def test_decode_int4_fused_step(rt, split):
+    """Fused int4 step: the decode kernel appends the token (V nibble shared
+    with the neighbouring slot) and attends; codes bit-exact with the oracle."""
+    log(f"fused int4 decode step split={split}")
+    prev_s = rt.set_decode_split(split)
+    try:
+        c = Case(rt, 0x1440, 3, 32, 8, 128, [700, 4, 4100], 1, theta=5e5, kv_dtype="bf16",
+                 quant=S.KV_INT4, k_transform=outlier_student_t, permute_pages=True,
+                 extra_tokens=2)
+        for step in range(3):
+            q = c.query("bf16")
+            got = c.step_fused(q, "bf16")
+            assert_close(got, c.oracle_attend(q), f"fused int4 step {step}")
+            c.check_codes(seqs=[1])
+            c.cache.advance()
+    finally:
+        rt.set_decode_split(prev_s)
+
+
+def test_decode_int4_long_context_full_size(rt):
+    """Long-context int4 decode at full size: B=4, 32k context, 32Q/8KV, K
+    Student-t with x20 outlier channels."""
+    log("decode int4 full size: B=4 ctx 32768 32Q/8KV D=128")
+    c = Case(rt, 0x5A1A0002, 4, 32, 8, 128, [32767] * 4, 1, theta=5e5, quant=S.KV_INT4,
+             k_transform=outlier_student_t)
+    c.step_kv()
+    q = c.query("bf16")
+    got = c.gpu_decode(q, "bf16")
+    ref = c.oracle_attend(q)
+    err = assert_close(got, ref, "c3 decode")
+    log(f"  max abs err {err:.2e}")
+    c.check_codes(seqs=[3])
 
 
 # ---------------------------------------------------------------- prefill ---
