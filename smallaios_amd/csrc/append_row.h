@@ -88,22 +88,23 @@ __device__ __forceinline__ void quant_store_row_int8(float (&x)[D / 64], int lan
 }
 
 // Full K+V append of one (token, kv head) row. k_row / v_row point at the
-// row's D elements (f32 or bf16).
+// row's D elements (f32 or bf16). Every load is issued before the first
+// store, so the row costs one memory round trip.
 template <int D>
 __device__ __forceinline__ void append_row_int8(const void* k_row, const void* v_row, int dtype,
                                                 int lane, int pos, uint8_t* blk, int slot,
                                                 int do_rotary, bool interleaved,
                                                 const float* cos_cache, const float* sin_cache) {
   constexpr int J = D / 64;
+  float xk[J], xv[J];
 #pragma unroll
-  for (int which = 0; which < 2; ++which) {
-    float x[J];
-    const void* in = which == 0 ? k_row : v_row;
-#pragma unroll
-    for (int j = 0; j < J; ++j) x[j] = load_elem(in, lane + 64 * j, dtype);
-    if (which == 0 && do_rotary) rope_row_wave<D>(x, lane, pos, cos_cache, sin_cache, interleaved);
-    quant_store_row_int8<D>(x, lane, blk, slot, which);
+  for (int j = 0; j < J; ++j) {
+    xk[j] = load_elem(k_row, lane + 64 * j, dtype);
+    xv[j] = load_elem(v_row, lane + 64 * j, dtype);
   }
+  if (do_rotary) rope_row_wave<D>(xk, lane, pos, cos_cache, sin_cache, interleaved);
+  quant_store_row_int8<D>(xk, lane, blk, slot, 0);
+  quant_store_row_int8<D>(xv, lane, blk, slot, 1);
 }
 
 // int4 code of element x of a group of 32 = one half-wave (lanes 0-31 /
@@ -148,7 +149,8 @@ __device__ __forceinline__ void quant_int4_elem(float x, uint32_t& q, uint16_t& 
 // Full K+V append of one (token, kv head) row into an int4 page block, one
 // wave. K is packed LSB-first along D; V is dim-major and shares each byte
 // with the neighbouring slot, whose nibble is kept (read-modify-write; the
-// caller guarantees no other wave writes that byte concurrently).
+// caller guarantees no other wave writes that byte concurrently). Every load
+// is issued before the first store.
 __device__ __forceinline__ void append_row_int4_d128(const void* k_row, const void* v_row,
                                                      int dtype, int lane, int pos, uint8_t* blk,
                                                      int slot, int do_rotary, bool interleaved,
@@ -156,19 +158,26 @@ __device__ __forceinline__ void append_row_int4_d128(const void* k_row, const vo
                                                      const float* sin_cache) {
   constexpr int D = 128;
   constexpr int NG = D / 32;
+  float xk[2], xv[2];
+  uint8_t* vdst[2];
+  uint8_t vcur[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = lane + 64 * j;
+    xk[j] = load_elem(k_row, e, dtype);
+    xv[j] = load_elem(v_row, e, dtype);
+    vdst[j] = blk + (size_t)8 * D + (size_t)e * 8 + (slot >> 1);
+    vcur[j] = *vdst[j];
+  }
+  if (do_rotary) rope_row_wave<D>(xk, lane, pos, cos_cache, sin_cache, interleaved);
 #pragma unroll
   for (int which = 0; which < 2; ++which) {
-    float x[2];
-    const void* in = which == 0 ? k_row : v_row;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) x[j] = load_elem(in, lane + 64 * j, dtype);
-    if (which == 0 && do_rotary) rope_row_wave<D>(x, lane, pos, cos_cache, sin_cache, interleaved);
     uint16_t* sz = (uint16_t*)(blk + 16 * D + 64 * NG * which) + (size_t)slot * NG * 2;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       uint32_t q;
       uint16_t s16, z16;
-      quant_int4_elem(x[j], q, s16, z16);
+      quant_int4_elem(which == 0 ? xk[j] : xv[j], q, s16, z16);
       const int e = lane + 64 * j;
       if ((lane & 31) == 0) {
         sz[(e / 32) * 2 + 0] = s16;
@@ -178,9 +187,8 @@ __device__ __forceinline__ void append_row_int4_d128(const void* k_row, const vo
         const uint32_t other = (uint32_t)__shfl_xor((int)q, 1, 64);
         if ((lane & 1) == 0) blk[(size_t)slot * (D / 2) + e / 2] = (uint8_t)(q | (other << 4));
       } else {
-        uint8_t* dst = blk + (size_t)8 * D + (size_t)e * 8 + (slot >> 1);
-        const uint8_t cur = *dst;
-        *dst = (slot & 1) ? (uint8_t)((cur & 0x0F) | (q << 4)) : (uint8_t)((cur & 0xF0) | q);
+        *vdst[j] = (slot & 1) ? (uint8_t)((vcur[j] & 0x0F) | (q << 4))
+                              : (uint8_t)((vcur[j] & 0xF0) | q);
       }
     }
   }

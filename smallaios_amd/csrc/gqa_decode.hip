@@ -225,18 +225,38 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   for (int i = threadIdx.x; i < split_pages; i += 64 * NW)
     sm_pg[i] = pt[min(first_page + i, p.max_pages - 1)];
 
+  // ---- the query (and its RoPE partner chunk) loads with the page ids ---------
+  constexpr int HALF = D / 2;
+  const int hterm = r;  // column j of the QK product
+  const int h = hterm >> 1;
+  const bool is_hi = (hterm & 1) == 0;
+  const bool live = h < G;
+  const int Hq = p.kv_heads * G;
+  const size_t qbase = ((size_t)b * Hq + kvh * G + (live ? h : 0)) * D;
+  float xq[KS][16], xq_p[KS][16];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int c0 = (D / 4) * g + 16 * ks;  // first dim of this lane's chunk
+    load16(p.q, qbase + c0, p.q_dtype, xq[ks]);
+    if (p.do_rotary && !p.interleaved)
+      load16(p.q, qbase + (c0 < HALF ? c0 + HALF : c0 - HALF), p.q_dtype, xq_p[ks]);
+  }
+
   const int L = p.seq_lens[b] + p.pending;
   const int t_begin = split * p.split_tokens;
   const int t_end = min(L, t_begin + p.split_tokens);
-  const int Hq = p.kv_heads * G;
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
   const int n_tiles = (t_end - t_begin + 63) / 64;
   // the wave that streams the split's last tile (it holds the newest token)
   const int last_owner = (n_tiles - 1) % NW;
   __syncthreads();
 
-  // ---- fused append: the last tile's owner writes the new token first ---------
-  if (p.k_new != nullptr && split == nsplit - 1 && wave == last_owner) {
+  // ---- fused append by the last tile's owner: before its first load if that
+  // tile is its only one, else while its first tile is in flight -----------------
+  const bool appender = p.k_new != nullptr && split == nsplit - 1 && wave == last_owner;
+  int tile = wave;
+  const int my_tiles = tile < n_tiles ? (n_tiles - 1 - tile) / NW + 1 : 0;
+  auto append = [&]() {
     const int pos = L - 1;
     uint8_t* blk = (uint8_t*)p.pool +
                    block_offset(sm_pg[pos / kPageTokens - first_page], kvh, p.num_pages,
@@ -247,33 +267,26 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
                        p.cos_cache, p.sin_cache);
     // this wave reads the page back in its last tile: order the stores first
     __threadfence_block();
-  }
-
-  // ---- first tile in flight while Q is prepared ----------------------------------
+  };
+  if (appender && my_tiles == 1) append();
   const int tile_off = 0;  // splits start on a tile (64-token) boundary
   TileRegs<D> TA;
-  int tile = wave;
   if (tile < n_tiles) load_tile<D>(TA, p.pool, sm_pg + tile_off, tile, p.num_pages, kvh, r, g, n_pages_split);
+  if (appender && my_tiles > 1) append();
 
   // ---- Q: RoPE at position L-1, split into int8 (hi, lo) terms -------------
-  const int hterm = r;  // column j of the QK product
-  const int h = hterm >> 1;
-  const bool is_hi = (hterm & 1) == 0;
-  const bool live = h < G;
   v4i qB[KS];
   float sq_hi;
   {
-    constexpr int HALF = D / 2;
     const int pos = L - 1;
-    const int hq = kvh * G + (live ? h : 0);
-    const size_t qbase = ((size_t)b * Hq + hq) * D;
     float qv[KS][16];
     float amax = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int c0 = (D / 4) * g + 16 * ks;  // first dim of this lane's chunk
       float x[16];
-      load16(p.q, qbase + c0, p.q_dtype, x);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = xq[ks][i];
       if (p.do_rotary) {
         const float* cr = p.cos_cache + (size_t)pos * HALF;
         const float* sr = p.sin_cache + (size_t)pos * HALF;
@@ -290,8 +303,7 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
         } else {
           const bool first = c0 < HALF;
           const int pc0 = first ? c0 : c0 - HALF;  // pair index of element 0
-          float xp[16];
-          load16(p.q, qbase + (first ? c0 + HALF : c0 - HALF), p.q_dtype, xp);
+          const float* xp = xq_p[ks];
 #pragma unroll
           for (int i4 = 0; i4 < 4; ++i4) {
             const float4 cv = *(const float4*)(cr + pc0 + 4 * i4);
@@ -345,7 +357,6 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   // the loop is unconditional (straight-line code), so the compiler's wait
   // counts only cover the tile being computed, never the one in flight.
   TileRegs<D> TB;
-  const int my_tiles = tile < n_tiles ? (n_tiles - 1 - tile) / NW + 1 : 0;
   auto tok0 = [&](int k) { return t_begin + (wave + k * NW) * 64 + 16 * g; };
   auto ld = [&](TileRegs<D>& T, int k) {
     load_tile<D>(T, p.pool, sm_pg + tile_off, wave + k * NW, p.num_pages, kvh, r, g,
@@ -451,6 +462,11 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
 }
 
 // Merge of the split partials of one (sequence, kv head): grid (batch, Hkv).
+// The partials were just written by other workgroups (often on other XCDs),
+// so every global read here is a full memory latency: the kernel issues them
+// in independent batches. Phase 1, one wave per head: max of the split maxima
+// and the rescaled sum of the split sums. Phase 2, one thread per (head, dim):
+// the rescaled sum of the split outputs, eight splits per batch of loads.
 template <int D, int G>
 __global__ __launch_bounds__(256) void gqa_decode_combine_kernel(DecodeParams p) {
   const int b = blockIdx.x;
@@ -461,19 +477,50 @@ __global__ __launch_bounds__(256) void gqa_decode_combine_kernel(DecodeParams p)
   const int Hq = p.kv_heads * G;
   const size_t stride = (size_t)p.kv_heads * (G * (D + 2));
   const float* p0 = p.partials + ((size_t)split_base * p.kv_heads + kvh) * (G * (D + 2));
+  __shared__ float sm_M[G], sm_inv[G];
+  const int lane = threadIdx.x & 63;
+  for (int hd = threadIdx.x >> 6; hd < G; hd += 4) {
+    float M = -INFINITY;
+    for (int s0 = 0; s0 < nsplit; s0 += 64)
+      if (s0 + lane < nsplit) M = fmaxf(M, p0[(s0 + lane) * stride + hd * (D + 2)]);
+    M = wave_max(M);
+    float Ls = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += 64) {
+      if (s0 + lane < nsplit) {
+        const float* ps = p0 + (s0 + lane) * stride + hd * (D + 2);
+        const float m = ps[0];
+        if (m != -INFINITY) Ls += ps[1] * fast_exp2(m - M);
+      }
+    }
+    Ls = wave_sum(Ls);
+    if (lane == 0) {
+      sm_M[hd] = M;
+      sm_inv[hd] = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+    }
+  }
+  __syncthreads();
   for (int t = threadIdx.x; t < G * D; t += 256) {
     const int hd = t / D, d = t % D;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p0[s * stride + hd * (D + 2)]);
-    float Ls = 0.0f, O = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float* ps = p0 + s * stride + hd * (D + 2);
-      if (ps[0] == -INFINITY) continue;
-      const float f = fast_exp2(ps[0] - M);
-      Ls += ps[1] * f;
-      O += ps[2 + d] * f;
+    const float M = sm_M[hd];
+    const float* ph = p0 + hd * (D + 2);
+    float O = 0.0f;
+    int s = 0;
+    for (; s + 8 <= nsplit; s += 8) {
+      float m[8], o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        m[i] = ph[(s + i) * stride];
+        o[i] = ph[(s + i) * stride + 2 + d];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (m[i] != -INFINITY) O += o[i] * fast_exp2(m[i] - M);
     }
-    p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+    for (; s < nsplit; ++s) {
+      const float m = ph[s * stride];
+      if (m != -INFINITY) O += ph[s * stride + 2 + d] * fast_exp2(m - M);
+    }
+    p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = O * sm_inv[hd];
   }
 }
 

@@ -258,6 +258,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   decode_work_item(p, work, lane, b, split, nsplit, split_base);
   if (b < 0 || b >= p.batch) return;  // uniform over the workgroup
 
+  // page ids of the split, the query and the length in one round of loads;
+  // cos / sin of the position follow once the length is known
   const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
   const int first_page = split * (p.split_tokens / kPageTokens);
   __shared__ int sm_pg[kMaxSplitPages];
@@ -265,17 +267,44 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   for (int i = threadIdx.x; i < split_pages; i += 64 * NW)
     sm_pg[i] = pt[min(first_page + i, p.max_pages - 1)];
 
+  // lane (j = 4*hh + G', g) holds the 32 dims of group g of head 4*qd + hh
+  const int gp = r & 3;
+  const int hh = r >> 2;
+  const int Hq = p.kv_heads * G;
+  float x[HT][32];
+#pragma unroll
+  for (int qd = 0; qd < HT; ++qd) {
+    const int h = 4 * qd + hh;
+    if (h < G) {
+      const size_t qbase = ((size_t)b * Hq + kvh * G + h) * kD + 32 * g;
+      float t[16];
+      load16(p.q, qbase, p.q_dtype, t);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[qd][i] = t[i];
+      load16(p.q, qbase + 16, p.q_dtype, t);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[qd][16 + i] = t[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[qd][i] = 0.0f;
+    }
+  }
+
   const int L = p.seq_lens[b] + p.pending;
   const int t_begin = split * p.split_tokens;
   const int t_end = min(L, t_begin + p.split_tokens);
-  const int Hq = p.kv_heads * G;
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
   const int n_tiles = (t_end - t_begin + 63) / 64;
   const int last_owner = (n_tiles - 1) % NW;
   __syncthreads();
 
-  // fused append: the last tile's owner writes the new token first
-  if (p.k_new != nullptr && split == nsplit - 1 && wave == last_owner) {
+  // fused append by the wave that streams the split's last tile (the page of
+  // the new token): before its first load if that tile is its only one, else
+  // while its first tile is in flight
+  const bool appender = p.k_new != nullptr && split == nsplit - 1 && wave == last_owner;
+  int tile = wave;
+  const int my_tiles = tile < n_tiles ? (n_tiles - 1 - tile) / NW + 1 : 0;
+  auto append = [&]() {
     const int pos = L - 1;
     uint8_t* blk = (uint8_t*)p.pool +
                    block_offset(sm_pg[pos / kPageTokens - first_page], kvh, p.num_pages, kBB);
@@ -283,49 +312,39 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
     append_row_int4_d128((const uint8_t*)p.k_new + row, (const uint8_t*)p.v_new + row,
                          p.kv_dtype, lane, pos, blk, pos % kPageTokens, p.do_rotary,
                          p.interleaved != 0, p.cos_cache, p.sin_cache);
+    // the page is read back by this wave's last tile
     __threadfence_block();
-  }
-
-  // first tile in flight while Q is prepared
+  };
+  if (appender && my_tiles == 1) append();
   Tile4 TA;
-  int tile = wave;
   if (tile < n_tiles) load_tile4(TA, p.pool, sm_pg, tile, p.num_pages, kvh, r, g, n_pages_split);
+  if (appender && my_tiles > 1) append();
 
-  // ---- Q: lane (j = 4*hh + G', g) holds the 32 dims of group g of head
-  // 4*qd + hh, RoPE'd at position L-1, normalised by the head's max|Q| ----
-  const int gp = r & 3;
-  const int hh = r >> 2;
+  // ---- Q: RoPE at position L-1, normalised by the head's max|Q| ----
+  float cq[32], sq[32];
+  if (p.do_rotary) {
+    const int pos = L - 1;
+    const int c0 = p.interleaved ? 16 * g : (g < 2 ? 32 * g : 32 * g - kD / 2);
+    const float* cr = p.cos_cache + (size_t)pos * (kD / 2) + c0;
+    const float* sr = p.sin_cache + (size_t)pos * (kD / 2) + c0;
+    // interleaved: pair i >> 1 of the lane's 32 dims, 16 values
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int ci = p.interleaved ? (i >> 1) : i;
+      cq[i] = cr[ci];
+      sq[i] = sr[ci];
+    }
+  }
   v8h Bh[HT][kNG], Bl[HT][kNG];
   float qsn[HT], q_scale[HT];
 #pragma unroll
   for (int qd = 0; qd < HT; ++qd) {
-    const int h = 4 * qd + hh;
-    const bool live = h < G;
-    const int pos = L - 1;
-    const size_t qbase = ((size_t)b * Hq + kvh * G + (live ? h : 0)) * kD;
-    float x[32];
-    if (live) {
-      float t[16];
-      load16(p.q, qbase + 32 * g, p.q_dtype, t);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) x[i] = t[i];
-      load16(p.q, qbase + 32 * g + 16, p.q_dtype, t);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) x[16 + i] = t[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) x[i] = 0.0f;
-    }
     if (p.do_rotary) {
-      const float* cr = p.cos_cache + (size_t)pos * (kD / 2);
-      const float* sr = p.sin_cache + (size_t)pos * (kD / 2);
       float y[32];
       if (p.interleaved) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int d = 32 * g + i;
-          y[i] = rope_elem(cr[d >> 1], sr[d >> 1], x[i], x[i ^ 1], (i & 1) == 0);
-        }
+        for (int i = 0; i < 32; ++i)
+          y[i] = rope_elem(cq[i], sq[i], x[qd][i], x[qd][i ^ 1], (i & 1) == 0);
       } else {
         // partner d +- 64: group g ^ 2, the lane 32 away
         const bool first = g < 2;
@@ -333,21 +352,20 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
         for (int i = 0; i < 32; ++i) {
           // permlane32_swap(x, x): [0] = lanes 0-31's x on both halves, [1] =
           // lanes 32-63's x on both halves
-          auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i]), __float_as_uint(x[i]),
-                                                     false, false);
+          auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[qd][i]),
+                                                     __float_as_uint(x[qd][i]), false, false);
           const float xp = __uint_as_float(first ? sw[1] : sw[0]);
-          const int pi = (first ? 32 * g : 32 * g - kD / 2) + i;
-          y[i] = rope_elem(cr[pi], sr[pi], x[i], xp, first);
+          y[i] = rope_elem(cq[i], sq[i], x[qd][i], xp, first);
         }
       }
 #pragma unroll
-      for (int i = 0; i < 32; ++i) x[i] = y[i];
+      for (int i = 0; i < 32; ++i) x[qd][i] = y[i];
     }
     float amax = 0.0f, sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      amax = fmaxf(amax, fabsf(x[i]));
-      sum += x[i];
+      amax = fmaxf(amax, fabsf(x[qd][i]));
+      sum += x[qd][i];
     }
     amax = xgroup_max(amax);
     const float norm = amax > 0.0f ? amax : 1.0f;
@@ -363,7 +381,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
       v8h qh, ql;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        float yv = x[8 * c + sub_elem(i)] * inv * (sub_small(i) ? 16.0f : 1.0f);
+        float yv = x[qd][8 * c + sub_elem(i)] * inv * (sub_small(i) ? 16.0f : 1.0f);
         // hi and lo must split one f32 value; without this barrier the
         // backend may fold the product into one of the two f16 conversions
         // only (v_fma_mixlo_f16, a single rounding) and hi + lo drifts
@@ -390,7 +408,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   }
 
   Tile4 TB;
-  const int my_tiles = tile < n_tiles ? (n_tiles - 1 - tile) / NW + 1 : 0;
   auto tok0 = [&](int k) { return t_begin + (wave + k * NW) * 64 + 16 * g; };
   auto ld = [&](Tile4& T, int k) {
     load_tile4(T, p.pool, sm_pg, wave + k * NW, p.num_pages, kvh, r, g, n_pages_split);
