@@ -19,13 +19,18 @@ namespace sai {
 
 // RoPE of one element. `first` = this element is x0 of its pair.
 // Reference: rotate_rope_block, onnx-rt/src/ops/microsoft.rs:137-160.
+// Branch-free: both products rounded on their own, then a - b for x0 and
+// a + b (== s*x0 + c*x1, IEEE addition commutes) for x1.
 __device__ __forceinline__ float rope_pair_elem(float c, float s, float own, float partner,
                                                 bool first) {
 #pragma clang fp contract(off)
-  return first ? (c * own - s * partner) : (s * partner + c * own);
+  const float a = c * own;
+  const float b = s * partner;
+  return a + (first ? -b : b);
 }
 
 // x[j] = element lane + 64*j of the row; rotates in place at position `pos`.
+// The cos / sin loads come first so that they overlap the row's own loads.
 template <int D>
 __device__ __forceinline__ void rope_row_wave(float (&x)[D / 64], int lane, int pos,
                                               const float* __restrict__ cos_cache,
@@ -33,6 +38,18 @@ __device__ __forceinline__ void rope_row_wave(float (&x)[D / 64], int lane, int 
                                               bool interleaved) {
   constexpr int J = D / 64;
   constexpr int HALF = D / 2;
+  const float* cr = cos_cache + (size_t)pos * HALF;
+  const float* sr = sin_cache + (size_t)pos * HALF;
+  float c[J], s[J];
+  bool first[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int e = lane + 64 * j;
+    first[j] = interleaved ? (e & 1) == 0 : e < HALF;
+    const int i = interleaved ? (e >> 1) : (first[j] ? e : e - HALF);
+    c[j] = cr[i];
+    s[j] = sr[i];
+  }
   float xp[J];
   if (interleaved) {
 #pragma unroll
@@ -44,22 +61,8 @@ __device__ __forceinline__ void rope_row_wave(float (&x)[D / 64], int lane, int 
 #pragma unroll
     for (int j = 0; j < J; ++j) xp[j] = __shfl_xor(x[j], HALF, 64);
   }
-  const float* cr = cos_cache + (size_t)pos * HALF;
-  const float* sr = sin_cache + (size_t)pos * HALF;
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int e = lane + 64 * j;
-    int i;
-    bool first;
-    if (interleaved) {
-      i = e >> 1;
-      first = (e & 1) == 0;
-    } else {
-      first = e < HALF;
-      i = first ? e : e - HALF;
-    }
-    x[j] = rope_pair_elem(cr[i], sr[i], x[j], xp[j], first);
-  }
+  for (int j = 0; j < J; ++j) x[j] = rope_pair_elem(c[j], s[j], x[j], xp[j], first[j]);
 }
 
 // Quantise one row (int8, symmetric, per row) and store it into the page

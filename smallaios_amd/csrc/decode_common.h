@@ -15,10 +15,16 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxSplitPages = 1024;  // split_tokens <= 16384 (page ids staged in LDS)
 
+// RoPE of one element; `first` = this element is x0 of its pair. Both
+// products are rounded on their own and the select picks the sign of the
+// second, so x0: c*x0 - s*x1 and x1: s*x0 + c*x1 (== c*x1 + s*x0) without a
+// branch per lane.
 __device__ __forceinline__ float rope_elem(float c, float s, float own, float partner,
                                            bool first) {
 #pragma clang fp contract(off)
-  return first ? (c * own - s * partner) : (s * partner + c * own);
+  const float a = c * own;
+  const float b = s * partner;
+  return a + (first ? -b : b);
 }
 
 __device__ __forceinline__ int pack4(int a, int b, int c, int d) {

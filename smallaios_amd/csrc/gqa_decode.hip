@@ -219,13 +219,15 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   // page ids of the split, loaded before the length is known (the page-table
   // row has max_pages entries; the split's range is clamped to it)
   const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
+  // length first; then the page ids of the split and the query, in flight
+  // across the barrier
+  const int L = p.seq_lens[b] + p.pending;
   const int first_page = split * (p.split_tokens / kPageTokens);
   __shared__ int sm_pg[kMaxSplitPages];
   const int split_pages = p.split_tokens / kPageTokens;
   for (int i = threadIdx.x; i < split_pages; i += 64 * NW)
     sm_pg[i] = pt[min(first_page + i, p.max_pages - 1)];
 
-  // ---- the query (and its RoPE partner chunk) loads with the page ids ---------
   constexpr int HALF = D / 2;
   const int hterm = r;  // column j of the QK product
   const int h = hterm >> 1;
@@ -233,16 +235,9 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   const bool live = h < G;
   const int Hq = p.kv_heads * G;
   const size_t qbase = ((size_t)b * Hq + kvh * G + (live ? h : 0)) * D;
-  float xq[KS][16], xq_p[KS][16];
+  float xq[KS][16];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    const int c0 = (D / 4) * g + 16 * ks;  // first dim of this lane's chunk
-    load16(p.q, qbase + c0, p.q_dtype, xq[ks]);
-    if (p.do_rotary && !p.interleaved)
-      load16(p.q, qbase + (c0 < HALF ? c0 + HALF : c0 - HALF), p.q_dtype, xq_p[ks]);
-  }
-
-  const int L = p.seq_lens[b] + p.pending;
+  for (int ks = 0; ks < KS; ++ks) load16(p.q, qbase + (D / 4) * g + 16 * ks, p.q_dtype, xq[ks]);
   const int t_begin = split * p.split_tokens;
   const int t_end = min(L, t_begin + p.split_tokens);
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
@@ -250,6 +245,25 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   // the wave that streams the split's last tile (it holds the newest token)
   const int last_owner = (n_tiles - 1) % NW;
   __syncthreads();
+
+  // cos / sin of position L-1: issued ahead of the first tile, so the query's
+  // RoPE only waits for them and not for the tile
+  float cq[KS][16], sq[KS][16];
+  if (p.do_rotary) {
+    const float* cr = p.cos_cache + (size_t)(L - 1) * HALF;
+    const float* sr = p.sin_cache + (size_t)(L - 1) * HALF;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int c0 = (D / 4) * g + 16 * ks;
+      const int base = p.interleaved ? (c0 >> 1) : (c0 < HALF ? c0 : c0 - HALF);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int idx = base + (p.interleaved ? (i >> 1) : i);
+        cq[ks][i] = cr[idx];
+        sq[ks][i] = sr[idx];
+      }
+    }
+  }
 
   // ---- fused append by the last tile's owner: before its first load if that
   // tile is its only one, else while its first tile is in flight -----------------
@@ -288,33 +302,21 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
 #pragma unroll
       for (int i = 0; i < 16; ++i) x[i] = xq[ks][i];
       if (p.do_rotary) {
-        const float* cr = p.cos_cache + (size_t)pos * HALF;
-        const float* sr = p.sin_cache + (size_t)pos * HALF;
-        if (p.interleaved) {
-          const float4 c0v = *(const float4*)(cr + c0 / 2), c1v = *(const float4*)(cr + c0 / 2 + 4);
-          const float4 s0v = *(const float4*)(sr + c0 / 2), s1v = *(const float4*)(sr + c0 / 2 + 4);
-          const float cc[8] = {c0v.x, c0v.y, c0v.z, c0v.w, c1v.x, c1v.y, c1v.z, c1v.w};
-          const float ss[8] = {s0v.x, s0v.y, s0v.z, s0v.w, s1v.x, s1v.y, s1v.z, s1v.w};
-          float y[16];
+        float y[16];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) y[i] = rope_elem(cc[i >> 1], ss[i >> 1], x[i], x[i ^ 1], (i & 1) == 0);
-#pragma unroll
-          for (int i = 0; i < 16; ++i) x[i] = y[i];
-        } else {
-          const bool first = c0 < HALF;
-          const int pc0 = first ? c0 : c0 - HALF;  // pair index of element 0
-          const float* xp = xq_p[ks];
-#pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) {
-            const float4 cv = *(const float4*)(cr + pc0 + 4 * i4);
-            const float4 sv = *(const float4*)(sr + pc0 + 4 * i4);
-            const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
-            const float ss[4] = {sv.x, sv.y, sv.z, sv.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              x[4 * i4 + e] = rope_elem(cc[e], ss[e], x[4 * i4 + e], xp[4 * i4 + e], first);
-          }
+        for (int i = 0; i < 16; ++i) {
+          // split-half partner d +- D/2: the same element of lane g ^ 2 (32
+          // lanes away); permlane32_swap(x, x) gives [0] = lanes 0-31's x,
+          // [1] = lanes 32-63's x on both halves
+          auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i]), __float_as_uint(x[i]),
+                                                     false, false);
+          const float half_partner = __uint_as_float(c0 < HALF ? sw[1] : sw[0]);
+          const float partner = p.interleaved ? x[i ^ 1] : half_partner;
+          const bool first = p.interleaved ? (i & 1) == 0 : c0 < HALF;
+          y[i] = rope_elem(cq[ks][i], sq[ks][i], x[i], partner, first);
         }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = y[i];
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -463,64 +465,55 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
 
 // Merge of the split partials of one (sequence, kv head): grid (batch, Hkv).
 // The partials were just written by other workgroups (often on other XCDs),
-// so every global read here is a full memory latency: the kernel issues them
-// in independent batches. Phase 1, one wave per head: max of the split maxima
-// and the rescaled sum of the split sums. Phase 2, one thread per (head, dim):
-// the rescaled sum of the split outputs, eight splits per batch of loads.
+// so every global read is a full memory latency: each thread loads the (m, l,
+// o) of up to 16 splits in one batch and merges them online; with a uniform
+// split count the range comes from the launch, not from seq_info.
 template <int D, int G>
 __global__ __launch_bounds__(256) void gqa_decode_combine_kernel(DecodeParams p) {
   const int b = blockIdx.x;
   const int kvh = blockIdx.y;
-  const int split_base = p.seq_info[2 * b];
-  const int nsplit = p.seq_info[2 * b + 1];
+  int split_base, nsplit;
+  if (p.uniform_nsplit > 0) {
+    nsplit = p.uniform_nsplit;
+    split_base = b * nsplit;
+  } else {
+    split_base = p.seq_info[2 * b];
+    nsplit = p.seq_info[2 * b + 1];
+  }
   if (nsplit <= 1) return;
   const int Hq = p.kv_heads * G;
   const size_t stride = (size_t)p.kv_heads * (G * (D + 2));
   const float* p0 = p.partials + ((size_t)split_base * p.kv_heads + kvh) * (G * (D + 2));
-  __shared__ float sm_M[G], sm_inv[G];
-  const int lane = threadIdx.x & 63;
-  for (int hd = threadIdx.x >> 6; hd < G; hd += 4) {
-    float M = -INFINITY;
-    for (int s0 = 0; s0 < nsplit; s0 += 64)
-      if (s0 + lane < nsplit) M = fmaxf(M, p0[(s0 + lane) * stride + hd * (D + 2)]);
-    M = wave_max(M);
-    float Ls = 0.0f;
-    for (int s0 = 0; s0 < nsplit; s0 += 64) {
-      if (s0 + lane < nsplit) {
-        const float* ps = p0 + (s0 + lane) * stride + hd * (D + 2);
-        const float m = ps[0];
-        if (m != -INFINITY) Ls += ps[1] * fast_exp2(m - M);
-      }
-    }
-    Ls = wave_sum(Ls);
-    if (lane == 0) {
-      sm_M[hd] = M;
-      sm_inv[hd] = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-    }
-  }
-  __syncthreads();
   for (int t = threadIdx.x; t < G * D; t += 256) {
     const int hd = t / D, d = t % D;
-    const float M = sm_M[hd];
     const float* ph = p0 + hd * (D + 2);
-    float O = 0.0f;
-    int s = 0;
-    for (; s + 8 <= nsplit; s += 8) {
-      float m[8], o[8];
+    float M = -INFINITY, Ls = 0.0f, O = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += 16) {
+      float m[16], l[16], o[16];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        m[i] = ph[(s + i) * stride];
-        o[i] = ph[(s + i) * stride + 2 + d];
+      for (int i = 0; i < 16; ++i) {
+        const bool in = s0 + i < nsplit;
+        const float* ps = ph + (size_t)(in ? s0 + i : s0) * stride;
+        m[i] = in ? ps[0] : -INFINITY;
+        l[i] = ps[1];
+        o[i] = ps[2 + d];
       }
+      float mb = M;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (m[i] != -INFINITY) O += o[i] * fast_exp2(m[i] - M);
+      for (int i = 0; i < 16; ++i) mb = fmaxf(mb, m[i]);
+      if (mb == -INFINITY) continue;
+      const float f0 = M == -INFINITY ? 0.0f : fast_exp2(M - mb);
+      Ls *= f0;
+      O *= f0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float f = m[i] == -INFINITY ? 0.0f : fast_exp2(m[i] - mb);
+        Ls += l[i] * f;
+        O += o[i] * f;
+      }
+      M = mb;
     }
-    for (; s < nsplit; ++s) {
-      const float m = ph[s * stride];
-      if (m != -INFINITY) O += ph[s * stride + 2 + d] * fast_exp2(m - M);
-    }
-    p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = O * sm_inv[hd];
+    p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
   }
 }
 

@@ -258,8 +258,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   decode_work_item(p, work, lane, b, split, nsplit, split_base);
   if (b < 0 || b >= p.batch) return;  // uniform over the workgroup
 
-  // page ids of the split, the query and the length in one round of loads;
-  // cos / sin of the position follow once the length is known
+  // length first; then the page ids of the split; then the query and the
+  // cos / sin of position L-1, all in flight across the barrier and ahead
+  // of the first tile
+  const int L = p.seq_lens[b] + p.pending;
   const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
   const int first_page = split * (p.split_tokens / kPageTokens);
   __shared__ int sm_pg[kMaxSplitPages];
@@ -289,8 +291,20 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
       for (int i = 0; i < 32; ++i) x[qd][i] = 0.0f;
     }
   }
+  float cq[32], sq[32];
+  if (p.do_rotary) {
+    const int c0 = p.interleaved ? 16 * g : (g < 2 ? 32 * g : 32 * g - kD / 2);
+    const float* cr = p.cos_cache + (size_t)(L - 1) * (kD / 2) + c0;
+    const float* sr = p.sin_cache + (size_t)(L - 1) * (kD / 2) + c0;
+    // interleaved: pair i >> 1 of the lane's 32 dims, 16 values
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int ci = p.interleaved ? (i >> 1) : i;
+      cq[i] = cr[ci];
+      sq[i] = sr[ci];
+    }
+  }
 
-  const int L = p.seq_lens[b] + p.pending;
   const int t_begin = split * p.split_tokens;
   const int t_end = min(L, t_begin + p.split_tokens);
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
@@ -321,20 +335,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   if (appender && my_tiles > 1) append();
 
   // ---- Q: RoPE at position L-1, normalised by the head's max|Q| ----
-  float cq[32], sq[32];
-  if (p.do_rotary) {
-    const int pos = L - 1;
-    const int c0 = p.interleaved ? 16 * g : (g < 2 ? 32 * g : 32 * g - kD / 2);
-    const float* cr = p.cos_cache + (size_t)pos * (kD / 2) + c0;
-    const float* sr = p.sin_cache + (size_t)pos * (kD / 2) + c0;
-    // interleaved: pair i >> 1 of the lane's 32 dims, 16 values
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const int ci = p.interleaved ? (i >> 1) : i;
-      cq[i] = cr[ci];
-      sq[i] = sr[ci];
-    }
-  }
   v8h Bh[HT][kNG], Bl[HT][kNG];
   float qsn[HT], q_scale[HT];
 #pragma unroll
