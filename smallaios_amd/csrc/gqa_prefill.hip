@@ -4,18 +4,24 @@
 //
 // Workgroup = 4 waves = 128 attention rows = (128/G query positions) x (G
 // heads of one kv head), so every K/V tile is loaded once per workgroup and
-// shared by the whole GQA group. Per 64-token KV tile (4 pages):
-//   staging  all threads: int8 codes -> f16 (exact: |code| <= 128) into LDS,
-//            K token-major, V in the permuted k-order the PV operand needs;
-//            rows padded so the 16-byte LDS reads are bank-conflict free.
-//   S^T      A = K tile (LDS), B = Q^T (registers, f16 of q / rowmax|q|);
-//            lane (row r, g) receives tokens 4g+e of each 16-token block,
-//            so the row softmax is in-lane plus two cross-group shuffles and
-//            P feeds the PV A operand straight from registers.
-//   PV       A = P * s_v / max(s_v) (f16), B = V codes (LDS f16); the tile's
-//            max(s_v) is carried in the accumulator's running scale.
-// Scores are rescaled per element: s = <q', k_code> * rowmax|q| * s_k[t] *
-// scale * log2(e); online softmax in the log2 domain.
+// shared by the whole GQA group; each wave owns two 16-row blocks.
+// Per 64-token KV tile (4 pages):
+//   staging  the next tile's int8 codes and scales are loaded into registers
+//            while the current tile is computed, then converted to f16
+//            (exact: |code| <= 128) into the other half of a double-buffered
+//            LDS tile: K token-major, V in the permuted k-order of the PV
+//            operand; rows padded so the 16-byte LDS reads are conflict-free.
+//            One barrier per tile.
+//   S^T      A = K tile (LDS), B = Q^T (registers, f16 of q * scale * log2 e);
+//            lane (row r, g) receives tokens 4g+e of each 16-token block, so
+//            the row softmax is in-lane plus two cross-group reductions and P
+//            feeds the PV A operand straight from registers. Each K fragment
+//            read from LDS serves both row blocks of the wave.
+//   PV       A = P * s_v (f16), B = V codes (LDS f16); each V fragment serves
+//            both row blocks.
+// Scores: s = <q', k_code> * s_k[t], online softmax in the log2 domain. Only
+// tiles that cross the causal diagonal (or the end of the sequence) apply the
+// mask; the accumulator rescale is skipped when no row maximum moved.
 #include "sai_internal.h"
 
 namespace sai {
@@ -26,10 +32,13 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// RoPE of one element; both products rounded on their own, branch-free.
 __device__ __forceinline__ float rope_elem(float c, float s, float own, float partner,
                                            bool first) {
 #pragma clang fp contract(off)
-  return first ? (c * own - s * partner) : (s * partner + c * own);
+  const float a = c * own;
+  const float b = s * partner;
+  return a + (first ? -b : b);
 }
 
 // 4 int8 codes (one dword) -> 4 exact f16 values, as two packed halves:
@@ -44,29 +53,139 @@ __device__ __forceinline__ void codes4_to_f16(uint32_t w, uint32_t& h01, uint32_
   h23 = __builtin_bit_cast(uint32_t, hb);
 }
 
+// max / sum over the four lane groups (lanes r, r+16, r+32, r+48), on the
+// VALU lane-swap instructions rather than LDS permutes
 __device__ __forceinline__ float xgroup_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float xgroup_sum(float v) {
-  v += __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <int D, int G>
-__global__ __launch_bounds__(256) void gqa_prefill_int8_kernel(PrefillParams p) {
-  constexpr int KS = D / 32;       // 32-dim k steps of QK
-  constexpr int JB = D / 16;       // 16-dim column blocks of PV
-  constexpr int QT = 128 / G;      // query positions per workgroup
-  constexpr int KROW = D + 8;      // padded f16 row of the K tile
-  constexpr int VROW = 4 * 8 + 8;  // padded f16 (kstep, dim) row of the V tile: 4 groups x 8
-  constexpr size_t BB = block_bytes_int8(D);
+template <int D>
+struct PrefillTile {
+  static constexpr int KROW = D + 8;      // padded f16 row of the K tile
+  static constexpr int VROW = 4 * 8 + 8;  // padded f16 (kstep, dim) row: 4 groups x 8
+  _Float16 k[64 * KROW];
+  _Float16 v[2 * D * VROW];
+  float sk[64];
+  float sv[64];
+};
 
-  __shared__ _Float16 sK[64 * KROW];
-  __shared__ _Float16 sV[2 * D * VROW];
-  __shared__ float sSk[64];
-  __shared__ float sSv[64];
+// Codes and scales of one 64-token tile, held in registers between the load
+// and the LDS store: K chunks (token, 16 dims), V chunks (page, dim), and one
+// scale per thread for the first 128 threads.
+template <int D, int NT>
+struct TileStage {
+  static constexpr int KN = 64 * (D / 16);      // 16-byte K chunks of a tile
+  static constexpr int VN = 4 * D;              // 16-byte V chunks of a tile
+  static constexpr int KC = (KN + NT - 1) / NT;  // per thread
+  static constexpr int VC = (VN + NT - 1) / NT;
+  uint4 kc[KC];
+  uint4 vc[VC];
+  float sc;
+};
+
+template <int D, int NT>
+__device__ __forceinline__ void stage_load(TileStage<D, NT>& S, const PrefillParams& p,
+                                           const int32_t* pt, int kvh, int t0, int last_page,
+                                           int total, int tid) {
+  constexpr size_t BB = block_bytes_int8(D);
+#pragma unroll
+  for (int i = 0; i < TileStage<D, NT>::KC; ++i) {
+    const int c = tid + NT * i;
+    if (TileStage<D, NT>::KN % NT != 0 && c >= TileStage<D, NT>::KN) break;
+    const int tok = c / (D / 16);
+    const int dp = c % (D / 16);
+    const int pg = min((t0 + tok) / kPageTokens, last_page);
+    const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
+    S.kc[i] = *(const uint4*)(blk + (size_t)((t0 + tok) % kPageTokens) * D + 16 * dp);
+  }
+#pragma unroll
+  for (int i = 0; i < TileStage<D, NT>::VC; ++i) {
+    const int c = tid + NT * i;
+    if (TileStage<D, NT>::VN % NT != 0 && c >= TileStage<D, NT>::VN) break;
+    const int cb = c / D;
+    const int d = c % D;
+    const int pg = min(t0 / kPageTokens + cb, last_page);
+    const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
+    S.vc[i] = *(const uint4*)(blk + 16 * D + (size_t)d * 16);
+  }
+  S.sc = 0.0f;
+  if (tid < 128) {
+    const int which = tid >> 6;
+    const int tok = tid & 63;
+    const int pg = min((t0 + tok) / kPageTokens, last_page);
+    const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
+    const float v = ((const float*)(blk + 32 * D + 64 * which))[(t0 + tok) % kPageTokens];
+    S.sc = t0 + tok < total ? v : 0.0f;
+  }
+}
+
+template <int D, int NT>
+__device__ __forceinline__ void stage_store(const TileStage<D, NT>& S, PrefillTile<D>& T,
+                                            int tid) {
+  constexpr int KROW = PrefillTile<D>::KROW;
+  constexpr int VROW = PrefillTile<D>::VROW;
+#pragma unroll
+  for (int i = 0; i < TileStage<D, NT>::KC; ++i) {
+    const int c = tid + NT * i;
+    if (TileStage<D, NT>::KN % NT != 0 && c >= TileStage<D, NT>::KN) break;
+    const int tok = c / (D / 16);
+    const int dp = c % (D / 16);
+    uint32_t h[8];
+    codes4_to_f16(S.kc[i].x, h[0], h[1]);
+    codes4_to_f16(S.kc[i].y, h[2], h[3]);
+    codes4_to_f16(S.kc[i].z, h[4], h[5]);
+    codes4_to_f16(S.kc[i].w, h[6], h[7]);
+    uint4* dst = (uint4*)(T.k + tok * KROW + 16 * dp);
+    dst[0] = uint4{h[0], h[1], h[2], h[3]};
+    dst[1] = uint4{h[4], h[5], h[6], h[7]};
+  }
+#pragma unroll
+  for (int i = 0; i < TileStage<D, NT>::VC; ++i) {
+    const int c = tid + NT * i;
+    if (TileStage<D, NT>::VN % NT != 0 && c >= TileStage<D, NT>::VN) break;
+    const int cb = c / D;
+    const int d = c % D;
+    // slot s of page cb = token 16*cb + s: k step cb>>1, group s>>2, element
+    // (cb&1)*4 + (s&3) of the PV operand's k-order
+    _Float16* row = T.v + ((size_t)(cb >> 1) * D + d) * VROW;
+    const int half = (cb & 1) * 4;
+    const uint32_t ws[4] = {S.vc[i].x, S.vc[i].y, S.vc[i].z, S.vc[i].w};
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) {
+      uint32_t h01, h23;
+      codes4_to_f16(ws[gg], h01, h23);
+      *(uint2*)(row + gg * 8 + half) = uint2{h01, h23};
+    }
+  }
+  if (tid < 128) {
+    if (tid < 64)
+      T.sk[tid] = S.sc;
+    else
+      T.sv[tid - 64] = S.sc;
+  }
+}
+
+template <int D, int G, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_int8_kernel(PrefillParams p) {
+  constexpr int NT = 64 * NW;
+  constexpr int KS = D / 32;      // 32-dim k steps of QK
+  constexpr int JB = D / 16;      // 16-dim column blocks of PV
+  constexpr int QT = 32 * NW / G; // query positions per workgroup
+  constexpr int KROW = PrefillTile<D>::KROW;
+  constexpr int VROW = PrefillTile<D>::VROW;
+  constexpr int HALF = D / 2;
+
+  __shared__ PrefillTile<D> sT[2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -83,58 +202,62 @@ __global__ __launch_bounds__(256) void gqa_prefill_int8_kernel(PrefillParams p) 
   const int Hq = p.kv_heads * G;
   const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
   const int last_page = (total - 1) / kPageTokens;
+  const int max_pos = past + min(q0 + QT, p.sq) - 1;
+  const int n_tiles = max_pos / 64 + 1;
+  // tiles entirely at or below the smallest position of the workgroup need
+  // no causal mask (they are also inside the sequence)
+  const int full_tiles = (past + q0 + 1) / 64;
+
+  // first tile in flight while Q is prepared
+  TileStage<D, NT> S;
+  stage_load<D, NT>(S, p, pt, kvh, 0, last_page, total, tid);
 
   // ---- Q^T operand: rows R = wave*32 + rb*16 + r -> (position, head) -------
+  // f16 of RoPE(q) * scale * log2(e); lane (r, g) holds dims 32ks + 8g .. +7
   v8h qB[2][KS];
-  float qfac[2];   // rowmax|q| * scale * log2(e)
-  int qpos[2];     // absolute position of the row (clamped for dead rows)
-  bool qlive[2];
+  int qpos[2];  // absolute position of the row (clamped for dead rows)
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     const int R = wave * 32 + rb * 16 + r;
     const int il = q0 + R / G;
     const int hq = kvh * G + R % G;
-    qlive[rb] = il < p.sq;
-    const int i = qlive[rb] ? il : p.sq - 1;
+    const int i = il < p.sq ? il : p.sq - 1;
     const int pos = past + i;
-    qpos[rb] = pos;
+    qpos[rb] = il < p.sq ? pos : -1;
     const size_t qbase = (((size_t)b * p.sq + i) * Hq + hq) * D;
-    constexpr int HALF = D / 2;
     float x[KS][8];
-    float amax = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = 8 * g + 32 * ks + e;
-        float v = load_elem(p.q, qbase + d, p.q_dtype);
-        if (p.do_rotary) {
-          int dp, pi;
-          bool first;
-          if (p.interleaved) {
-            dp = d ^ 1;
-            pi = d >> 1;
-            first = (d & 1) == 0;
-          } else {
-            first = d < HALF;
-            dp = first ? d + HALF : d - HALF;
-            pi = first ? d : d - HALF;
-          }
-          const float vp = load_elem(p.q, qbase + dp, p.q_dtype);
-          v = rope_elem(p.cos_cache[(size_t)pos * HALF + pi], p.sin_cache[(size_t)pos * HALF + pi],
-                        v, vp, first);
+      for (int e = 0; e < 8; ++e) x[ks][e] = load_elem(p.q, qbase + 32 * ks + 8 * g + e, p.q_dtype);
+    if (p.do_rotary) {
+      // partners: interleaved d ^ 1 (same chunk); split-half d +- D/2 (chunk
+      // ks +- KS/2, the same lane)
+      float y[KS][8];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = 32 * ks + 8 * g + e;
+          const bool first = p.interleaved ? (e & 1) == 0 : d < HALF;
+          const int pi = p.interleaved ? (d >> 1) : (first ? d : d - HALF);
+          const float partner = p.interleaved ? x[ks][e ^ 1] : x[(ks + KS / 2) % KS][e];
+          y[ks][e] = rope_elem(p.cos_cache[(size_t)pos * HALF + pi],
+                               p.sin_cache[(size_t)pos * HALF + pi], x[ks][e], partner, first);
         }
-        x[ks][e] = v;
-        amax = fmaxf(amax, fabsf(v));
-      }
-    amax = xgroup_max(amax);
-    const float inv = amax > 0.0f ? 1.0f / amax : 0.0f;
-    qfac[rb] = amax * p.scale_log2;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[ks][e] = y[ks][e];
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qB[rb][ks][e] = (_Float16)(x[ks][e] * inv);
+      for (int e = 0; e < 8; ++e) qB[rb][ks][e] = (_Float16)(x[ks][e] * p.scale_log2);
   }
+
+  stage_store<D, NT>(S, sT[0], tid);
+  __syncthreads();
 
   // ---- online softmax state ----------------------------------------------------
   float m_run[2] = {-INFINITY, -INFINITY};  // lane (row r): row r of block rb
@@ -144,130 +267,105 @@ __global__ __launch_bounds__(256) void gqa_prefill_int8_kernel(PrefillParams p) 
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
     for (int jb = 0; jb < JB; ++jb) acc[rb][jb] = v4f{0.f, 0.f, 0.f, 0.f};
-  float vscale = 1.0f;  // accumulator units: true O = acc * vscale
 
-  const int max_pos = past + min(q0 + QT, p.sq) - 1;
-  const int n_tiles = max_pos / 64 + 1;
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int t0 = tile * 64;
-    __syncthreads();  // previous tile's LDS reads are done
-    // -- stage K: 64 tokens x D codes, 16-code chunks
-    for (int c = tid; c < 64 * (D / 16); c += 256) {
-      const int tok = c / (D / 16);
-      const int dp = c % (D / 16);
-      const int pg = min((t0 + tok) / kPageTokens, last_page);
-      const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
-      const uint4 w = *(const uint4*)(blk + (size_t)((t0 + tok) % kPageTokens) * D + 16 * dp);
-      uint32_t h[8];
-      codes4_to_f16(w.x, h[0], h[1]);
-      codes4_to_f16(w.y, h[2], h[3]);
-      codes4_to_f16(w.z, h[4], h[5]);
-      codes4_to_f16(w.w, h[6], h[7]);
-      uint4* dst = (uint4*)(sK + tok * KROW + 16 * dp);
-      dst[0] = uint4{h[0], h[1], h[2], h[3]};
-      dst[1] = uint4{h[4], h[5], h[6], h[7]};
-    }
-    // -- stage V: (page cb, dim d) rows of 16 slots -> sV[kst][d][g][elem]
-    for (int c = tid; c < 4 * D; c += 256) {
-      const int cb = c / D;
-      const int d = c % D;
-      const int pg = min(t0 / kPageTokens + cb, last_page);
-      const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
-      const uint4 w = *(const uint4*)(blk + 16 * D + (size_t)d * 16);
-      const int kst = cb >> 1;
-      const int half = (cb & 1) * 4;
-      _Float16* row = sV + ((size_t)kst * D + d) * VROW;
-      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int gg = 0; gg < 4; ++gg) {  // slots 4gg..4gg+3
-        uint32_t h01, h23;
-        codes4_to_f16(ws[gg], h01, h23);
-        *(uint2*)(row + gg * 8 + half) = uint2{h01, h23};
-      }
-    }
-    if (tid < 128) {
-      const int which = tid >> 6;
-      const int tok = tid & 63;
-      const int pg = min((t0 + tok) / kPageTokens, last_page);
-      const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
-      const float v = ((const float*)(blk + 32 * D + 64 * which))[(t0 + tok) % kPageTokens];
-      const bool ok = t0 + tok < total;
-      if (which == 0)
-        sSk[tok] = ok ? v : 0.0f;
-      else
-        sSv[tok] = ok ? v : 0.0f;
-    }
-    __syncthreads();
+    const PrefillTile<D>& T = sT[tile & 1];
+    const bool more = tile + 1 < n_tiles;
+    if (more) stage_load<D, NT>(S, p, pt, kvh, t0 + 64, last_page, total, tid);
 
-    const float svmax = wave_max(sSv[lane]);
-    const float inv_svmax = svmax > 0.0f ? 1.0f / svmax : 0.0f;
-
+    // S^T for both row blocks: 4 column blocks of 16 tokens; k steps outer so
+    // that eight independent accumulation chains interleave on the MFMA pipe
+    float s[2][4][4];
+    {
+      v4f c[4][2];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      // S^T for this row block: 4 column blocks of 16 tokens
-      float s[4][4];
+      for (int cb = 0; cb < 4; ++cb) c[cb][0] = c[cb][1] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+          const v8h a = *(const v8h*)(T.k + (16 * cb + r) * KROW + 8 * g + 32 * ks);
+          c[cb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qB[0][ks], c[cb][0], 0, 0, 0);
+          c[cb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qB[1][ks], c[cb][1], 0, 0, 0);
+        }
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
-        v4f c = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const v8h a = *(const v8h*)(sK + (16 * cb + r) * KROW + 8 * g + 32 * ks);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qB[rb][ks], c, 0, 0, 0);
-        }
-        const float4 skv = *(const float4*)(sSk + 16 * cb + 4 * g);
+        const float4 skv = *(const float4*)(T.sk + 16 * cb + 4 * g);
         const float skx[4] = {skv.x, skv.y, skv.z, skv.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int t = t0 + 16 * cb + 4 * g + e;
-          const float sc = c[e] * qfac[rb] * skx[e];
-          s[cb][e] = (t <= qpos[rb]) ? sc : -INFINITY;
-        }
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[rb][cb][e] = c[cb][rb][e] * skx[e];
       }
+    }
+    if (tile >= full_tiles) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int t = t0 + 16 * cb + 4 * g + e;
+            s[rb][cb][e] = t <= qpos[rb] ? s[rb][cb][e] : -INFINITY;
+          }
+    }
+
+    v8h pa[2][2];
+    float alpha[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
       float mt = -INFINITY;
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[cb][e]);
+        for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[rb][cb][e]);
       mt = xgroup_max(mt);
       const float m_new = fmaxf(m_run[rb], mt);
       const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      const float alpha = fast_exp2(m_run[rb] - m_use);
+      alpha[rb] = fast_exp2(m_run[rb] - m_use);
       float psum = 0.0f;
-      v8h pa[2];
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
-        const float4 svv = *(const float4*)(sSv + 16 * cb + 4 * g);
+        const float4 svv = *(const float4*)(T.sv + 16 * cb + 4 * g);
         const float svx[4] = {svv.x, svv.y, svv.z, svv.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float pe = fast_exp2(s[cb][e] - m_use);
+          const float pe = fast_exp2(s[rb][cb][e] - m_use);
           psum += pe;
-          pa[cb >> 1][(cb & 1) * 4 + e] = (_Float16)(pe * svx[e] * inv_svmax);
+          pa[rb][cb >> 1][(cb & 1) * 4 + e] = (_Float16)(pe * svx[e]);
         }
       }
       psum = xgroup_sum(psum);
-      l_run[rb] = l_run[rb] * alpha + psum;
+      l_run[rb] = l_run[rb] * alpha[rb] + psum;
       m_run[rb] = m_new;
+    }
 
-      // rescale the accumulator rows 4g+e (alpha of row j lives in lane j)
-      const float ratio = vscale * inv_svmax;  // old units -> new units
-      float ae[4];
+    // rescale the accumulator rows 4g+e (alpha of row j lives in lane j),
+    // unless no row of the wave moved its maximum
+    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.0f || alpha[1] != 1.0f) != 0) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ae[e] = __shfl(alpha, 4 * g + e, 64) * (svmax > 0.0f ? ratio : 1.0f);
+      for (int rb = 0; rb < 2; ++rb) {
+        float ae[4];
 #pragma unroll
-      for (int jb = 0; jb < JB; ++jb) {
-        v4f o = acc[rb][jb];
+        for (int e = 0; e < 4; ++e) ae[e] = __shfl(alpha[rb], 4 * g + e, 64);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] *= ae[e];
+        for (int jb = 0; jb < JB; ++jb)
 #pragma unroll
-        for (int kst = 0; kst < 2; ++kst) {
-          const v8h bv = *(const v8h*)(sV + ((size_t)kst * D + 16 * jb + r) * VROW + 8 * g);
-          o = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kst], bv, o, 0, 0, 0);
-        }
-        acc[rb][jb] = o;
+          for (int e = 0; e < 4; ++e) acc[rb][jb][e] *= ae[e];
       }
     }
-    if (svmax > 0.0f) vscale = svmax;
+#pragma unroll
+    for (int kst = 0; kst < 2; ++kst)
+#pragma unroll
+      for (int jb = 0; jb < JB; ++jb) {
+        const v8h bv = *(const v8h*)(T.v + ((size_t)kst * D + 16 * jb + r) * VROW + 8 * g);
+        acc[0][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[0][kst], bv, acc[0][jb], 0, 0, 0);
+        acc[1][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[1][kst], bv, acc[1][jb], 0, 0, 0);
+      }
+
+    if (more) stage_store<D, NT>(S, sT[(tile + 1) & 1], tid);
+    __syncthreads();
   }
 
   // ---- write O / l ------------------------------------------------------------
@@ -282,24 +380,33 @@ __global__ __launch_bounds__(256) void gqa_prefill_int8_kernel(PrefillParams p) 
       if (il >= p.sq) continue;
       const int hq = kvh * G + R % G;
       float* o = p.out + (((size_t)b * p.sq + il) * Hq + hq) * D;
-      const float f = l > 0.0f ? vscale / l : 0.0f;
+      const float f = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
       for (int jb = 0; jb < JB; ++jb) o[16 * jb + r] = acc[rb][jb][e] * f;
     }
   }
 }
 
-template <int D>
-hipError_t launch_d(const PrefillParams& p, int group, hipStream_t st) {
+template <int D, int NW>
+hipError_t launch_dn(const PrefillParams& p, int group, hipStream_t st) {
   auto grid = [&](int qt) { return dim3((p.sq + qt - 1) / qt, p.kv_heads, p.batch); };
+  const dim3 block(64 * NW);
   switch (group) {
-    case 1: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 1>), grid(128), dim3(256), 0, st, p); break;
-    case 2: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 2>), grid(64), dim3(256), 0, st, p); break;
-    case 4: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 4>), grid(32), dim3(256), 0, st, p); break;
-    case 8: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 8>), grid(16), dim3(256), 0, st, p); break;
+    case 1: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 1, NW>), grid(32 * NW), block, 0, st, p); break;
+    case 2: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 2, NW>), grid(16 * NW), block, 0, st, p); break;
+    case 4: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 4, NW>), grid(8 * NW), block, 0, st, p); break;
+    case 8: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 8, NW>), grid(4 * NW), block, 0, st, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// 8 waves (256 rows) per workgroup: the staged K/V tile serves twice the rows
+// of a 4-wave workgroup at the same LDS footprint (measured 10% faster on the
+// 2 x 2048-over-8192 chunk).
+template <int D>
+hipError_t launch_d(const PrefillParams& p, int group, hipStream_t st) {
+  return launch_dn<D, 8>(p, group, st);
 }
 
 }  // namespace
