@@ -202,6 +202,18 @@ int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves);
 int32_t sai_set_decode_merge(sai_ctx* ctx, int32_t in_kernel);
 /* Number of workgroups and split size of the last decode launch on ctx. */
 sai_status sai_last_decode_shape(const sai_ctx* ctx, int32_t* workgroups, int32_t* split_tokens);
+/* Kernel timing of the decode step: with slots > 0, every sai_gqa_decode /
+ * sai_gqa_with_cache call records two HIP events on its stream around the
+ * decode kernel alone (not the split merge that follows it), in a ring of
+ * `slots` event pairs (at most 4096), so back-to-back calls are timed without
+ * synchronizing between them. 0 turns timing off. Returns the previous slot
+ * count. */
+int32_t sai_set_decode_timing(sai_ctx* ctx, int32_t slots);
+/* Decode-kernel durations in microseconds of the most recent timed calls,
+ * oldest first, at most max_n of them (and at most the slot count); waits for
+ * the last call's end event. Returns how many were written, or a negative
+ * status. */
+int32_t sai_decode_kernel_times(sai_ctx* ctx, float* us, int32_t max_n);
 
 #ifdef __cplusplus
 }

@@ -74,6 +74,7 @@ EXPORTS = [
     "sai_kvcache_lengths", "sai_kvcache_read", "sai_kvcache_pool", "sai_kv_append",
     "sai_gqa_decode", "sai_gqa_with_cache", "sai_gqa_prefill", "sai_set_decode_split",
     "sai_set_decode_waves", "sai_set_decode_merge", "sai_last_decode_shape",
+    "sai_set_decode_timing", "sai_decode_kernel_times",
 ]
 
 
@@ -106,6 +107,8 @@ def _declare(L: C.CDLL) -> None:
         "sai_set_decode_waves": (i32, [p, i32]),
         "sai_set_decode_merge": (i32, [p, i32]),
         "sai_last_decode_shape": (i32, [p, C.POINTER(i32), C.POINTER(i32)]),
+        "sai_set_decode_timing": (i32, [p, i32]),
+        "sai_decode_kernel_times": (i32, [p, C.POINTER(C.c_float), i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -199,6 +202,19 @@ class Runtime:
         wg, sp = C.c_int32(), C.c_int32()
         self._L.sai_last_decode_shape(self.handle, C.byref(wg), C.byref(sp))
         return wg.value, sp.value
+
+    def set_decode_timing(self, slots: int) -> int:
+        """HIP events around the decode kernel alone for the last `slots`
+        decode calls (0 = off)."""
+        return int(self._L.sai_set_decode_timing(self.handle, int(slots)))
+
+    def decode_kernel_times(self, max_n: int):
+        """Decode-kernel durations (us) of the most recent timed calls."""
+        buf = (C.c_float * max_n)()
+        n = self._L.sai_decode_kernel_times(self.handle, buf, max_n)
+        if n < 0:
+            self.check(n, "sai_decode_kernel_times")
+        return [float(buf[i]) for i in range(n)]
 
 
 class KvCache:

@@ -113,12 +113,6 @@ __device__ __forceinline__ void decode_work_item(const DecodeParams& p, int work
   }
 }
 
-// Split-partial merge launcher (the combine kernel lives in gqa_decode.hip).
-hipError_t launch_decode_combine(const DecodeParams& p, int head_dim, int group, hipStream_t st);
 
-// int4 decode (gqa_decode_int4.hip): head_dim 128; always merges through the
-// combine kernel when a sequence has several splits.
-hipError_t launch_gqa_decode_int4(const DecodeParams& p, int head_dim, int group, int work_items,
-                                  bool combine, hipStream_t st);
 
 }  // namespace sai

@@ -35,6 +35,9 @@ struct sai_ctx {
   int32_t decode_merge = 0;  // 0: combine kernel, 1: in-kernel merge
   int32_t last_wg = 0;
   int32_t last_split = 0;
+  // decode-kernel timing ring: event pairs of the last `slots` calls
+  std::vector<hipEvent_t> ev_start, ev_end;
+  int64_t timed_calls = 0;
 };
 
 struct sai_kvcache {
@@ -196,6 +199,8 @@ SAI_API void sai_destroy(sai_ctx* ctx) {
   if (ctx->partials) (void)hipFree(ctx->partials);
   if (ctx->seq_info) (void)hipFree(ctx->seq_info);
   if (ctx->counters) (void)hipFree(ctx->counters);
+  for (hipEvent_t e : ctx->ev_start) (void)hipEventDestroy(e);
+  for (hipEvent_t e : ctx->ev_end) (void)hipEventDestroy(e);
   delete ctx;
 }
 
@@ -230,6 +235,48 @@ SAI_API int32_t sai_set_decode_merge(sai_ctx* ctx, int32_t in_kernel) {
   int32_t prev = ctx->decode_merge;
   ctx->decode_merge = in_kernel ? 1 : 0;
   return prev;
+}
+
+SAI_API int32_t sai_set_decode_timing(sai_ctx* ctx, int32_t slots) {
+  if (!ctx) return 0;
+  const int32_t prev = (int32_t)ctx->ev_start.size();
+  DeviceGuard dg(ctx->device);
+  for (hipEvent_t e : ctx->ev_start) (void)hipEventDestroy(e);
+  for (hipEvent_t e : ctx->ev_end) (void)hipEventDestroy(e);
+  ctx->ev_start.clear();
+  ctx->ev_end.clear();
+  ctx->timed_calls = 0;
+  const int32_t n = std::min<int32_t>(std::max<int32_t>(slots, 0), 4096);
+  for (int32_t i = 0; i < n; ++i) {
+    hipEvent_t a = nullptr, b = nullptr;
+    if (hipEventCreate(&a) != hipSuccess) break;
+    if (hipEventCreate(&b) != hipSuccess) {
+      (void)hipEventDestroy(a);
+      break;
+    }
+    ctx->ev_start.push_back(a);
+    ctx->ev_end.push_back(b);
+  }
+  return prev;
+}
+
+SAI_API int32_t sai_decode_kernel_times(sai_ctx* ctx, float* us, int32_t max_n) {
+  if (!ctx || !us) return SAI_ERR_NULL;
+  const int64_t slots = (int64_t)ctx->ev_start.size();
+  if (slots == 0 || ctx->timed_calls == 0 || max_n <= 0) return 0;
+  DeviceGuard dg(ctx->device);
+  const int64_t n = std::min<int64_t>({(int64_t)max_n, slots, ctx->timed_calls});
+  const int64_t last = (ctx->timed_calls - 1) % slots;
+  hipError_t e = hipEventSynchronize(ctx->ev_end[last]);
+  if (e != hipSuccess) return hip_fail(ctx, e, "decode timing");
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t k = (ctx->timed_calls - n + i) % slots;
+    float ms = 0.0f;
+    e = hipEventElapsedTime(&ms, ctx->ev_start[k], ctx->ev_end[k]);
+    if (e != hipSuccess) return hip_fail(ctx, e, "decode timing");
+    us[i] = ms * 1000.0f;
+  }
+  return (int32_t)n;
 }
 
 SAI_API sai_status sai_last_decode_shape(const sai_ctx* ctx, int32_t* workgroups,
@@ -613,9 +660,26 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   p.k_new = k_new;
   p.v_new = v_new;
   p.kv_dtype = kv_dtype;
-  hipError_t e =
-      sai::launch_gqa_decode(p, D, G, c->desc.quant, (int)work, multi, (hipStream_t)stream);
+  const hipStream_t hs = (hipStream_t)stream;
+  const int64_t slots = (int64_t)ctx->ev_start.size();
+  const int64_t slot = slots ? ctx->timed_calls % slots : 0;
+  if (slots) {
+    const hipError_t ee = hipEventRecord(ctx->ev_start[slot], hs);
+    if (ee != hipSuccess) return hip_fail(ctx, ee, "gqa_decode timing event");
+  }
+  // the decode kernel, then (several splits, merge not in-kernel) the combine
+  hipError_t e = sai::launch_gqa_decode(p, D, G, c->desc.quant, (int)work, false, hs);
   if (e != hipSuccess) return hip_fail(ctx, e, "gqa_decode launch");
+  if (slots) {
+    e = hipEventRecord(ctx->ev_end[slot], hs);
+    if (e != hipSuccess) return hip_fail(ctx, e, "gqa_decode timing event");
+    ++ctx->timed_calls;
+  }
+  const bool in_kernel = c->desc.quant == SAI_KV_INT8 && p.merge_in_kernel;
+  if (multi && !in_kernel) {
+    e = sai::launch_decode_combine(p, D, G, hs);
+    if (e != hipSuccess) return hip_fail(ctx, e, "gqa_decode combine launch");
+  }
   ctx->last_wg = (int32_t)(work * kvh);
   ctx->last_split = split;
   return SAI_OK;

@@ -154,6 +154,12 @@ hipError_t launch_gqa_decode(const DecodeParams& p, int head_dim, int group, int
                              int work_items, bool combine, hipStream_t s);
 hipError_t launch_gqa_prefill(const PrefillParams& p, int head_dim, int group, int quant,
                               hipStream_t s);
+// Split-partial merge of the decode kernels (gqa_decode.hip).
+hipError_t launch_decode_combine(const DecodeParams& p, int head_dim, int group, hipStream_t st);
+// int4 decode (gqa_decode_int4.hip): head_dim 128; merges through the combine
+// kernel when `combine` and a sequence has several splits.
+hipError_t launch_gqa_decode_int4(const DecodeParams& p, int head_dim, int group, int work_items,
+                                  bool combine, hipStream_t st);
 hipError_t launch_seq_advance(int32_t* seq_lens, int batch, int pending, hipStream_t s);
 
 }  // namespace sai

@@ -325,3 +325,23 @@ def test_prefill_chunk_full_size_sampled(rt):
         oc.seq_len = np.array([6144 + i + 1] * 2, dtype=np.int32)
         ref = oc.attend(q[:, i:i + 1], 32, c.cos, c.sin, deq=deq)
         assert_close(got[:, i:i + 1], ref, f"prefill row {i}")
+
+
+# ------------------------------------------------------------- introspection ---
+def test_decode_kernel_timing_ring(rt):
+    """sai_set_decode_timing / sai_decode_kernel_times: events around the decode
+    kernel of back-to-back calls, oldest first, at most the slot count."""
+    log("decode kernel timing ring")
+    c = Case(rt, 0x7100, 2, 8, 2, 128, [700, 300], 1)
+    c.step_kv()
+    q = c.query()
+    prev = rt.set_decode_timing(3)
+    try:
+        assert rt.decode_kernel_times(8) == []
+        for _ in range(5):
+            c.gpu_decode(q)
+        t = rt.decode_kernel_times(8)
+        assert len(t) == 3 and all(0.0 < x < 1e5 for x in t), t
+    finally:
+        rt.set_decode_timing(prev)
+    assert rt.decode_kernel_times(8) == []
