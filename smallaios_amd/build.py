@@ -1,7 +1,9 @@
-"""Builds libsai_hip.so (gfx950 only) in-tree with hipcc.
+"""Builds libsai_hip.so (gfx950 only) in-tree with hipcc, then the C++ host
+library libsai_gqa_host.so over it with g++.
 
 Each .hip source is compiled to an object with its own flags, then linked into
-one shared library that exports only the C ABI of include/sai_hip.h.
+one shared library that exports only the C ABI of include/sai_hip.h. The host
+library (host/gqa_host.cpp) holds no device code.
 """
 from __future__ import annotations
 
@@ -13,6 +15,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsai_hip.so")
+HOST_LIB = os.path.join(HERE, "libsai_gqa_host.so")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+CXX = os.environ.get("CXX", "g++")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 COMMON = [
@@ -59,7 +64,20 @@ def build(verbose: bool = False) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", tmp, *objs])
     os.replace(tmp, LIB)
+    build_host()
     return LIB
+
+
+def build_host() -> str:
+    """libsai_gqa_host.so: the C++ mirror of the reference's GPU dispatch API."""
+    tmp = HOST_LIB + ".tmp"
+    _run([CXX, "-std=c++17", "-O2", "-fPIC", "-shared", "-ffp-contract=off", "-Wall", "-Wextra",
+          "-D__HIP_PLATFORM_AMD__", "-I", INCLUDE, "-I", "/opt/rocm/include",
+          os.path.join(HERE, "host", "gqa_host.cpp"), "-o", tmp,
+          "-L", HERE, "-lsai_hip", "-L", "/opt/rocm/lib", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib"])
+    os.replace(tmp, HOST_LIB)
+    return HOST_LIB
 
 
 if __name__ == "__main__":

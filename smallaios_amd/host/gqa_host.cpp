@@ -1,0 +1,755 @@
+// Implementation of the C++ host side (gqa_host.hpp) over libsai_hip's C ABI.
+// Host code only: device work is done by the library's kernels; this file
+// validates, keeps the cache bookkeeping and maps status codes to errors.
+#include "gqa_host.hpp"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+
+namespace sai::rocm {
+
+namespace {
+
+std::string fmt_code(const char* fmt, const std::string& a, long long b) {
+  char buf[512];
+  std::snprintf(buf, sizeof buf, fmt, a.c_str(), b);
+  return buf;
+}
+
+OpError::Kind kind_of(sai_status st) {
+  switch (st) {
+    case SAI_ERR_INVALID_ATTRIBUTE: return OpError::Kind::InvalidAttribute;
+    case SAI_ERR_SHAPE_MISMATCH: return OpError::Kind::ShapeMismatch;
+    case SAI_ERR_UNSUPPORTED: return OpError::Kind::UnsupportedOp;
+    default: return OpError::Kind::InternalError;
+  }
+}
+
+// IEEE binary16 -> binary32, exact (every half is a float).
+float half_to_float(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1Fu;
+  uint32_t mant = h & 0x3FFu;
+  uint32_t bits;
+  if (exp == 0x1Fu) {
+    bits = sign | 0x7F800000u | (mant << 13);
+  } else if (exp != 0) {
+    bits = sign | ((exp + 112u) << 23) | (mant << 13);
+  } else if (mant == 0) {
+    bits = sign;
+  } else {
+    // subnormal: normalise
+    int e = -1;
+    do {
+      mant <<= 1;
+      ++e;
+    } while ((mant & 0x400u) == 0);
+    bits = sign | ((uint32_t)(112 - e) << 23) | ((mant & 0x3FFu) << 13);
+  }
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+bool is_float_like(DataType dt) { return dt == DataType::Float || dt == DataType::BFloat16; }
+
+int32_t sai_dtype(DataType dt) {
+  return dt == DataType::BFloat16 ? SAI_DTYPE_BF16 : SAI_DTYPE_F32;
+}
+
+}  // namespace
+
+// ----------------------------------------------------------------- errors ---
+HipError HipError::runtime(std::string op, int32_t code) {
+  HipError e;
+  e.kind = Kind::RuntimeError;
+  e.op = std::move(op);
+  e.code = code;
+  return e;
+}
+HipError HipError::alloc_failed(size_t size, int32_t code) {
+  HipError e;
+  e.kind = Kind::AllocFailed;
+  e.size = size;
+  e.code = code;
+  return e;
+}
+HipError HipError::copy_failed(std::string what, int32_t code) {
+  HipError e;
+  e.kind = Kind::CopyFailed;
+  e.op = std::move(what);
+  e.code = code;
+  return e;
+}
+HipError HipError::no_device() {
+  HipError e;
+  e.kind = Kind::NoDevice;
+  return e;
+}
+
+std::string HipError::to_string() const {
+  switch (kind) {
+    case Kind::NoDevice: return "no HIP device found";
+    case Kind::AllocFailed: {
+      char buf[96];
+      std::snprintf(buf, sizeof buf, "hipMalloc(%zu bytes) failed: code %d", size, code);
+      return buf;
+    }
+    case Kind::CopyFailed: return fmt_code("hipMemcpy %s failed: code %lld", op, code);
+    case Kind::RuntimeError: break;
+  }
+  return fmt_code("HIP %s failed: code %lld", op, code);
+}
+
+std::string OpError::to_string() const {
+  switch (kind) {
+    case Kind::UnsupportedOp: return "unsupported operator: " + message;
+    case Kind::ShapeMismatch: return "shape mismatch: " + message;
+    case Kind::InvalidAttribute: return "invalid attribute: " + message;
+    case Kind::InternalError: break;
+  }
+  return "internal error: " + message;
+}
+
+size_t element_size(DataType dt) {
+  switch (dt) {
+    case DataType::Float: case DataType::Int32: return 4;
+    case DataType::Int64: return 8;
+    case DataType::Float16: case DataType::BFloat16: case DataType::UInt16: return 2;
+    case DataType::UInt8: case DataType::Int8: return 1;
+    case DataType::Undefined: break;
+  }
+  return 0;
+}
+
+const char* data_type_name(DataType dt) {
+  switch (dt) {
+    case DataType::Float: return "Float";
+    case DataType::UInt8: return "UInt8";
+    case DataType::Int8: return "Int8";
+    case DataType::UInt16: return "UInt16";
+    case DataType::Int32: return "Int32";
+    case DataType::Int64: return "Int64";
+    case DataType::Float16: return "Float16";
+    case DataType::BFloat16: return "BFloat16";
+    case DataType::Undefined: break;
+  }
+  return "Undefined";
+}
+
+// ---------------------------------------------------------------- runtime ---
+Result<RocmRuntime, HipError> RocmRuntime::init(int device) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0 || device < 0 || device >= n)
+    return HipError::no_device();
+  if (!sai_device_supported(device)) return HipError::runtime("rocm_runtime_init:not_gfx950");
+  sai_ctx* c = nullptr;
+  const sai_status st = sai_init(device, &c);
+  if (st != SAI_OK || !c) return HipError::runtime("rocm_runtime_init", st);
+  return RocmRuntime(c, device);
+}
+
+bool RocmRuntime::supports_op(std::string_view op_type) {
+  return op_type == "GroupQueryAttention";
+}
+
+RocmRuntime& RocmRuntime::operator=(RocmRuntime&& o) noexcept {
+  if (this != &o) {
+    if (ctx_) sai_destroy(ctx_);
+    ctx_ = std::exchange(o.ctx_, nullptr);
+    device_ = o.device_;
+  }
+  return *this;
+}
+
+RocmRuntime::~RocmRuntime() {
+  if (ctx_) sai_destroy(ctx_);
+}
+
+Result<Unit, HipError> RocmRuntime::synchronize() const {
+  if (hipSetDevice(device_) != hipSuccess) return HipError::runtime("synchronize:set_device");
+  const hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return HipError::runtime("synchronize", (int32_t)e);
+  return Unit{};
+}
+
+std::string RocmRuntime::last_error() const { return ctx_ ? sai_last_error(ctx_) : ""; }
+
+// ----------------------------------------------------------- device memory ---
+Result<DeviceBuffer, HipError> DeviceBuffer::alloc(size_t bytes) {
+  DeviceBuffer b;
+  if (bytes == 0) return b;
+  const hipError_t e = hipMalloc(&b.ptr_, bytes);
+  if (e != hipSuccess) {
+    b.ptr_ = nullptr;
+    return HipError::alloc_failed(bytes, (int32_t)e);
+  }
+  b.bytes_ = bytes;
+  return b;
+}
+
+DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
+  if (this != &o) {
+    if (ptr_) (void)hipFree(ptr_);
+    ptr_ = std::exchange(o.ptr_, nullptr);
+    bytes_ = std::exchange(o.bytes_, 0);
+  }
+  return *this;
+}
+
+DeviceBuffer::~DeviceBuffer() {
+  if (ptr_) (void)hipFree(ptr_);
+}
+
+Result<Unit, HipError> DeviceBuffer::copy_from_host(const void* src, size_t bytes) {
+  if (bytes > bytes_) return HipError::copy_failed("host_to_device:size", -1);
+  if (bytes == 0) return Unit{};
+  const hipError_t e = hipMemcpy(ptr_, src, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return HipError::copy_failed("host_to_device", (int32_t)e);
+  return Unit{};
+}
+
+Result<Unit, HipError> DeviceBuffer::copy_to_host(void* dst, size_t bytes) const {
+  if (bytes > bytes_) return HipError::copy_failed("device_to_host:size", -1);
+  if (bytes == 0) return Unit{};
+  const hipError_t e = hipMemcpy(dst, ptr_, bytes, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return HipError::copy_failed("device_to_host", (int32_t)e);
+  return Unit{};
+}
+
+size_t DeviceTensor::total_elements() const {
+  size_t n = 1;
+  for (int64_t d : shape) {
+    if (d < 0) return 0;
+    if (d != 0 && n > std::numeric_limits<size_t>::max() / (size_t)d)
+      return std::numeric_limits<size_t>::max();
+    n *= (size_t)d;
+  }
+  return n;
+}
+
+size_t DeviceTensor::byte_size() const {
+  const size_t n = total_elements();
+  const size_t es = element_size(dtype);
+  if (es && n > std::numeric_limits<size_t>::max() / es) return std::numeric_limits<size_t>::max();
+  return n * es;
+}
+
+Result<DeviceTensor, HipError> DeviceTensor::alloc(std::vector<int64_t> shape, DataType dtype) {
+  DeviceTensor t;
+  t.shape = std::move(shape);
+  t.dtype = dtype;
+  auto b = DeviceBuffer::alloc(t.byte_size());
+  if (!b) return b.error();
+  t.buffer = std::move(b).value();
+  return t;
+}
+
+Result<DeviceTensor, HipError> DeviceTensor::from_host(const void* raw, size_t bytes,
+                                                       std::vector<int64_t> shape,
+                                                       DataType dtype, std::string name) {
+  auto t = alloc(std::move(shape), dtype);
+  if (!t) return t.error();
+  if (t.value().byte_size() != bytes) return HipError::copy_failed("host_to_device:size", -1);
+  auto c = t.value().buffer.copy_from_host(raw, bytes);
+  if (!c) return c.error();
+  t.value().name = std::move(name);
+  return t;
+}
+
+Result<DeviceTensor, HipError> DeviceTensor::from_f32(const std::vector<float>& v,
+                                                      std::vector<int64_t> shape) {
+  return from_host(v.data(), v.size() * sizeof(float), std::move(shape), DataType::Float);
+}
+
+Result<std::vector<uint8_t>, HipError> DeviceTensor::to_host() const {
+  std::vector<uint8_t> out(byte_size());
+  auto c = buffer.copy_to_host(out.data(), out.size());
+  if (!c) return c.error();
+  return out;
+}
+
+Result<std::vector<float>, HipError> DeviceTensor::to_host_f32() const {
+  if (dtype != DataType::Float) return HipError::runtime("to_host_f32:dtype");
+  std::vector<float> out(total_elements());
+  auto c = buffer.copy_to_host(out.data(), out.size() * sizeof(float));
+  if (!c) return c.error();
+  return out;
+}
+
+// ------------------------------------------------------------------ cache ---
+Result<GpuKvCache, HipError> GpuKvCache::allocate(RocmRuntime& rt, size_t num_layers,
+                                                  size_t num_kv_heads, size_t head_dim,
+                                                  size_t max_seq_len, KvQuant quant,
+                                                  const std::vector<LayerKind>& layer_kinds,
+                                                  size_t max_batch) {
+  if (layer_kinds.size() != num_layers) return HipError::runtime("kv_cache_allocate:layer_kinds_len");
+  if (num_layers == 0 || num_kv_heads == 0 || head_dim == 0 || max_seq_len == 0 || max_batch == 0)
+    return HipError::runtime("kv_cache_allocate:zero_dim");
+  for (const LayerKind& k : layer_kinds)
+    if (k.tag != LayerKind::Tag::Global) return HipError::runtime("kv_cache_allocate:sliding_window");
+  const size_t pps = (max_seq_len + SAI_PAGE_TOKENS - 1) / SAI_PAGE_TOKENS;
+  const size_t lim = (size_t)std::numeric_limits<int32_t>::max();
+  if (num_layers > lim || num_kv_heads > lim || head_dim > lim || pps > lim / max_batch)
+    return HipError::alloc_failed(std::numeric_limits<size_t>::max(), -1);
+  sai_kvcache_desc d{};
+  d.num_layers = (int32_t)num_layers;
+  d.num_kv_heads = (int32_t)num_kv_heads;
+  d.head_dim = (int32_t)head_dim;
+  d.num_pages = (int32_t)(pps * max_batch);
+  d.max_batch = (int32_t)max_batch;
+  d.max_pages_per_seq = (int32_t)pps;
+  d.quant = (int32_t)quant;
+  GpuKvCache c;
+  c.rt_ = &rt;
+  const sai_status st = sai_kvcache_create(rt.raw(), &d, &c.cache_);
+  if (st == SAI_ERR_UNSUPPORTED) return HipError::runtime("kv_cache_allocate:unsupported_head_dim", st);
+  if (st == SAI_ERR_ALLOC) {
+    const size_t per = quant == KvQuant::Int8 ? 32 * head_dim + 128 : 20 * head_dim;
+    return HipError::alloc_failed(num_layers * (size_t)d.num_pages * num_kv_heads * per, st);
+  }
+  if (st != SAI_OK) return HipError::runtime("kv_cache_allocate", st);
+  c.num_layers_ = num_layers;
+  c.num_kv_heads_ = num_kv_heads;
+  c.head_dim_ = head_dim;
+  c.max_seq_len_ = max_seq_len;
+  c.max_batch_ = max_batch;
+  c.pages_per_seq_ = pps;
+  c.quant_ = quant;
+  auto b = c.ensure_batch(max_batch, "kv_cache_allocate");
+  if (!b) return b.error();
+  return c;
+}
+
+GpuKvCache::GpuKvCache(GpuKvCache&& o) noexcept { *this = std::move(o); }
+
+GpuKvCache& GpuKvCache::operator=(GpuKvCache&& o) noexcept {
+  if (this != &o) {
+    if (cache_) sai_kvcache_destroy(cache_);
+    rt_ = o.rt_;
+    cache_ = std::exchange(o.cache_, nullptr);
+    num_layers_ = o.num_layers_;
+    num_kv_heads_ = o.num_kv_heads_;
+    head_dim_ = o.head_dim_;
+    max_seq_len_ = o.max_seq_len_;
+    max_batch_ = o.max_batch_;
+    pages_per_seq_ = o.pages_per_seq_;
+    batch_ = o.batch_;
+    position_ = o.position_;
+    quant_ = o.quant_;
+  }
+  return *this;
+}
+
+GpuKvCache::~GpuKvCache() {
+  if (cache_) {
+    // kernels of this cache may still be queued on the device
+    (void)hipDeviceSynchronize();
+    sai_kvcache_destroy(cache_);
+  }
+}
+
+size_t GpuKvCache::pending() const {
+  int32_t p = 0;
+  if (cache_) (void)sai_kvcache_lengths(cache_, nullptr, &p, nullptr);
+  return (size_t)p;
+}
+
+// Identity page table for `batch` sequences: sequence b owns pages
+// [b * pages_per_seq, (b + 1) * pages_per_seq). Only at position 0 with
+// nothing pending, since setting a table clears the lengths.
+Result<Unit, HipError> GpuKvCache::ensure_batch(size_t batch, const char* op) {
+  if (batch == batch_) return Unit{};
+  std::string where = std::string(op) + ":batch_mismatch";
+  if (batch == 0 || batch > max_batch_ || position_ != 0 || pending() != 0)
+    return HipError::runtime(where);
+  std::vector<int32_t> pt(batch * pages_per_seq_);
+  for (size_t i = 0; i < pt.size(); ++i) pt[i] = (int32_t)i;
+  const sai_status st = sai_kvcache_set_page_table(rt_->raw(), cache_, pt.data(), (int32_t)batch);
+  if (st != SAI_OK) return HipError::runtime(where, st);
+  batch_ = batch;
+  return Unit{};
+}
+
+Result<Unit, HipError> GpuKvCache::append(size_t layer_idx, const DeviceTensor& new_k,
+                                          const DeviceTensor& new_v, const RopeTables* rope,
+                                          void* stream) {
+  if (layer_idx >= num_layers_) return HipError::runtime("kv_cache_append:layer_idx");
+  if (!is_float_like(new_k.dtype) || new_v.dtype != new_k.dtype)
+    return HipError::runtime("kv_cache_append:dtype_mismatch");
+  const std::vector<int64_t>& s = new_k.shape;
+  size_t b = 0, sn = 0;
+  if (s.size() == 3 && s[0] > 0 && s[1] > 0 && (size_t)s[2] == num_kv_heads_ * head_dim_) {
+    b = (size_t)s[0];
+    sn = (size_t)s[1];
+  } else if (s.size() == 4 && s[0] > 0 && (size_t)s[1] == num_kv_heads_ && s[2] == 1 &&
+             (size_t)s[3] == head_dim_) {
+    b = (size_t)s[0];
+    sn = 1;
+  }
+  if (b == 0 || new_v.shape != new_k.shape ||
+      new_k.byte_size() != b * sn * num_kv_heads_ * head_dim_ * element_size(new_k.dtype))
+    return HipError::runtime("kv_cache_append:tensor_byte_size_mismatch");
+  auto ck = check_append(b, sn);
+  if (!ck) return ck;
+  const sai_status st = sai_kv_append(
+      rt_->raw(), cache_, (int32_t)layer_idx, new_k.buffer.as_ptr(), new_v.buffer.as_ptr(),
+      sai_dtype(new_k.dtype), (int32_t)b, (int32_t)sn, rope ? rope->cos : nullptr,
+      rope ? rope->sin : nullptr, rope ? rope->rows : 0, rope ? 1 : 0,
+      rope && rope->interleaved ? 1 : 0, stream);
+  if (st != SAI_OK) return HipError::runtime("kv_cache_append: " + rt_->last_error(), st);
+  return Unit{};
+}
+
+Result<Unit, HipError> GpuKvCache::check_append(size_t batch, size_t s_new) {
+  auto eb = ensure_batch(batch, "kv_cache_append");
+  if (!eb) return eb;
+  if (position_ + s_new > max_seq_len_) return HipError::runtime("kv_cache_append:position_overflow");
+  const size_t pend = pending();
+  if (pend != 0 && pend != s_new) return HipError::runtime("kv_cache_append:pending_mismatch");
+  return Unit{};
+}
+
+Result<Unit, HipError> GpuKvCache::advance_position(void* stream) {
+  const size_t pend = pending();
+  if (pend == 0) return HipError::runtime("kv_cache_advance:nothing_pending");
+  if (position_ + pend > max_seq_len_) return HipError::runtime("kv_cache_advance:position_overflow");
+  const sai_status st = sai_kvcache_advance(rt_->raw(), cache_, stream);
+  if (st != SAI_OK) return HipError::runtime("kv_cache_advance", st);
+  position_ += pend;
+  return Unit{};
+}
+
+Result<KvView, HipError> GpuKvCache::view_at(size_t layer_idx, size_t count, const char* op) const {
+  if (layer_idx >= num_layers_) return HipError::runtime(op);
+  KvView v;
+  void* pool = nullptr;
+  const sai_status st =
+      sai_kvcache_pool(cache_, (int32_t)layer_idx, &pool, &v.pool_bytes, &v.block_bytes);
+  if (st != SAI_OK) return HipError::runtime(op, st);
+  v.pool = pool;
+  v.token_count = count;
+  v.num_kv_heads = num_kv_heads_;
+  v.head_dim = head_dim_;
+  v.batch = batch_;
+  v.quant = quant_;
+  return v;
+}
+
+Result<KvView, HipError> GpuKvCache::view(size_t layer_idx) const {
+  return view_at(layer_idx, position_, "kv_cache_view:layer_idx");
+}
+
+Result<KvView, HipError> GpuKvCache::view_pending(size_t layer_idx) const {
+  return view_at(layer_idx, position_ + pending(), "kv_cache_view_pending:layer_idx");
+}
+
+void GpuKvCache::reset() {
+  if (cache_) (void)sai_kvcache_reset(rt_->raw(), cache_);
+  position_ = 0;
+}
+
+Result<std::pair<std::vector<float>, std::vector<float>>, HipError> GpuKvCache::read_dequantized(
+    size_t layer_idx, size_t seq, size_t kv_head, size_t t0, size_t n) const {
+  if (layer_idx >= num_layers_ || seq >= batch_ || kv_head >= num_kv_heads_)
+    return HipError::runtime("kv_cache_read:index");
+  if (t0 + n > position_ + pending()) return HipError::runtime("kv_cache_read:range");
+  const size_t D = head_dim_;
+  std::vector<float> k(n * D), v(n * D);
+  if (n == 0) return std::make_pair(std::move(k), std::move(v));
+  sai_status st;
+  if (quant_ == KvQuant::Int8) {
+    std::vector<int8_t> kc(n * D), vc(n * D);
+    std::vector<float> ks(n), vs(n);
+    st = sai_kvcache_read(rt_->raw(), cache_, (int32_t)layer_idx, (int32_t)seq, (int32_t)kv_head,
+                          (int32_t)t0, (int32_t)n, kc.data(), vc.data(), ks.data(), vs.data());
+    if (st != SAI_OK) return HipError::runtime("kv_cache_read", st);
+    for (size_t t = 0; t < n; ++t)
+      for (size_t d = 0; d < D; ++d) {
+        k[t * D + d] = (float)kc[t * D + d] * ks[t];
+        v[t * D + d] = (float)vc[t * D + d] * vs[t];
+      }
+  } else {
+    const size_t G = D / 32;
+    std::vector<uint8_t> kc(n * D / 2), vc(n * D / 2);
+    std::vector<uint16_t> kp(n * G * 2), vp(n * G * 2);
+    st = sai_kvcache_read(rt_->raw(), cache_, (int32_t)layer_idx, (int32_t)seq, (int32_t)kv_head,
+                          (int32_t)t0, (int32_t)n, kc.data(), vc.data(), kp.data(), vp.data());
+    if (st != SAI_OK) return HipError::runtime("kv_cache_read", st);
+    for (size_t t = 0; t < n; ++t)
+      for (size_t d = 0; d < D; ++d) {
+        const size_t g = d / 32;
+        const uint8_t kb = kc[t * D / 2 + d / 2], vb = vc[t * D / 2 + d / 2];
+        const float kq = (float)((d & 1) ? kb >> 4 : kb & 0xF);
+        const float vq = (float)((d & 1) ? vb >> 4 : vb & 0xF);
+        // code * scale + zero, each rounded on its own
+        const float ka = kq * half_to_float(kp[(t * G + g) * 2]);
+        const float va = vq * half_to_float(vp[(t * G + g) * 2]);
+        k[t * D + d] = ka + half_to_float(kp[(t * G + g) * 2 + 1]);
+        v[t * D + d] = va + half_to_float(vp[(t * G + g) * 2 + 1]);
+      }
+  }
+  return std::make_pair(std::move(k), std::move(v));
+}
+
+// ------------------------------------------------------------- operator ---
+AttributeProto AttributeProto::make_int(std::string n, int64_t v) {
+  AttributeProto a;
+  a.name = std::move(n);
+  a.attr_type = AttributeType::Int;
+  a.i = v;
+  return a;
+}
+
+AttributeProto AttributeProto::make_float(std::string n, float v) {
+  AttributeProto a;
+  a.name = std::move(n);
+  a.attr_type = AttributeType::Float;
+  a.f = v;
+  return a;
+}
+
+GqaAttrs parse_gqa_attrs(const std::vector<AttributeProto>& attrs) {
+  GqaAttrs a;
+  // first attribute of a name and type wins (executor.rs:350-365)
+  bool seen_nh = false, seen_kv = false, seen_lw = false, seen_rot = false, seen_il = false;
+  for (const AttributeProto& p : attrs) {
+    if (p.attr_type == AttributeType::Int) {
+      if (p.name == "num_heads" && !seen_nh) {
+        a.num_heads = p.i;
+        seen_nh = true;
+      } else if (p.name == "kv_num_heads" && !seen_kv) {
+        a.kv_num_heads = p.i;
+        seen_kv = true;
+      } else if (p.name == "local_window_size" && !seen_lw) {
+        a.local_window_size = p.i;
+        seen_lw = true;
+      } else if (p.name == "do_rotary" && !seen_rot) {
+        a.do_rotary = p.i != 0;
+        a.do_rotary_set = true;
+        seen_rot = true;
+      } else if (p.name == "rotary_interleaved" && !seen_il) {
+        a.rotary_interleaved = p.i != 0;
+        seen_il = true;
+      }
+    } else if (p.attr_type == AttributeType::Float && p.name == "scale" && !a.scale) {
+      a.scale = p.f;
+    }
+  }
+  return a;
+}
+
+Result<GqaShape, OpError> gqa_validate(const std::vector<int64_t>& q, const std::vector<int64_t>& k,
+                                       const std::vector<int64_t>& v, int64_t num_heads,
+                                       int64_t kv_num_heads) {
+  GqaShape g;
+  if (q.size() == 4 && k.size() == 4 && v.size() == 4) {
+    // [B, H, S, D]: heads from the shapes (gpu_gqa's rank-4 contract)
+    if (q[1] <= 0 || k[1] <= 0)
+      return OpError::attribute("GroupQueryAttention: num_heads and kv_num_heads must be > 0");
+    if (q[1] % k[1] != 0)
+      return OpError::attribute("GroupQueryAttention: num_heads must be a multiple of kv_num_heads");
+    if (q[0] < 0 || q[2] < 0 || q[3] <= 0)
+      return OpError::shape("GroupQueryAttention: Q/K/V must be rank-3");
+    if (k[3] != q[3]) return OpError::shape("GroupQueryAttention: Q and KV head_dim must match");
+    if (v != k) return OpError::shape("GroupQueryAttention: key and value must have the same shape");
+    if (q[2] != 1 || k[2] != 1 || k[0] != q[0])
+      return OpError::shape("GroupQueryAttention: rank-4 [B, H, S, D] inputs need S = 1 (decode)");
+    g.num_heads = (size_t)q[1];
+    g.kv_heads = (size_t)k[1];
+    g.batch = (size_t)q[0];
+    g.seq = 1;
+    g.head_dim = (size_t)q[3];
+    g.q_hidden = g.num_heads * g.head_dim;
+    return g;
+  }
+  if (num_heads <= 0 || kv_num_heads <= 0)
+    return OpError::attribute("GroupQueryAttention: num_heads and kv_num_heads must be > 0");
+  if (num_heads % kv_num_heads != 0)
+    return OpError::attribute("GroupQueryAttention: num_heads must be a multiple of kv_num_heads");
+  if (q.size() != 3 || k.size() != 3 || v.size() != 3)
+    return OpError::shape("GroupQueryAttention: Q/K/V must be rank-3");
+  if (q[0] < 0 || q[1] < 0 || q[2] < 0 || k[2] < 0)
+    return OpError::shape("GroupQueryAttention: Q/K/V must be rank-3");
+  const size_t nh = (size_t)num_heads, kvh = (size_t)kv_num_heads;
+  const size_t q_hidden = (size_t)q[2], kv_hidden = (size_t)k[2];
+  if (q_hidden % nh != 0)
+    return OpError::shape("GroupQueryAttention: q_hidden not divisible by num_heads");
+  if (kv_hidden % kvh != 0)
+    return OpError::shape("GroupQueryAttention: kv_hidden not divisible by kv_num_heads");
+  const size_t head_dim = q_hidden / nh;
+  if (kv_hidden / kvh != head_dim)
+    return OpError::shape("GroupQueryAttention: Q and KV head_dim must match");
+  if (v != k) return OpError::shape("GroupQueryAttention: key and value must have the same shape");
+  // the op reads K/V with Q's batch and sequence (reshape_to_bhsd(key, b, sq, ...))
+  if (k[0] != q[0] || k[1] != q[1])
+    return OpError::shape("GroupQueryAttention: key batch/sequence must match query");
+  g.num_heads = nh;
+  g.kv_heads = kvh;
+  g.batch = (size_t)q[0];
+  g.seq = (size_t)q[1];
+  g.q_hidden = q_hidden;
+  g.head_dim = head_dim;
+  return g;
+}
+
+namespace {
+
+const DeviceTensor* slot(const std::vector<const DeviceTensor*>& in, size_t i) {
+  return i < in.size() ? in[i] : nullptr;
+}
+
+// validate_rope_caches (ops/microsoft.rs:71-110) with rotary_dim = head_dim.
+Result<int32_t, OpError> check_rope_tables(const DeviceTensor& cos, const DeviceTensor& sin,
+                                           size_t head_dim) {
+  if (cos.dtype != DataType::Float || sin.dtype != DataType::Float)
+    return OpError::shape("RotaryEmbedding requires Float input");
+  if (head_dim % 2 != 0)
+    return OpError::attribute("apply_rope_in_place: rotary_dim must be even");
+  if (cos.shape.size() != 2 || sin.shape.size() != 2)
+    return OpError::shape("apply_rope_in_place: cos/sin caches must be rank-2");
+  if (sin.shape[1] != cos.shape[1])
+    return OpError::shape("apply_rope_in_place: cos and sin caches must share the inner dim");
+  if (cos.shape[1] != (int64_t)(head_dim / 2)) {
+    char buf[128];
+    std::snprintf(buf, sizeof buf, "apply_rope_in_place: cache inner dim %lld != rotary_dim/2 = %zu",
+                  (long long)cos.shape[1], head_dim / 2);
+    return OpError::shape(buf);
+  }
+  // both tables are read at the same rows
+  const int64_t rows = std::min(cos.shape[0], sin.shape[0]);
+  if (rows < 0 || rows > std::numeric_limits<int32_t>::max())
+    return OpError::shape("apply_rope_in_place: cos/sin caches must be rank-2");
+  return (int32_t)rows;
+}
+
+OpError from_status(sai_status st, const std::string& prefix, const RocmRuntime& rt) {
+  return OpError{kind_of(st), prefix + rt.last_error()};
+}
+
+// One GQA node over `cache` (layer `layer`): fused append + decode for S = 1,
+// append + prefill chunk for S > 1.
+Result<DeviceTensor, OpError> gqa_over_cache(RocmRuntime& rt, GpuKvCache& cache, size_t layer,
+                                             const DeviceTensor& q, const DeviceTensor& k,
+                                             const DeviceTensor& v, const GqaShape& g,
+                                             const GqaAttrs& a, const RopeTables* rope,
+                                             const std::string& prefix) {
+  if (g.kv_heads != cache.num_kv_heads() || g.head_dim != cache.head_dim())
+    return OpError::shape(prefix + "K/V heads or head_dim differ from the cache's");
+  auto out = DeviceTensor::alloc({(int64_t)g.batch, (int64_t)g.seq, (int64_t)g.q_hidden},
+                                 DataType::Float);
+  if (!out) return OpError::internal(prefix + out.error().to_string());
+  if (g.batch == 0 || g.seq == 0) return std::move(out).value();
+  const float* cs = rope ? rope->cos : nullptr;
+  const float* sn = rope ? rope->sin : nullptr;
+  const int32_t rows = rope ? rope->rows : 0;
+  const int32_t rot = rope ? 1 : 0;
+  const int32_t il = a.rotary_interleaved ? 1 : 0;
+  const int32_t has_scale = a.scale ? 1 : 0;
+  const float scale = a.scale ? *a.scale : 0.0f;
+  float* o = (float*)out.value().buffer.as_ptr();
+  if (g.seq == 1) {
+    auto ck = cache.check_append(g.batch, 1);
+    if (!ck) return OpError::internal(prefix + ck.error().to_string());
+    const sai_status st = sai_gqa_with_cache(
+        rt.raw(), cache.raw(), (int32_t)layer, q.buffer.as_ptr(), sai_dtype(q.dtype),
+        k.buffer.as_ptr(), v.buffer.as_ptr(), sai_dtype(k.dtype), (int32_t)g.batch,
+        (int32_t)g.num_heads, cs, sn, rows, rot, il, has_scale, scale, o, nullptr);
+    if (st != SAI_OK) return from_status(st, prefix, rt);
+    return std::move(out).value();
+  }
+  auto ap = cache.append(layer, k, v, rope, nullptr);
+  if (!ap) return OpError::internal(prefix + ap.error().to_string());
+  const sai_status st = sai_gqa_prefill(rt.raw(), cache.raw(), (int32_t)layer, q.buffer.as_ptr(),
+                                        sai_dtype(q.dtype), (int32_t)g.batch, (int32_t)g.seq,
+                                        (int32_t)g.num_heads, cs, sn, rows, rot, il, has_scale,
+                                        scale, o, nullptr);
+  if (st != SAI_OK) return from_status(st, prefix, rt);
+  return std::move(out).value();
+}
+
+}  // namespace
+
+Result<std::vector<DeviceTensor>, OpError> dispatch_gqa(
+    RocmRuntime& runtime, const std::vector<const DeviceTensor*>& inputs,
+    const std::vector<AttributeProto>& attrs, KvCacheDispatchCtx* kv_cache_ctx) {
+  static const char* const roles[3] = {"Q", "K", "V"};
+  for (size_t i = 0; i < 3; ++i)
+    if (!slot(inputs, i))
+      return OpError::internal(std::string("GPU GroupQueryAttention: missing input '") + roles[i] + "'");
+  const DeviceTensor& q = *inputs[0];
+  const DeviceTensor& k = *inputs[1];
+  const DeviceTensor& v = *inputs[2];
+  const GqaAttrs a = parse_gqa_attrs(attrs);
+  if (a.local_window_size != -1)
+    return OpError::attribute("GroupQueryAttention: local_window_size != -1 not supported in this tier");
+  auto gs = gqa_validate(q.shape, k.shape, v.shape, a.num_heads, a.kv_num_heads);
+  if (!gs) return gs.error();
+  const GqaShape g = gs.value();
+  if (!is_float_like(q.dtype) || !is_float_like(k.dtype) || v.dtype != k.dtype)
+    return OpError::shape("GroupQueryAttention requires Float or BFloat16 input");
+  if (q.byte_size() != g.batch * g.seq * g.q_hidden * element_size(q.dtype) ||
+      k.byte_size() != g.batch * g.seq * g.kv_heads * g.head_dim * element_size(k.dtype) ||
+      !(q.buffer.as_ptr() || q.byte_size() == 0) || !(k.buffer.as_ptr() || k.byte_size() == 0) ||
+      !(v.buffer.as_ptr() || v.byte_size() == 0))
+    return OpError::shape("GroupQueryAttention: input buffer does not hold its shape");
+
+  // RoPE tables (inputs 7 and 8, gqa_apply_rotary, ops/microsoft.rs:1004-1020)
+  const DeviceTensor* cos = slot(inputs, 7);
+  const DeviceTensor* sin = slot(inputs, 8);
+  RopeTables rope;
+  const RopeTables* rope_ptr = nullptr;
+  if (a.do_rotary && (a.do_rotary_set || cos || sin)) {
+    if (!cos) return OpError::shape("GroupQueryAttention: do_rotary=1 but cos_cache is missing");
+    if (!sin) return OpError::shape("GroupQueryAttention: do_rotary=1 but sin_cache is missing");
+    auto rows = check_rope_tables(*cos, *sin, g.head_dim);
+    if (!rows) return rows.error();
+    rope.cos = (const float*)cos->buffer.as_ptr();
+    rope.sin = (const float*)sin->buffer.as_ptr();
+    rope.rows = rows.value();
+    rope.interleaved = a.rotary_interleaved;
+    rope_ptr = &rope;
+  }
+
+  if (kv_cache_ctx && kv_cache_ctx->cache) {
+    const size_t layer = kv_cache_ctx->next_layer_idx++;
+    auto r = gqa_over_cache(runtime, *kv_cache_ctx->cache, layer, q, k, v, g, a, rope_ptr,
+                            "ROCm GroupQueryAttention (cache): ");
+    if (!r) return r.error();
+    std::vector<DeviceTensor> outs;
+    outs.push_back(std::move(r).value());
+    return outs;
+  }
+
+  // No cache: attention over the node's own K/V (gqa_cacheless,
+  // gpu_executor.rs:933-942), through a transient one-layer cache.
+  const std::string prefix = "ROCm GroupQueryAttention: ";
+  if (g.batch == 0 || g.seq == 0) {
+    auto out = DeviceTensor::alloc({(int64_t)g.batch, (int64_t)g.seq, (int64_t)g.q_hidden},
+                                   DataType::Float);
+    if (!out) return OpError::internal(prefix + out.error().to_string());
+    std::vector<DeviceTensor> outs;
+    outs.push_back(std::move(out).value());
+    return outs;
+  }
+  auto cache = GpuKvCache::allocate(runtime, 1, g.kv_heads, g.head_dim, g.seq, KvQuant::Int8,
+                                    {LayerKind::global()}, g.batch);
+  if (!cache) {
+    const HipError& e = cache.error();
+    if (e.op == "kv_cache_allocate:unsupported_head_dim")
+      return OpError::unsupported(prefix + e.to_string());
+    return OpError::internal(prefix + e.to_string());
+  }
+  auto r = gqa_over_cache(runtime, cache.value(), 0, q, k, v, g, a, rope_ptr, prefix);
+  if (!r) return r.error();
+  // the transient cache is freed on return, after the device has drained
+  std::vector<DeviceTensor> outs;
+  outs.push_back(std::move(r).value());
+  return outs;
+}
+
+}  // namespace sai::rocm

@@ -1,0 +1,39 @@
+"""The C++ host mirror of the reference's GPU dispatch API
+(smallaios_amd/host/gqa_host.hpp), exercised through its test binary
+tests/cpp/test_gqa_host (built by __graft_entry__.build()).
+
+The CPU case covers attribute parsing, gqa_validate's messages
+(onnx-rt/src/ops/microsoft.rs:933-984) and the error types. The GPU case runs,
+in one child process, the restated reference cache tests
+(onnx-rt/tests/test_cuda.rs:1124-1375), the first-token GQA tests
+(test_cuda.rs:3426-3525), dispatch_gqa's error contract, and four multi-layer
+prefill/decode sessions checked against the oracle (outputs within
+2e-3 abs + 1e-2 rel, cache contents bit-exact).
+"""
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "tests", "cpp", "test_gqa_host")
+
+
+def _run(args, timeout):
+    if not os.path.exists(BIN):
+        pytest.fail("tests/cpp/test_gqa_host is not built: run __graft_entry__.build() first")
+    print(f"[host-mirror] {' '.join(args)}", flush=True)
+    r = subprocess.run([BIN, *args], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                       timeout=timeout)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0, r.stdout
+    assert "FAIL" not in r.stdout
+
+
+def test_host_mirror_cpu():
+    _run(["--cpu"], 60)
+
+
+@pytest.mark.gpu
+def test_host_mirror_gpu():
+    _run(["--gpu"], 110)
