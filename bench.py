@@ -193,7 +193,23 @@ def cpu_baseline(w, seconds_target=12.0):
                    f"{step_s * 1e3:.0f} ms per step, {w['batch'] / step_s:.2f} tokens/s"),
         "ms_per_step": round(step_s * 1e3, 2),
         "tokens_per_s": round(w["batch"] / step_s, 3),
+        "threads": 1,
+        "host_nproc": os.cpu_count(),
+        "host_cpus_usable": len(os.sched_getaffinity(0)),
+        "host_cpu": host_cpu_model(),
     }
+
+
+def host_cpu_model():
+    """The CPU model string of /proc/cpuinfo (None where there is none)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def time_steps(torch, run, steps):
