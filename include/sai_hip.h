@@ -197,8 +197,11 @@ int32_t sai_set_decode_split(sai_ctx* ctx, int32_t tokens);
 /* Waves per decode workgroup: 4 or 8, or 0 = automatic (4 for an int8
  * cache, 8 for int4). Returns the previous value. */
 int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves);
-/* Split merge of the decode kernel: 0 = separate combine kernel, 1 = the last
- * workgroup of a sequence merges in-kernel. Returns the previous value. */
+/* Split merge of the decode kernel: 0 = separate combine kernel (default),
+ * 1 = the last workgroup of a (sequence, kv head) merges in-kernel (int8; every
+ * wave then releases its partials with an agent-scope fence, which writes back
+ * its XCD's L2, so this is slower at the Llama layer shape). Returns the
+ * previous value. */
 int32_t sai_set_decode_merge(sai_ctx* ctx, int32_t in_kernel);
 /* Number of workgroups and split size of the last decode launch on ctx. */
 sai_status sai_last_decode_shape(const sai_ctx* ctx, int32_t* workgroups, int32_t* split_tokens);

@@ -16,6 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsai_hip.so")
 HOST_LIB = os.path.join(HERE, "libsai_gqa_host.so")
+PROBE_LIB = os.path.join(HERE, "libsai_read_probe.so")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 CXX = os.environ.get("CXX", "g++")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -65,7 +66,16 @@ def build(verbose: bool = False) -> str:
     _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", tmp, *objs])
     os.replace(tmp, LIB)
     build_host()
+    build_probe()
     return LIB
+
+
+def build_probe() -> str:
+    """libsai_read_probe.so: the streaming-read ceiling the bench reports."""
+    tmp = PROBE_LIB + ".tmp"
+    _run([HIPCC, *COMMON, "-shared", os.path.join(CSRC, "read_probe.hip"), "-o", tmp])
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 def build_host() -> str:

@@ -397,7 +397,13 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   __syncthreads();
 
   float* part = p.partials + ((size_t)(split_base + split) * p.kv_heads + kvh) * (G * (D + 2));
-  for (int t = threadIdx.x; t < G * D; t += 64 * NW) {
+  // (m, l, o) of this split for the (head, dim) entries t = threadIdx.x + k*64*NW
+  constexpr int PER = (G * D + 64 * NW - 1) / (64 * NW);
+  float mM[PER], mL[PER], mO[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int t = threadIdx.x + k * 64 * NW;
+    if (G * D % (64 * NW) != 0 && t >= G * D) break;
     const int hd = t / D, d = t % D;
     float M = -INFINITY;
 #pragma unroll
@@ -410,6 +416,9 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
       Ls += sm_l[w][hd] * f;
       O += sm_o[w][hd][d] * f;
     }
+    mM[k] = M;
+    mL[k] = Ls;
+    mO[k] = O;
     if (nsplit == 1) {
       p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
     } else {
@@ -432,12 +441,14 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   if (nsplit == 1) return;
 
   // ---- in-kernel merge: the last workgroup of (b, kvh) to finish merges -------
-  // One agent-scope release (thread 0, after the barrier has made every
-  // wave's partial stores complete) and one acquire; the counter resets itself.
+  // Every thread releases its own partial stores at agent scope (the splits
+  // run on different XCDs, whose L2s are not coherent with each other), the
+  // barrier orders those releases before thread 0's counter increment, and
+  // the last workgroup acquires before reading. The counter resets itself.
   __shared__ int sm_last;
+  __threadfence();
   __syncthreads();
   if (threadIdx.x == 0) {
-    __threadfence();
     const int prev = atomicAdd(&p.counters[b * p.kv_heads + kvh], 1);
     sm_last = (prev == nsplit - 1);
     if (sm_last) __threadfence();
@@ -446,17 +457,33 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   if (!sm_last) return;
   const size_t stride = (size_t)p.kv_heads * (G * (D + 2));
   const float* p0 = p.partials + ((size_t)split_base * p.kv_heads + kvh) * (G * (D + 2));
-  for (int t = threadIdx.x; t < G * D; t += 64 * NW) {
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int t = threadIdx.x + k * 64 * NW;
+    if (G * D % (64 * NW) != 0 && t >= G * D) break;
     const int hd = t / D, d = t % D;
-    float M = -INFINITY;
-    for (int sidx = 0; sidx < nsplit; ++sidx) M = fmaxf(M, p0[sidx * stride + hd * (D + 2)]);
-    float Ls = 0.0f, O = 0.0f;
-    for (int sidx = 0; sidx < nsplit; ++sidx) {
-      const float* ps = p0 + sidx * stride + hd * (D + 2);
-      if (ps[0] == -INFINITY) continue;
-      const float f = fast_exp2(ps[0] - M);
-      Ls += ps[1] * f;
-      O += ps[2 + d] * f;
+    float M = mM[k], Ls = mL[k], O = mO[k];
+    // the other splits' (m, l, o), up to 16 loads in flight per round
+    for (int s0 = 0; s0 < nsplit; s0 += 16) {
+      float pm[16], pl[16], po[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float* ps = p0 + (size_t)min(s0 + j, nsplit - 1) * stride + hd * (D + 2);
+        pm[j] = ps[0];
+        pl[j] = ps[1];
+        po[j] = ps[2 + d];
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int sidx = s0 + j;
+        if (sidx >= nsplit || sidx == split || pm[j] == -INFINITY) continue;
+        const float Mn = fmaxf(M, pm[j]);
+        const float fa = fast_exp2(M - Mn);
+        const float fb = fast_exp2(pm[j] - Mn);
+        Ls = Ls * fa + pl[j] * fb;
+        O = O * fa + po[j] * fb;
+        M = Mn;
+      }
     }
     p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
   }
@@ -526,12 +553,11 @@ hipError_t launch_combine_dg(const DecodeParams& p, hipStream_t st) {
 
 template <int D, int G>
 hipError_t launch_dg(const DecodeParams& p, int work_items, bool combine, hipStream_t st) {
+  const dim3 grid(work_items, p.kv_heads);
   if (p.waves == 8)
-    hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, 8>), dim3(work_items, p.kv_heads), dim3(512),
-                       0, st, p);
+    hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, 8>), grid, dim3(512), 0, st, p);
   else
-    hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, 4>), dim3(work_items, p.kv_heads), dim3(256),
-                       0, st, p);
+    hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, 4>), grid, dim3(256), 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !combine || p.merge_in_kernel) return e;
   return launch_combine_dg<D, G>(p, st);
