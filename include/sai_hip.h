@@ -179,10 +179,11 @@ sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, c
                               int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
                               float scale, float* out, void* stream);
 
-/* ---- kernel 3: prefill chunk (bf16/f16 MFMA) ---------------------------------
+/* ---- kernel 3: prefill chunk (f16 MFMA) ---------------------------------------
  * Same contract as sai_gqa_decode for a chunk of sq == pending query tokens per
  * sequence (the reference's op_group_query_attention with Sq > 1, causal with
- * past_sk = seq_len[b], microsoft.rs:1156 and :331-337).
+ * past_sk = seq_len[b], microsoft.rs:1156 and :331-337), over an int8 or int4
+ * cache (head_dim 64 or 128).
  * q: device [batch, sq, num_heads*D]; out: device [batch, sq, num_heads*D] f32. */
 sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
                            int32_t dtype, int32_t batch, int32_t sq, int32_t num_heads,

@@ -1,27 +1,30 @@
 // Kernel 3: prefill chunk -- causal GQA attention of sq new query tokens per
-// sequence over the paged int8 cache (past + the chunk, already appended by
-// kernel 1), on f16 matrix cores (v_mfma_f32_16x16x32_f16).
+// sequence over the paged int8 or int4 cache (past + the chunk, already
+// appended by kernel 1), on f16 matrix cores (v_mfma_f32_16x16x32_f16).
 //
-// Workgroup = 4 waves = 128 attention rows = (128/G query positions) x (G
+// Workgroup = 8 waves = 256 attention rows = (256/G query positions) x (G
 // heads of one kv head), so every K/V tile is loaded once per workgroup and
 // shared by the whole GQA group; each wave owns two 16-row blocks.
 // Per 64-token KV tile (4 pages):
-//   staging  the next tile's int8 codes and scales are loaded into registers
-//            while the current tile is computed, then converted to f16
-//            (exact: |code| <= 128) into the other half of a double-buffered
-//            LDS tile: K token-major, V in the permuted k-order of the PV
-//            operand; rows padded so the 16-byte LDS reads are conflict-free.
-//            One barrier per tile.
+//   staging  the next tile's codes and scales are loaded into registers while
+//            the current tile is computed, then written as f16 into the other
+//            half of a double-buffered LDS tile: K token-major, V in the
+//            permuted k-order of the PV operand; rows padded so the 16-byte
+//            LDS reads are conflict-free. One barrier per tile. int8 codes are
+//            stored exactly (|code| <= 128) and their per-token scales applied
+//            to the scores and to P; int4 codes are dequantised while staged.
 //   S^T      A = K tile (LDS), B = Q^T (registers, f16 of q * scale * log2 e);
 //            lane (row r, g) receives tokens 4g+e of each 16-token block, so
 //            the row softmax is in-lane plus two cross-group reductions and P
 //            feeds the PV A operand straight from registers. Each K fragment
 //            read from LDS serves both row blocks of the wave.
-//   PV       A = P * s_v (f16), B = V codes (LDS f16); each V fragment serves
-//            both row blocks.
-// Scores: s = <q', k_code> * s_k[t], online softmax in the log2 domain. Only
-// tiles that cross the causal diagonal (or the end of the sequence) apply the
-// mask; the accumulator rescale is skipped when no row maximum moved.
+//   PV       A = P * s_v (f16), B = V (LDS f16); each V fragment serves both
+//            row blocks.
+// Scores: s = <q', k> * s_k[t], online softmax in the log2 domain. Only tiles
+// that cross the causal diagonal (or the end of the sequence) apply the mask;
+// the accumulator rescale is skipped when no row maximum moved.
+#include <type_traits>
+
 #include "sai_internal.h"
 
 namespace sai {
@@ -69,14 +72,16 @@ __device__ __forceinline__ float xgroup_sum(float v) {
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <int D>
+template <int D, bool KLO = false>
 struct PrefillTile {
   static constexpr int KROW = D + 8;      // padded f16 row of the K tile
   static constexpr int VROW = 4 * 8 + 8;  // padded f16 (kstep, dim) row: 4 groups x 8
-  _Float16 k[64 * KROW];
-  _Float16 v[2 * D * VROW];
-  float sk[64];
-  float sv[64];
+  // every member 16-byte aligned: fragments are read with ds_read_b128
+  alignas(16) _Float16 k[64 * KROW];
+  alignas(16) _Float16 klo[KLO ? 64 * KROW : 8];  // int4: K - f16(K), hi + lo hold K to ~22 bits
+  alignas(16) _Float16 v[2 * D * VROW];
+  alignas(16) float sk[64];
+  alignas(16) float sv[64];
 };
 
 // Codes and scales of one 64-token tile, held in registers between the load
@@ -129,11 +134,10 @@ __device__ __forceinline__ void stage_load(TileStage<D, NT>& S, const PrefillPar
   }
 }
 
-template <int D, int NT>
-__device__ __forceinline__ void stage_store(const TileStage<D, NT>& S, PrefillTile<D>& T,
-                                            int tid) {
-  constexpr int KROW = PrefillTile<D>::KROW;
-  constexpr int VROW = PrefillTile<D>::VROW;
+template <int D, int NT, class Tile>
+__device__ __forceinline__ void stage_store(const TileStage<D, NT>& S, Tile& T, int tid) {
+  constexpr int KROW = Tile::KROW;
+  constexpr int VROW = Tile::VROW;
 #pragma unroll
   for (int i = 0; i < TileStage<D, NT>::KC; ++i) {
     const int c = tid + NT * i;
@@ -175,17 +179,141 @@ __device__ __forceinline__ void stage_store(const TileStage<D, NT>& S, PrefillTi
   }
 }
 
-template <int D, int G, int NW>
-__global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_int8_kernel(PrefillParams p) {
+// ---- int4 cache: the same LDS tile, filled with dequantised f16 values -------
+// A group's scale and zero vary along head_dim, so they cannot be applied after
+// the dot product: K and V are dequantised while staged (code * s + z in f32,
+// rounded once to f16; the binary16 parameters bound the range anyway), and
+// the softmax then uses unit token scales. Tokens past the sequence end are
+// zeroed so a stale slot can never inject a NaN into the PV product.
+template <int D, int NT>
+struct TileStage4 {
+  static constexpr int NG = D / 32;
+  static constexpr int KN = 64 * NG;             // K chunks: (token, group), 16 B
+  static constexpr int VN = 4 * D;               // V chunks: (page, dim), 8 B
+  static constexpr int KC = (KN + NT - 1) / NT;  // per thread
+  static constexpr int VC = (VN + NT - 1) / NT;
+  uint4 kc[KC];
+  uint32_t kp[KC];      // (scale, zero) binary16 pair of the K chunk's group
+  uint2 vc[VC];
+  uint32_t vp[VC][16];  // (scale, zero) of each of the V chunk's 16 slots
+};
+
+__device__ __forceinline__ float half_lo(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+}
+__device__ __forceinline__ float half_hi(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+template <int D, int NT>
+__device__ __forceinline__ void stage_load4(TileStage4<D, NT>& S, const PrefillParams& p,
+                                            const int32_t* pt, int kvh, int t0, int last_page,
+                                            int tid) {
+  constexpr size_t BB = block_bytes_int4(D);
+  constexpr int NG = D / 32;
+#pragma unroll
+  for (int i = 0; i < TileStage4<D, NT>::KC; ++i) {
+    const int c = min(tid + NT * i, TileStage4<D, NT>::KN - 1);  // spare threads repeat the last
+    const int tok = c / NG;
+    const int grp = c % NG;
+    const int pg = min((t0 + tok) / kPageTokens, last_page);
+    const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
+    const int slot = (t0 + tok) % kPageTokens;
+    S.kc[i] = *(const uint4*)(blk + (size_t)slot * (D / 2) + 16 * grp);
+    S.kp[i] = *(const uint32_t*)(blk + 16 * D + (size_t)(slot * NG + grp) * 4);
+  }
+#pragma unroll
+  for (int i = 0; i < TileStage4<D, NT>::VC; ++i) {
+    const int c = min(tid + NT * i, TileStage4<D, NT>::VN - 1);
+    const int cb = c / D;
+    const int d = c % D;
+    const int pg = min(t0 / kPageTokens + cb, last_page);
+    const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
+    S.vc[i] = *(const uint2*)(blk + 8 * D + (size_t)d * 8);
+    const uint8_t* par = blk + 16 * D + 64 * NG + (size_t)(d / 32) * 4;
+#pragma unroll
+    for (int sl = 0; sl < 16; ++sl) S.vp[i][sl] = *(const uint32_t*)(par + (size_t)sl * NG * 4);
+  }
+}
+
+template <int D, int NT>
+__device__ __forceinline__ void stage_store4(const TileStage4<D, NT>& S, PrefillTile<D, true>& T,
+                                             int t0, int total, int tid) {
+  constexpr int KROW = PrefillTile<D, true>::KROW;
+  constexpr int VROW = PrefillTile<D, true>::VROW;
+  constexpr int NG = D / 32;
+#pragma unroll
+  for (int i = 0; i < TileStage4<D, NT>::KC; ++i) {
+    const int c = tid + NT * i;
+    if (c >= TileStage4<D, NT>::KN) break;
+    const int tok = c / NG;
+    const int grp = c % NG;
+    const bool valid = t0 + tok < total;
+    const float sc = half_lo(S.kp[i]), zr = half_hi(S.kp[i]);
+    const uint32_t w[4] = {S.kc[i].x, S.kc[i].y, S.kc[i].z, S.kc[i].w};
+    uint32_t h[16], l[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      // elements 2j, 2j+1: nibbles 2j, 2j+1 of the chunk (LSB first); the
+      // value code * s + z (code * s exact in f32) as an f16 pair hi + lo
+      const uint32_t wj = w[j >> 2] >> (8 * (j & 3));
+      float a = valid ? (float)(wj & 0xF) * sc + zr : 0.0f;
+      float b = valid ? (float)((wj >> 4) & 0xF) * sc + zr : 0.0f;
+      // one rounded value feeds both halves of the split
+      __asm__("" : "+v"(a), "+v"(b));
+      const _Float16 ah = (_Float16)a, bh = (_Float16)b;
+      h[j] = __builtin_bit_cast(uint32_t, v2h{ah, bh});
+      l[j] = __builtin_bit_cast(uint32_t, v2h{(_Float16)(a - (float)ah), (_Float16)(b - (float)bh)});
+    }
+    uint4* dst = (uint4*)(T.k + tok * KROW + 32 * grp);
+    uint4* dlo = (uint4*)(T.klo + tok * KROW + 32 * grp);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      dst[q] = uint4{h[4 * q], h[4 * q + 1], h[4 * q + 2], h[4 * q + 3]};
+      dlo[q] = uint4{l[4 * q], l[4 * q + 1], l[4 * q + 2], l[4 * q + 3]};
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TileStage4<D, NT>::VC; ++i) {
+    const int c = tid + NT * i;
+    if (c >= TileStage4<D, NT>::VN) break;
+    const int cb = c / D;
+    const int d = c % D;
+    const uint32_t w[2] = {S.vc[i].x, S.vc[i].y};
+    float val[16];
+#pragma unroll
+    for (int sl = 0; sl < 16; ++sl) {
+      const uint32_t nib = (w[sl >> 3] >> (4 * (sl & 7))) & 0xF;
+      const bool valid = t0 + 16 * cb + sl < total;
+      val[sl] = valid ? (float)nib * half_lo(S.vp[i][sl]) + half_hi(S.vp[i][sl]) : 0.0f;
+    }
+    // slot s of page cb: k step cb>>1, group s>>2, element (cb&1)*4 + (s&3)
+    _Float16* row = T.v + ((size_t)(cb >> 1) * D + d) * VROW;
+    const int half = (cb & 1) * 4;
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) {
+      const uint32_t h01 = __builtin_bit_cast(
+          uint32_t, v2h{(_Float16)val[4 * gg], (_Float16)val[4 * gg + 1]});
+      const uint32_t h23 = __builtin_bit_cast(
+          uint32_t, v2h{(_Float16)val[4 * gg + 2], (_Float16)val[4 * gg + 3]});
+      *(uint2*)(row + gg * 8 + half) = uint2{h01, h23};
+    }
+  }
+}
+
+template <int D, int G, int NW, int Q>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillParams p) {
   constexpr int NT = 64 * NW;
   constexpr int KS = D / 32;      // 32-dim k steps of QK
   constexpr int JB = D / 16;      // 16-dim column blocks of PV
   constexpr int QT = 32 * NW / G; // query positions per workgroup
-  constexpr int KROW = PrefillTile<D>::KROW;
-  constexpr int VROW = PrefillTile<D>::VROW;
+  constexpr bool INT4 = Q == kQuantInt4;
+  typedef PrefillTile<D, INT4> Tile;
+  constexpr int KROW = Tile::KROW;
+  constexpr int VROW = Tile::VROW;
   constexpr int HALF = D / 2;
 
-  __shared__ PrefillTile<D> sT[2];
+  __shared__ Tile sT[2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -209,12 +337,27 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_int8_kernel(Prefi
   const int full_tiles = (past + q0 + 1) / 64;
 
   // first tile in flight while Q is prepared
-  TileStage<D, NT> S;
-  stage_load<D, NT>(S, p, pt, kvh, 0, last_page, total, tid);
+  typedef typename std::conditional<INT4, TileStage4<D, NT>, TileStage<D, NT>>::type Stage;
+  Stage S;
+  auto load_stage = [&](int t0) {
+    if constexpr (INT4)
+      stage_load4<D, NT>(S, p, pt, kvh, t0, last_page, tid);
+    else
+      stage_load<D, NT>(S, p, pt, kvh, t0, last_page, total, tid);
+  };
+  auto store_stage = [&](Tile& T, int t0) {
+    if constexpr (INT4)
+      stage_store4<D, NT>(S, T, t0, total, tid);
+    else
+      stage_store<D, NT>(S, T, tid);
+  };
+  load_stage(0);
 
   // ---- Q^T operand: rows R = wave*32 + rb*16 + r -> (position, head) -------
-  // f16 of RoPE(q) * scale * log2(e); lane (r, g) holds dims 32ks + 8g .. +7
-  v8h qB[2][KS];
+  // RoPE(q) * scale * log2(e) as an f16 pair hi + lo (~22 bits: a score's
+  // rounding error stays ~2^-20 of its largest term, outlier channels
+  // included); lane (r, g) holds dims 32ks + 8g .. +7
+  v8h qB[2][KS], qL[2][KS];
   int qpos[2];  // absolute position of the row (clamped for dead rows)
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
@@ -253,10 +396,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_int8_kernel(Prefi
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qB[rb][ks][e] = (_Float16)(x[ks][e] * p.scale_log2);
+      for (int e = 0; e < 8; ++e) {
+        float xs = x[ks][e] * p.scale_log2;
+        // one rounded product feeds both halves of the split
+        __asm__("" : "+v"(xs));
+        const _Float16 hi = (_Float16)xs;
+        qB[rb][ks][e] = hi;
+        qL[rb][ks][e] = (_Float16)(xs - (float)hi);
+      }
   }
 
-  stage_store<D, NT>(S, sT[0], tid);
+  store_stage(sT[0], 0);
   __syncthreads();
 
   // ---- online softmax state ----------------------------------------------------
@@ -270,9 +420,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_int8_kernel(Prefi
 
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int t0 = tile * 64;
-    const PrefillTile<D>& T = sT[tile & 1];
+    const Tile& T = sT[tile & 1];
     const bool more = tile + 1 < n_tiles;
-    if (more) stage_load<D, NT>(S, p, pt, kvh, t0 + 64, last_page, total, tid);
+    if (more) load_stage(t0 + 64);
 
     // S^T for both row blocks: 4 column blocks of 16 tokens; k steps outer so
     // that eight independent accumulation chains interleave on the MFMA pipe
@@ -282,21 +432,43 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_int8_kernel(Prefi
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) c[cb][0] = c[cb][1] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int ks = 0; ks < KS; ++ks) {
+        // one term at a time over all eight accumulators, so that consecutive
+        // MFMAs never wait for each other's result
+        v8h a[4];
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-          const v8h a = *(const v8h*)(T.k + (16 * cb + r) * KROW + 8 * g + 32 * ks);
-          c[cb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qB[0][ks], c[cb][0], 0, 0, 0);
-          c[cb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qB[1][ks], c[cb][1], 0, 0, 0);
+        for (int cb = 0; cb < 4; ++cb) a[cb] = *(const v8h*)(T.k + (16 * cb + r) * KROW + 8 * g + 32 * ks);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb)
+            c[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cb], qB[rb][ks], c[cb][rb], 0, 0, 0);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb)
+            c[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cb], qL[rb][ks], c[cb][rb], 0, 0, 0);
+        if constexpr (INT4) {
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb) {
+            const v8h al = *(const v8h*)(T.klo + (16 * cb + r) * KROW + 8 * g + 32 * ks);
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+              c[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qB[rb][ks], c[cb][rb], 0, 0, 0);
+          }
         }
+      }
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
-        const float4 skv = *(const float4*)(T.sk + 16 * cb + 4 * g);
-        const float skx[4] = {skv.x, skv.y, skv.z, skv.w};
+        float skx[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (!INT4) {
+          const float4 skv = *(const float4*)(T.sk + 16 * cb + 4 * g);
+          skx[0] = skv.x, skx[1] = skv.y, skx[2] = skv.z, skx[3] = skv.w;
+        }
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s[rb][cb][e] = c[cb][rb][e] * skx[e];
+          for (int e = 0; e < 4; ++e) s[rb][cb][e] = INT4 ? c[cb][rb][e] : c[cb][rb][e] * skx[e];
       }
     }
     if (tile >= full_tiles) {
@@ -327,13 +499,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_int8_kernel(Prefi
       float psum = 0.0f;
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
-        const float4 svv = *(const float4*)(T.sv + 16 * cb + 4 * g);
-        const float svx[4] = {svv.x, svv.y, svv.z, svv.w};
+        float svx[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (!INT4) {
+          const float4 svv = *(const float4*)(T.sv + 16 * cb + 4 * g);
+          svx[0] = svv.x, svx[1] = svv.y, svx[2] = svv.z, svx[3] = svv.w;
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float pe = fast_exp2(s[rb][cb][e] - m_use);
           psum += pe;
-          pa[rb][cb >> 1][(cb & 1) * 4 + e] = (_Float16)(pe * svx[e]);
+          pa[rb][cb >> 1][(cb & 1) * 4 + e] = (_Float16)(INT4 ? pe : pe * svx[e]);
         }
       }
       psum = xgroup_sum(psum);
@@ -364,7 +539,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_int8_kernel(Prefi
         acc[1][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[1][kst], bv, acc[1][jb], 0, 0, 0);
       }
 
-    if (more) stage_store<D, NT>(S, sT[(tile + 1) & 1], tid);
+    if (more) store_stage(sT[(tile + 1) & 1], t0 + 64);
     __syncthreads();
   }
 
@@ -387,15 +562,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_int8_kernel(Prefi
   }
 }
 
-template <int D, int NW>
+template <int D, int NW, int Q>
 hipError_t launch_dn(const PrefillParams& p, int group, hipStream_t st) {
   auto grid = [&](int qt) { return dim3((p.sq + qt - 1) / qt, p.kv_heads, p.batch); };
   const dim3 block(64 * NW);
   switch (group) {
-    case 1: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 1, NW>), grid(32 * NW), block, 0, st, p); break;
-    case 2: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 2, NW>), grid(16 * NW), block, 0, st, p); break;
-    case 4: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 4, NW>), grid(8 * NW), block, 0, st, p); break;
-    case 8: hipLaunchKernelGGL((gqa_prefill_int8_kernel<D, 8, NW>), grid(4 * NW), block, 0, st, p); break;
+    case 1: hipLaunchKernelGGL((gqa_prefill_kernel<D, 1, NW, Q>), grid(32 * NW), block, 0, st, p); break;
+    case 2: hipLaunchKernelGGL((gqa_prefill_kernel<D, 2, NW, Q>), grid(16 * NW), block, 0, st, p); break;
+    case 4: hipLaunchKernelGGL((gqa_prefill_kernel<D, 4, NW, Q>), grid(8 * NW), block, 0, st, p); break;
+    case 8: hipLaunchKernelGGL((gqa_prefill_kernel<D, 8, NW, Q>), grid(4 * NW), block, 0, st, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -405,17 +580,18 @@ hipError_t launch_dn(const PrefillParams& p, int group, hipStream_t st) {
 // of a 4-wave workgroup at the same LDS footprint (measured 10% faster on the
 // 2 x 2048-over-8192 chunk).
 template <int D>
-hipError_t launch_d(const PrefillParams& p, int group, hipStream_t st) {
-  return launch_dn<D, 8>(p, group, st);
+hipError_t launch_d(const PrefillParams& p, int group, int quant, hipStream_t st) {
+  if (quant == kQuantInt4) return launch_dn<D, 8, kQuantInt4>(p, group, st);
+  return launch_dn<D, 8, kQuantInt8>(p, group, st);
 }
 
 }  // namespace
 
 hipError_t launch_gqa_prefill(const PrefillParams& p, int head_dim, int group, int quant,
                               hipStream_t st) {
-  if (quant != kQuantInt8) return hipErrorInvalidValue;
-  if (head_dim == 64) return launch_d<64>(p, group, st);
-  if (head_dim == 128) return launch_d<128>(p, group, st);
+  if (quant != kQuantInt8 && quant != kQuantInt4) return hipErrorInvalidValue;
+  if (head_dim == 64) return launch_d<64>(p, group, quant, st);
+  if (head_dim == 128) return launch_d<128>(p, group, quant, st);
   return hipErrorInvalidValue;
 }
 

@@ -745,8 +745,6 @@ SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, 
   sai_status st = attention_common(ctx, c, layer, q, dtype, batch, sq, num_heads, cos_cache,
                                    sin_cache, cache_rows, do_rotary, out, op, &G);
   if (st != SAI_OK) return st;
-  if (c->desc.quant != SAI_KV_INT8)
-    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: int4 prefill is not built yet", op);
   const int D = c->desc.head_dim;
   DeviceGuard dg(ctx->device);
   sai::PrefillParams p{};

@@ -459,7 +459,7 @@ static void gpu_dispatch_rope_tables() {
 }
 
 // A session: `layers` GQA nodes per forward pass over one cache, a prefill
-// chunk of `prefill` tokens (int8 only) then `steps` decode passes, each pass
+// chunk of `prefill` tokens then `steps` decode passes, each pass
 // followed by one advance_position. Every node's output and the cache
 // contents are checked against the oracle: the oracle quantises the same
 // appends into a logical cache and attends over its dequantised contents.
@@ -554,6 +554,7 @@ static void session(KvQuant quant, bool bf16, int B, int Hq, int Hkv, int D, int
 static void gpu_session_int8_prefill_decode() { session(KvQuant::Int8, false, 2, 8, 2, 128, 40, 6, 11); }
 static void gpu_session_int8_bf16_d64() { session(KvQuant::Int8, true, 3, 8, 2, 64, 17, 4, 12); }
 static void gpu_session_int4_decode() { session(KvQuant::Int4, false, 2, 16, 2, 128, 0, 24, 13); }
+static void gpu_session_int4_prefill_decode() { session(KvQuant::Int4, true, 2, 8, 2, 128, 37, 5, 15); }
 static void gpu_session_int4_bf16_group4() { session(KvQuant::Int4, true, 1, 8, 2, 128, 0, 20, 14); }
 
 int main(int argc, char** argv) {
@@ -578,6 +579,7 @@ int main(int argc, char** argv) {
       {"gpu_session_int8_bf16_d64", true, gpu_session_int8_bf16_d64},
       {"gpu_session_int4_decode", true, gpu_session_int4_decode},
       {"gpu_session_int4_bf16_group4", true, gpu_session_int4_bf16_group4},
+      {"gpu_session_int4_prefill_decode", true, gpu_session_int4_prefill_decode},
   };
   std::vector<const Case*> run;
   for (int i = 1; i < argc; ++i) {

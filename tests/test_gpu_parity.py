@@ -327,6 +327,36 @@ def test_prefill_chunk_full_size_sampled(rt):
         assert_close(got[:, i:i + 1], ref, f"prefill row {i}")
 
 
+@pytest.mark.parametrize("quant,hq,hkv,d,past,new,qd", [
+    (S.KV_INT4, 16, 4, 128, [300, 0], 150, "bf16"),
+    (S.KV_INT4, 8, 2, 64, [100, 37], 70, "f32"),
+    (S.KV_INT4, 32, 8, 128, [64, 640], 33, "f32"),
+    (S.KV_INT8, 16, 4, 128, [300, 0], 150, "bf16"),
+    (S.KV_INT8, 8, 2, 64, [100, 37], 70, "f32"),
+])
+def test_prefill_outlier_keys(rt, quant, hq, hkv, d, past, new, qd):
+    """Prefill with K carrying x20 outlier channels (Student-t elsewhere), whose
+    largest score terms are in the hundreds: the split (hi + lo) query and, for
+    int4, the split dequantised K keep the outputs within tolerance. int4 codes
+    and group parameters bit-exact; ragged past lengths."""
+    log(f"prefill outlier K quant={quant} hq={hq} hkv={hkv} d={d} past={past} new={new} {qd}")
+
+    def outliers(rng, k):
+        b, n, hd = k.shape
+        t = rng.standard_t(3, size=k.shape).astype(np.float32).reshape(b, n, hd // d, d)
+        t[..., [5, 17, d - 3]] *= 20.0
+        return t.reshape(b, n, hd)
+
+    c = Case(rt, 131 + new, len(past), hq, hkv, d, past, new, theta=5e5, quant=quant,
+             permute_pages=True, kv_dtype=qd, k_transform=outliers)
+    c.step_kv()
+    c.check_codes()
+    q = c.query(qd)
+    got = c.gpu_prefill(q, qd)
+    err = assert_close(got, c.oracle_attend(q), "outlier-K prefill")
+    log(f"  max abs err {err:.2e}")
+
+
 # ------------------------------------------------------------- introspection ---
 def test_decode_kernel_timing_ring(rt):
     """sai_set_decode_timing / sai_decode_kernel_times: events around the decode
