@@ -286,6 +286,29 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   const int tile_off = 0;  // splits start on a tile (64-token) boundary
   TileRegs<D> TA;
   if (tile < n_tiles) load_tile<D>(TA, p.pool, sm_pg + tile_off, tile, p.num_pages, kvh, r, g, n_pages_split);
+  // The wave's second tile is touched (one dword per 128-byte line) so that
+  // it streams into L2 while the query is prepared, instead of the memory
+  // pipe idling until the loop issues its load. Its own lines only: the new
+  // token's page may be rewritten by the append below. The values are
+  // consumed only where the first tile is needed anyway.
+  // Branch-free (lanes past the last line repeat it): a divergent branch here
+  // would make the compiler wait for every outstanding load at its join.
+  constexpr int kLines = (int)(block_bytes_int8(D) / 128);  // 33 for D = 128
+  constexpr int kTouch = (4 * kLines + 63) / 64;              // loads per lane
+  uint32_t touch[kTouch];
+#pragma unroll
+  for (int j = 0; j < kTouch; ++j) touch[j] = 0;
+  if (my_tiles > 1 && !(appender && my_tiles == 2)) {  // uniform over the wave
+    const int t1 = tile + NW;
+#pragma unroll
+    for (int j = 0; j < kTouch; ++j) {
+      const int line = min(lane + 64 * j, 4 * kLines - 1);
+      const int pg = sm_pg[min(t1 * 4 + line / kLines, n_pages_split - 1)];
+      const uint8_t* a = p.pool + block_offset(pg, kvh, p.num_pages, block_bytes_int8(D)) +
+                         (size_t)(line % kLines) * 128;
+      touch[j] = *(const uint32_t*)a;
+    }
+  }
   if (appender && my_tiles > 1) append();
 
   // ---- Q: RoPE at position L-1, split into int8 (hi, lo) terms -------------
@@ -364,6 +387,10 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
     load_tile<D>(T, p.pool, sm_pg + tile_off, wave + k * NW, p.num_pages, kvh, r, g,
                  n_pages_split);
   };
+  // the touch loads, consumed (an empty asm use keeps them): issued right
+  // after the first tile, which the loop waits for first anyway
+#pragma unroll
+  for (int j = 0; j < kTouch; ++j) __asm__ volatile("" ::"v"(touch[j]));
   int k = 0;
   for (; k + 2 < my_tiles; k += 2) {
     ld(TB, k + 1);
