@@ -517,13 +517,15 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   if (threadIdx.x == 0) atomicExch(&p.counters[b * p.kv_heads + kvh], 0);
 }
 
-// Merge of the split partials of one (sequence, kv head): grid (batch, Hkv).
-// The partials were just written by other workgroups (often on other XCDs),
-// so every global read is a full memory latency: each thread loads the (m, l,
-// o) of up to 16 splits in one batch and merges them online; with a uniform
-// split count the range comes from the launch, not from seq_info.
-template <int D, int G>
-__global__ __launch_bounds__(256) void gqa_decode_combine_kernel(DecodeParams p) {
+// Merge of the split partials of one (sequence, kv head): grid (batch, Hkv),
+// one thread per (head, dim) entry. The partials were just written by other
+// workgroups (often on other XCDs), so every global read is a full memory
+// latency: each thread loads the (m, l, o) of C splits in one batch and merges
+// them online (C = the split count rounded up to 2, 4, 8 or 16, so a 2-split
+// merge is one round trip of 6 loads); with a uniform split count the range
+// comes from the launch, not from seq_info.
+template <int D, int G, int C>
+__global__ __launch_bounds__(G * D) void gqa_decode_combine_kernel(DecodeParams p) {
   const int b = blockIdx.x;
   const int kvh = blockIdx.y;
   int split_base, nsplit;
@@ -538,43 +540,52 @@ __global__ __launch_bounds__(256) void gqa_decode_combine_kernel(DecodeParams p)
   const int Hq = p.kv_heads * G;
   const size_t stride = (size_t)p.kv_heads * (G * (D + 2));
   const float* p0 = p.partials + ((size_t)split_base * p.kv_heads + kvh) * (G * (D + 2));
-  for (int t = threadIdx.x; t < G * D; t += 256) {
-    const int hd = t / D, d = t % D;
-    const float* ph = p0 + hd * (D + 2);
-    float M = -INFINITY, Ls = 0.0f, O = 0.0f;
-    for (int s0 = 0; s0 < nsplit; s0 += 16) {
-      float m[16], l[16], o[16];
+  const int t = threadIdx.x;
+  const int hd = t / D, d = t % D;
+  const float* ph = p0 + hd * (D + 2);
+  float M = -INFINITY, Ls = 0.0f, O = 0.0f;
+  for (int s0 = 0; s0 < nsplit; s0 += C) {
+    float m[C], l[C], o[C];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const bool in = s0 + i < nsplit;
-        const float* ps = ph + (size_t)(in ? s0 + i : s0) * stride;
-        m[i] = in ? ps[0] : -INFINITY;
-        l[i] = ps[1];
-        o[i] = ps[2 + d];
-      }
-      float mb = M;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mb = fmaxf(mb, m[i]);
-      if (mb == -INFINITY) continue;
-      const float f0 = M == -INFINITY ? 0.0f : fast_exp2(M - mb);
-      Ls *= f0;
-      O *= f0;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float f = m[i] == -INFINITY ? 0.0f : fast_exp2(m[i] - mb);
-        Ls += l[i] * f;
-        O += o[i] * f;
-      }
-      M = mb;
+    for (int i = 0; i < C; ++i) {
+      const bool in = s0 + i < nsplit;
+      const float* ps = ph + (size_t)(in ? s0 + i : s0) * stride;
+      m[i] = in ? ps[0] : -INFINITY;
+      l[i] = ps[1];
+      o[i] = ps[2 + d];
     }
-    p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+    float mb = M;
+#pragma unroll
+    for (int i = 0; i < C; ++i) mb = fmaxf(mb, m[i]);
+    if (mb == -INFINITY) continue;
+    const float f0 = M == -INFINITY ? 0.0f : fast_exp2(M - mb);
+    Ls *= f0;
+    O *= f0;
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      const float f = m[i] == -INFINITY ? 0.0f : fast_exp2(m[i] - mb);
+      Ls += l[i] * f;
+      O += o[i] * f;
+    }
+    M = mb;
   }
+  p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
 }
 
 template <int D, int G>
 hipError_t launch_combine_dg(const DecodeParams& p, hipStream_t st) {
-  hipLaunchKernelGGL((gqa_decode_combine_kernel<D, G>), dim3(p.batch, p.kv_heads), dim3(256), 0,
-                     st, p);
+  // the largest split count decides the batch width (uniform: the launch's;
+  // ragged: bounded by the longest sequence)
+  const int n = p.uniform_nsplit > 0 ? p.uniform_nsplit : p.max_nsplit;
+  const dim3 grid(p.batch, p.kv_heads), block(G * D);
+  if (n <= 2)
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, G, 2>), grid, block, 0, st, p);
+  else if (n <= 4)
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, G, 4>), grid, block, 0, st, p);
+  else if (n <= 8)
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, G, 8>), grid, block, 0, st, p);
+  else
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, G, 16>), grid, block, 0, st, p);
   return hipGetLastError();
 }
 

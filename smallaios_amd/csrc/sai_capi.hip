@@ -614,7 +614,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   split = std::min(split, kMaxDecodeSplit);
   int64_t work = 0;
   bool multi = false;
-  int64_t n_first = -1;
+  int64_t n_first = -1, n_max = 0;
   bool uniform = true;
   for (int b = 0; b < batch; ++b) {
     const int64_t n = (c->h_seq_lens[b] + 1 + split - 1) / split;
@@ -622,6 +622,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
     multi = multi || n > 1;
     if (n_first < 0) n_first = n;
     uniform = uniform && n == n_first;
+    n_max = std::max(n_max, n);
   }
   if (work <= 0 || work > 0x7FFFFFFF)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: bad work size", op);
@@ -653,6 +654,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   // int4 tiles are compute-heavier: two waves per SIMD from one workgroup
   p.waves = ctx->decode_waves ? ctx->decode_waves : (c->desc.quant == SAI_KV_INT4 ? 8 : 4);
   p.uniform_nsplit = uniform ? (int)n_first : 0;
+  p.max_nsplit = (int)n_max;
   p.partials = ctx->partials;
   p.seq_info = ctx->seq_info;
   p.merge_in_kernel = ctx->decode_merge;

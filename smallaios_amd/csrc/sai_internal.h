@@ -122,6 +122,7 @@ struct DecodeParams {
   int split_tokens;   // tokens per workgroup, multiple of 64
   int waves;          // waves per workgroup (4 or 8)
   int uniform_nsplit; // > 0: every sequence has this many splits (no scan)
+  int max_nsplit;     // the largest split count of any sequence
   float* partials;    // [work_items * Hkv][G][D + 2]
   int32_t* seq_info;  // [batch][2]: first work item, number of splits
   int merge_in_kernel;  // 1: last workgroup merges the splits (counters)
