@@ -16,8 +16,11 @@ Other workloads (--workload, for the per-configuration table): `batch1`
 (8Q/2KV, head_dim 64, context 512), `int4long` (4 sequences of 32768 tokens,
 int4 KV with f16 (scale, zero) per group of 32 dims, K Student-t df 3 with
 four x20 outlier channels), `ragged` (64 sequences with seeded lengths
-U[128, 16384], randomly permuted page table) and `prefill` (2 x 2048 new
-tokens appended to a 6144-token cache, then causal MFMA attention).
+U[128, 16384], randomly permuted page table), `prefill` (2 x 2048 new
+tokens appended to a 6144-token cache, then causal MFMA attention) and `rope`
+(the standalone RotaryEmbedding op over that chunk's queries: [2, 2048,
+32*128] bf16 in the [B, S, H*D] layout at positions 6144.., out of place,
+f32 tables; an f32 input is timed beside it).
 
 Printed: one JSON line with whole-step algorithmic throughput (`value`), % of
 peak, tokens/s, the dominant kernel's roofline from HIP events on its stream,
@@ -55,6 +58,7 @@ WORKLOADS = {
                    theta=500000.0, q_dtype="bf16", permute=True),
     "prefill": dict(kind="prefill", batch=2, hq=32, hkv=8, d=128, past=6144, new=2048,
                     theta=500000.0, q_dtype="bf16", permute=False),
+    "rope": dict(kind="rotary", batch=2, hq=32, d=128, past=6144, new=2048, theta=500000.0),
 }
 
 
@@ -315,8 +319,8 @@ def main():
         rt.set_decode_waves(args.waves)
     if args.merge != "auto":
         rt.set_decode_merge(args.merge == "inkernel")
-    b, hq, hkv, d = w["batch"], w["hq"], w["hkv"], w["d"]
-    qdt = torch.bfloat16 if w["q_dtype"] == "bf16" else torch.float32
+    b, hq, hkv, d = w["batch"], w["hq"], w.get("hkv", 0), w["d"]
+    qdt = torch.bfloat16 if w.get("q_dtype", "bf16") == "bf16" else torch.float32
     stream = torch.cuda.Stream()  # default priority
     seed = 0x5A1A0001
 
@@ -390,6 +394,49 @@ def main():
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                          "traffic": traffic_from_profile(args.workload)},
         }
+    elif w["kind"] == "rotary":
+        past, new = w["past"], w["new"]
+        half = d // 2
+        cos, sin = S.rope_tables(past + new, d, w["theta"])
+        cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        runs = {}
+        for name, dt in (("bf16", torch.bfloat16), ("f32", torch.float32)):
+            x = torch.randn((b, new, hq * d), generator=g, device="cuda").to(dt)
+            y = torch.empty_like(x)
+
+            def kern(x=x, y=y):
+                rt.rotary_embedding(x, y, b, hq, new, d, cos_d, sin_d, start_position=past,
+                                    layout=S.ROPE_BSHD, stream=stream)
+
+            for _ in range(args.warmup):
+                kern()
+            ms = time_steps(torch, kern, args.steps)
+            kus = event_times(torch, stream, lambda: None, kern, args.steps)
+            # x read once, y written once, the chunk's table rows read once
+            alg = 2 * x.numel() * x.element_size() + 2 * new * half * 4
+            runs[name] = (ms, float(np.median(kus)), alg)
+        ms_step, k_us, alg = runs["bf16"]
+        achieved = alg / (k_us * 1e-6) / 1e9
+        result = {
+            "metric": "RotaryEmbedding HBM GB/s (% of peak), 1 MI355X",
+            "value": round(alg / (ms_step * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) queries; no checkpoint)",
+            "config": {"workload": "rope", "batch": b, "heads": hq, "head_dim": d,
+                       "seq": new, "start_position": past, "layout": "[B, S, H*D]",
+                       "tables": "f32 [8192, 64]", "rope_theta": w["theta"]},
+            "algorithmic_bytes_per_step": alg,
+            "rotary_kernel": {"median_us": round(k_us, 3)},
+            "f32_input": {"median_us": round(runs["f32"][1], 3),
+                          "gbps": round(runs["f32"][2] / (runs["f32"][1] * 1e-6) / 1e9, 1)},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                         "traffic": None},
+        }
+        cache = None
     else:  # prefill
         past, new = w["past"], w["new"]
         cos, sin = S.rope_tables(past + new, d, w["theta"])
@@ -437,13 +484,14 @@ def main():
                          "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
         }
     result["measured_copy_gbps"] = round(copy_bandwidth(torch), 1)
-    if args.workload != "prefill" and result["algorithmic_bytes_per_step"] >= 1 << 26:
+    if w["kind"] == "decode" and result["algorithmic_bytes_per_step"] >= 1 << 26:
         rc = read_ceiling(torch, result["algorithmic_bytes_per_step"])
         result["measured_read_ceiling"] = {
             **rc, "bytes": result["algorithmic_bytes_per_step"],
             "step_frac": round(result["value"] / rc["gbps"], 4),
             "decode_kernel_frac": round(result["roofline"]["achieved"] / rc["gbps"], 4)}
-    cache.close()
+    if cache is not None:
+        cache.close()
     rt.close()
     if args.workload == "llama8k" and not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(w)

@@ -191,6 +191,52 @@ sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, cons
                            int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
                            float scale, float* out, void* stream);
 
+/* ---- standalone rotary embedding ----------------------------------------------
+ * Replaces op_rotary_embedding (onnx-rt/src/ops/microsoft.rs:556-652, through
+ * apply_rope_in_place :177-233 and validate_rope_caches :71-110) and
+ * rotary_gpu (onnx-rt/src/cuda/kernels/rotary.rs:274-374).
+ * x, y: device, batch*num_heads*seq rows of head_dim elements of `dtype`
+ * (F32 or BF16); y == x rotates in place, otherwise y must not overlap x and
+ * the elements at and past rotary_dim are copied to y unchanged. Row order:
+ *   SAI_ROPE_BHSD: rows (b, h, s) of [batch, num_heads, seq, head_dim] (also
+ *                  op_rotary_embedding's view of a rank-3 [B, S, H*D] buffer,
+ *                  which it reinterprets without a transpose);
+ *   SAI_ROPE_BSHD: rows (b, s, h) of [batch, seq, num_heads*head_dim]
+ *                  (rotary_gpu's rank-3 layout).
+ * Positions: position_ids (HOST memory) of n_pos == seq entries (shared by all
+ * sequences; tested first) or n_pos == batch*seq (row b*seq + s); or, with
+ * position_ids == NULL, start_position + s for every sequence (rotary_gpu).
+ * cos/sin: device [cache_rows, cache_cols] of table_dtype (F32, or BF16 read
+ * as its exact f32 value); cache_cols must equal rotary_dim / 2.
+ * rotary_dim: <= 0 means head_dim; must be even and at most head_dim.
+ * Pairs (i, i + rotary_dim/2), or (2i, 2i+1) when interleaved; y0 = c*x0 - s*x1,
+ * y1 = s*x0 + c*x1 in f32 with each product rounded on its own; BF16 output
+ * rounds to nearest even.
+ * Errors: SHAPE_MISMATCH (negative dims, n_pos, cache_cols, a position outside
+ * [0, cache_rows), missing tables), INVALID_ATTRIBUTE (rotary_dim, layout),
+ * UNSUPPORTED (dtype, or one (b, s) step larger than 2^31 work items). */
+#define SAI_ROPE_BHSD 0
+#define SAI_ROPE_BSHD 1
+sai_status sai_rotary_embedding(sai_ctx* ctx, const void* x, void* y, int32_t dtype, int32_t batch,
+                                int32_t num_heads, int32_t seq, int32_t head_dim, int32_t layout,
+                                const int64_t* position_ids, int64_t n_pos,
+                                int64_t start_position, const void* cos_cache,
+                                const void* sin_cache, int32_t table_dtype, int32_t cache_rows,
+                                int32_t cache_cols, int32_t rotary_dim, int32_t interleaved,
+                                void* stream);
+
+/* ---- RoPE tables ---------------------------------------------------------------
+ * Replaces precompute_rope_tables (onnx-rt/src/model_loader/gemma.rs:458-472)
+ * with its f32 approximations powf/ln/exp/floor/sin/cos (gemma.rs:480-541):
+ * row pos, column i: inv_freq = 1 / powf_approx(rope_theta, 2i / (2*half)),
+ * angle = pos * inv_freq, cos_approx / sin_approx of angle rounded to bf16;
+ * bit for bit the reference's tables. cos_out, sin_out: device
+ * [max_pos, half] of dtype BF16, or F32 (the same bf16 values widened, as the
+ * reference's GPU dispatch casts them). Errors: UNSUPPORTED (dtype,
+ * max_pos*half >= 2^31), SHAPE_MISMATCH (negative sizes). */
+sai_status sai_rope_tables(sai_ctx* ctx, float rope_theta, int32_t max_pos, int32_t half,
+                           int32_t dtype, void* cos_out, void* sin_out, void* stream);
+
 /* ---- tuning / introspection ------------------------------------------------- */
 /* Tokens per split-K work item of the decode kernel (0 = automatic, else a
  * multiple of 64). Returns the previous value. */

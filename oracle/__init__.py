@@ -79,6 +79,12 @@ def _declare(L: C.CDLL) -> None:
         "sai_or_gqa_cached": (_i, [_p, _i, _i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _i, _i, _i,
                                    _i, _f, _p]),
         "sai_or_check_rhe_vs_rint": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+        "sai_or_ln_approx": (_f, [_f]),
+        "sai_or_exp_approx": (_f, [_f]),
+        "sai_or_floor_approx": (_f, [_f]),
+        "sai_or_sin_approx": (_f, [_f]),
+        "sai_or_cos_approx": (_f, [_f]),
+        "sai_or_rope_tables_bf16": (None, [_i, _i, _f, _p, _p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -157,6 +163,29 @@ def unpack_bits(data, count: int, bits: int):
     out = np.empty(count, dtype=np.uint32)
     lib().sai_or_unpack_bits(_ptr(d), d.size, count, bits, _ptr(out))
     return out
+
+
+# ------------------------------------------------------------ RoPE tables ---
+def rope_tables_bf16(max_pos: int, half: int, theta: float):
+    """The Gemma loader's precomputed tables (gemma.rs:458-472): (cos, sin)
+    as bf16 bit patterns, uint16 [max_pos, half]."""
+    c = np.empty((max_pos, half), np.uint16)
+    s = np.empty((max_pos, half), np.uint16)
+    lib().sai_or_rope_tables_bf16(max_pos, half, float(theta), _ptr(c), _ptr(s))
+    return c, s
+
+
+def bf16_bits_to_f32(bits) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """Round to nearest even, NaN kept quiet (tensor.rs:312-329)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = np.isnan(np.ascontiguousarray(x, dtype=np.float32))
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
 
 
 # ------------------------------------------------------------ RoPE / SDPA ---

@@ -223,6 +223,81 @@ void sai_or_unpack_bits(const uint8_t* data, size_t nbytes, size_t count, int bi
 }
 
 /* ------------------------------------------------------------------------
+ * RoPE tables of the Gemma loader: precompute_rope_tables
+ * (onnx-rt/src/model_loader/gemma.rs:458-472) with powf_approx (:480-483),
+ * ln_approx (:485-500), exp_approx (:502-513), libm_floor_f32 (:517-524),
+ * sin_approx (:526-535), cos_approx (:537-539). Every step is one f32
+ * operation, rounded on its own, in the reference's order; the constants are
+ * Rust's core::f32::consts, written here as decimal literals that the
+ * compiler rounds to the same f32 values.
+ * ---------------------------------------------------------------------- */
+#define OR_LN_2 0.693147180559945309417232121458176568f
+#define OR_LOG2_E 1.44269504088896340735992468100189214f
+#define OR_TAU 6.28318530717958647692528676655900577f
+#define OR_PI 3.14159265358979323846264338327950288f
+#define OR_FRAC_PI_2 1.57079632679489661923132169163975144f
+
+float sai_or_floor_approx(float x) {
+  float xi = (float)sai_or_sat_i32(x); /* `x as i32 as f32` */
+  return x < xi ? xi - 1.0f : xi;
+}
+
+float sai_or_ln_approx(float x) {
+  if (x <= 0.0f) return -INFINITY;
+  uint32_t bits = f2u(x);
+  int32_t e = (int32_t)((bits >> 23) & 0xffu) - 127;
+  float m = u2f((bits & 0x7fffffu) | (127u << 23));
+  float y = (m - 1.0f) / (m + 1.0f);
+  float y2 = y * y;
+  float acc = y + y2 * y / 3.0f;
+  acc = acc + y2 * y2 * y / 5.0f;
+  acc = acc + y2 * y2 * y2 * y / 7.0f;
+  float ln_m = 2.0f * acc;
+  return (float)e * OR_LN_2 + ln_m;
+}
+
+float sai_or_exp_approx(float x) {
+  float y = x * OR_LOG2_E;
+  int32_t k = sai_or_sat_i32(sai_or_floor_approx(y));
+  float r = x - (float)k * OR_LN_2;
+  float p = 1.0f / 24.0f + r * (1.0f / 120.0f);
+  p = 1.0f / 6.0f + r * p;
+  p = 0.5f + r * p;
+  p = 1.0f + r * p;
+  float e_r = 1.0f + r * p;
+  int32_t kc = k < -126 ? -126 : (k > 127 ? 127 : k);
+  float two_k = u2f((uint32_t)(kc + 127) << 23);
+  return e_r * two_k;
+}
+
+float sai_or_sin_approx(float x) {
+  float y = x - sai_or_floor_approx(x / OR_TAU) * OR_TAU;
+  if (y > OR_PI) y -= OR_TAU;
+  float y2 = y * y;
+  float p = 1.0f / 5040.0f - y2 * (1.0f / 362880.0f);
+  p = 1.0f / 120.0f - y2 * p;
+  p = 1.0f / 6.0f - y2 * p;
+  p = 1.0f - y2 * p;
+  return y * p;
+}
+
+float sai_or_cos_approx(float x) { return sai_or_sin_approx(x + OR_FRAC_PI_2); }
+
+void sai_or_rope_tables_bf16(int max_pos, int half, float rope_theta, uint16_t* cos_out,
+                             uint16_t* sin_out) {
+  float head_dim = (float)(half * 2);
+  for (int pos = 0; pos < max_pos; ++pos)
+    for (int i = 0; i < half; ++i) {
+      float ex = (2.0f * (float)i) / head_dim;
+      float inv_freq = 1.0f / sai_or_exp_approx(ex * sai_or_ln_approx(rope_theta));
+      float angle = (float)pos * inv_freq;
+      size_t o = (size_t)pos * half + i;
+      cos_out[o] = sai_or_f32_to_bf16(sai_or_cos_approx(angle));
+      sin_out[o] = sai_or_f32_to_bf16(sai_or_sin_approx(angle));
+    }
+}
+
+/* ------------------------------------------------------------------------
  * RoPE -- apply_rope_in_place (onnx-rt/src/ops/microsoft.rs:177-233) with
  * validate_rope_caches (:71-110), rope_position_for (:115-121),
  * check_rope_position (:125-133) and rotate_rope_block (:137-160).

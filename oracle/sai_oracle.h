@@ -54,6 +54,16 @@ void sai_or_pack_bits(const uint32_t* values, size_t n, int bits, uint8_t* out);
 void sai_or_unpack_bits(const uint8_t* data, size_t nbytes, size_t count, int bits,
                         uint32_t* out);
 
+/* --- RoPE tables of the Gemma loader (f32 approximations) -------------- */
+float sai_or_ln_approx(float x);
+float sai_or_exp_approx(float x);
+float sai_or_floor_approx(float x);
+float sai_or_sin_approx(float x);
+float sai_or_cos_approx(float x);
+/* precompute_rope_tables: bf16 bits, row-major [max_pos, half]. */
+void sai_or_rope_tables_bf16(int max_pos, int half, float rope_theta, uint16_t* cos_out,
+                             uint16_t* sin_out);
+
 /* --- RoPE / SDPA / GQA (f32 reference op) ------------------------------ */
 int sai_or_apply_rope(float* x, int b, int heads, int sq, int head_dim, const float* cos_cache,
                       const float* sin_cache, int cache_rows, int cache_cols,

@@ -74,8 +74,11 @@ EXPORTS = [
     "sai_kvcache_lengths", "sai_kvcache_read", "sai_kvcache_pool", "sai_kv_append",
     "sai_gqa_decode", "sai_gqa_with_cache", "sai_gqa_prefill", "sai_set_decode_split",
     "sai_set_decode_waves", "sai_set_decode_merge", "sai_last_decode_shape",
-    "sai_set_decode_timing", "sai_decode_kernel_times",
+    "sai_set_decode_timing", "sai_decode_kernel_times", "sai_rotary_embedding",
+    "sai_rope_tables",
 ]
+ROPE_BHSD = 0
+ROPE_BSHD = 1
 
 
 def _declare(L: C.CDLL) -> None:
@@ -109,6 +112,9 @@ def _declare(L: C.CDLL) -> None:
         "sai_last_decode_shape": (i32, [p, C.POINTER(i32), C.POINTER(i32)]),
         "sai_set_decode_timing": (i32, [p, i32]),
         "sai_decode_kernel_times": (i32, [p, C.POINTER(C.c_float), i32]),
+        "sai_rotary_embedding": (i32, [p, p, p, i32, i32, i32, i32, i32, i32, p, C.c_int64,
+                                       C.c_int64, p, p, i32, i32, i32, i32, i32, p]),
+        "sai_rope_tables": (i32, [p, f, i32, i32, i32, p, p, p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -215,6 +221,36 @@ class Runtime:
         if n < 0:
             self.check(n, "sai_decode_kernel_times")
         return [float(buf[i]) for i in range(n)]
+
+
+    # ---- standalone RoPE --------------------------------------------------
+    def rotary_embedding(self, x, y, batch, num_heads, seq, head_dim, cos, sin, *,
+                         position_ids=None, start_position=0, layout=ROPE_BHSD,
+                         rotary_dim=0, interleaved=False, stream=None, dtype=None,
+                         table_dtype=None):
+        """sai_rotary_embedding: rotate x (device, F32/BF16) into y (may be x).
+        position_ids: host int array of seq or batch*seq entries, or None for
+        start_position + s. cos/sin: device [rows, cols] (F32 or BF16)."""
+        dt = dtype if dtype is not None else _dtype_code(x)
+        tdt = table_dtype if table_dtype is not None else _dtype_code(cos)
+        rows, cols = int(cos.shape[0]), int(cos.shape[1])
+        ids = None
+        n_pos = 0
+        if position_ids is not None:
+            ids = np.ascontiguousarray(position_ids, dtype=np.int64).ravel()
+            n_pos = ids.size
+        self.check(self._L.sai_rotary_embedding(
+            self.handle, _dev_ptr(x), _dev_ptr(y), dt, batch, num_heads, seq, head_dim, layout,
+            None if ids is None else ids.ctypes.data_as(C.c_void_p), n_pos, int(start_position),
+            _dev_ptr(cos), _dev_ptr(sin), tdt, rows, cols, int(rotary_dim), int(interleaved),
+            _stream(stream)), "rotary_embedding")
+
+    def rope_tables(self, max_pos, half, theta, cos_out, sin_out, dtype=DTYPE_BF16,
+                    stream=None):
+        """sai_rope_tables: the Gemma loader's [max_pos, half] tables on the device."""
+        self.check(self._L.sai_rope_tables(self.handle, float(theta), int(max_pos), int(half),
+                                           int(dtype), _dev_ptr(cos_out), _dev_ptr(sin_out),
+                                           _stream(stream)), "rope_tables")
 
 
 class KvCache:

@@ -31,8 +31,10 @@ COMMON = [
 EXTRA = {
     "kv_append.hip": ["-ffp-contract=off"],
     "sai_capi.hip": ["-ffp-contract=off"],
+    "rotary.hip": ["-ffp-contract=off"],
 }
-SOURCES = ["kv_append.hip", "gqa_decode.hip", "gqa_decode_int4.hip", "gqa_prefill.hip", "sai_capi.hip"]
+SOURCES = ["kv_append.hip", "gqa_decode.hip", "gqa_decode_int4.hip", "gqa_prefill.hip",
+           "rotary.hip", "sai_capi.hip"]
 
 
 def _run(cmd):

@@ -315,7 +315,6 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   v4i qB[KS];
   float sq_hi;
   {
-    const int pos = L - 1;
     float qv[KS][16];
     float amax = 0.0f;
 #pragma unroll

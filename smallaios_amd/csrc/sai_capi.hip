@@ -772,3 +772,224 @@ SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, 
   if (e != hipSuccess) return hip_fail(ctx, e, "gqa_prefill launch");
   return SAI_OK;
 }
+
+// ------------------------------------------------ standalone rotary embedding ---
+namespace {
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Launches over sequences [b0, b0 + nb) x sequence indices [s0, s0 + ns) with
+// the positions `tab` (mode 0: one start per sequence, mode 1: one position
+// per sequence index). Splits the range so that every launch holds at most
+// sai::kRotaryTab positions and fewer than 2^31 work items.
+struct RotaryPlan {
+  sai::RotaryArgs base;
+  bool x_bf16, t_bf16, interleaved;
+  hipStream_t st;
+  uint64_t unit;  // work items of one (b, s) step: head_groups * items
+};
+
+constexpr uint64_t kRotaryMaxItems = (uint64_t)1 << 31;
+
+hipError_t rotary_launch_range(const RotaryPlan& pl, int mode, int32_t b0, int32_t nb,
+                               int32_t s0, int32_t ns, const int32_t* tab) {
+  sai::RotaryArgs a = pl.base;
+  a.mode = mode;
+  a.b0 = b0;
+  a.s0 = s0;
+  a.ns = ns;
+  const uint64_t total = (uint64_t)nb * (uint64_t)ns * pl.unit;
+  a.total = (uint32_t)total;
+  const int n = mode == 0 ? nb : ns;
+  for (int i = 0; i < n; ++i) a.tab[i] = tab[i];
+  return sai::launch_rotary(a, pl.x_bf16, pl.t_bf16, pl.interleaved, pl.st);
+}
+
+// Mode 0 over all sequences: row position = start[b] + s.
+hipError_t rotary_affine(const RotaryPlan& pl, int32_t batch, int32_t seq,
+                         const std::vector<int32_t>& start) {
+  const int32_t ns_max = (int32_t)std::min<uint64_t>((uint64_t)seq, kRotaryMaxItems / pl.unit);
+  for (int32_t s0 = 0; s0 < seq; s0 += ns_max) {
+    const int32_t ns = std::min(ns_max, seq - s0);
+    const uint64_t per_b = (uint64_t)ns * pl.unit;
+    const int32_t nb_max =
+        (int32_t)std::min<uint64_t>((uint64_t)sai::kRotaryTab, kRotaryMaxItems / per_b);
+    for (int32_t b0 = 0; b0 < batch; b0 += nb_max) {
+      const int32_t nb = std::min(nb_max, batch - b0);
+      hipError_t e = rotary_launch_range(pl, 0, b0, nb, s0, ns, start.data() + b0);
+      if (e != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
+}
+
+// Mode 1 over sequences [b0, b0 + nb): row position = pos[s].
+hipError_t rotary_explicit(const RotaryPlan& pl, int32_t b0, int32_t nb, int32_t seq,
+                           const int32_t* pos) {
+  const int32_t ns_max = (int32_t)std::min<uint64_t>(
+      (uint64_t)sai::kRotaryTab, kRotaryMaxItems / pl.unit);
+  for (int32_t s0 = 0; s0 < seq; s0 += ns_max) {
+    const int32_t ns = std::min(ns_max, seq - s0);
+    const int32_t nb_max = (int32_t)std::max<uint64_t>(
+        1, std::min<uint64_t>((uint64_t)nb, kRotaryMaxItems / ((uint64_t)ns * pl.unit)));
+    for (int32_t bb = 0; bb < nb; bb += nb_max) {
+      const int32_t n = std::min(nb_max, nb - bb);
+      hipError_t e = rotary_launch_range(pl, 1, b0 + bb, n, s0, ns, pos + s0);
+      if (e != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
+SAI_API sai_status sai_rotary_embedding(sai_ctx* ctx, const void* x, void* y, int32_t dtype,
+                                        int32_t batch, int32_t num_heads, int32_t seq,
+                                        int32_t head_dim, int32_t layout,
+                                        const int64_t* position_ids, int64_t n_pos,
+                                        int64_t start_position, const void* cos_cache,
+                                        const void* sin_cache, int32_t table_dtype,
+                                        int32_t cache_rows, int32_t cache_cols, int32_t rotary_dim,
+                                        int32_t interleaved, void* stream) {
+  if (!ctx) return SAI_ERR_NULL;
+  const char* op = "sai_rotary_embedding";
+  if (dtype != SAI_DTYPE_F32 && dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (need F32 or BF16)", op, dtype);
+  if (table_dtype != SAI_DTYPE_F32 && table_dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: table dtype %d (need F32 or BF16)", op,
+                table_dtype);
+  if (layout != SAI_ROPE_BHSD && layout != SAI_ROPE_BSHD)
+    return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE, "%s: unknown layout %d", op, layout);
+  if (batch < 0 || num_heads < 0 || seq < 0 || head_dim < 0 || cache_rows < 0)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: negative dimension", op);
+  // apply_rope_in_place's order of checks (ops/microsoft.rs:197-232)
+  const int64_t bs = (int64_t)batch * seq;
+  if (position_ids && n_pos != bs && n_pos != seq)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                "apply_rope_in_place: position_ids length %lld != B*Sq = %lld", (long long)n_pos,
+                (long long)bs);
+  if (!cos_cache || !sin_cache)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "RotaryEmbedding: missing %s",
+                cos_cache ? "sin_cache" : "cos_cache");
+  const int32_t rd = rotary_dim <= 0 ? head_dim : rotary_dim;
+  if (rd == 0 || rd > head_dim)
+    return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE,
+                "apply_rope_in_place: rotary_dim must be in 1..=head_dim");
+  if (rd % 2 != 0)
+    return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE, "apply_rope_in_place: rotary_dim must be even");
+  const int32_t half = rd / 2;
+  if (cache_cols != half)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                "apply_rope_in_place: cache inner dim %d != rotary_dim/2 = %d", cache_cols, half);
+  const bool any_rows = batch > 0 && num_heads > 0 && seq > 0;
+  // Positions: every row's table row is checked here, so the kernel reads
+  // only rows that exist.
+  std::vector<int32_t> start;  // per sequence, when every sequence is start + s
+  std::vector<int32_t> pos;    // explicit, [n_pos]
+  bool shared = false;
+  if (position_ids) {
+    shared = n_pos == seq;
+    if (any_rows) {
+      for (int32_t b = 0; b < batch; ++b)
+        for (int32_t s = 0; s < seq; ++s) {
+          const int64_t p = shared ? position_ids[s] : position_ids[(int64_t)b * seq + s];
+          if (p < 0 || p >= cache_rows)
+            return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                        "apply_rope_in_place: position %lld out of cache range %d", (long long)p,
+                        cache_rows);
+        }
+      const int64_t n = shared ? seq : bs;
+      pos.resize((size_t)n);
+      for (int64_t i = 0; i < n; ++i) pos[(size_t)i] = (int32_t)position_ids[i];
+      // one start per sequence when the ids run start, start + 1, ...
+      bool affine = true;
+      const int32_t nseq = shared ? 1 : batch;
+      for (int32_t b = 0; b < nseq && affine; ++b)
+        for (int32_t s = 1; s < seq; ++s)
+          if (pos[(size_t)b * seq + s] != pos[(size_t)b * seq] + s) {
+            affine = false;
+            break;
+          }
+      if (affine) {
+        start.resize((size_t)batch);
+        for (int32_t b = 0; b < batch; ++b) start[(size_t)b] = pos[shared ? 0 : (size_t)b * seq];
+      }
+    }
+  } else {
+    // rotary_gpu (rotary.rs:247-252): the start and the whole run must be rows
+    if (start_position < 0 || start_position + seq > cache_rows)
+      return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                  "rotary_gpu: position + seq_len exceeds cos/sin table length (%lld + %d > %d)",
+                  (long long)start_position, seq, cache_rows);
+    start.assign((size_t)batch, (int32_t)start_position);
+  }
+  if (!any_rows) return SAI_OK;
+  if (!x || !y) return fail(ctx, SAI_ERR_NULL, "%s: x or y is NULL", op);
+
+  // vector path: 4 or 8 pairs per item with 8- to 64-byte accesses (every
+  // row, half row and table row then starts on a multiple of the access);
+  // the heads of an item share its cos/sin loads. bf16 rows: 8 pairs x 2
+  // heads (16-byte row loads); f32 rows: 4 pairs x 4 heads.
+  const bool vec = half % 4 == 0 && head_dim % 8 == 0 && aligned16(x) && aligned16(y) &&
+                   aligned16(cos_cache) && aligned16(sin_cache);
+  const int32_t P = !vec ? 1 : (dtype == SAI_DTYPE_BF16 && half % 8 == 0 ? 8 : 4);
+  const int32_t NH = !vec ? 1 : (P == 8 ? 2 : 4);
+  RotaryPlan pl{};
+  pl.base.x = x;
+  pl.base.y = y;
+  pl.base.cos = cos_cache;
+  pl.base.sin = sin_cache;
+  pl.base.rot_items = half / P;
+  pl.base.items = pl.base.rot_items + (x != y ? (head_dim - rd) / P : 0);
+  pl.base.pairs_per_item = P;
+  pl.base.heads_per_item = NH;
+  pl.base.head_groups = (num_heads + NH - 1) / NH;
+  pl.base.heads = num_heads;
+  pl.base.seq = seq;
+  pl.base.head_dim = head_dim;
+  pl.base.rot_dim = rd;
+  pl.base.cache_cols = cache_cols;
+  pl.base.layout = layout;
+  pl.x_bf16 = dtype == SAI_DTYPE_BF16;
+  pl.t_bf16 = table_dtype == SAI_DTYPE_BF16;
+  pl.interleaved = interleaved != 0;
+  pl.st = (hipStream_t)stream;
+  pl.unit = (uint64_t)pl.base.head_groups * (uint64_t)pl.base.items;
+  if (pl.unit == 0) return SAI_OK;
+  if (pl.unit >= kRotaryMaxItems)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: %d head groups x %d items per step exceed 2^31", op,
+                pl.base.head_groups, pl.base.items);
+  DeviceGuard dg(ctx->device);
+  hipError_t e = hipSuccess;
+  if (!start.empty()) {
+    e = rotary_affine(pl, batch, seq, start);
+  } else if (shared) {
+    e = rotary_explicit(pl, 0, batch, seq, pos.data());
+  } else {
+    for (int32_t b = 0; b < batch && e == hipSuccess; ++b)
+      e = rotary_explicit(pl, b, 1, seq, pos.data() + (size_t)b * seq);
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "rotary launch");
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_rope_tables(sai_ctx* ctx, float rope_theta, int32_t max_pos, int32_t half,
+                                   int32_t dtype, void* cos_out, void* sin_out, void* stream) {
+  if (!ctx) return SAI_ERR_NULL;
+  if (dtype != SAI_DTYPE_F32 && dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "sai_rope_tables: dtype %d (need BF16 or F32)", dtype);
+  if (max_pos < 0 || half < 0)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "sai_rope_tables: negative size");
+  const uint64_t n = (uint64_t)max_pos * (uint64_t)half;
+  if (n >= kRotaryMaxItems)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "sai_rope_tables: %d x %d entries exceed 2^31", max_pos,
+                half);
+  if (n == 0) return SAI_OK;
+  if (!cos_out || !sin_out) return fail(ctx, SAI_ERR_NULL, "sai_rope_tables: NULL output");
+  DeviceGuard dg(ctx->device);
+  hipError_t e = sai::launch_rope_tables(rope_theta, (uint32_t)max_pos, (uint32_t)half,
+                                         dtype == SAI_DTYPE_BF16, cos_out, sin_out,
+                                         (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "rope_tables launch");
+  return SAI_OK;
+}

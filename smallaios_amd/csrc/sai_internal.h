@@ -149,7 +149,39 @@ struct PrefillParams {
   float scale_log2;
 };
 
+// Positions carried by one rotary launch (kernel argument block).
+constexpr int kRotaryTab = 512;
+
+// One launch of the standalone rotary kernel over sequences [b0, b0 + nb) and
+// sequence indices [s0, s0 + ns) (nb is implied by total). Rows of head_dim
+// elements: layout 0 = (b, h, s) order ([B, H, S, D]), 1 = (b, s, h) order
+// ([B, S, H*D]). Position of row (b, s): mode 0: tab[b - b0] + s, mode 1:
+// tab[s - s0]. A (b, s) step has head_groups groups of heads_per_item heads
+// (the last one may be short), each with `items` work items: rot_items
+// rotation items of pairs_per_item pairs, then (out of place) pass-through
+// items of pairs_per_item elements from rot_dim on. Supported
+// (pairs_per_item, heads_per_item): (1, 1), (4, 4), (8, 2).
+struct RotaryArgs {
+  const void* x;
+  void* y;
+  const void* cos;
+  const void* sin;
+  uint32_t total;  // work items of the launch
+  int32_t items, rot_items, pairs_per_item, heads_per_item, head_groups;
+  int32_t heads, seq, head_dim, rot_dim, cache_cols;
+  int32_t layout, mode;
+  int32_t b0, s0, ns;
+  int32_t tab[kRotaryTab];
+};
+
 // Launchers (return hipError_t of the launch).
+// Standalone RoPE (rotary.hip): x/y f32 or bf16, tables f32 or bf16.
+hipError_t launch_rotary(const RotaryArgs& a, bool x_bf16, bool table_bf16, bool interleaved,
+                         hipStream_t st);
+// RoPE tables [max_pos, half] of the Gemma loader's precompute (rotary.hip),
+// bf16 or (bf16 values widened to) f32.
+hipError_t launch_rope_tables(float theta, uint32_t max_pos, uint32_t half, bool bf16,
+                              void* cos_out, void* sin_out, hipStream_t st);
 hipError_t launch_kv_append(const AppendParams& p, int head_dim, int quant, hipStream_t s);
 hipError_t launch_gqa_decode(const DecodeParams& p, int head_dim, int group, int quant,
                              int work_items, bool combine, hipStream_t s);

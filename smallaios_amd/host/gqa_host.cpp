@@ -154,7 +154,7 @@ Result<RocmRuntime, HipError> RocmRuntime::init(int device) {
 }
 
 bool RocmRuntime::supports_op(std::string_view op_type) {
-  return op_type == "GroupQueryAttention";
+  return op_type == "GroupQueryAttention" || op_type == "RotaryEmbedding";
 }
 
 RocmRuntime& RocmRuntime::operator=(RocmRuntime&& o) noexcept {
@@ -750,6 +750,238 @@ Result<std::vector<DeviceTensor>, OpError> dispatch_gqa(
   std::vector<DeviceTensor> outs;
   outs.push_back(std::move(r).value());
   return outs;
+}
+
+// --------------------------------------------------------- RotaryEmbedding ---
+namespace {
+
+// find_int_attr (gpu_executor.rs:701-703): the first attribute of that name.
+const AttributeProto* find_attr(const std::vector<AttributeProto>& attrs, const char* name) {
+  for (const AttributeProto& a : attrs)
+    if (a.name == name) return &a;
+  return nullptr;
+}
+
+bool is_table_dtype(DataType dt) { return dt == DataType::Float || dt == DataType::BFloat16; }
+
+OpError rotary_gpu_error(const char* what) {
+  return OpError::internal(std::string("ROCm RotaryEmbedding: ") +
+                           HipError::runtime(what).to_string());
+}
+
+// The host copy of a device tensor's bytes.
+Result<std::vector<uint8_t>, OpError> read_back(const DeviceTensor& t, const char* what) {
+  auto h = t.to_host();
+  if (!h) return OpError::internal(std::string(what) + ": " + h.error().to_string());
+  return std::move(h).value();
+}
+
+}  // namespace
+
+Result<std::vector<DeviceTensor>, OpError> dispatch_rotary_embedding(
+    RocmRuntime& runtime, const std::vector<const DeviceTensor*>& inputs,
+    const std::vector<AttributeProto>& attrs, const KvCacheDispatchCtx* kv_cache_ctx) {
+  auto missing = [](const char* role) {
+    return OpError::internal(std::string("GPU RotaryEmbedding: missing input '") + role + "'");
+  };
+  const DeviceTensor* x = slot(inputs, 0);
+  if (!x) return missing("X");
+  // resolve_rotary_inputs (gpu_executor.rs:724-745)
+  const DeviceTensor *pos = nullptr, *cos = nullptr, *sin = nullptr;
+  if (inputs.size() >= 4) {
+    if (!(pos = slot(inputs, 1))) return missing("position_ids");
+    if (!(cos = slot(inputs, 2))) return missing("cos_cache");
+    if (!(sin = slot(inputs, 3))) return missing("sin_cache");
+  } else {
+    if (!(cos = slot(inputs, 1))) return missing("cos_cache");
+    if (!(sin = slot(inputs, 2))) return missing("sin_cache");
+  }
+  const AttributeProto* il = find_attr(attrs, "interleaved");
+  const bool interleaved = il && il->i != 0;
+  // pick_rotary_position / read_first_i64_position (gpu_executor.rs:747-771)
+  int32_t position = 0;
+  if (pos) {
+    auto raw = read_back(*pos, "RotaryEmbedding pos D2H");
+    if (!raw) return raw.error();
+    const std::vector<uint8_t>& b = raw.value();
+    if (b.size() >= 8) {
+      int64_t v;
+      std::memcpy(&v, b.data(), 8);
+      position = (int32_t)(uint32_t)(uint64_t)v;  // `as i32`: the low 32 bits
+    }
+  } else if (kv_cache_ctx && kv_cache_ctx->cache) {
+    position = (int32_t)kv_cache_ctx->cache->current_position();
+  }
+  // rotary_num_heads_for_rank3 (gpu_executor.rs:795-813)
+  std::optional<int64_t> nh3;
+  if (x->shape.size() == 3) {
+    if (const AttributeProto* nh = find_attr(attrs, "num_heads")) {
+      nh3 = nh->i;
+    } else {
+      const int64_t hd = (cos->shape.empty() ? 0 : cos->shape.back()) * 2;
+      if (hd > 0 && x->shape[2] % hd == 0) nh3 = x->shape[2] / hd;
+    }
+  }
+  // rotary_gpu (kernels/rotary.rs:274-374)
+  if (x->dtype != DataType::Float && x->dtype != DataType::BFloat16)
+    return rotary_gpu_error("rotary_gpu: unsupported dtype (need Float or BFloat16)");
+  int64_t B, H, S, D;
+  int32_t layout;
+  if (x->shape.size() == 4) {
+    B = x->shape[0], H = x->shape[1], S = x->shape[2], D = x->shape[3];
+    layout = SAI_ROPE_BHSD;
+  } else if (x->shape.size() == 3) {
+    if (!nh3) return rotary_gpu_error("rotary_gpu: rank-3 input requires num_heads_for_rank3");
+    if (*nh3 <= 0) return rotary_gpu_error("rotary_gpu: num_heads must be > 0 for rank-3 input");
+    if (x->shape[2] % *nh3 != 0)
+      return rotary_gpu_error("rotary_gpu: hidden not divisible by num_heads (rank-3)");
+    B = x->shape[0], H = *nh3, S = x->shape[1], D = x->shape[2] / *nh3;
+    layout = SAI_ROPE_BSHD;
+  } else {
+    return rotary_gpu_error("rotary_gpu: x must be rank-3 or rank-4");
+  }
+  if (D <= 0 || D % 2 != 0)
+    return rotary_gpu_error("rotary_gpu: head_dim must be a positive even integer");
+  const int64_t half = D / 2;
+  // validate_rotary_tables (rotary.rs:218-256); bf16 tables count as Float,
+  // as the reference casts them first
+  if (!is_table_dtype(cos->dtype) || !is_table_dtype(sin->dtype))
+    return rotary_gpu_error("rotary_gpu: cos/sin tables must be Float");
+  if (cos->shape.size() != 2 || sin->shape.size() != 2)
+    return rotary_gpu_error("rotary_gpu: cos/sin tables must be rank-2");
+  if (cos->shape[1] != half || sin->shape[1] != half)
+    return rotary_gpu_error("rotary_gpu: cos/sin inner dim must equal head_dim / 2");
+  const int64_t max_seq = cos->shape[0];
+  if (sin->shape[0] != max_seq)
+    return rotary_gpu_error("rotary_gpu: cos/sin tables must share max_seq_len");
+  if (position < 0 || (int64_t)position + S > max_seq)
+    return rotary_gpu_error("rotary_gpu: position + seq_len exceeds cos/sin table length");
+  if (cos->dtype != sin->dtype)
+    return rotary_gpu_error("rotary_gpu: cos/sin tables must share a dtype");
+  auto out = DeviceTensor::alloc(x->shape, x->dtype);
+  if (!out) return OpError::internal("ROCm RotaryEmbedding: " + out.error().to_string());
+  std::vector<DeviceTensor> outs;
+  if (B <= 0 || H <= 0 || S <= 0) {
+    outs.push_back(std::move(out).value());
+    return outs;
+  }
+  const int64_t lim = std::numeric_limits<int32_t>::max();
+  if (B > lim || H > lim || S > lim || D > lim || max_seq > lim)
+    return rotary_gpu_error("rotary_gpu: dimension exceeds i32");
+  const sai_status st = sai_rotary_embedding(
+      runtime.raw(), x->buffer.as_ptr(), out.value().buffer.as_ptr(), sai_dtype(x->dtype),
+      (int32_t)B, (int32_t)H, (int32_t)S, (int32_t)D, layout, nullptr, 0, position,
+      cos->buffer.as_ptr(), sin->buffer.as_ptr(), sai_dtype(cos->dtype), (int32_t)max_seq,
+      (int32_t)half, (int32_t)D, interleaved ? 1 : 0, nullptr);
+  if (st != SAI_OK) return from_status(st, "ROCm RotaryEmbedding: ", runtime);
+  outs.push_back(std::move(out).value());
+  return outs;
+}
+
+Result<DeviceTensor, OpError> op_rotary_embedding(RocmRuntime& runtime,
+                                                  const std::vector<const DeviceTensor*>& inputs,
+                                                  bool interleaved, int64_t rotary_embedding_dim,
+                                                  int64_t num_heads_attr) {
+  const DeviceTensor* input = slot(inputs, 0);
+  if (!input) return OpError::shape("RotaryEmbedding: missing input");
+  const DeviceTensor* position_ids = slot(inputs, 1);
+  if (!position_ids) return OpError::shape("RotaryEmbedding: missing position_ids");
+  const DeviceTensor* cos = slot(inputs, 2);
+  if (!cos) return OpError::shape("RotaryEmbedding: missing cos_cache");
+  const DeviceTensor* sin = slot(inputs, 3);
+  if (!sin) return OpError::shape("RotaryEmbedding: missing sin_cache");
+  if (input->dtype != DataType::Float) return OpError::shape("RotaryEmbedding requires Float input");
+  // rank 3 is read as [B, num_heads, S, D] over the same bytes (microsoft.rs:578-600)
+  std::vector<int64_t> view;
+  if (input->shape.size() == 3) {
+    const int64_t b = input->shape[0], sq = input->shape[1], hidden = input->shape[2];
+    if (num_heads_attr <= 0)
+      return OpError::attribute("RotaryEmbedding: num_heads must be > 0 for rank-3 input");
+    if (hidden % num_heads_attr != 0)
+      return OpError::shape("RotaryEmbedding: hidden not divisible by num_heads");
+    view = {b, num_heads_attr, sq, hidden / num_heads_attr};
+  } else if (input->shape.size() == 4) {
+    view = input->shape;
+  } else {
+    return OpError::shape("RotaryEmbedding: input must be rank-3 or rank-4");
+  }
+  for (int64_t v : view)
+    if (v < 0 || v > std::numeric_limits<int32_t>::max())
+      return OpError::shape("RotaryEmbedding: dimension out of range");
+  const int64_t head_dim = view[3];
+  const int64_t rotary_dim = rotary_embedding_dim <= 0 ? head_dim : rotary_embedding_dim;
+  std::vector<int64_t> positions;
+  if (position_ids->dtype == DataType::Int64 || position_ids->dtype == DataType::Int32) {
+    auto raw = read_back(*position_ids, "RotaryEmbedding position_ids D2H");
+    if (!raw) return raw.error();
+    const std::vector<uint8_t>& b = raw.value();
+    const size_t n = position_ids->total_elements();
+    positions.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+      if (position_ids->dtype == DataType::Int64) {
+        std::memcpy(&positions[i], b.data() + 8 * i, 8);
+      } else {
+        int32_t v;
+        std::memcpy(&v, b.data() + 4 * i, 4);
+        positions[i] = v;
+      }
+    }
+  } else {
+    return OpError::shape("RotaryEmbedding: position_ids must be int32 or int64");
+  }
+  // apply_rope_in_place (microsoft.rs:177-233) with validate_rope_caches (:71-110)
+  const int64_t b = view[0], sq = view[2];
+  if ((int64_t)positions.size() != b * sq && (int64_t)positions.size() != sq) {
+    char buf[160];
+    std::snprintf(buf, sizeof buf, "apply_rope_in_place: position_ids length %zu != B*Sq = %lld",
+                  positions.size(), (long long)(b * sq));
+    return OpError::shape(buf);
+  }
+  if (cos->dtype != DataType::Float || sin->dtype != DataType::Float)
+    return OpError::shape("RotaryEmbedding requires Float input");
+  if (rotary_dim == 0 || rotary_dim > head_dim)
+    return OpError::attribute("apply_rope_in_place: rotary_dim must be in 1..=head_dim");
+  if (rotary_dim % 2 != 0) return OpError::attribute("apply_rope_in_place: rotary_dim must be even");
+  if (cos->shape.size() != 2 || sin->shape.size() != 2)
+    return OpError::shape("apply_rope_in_place: cos/sin caches must be rank-2");
+  if (sin->shape[1] != cos->shape[1])
+    return OpError::shape("apply_rope_in_place: cos and sin caches must share the inner dim");
+  if (cos->shape[1] != rotary_dim / 2) {
+    char buf[128];
+    std::snprintf(buf, sizeof buf, "apply_rope_in_place: cache inner dim %lld != rotary_dim/2 = %lld",
+                  (long long)cos->shape[1], (long long)(rotary_dim / 2));
+    return OpError::shape(buf);
+  }
+  // both tables are read at the same rows
+  const int64_t rows = std::min(cos->shape[0], sin->shape[0]);
+  if (rows < 0 || rows > std::numeric_limits<int32_t>::max())
+    return OpError::shape("apply_rope_in_place: cos/sin caches must be rank-2");
+  auto out = DeviceTensor::alloc(input->shape, DataType::Float);
+  if (!out) return OpError::internal("ROCm RotaryEmbedding: " + out.error().to_string());
+  const sai_status st = sai_rotary_embedding(
+      runtime.raw(), input->buffer.as_ptr(), out.value().buffer.as_ptr(), SAI_DTYPE_F32,
+      (int32_t)view[0], (int32_t)view[1], (int32_t)view[2], (int32_t)view[3], SAI_ROPE_BHSD,
+      positions.data(), (int64_t)positions.size(), 0, cos->buffer.as_ptr(), sin->buffer.as_ptr(),
+      SAI_DTYPE_F32, (int32_t)rows, (int32_t)cos->shape[1], (int32_t)rotary_dim,
+      interleaved ? 1 : 0, nullptr);
+  if (st != SAI_OK) return from_status(st, "", runtime);
+  return std::move(out).value();
+}
+
+Result<std::pair<DeviceTensor, DeviceTensor>, HipError> precompute_rope_tables(
+    RocmRuntime& runtime, size_t max_pos, size_t half, float rope_theta) {
+  if (max_pos > (size_t)std::numeric_limits<int32_t>::max() ||
+      half > (size_t)std::numeric_limits<int32_t>::max())
+    return HipError::runtime("precompute_rope_tables:size", SAI_ERR_UNSUPPORTED);
+  auto c = DeviceTensor::alloc({(int64_t)max_pos, (int64_t)half}, DataType::BFloat16);
+  if (!c) return c.error();
+  auto s = DeviceTensor::alloc({(int64_t)max_pos, (int64_t)half}, DataType::BFloat16);
+  if (!s) return s.error();
+  const sai_status st =
+      sai_rope_tables(runtime.raw(), rope_theta, (int32_t)max_pos, (int32_t)half, SAI_DTYPE_BF16,
+                      c.value().buffer.as_ptr(), s.value().buffer.as_ptr(), nullptr);
+  if (st != SAI_OK) return HipError::runtime("precompute_rope_tables", st);
+  return std::make_pair(std::move(c).value(), std::move(s).value());
 }
 
 }  // namespace sai::rocm

@@ -16,6 +16,10 @@
 //   parse_gqa_attrs (gpu_executor.rs:862-884)            parse_gqa_attrs
 //   gqa_validate (ops/microsoft.rs:933-984)              gqa_validate
 //   dispatch_gqa (gpu_executor.rs:944-970)               dispatch_gqa
+//   dispatch_rotary_embedding (gpu_executor.rs:815-851)  dispatch_rotary_embedding
+//     with rotary_gpu (kernels/rotary.rs:274-374)
+//   op_rotary_embedding (ops/microsoft.rs:556-652)       op_rotary_embedding
+//   precompute_rope_tables (model_loader/gemma.rs:458)   precompute_rope_tables
 //
 // Differences by design, each forced by the quantised paged cache:
 //   * the cache stores int8 (per token-head scale) or int4 (group-32 scale and
@@ -29,7 +33,11 @@
 //   * RoPE is fused: cos/sin caches at inputs 7 and 8 rotate Q and the new K
 //     inside the kernels, as op_group_query_attention does on the CPU
 //     (ops/microsoft.rs:1108-1133);
-//   * the attention output is always f32.
+//   * the attention output is always f32;
+//   * dispatch_rotary_embedding reads bf16 cos/sin tables directly (their
+//     exact f32 values, which the reference's bf16->f32 cast produces) instead
+//     of casting them into a new device tensor; op_rotary_embedding takes
+//     device tensors and reads position_ids back to the host.
 //
 // Errors never throw: every fallible call returns Result<T, E>.
 #ifndef SAI_GQA_HOST_HPP
@@ -122,7 +130,7 @@ class RocmRuntime {
   // RuntimeError{"rocm_runtime_init:not_gfx950"} when the device is not gfx950.
   static Result<RocmRuntime, HipError> init(int device = 0);
   // The ops this runtime dispatches (CudaRuntime::supports_op, mod.rs:874-889,
-  // narrowed to the one op this library implements).
+  // narrowed to the ops this library implements).
   static bool supports_op(std::string_view op_type);
 
   RocmRuntime(RocmRuntime&& o) noexcept : ctx_(std::exchange(o.ctx_, nullptr)), device_(o.device_) {}
@@ -365,6 +373,39 @@ Result<GqaShape, OpError> gqa_validate(const std::vector<int64_t>& q_shape,
 Result<std::vector<DeviceTensor>, OpError> dispatch_gqa(
     RocmRuntime& runtime, const std::vector<const DeviceTensor*>& inputs,
     const std::vector<AttributeProto>& attrs, KvCacheDispatchCtx* kv_cache_ctx);
+
+// gpu_executor.rs:815-851 over rotary_gpu (kernels/rotary.rs:274-374).
+// Inputs: [X, position_ids, cos_cache, sin_cache] (4 or more) or
+// [X, cos_cache, sin_cache]. The start position is the first i64 of
+// position_ids (its first 8 bytes, truncated to i32; 0 when it holds fewer
+// than 8 bytes), else the cache's current_position(), else 0; row s of every
+// sequence uses table row start + s. X: [B, H, S, D] or [B, S, H*D] (rank 3:
+// num_heads from the attribute, else hidden / (2 * table inner dim)), Float or
+// BFloat16; tables Float or BFloat16 [max_seq, D/2]; attribute `interleaved`.
+// Returns { Y } of X's shape and dtype. Errors: InternalError
+// "GPU RotaryEmbedding: missing input '...'", and "ROCm RotaryEmbedding: "
+// followed by the HipError of rotary_gpu's checks (same wording).
+// Asynchronous on the null stream, except the position_ids read-back.
+Result<std::vector<DeviceTensor>, OpError> dispatch_rotary_embedding(
+    RocmRuntime& runtime, const std::vector<const DeviceTensor*>& inputs,
+    const std::vector<AttributeProto>& attrs, const KvCacheDispatchCtx* kv_cache_ctx);
+
+// ops/microsoft.rs:556-652 on device tensors, with the CPU op's checks, order
+// and messages: Float X of rank 4 [B, H, S, D], or rank 3 [B, S, H*D] read as
+// [B, num_heads, S, D] without a transpose; position_ids Int64 or Int32 of
+// S or B*S entries (read back to the host and range-checked); rotary_dim
+// <= 0 means D, else a partial rotation with the tail copied. Returns Y (Float,
+// X's shape).
+Result<DeviceTensor, OpError> op_rotary_embedding(RocmRuntime& runtime,
+                                                  const std::vector<const DeviceTensor*>& inputs,
+                                                  bool interleaved, int64_t rotary_embedding_dim,
+                                                  int64_t num_heads_attr);
+
+// model_loader/gemma.rs:458-472: (cos, sin) BFloat16 device tensors
+// [max_pos, half], bit for bit the loader's tables. Errors: RuntimeError
+// "precompute_rope_tables" with the C ABI status; AllocFailed.
+Result<std::pair<DeviceTensor, DeviceTensor>, HipError> precompute_rope_tables(
+    RocmRuntime& runtime, size_t max_pos, size_t half, float rope_theta);
 
 }  // namespace sai::rocm
 

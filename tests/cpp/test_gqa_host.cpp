@@ -16,6 +16,7 @@
 #include <functional>
 #include <random>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../../oracle/sai_oracle.h"
@@ -175,7 +176,9 @@ void cpu_errors_and_types() {
           "%s", HipError::runtime("kv_cache_append:layer_idx").to_string().c_str());
   REQUIRE(HipError::alloc_failed(64, 2).to_string() == "hipMalloc(64 bytes) failed: code 2", "display");
   REQUIRE(RocmRuntime::supports_op("GroupQueryAttention"), "supports GQA");
-  REQUIRE(!RocmRuntime::supports_op("MatMul") && !RocmRuntime::supports_op(""), "only GQA");
+  REQUIRE(RocmRuntime::supports_op("RotaryEmbedding"), "supports RotaryEmbedding");
+  REQUIRE(!RocmRuntime::supports_op("MatMul") && !RocmRuntime::supports_op(""),
+          "only GQA and RotaryEmbedding");
   REQUIRE(element_size(DataType::Float) == 4 && element_size(DataType::BFloat16) == 2 &&
               element_size(DataType::Int64) == 8 && element_size(DataType::Int8) == 1,
           "element sizes");
@@ -462,6 +465,304 @@ static void gpu_dispatch_rope_tables() {
 // chunk of `prefill` tokens then `steps` decode passes, each pass
 // followed by one advance_position. Every node's output and the cache
 // contents are checked against the oracle: the oracle quantises the same
+// ------------------------------------------------------- RotaryEmbedding ---
+// make_rope_caches with taylor_cos / taylor_sin (ops/microsoft.rs:1318-1343),
+// f32 throughout like the Rust test helpers.
+float taylor_cos(float x) {
+  const float x2 = x * x;
+  return 1.0f - x2 / 2.0f + x2 * x2 / 24.0f - x2 * x2 * x2 / 720.0f;
+}
+float taylor_sin(float x) {
+  const float x2 = x * x;
+  return x * (1.0f - x2 / 6.0f + x2 * x2 / 120.0f - x2 * x2 * x2 / 5040.0f);
+}
+std::pair<DeviceTensor, DeviceTensor> make_rope_caches(int max_seq, int half) {
+  std::vector<float> c, s;
+  for (int p = 0; p < max_seq; ++p)
+    for (int i = 0; i < half; ++i) {
+      const float theta = (float)p * (0.1f + (float)i * 0.01f);
+      c.push_back(taylor_cos(theta));
+      s.push_back(taylor_sin(theta));
+    }
+  return {f32_tensor(c, shp({max_seq, half})), f32_tensor(s, shp({max_seq, half}))};
+}
+
+DeviceTensor i64_tensor(const std::vector<int64_t>& v, std::vector<int64_t> shape) {
+  return must(DeviceTensor::from_host(v.data(), v.size() * 8, std::move(shape), DataType::Int64),
+              "i64 upload");
+}
+
+std::vector<float> host_f32(const DeviceTensor& t) { return must(t.to_host_f32(), "to_host_f32"); }
+
+// The reference's microsoft.rs RotaryEmbedding tests (:1346-1416, :1876-1939)
+// through op_rotary_embedding, plus its rank-3 view and partial rotation
+// against the oracle.
+void gpu_rotary_cpu_op_kats() {
+  RocmRuntime& rt = runtime();
+  const std::vector<float> x4 = {1.0f, 2.0f, 3.0f, 4.0f};
+  {  // rope_position_zero_is_identity / rope_interleaved_position_zero_identity
+    auto [c, s] = make_rope_caches(4, 2);
+    DeviceTensor in = f32_tensor(x4, shp({1, 1, 1, 4}));
+    DeviceTensor pos = i64_tensor({0}, shp({1, 1}));
+    for (bool il : {false, true}) {
+      DeviceTensor out = must(op_rotary_embedding(rt, {&in, &pos, &c, &s}, il, 0, 1), "pos 0");
+      const std::vector<float> v = host_f32(out);
+      for (int i = 0; i < 4; ++i) REQUIRE(std::fabs(v[i] - x4[i]) < 1e-5f, "identity %d", i);
+    }
+  }
+  {  // rope_interleaved_vs_noninterleaved_differ
+    auto [c, s] = make_rope_caches(4, 2);
+    DeviceTensor in = f32_tensor(x4, shp({1, 1, 1, 4}));
+    DeviceTensor pos = i64_tensor({1}, shp({1, 1}));
+    const std::vector<float> a = host_f32(must(op_rotary_embedding(rt, {&in, &pos, &c, &s}, false, 0, 1), "a"));
+    const std::vector<float> b = host_f32(must(op_rotary_embedding(rt, {&in, &pos, &c, &s}, true, 0, 1), "b"));
+    bool diff = false;
+    for (int i = 0; i < 4; ++i) diff |= std::fabs(a[i] - b[i]) > 1e-4f;
+    REQUIRE(diff, "interleaved and non-interleaved RoPE should differ");
+  }
+  {  // rope_non_interleaved_manual_calc
+    auto [c, s] = make_rope_caches(2, 2);
+    DeviceTensor in = f32_tensor(x4, shp({1, 1, 1, 4}));
+    DeviceTensor pos = i64_tensor({1}, shp({1, 1}));
+    const std::vector<float> v = host_f32(must(op_rotary_embedding(rt, {&in, &pos, &c, &s}, false, 0, 1), "manual"));
+    const float c0 = taylor_cos(0.1f), s0 = taylor_sin(0.1f), c1 = taylor_cos(0.11f), s1 = taylor_sin(0.11f);
+    const float e[4] = {c0 * 1.0f - s0 * 3.0f, c1 * 2.0f - s1 * 4.0f, s0 * 1.0f + c0 * 3.0f,
+                        s1 * 2.0f + c1 * 4.0f};
+    for (int i = 0; i < 4; ++i) REQUIRE(std::fabs(v[i] - e[i]) < 1e-4f, "manual %d: %g vs %g", i, v[i], e[i]);
+  }
+  {  // rope_int32_positions
+    auto [c, s] = make_rope_caches(4, 2);
+    DeviceTensor in = f32_tensor(x4, shp({1, 1, 1, 4}));
+    const int32_t zero = 0;
+    DeviceTensor pos = must(DeviceTensor::from_host(&zero, 4, shp({1, 1}), DataType::Int32), "i32");
+    const std::vector<float> v = host_f32(must(op_rotary_embedding(rt, {&in, &pos, &c, &s}, false, 0, 1), "i32 pos"));
+    for (int i = 0; i < 4; ++i) REQUIRE(std::fabs(v[i] - x4[i]) < 1e-5f, "i32 identity %d", i);
+  }
+  {  // rope_rank3_reshape_path
+    auto [c, s] = make_rope_caches(4, 1);
+    DeviceTensor in = f32_tensor(x4, shp({1, 1, 4}));
+    DeviceTensor pos = i64_tensor({0}, shp({1, 1}));
+    DeviceTensor out = must(op_rotary_embedding(rt, {&in, &pos, &c, &s}, false, 0, 2), "rank3");
+    REQUIRE(out.shape == shp({1, 1, 4}), "rank-3 output shape");
+  }
+  {  // rope_rejects_bad_rank / _bad_num_heads_for_rank3 / _missing_inputs
+    auto [c, s] = make_rope_caches(2, 2);
+    DeviceTensor r2 = f32_tensor(x4, shp({1, 4}));
+    DeviceTensor r3 = f32_tensor(x4, shp({1, 1, 4}));
+    DeviceTensor r4 = f32_tensor(x4, shp({1, 1, 1, 4}));
+    DeviceTensor pos = i64_tensor({0}, shp({1}));
+    OpError e = must_fail(op_rotary_embedding(rt, {&r2, &pos, &c, &s}, false, 0, 1), "rank 2");
+    REQUIRE(e.kind == OpError::Kind::ShapeMismatch &&
+                e.message == "RotaryEmbedding: input must be rank-3 or rank-4", "%s", e.to_string().c_str());
+    e = must_fail(op_rotary_embedding(rt, {&r3, &pos, &c, &s}, false, 0, 0), "num_heads 0");
+    REQUIRE(e.kind == OpError::Kind::InvalidAttribute &&
+                e.message == "RotaryEmbedding: num_heads must be > 0 for rank-3 input", "%s", e.to_string().c_str());
+    e = must_fail(op_rotary_embedding(rt, {&r4}, false, 0, 1), "missing");
+    REQUIRE(e.message == "RotaryEmbedding: missing position_ids", "%s", e.to_string().c_str());
+    e = must_fail(op_rotary_embedding(rt, {&r4, &pos, &c}, false, 0, 1), "missing sin");
+    REQUIRE(e.message == "RotaryEmbedding: missing sin_cache", "%s", e.to_string().c_str());
+    DeviceTensor pos9 = i64_tensor({9}, shp({1}));
+    e = must_fail(op_rotary_embedding(rt, {&r4, &pos9, &c, &s}, false, 0, 1), "pos 9");
+    REQUIRE(e.kind == OpError::Kind::ShapeMismatch &&
+                e.message == "apply_rope_in_place: position 9 out of cache range 2", "%s", e.to_string().c_str());
+    DeviceTensor pos2 = i64_tensor({0, 1}, shp({2}));
+    e = must_fail(op_rotary_embedding(rt, {&r4, &pos2, &c, &s}, false, 0, 1), "n_pos");
+    REQUIRE(e.message == "apply_rope_in_place: position_ids length 2 != B*Sq = 1", "%s", e.to_string().c_str());
+    e = must_fail(op_rotary_embedding(rt, {&r4, &pos, &c, &s}, false, 3, 1), "odd rotary_dim");
+    REQUIRE(e.kind == OpError::Kind::InvalidAttribute &&
+                e.message == "apply_rope_in_place: rotary_dim must be even", "%s", e.to_string().c_str());
+    e = must_fail(op_rotary_embedding(rt, {&r4, &pos, &c, &s}, false, 2, 1), "cols");
+    REQUIRE(e.message == "apply_rope_in_place: cache inner dim 2 != rotary_dim/2 = 1", "%s", e.to_string().c_str());
+    DeviceTensor f = i64_tensor({0}, shp({1}));
+    f.dtype = DataType::Float16;
+    f.shape = shp({4});
+    e = must_fail(op_rotary_embedding(rt, {&r4, &f, &c, &s}, false, 0, 1), "pos dtype");
+    REQUIRE(e.message == "RotaryEmbedding: position_ids must be int32 or int64", "%s", e.to_string().c_str());
+  }
+  {  // rank 3 [B, S, H*D] read as [B, H, S, D] over the same bytes; partial rotary_dim
+    const int B = 2, S = 3, H = 2, D = 16, RD = 8, rows = 16;
+    std::mt19937_64 g(21);
+    std::vector<float> x = gauss(g, (size_t)B * S * H * D);
+    std::vector<float> c, sn;
+    rope_tables(rows, RD, 1e4, c, sn);
+    DeviceTensor cd = f32_tensor(c, shp({rows, RD / 2})), sd = f32_tensor(sn, shp({rows, RD / 2}));
+    std::vector<int64_t> ids = {5, 2, 9, 0, 1, 15};
+    DeviceTensor in = f32_tensor(x, shp({B, S, H * D}));
+    DeviceTensor pos = i64_tensor(ids, shp({B, S}));
+    for (bool il : {false, true}) {
+      const std::vector<float> got = host_f32(must(op_rotary_embedding(rt, {&in, &pos, &cd, &sd}, il, RD, H), "rank3 partial"));
+      std::vector<float> want = x;
+      REQUIRE(sai_or_apply_rope(want.data(), B, H, S, D, c.data(), sn.data(), rows, RD / 2, ids.data(),
+                                (int)ids.size(), il ? 1 : 0, RD) == 0, "oracle");
+      REQUIRE(std::memcmp(got.data(), want.data(), got.size() * 4) == 0, "rank-3 partial (il %d) differs from the oracle", (int)il);
+    }
+  }
+}
+
+// The reference's GPU rotary tests (tests/test_cuda.rs:2622-2830) through
+// dispatch_rotary_embedding, and the dispatcher's position / layout rules.
+void gpu_rotary_dispatch() {
+  RocmRuntime& rt = runtime();
+  std::mt19937_64 g(33);
+  auto check = [&](const std::vector<float>& x, int B, int H, int S, int D, bool bshd,
+                   const std::vector<float>& c, const std::vector<float>& sn, int rows, int start,
+                   bool il, const std::vector<float>& got, const char* what) {
+    // oracle over [B, H, S, D]
+    std::vector<float> v((size_t)B * H * S * D);
+    for (int b = 0; b < B; ++b)
+      for (int h = 0; h < H; ++h)
+        for (int s = 0; s < S; ++s)
+          for (int d = 0; d < D; ++d) {
+            const size_t src = bshd ? (((size_t)b * S + s) * H + h) * D + d : (((size_t)b * H + h) * S + s) * D + d;
+            v[(((size_t)b * H + h) * S + s) * D + d] = x[src];
+          }
+    std::vector<int64_t> ids(S);
+    for (int s = 0; s < S; ++s) ids[s] = start + s;
+    REQUIRE(sai_or_apply_rope(v.data(), B, H, S, D, c.data(), sn.data(), rows, D / 2, ids.data(), S,
+                              il ? 1 : 0, D) == 0, "%s: oracle", what);
+    for (int b = 0; b < B; ++b)
+      for (int h = 0; h < H; ++h)
+        for (int s = 0; s < S; ++s)
+          for (int d = 0; d < D; ++d) {
+            const size_t dst = bshd ? (((size_t)b * S + s) * H + h) * D + d : (((size_t)b * H + h) * S + s) * D + d;
+            const float w = v[(((size_t)b * H + h) * S + s) * D + d];
+            REQUIRE(std::memcmp(&got[dst], &w, 4) == 0, "%s: (%d,%d,%d,%d) got %g want %g", what, b, h, s, d, got[dst], w);
+          }
+  };
+  {  // test_gpu_rotary_f32_small_split_half: [1,2,4,8], [X, cos, sin] -> position 0
+    const int B = 1, H = 2, S = 4, D = 8, rows = 16;
+    std::vector<float> x(B * H * S * D);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = (float)i * 0.0125f - 0.25f;
+    std::vector<float> c, sn;
+    rope_tables(rows, D, 1e4, c, sn);
+    DeviceTensor xd = f32_tensor(x, shp({B, H, S, D}));
+    DeviceTensor cd = f32_tensor(c, shp({rows, D / 2})), sd = f32_tensor(sn, shp({rows, D / 2}));
+    auto out = must(dispatch_rotary_embedding(rt, {&xd, &cd, &sd}, {}, nullptr), "small split-half");
+    REQUIRE(out.size() == 1 && out[0].shape == xd.shape && out[0].dtype == DataType::Float, "output");
+    check(x, B, H, S, D, false, c, sn, rows, 0, false, host_f32(out[0]), "small split-half");
+  }
+  {  // test_gpu_rotary_f32_decode_step_interleaved: [2,4,1,16] at 37 from position_ids
+    const int B = 2, H = 4, S = 1, D = 16, rows = 64;
+    std::vector<float> x(B * H * S * D);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin((float)i * 0.07f);
+    std::vector<float> c, sn;
+    rope_tables(rows, D, 1e4, c, sn);
+    DeviceTensor xd = f32_tensor(x, shp({B, H, S, D}));
+    DeviceTensor cd = f32_tensor(c, shp({rows, D / 2})), sd = f32_tensor(sn, shp({rows, D / 2}));
+    DeviceTensor pos = i64_tensor({37}, shp({1, 1}));
+    auto out = must(dispatch_rotary_embedding(rt, {&xd, &pos, &cd, &sd},
+                                              {AttributeProto::make_int("interleaved", 1)}, nullptr),
+                    "decode interleaved");
+    check(x, B, H, S, D, false, c, sn, rows, 37, true, host_f32(out[0]), "decode interleaved");
+  }
+  {  // test_gpu_rotary_bf16_gemma_shape: [1,8,8,128] bf16 against the f32 op within 1e-2
+    const int B = 1, H = 8, S = 8, D = 128, rows = 32;
+    std::vector<float> x(B * H * S * D);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = std::cos((float)i * 0.001f) * 0.5f;
+    DeviceTensor xd = bf16_tensor(x, shp({B, H, S, D}));  // x now holds the bf16 values
+    std::vector<float> c, sn;
+    rope_tables(rows, D, 1e4, c, sn);
+    DeviceTensor cd = f32_tensor(c, shp({rows, D / 2})), sd = f32_tensor(sn, shp({rows, D / 2}));
+    auto out = must(dispatch_rotary_embedding(rt, {&xd, &cd, &sd}, {}, nullptr), "bf16 gemma");
+    REQUIRE(out[0].dtype == DataType::BFloat16, "bf16 output");
+    auto raw = must(out[0].to_host(), "bf16 read");
+    std::vector<float> want = x;
+    std::vector<int64_t> ids(S);
+    for (int s = 0; s < S; ++s) ids[s] = s;
+    REQUIRE(sai_or_apply_rope(want.data(), B, H, S, D, c.data(), sn.data(), rows, D / 2, ids.data(), S, 0, D) == 0, "oracle");
+    for (size_t i = 0; i < want.size(); ++i) {
+      uint16_t b;
+      std::memcpy(&b, raw.data() + 2 * i, 2);
+      REQUIRE(std::fabs(sai_or_bf16_to_f32(b) - want[i]) < 1e-2f, "bf16 element %zu", i);
+      REQUIRE(b == sai_or_f32_to_bf16(want[i]), "bf16 element %zu not the rounded oracle value", i);
+    }
+  }
+  {  // rank 3 [B, S, H*D]: rows (b, s, h), num_heads from the attribute or the tables
+    const int B = 2, H = 3, S = 5, D = 64, rows = 40;
+    std::vector<float> x = gauss(g, (size_t)B * S * H * D);
+    std::vector<float> c, sn;
+    rope_tables(rows, D, 5e5, c, sn);
+    DeviceTensor xd = f32_tensor(x, shp({B, S, H * D}));
+    DeviceTensor cd = f32_tensor(c, shp({rows, D / 2})), sd = f32_tensor(sn, shp({rows, D / 2}));
+    DeviceTensor pos = i64_tensor({11, 99, 3}, shp({3}));  // only the first id counts
+    auto a = must(dispatch_rotary_embedding(rt, {&xd, &pos, &cd, &sd}, {AttributeProto::make_int("num_heads", H)}, nullptr), "rank3 attr");
+    check(x, B, H, S, D, true, c, sn, rows, 11, false, host_f32(a[0]), "rank3 attr");
+    auto b = must(dispatch_rotary_embedding(rt, {&xd, &pos, &cd, &sd}, {}, nullptr), "rank3 derived");
+    check(x, B, H, S, D, true, c, sn, rows, 11, false, host_f32(b[0]), "rank3 derived");
+    // bf16 tables are read as their f32 values (the reference casts them)
+    std::vector<float> cb = c, sb = sn;
+    DeviceTensor cbd = bf16_tensor(cb, shp({rows, D / 2})), sbd = bf16_tensor(sb, shp({rows, D / 2}));
+    auto t = must(dispatch_rotary_embedding(rt, {&xd, &pos, &cbd, &sbd}, {}, nullptr), "bf16 tables");
+    check(x, B, H, S, D, true, cb, sb, rows, 11, false, host_f32(t[0]), "bf16 tables");
+  }
+  {  // no position_ids: the cache's current position
+    const int D = 128, rows = 64;
+    auto cache = must(GpuKvCache::allocate(rt, 1, 1, D, rows, KvQuant::Int8, {LayerKind::global()}, 1), "cache");
+    std::vector<float> k1 = gauss(g, 7 * D), v1 = gauss(g, 7 * D);
+    DeviceTensor kd = f32_tensor(k1, shp({1, 7, D})), vd = f32_tensor(v1, shp({1, 7, D}));
+    must(cache.append(0, kd, vd), "append 7");
+    must(cache.advance_position(), "advance");
+    KvCacheDispatchCtx ctx{&cache, 0};
+    std::vector<float> x = gauss(g, 4 * 2 * D);
+    std::vector<float> c, sn;
+    rope_tables(rows, D, 1e4, c, sn);
+    DeviceTensor xd = f32_tensor(x, shp({1, 4, 2, D}));
+    DeviceTensor cd = f32_tensor(c, shp({rows, D / 2})), sd = f32_tensor(sn, shp({rows, D / 2}));
+    auto out = must(dispatch_rotary_embedding(rt, {&xd, &cd, &sd}, {}, &ctx), "cache position");
+    check(x, 1, 4, 2, D, false, c, sn, rows, 7, false, host_f32(out[0]), "cache position");
+  }
+  {  // errors (rotary.rs:150-256, gpu_executor.rs:724-745)
+    std::vector<float> c, sn;
+    rope_tables(4, 8, 1e4, c, sn);
+    DeviceTensor cd = f32_tensor(c, shp({4, 4})), sd = f32_tensor(sn, shp({4, 4}));
+    DeviceTensor x7 = f32_tensor(std::vector<float>(7), shp({1, 1, 1, 7}));
+    DeviceTensor c3 = f32_tensor(std::vector<float>(3), shp({1, 3}));
+    struct E {
+      std::vector<const DeviceTensor*> in;
+      std::vector<AttributeProto> attrs;
+      const char* msg;
+    };
+    DeviceTensor x8 = f32_tensor(std::vector<float>(8 * 5), shp({1, 1, 5, 8}));
+    DeviceTensor x2 = f32_tensor(std::vector<float>(8), shp({1, 8}));
+    DeviceTensor x3 = f32_tensor(std::vector<float>(2 * 12), shp({1, 2, 12}));
+    DeviceTensor xi = i64_tensor({0, 0, 0, 0}, shp({1, 1, 1, 4}));
+    DeviceTensor ci = i64_tensor(std::vector<int64_t>(16), shp({4, 4}));
+    const std::vector<E> cases = {
+        {{&x7, &c3, &c3}, {}, "internal error: ROCm RotaryEmbedding: HIP rotary_gpu: head_dim must be a positive even integer failed: code -1"},
+        {{&x8, &cd, &sd}, {}, "internal error: ROCm RotaryEmbedding: HIP rotary_gpu: position + seq_len exceeds cos/sin table length failed: code -1"},
+        {{&x2, &cd, &sd}, {}, "internal error: ROCm RotaryEmbedding: HIP rotary_gpu: x must be rank-3 or rank-4 failed: code -1"},
+        {{&x3, &cd, &sd}, {}, "internal error: ROCm RotaryEmbedding: HIP rotary_gpu: rank-3 input requires num_heads_for_rank3 failed: code -1"},
+        {{&x3, &cd, &sd}, {AttributeProto::make_int("num_heads", 0)}, "internal error: ROCm RotaryEmbedding: HIP rotary_gpu: num_heads must be > 0 for rank-3 input failed: code -1"},
+        {{&x3, &cd, &sd}, {AttributeProto::make_int("num_heads", 5)}, "internal error: ROCm RotaryEmbedding: HIP rotary_gpu: hidden not divisible by num_heads (rank-3) failed: code -1"},
+        {{&xi, &cd, &sd}, {}, "internal error: ROCm RotaryEmbedding: HIP rotary_gpu: unsupported dtype (need Float or BFloat16) failed: code -1"},
+        {{&x8, &ci, &ci}, {}, "internal error: ROCm RotaryEmbedding: HIP rotary_gpu: cos/sin tables must be Float failed: code -1"},
+        {{&x8, &c3, &c3}, {}, "internal error: ROCm RotaryEmbedding: HIP rotary_gpu: cos/sin inner dim must equal head_dim / 2 failed: code -1"},
+        {{&x8}, {}, "internal error: GPU RotaryEmbedding: missing input 'cos_cache'"},
+        {{nullptr, &cd, &sd}, {}, "internal error: GPU RotaryEmbedding: missing input 'X'"},
+        {{&x8, nullptr, &cd, &sd}, {}, "internal error: GPU RotaryEmbedding: missing input 'position_ids'"},
+    };
+    for (const E& e : cases) {
+      OpError err = must_fail(dispatch_rotary_embedding(rt, e.in, e.attrs, nullptr), e.msg);
+      REQUIRE(err.to_string() == e.msg, "got '%s'", err.to_string().c_str());
+    }
+  }
+}
+
+// precompute_rope_tables (model_loader/gemma.rs:458-472) against the oracle.
+void gpu_rope_tables() {
+  RocmRuntime& rt = runtime();
+  for (auto [max_pos, half, theta] : {std::tuple<int, int, float>{16, 4, 1e4f}, {4096, 64, 1e6f}, {300, 128, 5e5f}}) {
+    auto t = must(precompute_rope_tables(rt, (size_t)max_pos, (size_t)half, theta), "tables");
+    REQUIRE(t.first.shape == shp({max_pos, half}) && t.first.dtype == DataType::BFloat16, "shape/dtype");
+    std::vector<uint16_t> wc((size_t)max_pos * half), ws(wc.size());
+    sai_or_rope_tables_bf16(max_pos, half, theta, wc.data(), ws.data());
+    auto gc = must(t.first.to_host(), "cos"), gs = must(t.second.to_host(), "sin");
+    REQUIRE(gc.size() == wc.size() * 2 && std::memcmp(gc.data(), wc.data(), gc.size()) == 0,
+            "cos table %dx%d differs from the oracle", max_pos, half);
+    REQUIRE(std::memcmp(gs.data(), ws.data(), gs.size()) == 0, "sin table %dx%d differs", max_pos, half);
+  }
+}
+
 // appends into a logical cache and attends over its dequantised contents.
 static void session(KvQuant quant, bool bf16, int B, int Hq, int Hkv, int D, int prefill,
                     int steps, unsigned seed) {
@@ -575,6 +876,9 @@ int main(int argc, char** argv) {
       {"gpu_gqa_first_token_no_history", true, gpu_gqa_first_token_no_history},
       {"gpu_dispatch_errors", true, gpu_dispatch_errors},
       {"gpu_dispatch_rope_tables", true, gpu_dispatch_rope_tables},
+      {"gpu_rotary_cpu_op_kats", true, gpu_rotary_cpu_op_kats},
+      {"gpu_rotary_dispatch", true, gpu_rotary_dispatch},
+      {"gpu_rope_tables", true, gpu_rope_tables},
       {"gpu_session_int8_prefill_decode", true, gpu_session_int8_prefill_decode},
       {"gpu_session_int8_bf16_d64", true, gpu_session_int8_bf16_d64},
       {"gpu_session_int4_decode", true, gpu_session_int4_decode},
