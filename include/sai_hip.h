@@ -114,6 +114,12 @@ sai_status sai_kvcache_set_seq_lens(sai_ctx* ctx, sai_kvcache* cache, const int3
  * length grows by the pending count. Stream-ordered. Replaces
  * GpuKvCache::advance_position (kv_cache.rs:295-304). */
 sai_status sai_kvcache_advance(sai_ctx* ctx, sai_kvcache* cache, void* stream);
+/* Layer kind (LayerKind, kv_cache.rs:53-60): window > 0 makes `layer` a
+ * sliding-window layer whose queries see only their last `window` keys
+ * (GpuKvCache::view_at, kv_cache.rs:340-360); 0 = global (the default). The
+ * pages keep every token; only attention is limited. Host-side. */
+sai_status sai_kvcache_set_layer_window(sai_ctx* ctx, sai_kvcache* cache, int32_t layer,
+                                        int32_t window);
 /* All lengths back to 0, buffers kept (GpuKvCache::reset, kv_cache.rs:386-388). */
 sai_status sai_kvcache_reset(sai_ctx* ctx, sai_kvcache* cache);
 /* Host view of the lengths: seq_lens_out[batch] (committed), *pending_out. */
@@ -157,12 +163,16 @@ sai_status sai_kv_append(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const 
  * kh = qh / (Hq/Hkv). Requires pending == 1.
  * q: device [batch, 1, num_heads*D] of `dtype` (F32 or BF16);
  * out: device [batch, 1, num_heads*D] f32. scale: used when has_scale != 0,
- * else sai_default_scale(D). */
+ * else sai_default_scale(D).
+ * window: gpu_gqa_with_cache's `window` (the node's local_window_size when
+ * > 0): the query at position p sees keys [p - window, p]; <= 0 = off. A
+ * sliding-window layer (sai_kvcache_set_layer_window) sees its last w keys;
+ * with both, the narrower span applies. */
 sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
                           int32_t dtype, int32_t batch, int32_t num_heads,
                           const float* cos_cache, const float* sin_cache, int32_t cache_rows,
                           int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
-                          float scale, float* out, void* stream);
+                          float scale, int32_t window, float* out, void* stream);
 
 /* ---- kernels 1 + 2 fused: one decode step in one launch ----------------------
  * Replaces gpu_gqa_with_cache (onnx-rt/src/cuda/kernels/attention.rs:1260-1295),
@@ -177,19 +187,21 @@ sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, c
                               int32_t kv_dtype, int32_t batch, int32_t num_heads,
                               const float* cos_cache, const float* sin_cache, int32_t cache_rows,
                               int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
-                              float scale, float* out, void* stream);
+                              float scale, int32_t window, float* out, void* stream);
 
 /* ---- kernel 3: prefill chunk (f16 MFMA) ---------------------------------------
  * Same contract as sai_gqa_decode for a chunk of sq == pending query tokens per
  * sequence (the reference's op_group_query_attention with Sq > 1, causal with
  * past_sk = seq_len[b], microsoft.rs:1156 and :331-337), over an int8 or int4
  * cache (head_dim 64 or 128).
- * q: device [batch, sq, num_heads*D]; out: device [batch, sq, num_heads*D] f32. */
+ * q: device [batch, sq, num_heads*D]; out: device [batch, sq, num_heads*D] f32.
+ * window and sliding-window layers as for sai_gqa_decode, applied to every
+ * query row at its own position (gpu_gqa's mask, attention.rs:79, :111). */
 sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
                            int32_t dtype, int32_t batch, int32_t sq, int32_t num_heads,
                            const float* cos_cache, const float* sin_cache, int32_t cache_rows,
                            int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
-                           float scale, float* out, void* stream);
+                           float scale, int32_t window, float* out, void* stream);
 
 /* ---- standalone rotary embedding ----------------------------------------------
  * Replaces op_rotary_embedding (onnx-rt/src/ops/microsoft.rs:556-652, through

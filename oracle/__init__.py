@@ -78,6 +78,9 @@ def _declare(L: C.CDLL) -> None:
         "sai_or_kv_dequant": (_i, [_i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
         "sai_or_gqa_cached": (_i, [_p, _i, _i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _i, _i, _i,
                                    _i, _f, _p]),
+        "sai_or_gqa_cached_window": (_i, [_p, _i, _i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _i, _i,
+                                          _i, _i, _f, _i, _i, _p]),
+        "sai_or_sdpa_window": (_i, [_p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _i, _i, _p]),
         "sai_or_check_rhe_vs_rint": (C.c_uint64, [C.c_uint64, C.c_uint64]),
         "sai_or_ln_approx": (_f, [_f]),
         "sai_or_exp_approx": (_f, [_f]),
@@ -201,6 +204,19 @@ def apply_rope(x, cos, sin, position_ids, interleaved=False, rotary_dim=None):
                                  d if rotary_dim is None else rotary_dim)
     _check(rc, "apply_rope")
     return x
+
+
+def sdpa_window(q, k, v, num_kv_heads, past_sk, scale, layer_window=0, mask_window=0):
+    """Causal SDPA with the reference's window rules; q [B,Hq,Sq,D], k/v [B,Hk,Sk,D]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    b, hq, sq, d = q.shape
+    sk = k.shape[2]
+    out = np.zeros_like(q)
+    rc = lib().sai_or_sdpa_window(_ptr(q), _ptr(k), _ptr(v), b, hq, num_kv_heads, sq, sk, d,
+                                  past_sk, float(scale), int(layer_window), int(mask_window),
+                                  _ptr(out))
+    _check(rc, "sdpa_window")
+    return out
 
 
 def sdpa(q, k, v, num_kv_heads, past_sk, scale, causal):
@@ -333,9 +349,11 @@ class LogicalCache:
         return kd, vd
 
     def attend(self, query, num_heads, cos=None, sin=None, do_rotary=True, interleaved=False,
-               scale=None, deq=None):
+               scale=None, deq=None, layer_window=0, mask_window=0):
         """query [B, Sq, Hq*D] (pre-RoPE) over the cache; the last Sq tokens of each
-        sequence are the query positions. Returns [B, Sq, Hq*D] f32."""
+        sequence are the query positions. layer_window: a sliding-window cache
+        layer's last keys; mask_window: the GPU mask's window (<= 0: off).
+        Returns [B, Sq, Hq*D] f32."""
         q = _f32(query)
         b, sq, _ = q.shape
         kd, vd = self.dequant() if deq is None else deq
@@ -344,11 +362,11 @@ class LogicalCache:
         cosa = None if cos is None else _f32(cos)
         sina = None if sin is None else _f32(sin)
         rows = 0 if cosa is None else cosa.shape[0]
-        rc = lib().sai_or_gqa_cached(_ptr(q), b, sq, num_heads, self.kv_heads, self.head_dim,
-                                     _ptr(sl), self.t_cap, _ptr(kd), _ptr(vd), _ptr(cosa),
-                                     _ptr(sina), rows, int(do_rotary), int(interleaved),
-                                     int(scale is not None),
-                                     0.0 if scale is None else float(scale), _ptr(out))
+        rc = lib().sai_or_gqa_cached_window(
+            _ptr(q), b, sq, num_heads, self.kv_heads, self.head_dim, _ptr(sl), self.t_cap,
+            _ptr(kd), _ptr(vd), _ptr(cosa), _ptr(sina), rows, int(do_rotary), int(interleaved),
+            int(scale is not None), 0.0 if scale is None else float(scale), int(layer_window),
+            int(mask_window), _ptr(out))
         _check(rc, "gqa_cached")
         return out
 

@@ -348,9 +348,25 @@ int sai_or_apply_rope(float* x, int b, int heads, int sq, int head_dim, const fl
  * sdpa_max_k (:331-337), sdpa_row (:341-359).
  * q [B,Hq,Sq,D], k/v [B,Hk,Sk,D], out [B,Hq,Sq,D].
  * ---------------------------------------------------------------------- */
-int sai_or_sdpa(const float* q, const float* k, const float* v, int batch, int num_q_heads,
-                int num_kv_heads, int sq, int sk, int head_dim, int past_sk, float scale,
-                int causal, float* out) {
+/* Key visibility with the reference's two window rules, for the query at
+ * absolute position q_pos (query qi of a chunk after past_sk cached keys):
+ *  - the GPU mask (gqa_softmax_mask_f32, cuda/kernels/attention.rs:79, :111):
+ *    keys k < q_pos - mask_window are hidden when mask_window > 0;
+ *  - a sliding-window cache layer (GpuKvCache::view_at, cuda/kv_cache.rs:
+ *    340-360): the view holds the last layer_window keys, k >= q_pos + 1 -
+ *    layer_window, when layer_window > 0 (for a chunk of several queries each
+ *    query's own last layer_window keys).
+ * Returns the first visible key. */
+static int first_visible_key(int q_pos, int layer_window, int mask_window) {
+  int lo = 0;
+  if (mask_window > 0 && q_pos - mask_window > lo) lo = q_pos - mask_window;
+  if (layer_window > 0 && q_pos + 1 - layer_window > lo) lo = q_pos + 1 - layer_window;
+  return lo;
+}
+
+static int sdpa_impl(const float* q, const float* k, const float* v, int batch, int num_q_heads,
+                     int num_kv_heads, int sq, int sk, int head_dim, int past_sk, float scale,
+                     int causal, int layer_window, int mask_window, float* out) {
   if (num_q_heads == 0 || num_kv_heads == 0 || head_dim == 0) return ERR_SHAPE_MISMATCH;
   if (num_q_heads % num_kv_heads != 0) return ERR_SHAPE_MISMATCH;
   int group = num_q_heads / num_kv_heads;
@@ -370,9 +386,10 @@ int sai_or_sdpa(const float* q, const float* k, const float* v, int batch, int n
       for (int qi = 0; qi < sq; ++qi) {
         size_t q_row = q_base + (size_t)qi * head_dim;
         int max_k = causal ? ((past_sk + qi + 1) < sk ? (past_sk + qi + 1) : sk) : sk;
+        int min_k = first_visible_key(past_sk + qi, layer_window, mask_window);
         /* scores */
         for (int ki = 0; ki < sk; ++ki) {
-          if (ki >= max_k) {
+          if (ki >= max_k || ki < min_k) {
             scores[ki] = -INFINITY;
             continue;
           }
@@ -412,6 +429,20 @@ int sai_or_sdpa(const float* q, const float* k, const float* v, int batch, int n
   }
   free(scores);
   return OK;
+}
+
+int sai_or_sdpa(const float* q, const float* k, const float* v, int batch, int num_q_heads,
+                int num_kv_heads, int sq, int sk, int head_dim, int past_sk, float scale,
+                int causal, float* out) {
+  return sdpa_impl(q, k, v, batch, num_q_heads, num_kv_heads, sq, sk, head_dim, past_sk, scale,
+                   causal, 0, 0, out);
+}
+
+int sai_or_sdpa_window(const float* q, const float* k, const float* v, int batch,
+                       int num_q_heads, int num_kv_heads, int sq, int sk, int head_dim,
+                       int past_sk, float scale, int layer_window, int mask_window, float* out) {
+  return sdpa_impl(q, k, v, batch, num_q_heads, num_kv_heads, sq, sk, head_dim, past_sk, scale, 1,
+                   layer_window, mask_window, out);
 }
 
 /* reshape_to_bhsd / reshape_from_bhsd -- microsoft.rs:660-704. */
@@ -678,6 +709,16 @@ int sai_or_gqa_cached(const float* query, int b, int sq, int num_heads, int kv_h
                       const float* v_deq, const float* cos_cache, const float* sin_cache,
                       int cache_rows, int do_rotary, int interleaved, int has_scale,
                       float scale_attr, float* out) {
+  return sai_or_gqa_cached_window(query, b, sq, num_heads, kv_heads, head_dim, seq_len, t_cap,
+                                  k_deq, v_deq, cos_cache, sin_cache, cache_rows, do_rotary,
+                                  interleaved, has_scale, scale_attr, 0, 0, out);
+}
+
+int sai_or_gqa_cached_window(const float* query, int b, int sq, int num_heads, int kv_heads,
+                             int head_dim, const int32_t* seq_len, int t_cap, const float* k_deq,
+                             const float* v_deq, const float* cos_cache, const float* sin_cache,
+                             int cache_rows, int do_rotary, int interleaved, int has_scale,
+                             float scale_attr, int layer_window, int mask_window, float* out) {
   if (num_heads <= 0 || kv_heads <= 0 || num_heads % kv_heads != 0) return ERR_INVALID_ATTRIBUTE;
   if (do_rotary && (cos_cache == NULL || sin_cache == NULL)) return ERR_SHAPE_MISMATCH;
   float scale = has_scale ? scale_attr : sai_or_default_scale(head_dim);
@@ -711,8 +752,8 @@ int sai_or_gqa_cached(const float* query, int b, int sq, int num_heads, int kv_h
       memcpy(kf + (size_t)h * total * head_dim, k_deq + src, sizeof(float) * (size_t)total * head_dim);
       memcpy(vf + (size_t)h * total * head_dim, v_deq + src, sizeof(float) * (size_t)total * head_dim);
     }
-    rc = sai_or_sdpa(q_bhsd, kf, vf, 1, num_heads, kv_heads, sq, total, head_dim, past, scale, 1,
-                     o_bhsd);
+    rc = sdpa_impl(q_bhsd, kf, vf, 1, num_heads, kv_heads, sq, total, head_dim, past, scale, 1,
+                   layer_window, mask_window, o_bhsd);
     free(kf);
     free(vf);
     if (rc == OK) reshape_from_bhsd(o_bhsd, 1, num_heads, sq, head_dim, out + (size_t)bi * sq * qrow);

@@ -72,6 +72,11 @@ int sai_or_apply_rope(float* x, int b, int heads, int sq, int head_dim, const fl
 int sai_or_sdpa(const float* q, const float* k, const float* v, int batch, int num_q_heads,
                 int num_kv_heads, int sq, int sk, int head_dim, int past_sk, float scale,
                 int causal, float* out);
+/* Causal SDPA with the reference's window rules (layer_window: last keys of a
+ * sliding-window cache layer; mask_window: the GPU mask's window); <= 0 = off. */
+int sai_or_sdpa_window(const float* q, const float* k, const float* v, int batch,
+                       int num_q_heads, int num_kv_heads, int sq, int sk, int head_dim,
+                       int past_sk, float scale, int layer_window, int mask_window, float* out);
 
 /* op_group_query_attention. past_k/past_v may be NULL (past_sk must then be 0).
  * scale_attr: used when has_scale != 0. Outputs: attn [B,Sq,Hq*D],
@@ -120,6 +125,11 @@ int sai_or_gqa_cached(const float* query, int b, int sq, int num_heads, int kv_h
                       const float* v_deq, const float* cos_cache, const float* sin_cache,
                       int cache_rows, int do_rotary, int interleaved, int has_scale,
                       float scale_attr, float* out);
+int sai_or_gqa_cached_window(const float* query, int b, int sq, int num_heads, int kv_heads,
+                             int head_dim, const int32_t* seq_len, int t_cap, const float* k_deq,
+                             const float* v_deq, const float* cos_cache, const float* sin_cache,
+                             int cache_rows, int do_rotary, int interleaved, int has_scale,
+                             float scale_attr, int layer_window, int mask_window, float* out);
 
 /* Exhaustive check that the int8 code rule built on round_half_even equals
  * the same rule built on IEEE roundTiesToEven (rintf) for every f32 bit

@@ -72,6 +72,7 @@ EXPORTS = [
     "sai_kvcache_create", "sai_kvcache_destroy", "sai_kvcache_set_page_table",
     "sai_kvcache_set_seq_lens", "sai_kvcache_advance", "sai_kvcache_reset",
     "sai_kvcache_lengths", "sai_kvcache_read", "sai_kvcache_pool", "sai_kv_append",
+    "sai_kvcache_set_layer_window",
     "sai_gqa_decode", "sai_gqa_with_cache", "sai_gqa_prefill", "sai_set_decode_split",
     "sai_set_decode_waves", "sai_set_decode_merge", "sai_last_decode_shape",
     "sai_set_decode_timing", "sai_decode_kernel_times", "sai_rotary_embedding",
@@ -100,12 +101,13 @@ def _declare(L: C.CDLL) -> None:
         "sai_kvcache_read": (i32, [p, p, i32, i32, i32, i32, i32, p, p, p, p]),
         "sai_kvcache_pool": (i32, [p, i32, pp, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
         "sai_kv_append": (i32, [p, p, i32, p, p, i32, i32, i32, p, p, i32, i32, i32, p]),
-        "sai_gqa_decode": (i32, [p, p, i32, p, i32, i32, i32, p, p, i32, i32, i32, i32, f, p,
-                                 p]),
+        "sai_gqa_decode": (i32, [p, p, i32, p, i32, i32, i32, p, p, i32, i32, i32, i32, f, i32,
+                                 p, p]),
         "sai_gqa_with_cache": (i32, [p, p, i32, p, i32, p, p, i32, i32, i32, p, p, i32, i32,
-                                     i32, i32, f, p, p]),
+                                     i32, i32, f, i32, p, p]),
         "sai_gqa_prefill": (i32, [p, p, i32, p, i32, i32, i32, i32, p, p, i32, i32, i32, i32,
-                                  f, p, p]),
+                                  f, i32, p, p]),
+        "sai_kvcache_set_layer_window": (i32, [p, p, i32, i32]),
         "sai_set_decode_split": (i32, [p, i32]),
         "sai_set_decode_waves": (i32, [p, i32]),
         "sai_set_decode_merge": (i32, [p, i32]),
@@ -301,6 +303,11 @@ class KvCache:
     def reset(self):
         self.rt.check(self._L.sai_kvcache_reset(self.rt.handle, self.handle), "reset")
 
+    def set_layer_window(self, layer: int, window: int):
+        """Sliding-window layer: its queries see their last `window` keys (0: global)."""
+        self.rt.check(self._L.sai_kvcache_set_layer_window(self.rt.handle, self.handle, layer,
+                                                           int(window)), "set_layer_window")
+
     def lengths(self):
         b = C.c_int32()
         pend = C.c_int32()
@@ -346,17 +353,18 @@ class KvCache:
             _stream(stream)), "kv_append")
 
     def decode(self, layer, q, out, batch, num_heads, cos=None, sin=None, cache_rows=0,
-               do_rotary=True, interleaved=False, scale=None, stream=None, dtype=None):
+               do_rotary=True, interleaved=False, scale=None, stream=None, dtype=None, window=0):
+        """window: the node's local_window_size (> 0: keys [p - window, p])."""
         dt = dtype if dtype is not None else _dtype_code(q)
         self.rt.check(self._L.sai_gqa_decode(
             self.rt.handle, self.handle, layer, _dev_ptr(q), dt, batch, num_heads, _dev_ptr(cos),
             _dev_ptr(sin), cache_rows, int(do_rotary), int(interleaved), int(scale is not None),
-            0.0 if scale is None else float(scale), _dev_ptr(out), _stream(stream)),
+            0.0 if scale is None else float(scale), int(window), _dev_ptr(out), _stream(stream)),
             "gqa_decode")
 
     def decode_with_cache(self, layer, q, k_new, v_new, out, batch, num_heads, cos=None,
                           sin=None, cache_rows=0, do_rotary=True, interleaved=False, scale=None,
-                          stream=None, q_dtype=None, kv_dtype=None):
+                          stream=None, q_dtype=None, kv_dtype=None, window=0):
         """Fused step: append the token (k_new/v_new [B,1,Hkv*D]) and attend."""
         qd = q_dtype if q_dtype is not None else _dtype_code(q)
         kd = kv_dtype if kv_dtype is not None else _dtype_code(k_new)
@@ -364,16 +372,16 @@ class KvCache:
             self.rt.handle, self.handle, layer, _dev_ptr(q), qd, _dev_ptr(k_new), _dev_ptr(v_new),
             kd, batch, num_heads, _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary),
             int(interleaved), int(scale is not None), 0.0 if scale is None else float(scale),
-            _dev_ptr(out), _stream(stream)), "gqa_with_cache")
+            int(window), _dev_ptr(out), _stream(stream)), "gqa_with_cache")
 
     def prefill(self, layer, q, out, batch, sq, num_heads, cos=None, sin=None, cache_rows=0,
-                do_rotary=True, interleaved=False, scale=None, stream=None, dtype=None):
+                do_rotary=True, interleaved=False, scale=None, stream=None, dtype=None, window=0):
         dt = dtype if dtype is not None else _dtype_code(q)
         self.rt.check(self._L.sai_gqa_prefill(
             self.rt.handle, self.handle, layer, _dev_ptr(q), dt, batch, sq, num_heads,
             _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary), int(interleaved),
-            int(scale is not None), 0.0 if scale is None else float(scale), _dev_ptr(out),
-            _stream(stream)), "gqa_prefill")
+            int(scale is not None), 0.0 if scale is None else float(scale), int(window),
+            _dev_ptr(out), _stream(stream)), "gqa_prefill")
 
 
 def identity_page_table(batch: int, pages_per_seq: int):

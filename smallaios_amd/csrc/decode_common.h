@@ -92,7 +92,7 @@ __device__ __forceinline__ void decode_work_item(const DecodeParams& p, int work
   for (int c0 = 0; c0 < p.batch; c0 += 64) {
     const int bi = c0 + lane;
     const int Lb = bi < p.batch ? p.seq_lens[bi] + p.pending : 0;
-    const int n = (Lb + p.split_tokens - 1) / p.split_tokens;
+    const int n = (Lb - window_origin(Lb, p.window) + p.split_tokens - 1) / p.split_tokens;
     int incl = n;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {

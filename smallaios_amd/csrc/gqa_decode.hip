@@ -89,8 +89,8 @@ struct WaveState {
 template <int D, int G>
 __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, G>& st,
                                              const v4i (&qB)[D / 64], float q_own, float q_oth,
-                                             int tok0, int t_end, bool is_hi, bool live, int g,
-                                             float* sm_sc) {
+                                             int tok0, int t_lo, int t_end, bool is_hi, bool live,
+                                             int g, float* sm_sc) {
   constexpr int KS = D / 64;
   constexpr int JB = D / 16;
   // QK^T on the matrix cores
@@ -115,8 +115,12 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, 
     skv[4 * w] = a.x, skv[4 * w + 1] = a.y, skv[4 * w + 2] = a.z, skv[4 * w + 3] = a.w;
     svv[4 * w] = c.x, svv[4 * w + 1] = c.y, svv[4 * w + 2] = c.z, svv[4 * w + 3] = c.w;
   }
-  const int nvalid = t_end - tok0;  // slots [0, nvalid) of page g are visible
-  const bool full = __builtin_amdgcn_readfirstlane(t_end - (tok0 - 16 * g) >= 64);
+  // slots [nlow, nvalid) of page g are visible: inside the split and at or
+  // after the first key of the window
+  const int nvalid = t_end - tok0;
+  const int nlow = t_lo - tok0;
+  const bool full =
+      __builtin_amdgcn_readfirstlane(t_end - (tok0 - 16 * g) >= 64 && tok0 - 16 * g >= t_lo);
   float s[16];
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk)
@@ -130,8 +134,9 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, 
   if (!full) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      s[i] = (i < nvalid) ? s[i] : -INFINITY;
-      svv[i] = (i < nvalid) ? svv[i] : 0.0f;
+      const bool vis = i < nvalid && i >= nlow;
+      s[i] = vis ? s[i] : -INFINITY;
+      svv[i] = vis ? svv[i] : 0.0f;
     }
   }
   float mt = s[0];
@@ -222,7 +227,10 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   // length first; then the page ids of the split and the query, in flight
   // across the barrier
   const int L = p.seq_lens[b] + p.pending;
-  const int first_page = split * (p.split_tokens / kPageTokens);
+  // sliding window: keys [k_lo, L) visible, splits from the tile holding k_lo
+  const int k_lo = window_first_key(L, p.window);
+  const int origin = (k_lo / 64) * 64;
+  const int first_page = origin / kPageTokens + split * (p.split_tokens / kPageTokens);
   __shared__ int sm_pg[kMaxSplitPages];
   const int split_pages = p.split_tokens / kPageTokens;
   for (int i = threadIdx.x; i < split_pages; i += 64 * NW)
@@ -238,7 +246,7 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   float xq[KS][16];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) load16(p.q, qbase + (D / 4) * g + 16 * ks, p.q_dtype, xq[ks]);
-  const int t_begin = split * p.split_tokens;
+  const int t_begin = origin + split * p.split_tokens;
   const int t_end = min(L, t_begin + p.split_tokens);
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
   const int n_tiles = (t_end - t_begin + 63) / 64;
@@ -393,16 +401,16 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   int k = 0;
   for (; k + 2 < my_tiles; k += 2) {
     ld(TB, k + 1);
-    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), t_end, is_hi, live, g, sm_sc[wave]);
+    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
     ld(TA, k + 2);
-    compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), t_end, is_hi, live, g, sm_sc[wave]);
+    compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
   }
   if (k + 1 < my_tiles) {  // two left
     ld(TB, k + 1);
-    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), t_end, is_hi, live, g, sm_sc[wave]);
-    compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), t_end, is_hi, live, g, sm_sc[wave]);
+    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+    compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
   } else if (k < my_tiles) {  // one left
-    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), t_end, is_hi, live, g, sm_sc[wave]);
+    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
   }
 
   // ---- merge the NW waves of the workgroup --------------------------------------

@@ -107,14 +107,15 @@ struct State4 {
 };
 
 // One 64-token tile: lane (r, g) owns page g of the tile (slots 0..15) for
-// column j = r. MASK: the tile crosses the end of the split (t_end).
+// column j = r. MASK: the tile crosses the end of the split (t_end) or the
+// first key of a sliding window (t_lo).
 template <int G, bool MASK>
 __device__ __forceinline__ void compute_tile4(const Tile4& T, State4<G>& st,
                                               const v8h (&Bh)[State4<G>::HT][kNG],
                                               const v8h (&Bl)[State4<G>::HT][kNG],
                                               const float (&qsn)[State4<G>::HT],
                                               const float (&q_scale)[State4<G>::HT], int tok0,
-                                              int t_end, int r, int g, uint4* sm_p) {
+                                              int t_lo, int t_end, int r, int g, uint4* sm_p) {
   constexpr int HT = State4<G>::HT;
   const int lane = threadIdx.x & 63;
   const int gp = r & 3;
@@ -142,7 +143,9 @@ __device__ __forceinline__ void compute_tile4(const Tile4& T, State4<G>& st,
       cs[qd][blk] = acc;
     }
   }
+  // MASK: slots [nlow, nvalid) of page g are visible (split end, window start)
   const int nvalid = t_end - tok0;
+  const int nlow = t_lo - tok0;
   // u = sum_G' (s_G' * dot_G' + z_G' * qsn); score (log2) = q_scale * u
   float u[HT][16];
 #pragma unroll
@@ -159,7 +162,7 @@ __device__ __forceinline__ void compute_tile4(const Tile4& T, State4<G>& st,
 #pragma unroll
     for (int qd = 0; qd < HT; ++qd)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) u[qd][i] = (i < nvalid) ? u[qd][i] : -INFINITY;
+      for (int i = 0; i < 16; ++i) u[qd][i] = (i < nvalid && i >= nlow) ? u[qd][i] : -INFINITY;
   }
   // p of even slots; odd slots hold p / 16 (their V codes carry 2^-20)
   float p[HT][16];
@@ -205,8 +208,8 @@ __device__ __forceinline__ void compute_tile4(const Tile4& T, State4<G>& st,
         float z = p[qd][slot] * (float)sz[1];
         if (MASK) {
           // masked slots may hold stale parameters: select, do not multiply
-          a = (slot < nvalid) ? a : 0.0f;
-          z = (slot < nvalid) ? z : 0.0f;
+          a = (slot < nvalid && slot >= nlow) ? a : 0.0f;
+          z = (slot < nvalid && slot >= nlow) ? z : 0.0f;
         }
         pa[qd][half][i] = (_Float16)a;
         if (slot & 1)
@@ -263,7 +266,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   // of the first tile
   const int L = p.seq_lens[b] + p.pending;
   const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
-  const int first_page = split * (p.split_tokens / kPageTokens);
+  // sliding window: keys [k_lo, L) visible, splits from the tile holding k_lo
+  const int k_lo = window_first_key(L, p.window);
+  const int origin = (k_lo / 64) * 64;
+  const int first_page = origin / kPageTokens + split * (p.split_tokens / kPageTokens);
   __shared__ int sm_pg[kMaxSplitPages];
   const int split_pages = p.split_tokens / kPageTokens;
   for (int i = threadIdx.x; i < split_pages; i += 64 * NW)
@@ -305,7 +311,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
     }
   }
 
-  const int t_begin = split * p.split_tokens;
+  const int t_begin = origin + split * p.split_tokens;
   const int t_end = min(L, t_begin + p.split_tokens);
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
   const int n_tiles = (t_end - t_begin + 63) / 64;
@@ -417,20 +423,34 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   auto run = [&](const Tile4& T, int k) {
     const bool partial = last_partial && wave + k * NW == n_tiles - 1;
     if (__builtin_amdgcn_readfirstlane(partial))
-      compute_tile4<G, true>(T, st, Bh, Bl, qsn, q_scale, tok0(k), t_end, r, g, sm_par[wave]);
+      compute_tile4<G, true>(T, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
     else
-      compute_tile4<G, false>(T, st, Bh, Bl, qsn, q_scale, tok0(k), t_end, r, g, sm_par[wave]);
+      compute_tile4<G, false>(T, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
   };
   int k = 0;
+  // the window's first key inside the split's first tile (wave 0's tile 0):
+  // that tile runs the masked path, and its successor moves into TA so the
+  // ping-pong below starts at k = 1
+  if (wave == 0 && k_lo > t_begin) {  // uniform over the wave
+    if (my_tiles > 1) {
+      ld(TB, 1);
+      compute_tile4<G, true>(TA, st, Bh, Bl, qsn, q_scale, tok0(0), k_lo, t_end, r, g, sm_par[wave]);
+      TA = TB;
+      k = 1;
+    } else {
+      compute_tile4<G, true>(TA, st, Bh, Bl, qsn, q_scale, tok0(0), k_lo, t_end, r, g, sm_par[wave]);
+      k = 1;
+    }
+  }
   for (; k + 2 < my_tiles; k += 2) {
     ld(TB, k + 1);
-    compute_tile4<G, false>(TA, st, Bh, Bl, qsn, q_scale, tok0(k), t_end, r, g, sm_par[wave]);
+    compute_tile4<G, false>(TA, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
     ld(TA, k + 2);
-    compute_tile4<G, false>(TB, st, Bh, Bl, qsn, q_scale, tok0(k + 1), t_end, r, g, sm_par[wave]);
+    compute_tile4<G, false>(TB, st, Bh, Bl, qsn, q_scale, tok0(k + 1), k_lo, t_end, r, g, sm_par[wave]);
   }
   if (k + 1 < my_tiles) {
     ld(TB, k + 1);
-    compute_tile4<G, false>(TA, st, Bh, Bl, qsn, q_scale, tok0(k), t_end, r, g, sm_par[wave]);
+    compute_tile4<G, false>(TA, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
     run(TB, k + 1);
   } else if (k < my_tiles) {
     run(TA, k);

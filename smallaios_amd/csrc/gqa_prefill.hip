@@ -21,7 +21,8 @@
 //   PV       A = P * s_v (f16), B = V (LDS f16); each V fragment serves both
 //            row blocks.
 // Scores: s = <q', k> * s_k[t], online softmax in the log2 domain. Only tiles
-// that cross the causal diagonal (or the end of the sequence) apply the mask;
+// that cross the causal diagonal (or the end of the sequence), or the first
+// key of a sliding window, apply the mask;
 // the accumulator rescale is skipped when no row maximum moved.
 #include <type_traits>
 
@@ -335,6 +336,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   // tiles entirely at or below the smallest position of the workgroup need
   // no causal mask (they are also inside the sequence)
   const int full_tiles = (past + q0 + 1) / 64;
+  // sliding window (W keys per row, W > 0): the rows see keys from
+  // past + q0 - W + 1 on, so earlier tiles are skipped; tiles before lo_full
+  // hold keys that some row of the workgroup does not see
+  const int W = p.window;
+  const int tile_lo = W > 0 ? max(0, past + q0 - W + 1) / 64 : 0;
+  const int lo_full = W > 0 ? (max(0, max_pos - W + 1) + 63) / 64 : 0;
 
   // first tile in flight while Q is prepared
   typedef typename std::conditional<INT4, TileStage4<D, NT>, TileStage<D, NT>>::type Stage;
@@ -351,7 +358,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
     else
       stage_store<D, NT>(S, T, tid);
   };
-  load_stage(0);
+  load_stage(tile_lo * 64);
 
   // ---- Q^T operand: rows R = wave*32 + rb*16 + r -> (position, head) -------
   // RoPE(q) * scale * log2(e) as an f16 pair hi + lo (~22 bits: a score's
@@ -406,7 +413,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       }
   }
 
-  store_stage(sT[0], 0);
+  store_stage(sT[tile_lo & 1], tile_lo * 64);
   __syncthreads();
 
   // ---- online softmax state ----------------------------------------------------
@@ -418,7 +425,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 #pragma unroll
     for (int jb = 0; jb < JB; ++jb) acc[rb][jb] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int tile = 0; tile < n_tiles; ++tile) {
+  for (int tile = tile_lo; tile < n_tiles; ++tile) {
     const int t0 = tile * 64;
     const Tile& T = sT[tile & 1];
     const bool more = tile + 1 < n_tiles;
@@ -471,7 +478,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
           for (int e = 0; e < 4; ++e) s[rb][cb][e] = INT4 ? c[cb][rb][e] : c[cb][rb][e] * skx[e];
       }
     }
-    if (tile >= full_tiles) {
+    if (tile >= full_tiles || tile < lo_full) {
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -479,7 +486,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int t = t0 + 16 * cb + 4 * g + e;
-            s[rb][cb][e] = t <= qpos[rb] ? s[rb][cb][e] : -INFINITY;
+            const bool vis = t <= qpos[rb] && (W <= 0 || t > qpos[rb] - W);
+            s[rb][cb][e] = vis ? s[rb][cb][e] : -INFINITY;
           }
     }
 

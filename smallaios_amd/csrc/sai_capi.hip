@@ -52,6 +52,7 @@ struct sai_kvcache {
   std::vector<int32_t> h_seq_lens;    // committed
   int32_t batch = 0;
   int32_t pending = 0;
+  std::vector<int32_t> layer_window;  // per layer: last keys visible (0: global)
 };
 
 namespace {
@@ -139,6 +140,19 @@ sai_status check_rope(sai_ctx* ctx, const sai_kvcache* c, int32_t batch, int32_t
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: position %d out of cache range %d", op,
                 maxlen - 1, cache_rows);
   return SAI_OK;
+}
+
+// Keys visible to a query (0: all): the cache layer's window keeps the last
+// layer_window keys (GpuKvCache::view_at, kv_cache.rs:340-360); the node's
+// window hides keys before q_pos - window, which leaves window + 1
+// (gqa_softmax_mask_f32, cuda/kernels/attention.rs:79). Both: the narrower.
+int32_t visible_span(int32_t layer_window, int32_t window) {
+  int64_t w = layer_window > 0 ? layer_window : 0;
+  if (window > 0) {
+    const int64_t m = (int64_t)window + 1;
+    if (w == 0 || m < w) w = m;
+  }
+  return (int32_t)std::min<int64_t>(w, 0x7FFFFFFF);
 }
 
 sai_status ensure_workspace(sai_ctx* ctx, size_t partial_floats, size_t seq_info,
@@ -324,7 +338,20 @@ SAI_API sai_status sai_kvcache_create(sai_ctx* ctx, const sai_kvcache_desc* desc
   c->h_page_table.assign(pt_n, -1);
   c->h_mapped.assign(d.max_batch, 0);
   c->h_seq_lens.assign(d.max_batch, 0);
+  c->layer_window.assign(d.num_layers, 0);
   *out = c;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_kvcache_set_layer_window(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
+                                                int32_t window) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  if (layer < 0 || layer >= c->desc.num_layers)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "kv_cache_set_layer_window: layer_idx %d", layer);
+  if (window < 0)
+    return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE, "kv_cache_set_layer_window: window %d < 0",
+                window);
+  c->layer_window[layer] = window;
   return SAI_OK;
 }
 
@@ -585,9 +612,11 @@ namespace {
 sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
                          int32_t dtype, int32_t batch, int32_t G, const float* cos_cache,
                          const float* sin_cache, int32_t cache_rows, int32_t do_rotary,
-                         int32_t rotary_interleaved, int32_t has_scale, float scale, float* out,
-                         const void* k_new, const void* v_new, int32_t kv_dtype, void* stream) {
+                         int32_t rotary_interleaved, int32_t has_scale, float scale,
+                         int32_t window, float* out, const void* k_new, const void* v_new,
+                         int32_t kv_dtype, void* stream) {
   const char* op = "gqa_decode";
+  const int32_t W = visible_span(c->layer_window[layer], window);
   const int D = c->desc.head_dim;
   if (c->desc.quant == SAI_KV_INT4 && D != 128)
     return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: int4 decode needs head_dim 128 (got %d)", op, D);
@@ -597,11 +626,16 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   // (each streams one contiguous range; measured best at 16 x 8k). Ragged
   // lengths: cap the split so the longest sequences are cut into pieces that
   // balance across the CUs.
+  // streamed tokens of sequence b: from the tile of its first visible key
+  auto streamed = [&](int b) {
+    const int L = c->h_seq_lens[b] + 1;
+    return (int64_t)(L - sai::window_origin(L, W));
+  };
   int64_t tok_heads = 0;
   int64_t max_len = 0;
   for (int b = 0; b < batch; ++b) {
-    tok_heads += (int64_t)(c->h_seq_lens[b] + 1) * kvh;
-    max_len = std::max<int64_t>(max_len, c->h_seq_lens[b] + 1);
+    tok_heads += streamed(b) * kvh;
+    max_len = std::max<int64_t>(max_len, streamed(b));
   }
   int32_t split = ctx->decode_split;
   if (split <= 0) {
@@ -617,7 +651,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   int64_t n_first = -1, n_max = 0;
   bool uniform = true;
   for (int b = 0; b < batch; ++b) {
-    const int64_t n = (c->h_seq_lens[b] + 1 + split - 1) / split;
+    const int64_t n = (streamed(b) + split - 1) / split;
     work += n;
     multi = multi || n > 1;
     if (n_first < 0) n_first = n;
@@ -662,6 +696,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   p.k_new = k_new;
   p.v_new = v_new;
   p.kv_dtype = kv_dtype;
+  p.window = W;
   const hipStream_t hs = (hipStream_t)stream;
   const int64_t slots = (int64_t)ctx->ev_start.size();
   const int64_t slot = slots ? ctx->timed_calls % slots : 0;
@@ -694,15 +729,15 @@ SAI_API sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, c
                                   const float* cos_cache, const float* sin_cache,
                                   int32_t cache_rows, int32_t do_rotary,
                                   int32_t rotary_interleaved, int32_t has_scale, float scale,
-                                  float* out, void* stream) {
+                                  int32_t window, float* out, void* stream) {
   if (!ctx || !c) return SAI_ERR_NULL;
   int32_t G = 0;
   sai_status st = attention_common(ctx, c, layer, q, dtype, batch, 1, num_heads, cos_cache,
                                    sin_cache, cache_rows, do_rotary, out, "gqa_decode", &G);
   if (st != SAI_OK) return st;
   return launch_decode(ctx, c, layer, q, dtype, batch, G, cos_cache, sin_cache, cache_rows,
-                       do_rotary, rotary_interleaved, has_scale, scale, out, nullptr, nullptr,
-                       SAI_DTYPE_F32, stream);
+                       do_rotary, rotary_interleaved, has_scale, scale, window, out, nullptr,
+                       nullptr, SAI_DTYPE_F32, stream);
 }
 
 SAI_API sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
@@ -711,7 +746,8 @@ SAI_API sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* c, int32_t laye
                                       int32_t num_heads, const float* cos_cache,
                                       const float* sin_cache, int32_t cache_rows,
                                       int32_t do_rotary, int32_t rotary_interleaved,
-                                      int32_t has_scale, float scale, float* out, void* stream) {
+                                      int32_t has_scale, float scale, int32_t window, float* out,
+                                      void* stream) {
   if (!ctx || !c) return SAI_ERR_NULL;
   const char* op = "gqa_with_cache";
   if (!k_new || !v_new) return fail(ctx, SAI_ERR_NULL, "%s: missing key/value", op);
@@ -728,8 +764,8 @@ SAI_API sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* c, int32_t laye
                                    sin_cache, cache_rows, do_rotary, out, op, &G);
   if (st == SAI_OK)
     st = launch_decode(ctx, c, layer, q, q_dtype, batch, G, cos_cache, sin_cache, cache_rows,
-                       do_rotary, rotary_interleaved, has_scale, scale, out, k_new, v_new,
-                       kv_dtype, stream);
+                       do_rotary, rotary_interleaved, has_scale, scale, window, out, k_new,
+                       v_new, kv_dtype, stream);
   if (st != SAI_OK) c->pending = prev_pending;
   return st;
 }
@@ -739,7 +775,7 @@ SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, 
                                    const float* cos_cache, const float* sin_cache,
                                    int32_t cache_rows, int32_t do_rotary,
                                    int32_t rotary_interleaved, int32_t has_scale, float scale,
-                                   float* out, void* stream) {
+                                   int32_t window, float* out, void* stream) {
   if (!ctx || !c) return SAI_ERR_NULL;
   const char* op = "gqa_prefill";
   if (sq <= 0) return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: sq must be > 0", op);
@@ -768,6 +804,7 @@ SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, 
   p.interleaved = rotary_interleaved ? 1 : 0;
   const float sc = has_scale ? scale : sai_default_scale(D);
   p.scale_log2 = sc * 1.4426950408889634f;
+  p.window = visible_span(c->layer_window[layer], window);
   hipError_t e = sai::launch_gqa_prefill(p, D, G, c->desc.quant, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gqa_prefill launch");
   return SAI_OK;

@@ -130,6 +130,7 @@ struct DecodeParams {
   const void* k_new;    // fused append: [batch, 1, Hkv*D] pre-RoPE K, or null
   const void* v_new;
   int kv_dtype;
+  int window;           // visible keys per query (0: all); see window_first_key
 };
 
 struct PrefillParams {
@@ -147,7 +148,14 @@ struct PrefillParams {
   const float* sin_cache;
   int cache_rows, do_rotary, interleaved;
   float scale_log2;
+  int window;  // visible keys per query (0: all)
 };
+
+// Sliding windows: a query at position L-1 sees keys [L - W, L-1] (W > 0)
+// or all keys (W == 0). The decode splits of a sequence start at the tile
+// (64 tokens) holding its first visible key.
+__host__ __device__ inline int window_first_key(int L, int W) { return W > 0 && L > W ? L - W : 0; }
+__host__ __device__ inline int window_origin(int L, int W) { return (window_first_key(L, W) / 64) * 64; }
 
 // Positions carried by one rotary launch (kernel argument block).
 constexpr int kRotaryTab = 512;

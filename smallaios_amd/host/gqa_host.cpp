@@ -291,7 +291,9 @@ Result<GpuKvCache, HipError> GpuKvCache::allocate(RocmRuntime& rt, size_t num_la
   if (num_layers == 0 || num_kv_heads == 0 || head_dim == 0 || max_seq_len == 0 || max_batch == 0)
     return HipError::runtime("kv_cache_allocate:zero_dim");
   for (const LayerKind& k : layer_kinds)
-    if (k.tag != LayerKind::Tag::Global) return HipError::runtime("kv_cache_allocate:sliding_window");
+    if (k.tag == LayerKind::Tag::SlidingWindow &&
+        (k.window == 0 || k.window > (size_t)std::numeric_limits<int32_t>::max()))
+      return HipError::runtime("kv_cache_allocate:sliding_window");
   const size_t pps = (max_seq_len + SAI_PAGE_TOKENS - 1) / SAI_PAGE_TOKENS;
   const size_t lim = (size_t)std::numeric_limits<int32_t>::max();
   if (num_layers > lim || num_kv_heads > lim || head_dim > lim || pps > lim / max_batch)
@@ -320,6 +322,14 @@ Result<GpuKvCache, HipError> GpuKvCache::allocate(RocmRuntime& rt, size_t num_la
   c.max_batch_ = max_batch;
   c.pages_per_seq_ = pps;
   c.quant_ = quant;
+  c.layer_windows_.assign(num_layers, 0);
+  for (size_t l = 0; l < num_layers; ++l) {
+    if (layer_kinds[l].tag != LayerKind::Tag::SlidingWindow) continue;
+    c.layer_windows_[l] = layer_kinds[l].window;
+    const sai_status ws =
+        sai_kvcache_set_layer_window(rt.raw(), c.cache_, (int32_t)l, (int32_t)layer_kinds[l].window);
+    if (ws != SAI_OK) return HipError::runtime("kv_cache_allocate:sliding_window", ws);
+  }
   auto b = c.ensure_batch(max_batch, "kv_cache_allocate");
   if (!b) return b.error();
   return c;
@@ -338,6 +348,7 @@ GpuKvCache& GpuKvCache::operator=(GpuKvCache&& o) noexcept {
     max_seq_len_ = o.max_seq_len_;
     max_batch_ = o.max_batch_;
     pages_per_seq_ = o.pages_per_seq_;
+    layer_windows_ = std::move(o.layer_windows_);
     batch_ = o.batch_;
     position_ = o.position_;
     quant_ = o.quant_;
@@ -432,7 +443,11 @@ Result<KvView, HipError> GpuKvCache::view_at(size_t layer_idx, size_t count, con
       sai_kvcache_pool(cache_, (int32_t)layer_idx, &pool, &v.pool_bytes, &v.block_bytes);
   if (st != SAI_OK) return HipError::runtime(op, st);
   v.pool = pool;
-  v.token_count = count;
+  // kv_cache.rs:351-358: a sliding-window layer exposes its last w tokens
+  const size_t w = layer_windows_[layer_idx];
+  const size_t n = w > 0 ? std::min(w, count) : count;
+  v.start_token = count - n;
+  v.token_count = n;
   v.num_kv_heads = num_kv_heads_;
   v.head_dim = head_dim_;
   v.batch = batch_;
@@ -651,6 +666,12 @@ Result<DeviceTensor, OpError> gqa_over_cache(RocmRuntime& rt, GpuKvCache& cache,
   const int32_t il = a.rotary_interleaved ? 1 : 0;
   const int32_t has_scale = a.scale ? 1 : 0;
   const float scale = a.scale ? *a.scale : 0.0f;
+  // parse_gqa_attrs (gpu_executor.rs:874-878): a positive local_window_size
+  // is the kernel's window, anything else none
+  const int32_t window = a.local_window_size > 0
+                             ? (int32_t)std::min<int64_t>(a.local_window_size,
+                                                          std::numeric_limits<int32_t>::max())
+                             : 0;
   float* o = (float*)out.value().buffer.as_ptr();
   if (g.seq == 1) {
     auto ck = cache.check_append(g.batch, 1);
@@ -658,7 +679,7 @@ Result<DeviceTensor, OpError> gqa_over_cache(RocmRuntime& rt, GpuKvCache& cache,
     const sai_status st = sai_gqa_with_cache(
         rt.raw(), cache.raw(), (int32_t)layer, q.buffer.as_ptr(), sai_dtype(q.dtype),
         k.buffer.as_ptr(), v.buffer.as_ptr(), sai_dtype(k.dtype), (int32_t)g.batch,
-        (int32_t)g.num_heads, cs, sn, rows, rot, il, has_scale, scale, o, nullptr);
+        (int32_t)g.num_heads, cs, sn, rows, rot, il, has_scale, scale, window, o, nullptr);
     if (st != SAI_OK) return from_status(st, prefix, rt);
     return std::move(out).value();
   }
@@ -667,7 +688,7 @@ Result<DeviceTensor, OpError> gqa_over_cache(RocmRuntime& rt, GpuKvCache& cache,
   const sai_status st = sai_gqa_prefill(rt.raw(), cache.raw(), (int32_t)layer, q.buffer.as_ptr(),
                                         sai_dtype(q.dtype), (int32_t)g.batch, (int32_t)g.seq,
                                         (int32_t)g.num_heads, cs, sn, rows, rot, il, has_scale,
-                                        scale, o, nullptr);
+                                        scale, window, o, nullptr);
   if (st != SAI_OK) return from_status(st, prefix, rt);
   return std::move(out).value();
 }
@@ -685,8 +706,6 @@ Result<std::vector<DeviceTensor>, OpError> dispatch_gqa(
   const DeviceTensor& k = *inputs[1];
   const DeviceTensor& v = *inputs[2];
   const GqaAttrs a = parse_gqa_attrs(attrs);
-  if (a.local_window_size != -1)
-    return OpError::attribute("GroupQueryAttention: local_window_size != -1 not supported in this tier");
   auto gs = gqa_validate(q.shape, k.shape, v.shape, a.num_heads, a.kv_num_heads);
   if (!gs) return gs.error();
   const GqaShape g = gs.value();

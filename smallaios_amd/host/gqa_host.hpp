@@ -198,8 +198,8 @@ struct DeviceTensor {
 };
 
 // ------------------------------------------------------------------ cache ---
-// kv_cache.rs:53-57. Sliding-window layers are rejected at allocation: the
-// kernels attend over the whole sequence.
+// kv_cache.rs:53-57. A sliding-window layer's queries see their last `window`
+// keys (the pages keep every token); window 0 is rejected at allocation.
 struct LayerKind {
   enum class Tag { Global, SlidingWindow };
   Tag tag = Tag::Global;
@@ -214,11 +214,13 @@ enum class KvQuant : int32_t { Int8 = SAI_KV_INT8, Int4 = SAI_KV_INT4 };
 // The reference's KvView (kv_cache.rs:72-80) points at linear K and V rows;
 // here one pool per layer holds both, in (page, kv head) blocks of
 // block_bytes (K codes, V codes, then the quantisation parameters). Tokens
-// [0, token_count) of every sequence are valid.
+// [start_token, start_token + token_count) of every sequence are in view
+// (start_token > 0 only for a sliding-window layer, kv_cache.rs:351-358).
 struct KvView {
   const void* pool = nullptr;
   size_t pool_bytes = 0;
   size_t block_bytes = 0;
+  size_t start_token = 0;
   size_t token_count = 0;
   size_t num_kv_heads = 0;
   size_t head_dim = 0;
@@ -243,8 +245,8 @@ class GpuKvCache {
   // kv_cache.rs:129-203. Every sequence slot b in [0, max_batch) owns
   // ceil(max_seq_len / 16) pages of its own (identity page table); the pools
   // are zero-filled. Errors: RuntimeError "kv_cache_allocate:layer_kinds_len",
-  // "kv_cache_allocate:zero_dim", "kv_cache_allocate:sliding_window",
-  // "kv_cache_allocate:unsupported_head_dim"; AllocFailed.
+  // "kv_cache_allocate:zero_dim", "kv_cache_allocate:sliding_window" (window
+  // 0 or above i32), "kv_cache_allocate:unsupported_head_dim"; AllocFailed.
   static Result<GpuKvCache, HipError> allocate(RocmRuntime& rt, size_t num_layers,
                                                size_t num_kv_heads, size_t head_dim,
                                                size_t max_seq_len, KvQuant quant,
@@ -285,7 +287,8 @@ class GpuKvCache {
   // kv_cache.rs:295-304: commit the pending tokens. Errors: RuntimeError
   // "kv_cache_advance:position_overflow", "kv_cache_advance:nothing_pending".
   Result<Unit, HipError> advance_position(void* stream = nullptr);
-  // kv_cache.rs:300-390: committed tokens, and committed + pending.
+  // kv_cache.rs:300-390: committed tokens, and committed + pending (the last
+  // `window` of them for a sliding-window layer).
   Result<KvView, HipError> view(size_t layer_idx) const;
   Result<KvView, HipError> view_pending(size_t layer_idx) const;
   // kv_cache.rs:386-388: position back to 0, buffers kept.
@@ -308,6 +311,7 @@ class GpuKvCache {
   sai_kvcache* cache_ = nullptr;
   size_t num_layers_ = 0, num_kv_heads_ = 0, head_dim_ = 0, max_seq_len_ = 0, max_batch_ = 0;
   size_t pages_per_seq_ = 0;
+  std::vector<size_t> layer_windows_;  // 0: global
   size_t batch_ = 0;
   size_t position_ = 0;
   KvQuant quant_ = KvQuant::Int8;
@@ -369,7 +373,10 @@ Result<GqaShape, OpError> gqa_validate(const std::vector<int64_t>& q_shape,
 // kernel. Without kv_cache_ctx the node attends over its own K/V only
 // through a transient one-layer cache. RoPE: applied when cos/sin are given
 // and do_rotary is 1; an explicit do_rotary=1 without them is the CPU op's
-// ShapeMismatch. Asynchronous on the null stream.
+// ShapeMismatch. local_window_size > 0 limits each query at position p to
+// keys [p - local_window_size, p] (the GPU mask, attention.rs:79), on top of
+// a sliding-window cache layer's last-w-keys rule; other values mean no
+// window (gpu_executor.rs:874-878). Asynchronous on the null stream.
 Result<std::vector<DeviceTensor>, OpError> dispatch_gqa(
     RocmRuntime& runtime, const std::vector<const DeviceTensor*>& inputs,
     const std::vector<AttributeProto>& attrs, KvCacheDispatchCtx* kv_cache_ctx);

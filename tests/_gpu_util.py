@@ -134,15 +134,16 @@ class Case:
                     np.testing.assert_array_equal(kp, oc.k_sz[b, h, :n], err_msg=f"K params b={b} h={h}")
                     np.testing.assert_array_equal(vp, oc.v_sz[b, h, :n], err_msg=f"V params b={b} h={h}")
 
-    def gpu_decode(self, q, q_dtype="f32", scale=None):
+    def gpu_decode(self, q, q_dtype="f32", scale=None, window=0):
         import torch
         out = torch.zeros((self.batch, 1, self.hq * self.d), dtype=torch.float32, device="cuda")
         self.cache.decode(0, dev(q, q_dtype), out, self.batch, self.hq, self.cos_d, self.sin_d,
-                          self.cos.shape[0], self.do_rotary, self.interleaved, scale)
+                          self.cos.shape[0], self.do_rotary, self.interleaved, scale,
+                          window=window)
         torch.cuda.synchronize()
         return out.cpu().numpy()
 
-    def step_fused(self, q, q_dtype="f32", scale=None):
+    def step_fused(self, q, q_dtype="f32", scale=None, window=0):
         """Append the step's token and attend in one launch (sai_gqa_with_cache)."""
         import torch
         k, v = self.kv(1)
@@ -151,23 +152,24 @@ class Case:
         self.cache.decode_with_cache(0, dev(q, q_dtype), dev(k, self.kv_dtype),
                                      dev(v, self.kv_dtype), out, self.batch, self.hq, self.cos_d,
                                      self.sin_d, self.cos.shape[0], self.do_rotary,
-                                     self.interleaved, scale)
+                                     self.interleaved, scale, window=window)
         torch.cuda.synchronize()
         return out.cpu().numpy()
 
-    def gpu_prefill(self, q, q_dtype="f32", scale=None):
+    def gpu_prefill(self, q, q_dtype="f32", scale=None, window=0):
         import torch
         out = torch.zeros((self.batch, self.new_tokens, self.hq * self.d), dtype=torch.float32,
                           device="cuda")
         self.cache.prefill(0, dev(q, q_dtype), out, self.batch, self.new_tokens, self.hq,
                            self.cos_d, self.sin_d, self.cos.shape[0], self.do_rotary,
-                           self.interleaved, scale)
+                           self.interleaved, scale, window=window)
         torch.cuda.synchronize()
         return out.cpu().numpy()
 
-    def oracle_attend(self, q, scale=None):
+    def oracle_attend(self, q, scale=None, layer_window=0, mask_window=0):
         return self.ocache.attend(q, self.hq, self.cos, self.sin, self.do_rotary,
-                                  self.interleaved, scale)
+                                  self.interleaved, scale, layer_window=layer_window,
+                                  mask_window=mask_window)
 
 
 def assert_close(got, ref, what=""):

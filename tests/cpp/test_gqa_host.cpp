@@ -292,8 +292,8 @@ void gpu_cache_errors() {
   REQUIRE(op_of(must_fail_hip(GpuKvCache::allocate(rt, 1, 0, 64, 8, KvQuant::Int8, {LayerKind::global()}),
                               "zero")) == "kv_cache_allocate:zero_dim", "zero_dim");
   REQUIRE(op_of(must_fail_hip(GpuKvCache::allocate(rt, 1, 2, 64, 8, KvQuant::Int8,
-                                                   {LayerKind::sliding_window(4)}),
-                              "window")) == "kv_cache_allocate:sliding_window", "sliding_window");
+                                                   {LayerKind::sliding_window(0)}),
+                              "window")) == "kv_cache_allocate:sliding_window", "sliding_window 0");
   REQUIRE(op_of(must_fail_hip(GpuKvCache::allocate(rt, 1, 2, 16, 8, KvQuant::Int8, {LayerKind::global()}),
                               "head_dim")) == "kv_cache_allocate:unsupported_head_dim", "head_dim");
   GpuKvCache cache = must(GpuKvCache::allocate(rt, 1, 2, 64, 2, KvQuant::Int8, {LayerKind::global()}),
@@ -399,10 +399,6 @@ void gpu_dispatch_errors() {
   };
   expect(dispatch_gqa(rt, {&q, nullptr, &k}, heads, nullptr), OpError::Kind::InternalError,
          "GPU GroupQueryAttention: missing input 'K'", "missing K");
-  std::vector<AttributeProto> win = heads;
-  win.push_back(AttributeProto::make_int("local_window_size", 4));
-  expect(dispatch_gqa(rt, {&q, &k, &k}, win, nullptr), OpError::Kind::InvalidAttribute,
-         "local_window_size != -1 not supported", "window");
   expect(dispatch_gqa(rt, {&q, &k, &k}, {}, nullptr), OpError::Kind::InvalidAttribute,
          "num_heads and kv_num_heads must be > 0", "rank-3 without heads");
   std::vector<AttributeProto> rot = heads;
@@ -764,15 +760,18 @@ void gpu_rope_tables() {
 }
 
 // appends into a logical cache and attends over its dequantised contents.
+// lw > 0: layer 1 is a sliding-window layer of lw keys; mw: the nodes'
+// local_window_size (-1: none).
 static void session(KvQuant quant, bool bf16, int B, int Hq, int Hkv, int D, int prefill,
-                    int steps, unsigned seed) {
+                    int steps, unsigned seed, int lw = 0, int mw = -1) {
   RocmRuntime& rt = runtime();
   const int layers = 2, rows = 512, t_cap = prefill + steps;
   std::vector<float> cs, sn;
   rope_tables(rows, D, 10000.0, cs, sn);
   DeviceTensor dcos = f32_tensor(cs, shp({rows, D / 2})), dsin = f32_tensor(sn, shp({rows, D / 2}));
-  GpuKvCache cache = must(GpuKvCache::allocate(rt, layers, Hkv, D, t_cap, quant,
-                                               std::vector<LayerKind>(layers, LayerKind::global()), B),
+  std::vector<LayerKind> kinds(layers, LayerKind::global());
+  if (lw > 0) kinds[1] = LayerKind::sliding_window((size_t)lw);
+  GpuKvCache cache = must(GpuKvCache::allocate(rt, layers, Hkv, D, t_cap, quant, kinds, B),
                           "allocate");
   const int q8 = quant == KvQuant::Int8 ? 1 : 2;
   const size_t rowsz = (size_t)B * Hkv * t_cap;
@@ -793,8 +792,9 @@ static void session(KvQuant quant, bool bf16, int B, int Hq, int Hkv, int D, int
     l.ksz.resize(rowsz * D / 16);
     l.vsz.resize(rowsz * D / 16);
   }
-  const std::vector<AttributeProto> attrs = {AttributeProto::make_int("num_heads", Hq),
-                                             AttributeProto::make_int("kv_num_heads", Hkv)};
+  std::vector<AttributeProto> attrs = {AttributeProto::make_int("num_heads", Hq),
+                                       AttributeProto::make_int("kv_num_heads", Hkv)};
+  if (mw != -1) attrs.push_back(AttributeProto::make_int("local_window_size", mw));
   std::mt19937_64 gen(seed);
   int pos = 0;
   const int passes = (prefill > 0 ? 1 : 0) + steps;
@@ -829,8 +829,9 @@ static void session(KvQuant quant, bool bf16, int B, int Hq, int Hkv, int D, int
                                 l.vs.data(), l.ksz.data(), l.vsz.data(), kd.data(), vd.data()) == 0,
               "oracle dequant");
       std::vector<float> want((size_t)B * S * Hq * D);
-      REQUIRE(sai_or_gqa_cached(q.data(), B, S, Hq, Hkv, D, lens.data(), t_cap, kd.data(), vd.data(),
-                                cs.data(), sn.data(), rows, 1, 0, 0, 0.0f, want.data()) == 0,
+      REQUIRE(sai_or_gqa_cached_window(q.data(), B, S, Hq, Hkv, D, lens.data(), t_cap, kd.data(),
+                                       vd.data(), cs.data(), sn.data(), rows, 1, 0, 0, 0.0f,
+                                       layer == 1 ? lw : 0, mw, want.data()) == 0,
               "oracle gqa");
       char what[96];
       std::snprintf(what, sizeof what, "pass %d layer %d output", pass, layer);
@@ -857,6 +858,41 @@ static void gpu_session_int8_bf16_d64() { session(KvQuant::Int8, true, 3, 8, 2, 
 static void gpu_session_int4_decode() { session(KvQuant::Int4, false, 2, 16, 2, 128, 0, 24, 13); }
 static void gpu_session_int4_prefill_decode() { session(KvQuant::Int4, true, 2, 8, 2, 128, 37, 5, 15); }
 static void gpu_session_int4_bf16_group4() { session(KvQuant::Int4, true, 1, 8, 2, 128, 0, 20, 14); }
+static void gpu_session_int8_windows() { session(KvQuant::Int8, false, 2, 8, 2, 128, 150, 6, 16, 30, 40); }
+static void gpu_session_int4_layer_window() { session(KvQuant::Int4, true, 2, 8, 2, 128, 100, 5, 17, 33); }
+
+// test_kv_cache_sliding_window (tests/test_cuda.rs:1275-1334): a global layer
+// and a sliding-window layer of 4; after 6 tokens the global view holds 6,
+// the local view the last 4 (positions 2..5), read back by value.
+void gpu_cache_sliding_window() {
+  RocmRuntime& rt = runtime();
+  const size_t Hkv = 2, D = 64;
+  GpuKvCache cache = must(GpuKvCache::allocate(rt, 2, Hkv, D, 16, KvQuant::Int8,
+                                               {LayerKind::global(), LayerKind::sliding_window(4)}),
+                          "allocate");
+  for (int pos = 0; pos < 6; ++pos) {
+    const float fill = (float)(pos + 1) * 0.1f;
+    DeviceTensor kv = fill_tensor(Hkv, D, fill);
+    for (size_t layer = 0; layer < 2; ++layer) must(cache.append(layer, kv, kv), "append");
+    must(cache.advance_position(), "advance");
+  }
+  REQUIRE(cache.current_position() == 6, "position");
+  KvView g = must(cache.view(0), "view global");
+  REQUIRE(g.start_token == 0 && g.token_count == 6, "global view %zu+%zu", g.start_token, g.token_count);
+  KvView l = must(cache.view(1), "view local");
+  REQUIRE(l.start_token == 2 && l.token_count == 4, "local view %zu+%zu", l.start_token, l.token_count);
+  for (size_t h = 0; h < Hkv; ++h) {
+    auto kv = must(cache.read_dequantized(1, 0, h, l.start_token, l.token_count), "read local");
+    for (size_t vp = 0; vp < 4; ++vp) {
+      const float expect = (float)(vp + 2 + 1) * 0.1f;
+      for (size_t d = 0; d < D; ++d)
+        REQUIRE(std::fabs(kv.first[vp * D + d] - expect) < 1e-2f, "local pos %zu: %g != %g", vp,
+                kv.first[vp * D + d], expect);
+    }
+  }
+  KvView lp = must(cache.view_pending(1), "view_pending local");
+  REQUIRE(lp.start_token == 2 && lp.token_count == 4, "nothing pending: same view");
+}
 
 int main(int argc, char** argv) {
   struct Case {
@@ -884,6 +920,9 @@ int main(int argc, char** argv) {
       {"gpu_session_int4_decode", true, gpu_session_int4_decode},
       {"gpu_session_int4_bf16_group4", true, gpu_session_int4_bf16_group4},
       {"gpu_session_int4_prefill_decode", true, gpu_session_int4_prefill_decode},
+      {"gpu_session_int8_windows", true, gpu_session_int8_windows},
+      {"gpu_session_int4_layer_window", true, gpu_session_int4_layer_window},
+      {"gpu_cache_sliding_window", true, gpu_cache_sliding_window},
   };
   std::vector<const Case*> run;
   for (int i = 1; i < argc; ++i) {
