@@ -237,6 +237,21 @@ sai_status sai_rotary_embedding(sai_ctx* ctx, const void* x, void* y, int32_t dt
                                 int32_t cache_cols, int32_t rotary_dim, int32_t interleaved,
                                 void* stream);
 
+/* ---- row copy between layouts ------------------------------------------------
+ * Replaces kv_concat / kv_copy_block (onnx-rt/src/ops/microsoft.rs:733-792) and
+ * reshape_to_bhsd / reshape_from_bhsd (microsoft.rs:660-704): src holds
+ * batch*heads*seq rows of head_dim elements of `dtype` (F32 or BF16) in
+ * src_layout; row (b, h, s) is copied to row (b, h, dst_offset + s) of dst,
+ * which holds dst_seq positions per (b, h) in dst_layout (SAI_ROPE_BHSD =
+ * [B, H, S, D], SAI_ROPE_BSHD = [B, S, H*D]). A past K/V [B, H, P, D] and a
+ * step's new rows [B, S, H*D] concatenate into present [B, H, P+S, D] with two
+ * calls. src and dst must not overlap. Errors: SHAPE_MISMATCH (the rows do not
+ * fit dst), INVALID_ATTRIBUTE (layout), UNSUPPORTED (dtype). */
+sai_status sai_copy_rows(sai_ctx* ctx, const void* src, int32_t src_layout, void* dst,
+                         int32_t dst_layout, int32_t dtype, int32_t batch, int32_t heads,
+                         int32_t seq, int32_t head_dim, int32_t dst_seq, int32_t dst_offset,
+                         void* stream);
+
 /* ---- RoPE tables ---------------------------------------------------------------
  * Replaces precompute_rope_tables (onnx-rt/src/model_loader/gemma.rs:458-472)
  * with its f32 approximations powf/ln/exp/floor/sin/cos (gemma.rs:480-541):

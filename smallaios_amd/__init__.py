@@ -76,7 +76,7 @@ EXPORTS = [
     "sai_gqa_decode", "sai_gqa_with_cache", "sai_gqa_prefill", "sai_set_decode_split",
     "sai_set_decode_waves", "sai_set_decode_merge", "sai_last_decode_shape",
     "sai_set_decode_timing", "sai_decode_kernel_times", "sai_rotary_embedding",
-    "sai_rope_tables",
+    "sai_rope_tables", "sai_copy_rows",
 ]
 ROPE_BHSD = 0
 ROPE_BSHD = 1
@@ -117,6 +117,7 @@ def _declare(L: C.CDLL) -> None:
         "sai_rotary_embedding": (i32, [p, p, p, i32, i32, i32, i32, i32, i32, p, C.c_int64,
                                        C.c_int64, p, p, i32, i32, i32, i32, i32, p]),
         "sai_rope_tables": (i32, [p, f, i32, i32, i32, p, p, p]),
+        "sai_copy_rows": (i32, [p, p, i32, p, i32, i32, i32, i32, i32, i32, i32, i32, p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -246,6 +247,15 @@ class Runtime:
             None if ids is None else ids.ctypes.data_as(C.c_void_p), n_pos, int(start_position),
             _dev_ptr(cos), _dev_ptr(sin), tdt, rows, cols, int(rotary_dim), int(interleaved),
             _stream(stream)), "rotary_embedding")
+
+    def copy_rows(self, src, src_layout, dst, dst_layout, batch, heads, seq, head_dim, dst_seq,
+                  dst_offset=0, dtype=None, stream=None):
+        """sai_copy_rows: rows (b, h, s) of src to (b, h, dst_offset + s) of dst."""
+        dt = dtype if dtype is not None else _dtype_code(src)
+        self.check(self._L.sai_copy_rows(self.handle, _dev_ptr(src), int(src_layout),
+                                         _dev_ptr(dst), int(dst_layout), dt, batch, heads, seq,
+                                         head_dim, dst_seq, dst_offset, _stream(stream)),
+                   "copy_rows")
 
     def rope_tables(self, max_pos, half, theta, cos_out, sin_out, dtype=DTYPE_BF16,
                     stream=None):

@@ -34,7 +34,7 @@ EXTRA = {
     "rotary.hip": ["-ffp-contract=off"],
 }
 SOURCES = ["kv_append.hip", "gqa_decode.hip", "gqa_decode_int4.hip", "gqa_prefill.hip",
-           "rotary.hip", "sai_capi.hip"]
+           "rotary.hip", "copy_rows.hip", "sai_capi.hip"]
 
 
 def _run(cmd):

@@ -1030,3 +1030,43 @@ SAI_API sai_status sai_rope_tables(sai_ctx* ctx, float rope_theta, int32_t max_p
   if (e != hipSuccess) return hip_fail(ctx, e, "rope_tables launch");
   return SAI_OK;
 }
+
+// ------------------------------------------------------------------ row copy ---
+SAI_API sai_status sai_copy_rows(sai_ctx* ctx, const void* src, int32_t src_layout, void* dst,
+                                 int32_t dst_layout, int32_t dtype, int32_t batch, int32_t heads,
+                                 int32_t seq, int32_t head_dim, int32_t dst_seq,
+                                 int32_t dst_offset, void* stream) {
+  if (!ctx) return SAI_ERR_NULL;
+  const char* op = "sai_copy_rows";
+  if (dtype != SAI_DTYPE_F32 && dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (need F32 or BF16)", op, dtype);
+  if ((src_layout != SAI_ROPE_BHSD && src_layout != SAI_ROPE_BSHD) ||
+      (dst_layout != SAI_ROPE_BHSD && dst_layout != SAI_ROPE_BSHD))
+    return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE, "%s: unknown layout", op);
+  if (batch < 0 || heads < 0 || seq < 0 || head_dim < 0 || dst_offset < 0 ||
+      (int64_t)dst_offset + seq > (int64_t)dst_seq)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                "%s: rows [%d, %d + %d) do not fit a destination of %d positions", op, dst_offset,
+                dst_offset, seq, dst_seq);
+  const uint64_t rows = (uint64_t)batch * (uint64_t)heads * (uint64_t)seq;
+  if (rows == 0 || head_dim == 0) return SAI_OK;
+  if (!src || !dst) return fail(ctx, SAI_ERR_NULL, "%s: src or dst is NULL", op);
+  const size_t esz = dtype == SAI_DTYPE_BF16 ? 2 : 4;
+  const size_t row_bytes = (size_t)head_dim * esz;
+  const int chunk = (row_bytes % 16 == 0 && aligned16(src) && aligned16(dst)) ? 16 : (int)esz;
+  sai::CopyRowsArgs a{};
+  a.src = src;
+  a.dst = dst;
+  a.chunks = (int32_t)(row_bytes / (size_t)chunk);
+  a.total = rows * (uint64_t)a.chunks;
+  a.heads = heads;
+  a.seq = seq;
+  a.dst_seq = dst_seq;
+  a.dst_offset = dst_offset;
+  a.src_layout = src_layout;
+  a.dst_layout = dst_layout;
+  DeviceGuard dg(ctx->device);
+  const hipError_t e = sai::launch_copy_rows(a, chunk, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "copy_rows launch");
+  return SAI_OK;
+}

@@ -182,7 +182,21 @@ struct RotaryArgs {
   int32_t tab[kRotaryTab];
 };
 
+// Row copy (copy_rows.hip): src holds batch x heads x seq rows of
+// `chunks` chunks in src_layout (0: (b, h, s) order, 1: (b, s, h)); row
+// (b, h, s) goes to row (b, h, dst_offset + s) of dst, which holds dst_seq
+// sequence positions in dst_layout.
+struct CopyRowsArgs {
+  const void* src;
+  void* dst;
+  uint64_t total;  // rows * chunks
+  int32_t chunks;  // chunks per row
+  int32_t heads, seq, dst_seq, dst_offset;
+  int32_t src_layout, dst_layout;
+};
+
 // Launchers (return hipError_t of the launch).
+hipError_t launch_copy_rows(const CopyRowsArgs& a, int chunk_bytes, hipStream_t st);
 // Standalone RoPE (rotary.hip): x/y f32 or bf16, tables f32 or bf16.
 hipError_t launch_rotary(const RotaryArgs& a, bool x_bf16, bool table_bf16, bool interleaved,
                          hipStream_t st);

@@ -1003,4 +1003,236 @@ Result<std::pair<DeviceTensor, DeviceTensor>, HipError> precompute_rope_tables(
   return std::make_pair(std::move(c).value(), std::move(s).value());
 }
 
+// ------------------------------------------------- CPU attention op contracts ---
+namespace {
+
+OpError shape_fmt(const char* fmt, long long a, long long b) {
+  char buf[192];
+  std::snprintf(buf, sizeof buf, fmt, a, b);
+  return OpError::shape(buf);
+}
+
+// validate_past_kv (ops/microsoft.rs:707-731): the past's sequence length.
+Result<size_t, OpError> validate_past_kv(const DeviceTensor* past, size_t batch, size_t heads,
+                                         size_t head_dim) {
+  if (!past) return (size_t)0;
+  if (past->dtype != DataType::Float) return OpError::shape("GroupQueryAttention requires Float input");
+  if (past->shape.size() != 4)
+    return OpError::shape("GQA/MHA: past_key/past_value must be rank-4");
+  if (past->shape[0] != (int64_t)batch || past->shape[1] != (int64_t)heads ||
+      past->shape[3] != (int64_t)head_dim || past->shape[2] < 0)
+    return OpError::shape("GQA/MHA: past cache batch/heads/head_dim mismatch");
+  return (size_t)past->shape[2];
+}
+
+Result<DeviceTensor, OpError> alloc_or(std::vector<int64_t> shape, DataType dt,
+                                       const std::string& prefix) {
+  auto t = DeviceTensor::alloc(std::move(shape), dt);
+  if (!t) return OpError::internal(prefix + t.error().to_string());
+  return std::move(t).value();
+}
+
+// Shared GPU path of the two ops. q [B, S, Hq*D], k/v [B, S, Hkv*D] (f32),
+// past_k/past_v [B, Hkv, P, D] or null (P == 0).
+Result<AttentionOutputs, OpError> attention_with_past(
+    RocmRuntime& rt, const DeviceTensor& q, const DeviceTensor& k, const DeviceTensor& v,
+    const DeviceTensor* past_k, const DeviceTensor* past_v, size_t P, const GqaShape& g,
+    const RopeTables* rope, std::optional<float> scale, const std::string& prefix) {
+  const size_t B = g.batch, S = g.seq, Hkv = g.kv_heads, D = g.head_dim, T = P + S;
+  const int64_t lim = std::numeric_limits<int32_t>::max();
+  if ((int64_t)T > lim || (int64_t)(B * Hkv) > lim)
+    return OpError::unsupported(prefix + "sequence or batch too large");
+  auto pk = alloc_or({(int64_t)B, (int64_t)Hkv, (int64_t)T, (int64_t)D}, DataType::Float, prefix);
+  if (!pk) return pk.error();
+  auto pv = alloc_or({(int64_t)B, (int64_t)Hkv, (int64_t)T, (int64_t)D}, DataType::Float, prefix);
+  if (!pv) return pv.error();
+  auto attn = alloc_or({(int64_t)B, (int64_t)S, (int64_t)g.q_hidden}, DataType::Float, prefix);
+  if (!attn) return attn.error();
+  sai_ctx* ctx = rt.raw();
+  auto copy = [&](const void* src, int32_t src_layout, void* dst, int32_t seq, int32_t off) {
+    return sai_copy_rows(ctx, src, src_layout, dst, SAI_ROPE_BHSD, SAI_DTYPE_F32, (int32_t)B,
+                         (int32_t)Hkv, seq, (int32_t)D, (int32_t)T, off, nullptr);
+  };
+  // present = past ++ new (kv_concat, microsoft.rs:762-792), new K rotated first
+  sai_status st = SAI_OK;
+  if (P > 0) {
+    st = copy(past_k->buffer.as_ptr(), SAI_ROPE_BHSD, pk.value().buffer.as_ptr(), (int32_t)P, 0);
+    if (st == SAI_OK)
+      st = copy(past_v->buffer.as_ptr(), SAI_ROPE_BHSD, pv.value().buffer.as_ptr(), (int32_t)P, 0);
+    if (st != SAI_OK) return from_status(st, prefix, rt);
+  }
+  DeviceTensor k_rot;
+  const void* k_new = k.buffer.as_ptr();
+  if (rope && B * S > 0) {
+    auto kr = alloc_or(k.shape, DataType::Float, prefix);
+    if (!kr) return kr.error();
+    k_rot = std::move(kr).value();
+    st = sai_rotary_embedding(ctx, k.buffer.as_ptr(), k_rot.buffer.as_ptr(), SAI_DTYPE_F32,
+                              (int32_t)B, (int32_t)Hkv, (int32_t)S, (int32_t)D, SAI_ROPE_BSHD,
+                              nullptr, 0, (int64_t)P, rope->cos, rope->sin, SAI_DTYPE_F32,
+                              rope->rows, (int32_t)(D / 2), (int32_t)D, rope->interleaved ? 1 : 0,
+                              nullptr);
+    if (st != SAI_OK) return from_status(st, prefix, rt);
+    k_new = k_rot.buffer.as_ptr();
+  }
+  st = copy(k_new, SAI_ROPE_BSHD, pk.value().buffer.as_ptr(), (int32_t)S, (int32_t)P);
+  if (st == SAI_OK) st = copy(v.buffer.as_ptr(), SAI_ROPE_BSHD, pv.value().buffer.as_ptr(), (int32_t)S, (int32_t)P);
+  if (st != SAI_OK) return from_status(st, prefix, rt);
+  AttentionOutputs out{std::move(attn).value(), std::move(pk).value(), std::move(pv).value()};
+  if (B == 0 || S == 0) return out;
+
+  // attention over a transient paged cache: the past (already rotated) first,
+  // committed; then the new tokens through the fused decode or append + prefill
+  auto cache = GpuKvCache::allocate(rt, 1, Hkv, D, T, KvQuant::Int8, {LayerKind::global()}, B);
+  if (!cache) {
+    const HipError& e = cache.error();
+    if (e.op == "kv_cache_allocate:unsupported_head_dim")
+      return OpError::unsupported(prefix + e.to_string());
+    return OpError::internal(prefix + e.to_string());
+  }
+  if (P > 0) {
+    auto rk = alloc_or({(int64_t)B, (int64_t)P, (int64_t)(Hkv * D)}, DataType::Float, prefix);
+    if (!rk) return rk.error();
+    auto rv = alloc_or({(int64_t)B, (int64_t)P, (int64_t)(Hkv * D)}, DataType::Float, prefix);
+    if (!rv) return rv.error();
+    auto to_rows = [&](const void* src, void* dst) {
+      return sai_copy_rows(ctx, src, SAI_ROPE_BHSD, dst, SAI_ROPE_BSHD, SAI_DTYPE_F32, (int32_t)B,
+                           (int32_t)Hkv, (int32_t)P, (int32_t)D, (int32_t)P, 0, nullptr);
+    };
+    st = to_rows(past_k->buffer.as_ptr(), rk.value().buffer.as_ptr());
+    if (st == SAI_OK) st = to_rows(past_v->buffer.as_ptr(), rv.value().buffer.as_ptr());
+    if (st != SAI_OK) return from_status(st, prefix, rt);
+    auto ap = cache.value().append(0, rk.value(), rv.value(), nullptr, nullptr);
+    if (!ap) return OpError::internal(prefix + ap.error().to_string());
+    auto adv = cache.value().advance_position(nullptr);
+    if (!adv) return OpError::internal(prefix + adv.error().to_string());
+  }
+  GqaAttrs a;
+  a.num_heads = (int64_t)g.num_heads;
+  a.kv_num_heads = (int64_t)Hkv;
+  a.scale = scale;
+  a.rotary_interleaved = rope && rope->interleaved;
+  auto r = gqa_over_cache(rt, cache.value(), 0, q, k, v, g, a, rope, prefix);
+  if (!r) return r.error();
+  out.attn = std::move(r).value();
+  return out;
+}
+
+// apply_rope_in_place's position check (microsoft.rs:125-133, :212-230) for
+// positions past .. past + S - 1: the first position past the table's end.
+Result<Unit, OpError> check_positions(size_t past, size_t S, int32_t rows, size_t B, size_t H) {
+  if (B == 0 || H == 0 || S == 0) return Unit{};
+  if (past + S > (size_t)rows) {
+    const size_t bad = past >= (size_t)rows ? past : (size_t)rows;
+    return shape_fmt("apply_rope_in_place: position %lld out of cache range %lld", (long long)bad,
+                     (long long)rows);
+  }
+  return Unit{};
+}
+
+}  // namespace
+
+Result<AttentionOutputs, OpError> op_group_query_attention(
+    RocmRuntime& runtime, const std::vector<const DeviceTensor*>& inputs, int64_t num_heads,
+    int64_t kv_num_heads, std::optional<float> scale_attr, int64_t local_window_size,
+    bool do_rotary, bool rotary_interleaved) {
+  if (local_window_size != -1)
+    return OpError::attribute("GroupQueryAttention: local_window_size != -1 not supported in this tier");
+  const DeviceTensor* q = slot(inputs, 0);
+  if (!q) return OpError::shape("GroupQueryAttention: missing query");
+  const DeviceTensor* k = slot(inputs, 1);
+  if (!k) return OpError::shape("GroupQueryAttention: missing key");
+  const DeviceTensor* v = slot(inputs, 2);
+  if (!v) return OpError::shape("GroupQueryAttention: missing value");
+  const DeviceTensor* past_key = slot(inputs, 3);
+  const DeviceTensor* past_value = slot(inputs, 4);
+  const DeviceTensor* cos = slot(inputs, 7);
+  const DeviceTensor* sin = slot(inputs, 8);
+  if (q->dtype != DataType::Float || k->dtype != DataType::Float || v->dtype != DataType::Float)
+    return OpError::shape("GroupQueryAttention requires Float input");
+  // gqa_validate (microsoft.rs:933-984) takes rank-3 Q/K/V only
+  if (q->shape.size() != 3 || k->shape.size() != 3 || v->shape.size() != 3) {
+    if (num_heads <= 0 || kv_num_heads <= 0)
+      return OpError::attribute("GroupQueryAttention: num_heads and kv_num_heads must be > 0");
+    if (num_heads % kv_num_heads != 0)
+      return OpError::attribute("GroupQueryAttention: num_heads must be a multiple of kv_num_heads");
+    return OpError::shape("GroupQueryAttention: Q/K/V must be rank-3");
+  }
+  auto gs = gqa_validate(q->shape, k->shape, v->shape, num_heads, kv_num_heads);
+  if (!gs) return gs.error();
+  const GqaShape g = gs.value();
+  // gqa_past_sk (microsoft.rs:988-1000)
+  size_t past = 0;
+  if (past_key) {
+    if (past_key->shape.size() != 4)
+      return OpError::shape("GroupQueryAttention: past_key must be rank-4");
+    past = past_key->shape[2] < 0 ? 0 : (size_t)past_key->shape[2];
+  }
+  RopeTables rope;
+  const RopeTables* rope_ptr = nullptr;
+  if (do_rotary) {  // gqa_apply_rotary (microsoft.rs:1004-1052)
+    if (!cos) return OpError::shape("GroupQueryAttention: do_rotary=1 but cos_cache is missing");
+    if (!sin) return OpError::shape("GroupQueryAttention: do_rotary=1 but sin_cache is missing");
+    auto rows = check_rope_tables(*cos, *sin, g.head_dim);
+    if (!rows) return rows.error();
+    auto pc = check_positions(past, g.seq, rows.value(), g.batch, g.num_heads);
+    if (!pc) return pc.error();
+    rope.cos = (const float*)cos->buffer.as_ptr();
+    rope.sin = (const float*)sin->buffer.as_ptr();
+    rope.rows = rows.value();
+    rope.interleaved = rotary_interleaved;
+    rope_ptr = &rope;
+  }
+  // kv_concat of both pasts (microsoft.rs:1138-1146)
+  auto pk = validate_past_kv(past_key, g.batch, g.kv_heads, g.head_dim);
+  if (!pk) return pk.error();
+  auto pv = validate_past_kv(past_value, g.batch, g.kv_heads, g.head_dim);
+  if (!pv) return pv.error();
+  if (pk.value() != past || pv.value() != past)
+    return OpError::shape("GroupQueryAttention: past_key / past_value sequence mismatch");
+  return attention_with_past(runtime, *q, *k, *v, past_key, past_value, past, g, rope_ptr,
+                             scale_attr, "ROCm GroupQueryAttention: ");
+}
+
+Result<AttentionOutputs, OpError> op_multi_head_attention(
+    RocmRuntime& runtime, const std::vector<const DeviceTensor*>& inputs, int64_t num_heads,
+    std::optional<float> scale_attr) {
+  const DeviceTensor* q = slot(inputs, 0);
+  if (!q) return OpError::shape("MultiHeadAttention: missing query");
+  const DeviceTensor* k = slot(inputs, 1);
+  if (!k) return OpError::shape("MultiHeadAttention: missing key");
+  const DeviceTensor* v = slot(inputs, 2);
+  if (!v) return OpError::shape("MultiHeadAttention: missing value");
+  // inputs 3..5 (bias, key_padding_mask, relative_position_bias) are not read
+  const DeviceTensor* past_key = slot(inputs, 6);
+  const DeviceTensor* past_value = slot(inputs, 7);
+  if (q->dtype != DataType::Float || k->dtype != DataType::Float || v->dtype != DataType::Float)
+    return OpError::shape("MultiHeadAttention requires Float input");
+  if (num_heads <= 0) return OpError::attribute("MultiHeadAttention: num_heads must be > 0");
+  if (q->shape.size() != 3 || k->shape.size() != 3 || v->shape.size() != 3)
+    return OpError::shape("MultiHeadAttention: Q/K/V must be rank-3 (B, Sq, hidden)");
+  const int64_t b = q->shape[0], sq = q->shape[1], hidden = q->shape[2];
+  if (b < 0 || sq < 0 || hidden < 0)
+    return OpError::shape("MultiHeadAttention: Q/K/V must be rank-3 (B, Sq, hidden)");
+  if (hidden % num_heads != 0)
+    return OpError::shape("MultiHeadAttention: hidden not divisible by num_heads");
+  if (k->shape != q->shape)
+    return OpError::shape("MultiHeadAttention: K shape must match Q (unpacked form)");
+  if (v->shape != q->shape) return OpError::shape("MultiHeadAttention: V shape must match Q");
+  GqaShape g;
+  g.num_heads = g.kv_heads = (size_t)num_heads;
+  g.batch = (size_t)b;
+  g.seq = (size_t)sq;
+  g.q_hidden = (size_t)hidden;
+  g.head_dim = (size_t)(hidden / num_heads);
+  auto pk = validate_past_kv(past_key, g.batch, g.kv_heads, g.head_dim);
+  if (!pk) return pk.error();
+  auto pv = validate_past_kv(past_value, g.batch, g.kv_heads, g.head_dim);
+  if (!pv) return pv.error();
+  if (pk.value() != pv.value())
+    return OpError::shape("MultiHeadAttention: past_key/past_value sequence length mismatch");
+  return attention_with_past(runtime, *q, *k, *v, past_key, past_value, pk.value(), g, nullptr,
+                             scale_attr, "ROCm MultiHeadAttention: ");
+}
+
 }  // namespace sai::rocm

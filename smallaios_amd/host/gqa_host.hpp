@@ -19,6 +19,8 @@
 //   dispatch_rotary_embedding (gpu_executor.rs:815-851)  dispatch_rotary_embedding
 //     with rotary_gpu (kernels/rotary.rs:274-374)
 //   op_rotary_embedding (ops/microsoft.rs:556-652)       op_rotary_embedding
+//   op_group_query_attention (ops/microsoft.rs:1082)     op_group_query_attention
+//   op_multi_head_attention (ops/microsoft.rs:806)       op_multi_head_attention
 //   precompute_rope_tables (model_loader/gemma.rs:458)   precompute_rope_tables
 //
 // Differences by design, each forced by the quantised paged cache:
@@ -380,6 +382,32 @@ Result<GqaShape, OpError> gqa_validate(const std::vector<int64_t>& q_shape,
 Result<std::vector<DeviceTensor>, OpError> dispatch_gqa(
     RocmRuntime& runtime, const std::vector<const DeviceTensor*>& inputs,
     const std::vector<AttributeProto>& attrs, KvCacheDispatchCtx* kv_cache_ctx);
+
+// Outputs of the CPU attention ops: attention [B, S, Hq*D] f32 and present
+// K/V [B, Hkv, past + S, D] f32.
+struct AttentionOutputs {
+  DeviceTensor attn, present_key, present_value;
+};
+
+// ops/microsoft.rs:1082-1190 (op_group_query_attention) on device tensors,
+// with its checks, order and messages: Float Q/K/V [B, S, H*D], optional
+// past_key / past_value [B, Hkv, P, D] at inputs 3/4, cos/sin at 7/8 when
+// do_rotary, local_window_size must be -1. present_key = past ++ RoPE(new K)
+// and present_value = past ++ new V, copied exactly (sai_copy_rows,
+// sai_rotary_embedding); the attention runs over a transient int8 paged
+// cache holding them (outputs within the kernels' tolerance). head_dim 64 or
+// 128 and a group of 1, 2, 4 or 8 (else UnsupportedOp).
+Result<AttentionOutputs, OpError> op_group_query_attention(
+    RocmRuntime& runtime, const std::vector<const DeviceTensor*>& inputs, int64_t num_heads,
+    int64_t kv_num_heads, std::optional<float> scale_attr, int64_t local_window_size,
+    bool do_rotary, bool rotary_interleaved);
+
+// ops/microsoft.rs:806-925 (op_multi_head_attention): Q/K/V [B, S, H*D] of
+// one shape, optional past_key / past_value at inputs 6/7, no RoPE, causal
+// over past + new; the same present outputs and attention path as above.
+Result<AttentionOutputs, OpError> op_multi_head_attention(
+    RocmRuntime& runtime, const std::vector<const DeviceTensor*>& inputs, int64_t num_heads,
+    std::optional<float> scale_attr);
 
 // gpu_executor.rs:815-851 over rotary_gpu (kernels/rotary.rs:274-374).
 // Inputs: [X, position_ids, cos_cache, sin_cache] (4 or more) or

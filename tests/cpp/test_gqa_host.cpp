@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <optional>
 #include <random>
 #include <string>
 #include <tuple>
@@ -861,6 +862,180 @@ static void gpu_session_int4_bf16_group4() { session(KvQuant::Int4, true, 1, 8, 
 static void gpu_session_int8_windows() { session(KvQuant::Int8, false, 2, 8, 2, 128, 150, 6, 16, 30, 40); }
 static void gpu_session_int4_layer_window() { session(KvQuant::Int4, true, 2, 8, 2, 128, 100, 5, 17, 33); }
 
+// The CPU ops' contract with explicit past K/V (op_group_query_attention,
+// ops/microsoft.rs:1082-1190; op_multi_head_attention, :806-925): present
+// K/V bit-exact against the oracle's restatement of the op (sai_or_gqa); the
+// attention within the parity bar of the oracle over the dequantised int8
+// cache that holds the same past and new rows.
+static void cpu_op_case(bool mha, int B, int Hq, int Hkv, int D, int S, int P, bool rot, bool il,
+                        bool has_scale, unsigned seed) {
+  RocmRuntime& rt = runtime();
+  std::mt19937_64 gen(seed);
+  const int rows = P + S + 5;
+  std::vector<float> cs, sn;
+  rope_tables(rows, D, 10000.0, cs, sn);
+  std::vector<float> q = gauss(gen, (size_t)B * S * Hq * D);
+  std::vector<float> k = gauss(gen, (size_t)B * S * Hkv * D);
+  std::vector<float> v = gauss(gen, (size_t)B * S * Hkv * D);
+  std::vector<float> pk = gauss(gen, (size_t)B * Hkv * P * D);
+  std::vector<float> pv = gauss(gen, (size_t)B * Hkv * P * D);
+  DeviceTensor dq = f32_tensor(q, shp({B, S, (int64_t)Hq * D}));
+  DeviceTensor dk = f32_tensor(k, shp({B, S, (int64_t)Hkv * D}));
+  DeviceTensor dv = f32_tensor(v, shp({B, S, (int64_t)Hkv * D}));
+  DeviceTensor dpk = f32_tensor(pk, shp({B, Hkv, P, D})), dpv = f32_tensor(pv, shp({B, Hkv, P, D}));
+  DeviceTensor dcos = f32_tensor(cs, shp({rows, D / 2})), dsin = f32_tensor(sn, shp({rows, D / 2}));
+  const std::optional<float> scale = has_scale ? std::optional<float>(0.07f) : std::nullopt;
+  const DeviceTensor* past_k = P > 0 ? &dpk : nullptr;
+  const DeviceTensor* past_v = P > 0 ? &dpv : nullptr;
+  AttentionOutputs o =
+      mha ? must(op_multi_head_attention(rt, {&dq, &dk, &dv, nullptr, nullptr, nullptr, past_k, past_v},
+                                         Hq, scale),
+                 "op_multi_head_attention")
+          : must(op_group_query_attention(rt, {&dq, &dk, &dv, past_k, past_v, nullptr, nullptr,
+                                               rot ? &dcos : nullptr, rot ? &dsin : nullptr},
+                                          Hq, Hkv, scale, -1, rot, il),
+                 "op_group_query_attention");
+  REQUIRE(o.attn.shape == shp({B, S, (int64_t)Hq * D}), "attn shape");
+  REQUIRE(o.present_key.shape == shp({B, Hkv, P + S, D}), "present shape");
+  // present: exact
+  const int T = P + S;
+  std::vector<float> w_attn((size_t)B * S * Hq * D), w_pk((size_t)B * Hkv * T * D), w_pv(w_pk.size());
+  REQUIRE(sai_or_gqa(q.data(), k.data(), v.data(), B, S, Hq * D, Hkv * D, P ? pk.data() : nullptr,
+                     P ? pv.data() : nullptr, P, cs.data(), sn.data(), rows, D / 2, Hq, Hkv,
+                     has_scale ? 1 : 0, 0.07f, -1, rot ? 1 : 0, il ? 1 : 0, w_attn.data(), w_pk.data(),
+                     w_pv.data()) == 0,
+          "oracle op");
+  const std::vector<float> g_pk = host_f32(o.present_key), g_pv = host_f32(o.present_value);
+  REQUIRE(std::memcmp(g_pk.data(), w_pk.data(), w_pk.size() * 4) == 0, "present_key differs from the oracle");
+  REQUIRE(std::memcmp(g_pv.data(), w_pv.data(), w_pv.size() * 4) == 0, "present_value differs from the oracle");
+  // attention: the oracle over the int8 cache of the same rows
+  std::vector<int8_t> k8((size_t)B * Hkv * T * D), v8(k8.size());
+  std::vector<float> ks((size_t)B * Hkv * T), vs(ks.size());
+  std::vector<int32_t> zero(B, 0), at_p(B, P), lens(B, T);
+  if (P > 0) {
+    std::vector<float> rk((size_t)B * P * Hkv * D), rv(rk.size());  // past as rows
+    for (int b = 0; b < B; ++b)
+      for (int h = 0; h < Hkv; ++h)
+        for (int t = 0; t < P; ++t)
+          for (int d = 0; d < D; ++d) {
+            const size_t src = (((size_t)b * Hkv + h) * P + t) * D + d;
+            const size_t dst = (((size_t)b * P + t) * Hkv + h) * D + d;
+            rk[dst] = pk[src];
+            rv[dst] = pv[src];
+          }
+    REQUIRE(sai_or_kv_append(rk.data(), rv.data(), B, P, Hkv, D, zero.data(), nullptr, nullptr, 0, 0, 0,
+                             1, T, k8.data(), v8.data(), ks.data(), vs.data(), nullptr, nullptr) == 0,
+            "oracle past append");
+  }
+  REQUIRE(sai_or_kv_append(k.data(), v.data(), B, S, Hkv, D, at_p.data(), cs.data(), sn.data(), rows,
+                           rot ? 1 : 0, il ? 1 : 0, 1, T, k8.data(), v8.data(), ks.data(), vs.data(),
+                           nullptr, nullptr) == 0,
+          "oracle new append");
+  std::vector<float> kd((size_t)B * Hkv * T * D), vd(kd.size());
+  REQUIRE(sai_or_kv_dequant(B, Hkv, D, 1, T, lens.data(), k8.data(), v8.data(), ks.data(), vs.data(),
+                            nullptr, nullptr, kd.data(), vd.data()) == 0,
+          "oracle dequant");
+  std::vector<float> want((size_t)B * S * Hq * D);
+  REQUIRE(sai_or_gqa_cached(q.data(), B, S, Hq, Hkv, D, lens.data(), T, kd.data(), vd.data(), cs.data(),
+                            sn.data(), rows, rot ? 1 : 0, il ? 1 : 0, has_scale ? 1 : 0, 0.07f,
+                            want.data()) == 0,
+          "oracle attention");
+  close(host_f32(o.attn), want, mha ? "MHA attention" : "GQA attention");
+}
+
+void gpu_cpu_op_gqa_with_past() {
+  cpu_op_case(false, 2, 8, 2, 128, 1, 37, true, false, false, 41);   // decode step
+  cpu_op_case(false, 1, 4, 4, 64, 5, 0, true, true, false, 42);      // first chunk, no past
+  cpu_op_case(false, 2, 8, 1, 128, 3, 20, false, false, true, 43);   // no RoPE, explicit scale
+  cpu_op_case(false, 1, 16, 2, 128, 70, 130, true, false, false, 44);  // prefill chunk over a past
+}
+
+void gpu_cpu_op_mha_with_past() {
+  cpu_op_case(true, 2, 4, 4, 64, 3, 0, false, false, false, 51);
+  cpu_op_case(true, 1, 2, 2, 128, 1, 17, false, false, true, 52);
+  cpu_op_case(true, 2, 8, 8, 64, 40, 25, false, false, false, 53);
+}
+
+// The reference's op tests (ops/microsoft.rs:1541-1600, :1602-1830, :2000-2060)
+// restated at head_dim 64: shapes of present across calls, Q = 0 giving the
+// mean of the visible values, and the error contract.
+void gpu_cpu_op_kats() {
+  RocmRuntime& rt = runtime();
+  const int D = 64;
+  {  // mha_basic_two_heads_no_cache: Q = 0 -> q0 = v0, q1 = (v0 + v1) / 2
+    std::vector<float> q(2 * 2 * D, 0.0f), k, v;
+    std::mt19937_64 gen(7);
+    k = gauss(gen, 2 * 2 * D);
+    v = gauss(gen, 2 * 2 * D);
+    DeviceTensor dq = f32_tensor(q, shp({1, 2, 2 * D})), dk = f32_tensor(k, shp({1, 2, 2 * D})),
+                 dv = f32_tensor(v, shp({1, 2, 2 * D}));
+    AttentionOutputs o = must(op_multi_head_attention(rt, {&dq, &dk, &dv}, 2, std::nullopt), "mha");
+    REQUIRE(o.attn.shape == shp({1, 2, 2 * D}) && o.present_key.shape == shp({1, 2, 2, D}) &&
+                o.present_value.shape == shp({1, 2, 2, D}),
+            "shapes");
+    const std::vector<float> a = host_f32(o.attn);
+    for (int h = 0; h < 2; ++h)
+      for (int d = 0; d < D; ++d) {
+        const float v0 = v[(size_t)h * D + d], v1 = v[(size_t)(2 + h) * D + d];
+        REQUIRE(std::fabs(a[(size_t)h * D + d] - v0) < 0.02f, "q0 = v0 (h %d d %d)", h, d);
+        REQUIRE(std::fabs(a[(size_t)(2 + h) * D + d] - 0.5f * (v0 + v1)) < 0.02f, "q1 = mean (h %d d %d)", h, d);
+      }
+  }
+  {  // gqa_kv_cache_mutation_across_calls: present grows 2 -> 3
+    DeviceTensor q1 = f32_tensor(std::vector<float>(2 * 4 * D, 0.0f), shp({1, 2, 4 * D}));
+    DeviceTensor k1 = f32_tensor(std::vector<float>(2 * 2 * D, 1.0f), shp({1, 2, 2 * D}));
+    DeviceTensor v1 = f32_tensor(std::vector<float>(2 * 2 * D, 2.0f), shp({1, 2, 2 * D}));
+    AttentionOutputs o1 = must(op_group_query_attention(rt, {&q1, &k1, &v1}, 4, 2, std::nullopt, -1, false, false),
+                               "call 1");
+    REQUIRE(o1.present_key.shape == shp({1, 2, 2, D}), "present 1");
+    DeviceTensor q2 = f32_tensor(std::vector<float>(4 * D, 0.0f), shp({1, 1, 4 * D}));
+    DeviceTensor k2 = f32_tensor(std::vector<float>(2 * D, 3.0f), shp({1, 1, 2 * D}));
+    DeviceTensor v2 = f32_tensor(std::vector<float>(2 * D, 4.0f), shp({1, 1, 2 * D}));
+    AttentionOutputs o2 = must(op_group_query_attention(rt, {&q2, &k2, &v2, &o1.present_key, &o1.present_value},
+                                                        4, 2, std::nullopt, -1, false, false),
+                               "call 2");
+    REQUIRE(o2.present_key.shape == shp({1, 2, 3, D}), "present 2");
+    // Q = 0: uniform over the 3 keys -> (2 + 2 + 4) / 3 in every value dim
+    for (float x : host_f32(o2.attn)) REQUIRE(std::fabs(x - 8.0f / 3.0f) < 0.02f, "mean %g", x);
+  }
+  {  // errors
+    DeviceTensor q = f32_tensor(std::vector<float>(4 * D, 0.0f), shp({1, 1, 4 * D}));
+    DeviceTensor k = f32_tensor(std::vector<float>(2 * D, 0.0f), shp({1, 1, 2 * D}));
+    DeviceTensor bad_past = f32_tensor(std::vector<float>(2 * 2 * D, 0.0f), shp({1, 2, 2 * D}));
+    DeviceTensor past = f32_tensor(std::vector<float>(2 * D, 0.0f), shp({1, 2, 1, D}));
+    auto gqa = [&](std::vector<const DeviceTensor*> in, int64_t lw, bool rot) {
+      return op_group_query_attention(rt, in, 4, 2, std::nullopt, lw, rot, false);
+    };
+    OpError e = must_fail(gqa({&q, &k, &k}, 512, false), "local window");
+    REQUIRE(e.kind == OpError::Kind::InvalidAttribute &&
+                e.message == "GroupQueryAttention: local_window_size != -1 not supported in this tier", "%s", e.to_string().c_str());
+    e = must_fail(gqa({&q, &k}, -1, false), "missing value");
+    REQUIRE(e.message == "GroupQueryAttention: missing value", "%s", e.to_string().c_str());
+    e = must_fail(gqa({&q, &k, &k}, -1, true), "do_rotary without tables");
+    REQUIRE(e.message == "GroupQueryAttention: do_rotary=1 but cos_cache is missing", "%s", e.to_string().c_str());
+    e = must_fail(gqa({&q, &k, &k, &bad_past}, -1, false), "past rank");
+    REQUIRE(e.message == "GroupQueryAttention: past_key must be rank-4", "%s", e.to_string().c_str());
+    e = must_fail(gqa({&q, &k, &k, &past}, -1, false), "past_value missing");
+    REQUIRE(e.message == "GroupQueryAttention: past_key / past_value sequence mismatch", "%s", e.to_string().c_str());
+    DeviceTensor odd = f32_tensor(std::vector<float>(3 * D, 0.0f), shp({1, 1, 3 * D}));
+    e = must_fail(op_group_query_attention(rt, {&odd, &k, &k}, 3, 2, std::nullopt, -1, false, false), "heads");
+    REQUIRE(e.kind == OpError::Kind::InvalidAttribute, "%s", e.to_string().c_str());
+    DeviceTensor m = f32_tensor(std::vector<float>(4 * D, 0.0f), shp({1, 1, 4 * D}));
+    DeviceTensor r2 = f32_tensor(std::vector<float>(4 * D, 0.0f), shp({1, 4 * D}));
+    e = must_fail(op_multi_head_attention(rt, {&r2, &m, &m}, 2, std::nullopt), "mha rank");
+    REQUIRE(e.message == "MultiHeadAttention: Q/K/V must be rank-3 (B, Sq, hidden)", "%s", e.to_string().c_str());
+    e = must_fail(op_multi_head_attention(rt, {&m, &m, &m}, 3, std::nullopt), "mha heads");
+    REQUIRE(e.message == "MultiHeadAttention: hidden not divisible by num_heads", "%s", e.to_string().c_str());
+    DeviceTensor mp = f32_tensor(std::vector<float>(4 * D, 0.0f), shp({1, 4, 1, D}));
+    e = must_fail(op_multi_head_attention(rt, {&m, &m, &m, nullptr, nullptr, nullptr, &mp}, 4, std::nullopt),
+                  "mha missing past_value");
+    REQUIRE(e.message == "MultiHeadAttention: past_key/past_value sequence length mismatch", "%s", e.to_string().c_str());
+    DeviceTensor d3 = f32_tensor(std::vector<float>(4 * 24, 0.0f), shp({1, 1, 4 * 24}));
+    e = must_fail(op_multi_head_attention(rt, {&d3, &d3, &d3}, 4, std::nullopt), "mha head_dim 24");
+    REQUIRE(e.kind == OpError::Kind::UnsupportedOp, "%s", e.to_string().c_str());
+  }
+}
+
 // test_kv_cache_sliding_window (tests/test_cuda.rs:1275-1334): a global layer
 // and a sliding-window layer of 4; after 6 tokens the global view holds 6,
 // the local view the last 4 (positions 2..5), read back by value.
@@ -923,6 +1098,9 @@ int main(int argc, char** argv) {
       {"gpu_session_int8_windows", true, gpu_session_int8_windows},
       {"gpu_session_int4_layer_window", true, gpu_session_int4_layer_window},
       {"gpu_cache_sliding_window", true, gpu_cache_sliding_window},
+      {"gpu_cpu_op_gqa_with_past", true, gpu_cpu_op_gqa_with_past},
+      {"gpu_cpu_op_mha_with_past", true, gpu_cpu_op_mha_with_past},
+      {"gpu_cpu_op_kats", true, gpu_cpu_op_kats},
   };
   std::vector<const Case*> run;
   for (int i = 1; i < argc; ++i) {
