@@ -85,7 +85,8 @@ def build_host() -> str:
     tmp = HOST_LIB + ".tmp"
     _run([CXX, "-std=c++17", "-O2", "-fPIC", "-shared", "-ffp-contract=off", "-Wall", "-Wextra",
           "-D__HIP_PLATFORM_AMD__", "-I", INCLUDE, "-I", "/opt/rocm/include",
-          os.path.join(HERE, "host", "gqa_host.cpp"), "-o", tmp,
+          os.path.join(HERE, "host", "gqa_host.cpp"), os.path.join(HERE, "host", "gqa_session.cpp"),
+          "-o", tmp,
           "-L", HERE, "-lsai_hip", "-L", "/opt/rocm/lib", "-lamdhip64",
           "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib"])
     os.replace(tmp, HOST_LIB)

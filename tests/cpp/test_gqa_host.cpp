@@ -22,6 +22,7 @@
 
 #include "../../oracle/sai_oracle.h"
 #include "../../smallaios_amd/host/gqa_host.hpp"
+#include "../../smallaios_amd/host/gqa_session.hpp"
 
 using namespace sai::rocm;
 
@@ -48,6 +49,12 @@ T must(Result<T, E>&& r, const char* what) {
 
 template <class T>
 OpError must_fail(Result<T, OpError>&& r, const char* what) {
+  if (r) throw Failure{std::string(what) + ": expected an error"};
+  return r.error();
+}
+
+template <class T>
+SessionError must_fail_session(Result<T, SessionError>&& r, const char* what) {
   if (r) throw Failure{std::string(what) + ": expected an error"};
   return r.error();
 }
@@ -1036,6 +1043,152 @@ void gpu_cpu_op_kats() {
   }
 }
 
+// RoPE of [B, S, H*D] rows at positions start + s, through the oracle's
+// apply_rope on the [B, H, S, D] view.
+static void oracle_rope_bshd(std::vector<float>& x, int B, int S, int H, int D, int start,
+                             const std::vector<float>& cs, const std::vector<float>& sn, int rows) {
+  std::vector<float> v(x.size());
+  for (int b = 0; b < B; ++b)
+    for (int s = 0; s < S; ++s)
+      for (int h = 0; h < H; ++h)
+        for (int d = 0; d < D; ++d)
+          v[(((size_t)b * H + h) * S + s) * D + d] = x[(((size_t)b * S + s) * H + h) * D + d];
+  std::vector<int64_t> ids(S);
+  for (int s = 0; s < S; ++s) ids[s] = start + s;
+  REQUIRE(sai_or_apply_rope(v.data(), B, H, S, D, cs.data(), sn.data(), rows, D / 2, ids.data(), S, 0, D) == 0,
+          "oracle rope");
+  for (int b = 0; b < B; ++b)
+    for (int s = 0; s < S; ++s)
+      for (int h = 0; h < H; ++h)
+        for (int d = 0; d < D; ++d)
+          x[(((size_t)b * S + s) * H + h) * D + d] = v[(((size_t)b * H + h) * S + s) * D + d];
+}
+
+// session.rs:579-593
+void cpu_layer_kinds_for_gemma() {
+  const auto k = layer_kinds_for_gemma(6, 16, 2);
+  REQUIRE(k.size() == 6, "count");
+  for (size_t i = 0; i < 6; ++i) {
+    const bool global = (i + 1) % 2 == 0;
+    REQUIRE((k[i].tag == LayerKind::Tag::Global) == global, "layer %zu", i);
+    if (!global) REQUIRE(k[i].window == 16, "window");
+  }
+  const auto k5 = layer_kinds_for_gemma(5, 0, 6);  // last layer global, window at least 1
+  REQUIRE(k5[4].tag == LayerKind::Tag::Global && k5[0].window == 1, "pattern 6 of 5 layers");
+  REQUIRE(SessionError::execution("x").to_string() == "execution failed: x", "display");
+}
+
+// A Gemma-shaped attention graph driven through GpuSession: per layer two
+// RotaryEmbedding nodes ([x, cos, sin]: the start is the cache position) and
+// one GroupQueryAttention node (local_window_size on the sliding layers);
+// layer kinds from layer_kinds_for_gemma. A prefill pass, decode passes, then
+// reset_kv_cache and a fresh pass, each checked against the oracle (RoPE by
+// apply_rope, the int8 cache by kv_append without rotation, attention with
+// both window rules).
+void gpu_session_gemma_graph() {
+  const int L = 4, B = 2, Hq = 8, Hkv = 2, D = 128, W = 24, rows = 160;
+  SessionConfig cfg;
+  cfg.num_hidden_layers = L;
+  cfg.num_key_value_heads = Hkv;
+  cfg.head_dim = D;
+  cfg.max_seq_len = 128;
+  cfg.max_batch = B;
+  cfg.sliding_window = W;
+  cfg.sliding_window_pattern = 2;
+  std::vector<ExecutionNode> graph;
+  std::vector<std::string> outs;
+  for (int l = 0; l < L; ++l) {
+    const std::string i = std::to_string(l);
+    graph.push_back({"rope_q" + i, "RotaryEmbedding", {"q" + i, "cos", "sin"}, {"qr" + i},
+                     {AttributeProto::make_int("rotary_embedding_dim", D), AttributeProto::make_int("interleaved", 0)}});
+    graph.push_back({"rope_k" + i, "RotaryEmbedding", {"k" + i, "cos", "sin"}, {"kr" + i},
+                     {AttributeProto::make_int("rotary_embedding_dim", D), AttributeProto::make_int("interleaved", 0)}});
+    std::vector<AttributeProto> a = {AttributeProto::make_int("num_heads", Hq), AttributeProto::make_int("kv_num_heads", Hkv)};
+    if (l % 2 == 0) a.push_back(AttributeProto::make_int("local_window_size", W));
+    graph.push_back({"gqa" + i, "GroupQueryAttention", {"qr" + i, "kr" + i, "v" + i, "", ""},
+                     {"attn" + i, "present_k" + i, "present_v" + i}, a});
+    outs.push_back("attn" + i);
+  }
+  auto session = must(GpuSession::create(0, cfg, graph, outs), "GpuSession::create");
+  REQUIRE(session->layer_kinds()[0].tag == LayerKind::Tag::SlidingWindow && session->layer_kinds()[1].tag == LayerKind::Tag::Global,
+          "layer kinds");
+  std::vector<float> cs, sn;
+  rope_tables(rows, D, 10000.0, cs, sn);
+  // oracle state per layer: int8 codes of the rotated keys
+  const int T = 128;
+  struct Lay { std::vector<int8_t> k8, v8; std::vector<float> ks, vs; };
+  std::vector<Lay> lay(L);
+  auto clear = [&]() {
+    for (Lay& x : lay) {
+      x.k8.assign((size_t)B * Hkv * T * D, 0); x.v8.assign(x.k8.size(), 0);
+      x.ks.assign((size_t)B * Hkv * T, 0.0f); x.vs.assign(x.ks.size(), 0.0f);
+    }
+  };
+  clear();
+  std::mt19937_64 gen(61);
+  int pos = 0;
+  auto pass = [&](int S, const char* what) {
+    std::vector<std::pair<std::string, DeviceTensor>> in;
+    in.emplace_back("cos", f32_tensor(cs, shp({rows, D / 2})));
+    in.emplace_back("sin", f32_tensor(sn, shp({rows, D / 2})));
+    std::vector<std::vector<float>> qs(L), ks(L), vs(L);
+    for (int l = 0; l < L; ++l) {
+      const std::string i = std::to_string(l);
+      qs[l] = gauss(gen, (size_t)B * S * Hq * D);
+      ks[l] = gauss(gen, (size_t)B * S * Hkv * D);
+      vs[l] = gauss(gen, (size_t)B * S * Hkv * D);
+      in.emplace_back("q" + i, f32_tensor(qs[l], shp({B, S, (int64_t)Hq * D})));
+      in.emplace_back("k" + i, f32_tensor(ks[l], shp({B, S, (int64_t)Hkv * D})));
+      in.emplace_back("v" + i, f32_tensor(vs[l], shp({B, S, (int64_t)Hkv * D})));
+    }
+    auto got = must(session->run(std::move(in)), what);
+    REQUIRE(got.size() == (size_t)L, "%s: outputs", what);
+    for (int l = 0; l < L; ++l) {
+      std::vector<float> q = qs[l], k = ks[l];
+      oracle_rope_bshd(q, B, S, Hq, D, pos, cs, sn, rows);
+      oracle_rope_bshd(k, B, S, Hkv, D, pos, cs, sn, rows);
+      std::vector<int32_t> start(B, pos), lens(B, pos + S);
+      REQUIRE(sai_or_kv_append(k.data(), vs[l].data(), B, S, Hkv, D, start.data(), nullptr, nullptr, 0, 0, 0, 1,
+                               T, lay[l].k8.data(), lay[l].v8.data(), lay[l].ks.data(), lay[l].vs.data(), nullptr,
+                               nullptr) == 0,
+              "oracle append");
+      std::vector<float> kd((size_t)B * Hkv * T * D), vd(kd.size());
+      REQUIRE(sai_or_kv_dequant(B, Hkv, D, 1, T, lens.data(), lay[l].k8.data(), lay[l].v8.data(), lay[l].ks.data(),
+                                lay[l].vs.data(), nullptr, nullptr, kd.data(), vd.data()) == 0,
+              "oracle dequant");
+      std::vector<float> want((size_t)B * S * Hq * D);
+      const bool sliding = l % 2 == 0;
+      REQUIRE(sai_or_gqa_cached_window(q.data(), B, S, Hq, Hkv, D, lens.data(), T, kd.data(), vd.data(), nullptr,
+                                       nullptr, 0, 0, 0, 0, 0.0f, sliding ? W : 0, sliding ? W : -1,
+                                       want.data()) == 0,
+              "oracle attention");
+      char w[96];
+      std::snprintf(w, sizeof w, "%s layer %d", what, l);
+      close(host_f32(got[l]), want, w);
+    }
+    pos += S;
+    REQUIRE(session->position() == (size_t)pos, "%s: position %zu", what, session->position());
+  };
+  pass(40, "prefill pass");
+  for (int step = 0; step < 6; ++step) pass(1, "decode pass");
+  must(session->reset_kv_cache(), "reset");
+  REQUIRE(session->position() == 0, "reset position");
+  clear();
+  pos = 0;
+  pass(9, "pass after reset");
+  pass(1, "decode after reset");
+  // errors: an op this library does not implement, an output never produced
+  std::vector<ExecutionNode> g2 = {{"mm", "MatMul", {"a", "b"}, {"c"}, {}}};
+  auto s2 = must(GpuSession::create(0, cfg, g2, {"c"}), "create");
+  SessionError e = must_fail_session(s2->run({}), "MatMul");
+  REQUIRE(e.to_string() == "execution failed: mm: internal error: GPU executor: no GPU implementation for MatMul",
+          "%s", e.to_string().c_str());
+  auto s3 = must(GpuSession::create(0, cfg, {}, {"nothing"}), "create");
+  e = must_fail_session(s3->run({}), "missing output");
+  REQUIRE(e.to_string() == "execution failed: GPU executor: output tensor 'nothing' not produced", "%s",
+          e.to_string().c_str());
+}
+
 // test_kv_cache_sliding_window (tests/test_cuda.rs:1275-1334): a global layer
 // and a sliding-window layer of 4; after 6 tokens the global view holds 6,
 // the local view the last 4 (positions 2..5), read back by value.
@@ -1079,6 +1232,7 @@ int main(int argc, char** argv) {
       {"cpu_attrs", false, cpu_attrs},
       {"cpu_validate", false, cpu_validate},
       {"cpu_errors_and_types", false, cpu_errors_and_types},
+      {"cpu_layer_kinds_for_gemma", false, cpu_layer_kinds_for_gemma},
       {"gpu_cache_allocate_and_append", true, gpu_cache_allocate_and_append},
       {"gpu_cache_multiple_tokens", true, gpu_cache_multiple_tokens},
       {"gpu_cache_reset", true, gpu_cache_reset},
@@ -1101,6 +1255,7 @@ int main(int argc, char** argv) {
       {"gpu_cpu_op_gqa_with_past", true, gpu_cpu_op_gqa_with_past},
       {"gpu_cpu_op_mha_with_past", true, gpu_cpu_op_mha_with_past},
       {"gpu_cpu_op_kats", true, gpu_cpu_op_kats},
+      {"gpu_session_gemma_graph", true, gpu_session_gemma_graph},
   };
   std::vector<const Case*> run;
   for (int i = 1; i < argc; ++i) {

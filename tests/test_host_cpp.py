@@ -6,9 +6,12 @@ The CPU case covers attribute parsing, gqa_validate's messages
 (onnx-rt/src/ops/microsoft.rs:933-984) and the error types. The GPU case runs,
 in one child process, the restated reference cache tests
 (onnx-rt/tests/test_cuda.rs:1124-1375), the first-token GQA tests
-(test_cuda.rs:3426-3525), dispatch_gqa's error contract, and four multi-layer
-prefill/decode sessions checked against the oracle (outputs within
-2e-3 abs + 1e-2 rel, cache contents bit-exact).
+(test_cuda.rs:3426-3525), dispatch_gqa's error contract, multi-layer
+prefill/decode sessions (global and sliding-window layers, local_window_size)
+checked against the oracle (outputs within 2e-3 abs + 1e-2 rel, cache contents
+bit-exact), the RotaryEmbedding op and dispatcher (bit-exact), the CPU
+attention ops with explicit past/present (present bit-exact), and a
+Gemma-shaped graph run through GpuSession (gqa_session.hpp).
 """
 import os
 import subprocess
