@@ -264,6 +264,79 @@ sai_status sai_copy_rows(sai_ctx* ctx, const void* src, int32_t src_layout, void
 sai_status sai_rope_tables(sai_ctx* ctx, float rope_theta, int32_t max_pos, int32_t half,
                            int32_t dtype, void* cos_out, void* sin_out, void* stream);
 
+/* ---- TurboQuant compressed KV cache -------------------------------------------
+ * Replaces CompressedKVCache (onnx-rt/src/kv_compression.rs:738-963, with
+ * kv_lowrank_k = None) on the device, plus the decode read path of its design
+ * (docs/kv-compression-design.md section 9). Each row (token, kv head) of K
+ * and of V is PolarQuant-encoded with the head's quantizer (xorshift64 signs
+ * seeded seed * 0x9E3779B97F4A7C15 + layer * num_kv_heads + head, normalised
+ * Walsh-Hadamard rotation, one min/max quantiser of `bits` bits over the
+ * rotated row) and, with qjl, its QJL residual (sign bits of x - decode, mean
+ * |residual|); codes, scale, zero point, sign bits and mean are the
+ * reference's bit for bit. Every sequence of a pass appends the same number
+ * of rows (pending until sai_tqcache_advance), as the paged cache does. */
+typedef struct sai_tqcache sai_tqcache;
+typedef struct sai_tqcache_desc {
+  int32_t num_layers;
+  int32_t num_kv_heads;
+  int32_t head_dim;  /* 64 or 128 */
+  int32_t bits;      /* 3, 4 or 8 (kv_quant_bits) */
+  int32_t qjl;       /* kv_qjl_residual */
+  int32_t max_batch; /* sequences */
+  int32_t max_rows;  /* rows per sequence */
+  uint64_t seed;     /* KVCacheConfig::seed */
+} sai_tqcache_desc;
+/* Allocates the layers' storage and uploads the rotation signs. Synchronous.
+ * Errors: SHAPE_MISMATCH (zero sizes), UNSUPPORTED (head_dim),
+ * INVALID_ATTRIBUTE ("bits must be 3, 4, or 8"), ALLOC. */
+sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc, sai_tqcache** out);
+void sai_tqcache_destroy(sai_tqcache* cache);
+/* CompressedKVCache::write_kv for every kv head of `layer`: k, v device
+ * [batch, s_new, num_kv_heads*head_dim] (F32 or BF16) become rows
+ * len[b] .. len[b] + s_new - 1 (pending). Errors: SHAPE_MISMATCH (layer,
+ * sizes, a pass mixing row counts), OVERFLOW (past max_rows), UNSUPPORTED. */
+sai_status sai_tqcache_write(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, const void* k,
+                             const void* v, int32_t dtype, int32_t batch, int32_t s_new,
+                             void* stream);
+/* Commit the pending rows (one call per pass; none pending: no-op).
+ * Stream-ordered. */
+sai_status sai_tqcache_advance(sai_ctx* ctx, sai_tqcache* cache, void* stream);
+/* Committed lengths of sequences 0..batch-1 (<= max_rows; rows beyond a
+ * length are ignored), dropping anything pending; the next pass has `batch`
+ * sequences. Synchronous. Errors: SHAPE_MISMATCH, OVERFLOW. */
+sai_status sai_tqcache_set_lengths(sai_ctx* ctx, sai_tqcache* cache, const int32_t* lens,
+                                   int32_t batch);
+/* All lengths back to 0 (storage kept). Synchronous. */
+sai_status sai_tqcache_reset(sai_ctx* ctx, sai_tqcache* cache);
+/* Host view: lens_out[max_batch] committed rows, *pending_out, *batch_out. */
+sai_status sai_tqcache_lengths(const sai_tqcache* cache, int32_t* lens_out, int32_t* pending_out,
+                               int32_t* batch_out);
+/* read_k / read_v (kv_compression.rs:862-907): rows [start, start+len) of
+ * (layer, sequence b, kv head) decoded to f32, host arrays [len][head_dim]
+ * each. Synchronous. */
+sai_status sai_tqcache_read(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, int32_t b,
+                            int32_t head, int32_t start, int32_t len, float* k_out,
+                            float* v_out);
+/* The stored form of the same rows (host, any output may be NULL): codes
+ * [len][head_dim*bits/8] packed LSB first, params [len][3] f32 (scale,
+ * zero point, QJL mean), QJL sign words [len][head_dim/64] u64 (qjl only).
+ * Synchronous. */
+sai_status sai_tqcache_read_raw(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, int32_t b,
+                                int32_t head, int32_t start, int32_t len, void* k_codes,
+                                void* v_codes, float* k_params, float* v_params, void* k_signs,
+                                void* v_signs);
+/* Decode attention over the committed + pending rows of `layer`: for query
+ * head h (kv head h / (num_heads / num_kv_heads)) the logit of row t is the
+ * module's inner-product estimate <decode(q), decode(k_t)> + (qjl ?
+ * correction(residual(q), residual(k_t)) : 0) (kv_compression.rs:1254-1288),
+ * evaluated on the codes in the rotated domain; softmax(scale * logits); out
+ * = sum_t w_t decode(v_t), rotated back once. q: device [batch, 1,
+ * num_heads*head_dim] (F32 or BF16); out: device f32, same shape; scale when
+ * has_scale, else sai_default_scale(head_dim). */
+sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, const void* q,
+                              int32_t dtype, int32_t batch, int32_t num_heads, int32_t has_scale,
+                              float scale, float* out, void* stream);
+
 /* ---- tuning / introspection ------------------------------------------------- */
 /* Tokens per split-K work item of the decode kernel (0 = automatic, else a
  * multiple of 64). Returns the previous value. */

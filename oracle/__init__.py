@@ -88,6 +88,17 @@ def _declare(L: C.CDLL) -> None:
         "sai_or_sin_approx": (_f, [_f]),
         "sai_or_cos_approx": (_f, [_f]),
         "sai_or_rope_tables_bf16": (None, [_i, _i, _f, _p, _p]),
+        "sai_or_tq_signs": (None, [C.c_uint64, _i, _p]),
+        "sai_or_tq_head_seed": (C.c_uint64, [C.c_uint64, _i, _i, _i]),
+        "sai_or_wht_with_signs": (None, [_p, _p, _i]),
+        "sai_or_inverse_wht_with_signs": (None, [_p, _p, _i]),
+        "sai_or_tq_encode": (_i, [_p, _i, _i, _p, _p, _p, _p, _p, _p]),
+        "sai_or_tq_decode": (None, [_p, _i, _i, _f, _f, _p, _p]),
+        "sai_or_qjl_encode": (None, [_p, _p, _i, _p, _p]),
+        "sai_or_qjl_correction": (_f, [_p, _f, _p, _f, _i]),
+        "sai_or_tq_write_row": (_i, [_p, _i, _i, _p, _i, _p, _p, _p, _p, _p]),
+        "sai_or_tq_attend": (_i, [_p, _i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p,
+                                  _f, _p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -189,6 +200,104 @@ def f32_to_bf16_bits(x) -> np.ndarray:
     nan = np.isnan(np.ascontiguousarray(x, dtype=np.float32))
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
     return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+# ------------------------------------------------------------- TurboQuant ---
+def tq_signs(seed: int, dim: int) -> np.ndarray:
+    """PolarQuantizer::new's sign flips (xorshift64), int8 [dim] of +-1."""
+    s = np.empty(dim, np.int8)
+    lib().sai_or_tq_signs(C.c_uint64(seed & (2**64 - 1)), dim, _ptr(s))
+    return s
+
+
+def tq_head_seed(seed: int, layer: int, num_kv_heads: int, head: int) -> int:
+    return int(lib().sai_or_tq_head_seed(C.c_uint64(seed & (2**64 - 1)), layer, num_kv_heads,
+                                         head))
+
+
+def wht(x, signs, inverse=False):
+    y = _f32(x).copy()
+    sg = np.ascontiguousarray(signs, np.int8)
+    f = lib().sai_or_inverse_wht_with_signs if inverse else lib().sai_or_wht_with_signs
+    f(_ptr(y), _ptr(sg), y.size)
+    return y
+
+
+def tq_encode(x, bits: int, signs):
+    """PolarQuantizer::encode -> (packed u8, scale, zero, min, max)."""
+    x = _f32(x)
+    d = x.size
+    packed = np.zeros((d * bits + 7) // 8, np.uint8)
+    sc, z, mn, mx = (C.c_float() for _ in range(4))
+    sg = np.ascontiguousarray(signs, np.int8)
+    rc = lib().sai_or_tq_encode(_ptr(x), d, bits, _ptr(sg), _ptr(packed), C.byref(sc),
+                                C.byref(z), C.byref(mn), C.byref(mx))
+    _check(rc, "tq_encode")
+    return packed, sc.value, z.value, mn.value, mx.value
+
+
+def tq_decode(packed, dim: int, bits: int, scale: float, zero: float, signs):
+    out = np.empty(dim, np.float32)
+    p = np.ascontiguousarray(packed, np.uint8)
+    sg = np.ascontiguousarray(signs, np.int8)
+    lib().sai_or_tq_decode(_ptr(p), dim, bits, float(scale), float(zero), _ptr(sg), _ptr(out))
+    return out
+
+
+def qjl_encode(original, approx):
+    o, a = _f32(original), _f32(approx)
+    bits = np.zeros(max(1, (o.size + 63) // 64), np.uint64)
+    c = C.c_float()
+    lib().sai_or_qjl_encode(_ptr(o), _ptr(a), o.size, _ptr(bits), C.byref(c))
+    return bits, c.value
+
+
+def qjl_correction(a_bits, a_c, b_bits, b_c, dim: int) -> float:
+    a = np.ascontiguousarray(a_bits, np.uint64)
+    b = np.ascontiguousarray(b_bits, np.uint64)
+    return float(lib().sai_or_qjl_correction(_ptr(a), float(a_c), _ptr(b), float(b_c), dim))
+
+
+def tq_write_rows(x, bits: int, signs, qjl: bool):
+    """CompressedKVCache::write_kv over rows x [n, D]: (codes [n, D*bits/8],
+    scale [n], zero [n], sign words [n, D/64], c [n])."""
+    x = _f32(x)
+    n, d = x.shape
+    cb, w = (d * bits + 7) // 8, (d + 63) // 64
+    codes = np.zeros((n, cb), np.uint8)
+    sc = np.zeros(n, np.float32)
+    z = np.zeros(n, np.float32)
+    sb = np.zeros((n, w), np.uint64)
+    c = np.zeros(n, np.float32)
+    sg = np.ascontiguousarray(signs, np.int8)
+    for t in range(n):
+        st, zt, ct = C.c_float(), C.c_float(), C.c_float()
+        row = np.ascontiguousarray(x[t])
+        rc = lib().sai_or_tq_write_row(_ptr(row), d, bits, _ptr(sg), int(qjl),
+                                       codes[t].ctypes.data_as(C.c_void_p), C.byref(st),
+                                       C.byref(zt), sb[t].ctypes.data_as(C.c_void_p),
+                                       C.byref(ct))
+        _check(rc, "tq_write_row")
+        sc[t], z[t], c[t] = st.value, zt.value, ct.value
+    return codes, sc, z, sb, c
+
+
+def tq_attend(q, bits, qjl, signs, k, v, scale):
+    """Decode attention of q [G, D] over encoded rows k/v = tq_write_rows
+    outputs; returns [G, D]."""
+    q = _f32(q)
+    g, d = q.shape
+    kc, ks, kz, ksb, kcm = k
+    vc, vs, vz, _, _ = v
+    out = np.zeros((g, d), np.float32)
+    sg = np.ascontiguousarray(signs, np.int8)
+    rc = lib().sai_or_tq_attend(_ptr(q), g, d, bits, int(qjl), _ptr(sg), kc.shape[0],
+                                _ptr(np.ascontiguousarray(kc)), _ptr(ks), _ptr(kz),
+                                _ptr(np.ascontiguousarray(ksb)), _ptr(kcm),
+                                _ptr(np.ascontiguousarray(vc)), _ptr(vs), _ptr(vz),
+                                float(scale), _ptr(out))
+    _check(rc, "tq_attend")
+    return out
 
 
 # ------------------------------------------------------------ RoPE / SDPA ---

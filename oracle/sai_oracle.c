@@ -779,3 +779,185 @@ uint64_t sai_or_check_rhe_vs_rint(uint64_t lo, uint64_t hi) {
   }
   return bad;
 }
+
+/* ------------------------------------------------------------------------
+ * TurboQuant compressed KV (onnx-rt/src/kv_compression.rs), restated:
+ * Xorshift64 (:44-67), wht_butterfly_normalize (:81-110), apply_signs
+ * (:113-118), wht_with_signs / inverse_wht_with_signs (:124-140),
+ * PolarQuantizer::new / encode / decode (:197-291), QJLResidualEncoder
+ * encode / correction (:365-419), CompressedKVCache seeds (:766-790).
+ * ---------------------------------------------------------------------- */
+static uint64_t tq_xorshift_next(uint64_t* st) {
+  uint64_t x = *st;
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  *st = x;
+  return x;
+}
+
+void sai_or_tq_signs(uint64_t seed, int dim, int8_t* signs) {
+  uint64_t st = seed ? seed : 0x5EEDDEADBEEFCAFEull;
+  for (int i = 0; i < dim; ++i) signs[i] = (tq_xorshift_next(&st) & 1u) == 0 ? 1 : -1;
+}
+
+uint64_t sai_or_tq_head_seed(uint64_t seed, int layer, int num_kv_heads, int head) {
+  return seed * 0x9E3779B97F4A7C15ull + (uint64_t)((size_t)layer * num_kv_heads + head);
+}
+
+static void tq_butterfly_normalize(float* x, int n) {
+  for (int h = 1; h < n; h *= 2)
+    for (int i = 0; i < n; i += 2 * h)
+      for (int j = i; j < i + h; ++j) {
+        float a = x[j], b = x[j + h];
+        x[j] = a + b;
+        x[j + h] = a - b;
+      }
+  float scale = 1.0f / sai_or_sqrt_approx((float)n);
+  for (int i = 0; i < n; ++i) x[i] *= scale;
+}
+
+void sai_or_wht_with_signs(float* x, const int8_t* signs, int n) {
+  for (int i = 0; i < n; ++i) x[i] *= (float)signs[i];
+  tq_butterfly_normalize(x, n);
+}
+
+void sai_or_inverse_wht_with_signs(float* x, const int8_t* signs, int n) {
+  tq_butterfly_normalize(x, n);
+  for (int i = 0; i < n; ++i) x[i] *= (float)signs[i];
+}
+
+int sai_or_tq_encode(const float* input, int dim, int bits, const int8_t* signs, uint8_t* packed,
+                     float* scale_out, float* zero_out, float* min_out, float* max_out) {
+  if (dim <= 0 || (dim & (dim - 1)) != 0) return ERR_INVALID_ATTRIBUTE;
+  if (bits != 3 && bits != 4 && bits != 8) return ERR_INVALID_ATTRIBUTE;
+  float* rot = (float*)malloc(sizeof(float) * (size_t)dim);
+  uint32_t* q = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)dim);
+  memcpy(rot, input, sizeof(float) * (size_t)dim);
+  sai_or_wht_with_signs(rot, signs, dim);
+  float mn = INFINITY, mx = -INFINITY;
+  for (int i = 0; i < dim; ++i) {
+    if (rot[i] < mn) mn = rot[i];
+    if (rot[i] > mx) mx = rot[i];
+  }
+  uint32_t levels = (1u << bits) - 1u;
+  float range = mx - mn;
+  float scale = range > 0.0f ? range / (float)levels : 1.0f;
+  float zero = mn;
+  for (int i = 0; i < dim; ++i) {
+    uint32_t v = scale > 0.0f ? sai_or_sat_u32(sai_or_round_f32_kv((rot[i] - zero) / scale)) : 0u;
+    q[i] = v < levels ? v : levels;
+  }
+  sai_or_pack_bits(q, (size_t)dim, bits, packed);
+  *scale_out = scale;
+  *zero_out = zero;
+  if (min_out) *min_out = mn;
+  if (max_out) *max_out = mx;
+  free(rot);
+  free(q);
+  return OK;
+}
+
+void sai_or_tq_decode(const uint8_t* packed, int dim, int bits, float scale, float zero,
+                      const int8_t* signs, float* out) {
+  uint32_t* q = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)dim);
+  sai_or_unpack_bits(packed, ((size_t)dim * bits + 7) / 8, (size_t)dim, bits, q);
+  for (int i = 0; i < dim; ++i) out[i] = (float)q[i] * scale + zero;
+  sai_or_inverse_wht_with_signs(out, signs, dim);
+  free(q);
+}
+
+void sai_or_qjl_encode(const float* original, const float* approx, int dim, uint64_t* sign_bits,
+                       float* c_out) {
+  int words = (dim + 63) / 64;
+  for (int w = 0; w < words; ++w) sign_bits[w] = 0;
+  float sum = 0.0f;
+  for (int i = 0; i < dim; ++i) {
+    float r = original[i] - approx[i];
+    sum += fabsf(r);
+    if (r >= 0.0f) sign_bits[i / 64] |= 1ull << (i % 64);
+  }
+  *c_out = dim > 0 ? sum / (float)dim : 0.0f;
+}
+
+float sai_or_qjl_correction(const uint64_t* a_bits, float a_c, const uint64_t* b_bits, float b_c,
+                            int dim) {
+  if (dim == 0) return 0.0f;
+  uint32_t pop = 0;
+  for (int w = 0; w < (dim + 63) / 64; ++w) pop += (uint32_t)__builtin_popcountll(a_bits[w] ^ b_bits[w]);
+  float sign_inner = (float)dim - 2.0f * (float)pop;
+  return a_c * b_c * sign_inner / (float)dim;
+}
+
+/* CompressedKVCache::write_kv for one (layer, head) row (kv_compression.rs:
+ * 814-860, low-rank K off): codes, scale, zero and, with qjl, the residual's
+ * sign bits and mean |r| of the decoded row. */
+int sai_or_tq_write_row(const float* x, int dim, int bits, const int8_t* signs, int qjl,
+                        uint8_t* packed, float* scale, float* zero, uint64_t* sign_bits,
+                        float* c) {
+  int rc = sai_or_tq_encode(x, dim, bits, signs, packed, scale, zero, NULL, NULL);
+  if (rc != OK || !qjl) return rc;
+  float* approx = (float*)malloc(sizeof(float) * (size_t)dim);
+  sai_or_tq_decode(packed, dim, bits, *scale, *zero, signs, approx);
+  sai_or_qjl_encode(x, approx, dim, sign_bits, c);
+  free(approx);
+  return OK;
+}
+
+/* Decode attention over one (sequence, kv head) of a TurboQuant cache, the
+ * read path of docs/kv-compression-design.md section 9 with the module's
+ * inner-product estimator (kv_compression.rs:1254-1288): for each of the G
+ * query heads, q is encoded with the head's quantizer; the logit of row t
+ * is <decode(q), decode(k_t)> + (qjl ? correction(res(q), res(k_t)) : 0);
+ * weights = softmax(scale * logits) as the SDPA softmax computes it
+ * (max-subtracted expf_approx, microsoft.rs:270-299); out = sum_t w_t
+ * decode(v_t). Row t's K/V: packed codes at k_codes + t*code_bytes, per-row
+ * scale/zero/c arrays, sign words at k_signs + t*words. */
+int sai_or_tq_attend(const float* q, int G, int dim, int bits, int qjl, const int8_t* signs,
+                     int rows, const uint8_t* k_codes, const float* k_scale, const float* k_zero,
+                     const uint64_t* k_signs, const float* k_c, const uint8_t* v_codes,
+                     const float* v_scale, const float* v_zero, float scale, float* out) {
+  int code_bytes = (dim * bits + 7) / 8, words = (dim + 63) / 64;
+  float* qd = (float*)malloc(sizeof(float) * (size_t)dim);
+  float* kd = (float*)malloc(sizeof(float) * (size_t)dim);
+  float* logits = (float*)malloc(sizeof(float) * (size_t)(rows ? rows : 1));
+  uint8_t* qp = (uint8_t*)malloc((size_t)code_bytes);
+  uint64_t* qs = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)words);
+  int rc = OK;
+  for (int h = 0; h < G && rc == OK; ++h) {
+    const float* qh = q + (size_t)h * dim;
+    float qsc, qz, qc = 0.0f;
+    rc = sai_or_tq_write_row(qh, dim, bits, signs, qjl, qp, &qsc, &qz, qs, &qc);
+    if (rc != OK) break;
+    sai_or_tq_decode(qp, dim, bits, qsc, qz, signs, qd);
+    float mx = -INFINITY;
+    for (int t = 0; t < rows; ++t) {
+      sai_or_tq_decode(k_codes + (size_t)t * code_bytes, dim, bits, k_scale[t], k_zero[t], signs, kd);
+      float dot = 0.0f;
+      for (int i = 0; i < dim; ++i) dot += qd[i] * kd[i];
+      if (qjl) dot += sai_or_qjl_correction(qs, qc, k_signs + (size_t)t * words, k_c[t], dim);
+      logits[t] = dot * scale;
+      if (logits[t] > mx) mx = logits[t];
+    }
+    float denom = 0.0f;
+    for (int t = 0; t < rows; ++t) {
+      logits[t] = sai_or_expf_approx(logits[t] - mx);
+      denom += logits[t];
+    }
+    float* o = out + (size_t)h * dim;
+    for (int i = 0; i < dim; ++i) o[i] = 0.0f;
+    if (rows == 0 || !(denom > 0.0f)) continue;
+    float inv = 1.0f / denom;
+    for (int t = 0; t < rows; ++t) {
+      sai_or_tq_decode(v_codes + (size_t)t * code_bytes, dim, bits, v_scale[t], v_zero[t], signs, kd);
+      float w = logits[t] * inv;
+      for (int i = 0; i < dim; ++i) o[i] += w * kd[i];
+    }
+  }
+  free(qd);
+  free(kd);
+  free(logits);
+  free(qp);
+  free(qs);
+  return rc;
+}

@@ -64,6 +64,27 @@ float sai_or_cos_approx(float x);
 void sai_or_rope_tables_bf16(int max_pos, int half, float rope_theta, uint16_t* cos_out,
                              uint16_t* sin_out);
 
+/* --- TurboQuant compressed KV (kv_compression.rs) ---------------------- */
+void sai_or_tq_signs(uint64_t seed, int dim, int8_t* signs);
+uint64_t sai_or_tq_head_seed(uint64_t seed, int layer, int num_kv_heads, int head);
+void sai_or_wht_with_signs(float* x, const int8_t* signs, int n);
+void sai_or_inverse_wht_with_signs(float* x, const int8_t* signs, int n);
+int sai_or_tq_encode(const float* input, int dim, int bits, const int8_t* signs, uint8_t* packed,
+                     float* scale_out, float* zero_out, float* min_out, float* max_out);
+void sai_or_tq_decode(const uint8_t* packed, int dim, int bits, float scale, float zero,
+                      const int8_t* signs, float* out);
+void sai_or_qjl_encode(const float* original, const float* approx, int dim, uint64_t* sign_bits,
+                       float* c_out);
+float sai_or_qjl_correction(const uint64_t* a_bits, float a_c, const uint64_t* b_bits, float b_c,
+                            int dim);
+int sai_or_tq_write_row(const float* x, int dim, int bits, const int8_t* signs, int qjl,
+                        uint8_t* packed, float* scale, float* zero, uint64_t* sign_bits,
+                        float* c);
+int sai_or_tq_attend(const float* q, int G, int dim, int bits, int qjl, const int8_t* signs,
+                     int rows, const uint8_t* k_codes, const float* k_scale, const float* k_zero,
+                     const uint64_t* k_signs, const float* k_c, const uint8_t* v_codes,
+                     const float* v_scale, const float* v_zero, float scale, float* out);
+
 /* --- RoPE / SDPA / GQA (f32 reference op) ------------------------------ */
 int sai_or_apply_rope(float* x, int b, int heads, int sq, int head_dim, const float* cos_cache,
                       const float* sin_cache, int cache_rows, int cache_cols,

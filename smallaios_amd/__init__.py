@@ -46,6 +46,14 @@ class _Desc(C.Structure):
     ]
 
 
+class _TqDesc(C.Structure):
+    _fields_ = [
+        ("num_layers", C.c_int32), ("num_kv_heads", C.c_int32), ("head_dim", C.c_int32),
+        ("bits", C.c_int32), ("qjl", C.c_int32), ("max_batch", C.c_int32),
+        ("max_rows", C.c_int32), ("seed", C.c_uint64),
+    ]
+
+
 def lib() -> C.CDLL:
     """Load libsai_hip.so (built in-tree by smallaios_amd/build.py)."""
     global _lib
@@ -76,7 +84,9 @@ EXPORTS = [
     "sai_gqa_decode", "sai_gqa_with_cache", "sai_gqa_prefill", "sai_set_decode_split",
     "sai_set_decode_waves", "sai_set_decode_merge", "sai_last_decode_shape",
     "sai_set_decode_timing", "sai_decode_kernel_times", "sai_rotary_embedding",
-    "sai_rope_tables", "sai_copy_rows",
+    "sai_rope_tables", "sai_copy_rows", "sai_tqcache_create", "sai_tqcache_destroy",
+    "sai_tqcache_write", "sai_tqcache_advance", "sai_tqcache_reset", "sai_tqcache_set_lengths",
+    "sai_tqcache_lengths", "sai_tqcache_read", "sai_tqcache_read_raw", "sai_tqcache_attend",
 ]
 ROPE_BHSD = 0
 ROPE_BSHD = 1
@@ -118,6 +128,16 @@ def _declare(L: C.CDLL) -> None:
                                        C.c_int64, p, p, i32, i32, i32, i32, i32, p]),
         "sai_rope_tables": (i32, [p, f, i32, i32, i32, p, p, p]),
         "sai_copy_rows": (i32, [p, p, i32, p, i32, i32, i32, i32, i32, i32, i32, i32, p]),
+        "sai_tqcache_create": (i32, [p, C.POINTER(_TqDesc), pp]),
+        "sai_tqcache_destroy": (None, [p]),
+        "sai_tqcache_write": (i32, [p, p, i32, p, p, i32, i32, i32, p]),
+        "sai_tqcache_advance": (i32, [p, p, p]),
+        "sai_tqcache_reset": (i32, [p, p]),
+        "sai_tqcache_set_lengths": (i32, [p, p, p, i32]),
+        "sai_tqcache_lengths": (i32, [p, p, p, p]),
+        "sai_tqcache_read": (i32, [p, p, i32, i32, i32, i32, i32, p, p]),
+        "sai_tqcache_read_raw": (i32, [p, p, i32, i32, i32, i32, i32, p, p, p, p, p, p]),
+        "sai_tqcache_attend": (i32, [p, p, i32, p, i32, i32, i32, i32, f, p, p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -392,6 +412,96 @@ class KvCache:
             _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary), int(interleaved),
             int(scale is not None), 0.0 if scale is None else float(scale), int(window),
             _dev_ptr(out), _stream(stream)), "gqa_prefill")
+
+
+class TqCache:
+    """sai_tqcache: the TurboQuant compressed KV cache (CompressedKVCache of
+    kv_compression.rs) on the device."""
+
+    def __init__(self, rt: Runtime, num_layers, num_kv_heads, head_dim, bits, qjl, max_batch,
+                 max_rows, seed=0):
+        self.rt = rt
+        self._L = rt._L
+        self.desc = _TqDesc(num_layers, num_kv_heads, head_dim, bits, int(bool(qjl)), max_batch,
+                            max_rows, seed & (2**64 - 1))
+        h = C.c_void_p()
+        rt.check(self._L.sai_tqcache_create(rt.handle, C.byref(self.desc), C.byref(h)),
+                 "tqcache_create")
+        self.handle = h
+        self.num_layers, self.kv_heads, self.head_dim = num_layers, num_kv_heads, head_dim
+        self.bits, self.qjl, self.max_batch = bits, bool(qjl), max_batch
+
+    def close(self):
+        if self.handle:
+            self._L.sai_tqcache_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def write(self, layer, k, v, batch, s_new, stream=None, dtype=None):
+        """k, v: device [batch, s_new, kv_heads*head_dim] (f32 or bf16)."""
+        dt = dtype if dtype is not None else _dtype_code(k)
+        self.rt.check(self._L.sai_tqcache_write(self.rt.handle, self.handle, layer, _dev_ptr(k),
+                                                _dev_ptr(v), dt, batch, s_new, _stream(stream)),
+                      "tqcache_write")
+
+    def advance(self, stream=None):
+        self.rt.check(self._L.sai_tqcache_advance(self.rt.handle, self.handle, _stream(stream)),
+                      "tqcache_advance")
+
+    def reset(self):
+        self.rt.check(self._L.sai_tqcache_reset(self.rt.handle, self.handle), "tqcache_reset")
+
+    def set_lengths(self, lens):
+        a = np.ascontiguousarray(lens, dtype=np.int32)
+        self.rt.check(self._L.sai_tqcache_set_lengths(self.rt.handle, self.handle,
+                                                      a.ctypes.data_as(C.c_void_p), a.size),
+                      "tqcache_set_lengths")
+
+    def lengths(self):
+        out = np.zeros(self.max_batch, np.int32)
+        pend, b = C.c_int32(), C.c_int32()
+        self._L.sai_tqcache_lengths(self.handle, out.ctypes.data_as(C.c_void_p), C.byref(pend),
+                                    C.byref(b))
+        return out, pend.value, b.value
+
+    def read(self, layer, b, kv_head, start, n):
+        """Decoded rows (read_k, read_v), f32 [n, head_dim] each (synchronous)."""
+        k = np.zeros((n, self.head_dim), np.float32)
+        v = np.zeros((n, self.head_dim), np.float32)
+        self.rt.check(self._L.sai_tqcache_read(self.rt.handle, self.handle, layer, b, kv_head,
+                                               start, n, k.ctypes.data_as(C.c_void_p),
+                                               v.ctypes.data_as(C.c_void_p)), "tqcache_read")
+        return k, v
+
+    def read_raw(self, layer, b, kv_head, start, n):
+        """Stored rows: dict of k/v codes [n, D*bits/8] u8, params [n, 3] f32
+        (scale, zero, C), signs [n, D/64] u64 (zeros without QJL)."""
+        D = self.head_dim
+        cb = D * self.bits // 8
+        r = {"k_codes": np.zeros((n, cb), np.uint8), "v_codes": np.zeros((n, cb), np.uint8),
+             "k_params": np.zeros((n, 3), np.float32), "v_params": np.zeros((n, 3), np.float32),
+             "k_signs": np.zeros((n, D // 64), np.uint64),
+             "v_signs": np.zeros((n, D // 64), np.uint64)}
+        ptr = lambda key: r[key].ctypes.data_as(C.c_void_p)
+        sk = ptr("k_signs") if self.qjl else None
+        sv = ptr("v_signs") if self.qjl else None
+        self.rt.check(self._L.sai_tqcache_read_raw(
+            self.rt.handle, self.handle, layer, b, kv_head, start, n, ptr("k_codes"),
+            ptr("v_codes"), ptr("k_params"), ptr("v_params"), sk, sv), "tqcache_read_raw")
+        return r
+
+    def attend(self, layer, q, out, batch, num_heads, scale=None, stream=None, dtype=None):
+        """q: device [batch, 1, num_heads*head_dim]; out: device f32, same shape."""
+        dt = dtype if dtype is not None else _dtype_code(q)
+        self.rt.check(self._L.sai_tqcache_attend(
+            self.rt.handle, self.handle, layer, _dev_ptr(q), dt, batch, num_heads,
+            int(scale is not None), 0.0 if scale is None else float(scale), _dev_ptr(out),
+            _stream(stream)), "tqcache_attend")
 
 
 def identity_page_table(batch: int, pages_per_seq: int):

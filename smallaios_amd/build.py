@@ -32,9 +32,10 @@ EXTRA = {
     "kv_append.hip": ["-ffp-contract=off"],
     "sai_capi.hip": ["-ffp-contract=off"],
     "rotary.hip": ["-ffp-contract=off"],
+    "tq_cache.hip": ["-ffp-contract=off"],
 }
 SOURCES = ["kv_append.hip", "gqa_decode.hip", "gqa_decode_int4.hip", "gqa_prefill.hip",
-           "rotary.hip", "copy_rows.hip", "sai_capi.hip"]
+           "rotary.hip", "copy_rows.hip", "tq_cache.hip", "sai_capi.hip"]
 
 
 def _run(cmd):

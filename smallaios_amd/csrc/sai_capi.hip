@@ -38,6 +38,32 @@ struct sai_ctx {
   // decode-kernel timing ring: event pairs of the last `slots` calls
   std::vector<hipEvent_t> ev_start, ev_end;
   int64_t timed_calls = 0;
+  // TurboQuant attention workspace
+  float* tq_partials = nullptr;
+  size_t tq_partial_floats = 0;
+  float* tq_qenc = nullptr;
+  size_t tq_qenc_floats = 0;
+};
+
+struct sai_tqcache {
+  sai_tqcache_desc desc{};
+  size_t code_stride = 0;  // bytes of one row's codes, multiple of 16
+  size_t rows_total = 0;   // heads * max_batch * max_rows
+  struct Layer {
+    uint8_t* codes_k = nullptr;
+    uint8_t* codes_v = nullptr;
+    float4* par_k = nullptr;
+    float4* par_v = nullptr;
+    uint32_t* sg_k = nullptr;
+    uint32_t* sg_v = nullptr;
+    int8_t* rot = nullptr;  // rotation signs [heads][D]
+  };
+  std::vector<Layer> layers;
+  int32_t* d_lens = nullptr;
+  std::vector<int32_t> h_lens;
+  int32_t batch = 0;
+  int32_t pending = 0;
+  float norm = 0.0f;
 };
 
 struct sai_kvcache {
@@ -210,6 +236,8 @@ SAI_API sai_status sai_init(int device, sai_ctx** out) {
 SAI_API void sai_destroy(sai_ctx* ctx) {
   if (!ctx) return;
   DeviceGuard dg(ctx->device);
+  if (ctx->tq_partials) (void)hipFree(ctx->tq_partials);
+  if (ctx->tq_qenc) (void)hipFree(ctx->tq_qenc);
   if (ctx->partials) (void)hipFree(ctx->partials);
   if (ctx->seq_info) (void)hipFree(ctx->seq_info);
   if (ctx->counters) (void)hipFree(ctx->counters);
@@ -1068,5 +1096,337 @@ SAI_API sai_status sai_copy_rows(sai_ctx* ctx, const void* src, int32_t src_layo
   DeviceGuard dg(ctx->device);
   const hipError_t e = sai::launch_copy_rows(a, chunk, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "copy_rows launch");
+  return SAI_OK;
+}
+
+// ------------------------------------------------------- TurboQuant KV cache ---
+namespace {
+
+// sqrt_approx (onnx-rt/src/operators.rs:3311-3320), the WHT normalisation's
+// square root: ten Newton steps from x, each op rounded on its own.
+float sqrt_approx_newton(float x) {
+  if (x <= 0.0f) return 0.0f;
+  volatile float s = x;
+  for (int i = 0; i < 10; ++i) {
+    volatile float q = x / s;
+    volatile float t = s + q;
+    s = 0.5f * t;
+  }
+  return s;
+}
+
+// PolarQuantizer::new's signs (kv_compression.rs:197-214) from the cache's
+// per-head seed (CompressedKVCache::new, :766-790).
+void tq_rotation_signs(uint64_t seed, int layer, int heads, int head, int dim, int8_t* out) {
+  const uint64_t head_seed = seed * 0x9E3779B97F4A7C15ull + (uint64_t)((int64_t)layer * heads + head);
+  uint64_t st = head_seed ? head_seed : 0x5EEDDEADBEEFCAFEull;
+  for (int i = 0; i < dim; ++i) {
+    st ^= st << 13;
+    st ^= st >> 7;
+    st ^= st << 17;
+    out[i] = (st & 1u) == 0 ? 1 : -1;
+  }
+}
+
+sai::TqArgs tq_args(const sai_tqcache* c, int32_t layer) {
+  const sai_tqcache::Layer& L = c->layers[layer];
+  sai::TqArgs a{};
+  a.codes_k = L.codes_k;
+  a.codes_v = L.codes_v;
+  a.par_k = L.par_k;
+  a.par_v = L.par_v;
+  a.signs_k = L.sg_k;
+  a.signs_v = L.sg_v;
+  a.signs = L.rot;
+  a.seq_lens = c->d_lens;
+  a.pending = c->pending;
+  a.heads = c->desc.num_kv_heads;
+  a.batch_cap = c->desc.max_batch;
+  a.rows_cap = c->desc.max_rows;
+  a.head_dim = c->desc.head_dim;
+  a.bits = c->desc.bits;
+  a.qjl = c->desc.qjl;
+  a.code_stride = c->code_stride;
+  a.norm = c->norm;
+  return a;
+}
+
+}  // namespace
+
+SAI_API void sai_tqcache_destroy(sai_tqcache* c) {
+  if (!c) return;
+  for (auto& L : c->layers) {
+    for (void* p : {(void*)L.codes_k, (void*)L.codes_v, (void*)L.par_k, (void*)L.par_v,
+                    (void*)L.sg_k, (void*)L.sg_v, (void*)L.rot})
+      if (p) (void)hipFree(p);
+  }
+  if (c->d_lens) (void)hipFree(c->d_lens);
+  delete c;
+}
+
+SAI_API sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc,
+                                      sai_tqcache** out) {
+  if (!ctx || !desc || !out) return SAI_ERR_NULL;
+  *out = nullptr;
+  const sai_tqcache_desc& d = *desc;
+  if (d.num_layers <= 0 || d.num_kv_heads <= 0 || d.max_batch <= 0 || d.max_rows <= 0)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "tq_cache: zero dimension");
+  if (d.head_dim != 64 && d.head_dim != 128)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "tq_cache: head_dim %d (64 or 128)", d.head_dim);
+  if (d.bits != 3 && d.bits != 4 && d.bits != 8)
+    return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE, "bits must be 3, 4, or 8");
+  if (d.num_kv_heads > 65535 || d.max_batch > 65535)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "tq_cache: more than 65535 heads or sequences");
+  DeviceGuard dg(ctx->device);
+  sai_tqcache* c = new (std::nothrow) sai_tqcache();
+  if (!c) return fail(ctx, SAI_ERR_ALLOC, "tq_cache: host");
+  c->desc = d;
+  c->desc.qjl = d.qjl ? 1 : 0;
+  c->code_stride = (((size_t)d.head_dim * d.bits / 8) + 15) / 16 * 16;
+  c->rows_total = (size_t)d.num_kv_heads * d.max_batch * d.max_rows;
+  c->norm = 1.0f / sqrt_approx_newton((float)d.head_dim);
+  c->layers.resize(d.num_layers);
+  hipError_t e = hipSuccess;
+  std::vector<int8_t> rot((size_t)d.num_kv_heads * d.head_dim);
+  for (int l = 0; l < d.num_layers && e == hipSuccess; ++l) {
+    sai_tqcache::Layer& L = c->layers[l];
+    e = hipMalloc(&L.codes_k, c->rows_total * c->code_stride);
+    if (e == hipSuccess) e = hipMalloc(&L.codes_v, c->rows_total * c->code_stride);
+    if (e == hipSuccess) e = hipMalloc(&L.par_k, c->rows_total * sizeof(float4));
+    if (e == hipSuccess) e = hipMalloc(&L.par_v, c->rows_total * sizeof(float4));
+    if (e == hipSuccess && c->desc.qjl) e = hipMalloc(&L.sg_k, c->rows_total * d.head_dim / 8);
+    if (e == hipSuccess && c->desc.qjl) e = hipMalloc(&L.sg_v, c->rows_total * d.head_dim / 8);
+    if (e == hipSuccess) e = hipMalloc(&L.rot, rot.size());
+    if (e == hipSuccess) {
+      for (int h = 0; h < d.num_kv_heads; ++h)
+        tq_rotation_signs(d.seed, l, d.num_kv_heads, h, d.head_dim, rot.data() + (size_t)h * d.head_dim);
+      e = hipMemcpy(L.rot, rot.data(), rot.size(), hipMemcpyHostToDevice);
+    }
+  }
+  if (e == hipSuccess) e = hipMalloc(&c->d_lens, (size_t)d.max_batch * sizeof(int32_t));
+  if (e == hipSuccess) e = hipMemset(c->d_lens, 0, (size_t)d.max_batch * sizeof(int32_t));
+  if (e != hipSuccess) {
+    sai_tqcache_destroy(c);
+    return fail(ctx, SAI_ERR_ALLOC, "tq_cache: %s", hipGetErrorString(e));
+  }
+  c->h_lens.assign(d.max_batch, 0);
+  *out = c;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_tqcache_write(sai_ctx* ctx, sai_tqcache* c, int32_t layer, const void* k,
+                                     const void* v, int32_t dtype, int32_t batch, int32_t s_new,
+                                     void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "tq_cache_write";
+  if (layer < 0 || layer >= c->desc.num_layers)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: layer_idx %d", op, layer);
+  if (dtype != SAI_DTYPE_F32 && dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (want f32 or bf16)", op, dtype);
+  if (batch <= 0 || batch > c->desc.max_batch || s_new <= 0 ||
+      (int64_t)batch * s_new * c->desc.num_kv_heads * 2 > INT32_MAX)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: batch %d / rows %d", op, batch, s_new);
+  if (!k || !v) return fail(ctx, SAI_ERR_NULL, "%s: missing key/value", op);
+  const bool fresh = c->pending == 0;
+  if (!fresh && (s_new != c->pending || batch != c->batch))
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                "%s: %d rows x %d sequences, but this pass appends %d x %d", op, s_new, batch,
+                c->pending, c->batch);
+  for (int b = 0; b < batch; ++b)
+    if ((int64_t)c->h_lens[b] + s_new > c->desc.max_rows)
+      return fail(ctx, SAI_ERR_OVERFLOW, "%s: position_overflow (sequence %d: %d + %d > %d)", op,
+                  b, c->h_lens[b], s_new, c->desc.max_rows);
+  DeviceGuard dg(ctx->device);
+  sai::TqArgs a = tq_args(c, layer);
+  const hipError_t e = sai::launch_tq_write(a, k, v, dtype == SAI_DTYPE_BF16 ? 1 : 0, batch, s_new,
+                                            (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "tq_cache_write launch");
+  c->pending = s_new;
+  c->batch = batch;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_tqcache_advance(sai_ctx* ctx, sai_tqcache* c, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  if (c->pending == 0) return SAI_OK;
+  DeviceGuard dg(ctx->device);
+  const hipError_t e = sai::launch_seq_advance(c->d_lens, c->batch, c->pending, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "tq_cache_advance");
+  for (int b = 0; b < c->batch; ++b) c->h_lens[b] += c->pending;
+  c->pending = 0;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_tqcache_reset(sai_ctx* ctx, sai_tqcache* c) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  DeviceGuard dg(ctx->device);
+  const hipError_t e = hipMemset(c->d_lens, 0, (size_t)c->desc.max_batch * sizeof(int32_t));
+  if (e != hipSuccess) return hip_fail(ctx, e, "tq_cache_reset");
+  std::fill(c->h_lens.begin(), c->h_lens.end(), 0);
+  c->pending = 0;
+  c->batch = 0;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_tqcache_set_lengths(sai_ctx* ctx, sai_tqcache* c, const int32_t* lens,
+                                           int32_t batch) {
+  if (!ctx || !c || !lens) return SAI_ERR_NULL;
+  if (batch <= 0 || batch > c->desc.max_batch)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "tq_cache_set_lengths: batch %d", batch);
+  for (int b = 0; b < batch; ++b)
+    if (lens[b] < 0 || lens[b] > c->desc.max_rows)
+      return fail(ctx, SAI_ERR_OVERFLOW, "tq_cache_set_lengths: length %d of sequence %d exceeds %d",
+                  lens[b], b, c->desc.max_rows);
+  DeviceGuard dg(ctx->device);
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess)
+    e = hipMemcpy(c->d_lens, lens, (size_t)batch * sizeof(int32_t), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(ctx, e, "tq_cache_set_lengths");
+  std::copy(lens, lens + batch, c->h_lens.begin());
+  c->pending = 0;
+  c->batch = batch;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_tqcache_lengths(const sai_tqcache* c, int32_t* lens_out,
+                                       int32_t* pending_out, int32_t* batch_out) {
+  if (!c) return SAI_ERR_NULL;
+  if (lens_out)
+    for (int b = 0; b < c->desc.max_batch; ++b) lens_out[b] = c->h_lens[b];
+  if (pending_out) *pending_out = c->pending;
+  if (batch_out) *batch_out = c->batch;
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_tqcache_read(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int32_t b,
+                                    int32_t head, int32_t start, int32_t len, float* k_out,
+                                    float* v_out) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "tq_cache_read";
+  if (layer < 0 || layer >= c->desc.num_layers || b < 0 || b >= c->desc.max_batch || head < 0 ||
+      head >= c->desc.num_kv_heads || start < 0 || len < 0 ||
+      (int64_t)start + len > (int64_t)c->h_lens[b] + (b < c->batch ? c->pending : 0))
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: range out of the written rows", op);
+  if (len == 0) return SAI_OK;
+  if (!k_out || !v_out) return fail(ctx, SAI_ERR_NULL, "%s: NULL output", op);
+  DeviceGuard dg(ctx->device);
+  const size_t n = (size_t)len * c->desc.head_dim;
+  float* dk = nullptr;
+  hipError_t e = hipMalloc(&dk, 2 * n * sizeof(float));
+  if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "%s: %s", op, hipGetErrorString(e));
+  sai::TqArgs a = tq_args(c, layer);
+  e = sai::launch_tq_read(a, b, head, start, len, dk, dk + n, nullptr);
+  if (e == hipSuccess) e = hipMemcpy(k_out, dk, n * sizeof(float), hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(v_out, dk + n, n * sizeof(float), hipMemcpyDeviceToHost);
+  (void)hipFree(dk);
+  if (e != hipSuccess) return hip_fail(ctx, e, op);
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_tqcache_read_raw(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int32_t b,
+                                        int32_t head, int32_t start, int32_t len, void* k_codes,
+                                        void* v_codes, float* k_params, float* v_params,
+                                        void* k_signs, void* v_signs) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "tq_cache_read_raw";
+  if (layer < 0 || layer >= c->desc.num_layers || b < 0 || b >= c->desc.max_batch || head < 0 ||
+      head >= c->desc.num_kv_heads || start < 0 || len < 0 ||
+      (int64_t)start + len > (int64_t)c->h_lens[b] + (b < c->batch ? c->pending : 0))
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: range out of the written rows", op);
+  if (len == 0) return SAI_OK;
+  DeviceGuard dg(ctx->device);
+  const sai_tqcache::Layer& L = c->layers[layer];
+  const size_t row0 = ((size_t)head * c->desc.max_batch + b) * c->desc.max_rows + start;
+  const size_t cb = (size_t)c->desc.head_dim * c->desc.bits / 8;
+  hipError_t e = hipSuccess;
+  auto codes = [&](const uint8_t* src, void* dst) {
+    if (!dst || e != hipSuccess) return;
+    e = hipMemcpy2D(dst, cb, src + row0 * c->code_stride, c->code_stride, cb, len,
+                    hipMemcpyDeviceToHost);
+  };
+  auto params = [&](const float4* src, float* dst) {
+    if (!dst || e != hipSuccess) return;
+    std::vector<float4> tmp(len);
+    e = hipMemcpy(tmp.data(), src + row0, len * sizeof(float4), hipMemcpyDeviceToHost);
+    for (int t = 0; t < len && e == hipSuccess; ++t) {
+      dst[3 * t] = tmp[t].x;
+      dst[3 * t + 1] = tmp[t].y;
+      dst[3 * t + 2] = tmp[t].z;
+    }
+  };
+  auto signs = [&](const uint32_t* src, void* dst) {
+    if (!dst || !src || e != hipSuccess) return;
+    e = hipMemcpy(dst, src + row0 * (c->desc.head_dim / 32), (size_t)len * c->desc.head_dim / 8,
+                  hipMemcpyDeviceToHost);
+  };
+  codes(L.codes_k, k_codes);
+  codes(L.codes_v, v_codes);
+  params(L.par_k, k_params);
+  params(L.par_v, v_params);
+  signs(L.sg_k, k_signs);
+  signs(L.sg_v, v_signs);
+  if (e != hipSuccess) return hip_fail(ctx, e, op);
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t layer, const void* q,
+                                      int32_t dtype, int32_t batch, int32_t num_heads,
+                                      int32_t has_scale, float scale, float* out, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "tq_cache_attend";
+  if (!q || !out) return fail(ctx, SAI_ERR_NULL, "%s: missing query/output", op);
+  if (layer < 0 || layer >= c->desc.num_layers)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: layer_idx %d", op, layer);
+  if (dtype != SAI_DTYPE_F32 && dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (want f32 or bf16)", op, dtype);
+  const int H = c->desc.num_kv_heads, D = c->desc.head_dim;
+  if (num_heads <= 0 || num_heads % H != 0)
+    return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE,
+                "GroupQueryAttention: num_heads must be a multiple of kv_num_heads");
+  const int G = num_heads / H;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: group size %d (supported 1, 2, 4, 8)", op, G);
+  const int nb = c->pending > 0 ? c->batch : batch;
+  if (batch <= 0 || batch != nb || batch > c->desc.max_batch)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: batch %d does not match the cache's %d", op,
+                batch, nb);
+  int32_t max_len = 0;
+  for (int b = 0; b < batch; ++b) max_len = std::max(max_len, c->h_lens[b] + c->pending);
+  if (max_len <= 0) return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: empty cache", op);
+  // splits of 1024 rows (16 tiles of 64 per 4-wave workgroup)
+  const int32_t split_rows = 1024;
+  const int32_t max_splits = (max_len + split_rows - 1) / split_rows;
+  const size_t part_floats = (size_t)batch * H * max_splits * G * (D + 2);
+  const size_t qenc_floats = (size_t)batch * num_heads * (D + 2 + D / 32);
+  DeviceGuard dg(ctx->device);
+  if (part_floats > ctx->tq_partial_floats) {
+    if (ctx->tq_partials) (void)hipFree(ctx->tq_partials);
+    ctx->tq_partials = nullptr;
+    ctx->tq_partial_floats = 0;
+    if (hipMalloc(&ctx->tq_partials, part_floats * sizeof(float)) != hipSuccess)
+      return fail(ctx, SAI_ERR_ALLOC, "%s: workspace", op);
+    ctx->tq_partial_floats = part_floats;
+  }
+  if (qenc_floats > ctx->tq_qenc_floats) {
+    if (ctx->tq_qenc) (void)hipFree(ctx->tq_qenc);
+    ctx->tq_qenc = nullptr;
+    ctx->tq_qenc_floats = 0;
+    if (hipMalloc(&ctx->tq_qenc, qenc_floats * sizeof(float)) != hipSuccess)
+      return fail(ctx, SAI_ERR_ALLOC, "%s: workspace", op);
+    ctx->tq_qenc_floats = qenc_floats;
+  }
+  sai::TqArgs a = tq_args(c, layer);
+  sai::TqAttendArgs t{};
+  t.q = q;
+  t.q_bf16 = dtype == SAI_DTYPE_BF16 ? 1 : 0;
+  t.num_heads = num_heads;
+  t.out = out;
+  t.partials = ctx->tq_partials;
+  t.qenc = ctx->tq_qenc;
+  t.split_rows = split_rows;
+  t.max_splits = max_splits;
+  t.scale_log2 = (has_scale ? scale : sai_default_scale(D)) * 1.4426950408889634f;
+  const hipError_t e = sai::launch_tq_attend(a, t, G, max_splits, batch, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "tq_cache_attend launch");
   return SAI_OK;
 }

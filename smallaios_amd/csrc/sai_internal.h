@@ -195,7 +195,41 @@ struct CopyRowsArgs {
   int32_t src_layout, dst_layout;
 };
 
+// TurboQuant cache, one layer (tq_cache.hip). Row (head h, sequence b,
+// position r) = (h * batch_cap + b) * rows_cap + r of every array.
+struct TqArgs {
+  uint8_t* codes_k;
+  uint8_t* codes_v;
+  float4* par_k;  // (scale, zero, C, 0)
+  float4* par_v;
+  uint32_t* signs_k;  // QJL sign words [row][D/32]
+  uint32_t* signs_v;
+  const int8_t* signs;       // rotation signs [heads][D] of this layer
+  const int32_t* seq_lens;   // committed rows per sequence
+  int pending;
+  int heads, batch_cap, rows_cap, head_dim, bits, qjl;
+  size_t code_stride;  // bytes per row of codes (multiple of 16)
+  float norm;          // 1 / sqrt_approx(head_dim)
+};
+
+struct TqAttendArgs {
+  const void* q;  // [batch, 1, num_heads * D]
+  int q_bf16;
+  int num_heads;
+  float* out;       // [batch, 1, num_heads * D]
+  float* partials;  // [batch][heads][max_splits][G * (D + 2)]
+  float* qenc;      // [batch * num_heads][D + 2 + D/32]
+  int split_rows, max_splits;
+  float scale_log2;
+};
+
 // Launchers (return hipError_t of the launch).
+hipError_t launch_tq_write(const TqArgs& a, const void* k, const void* v, int bf16, int batch,
+                           int s_new, hipStream_t st);
+hipError_t launch_tq_read(const TqArgs& a, int b, int h, int start, int len, float* k_out,
+                          float* v_out, hipStream_t st);
+hipError_t launch_tq_attend(const TqArgs& a, const TqAttendArgs& t, int group, int nsplit,
+                            int batch, hipStream_t st);
 hipError_t launch_copy_rows(const CopyRowsArgs& a, int chunk_bytes, hipStream_t st);
 // Standalone RoPE (rotary.hip): x/y f32 or bf16, tables f32 or bf16.
 hipError_t launch_rotary(const RotaryArgs& a, bool x_bf16, bool table_bf16, bool interleaved,

@@ -1,0 +1,244 @@
+"""The TurboQuant compressed KV cache on the GPU (sai_tqcache_*), against the
+oracle's restatement of CompressedKVCache (onnx-rt/src/kv_compression.rs:
+738-963) and of the decode read path over it.
+
+Stored form (codes, scale, zero point, QJL sign bits and mean) is checked bit
+for bit against oracle.tq_write_rows with the cache's per-head seeds; decoded
+rows (read_k / read_v) bit for bit against oracle.tq_decode; attention
+against oracle.tq_attend within 2e-3 abs + 1e-2 rel (the kernel evaluates
+the same estimator in the rotated domain, so only rounding differs)."""
+import numpy as np
+import pytest
+
+import oracle as O
+import smallaios_amd as S
+from _gpu_util import log
+
+pytestmark = pytest.mark.gpu
+SEED = 0xDEADBEEFCAFE1234
+
+
+@pytest.fixture(scope="module")
+def rt():
+    import torch
+    assert torch.cuda.is_available()
+    r = S.Runtime(0)
+    yield r
+    r.close()
+
+
+def head_signs(seed, layer, heads, h, d):
+    return O.tq_signs(O.tq_head_seed(seed, layer, heads, h), d)
+
+
+def rows_of(x, b, h, heads, d):
+    """Rows of (sequence b, kv head h) from host [B, S, heads*D] f32."""
+    return np.ascontiguousarray(x[b].reshape(x.shape[1], heads, d)[:, h])
+
+
+def to_dev(x, bf16):
+    import torch
+    t = torch.from_numpy(x)
+    return (t.to(torch.bfloat16) if bf16 else t).cuda()
+
+
+def host_vals(x, bf16):
+    """The f32 values the kernel reads from the device copy of x."""
+    if not bf16:
+        return x
+    return O.bf16_bits_to_f32(O.f32_to_bf16_bits(x)).reshape(x.shape)
+
+
+def check_rows(cache, layer, b, h, t0, x_k, x_v, heads, d, bits, qjl, seed):
+    n = x_k.shape[0]
+    sg = head_signs(seed, layer, heads, h, d)
+    raw = cache.read_raw(layer, b, h, t0, n)
+    for kind, x in (("k", x_k), ("v", x_v)):
+        codes, sc, z, sb, c = O.tq_write_rows(x, bits, sg, qjl)
+        assert np.array_equal(raw[f"{kind}_codes"], codes), (kind, b, h)
+        assert np.array_equal(raw[f"{kind}_params"][:, 0].view(np.uint32), sc.view(np.uint32))
+        assert np.array_equal(raw[f"{kind}_params"][:, 1].view(np.uint32), z.view(np.uint32))
+        if qjl:
+            assert np.array_equal(raw[f"{kind}_signs"], sb), (kind, b, h)
+            assert np.array_equal(raw[f"{kind}_params"][:, 2].view(np.uint32), c.view(np.uint32))
+    dk, dv = cache.read(layer, b, h, t0, n)
+    ek = O.tq_write_rows(x_k, bits, sg, qjl)
+    ev = O.tq_write_rows(x_v, bits, sg, qjl)
+    for t in range(n):
+        wk = O.tq_decode(ek[0][t], d, bits, ek[1][t], ek[2][t], sg)
+        wv = O.tq_decode(ev[0][t], d, bits, ev[1][t], ev[2][t], sg)
+        assert np.array_equal(dk[t].view(np.uint32), wk.view(np.uint32)), (b, h, t)
+        assert np.array_equal(dv[t].view(np.uint32), wv.view(np.uint32)), (b, h, t)
+
+
+@pytest.mark.parametrize("d,bits,qjl,bf16", [(128, 4, True, False), (128, 3, True, True),
+                                             (64, 8, False, False), (64, 4, True, True),
+                                             (128, 8, True, False), (64, 3, False, False)])
+def test_write_read_bit_exact(rt, d, bits, qjl, bf16):
+    """A prefill pass then a decode pass, two layers; every stored row of
+    layer 1 checked."""
+    import torch
+    log(f"tq write/read d={d} bits={bits} qjl={qjl} bf16={bf16}")
+    rng = np.random.default_rng(d * 10 + bits)
+    batch, heads, s0 = 3, 2, 5
+    c = S.TqCache(rt, 2, heads, d, bits, qjl, 4, 16, seed=SEED)
+    try:
+        passes = []
+        for s in (s0, 1):
+            ks = [(rng.standard_normal((batch, s, heads * d)) * 0.7).astype(np.float32)
+                  for _ in range(2)]
+            vs = [(rng.standard_normal((batch, s, heads * d)) * 1.3).astype(np.float32)
+                  for _ in range(2)]
+            for layer in range(2):
+                c.write(layer, to_dev(ks[layer], bf16), to_dev(vs[layer], bf16), batch, s)
+            c.advance()
+            passes.append((host_vals(ks[1], bf16), host_vals(vs[1], bf16)))
+        torch.cuda.synchronize()
+        lens, pend, nb = c.lengths()
+        assert list(lens[:batch]) == [s0 + 1] * batch and pend == 0 and nb == batch
+        for b in range(batch):
+            for h in range(heads):
+                xk = np.concatenate([rows_of(p[0], b, h, heads, d) for p in passes])
+                xv = np.concatenate([rows_of(p[1], b, h, heads, d) for p in passes])
+                check_rows(c, 1, b, h, 0, xk, xv, heads, d, bits, qjl, SEED)
+    finally:
+        c.close()
+
+
+def test_constant_and_edge_rows(rt):
+    """Constant rows (range 0: scale 1.0), zeros, large magnitudes."""
+    import torch
+    d, heads = 64, 1
+    c = S.TqCache(rt, 1, heads, d, 4, True, 1, 8, seed=0)
+    try:
+        x = np.stack([np.full(d, 3.14, np.float32), np.zeros(d, np.float32),
+                      (np.arange(d, dtype=np.float32) - 32) * np.float32(1e4),
+                      np.where(np.arange(d) % 2 == 0, 1.0, -1.0).astype(np.float32)])
+        k = x.reshape(1, 4, d)
+        c.write(0, to_dev(k, False), to_dev(k[:, ::-1].copy(), False), 1, 4)
+        torch.cuda.synchronize()
+        check_rows(c, 0, 0, 0, 0, x, x[::-1].copy(), heads, d, 4, True, 0)
+    finally:
+        c.close()
+
+
+def oracle_attend(cache_rows_k, cache_rows_v, q, bits, qjl, sg, scale):
+    ek = O.tq_write_rows(cache_rows_k, bits, sg, qjl)
+    ev = O.tq_write_rows(cache_rows_v, bits, sg, qjl)
+    return O.tq_attend(q, bits, qjl, sg, ek, ev, scale)
+
+
+@pytest.mark.parametrize("d,bits,qjl,group,bf16", [
+    (128, 4, True, 4, False), (128, 3, True, 8, True), (64, 8, False, 2, False),
+    (128, 8, True, 1, False), (64, 4, True, 8, True), (64, 3, False, 4, False)])
+def test_attend_matches_oracle(rt, d, bits, qjl, group, bf16):
+    """Prefill 40 rows, then a decode pass whose appended row is attended
+    while pending (one split)."""
+    import torch
+    log(f"tq attend d={d} bits={bits} qjl={qjl} G={group} bf16={bf16}")
+    rng = np.random.default_rng(bits * 100 + group)
+    batch, heads, s0 = 2, 2, 40
+    nh = heads * group
+    c = S.TqCache(rt, 1, heads, d, bits, qjl, batch, 64, seed=SEED)
+    try:
+        k0 = rng.standard_normal((batch, s0, heads * d)).astype(np.float32)
+        v0 = rng.standard_normal((batch, s0, heads * d)).astype(np.float32)
+        c.write(0, to_dev(k0, bf16), to_dev(v0, bf16), batch, s0)
+        c.advance()
+        k1 = rng.standard_normal((batch, 1, heads * d)).astype(np.float32)
+        v1 = rng.standard_normal((batch, 1, heads * d)).astype(np.float32)
+        c.write(0, to_dev(k1, bf16), to_dev(v1, bf16), batch, 1)
+        q = rng.standard_normal((batch, 1, nh * d)).astype(np.float32)
+        out = torch.full((batch, 1, nh * d), float("nan"), device="cuda")
+        c.attend(0, to_dev(q, bf16), out, batch, nh)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(batch, nh, d)
+        kk = np.concatenate([host_vals(k0, bf16), host_vals(k1, bf16)], axis=1)
+        vv = np.concatenate([host_vals(v0, bf16), host_vals(v1, bf16)], axis=1)
+        qq = host_vals(q, bf16).reshape(batch, nh, d)
+        scale = S.default_scale(d)
+        for b in range(batch):
+            for h in range(heads):
+                sg = head_signs(SEED, 0, heads, h, d)
+                want = oracle_attend(rows_of(kk, b, h, heads, d), rows_of(vv, b, h, heads, d),
+                                     qq[b, h * group:(h + 1) * group], bits, qjl, sg, scale)
+                np.testing.assert_allclose(got[b, h * group:(h + 1) * group], want,
+                                           atol=2e-3, rtol=1e-2)
+    finally:
+        c.close()
+
+
+def test_attend_long_ragged_splits(rt):
+    """Ragged lengths over several 1024-row splits (one sequence shorter than
+    a split, one ending mid-tile), explicit scale."""
+    import torch
+    log("tq attend ragged long")
+    d, bits, qjl, group, heads = 128, 4, True, 4, 2
+    nh = heads * group
+    lens = [3000, 700, 2049]
+    batch, rows = len(lens), max(lens)
+    rng = np.random.default_rng(11)
+    c = S.TqCache(rt, 1, heads, d, bits, qjl, batch, rows, seed=7)
+    try:
+        k = rng.standard_normal((batch, rows, heads * d)).astype(np.float32)
+        v = rng.standard_normal((batch, rows, heads * d)).astype(np.float32)
+        c.write(0, to_dev(k, False), to_dev(v, False), batch, rows)
+        c.advance()
+        c.set_lengths(lens)
+        q = (rng.standard_normal((batch, 1, nh * d)) * 2.0).astype(np.float32)
+        out = torch.zeros((batch, 1, nh * d), device="cuda")
+        c.attend(0, to_dev(q, False), out, batch, nh, scale=0.05)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(batch, nh, d)
+        qq = q.reshape(batch, nh, d)
+        for b in range(batch):
+            for h in range(heads):
+                sg = head_signs(7, 0, heads, h, d)
+                want = oracle_attend(rows_of(k, b, h, heads, d)[:lens[b]],
+                                     rows_of(v, b, h, heads, d)[:lens[b]],
+                                     qq[b, h * group:(h + 1) * group], bits, qjl, sg, 0.05)
+                np.testing.assert_allclose(got[b, h * group:(h + 1) * group], want,
+                                           atol=2e-3, rtol=1e-2)
+    finally:
+        c.close()
+
+
+def test_errors_and_lifecycle(rt):
+    import torch
+    with pytest.raises(S.SaiError) as e:
+        S.TqCache(rt, 1, 2, 64, 5, True, 1, 8)
+    assert e.value.kind == "InvalidAttribute" and "bits must be 3, 4, or 8" in str(e.value)
+    with pytest.raises(S.SaiError) as e:
+        S.TqCache(rt, 1, 2, 96, 4, True, 1, 8)
+    assert e.value.kind == "Unsupported"
+    d, heads = 64, 2
+    c = S.TqCache(rt, 2, heads, d, 4, False, 2, 8)
+    try:
+        x = torch.randn(2, 6, heads * d, device="cuda")
+        c.write(0, x, x, 2, 6)
+        with pytest.raises(S.SaiError) as e:  # the pass appends 6 rows
+            c.write(1, x[:, :1], x[:, :1], 2, 1)
+        assert e.value.kind == "ShapeMismatch"
+        c.advance()
+        with pytest.raises(S.SaiError) as e:  # 6 + 6 > 8
+            c.write(0, x, x, 2, 6)
+        assert e.value.kind == "PositionOverflow"
+        with pytest.raises(S.SaiError) as e:
+            c.write(2, x, x, 2, 1)
+        assert e.value.kind == "ShapeMismatch"
+        q = torch.randn(2, 1, 3 * d, device="cuda")
+        out = torch.zeros(2, 1, 3 * d, device="cuda")
+        with pytest.raises(S.SaiError) as e:  # 3 query heads over 2 kv heads
+            c.attend(0, q, out, 2, 3)
+        assert e.value.kind == "InvalidAttribute"
+        with pytest.raises(S.SaiError) as e:
+            c.read(0, 0, 0, 4, 3)
+        assert e.value.kind == "ShapeMismatch"
+        c.reset()
+        lens, pend, _ = c.lengths()
+        assert not lens.any() and pend == 0
+        with pytest.raises(S.SaiError) as e:
+            c.attend(0, q[:, :, :2 * d].contiguous(), out, 2, 2)
+        assert e.value.kind == "ShapeMismatch"
+    finally:
+        c.close()
