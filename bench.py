@@ -59,7 +59,15 @@ WORKLOADS = {
     "prefill": dict(kind="prefill", batch=2, hq=32, hkv=8, d=128, past=6144, new=2048,
                     theta=500000.0, q_dtype="bf16", permute=False),
     "rope": dict(kind="rotary", batch=2, hq=32, d=128, past=6144, new=2048, theta=500000.0),
+    "tq4": dict(kind="tq", batch=16, hq=32, hkv=8, d=128, ctx=8192, bits=4, qjl=True,
+                q_dtype="bf16"),
 }
+
+
+def tq_bytes_per_row_head(d, bits, qjl):
+    """What TurboQuant decode attention must read per (row, kv head): K and V
+    codes, K (scale, zero[, QJL mean]), V (scale, zero), K's QJL sign bits."""
+    return 2 * d * bits // 8 + (12 if qjl else 8) + 8 + (d // 8 if qjl else 0)
 
 
 def decode_lengths(w, seed=0x5A1A0003):
@@ -437,6 +445,63 @@ def main():
                          "traffic": None},
         }
         cache = None
+    elif w["kind"] == "tq":
+        ctx, bits, qjl = w["ctx"], w["bits"], w["qjl"]
+        cache = S.TqCache(rt, 1, hkv, d, bits, qjl, b, ctx, seed=0x5EED)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        done = 0
+        while done < ctx - 1:
+            n = min(1024, ctx - 1 - done)
+            k = torch.randn((b, n, hkv * d), generator=g, device="cuda")
+            v = torch.randn((b, n, hkv * d), generator=g, device="cuda")
+            cache.write(0, k, v, b, n)
+            cache.advance()
+            done += n
+        torch.cuda.synchronize()
+        q = torch.randn((b, 1, hq * d), generator=g, device="cuda").to(qdt)
+        k_new = torch.randn((b, 1, hkv * d), generator=g, device="cuda").to(qdt)
+        v_new = torch.randn((b, 1, hkv * d), generator=g, device="cuda").to(qdt)
+        out = torch.empty((b, 1, hq * d), device="cuda", dtype=torch.float32)
+
+        def pre():
+            cache.write(0, k_new, v_new, b, 1, stream=stream)
+
+        def kern():
+            cache.attend(0, q, out, b, hq, stream=stream)
+
+        def step():
+            pre()  # rewrites the pending row: every step sees ctx rows
+            kern()
+
+        for _ in range(args.warmup):
+            step()
+        ms_step = time_steps(torch, step, args.steps)
+        kus = event_times(torch, stream, pre, kern, args.steps)   # query + attend + merge
+        wus = event_times(torch, stream, lambda: None, pre, args.steps)
+        per = tq_bytes_per_row_head(d, bits, qjl)
+        alg = b * ctx * hkv * per + b * hq * d * (2 + 4)
+        k_us = float(np.median(kus))
+        achieved = alg / (k_us * 1e-6) / 1e9
+        result = {
+            "metric": "TurboQuant decode attention HBM GB/s (% of peak), 1 MI355X",
+            "value": round(alg / (ms_step * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32 on u%d codes" % bits,
+            "data": "synthetic (seeded N(0,1) Q/K/V; no checkpoint)",
+            "config": {"workload": "tq4", "batch": b, "q_heads": hq, "kv_heads": hkv,
+                       "head_dim": d, "context": ctx, "bits": bits, "qjl": qjl,
+                       "step": "tq_cache_write (1 token, pending) + tq_cache_attend "
+                               "(query encode + attend + merge)"},
+            "algorithmic_bytes_per_step": alg,
+            "bytes_per_row_head": per,
+            "attend_us": {"median": round(k_us, 3), "mean": round(float(kus.mean()), 3)},
+            "write_us": {"median": round(float(np.median(wus)), 3)},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                         "traffic": None},
+        }
     else:  # prefill
         past, new = w["past"], w["new"]
         cos, sin = S.rope_tables(past + new, d, w["theta"])

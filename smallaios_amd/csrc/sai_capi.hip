@@ -41,14 +41,15 @@ struct sai_ctx {
   // TurboQuant attention workspace
   float* tq_partials = nullptr;
   size_t tq_partial_floats = 0;
-  float* tq_qenc = nullptr;
-  size_t tq_qenc_floats = 0;
+  uint32_t* tq_qenc = nullptr;
+  size_t tq_qenc_words = 0;
 };
 
 struct sai_tqcache {
   sai_tqcache_desc desc{};
-  size_t code_stride = 0;  // bytes of one row's codes, multiple of 16
+  size_t code_stride = 0;  // bytes of one row's K codes, multiple of 16
   size_t rows_total = 0;   // heads * max_batch * max_rows
+  int32_t tiles_cap = 0;   // 64-position V tiles per (head, sequence)
   struct Layer {
     uint8_t* codes_k = nullptr;
     uint8_t* codes_v = nullptr;
@@ -1143,6 +1144,7 @@ sai::TqArgs tq_args(const sai_tqcache* c, int32_t layer) {
   a.heads = c->desc.num_kv_heads;
   a.batch_cap = c->desc.max_batch;
   a.rows_cap = c->desc.max_rows;
+  a.tiles_cap = c->tiles_cap;
   a.head_dim = c->desc.head_dim;
   a.bits = c->desc.bits;
   a.qjl = c->desc.qjl;
@@ -1184,6 +1186,9 @@ SAI_API sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc
   c->desc.qjl = d.qjl ? 1 : 0;
   c->code_stride = (((size_t)d.head_dim * d.bits / 8) + 15) / 16 * 16;
   c->rows_total = (size_t)d.num_kv_heads * d.max_batch * d.max_rows;
+  c->tiles_cap = (d.max_rows + 63) / 64;
+  const size_t v_bytes =
+      (size_t)d.num_kv_heads * d.max_batch * c->tiles_cap * sai::tq_vtile_bytes(d.head_dim, d.bits);
   c->norm = 1.0f / sqrt_approx_newton((float)d.head_dim);
   c->layers.resize(d.num_layers);
   hipError_t e = hipSuccess;
@@ -1191,7 +1196,7 @@ SAI_API sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc
   for (int l = 0; l < d.num_layers && e == hipSuccess; ++l) {
     sai_tqcache::Layer& L = c->layers[l];
     e = hipMalloc(&L.codes_k, c->rows_total * c->code_stride);
-    if (e == hipSuccess) e = hipMalloc(&L.codes_v, c->rows_total * c->code_stride);
+    if (e == hipSuccess) e = hipMalloc(&L.codes_v, v_bytes);
     if (e == hipSuccess) e = hipMalloc(&L.par_k, c->rows_total * sizeof(float4));
     if (e == hipSuccess) e = hipMalloc(&L.par_v, c->rows_total * sizeof(float4));
     if (e == hipSuccess && c->desc.qjl) e = hipMalloc(&L.sg_k, c->rows_total * d.head_dim / 8);
@@ -1344,6 +1349,33 @@ SAI_API sai_status sai_tqcache_read_raw(sai_ctx* ctx, sai_tqcache* c, int32_t la
     e = hipMemcpy2D(dst, cb, src + row0 * c->code_stride, c->code_stride, cb, len,
                     hipMemcpyDeviceToHost);
   };
+  // V: the tiles covering the rows, repacked row-major (LSB first)
+  auto vcodes = [&](const uint8_t* src, void* dst) {
+    if (!dst || e != hipSuccess) return;
+    const int D = c->desc.head_dim, B = c->desc.bits;
+    const size_t tb = sai::tq_vtile_bytes(D, B);
+    const int t0 = start / 64, t1 = (start + len - 1) / 64;
+    std::vector<uint32_t> tiles((size_t)(t1 - t0 + 1) * tb / 4);
+    e = hipMemcpy(tiles.data(),
+                  src + (((size_t)head * c->desc.max_batch + b) * c->tiles_cap + t0) * tb,
+                  tiles.size() * 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return;
+    uint8_t* out = (uint8_t*)dst;
+    std::fill(out, out + (size_t)len * cb, 0);
+    for (int t = 0; t < len; ++t) {
+      const int r = start + t;
+      const uint32_t* tw = tiles.data() + (size_t)(r / 64 - t0) * (tb / 4);
+      for (int d = 0; d < D; ++d) {
+        const uint32_t* ew = tw + (size_t)d * 2 * B;
+        const int p = (r % 64) * B, w = p >> 5, sh = p & 31;
+        uint32_t code = ew[w] >> sh;
+        if (sh + B > 32) code |= ew[w + 1] << (32 - sh);
+        code &= (1u << B) - 1u;
+        for (int k = 0; k < B; ++k)
+          if (code >> k & 1u) out[(size_t)t * cb + (d * B + k) / 8] |= (uint8_t)(1u << ((d * B + k) % 8));
+      }
+    }
+  };
   auto params = [&](const float4* src, float* dst) {
     if (!dst || e != hipSuccess) return;
     std::vector<float4> tmp(len);
@@ -1360,7 +1392,7 @@ SAI_API sai_status sai_tqcache_read_raw(sai_ctx* ctx, sai_tqcache* c, int32_t la
                   hipMemcpyDeviceToHost);
   };
   codes(L.codes_k, k_codes);
-  codes(L.codes_v, v_codes);
+  vcodes(L.codes_v, v_codes);
   params(L.par_k, k_params);
   params(L.par_v, v_params);
   signs(L.sg_k, k_signs);
@@ -1397,7 +1429,7 @@ SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t laye
   const int32_t split_rows = 1024;
   const int32_t max_splits = (max_len + split_rows - 1) / split_rows;
   const size_t part_floats = (size_t)batch * H * max_splits * G * (D + 2);
-  const size_t qenc_floats = (size_t)batch * num_heads * (D + 2 + D / 32);
+  const size_t qenc_words = (size_t)batch * num_heads * sai::tq_qrec_words(D);
   DeviceGuard dg(ctx->device);
   if (part_floats > ctx->tq_partial_floats) {
     if (ctx->tq_partials) (void)hipFree(ctx->tq_partials);
@@ -1407,13 +1439,13 @@ SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t laye
       return fail(ctx, SAI_ERR_ALLOC, "%s: workspace", op);
     ctx->tq_partial_floats = part_floats;
   }
-  if (qenc_floats > ctx->tq_qenc_floats) {
+  if (qenc_words > ctx->tq_qenc_words) {
     if (ctx->tq_qenc) (void)hipFree(ctx->tq_qenc);
     ctx->tq_qenc = nullptr;
-    ctx->tq_qenc_floats = 0;
-    if (hipMalloc(&ctx->tq_qenc, qenc_floats * sizeof(float)) != hipSuccess)
+    ctx->tq_qenc_words = 0;
+    if (hipMalloc(&ctx->tq_qenc, qenc_words * sizeof(uint32_t)) != hipSuccess)
       return fail(ctx, SAI_ERR_ALLOC, "%s: workspace", op);
-    ctx->tq_qenc_floats = qenc_floats;
+    ctx->tq_qenc_words = qenc_words;
   }
   sai::TqArgs a = tq_args(c, layer);
   sai::TqAttendArgs t{};

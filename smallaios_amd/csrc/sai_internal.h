@@ -196,19 +196,33 @@ struct CopyRowsArgs {
 };
 
 // TurboQuant cache, one layer (tq_cache.hip). Row (head h, sequence b,
-// position r) = (h * batch_cap + b) * rows_cap + r of every array.
+// position r) = (h * batch_cap + b) * rows_cap + r of the row-major arrays:
+//   K codes   [row][code_stride bytes], packed LSB first along head_dim
+//   par_k/v   [row] float4 (scale, zero point, QJL mean, sum of the codes)
+//   signs_k/v [row][D/32] QJL sign words (bit i of word j: dim 32j + i)
+// V codes are tile-transposed for the PV product: tile = 64 positions of one
+// (h, b), at ((h * batch_cap + b) * tiles_cap + r / 64) * tq_vtile_bytes;
+// inside it dim d owns 64 * bits bits (8 * bits bytes) holding the codes of
+// the tile's 64 positions, position r % 64 at bit (r % 64) * bits, LSB first.
+__host__ __device__ constexpr size_t tq_vtile_bytes(int d, int bits) {
+  return (size_t)d * 8 * bits;
+}
+__host__ __device__ constexpr int tq_qrec_words(int d) {
+  return (d / 4 + 4 + d / 32 + 3) / 4 * 4;
+}
+
 struct TqArgs {
   uint8_t* codes_k;
   uint8_t* codes_v;
-  float4* par_k;  // (scale, zero, C, 0)
+  float4* par_k;
   float4* par_v;
-  uint32_t* signs_k;  // QJL sign words [row][D/32]
+  uint32_t* signs_k;
   uint32_t* signs_v;
   const int8_t* signs;       // rotation signs [heads][D] of this layer
   const int32_t* seq_lens;   // committed rows per sequence
   int pending;
-  int heads, batch_cap, rows_cap, head_dim, bits, qjl;
-  size_t code_stride;  // bytes per row of codes (multiple of 16)
+  int heads, batch_cap, rows_cap, tiles_cap, head_dim, bits, qjl;
+  size_t code_stride;  // bytes per row of K codes (multiple of 16)
   float norm;          // 1 / sqrt_approx(head_dim)
 };
 
@@ -218,7 +232,7 @@ struct TqAttendArgs {
   int num_heads;
   float* out;       // [batch, 1, num_heads * D]
   float* partials;  // [batch][heads][max_splits][G * (D + 2)]
-  float* qenc;      // [batch * num_heads][D + 2 + D/32]
+  uint32_t* qenc;   // [batch * num_heads][tq_qrec_words(D)]
   int split_rows, max_splits;
   float scale_log2;
 };

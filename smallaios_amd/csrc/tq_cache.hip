@@ -6,23 +6,23 @@
 // A row (one token of one kv head, K or V) is PolarQuant-encoded
 // (kv_compression.rs:216-268): signs s (the head's xorshift +-1 vector),
 // normalised Walsh-Hadamard butterfly y = H(s*x)/sqrt(D), one min/max
-// quantiser over y (codes of 3, 4 or 8 bits, packed LSB first), and, with
-// QJL on (:365-395), the sign bits of r = x - decode(codes) and C = mean|r|.
-// The write kernel does these f32 steps in the reference's order (no
-// contraction, IEEE division), so codes, scale, zero, sign bits and C are the
-// reference's bit for bit.
+// quantiser over y (codes of 3, 4 or 8 bits), and, with QJL on (:365-395),
+// the sign bits of r = x - decode(codes) and C = mean|r|. One wave encodes a
+// row, lane l holding dims l and l + 64: every f32 step is the reference's
+// (same operands, same order, no contraction, IEEE division; the running
+// sum of |r| is taken in dim order), so codes, scale, zero point, sign bits
+// and C are the reference's bit for bit.
 //
-// Attention never decodes a key. Decoding is linear and orthonormal, so
-//   <decode(q), decode(k_t)> = <q^, k^_t>   with  k^_t = s_t * code_t + z_t
-// in the rotated domain, where q^ is the encoded query's rotated
-// reconstruction; the logit adds the QJL popcount correction
-// C_q C_t (D - 2 popcount(sq ^ s_t)) / D. The values are likewise summed in
-// the rotated domain (sum_t p_t v^_t) and rotated back once per output
-// (inverse butterfly, signs), in the merge kernel.
-//
-// Storage per (layer, K|V): codes [H][B][R][CBP] bytes, params [H][B][R]
-// float4 (scale, zero, C, 0), sign words [H][B][R][D/32]; rows [0, R) of a
-// (head, sequence).
+// Attention never decodes a key. Decoding is linear and orthonormal, so with
+// the query encoded by the same quantiser (codes qc, scale qs, zero qz):
+//   <decode(q), decode(k_t)> = sum_i (qs qc_i + qz)(ks_t kc_ti + kz_t),
+// an integer dot product sum_i qc_i kc_ti (exact on the int8 MFMA, the
+// query codes centred so that the f32 terms around it stay small) plus
+// per-row terms; the logit adds the QJL popcount correction
+// C_q C_t (D - 2 popcount(sq ^ s_t)) / D. The values are summed in the
+// rotated domain on the f16 MFMA (weights p_t vs_t / S in f16, codes as exact
+// f16 subnormals code * 2^-24) and rotated back once per output (inverse
+// butterfly, signs), in the merge kernel.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -32,6 +32,10 @@
 
 namespace sai {
 namespace {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef int intx4_t __attribute__((ext_vector_type(4)));
 
 // round_f32 of kv_compression.rs:27-37 (half away from zero through a
 // truncation); x >= 0 here.
@@ -44,206 +48,396 @@ __device__ __forceinline__ float round_half_away(float x) {
   return t;
 }
 
-// The reference's butterfly (wht_butterfly_normalize, :81-110) on a register
-// array: stage h pairs (j, j + h) inside blocks of 2h; then * norm.
-template <int D>
-__device__ __forceinline__ void butterfly(float (&y)[D], float norm) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ float wave_min(float v) {
 #pragma unroll
-  for (int h = 1; h < D; h *= 2)
-#pragma unroll
-    for (int i = 0; i < D; i += 2 * h)
-#pragma unroll
-      for (int j = i; j < i + h; ++j) {
-        const float a = y[j], b = y[j + h];
-        y[j] = a + b;
-        y[j + h] = a - b;
-      }
-#pragma unroll
-  for (int i = 0; i < D; ++i) y[i] *= norm;
-}
-
-template <int D, int BITS>
-__device__ __forceinline__ uint32_t code_at(const uint32_t (&w)[D * BITS / 32], int i) {
-  const int bit = BITS * i, word = bit >> 5, off = bit & 31;
-  uint32_t v = w[word] >> off;
-  if (off + BITS > 32) v |= w[word + 1] << (32 - off);
-  return v & ((1u << BITS) - 1u);
+  for (int off = 32; off >= 1; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+  return v;
 }
 
 __device__ __forceinline__ float load_row_elem(const void* p, size_t i, bool bf16) {
   return bf16 ? __uint_as_float((uint32_t)((const uint16_t*)p)[i] << 16) : ((const float*)p)[i];
 }
 
-// ---- write: one thread per (b, s, head, K|V) row ---------------------------
-template <int D, int BITS>
-__global__ __launch_bounds__(64) void tq_write_kernel(const TqArgs a, const void* k, const void* v,
-                                                      int bf16, int batch, int s_new) {
+// The reference's butterfly (wht_butterfly_normalize, :81-110) over a row
+// spread across the wave (lane l: dims l + 64 e): stage h pairs dims (j, j+h)
+// into (a + b, a - b); stages below 64 pair lanes l and l ^ h, stage 64 the
+// two dims of a lane. Then * norm.
+template <int D>
+__device__ __forceinline__ void wave_butterfly(float (&y)[D / 64], int lane, float norm) {
 #pragma clang fp contract(off)
-  constexpr int W = D * BITS / 32;
-  constexpr uint32_t LEVELS = (1u << BITS) - 1u;
-  const int idx = blockIdx.x * 64 + threadIdx.x;
-  const int total = batch * s_new * a.heads * 2;
-  if (idx >= total) return;
-  const int kind = idx & 1;  // 0: K, 1: V
-  int r = idx >> 1;
-  const int h = r % a.heads;
-  r /= a.heads;
-  const int s = r % s_new;
-  const int b = r / s_new;
-  const void* src = kind ? v : k;
-  const size_t in_off = (((size_t)b * s_new + s) * a.heads + h) * D;
-  const int8_t* sg = a.signs + (size_t)h * D;
-  float y[D];
+  constexpr int E = D / 64;
 #pragma unroll
-  for (int i = 0; i < D; ++i) y[i] = load_row_elem(src, in_off + i, bf16 != 0) * (float)sg[i];
-  butterfly<D>(y, a.norm);
-  float mn = y[0], mx = y[0];
+  for (int h = 1; h < 64; h <<= 1) {
 #pragma unroll
-  for (int i = 1; i < D; ++i) {
-    mn = y[i] < mn ? y[i] : mn;
-    mx = y[i] > mx ? y[i] : mx;
-  }
-  const float range = mx - mn;
-  const float scale = range > 0.0f ? range / (float)LEVELS : 1.0f;
-  const float zero = mn;
-  uint32_t w[W];
-#pragma unroll
-  for (int j = 0; j < W; ++j) w[j] = 0u;
-#pragma unroll
-  for (int i = 0; i < D; ++i) {
-    uint32_t q = scale > 0.0f ? sat_u32(round_half_away((y[i] - zero) / scale)) : 0u;
-    q = q < LEVELS ? q : LEVELS;
-    const int bit = BITS * i, word = bit >> 5, off = bit & 31;
-    w[word] |= q << off;
-    if (off + BITS > 32) w[word + 1] |= q >> (32 - off);
-    y[i] = (float)q;  // keep the code for the QJL decode
-  }
-  const int pos = a.seq_lens[b] + s;
-  const size_t row = ((size_t)h * a.batch_cap + b) * a.rows_cap + pos;
-  uint8_t* codes = (kind ? a.codes_v : a.codes_k) + row * a.code_stride;
-#pragma unroll
-  for (int j = 0; j < W; ++j) ((uint32_t*)codes)[j] = w[j];
-  float c = 0.0f;
-  if (a.qjl) {
-    // decode (:270-291) then the residual's signs and mean |r| (:365-395),
-    // summed in index order
-#pragma unroll
-    for (int i = 0; i < D; ++i) y[i] = y[i] * scale + zero;
-    butterfly<D>(y, a.norm);
-    uint32_t sb[D / 32];
-#pragma unroll
-    for (int j = 0; j < D / 32; ++j) sb[j] = 0u;
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < D; ++i) {
-      const float approx = y[i] * (float)sg[i];
-      const float rr = load_row_elem(src, in_off + i, bf16 != 0) - approx;
-      sum += fabsf(rr);
-      if (rr >= 0.0f) sb[i >> 5] |= 1u << (i & 31);
+    for (int e = 0; e < E; ++e) {
+      const float p = __shfl_xor(y[e], h, 64);
+      y[e] = (lane & h) ? p - y[e] : y[e] + p;
     }
-    c = sum / (float)D;
-    uint32_t* sw = (kind ? a.signs_v : a.signs_k) + row * (D / 32);
-#pragma unroll
-    for (int j = 0; j < D / 32; ++j) sw[j] = sb[j];
   }
-  float4* par = (kind ? a.par_v : a.par_k) + row;
-  *par = make_float4(scale, zero, c, 0.0f);
+  if constexpr (E == 2) {
+    const float a0 = y[0], a1 = y[1];
+    y[0] = a0 + a1;
+    y[1] = a0 - a1;
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) y[e] *= norm;
 }
 
-// ---- read: one thread per (row, K|V), decode to f32 -------------------------
+// PolarQuantizer::encode of the row x (lane l: dims l + 64 e): rotated
+// values y, codes, scale, zero point.
+template <int D, int BITS>
+__device__ __forceinline__ void wave_encode(const float (&x)[D / 64], const float (&sgn)[D / 64],
+                                            int lane, float norm, float (&y)[D / 64],
+                                            uint32_t (&code)[D / 64], float& scale, float& zero) {
+#pragma clang fp contract(off)
+  constexpr int E = D / 64;
+  constexpr uint32_t LEVELS = (1u << BITS) - 1u;
+#pragma unroll
+  for (int e = 0; e < E; ++e) y[e] = x[e] * sgn[e];
+  wave_butterfly<D>(y, lane, norm);
+  float mn = y[0], mx = y[0];
+#pragma unroll
+  for (int e = 1; e < E; ++e) {
+    mn = fminf(mn, y[e]);
+    mx = fmaxf(mx, y[e]);
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  if (mn == 0.0f) {
+    // the reference keeps the first minimum in dim order: with a zero
+    // minimum, the sign of the first zero
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const uint64_t m = __ballot(y[e] == 0.0f);
+      if (m) {
+        mn = __shfl(y[e], __builtin_ctzll(m), 64);
+        break;
+      }
+    }
+  }
+  const float range = mx - mn;
+  scale = range > 0.0f ? range / (float)LEVELS : 1.0f;
+  zero = mn;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const uint32_t q = scale > 0.0f ? sat_u32(round_half_away((y[e] - zero) / scale)) : 0u;
+    code[e] = q < LEVELS ? q : LEVELS;
+  }
+}
+
+// QJLResidualEncoder::encode (:365-395) of x against decode(code): the sign
+// words (uniform, word j = dims 32j .. 32j+31) and C = sum|r| / D, summed in
+// dim order by lane 0. sres: the wave's D floats of LDS.
+template <int D>
+__device__ __forceinline__ float wave_qjl(const uint32_t (&code)[D / 64], float scale, float zero,
+                                          const float (&x)[D / 64], const float (&sgn)[D / 64],
+                                          int lane, float norm, float* sres,
+                                          uint64_t (&sbits)[D / 64]) {
+#pragma clang fp contract(off)
+  constexpr int E = D / 64;
+  float y[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) y[e] = (float)code[e] * scale + zero;
+  wave_butterfly<D>(y, lane, norm);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float r = x[e] - y[e] * sgn[e];
+    sbits[e] = __ballot(r >= 0.0f);
+    sres[lane + 64 * e] = fabsf(r);
+  }
+  __syncthreads();
+  float c = 0.0f;
+  if (lane == 0) {
+    float sum = 0.0f;
+#pragma unroll 16
+    for (int i = 0; i < D; ++i) sum += sres[i];
+    c = sum / (float)D;
+  }
+  __syncthreads();
+  return __shfl(c, 0, 64);
+}
+
+// ---- write: one wave per (sequence, kv head, K|V, 64-position tile) --------
+// The wave encodes the tile's rows of this pass in order. K rows go out
+// row-major; V codes are merged into the tile's words (read, modified in LDS,
+// written back) by the one wave that owns the tile.
+template <int D, int BITS>
+__global__ __launch_bounds__(64) void tq_write_kernel(const TqArgs a, const void* k, const void* v,
+                                                      int bf16, int s_new) {
+#pragma clang fp contract(off)
+  constexpr int E = D / 64;
+  constexpr int W = D * BITS / 32;  // K code words per row
+  constexpr int TBW = 2 * BITS;     // V words per dim per tile
+  constexpr uint32_t LEVELS = (1u << BITS) - 1u;
+  const int lane = threadIdx.x;
+  const int kind = blockIdx.y & 1, h = blockIdx.y >> 1, b = blockIdx.z;
+  const int len = a.seq_lens[b];
+  const int tile = len / 64 + (int)blockIdx.x;
+  const int r_lo = max(len, tile * 64), r_hi = min(len + s_new, tile * 64 + 64);
+  if (r_lo >= r_hi) return;  // uniform
+  __shared__ uint32_t scode[D];
+  __shared__ float sres[D];
+  __shared__ uint32_t stile[D][TBW + 1];
+  const void* src = kind ? v : k;
+  const bool is_bf16 = bf16 != 0;
+  float sgn[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) sgn[e] = (float)a.signs[(size_t)h * D + lane + 64 * e];
+  const size_t rbase = ((size_t)h * a.batch_cap + b) * a.rows_cap;
+  uint32_t* vt = (uint32_t*)(a.codes_v + (((size_t)h * a.batch_cap + b) * a.tiles_cap + tile) *
+                                             tq_vtile_bytes(D, BITS));
+  const int w_lo = ((r_lo - tile * 64) * BITS) >> 5;
+  const int w_hi = ((r_hi - tile * 64) * BITS - 1) >> 5;
+  if (kind) {
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      for (int w = w_lo; w <= w_hi; ++w) stile[lane + 64 * e][w] = vt[(lane + 64 * e) * TBW + w];
+  }
+  float4* par = (kind ? a.par_v : a.par_k) + rbase;
+  uint32_t* sw = (kind ? a.signs_v : a.signs_k) + rbase * (D / 32);
+  for (int r = r_lo; r < r_hi; ++r) {
+    const size_t in_off = (((size_t)b * s_new + (r - len)) * a.heads + h) * D;
+    float x[E], y[E], scale, zero;
+    uint32_t code[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) x[e] = load_row_elem(src, in_off + lane + 64 * e, is_bf16);
+    wave_encode<D, BITS>(x, sgn, lane, a.norm, y, code, scale, zero);
+    float csum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) csum += (float)code[e];
+    csum = wave_sum(csum);  // integers below 2^24: exact
+    if (kind == 0) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) scode[lane + 64 * e] = code[e];
+      __syncthreads();
+      if (lane < W) {
+        uint32_t wd = 0u;
+        const int i0 = (32 * lane) / BITS, i1 = (32 * lane + 31) / BITS;
+        for (int i = i0; i <= i1; ++i) {
+          const int bp = BITS * i - 32 * lane;
+          wd |= bp >= 0 ? (scode[i] << bp) : (scode[i] >> -bp);
+        }
+        ((uint32_t*)(a.codes_k + (rbase + r) * a.code_stride))[lane] = wd;
+      }
+      __syncthreads();
+    } else {
+      const int p = (r - tile * 64) * BITS, w = p >> 5, sh = p & 31;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        uint32_t* tw = stile[lane + 64 * e];
+        tw[w] = (tw[w] & ~(LEVELS << sh)) | (code[e] << sh);
+        if (sh + BITS > 32)
+          tw[w + 1] = (tw[w + 1] & ~(LEVELS >> (32 - sh))) | (code[e] >> (32 - sh));
+      }
+    }
+    float c = 0.0f;
+    if (a.qjl) {
+      uint64_t sb[E];
+      c = wave_qjl<D>(code, scale, zero, x, sgn, lane, a.norm, sres, sb);
+      if (lane < D / 32) {
+        const uint64_t m = sb[0];
+        uint64_t m1 = m;
+        if constexpr (E == 2) m1 = (lane >> 1) ? sb[1] : sb[0];
+        sw[(size_t)r * (D / 32) + lane] = (uint32_t)((lane & 1) ? (m1 >> 32) : m1);
+      }
+    }
+    if (lane == 0) par[r] = make_float4(scale, zero, c, csum);
+  }
+  if (kind) {
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      for (int w = w_lo; w <= w_hi; ++w) vt[(lane + 64 * e) * TBW + w] = stile[lane + 64 * e][w];
+  }
+}
+
+// V code of (position r, dim d) from the tile layout.
+template <int D, int BITS>
+__device__ __forceinline__ uint32_t v_code(const TqArgs& a, int h, int b, int r, int d) {
+  const uint32_t* e = (const uint32_t*)(a.codes_v + (((size_t)h * a.batch_cap + b) * a.tiles_cap +
+                                                     r / 64) * tq_vtile_bytes(D, BITS)) +
+                      d * (2 * BITS);
+  const int p = (r % 64) * BITS, w = p >> 5, sh = p & 31;
+  uint32_t c = e[w] >> sh;
+  if (sh + BITS > 32) c |= e[w + 1] << (32 - sh);
+  return c & ((1u << BITS) - 1u);
+}
+
+// ---- read: one thread per (row, K|V), decode to f32 (a checking path) -------
 template <int D, int BITS>
 __global__ __launch_bounds__(64) void tq_read_kernel(const TqArgs a, int b, int h, int start,
                                                      int len, float* k_out, float* v_out) {
 #pragma clang fp contract(off)
-  constexpr int W = D * BITS / 32;
   const int idx = blockIdx.x * 64 + threadIdx.x;
   if (idx >= 2 * len) return;
   const int kind = idx & 1;
   const int t = idx >> 1;
   const size_t row = ((size_t)h * a.batch_cap + b) * a.rows_cap + start + t;
-  const uint32_t* cw = (const uint32_t*)((kind ? a.codes_v : a.codes_k) + row * a.code_stride);
-  uint32_t w[W];
-#pragma unroll
-  for (int j = 0; j < W; ++j) w[j] = cw[j];
   const float4 par = (kind ? a.par_v : a.par_k)[row];
+  const uint8_t* kc = a.codes_k + row * a.code_stride;
   float y[D];
-#pragma unroll
-  for (int i = 0; i < D; ++i) y[i] = (float)code_at<D, BITS>(w, i) * par.x + par.y;
-  butterfly<D>(y, a.norm);
+  for (int i = 0; i < D; ++i) {
+    uint32_t c;
+    if (kind) {
+      c = v_code<D, BITS>(a, h, b, start + t, i);
+    } else {
+      const int p = BITS * i, w = p >> 5, sh = p & 31;
+      const uint32_t* cw = (const uint32_t*)kc;
+      c = cw[w] >> sh;
+      if (sh + BITS > 32) c |= cw[w + 1] << (32 - sh);
+      c &= (1u << BITS) - 1u;
+    }
+    y[i] = (float)c * par.x + par.y;
+  }
+  for (int hh = 1; hh < D; hh *= 2)
+    for (int i = 0; i < D; i += 2 * hh)
+      for (int j = i; j < i + hh; ++j) {
+        const float p = y[j], q = y[j + hh];
+        y[j] = p + q;
+        y[j + hh] = p - q;
+      }
   const int8_t* sg = a.signs + (size_t)h * D;
   float* out = (kind ? v_out : k_out) + (size_t)t * D;
-#pragma unroll
-  for (int i = 0; i < D; ++i) out[i] = y[i] * (float)sg[i];
+  for (int i = 0; i < D; ++i) out[i] = y[i] * a.norm * (float)sg[i];
 }
 
-// ---- query encoding: one thread per (sequence, query head) ------------------
-// The query row through the head's PolarQuantizer (as a cache row): its
-// rotated reconstruction q^ = code * scale + zero, sum(q^), and with QJL the
-// residual's C and sign words, as [D + 2 + D/32] floats per query head.
+// Byte position of dim d's code in a query record: the order in which the
+// attention kernel unpacks a K row into int8 MFMA operands (4 dims a step).
+// 4-bit: step 2w takes the low nibbles of word w (dims 8w, 8w+2, 8w+4,
+// 8w+6), step 2w+1 the high ones; 3- and 8-bit: dims in order.
+template <int BITS>
+__device__ __forceinline__ int q_code_pos(int d) {
+  if constexpr (BITS == 4) return 4 * (2 * (d >> 3) + (d & 1)) + ((d & 7) >> 1);
+  return d;
+}
+
+// ---- query encoding: one wave per (query head, sequence) --------------------
+// The query row through its kv head's quantizer; record (u32 words):
+//   [0, D/4)        codes - 2^(bits-1) as int8, in q_code_pos order
+//   D/4 + 0..3      alpha = qs, beta = qz', gamma = qs sum(qc') + D qz',
+//                   kappa = C / D, each times scale * log2(e)
+//   D/4 + 4 ..      QJL sign words
+// where qc' = qc - 2^(bits-1) and qz' = qz + qs 2^(bits-1), so that
+// decode(q) rotated = qs qc' + qz'.
 template <int D, int BITS>
-__global__ __launch_bounds__(64) void tq_query_kernel(const TqArgs a, TqAttendArgs t, int batch) {
+__global__ __launch_bounds__(64) void tq_query_kernel(const TqArgs a, TqAttendArgs t) {
 #pragma clang fp contract(off)
-  constexpr uint32_t LEVELS = (1u << BITS) - 1u;
-  constexpr int QREC = D + 2 + D / 32;
-  const int idx = blockIdx.x * 64 + threadIdx.x;
-  if (idx >= batch * t.num_heads) return;
-  const int qh = idx % t.num_heads;
+  constexpr int E = D / 64;
+  constexpr int QREC = tq_qrec_words(D);
+  constexpr int C0 = 1 << (BITS - 1);
+  __shared__ float sres[D];
+  const int lane = threadIdx.x;
+  const int qh = blockIdx.x, b = blockIdx.y;
   const int kvh = qh / (t.num_heads / a.heads);
-  const size_t qo = (size_t)idx * D;
-  const int8_t* sg = a.signs + (size_t)kvh * D;
-  float* rec = t.qenc + (size_t)idx * QREC;
-  float y[D];
+  const size_t qo = ((size_t)b * t.num_heads + qh) * D;
+  float x[E], y[E], sgn[E], scale, zero;
+  uint32_t code[E];
 #pragma unroll
-  for (int i = 0; i < D; ++i) y[i] = load_row_elem(t.q, qo + i, t.q_bf16 != 0) * (float)sg[i];
-  butterfly<D>(y, a.norm);
-  float mn = y[0], mx = y[0];
-#pragma unroll
-  for (int i = 1; i < D; ++i) {
-    mn = y[i] < mn ? y[i] : mn;
-    mx = y[i] > mx ? y[i] : mx;
+  for (int e = 0; e < E; ++e) {
+    sgn[e] = (float)a.signs[(size_t)kvh * D + lane + 64 * e];
+    x[e] = load_row_elem(t.q, qo + lane + 64 * e, t.q_bf16 != 0);
   }
-  const float range = mx - mn;
-  const float scale = range > 0.0f ? range / (float)LEVELS : 1.0f;
-  float qs = 0.0f;
+  wave_encode<D, BITS>(x, sgn, lane, a.norm, y, code, scale, zero);
+  uint32_t* rec = t.qenc + ((size_t)b * t.num_heads + qh) * QREC;
+  float sq = 0.0f;
 #pragma unroll
-  for (int i = 0; i < D; ++i) {
-    uint32_t q = scale > 0.0f ? sat_u32(round_half_away((y[i] - mn) / scale)) : 0u;
-    q = q < LEVELS ? q : LEVELS;
-    y[i] = (float)q * scale + mn;
-    rec[i] = y[i];
-    qs += y[i];
+  for (int e = 0; e < E; ++e) {
+    const int cc = (int)code[e] - C0;
+    sq += (float)cc;
+    ((int8_t*)rec)[q_code_pos<BITS>(lane + 64 * e)] = (int8_t)cc;
   }
-  rec[D] = qs;
+  sq = wave_sum(sq);
   float c = 0.0f;
-  uint32_t sb[D / 32];
+  uint64_t sb[E];
 #pragma unroll
-  for (int j = 0; j < D / 32; ++j) sb[j] = 0u;
-  if (a.qjl) {
-    butterfly<D>(y, a.norm);
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < D; ++i) {
-      const float rr = load_row_elem(t.q, qo + i, t.q_bf16 != 0) - y[i] * (float)sg[i];
-      sum += fabsf(rr);
-      if (rr >= 0.0f) sb[i >> 5] |= 1u << (i & 31);
-    }
-    c = sum / (float)D;
+  for (int e = 0; e < E; ++e) sb[e] = 0;
+  if (a.qjl) c = wave_qjl<D>(code, scale, zero, x, sgn, lane, a.norm, sres, sb);
+  if (lane == 0) {
+    const float qz = zero + scale * (float)C0;
+    float* rf = (float*)(rec + D / 4);
+    rf[0] = scale * t.scale_log2;
+    rf[1] = qz * t.scale_log2;
+    rf[2] = (scale * sq + (float)D * qz) * t.scale_log2;
+    rf[3] = c / (float)D * t.scale_log2;
   }
-  rec[D + 1] = c;
-#pragma unroll
-  for (int j = 0; j < D / 32; ++j) rec[D + 2 + j] = __uint_as_float(sb[j]);
+  if (lane < D / 32) {
+    uint64_t m = sb[0];
+    if constexpr (E == 2) m = (lane >> 1) ? sb[1] : sb[0];
+    rec[D / 4 + 4 + lane] = (uint32_t)((lane & 1) ? (m >> 32) : m);
+  }
+}
+
+// int8 MFMA operand of K row codes for logit step s (4 dims).
+template <int BITS, int KW>
+__device__ __forceinline__ int k_operand(const uint32_t (&kc)[KW], int s) {
+  if constexpr (BITS == 4) {
+    const uint32_t w = kc[s >> 1];
+    return (int)((s & 1) ? ((w >> 4) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu));
+  } else if constexpr (BITS == 8) {
+    return (int)(kc[s] ^ 0x80808080u);  // codes - 128
+  } else {
+    // dims 4s .. 4s+3: 12 bits at 12 s, spread to bytes
+    const int p = 12 * s, w = p >> 5, sh = p & 31;
+    uint32_t x = kc[w] >> sh;
+    if (sh > 20) x |= kc[w + 1] << (32 - sh);
+    x &= 0xFFFu;
+    x = (x | (x << 10)) & 0x003F003Fu;
+    return (int)((x | (x << 5)) & 0x07070707u);
+  }
+}
+
+// f16 MFMA operand (4 positions of one dim) of V codes, as subnormals
+// code * 2^-24, for value step s. 4-bit: word s/2 gives positions
+// (0, 4, 1, 5) + 8 (s/2) for even s and (2, 6, 3, 7) + 8 (s/2) for odd s;
+// 3- and 8-bit: positions 4s .. 4s+3 in order.
+template <int BITS, int TBW>
+__device__ __forceinline__ half4_t v_operand(const uint32_t (&vc)[TBW], int s) {
+  uint32_t lo, hi;
+  if constexpr (BITS == 4) {
+    const uint32_t w = vc[s >> 1] >> ((s & 1) * 8);
+    lo = w & 0x000F000Fu;
+    hi = (w >> 4) & 0x000F000Fu;
+  } else if constexpr (BITS == 8) {
+    lo = __builtin_amdgcn_perm(0u, vc[s], 0x0C010C00u);
+    hi = __builtin_amdgcn_perm(0u, vc[s], 0x0C030C02u);
+  } else {
+    const int p = 12 * s, w = p >> 5, sh = p & 31;
+    uint32_t x = vc[w] >> sh;
+    if (sh > 20) x |= vc[w + 1] << (32 - sh);
+    x &= 0xFFFu;
+    const uint32_t u = x | (x << 13);
+    lo = u & 0x00070007u;
+    hi = (u >> 6) & 0x00070007u;
+  }
+  const uint32_t pr[2] = {lo, hi};
+  half4_t r;
+  __builtin_memcpy(&r, pr, sizeof(r));
+  return r;
+}
+
+// Slot of tile position r in the P' rows, matching v_operand's order.
+template <int BITS>
+__device__ __forceinline__ int p_slot(int r) {
+  if constexpr (BITS == 4) return (r & ~7) + 2 * (r & 3) + ((r >> 2) & 1);
+  return r;
 }
 
 // ---- attention ---------------------------------------------------------------
-// Workgroup = (sequence b, kv head, split of split_rows rows), NW waves; a
-// wave takes 64-row tiles (lane = row for the logits, lane = dims for the
-// value sum); the group's encoded queries sit in LDS.
+// Workgroup = (split of split_rows positions, kv head, sequence), NW waves; a
+// wave takes 64-position tiles. Logits: lane = position, the group's heads in
+// quads (4x4x4 int8 MFMA: A = four heads' query codes, B = the lane's K row,
+// so lane l's result i is head 4u + i at position l). Values: lane = dim
+// (4x4x4 f16 MFMA: A = four heads' weights, B = the lane's dim over four
+// positions, so lane l's result i is head 4u + i at dim 64 e + l).
 template <int D, int BITS, int G, int NW>
 __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAttendArgs t) {
-  constexpr int W = D * BITS / 32;
-  constexpr uint32_t LEVELS = (1u << BITS) - 1u;
-  constexpr int DPL = D / 64;  // value dims per lane
+  constexpr int NQ = (G + 3) / 4;
+  constexpr int KW = D * BITS / 32;
+  constexpr int KWL = (KW + 3) / 4 * 4;  // words loaded (within code_stride)
+  constexpr int NS = D / 4;              // logit steps
+  constexpr int DH = D / 64;             // value dim halves
+  constexpr int TBW = 2 * BITS;          // V words per dim per tile
+  constexpr int QREC = tq_qrec_words(D);
+  constexpr int KOFF = BITS == 8 ? 128 : 0;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int kvh = blockIdx.y;
@@ -254,146 +448,205 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   if (r0 >= L) return;  // uniform: this split is past the sequence
   const int r1 = min(L, r0 + t.split_rows);
 
-  __shared__ float sq[G][D];       // q^
-  __shared__ float sqsum[G];       // sum_i q^_i
-  __shared__ float sqc[G];         // C_q
-  __shared__ uint32_t sqs[G][D / 32];
-  __shared__ uint32_t svk[NW][64][W + 1];  // a wave's tile of K codes (row-major, padded)
-  __shared__ uint32_t svc[NW][64][W + 1];  // a wave's tile of V codes
-  __shared__ float spv[NW][64][G];         // p * s_v of the tile's rows
-  {
-    // the group's encoded queries (tq_query_kernel): [G][QREC]
-    constexpr int QREC = D + 2 + D / 32;
-    const float* qe = t.qenc + ((size_t)b * t.num_heads + kvh * G) * QREC;
-    for (int e = threadIdx.x; e < G * QREC; e += 64 * NW) {
-      const int g = e / QREC, j = e % QREC;
-      const float v = qe[e];
-      if (j < D) sq[g][j] = v;
-      else if (j == D) sqsum[g] = v;
-      else if (j == D + 1) sqc[g] = v;
-      else sqs[g][j - D - 2] = __float_as_uint(v);
-    }
+  __shared__ uint32_t sqc[NQ * 4][NS];           // query code words (padding heads 0)
+  __shared__ _Float16 sp[NW][NQ * 4][64 + 4];    // a wave's P' rows
+  const uint32_t* qrec = t.qenc + ((size_t)b * t.num_heads + kvh * G) * QREC;
+  for (int e = threadIdx.x; e < NQ * 4 * NS; e += 64 * NW) {
+    const int g = e / NS, s = e % NS;
+    sqc[g][s] = g < G ? qrec[g * QREC + s] : 0u;
+  }
+  float qa[G], qb[G], qg[G], qk[G];
+  uint32_t qs[G][D / 32];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float* rf = (const float*)(qrec + g * QREC + D / 4);
+    qa[g] = rf[0];
+    qb[g] = rf[1];
+    qg[g] = rf[2];
+    qk[g] = rf[3];
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j) qs[g][j] = qrec[g * QREC + D / 4 + 4 + j];
   }
   __syncthreads();
 
-  float m_run[G], l_run[G], acc[G][DPL], zacc[G];
+  float m_run[G], l_run[G], z_run[G];
+  floatx4_t o_run[NQ][DH];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m_run[g] = -INFINITY;
     l_run[g] = 0.0f;
-    zacc[g] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) acc[g][e] = 0.0f;
+    z_run[g] = 0.0f;
   }
-  const size_t base = ((size_t)kvh * a.batch_cap + b) * a.rows_cap;
-  const float inv_d = 1.0f / (float)D;
+#pragma unroll
+  for (int u = 0; u < NQ; ++u)
+#pragma unroll
+    for (int e = 0; e < DH; ++e) o_run[u][e] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const size_t rbase = ((size_t)kvh * a.batch_cap + b) * a.rows_cap;
+  const uint8_t* vbase =
+      a.codes_v + ((size_t)kvh * a.batch_cap + b) * a.tiles_cap * tq_vtile_bytes(D, BITS);
   for (int tile0 = r0 + wave * 64; tile0 < r1; tile0 += 64 * NW) {
-    // q^ is re-read from LDS in every tile: kept out of registers, where the
-    // G * D values would not fit
-    __asm__ volatile("" ::: "memory");
     const int row = tile0 + lane;
     const bool live = row < r1;
-    const size_t rr = base + (live ? row : tile0);
-    // K and V codes of this lane's row into the wave's LDS tiles
-    const uint32_t* kc = (const uint32_t*)(a.codes_k + rr * a.code_stride);
-    const uint32_t* vc = (const uint32_t*)(a.codes_v + rr * a.code_stride);
+    const size_t rr = rbase + (live ? row : tile0);
+    // this lane's K row, its parameters and sign words; V codes of its dims
+    uint32_t kc[KWL];
+    {
+      const uint4* src = (const uint4*)(a.codes_k + rr * a.code_stride);
 #pragma unroll
-    for (int j = 0; j < W; ++j) {
-      svk[wave][lane][j] = kc[j];
-      svc[wave][lane][j] = vc[j];
+      for (int j = 0; j < KWL / 4; ++j) {
+        const uint4 w4 = src[j];
+        kc[4 * j] = w4.x;
+        kc[4 * j + 1] = w4.y;
+        kc[4 * j + 2] = w4.z;
+        kc[4 * j + 3] = w4.w;
+      }
     }
     const float4 kp = a.par_k[rr];
     const float4 vp = a.par_v[rr];
     uint32_t ks[D / 32];
     if (a.qjl) {
+      const uint4* src = (const uint4*)(a.signs_k + rr * (D / 32));
 #pragma unroll
-      for (int j = 0; j < D / 32; ++j) ks[j] = a.signs_k[rr * (D / 32) + j];
-    }
-    __builtin_amdgcn_wave_barrier();
-    // logits: 32 codes (BITS words) at a time, rolled, so that only one
-    // group's q^ values are live
-    float lg[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) lg[g] = 0.0f;
-#pragma unroll 1
-    for (int grp = 0; grp < D / 32; ++grp) {
-      uint32_t u[BITS + 1];
-#pragma unroll
-      for (int k = 0; k < BITS; ++k) u[k] = svk[wave][lane][grp * BITS + k];
-      u[BITS] = 0u;
-#pragma unroll
-      for (int c = 0; c < 32; ++c) {
-        const int bit = BITS * c, word = bit >> 5, off = bit & 31;
-        uint32_t v = u[word] >> off;
-        if (off + BITS > 32) v |= u[word + 1] << (32 - off);
-        const float cf = (float)(v & LEVELS);
-#pragma unroll
-        for (int g = 0; g < G; ++g) lg[g] += sq[g][grp * 32 + c] * cf;
+      for (int j = 0; j < D / 128; ++j) {
+        const uint4 w4 = src[j];
+        ks[4 * j] = w4.x;
+        ks[4 * j + 1] = w4.y;
+        ks[4 * j + 2] = w4.z;
+        ks[4 * j + 3] = w4.w;
+      }
+      if constexpr (D == 64) {
+        const uint2 w2 = *(const uint2*)(a.signs_k + rr * (D / 32));
+        ks[0] = w2.x;
+        ks[1] = w2.y;
       }
     }
+    uint32_t vc[DH][TBW];
+    {
+      const uint8_t* vt = vbase + (size_t)(tile0 / 64) * tq_vtile_bytes(D, BITS);
+#pragma unroll
+      for (int e = 0; e < DH; ++e) {
+        const uint2* src = (const uint2*)(vt + (size_t)(64 * e + lane) * (8 * BITS));
+#pragma unroll
+        for (int j = 0; j < TBW / 2; ++j) {
+          const uint2 w2 = src[j];
+          vc[e][2 * j] = w2.x;
+          vc[e][2 * j + 1] = w2.y;
+        }
+      }
+    }
+    // logits: exact integer dot products on the int8 MFMA
+    intx4_t ip[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) ip[u] = intx4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int kb = k_operand<BITS, KWL>(kc, s);
+#pragma unroll
+      for (int u = 0; u < NQ; ++u)
+        ip[u] = __builtin_amdgcn_mfma_i32_4x4x4i8((int)sqc[4 * u + (lane & 3)][s], kb, ip[u], 0, 0,
+                                                 0);
+    }
+    const float sk = kp.w - (float)(KOFF * D);
+    const float kz = kp.y + (float)KOFF * kp.x;
+    float lg[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float dot = kp.x * lg[g] + kp.y * sqsum[g];
+      const float ipf = (float)ip[g >> 2][g & 3];
+      float dot = kp.x * (qa[g] * ipf + qb[g] * sk) + kz * qg[g];
       if (a.qjl) {
         int pop = 0;
 #pragma unroll
-        for (int j = 0; j < D / 32; ++j) pop += __popc(sqs[g][j] ^ ks[j]);
-        dot += sqc[g] * kp.z * ((float)(D - 2 * pop) * inv_d);
+        for (int j = 0; j < D / 32; ++j) pop += __popc(qs[g][j] ^ ks[j]);
+        dot += qk[g] * kp.z * (float)(D - 2 * pop);
       }
-      lg[g] = live ? dot * t.scale_log2 : -INFINITY;
+      lg[g] = live ? dot : -INFINITY;
     }
-    // online softmax over the wave's 64 rows
+    // online softmax (log2 domain); the running max moves only when a lane
+    // exceeds it
     float alpha[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float mt = wave_max(lg[g]);
-      const float m_new = fmaxf(m_run[g], mt);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      alpha[g] = fast_exp2(m_run[g] - m_use);
-      const float p = fast_exp2(lg[g] - m_use);
-      l_run[g] = l_run[g] * alpha[g] + wave_sum(p);
-      m_run[g] = m_new;
-      spv[wave][lane][g] = p * vp.x;
-      zacc[g] = zacc[g] * alpha[g] + wave_sum(p * vp.y);
-    }
-    __builtin_amdgcn_wave_barrier();  // this wave's LDS tile, written above, read below
-    // values: lane owns dims DPL*lane .. +DPL-1
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) acc[g][e] *= alpha[g];
-    const int nrows = min(64, r1 - tile0);
-    for (int j = 0; j < nrows; ++j) {
-      float pv[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) pv[g] = spv[wave][j][g];
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) {
-        const int bit = BITS * (DPL * lane + e), word = bit >> 5, off = bit & 31;
-        uint32_t u = svc[wave][j][word] >> off;
-        if (BITS == 3 && off > 29) u |= svc[wave][j][word + 1] << (32 - off);
-        const float c = (float)(u & LEVELS);
-#pragma unroll
-        for (int g = 0; g < G; ++g) acc[g][e] += pv[g] * c;
+      alpha[g] = 1.0f;
+      if (__ballot(lg[g] > m_run[g])) {
+        const float m_new = fmaxf(m_run[g], wave_max(lg[g]));
+        alpha[g] = fast_exp2(m_run[g] - m_new);
+        m_run[g] = m_new;
       }
     }
-    __builtin_amdgcn_wave_barrier();  // this wave's LDS tile, written above, read below
+    // weights: P' = f16(p vs / S); the row's whole value (vs code + vz) and
+    // the normaliser take the same rounded weight p' = P' S / vs, so the
+    // f16 rounding perturbs each weight instead of splitting the row
+    const float vsmax = wave_max(live ? vp.x : 0.0f);
+    const float vsn = vp.x / vsmax;
+    const float rvsn = vsmax / vp.x;
+    const int slot = p_slot<BITS>(lane);
+#pragma unroll
+    for (int g = 0; g < NQ * 4; ++g) {
+      _Float16 ph = (_Float16)0.0f;
+      if (g < G) {
+        ph = (_Float16)(fast_exp2(lg[g] - m_run[g]) * vsn);
+        const float p = (float)ph * rvsn;
+        l_run[g] = l_run[g] * alpha[g] + p;
+        z_run[g] = z_run[g] * alpha[g] + p * vp.y;
+      }
+      sp[wave][g][slot] = ph;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // values: sum_t P'_t code_t on the f16 MFMA
+    floatx4_t mf[NQ][DH];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+#pragma unroll
+      for (int e = 0; e < DH; ++e) mf[u][e] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      half4_t pa[NQ];
+#pragma unroll
+      for (int u = 0; u < NQ; ++u) pa[u] = *(const half4_t*)&sp[wave][4 * u + (lane & 3)][4 * s];
+#pragma unroll
+      for (int e = 0; e < DH; ++e) {
+        const half4_t vb = v_operand<BITS, TBW>(vc[e], s);
+#pragma unroll
+        for (int u = 0; u < NQ; ++u)
+          mf[u][e] = __builtin_amdgcn_mfma_f32_4x4x4f16(pa[u], vb, mf[u][e], 0, 0, 0);
+      }
+    }
+    const float sc = vsmax * 16777216.0f;  // 2^24: the codes' subnormal scale
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+#pragma unroll
+      for (int e = 0; e < DH; ++e)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int g = 4 * u + i;
+          if (g < G) o_run[u][e][i] = o_run[u][e][i] * alpha[g] + mf[u][e][i] * sc;
+        }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   }
   // merge the waves through LDS, then one partial per workgroup
   __shared__ float sm_m[NW][G], sm_l[NW][G], sm_z[NW][G];
   __shared__ float sm_o[NW][G][D];
-  if (lane == 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < G; ++g) {
+    const float lsum = wave_sum(l_run[g]);
+    const float zsum = wave_sum(z_run[g]);
+    if (lane == 0) {
       sm_m[wave][g] = m_run[g];
-      sm_l[wave][g] = l_run[g];
-      sm_z[wave][g] = zacc[g];
+      sm_l[wave][g] = lsum;
+      sm_z[wave][g] = zsum;
     }
   }
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int u = 0; u < NQ; ++u)
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) sm_o[wave][g][DPL * lane + e] = acc[g][e];
+    for (int e = 0; e < DH; ++e)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * u + i < G) sm_o[wave][4 * u + i][64 * e + lane] = o_run[u][e][i];
   __syncthreads();
   float* part = t.partials + (((size_t)b * a.heads + kvh) * t.max_splits + split) * (G * (D + 2));
   for (int e = threadIdx.x; e < G * D; e += 64 * NW) {
@@ -455,9 +708,7 @@ __global__ __launch_bounds__(G * D) void tq_merge_kernel(const TqArgs a, TqAtten
 template <int D, int BITS>
 hipError_t attend_db(const TqArgs& a, const TqAttendArgs& t, int group, int nsplit, int batch,
                      hipStream_t st) {
-  const int nq = batch * t.num_heads;
-  hipLaunchKernelGGL((tq_query_kernel<D, BITS>), dim3((nq + 63) / 64), dim3(64), 0, st, a, t,
-                     batch);
+  hipLaunchKernelGGL((tq_query_kernel<D, BITS>), dim3(t.num_heads, batch), dim3(64), 0, st, a, t);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   const dim3 grid(nsplit, a.heads, batch);
   switch (group) {
@@ -483,12 +734,11 @@ hipError_t attend_db(const TqArgs& a, const TqAttendArgs& t, int group, int nspl
 template <typename F>
 hipError_t dispatch_dbits(int d, int bits, F&& f) {
   auto by_bits = [&](auto dd) -> hipError_t {
-    constexpr int DD = decltype(dd)::value;
     switch (bits) {
       case 3: return f(dd, std::integral_constant<int, 3>{});
       case 4: return f(dd, std::integral_constant<int, 4>{});
       case 8: return f(dd, std::integral_constant<int, 8>{});
-      default: (void)DD; return hipErrorInvalidValue;
+      default: return hipErrorInvalidValue;
     }
   };
   if (d == 64) return by_bits(std::integral_constant<int, 64>{});
@@ -500,12 +750,12 @@ hipError_t dispatch_dbits(int d, int bits, F&& f) {
 
 hipError_t launch_tq_write(const TqArgs& a, const void* k, const void* v, int bf16, int batch,
                            int s_new, hipStream_t st) {
-  const int total = batch * s_new * a.heads * 2;
-  if (total <= 0) return hipSuccess;
+  if (batch <= 0 || s_new <= 0) return hipSuccess;
+  // tiles a pass of s_new positions can touch, whatever the start's offset
+  const dim3 grid((s_new + 126) / 64, 2 * a.heads, batch);
   return dispatch_dbits(a.head_dim, a.bits, [&](auto dd, auto bb) -> hipError_t {
     constexpr int D = decltype(dd)::value, B = decltype(bb)::value;
-    hipLaunchKernelGGL((tq_write_kernel<D, B>), dim3((total + 63) / 64), dim3(64), 0, st, a, k,
-                       v, bf16, batch, s_new);
+    hipLaunchKernelGGL((tq_write_kernel<D, B>), grid, dim3(64), 0, st, a, k, v, bf16, s_new);
     return hipGetLastError();
   });
 }
