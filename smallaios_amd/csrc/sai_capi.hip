@@ -41,8 +41,6 @@ struct sai_ctx {
   // TurboQuant attention workspace
   float* tq_partials = nullptr;
   size_t tq_partial_floats = 0;
-  uint32_t* tq_qenc = nullptr;
-  size_t tq_qenc_words = 0;
 };
 
 struct sai_tqcache {
@@ -238,7 +236,6 @@ SAI_API void sai_destroy(sai_ctx* ctx) {
   if (!ctx) return;
   DeviceGuard dg(ctx->device);
   if (ctx->tq_partials) (void)hipFree(ctx->tq_partials);
-  if (ctx->tq_qenc) (void)hipFree(ctx->tq_qenc);
   if (ctx->partials) (void)hipFree(ctx->partials);
   if (ctx->seq_info) (void)hipFree(ctx->seq_info);
   if (ctx->counters) (void)hipFree(ctx->counters);
@@ -1429,7 +1426,6 @@ SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t laye
   const int32_t split_rows = 1024;
   const int32_t max_splits = (max_len + split_rows - 1) / split_rows;
   const size_t part_floats = (size_t)batch * H * max_splits * G * (D + 2);
-  const size_t qenc_words = (size_t)batch * num_heads * sai::tq_qrec_words(D);
   DeviceGuard dg(ctx->device);
   if (part_floats > ctx->tq_partial_floats) {
     if (ctx->tq_partials) (void)hipFree(ctx->tq_partials);
@@ -1439,14 +1435,6 @@ SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t laye
       return fail(ctx, SAI_ERR_ALLOC, "%s: workspace", op);
     ctx->tq_partial_floats = part_floats;
   }
-  if (qenc_words > ctx->tq_qenc_words) {
-    if (ctx->tq_qenc) (void)hipFree(ctx->tq_qenc);
-    ctx->tq_qenc = nullptr;
-    ctx->tq_qenc_words = 0;
-    if (hipMalloc(&ctx->tq_qenc, qenc_words * sizeof(uint32_t)) != hipSuccess)
-      return fail(ctx, SAI_ERR_ALLOC, "%s: workspace", op);
-    ctx->tq_qenc_words = qenc_words;
-  }
   sai::TqArgs a = tq_args(c, layer);
   sai::TqAttendArgs t{};
   t.q = q;
@@ -1454,7 +1442,6 @@ SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t laye
   t.num_heads = num_heads;
   t.out = out;
   t.partials = ctx->tq_partials;
-  t.qenc = ctx->tq_qenc;
   t.split_rows = split_rows;
   t.max_splits = max_splits;
   t.scale_log2 = (has_scale ? scale : sai_default_scale(D)) * 1.4426950408889634f;

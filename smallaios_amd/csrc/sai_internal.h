@@ -207,9 +207,6 @@ struct CopyRowsArgs {
 __host__ __device__ constexpr size_t tq_vtile_bytes(int d, int bits) {
   return (size_t)d * 8 * bits;
 }
-__host__ __device__ constexpr int tq_qrec_words(int d) {
-  return (d / 4 + 4 + d / 32 + 3) / 4 * 4;
-}
 
 struct TqArgs {
   uint8_t* codes_k;
@@ -232,7 +229,6 @@ struct TqAttendArgs {
   int num_heads;
   float* out;       // [batch, 1, num_heads * D]
   float* partials;  // [batch][heads][max_splits][G * (D + 2)]
-  uint32_t* qenc;   // [batch * num_heads][tq_qrec_words(D)]
   int split_rows, max_splits;
   float scale_log2;
 };

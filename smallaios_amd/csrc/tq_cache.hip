@@ -125,6 +125,14 @@ __device__ __forceinline__ void wave_encode(const float (&x)[D / 64], const floa
   }
 }
 
+// Orders a wave's LDS stores before its later LDS loads (the wave's LDS
+// operations complete in order; this keeps the compiler from moving them).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // QJLResidualEncoder::encode (:365-395) of x against decode(code): the sign
 // words (uniform, word j = dims 32j .. 32j+31) and C = sum|r| / D, summed in
 // dim order by lane 0. sres: the wave's D floats of LDS.
@@ -145,7 +153,7 @@ __device__ __forceinline__ float wave_qjl(const uint32_t (&code)[D / 64], float 
     sbits[e] = __ballot(r >= 0.0f);
     sres[lane + 64 * e] = fabsf(r);
   }
-  __syncthreads();
+  wave_lds_sync();
   float c = 0.0f;
   if (lane == 0) {
     float sum = 0.0f;
@@ -153,8 +161,9 @@ __device__ __forceinline__ float wave_qjl(const uint32_t (&code)[D / 64], float 
     for (int i = 0; i < D; ++i) sum += sres[i];
     c = sum / (float)D;
   }
-  __syncthreads();
-  return __shfl(c, 0, 64);
+  c = __shfl(c, 0, 64);
+  wave_lds_sync();  // sres is reused by the wave's next row
+  return c;
 }
 
 // ---- write: one wave per (sequence, kv head, K|V, 64-position tile) --------
@@ -310,24 +319,21 @@ __device__ __forceinline__ int q_code_pos(int d) {
   return d;
 }
 
-// ---- query encoding: one wave per (query head, sequence) --------------------
-// The query row through its kv head's quantizer; record (u32 words):
-//   [0, D/4)        codes - 2^(bits-1) as int8, in q_code_pos order
-//   D/4 + 0..3      alpha = qs, beta = qz', gamma = qs sum(qc') + D qz',
-//                   kappa = C / D, each times scale * log2(e)
-//   D/4 + 4 ..      QJL sign words
+// ---- query encoding: one wave per query head -------------------------------
+// The query row through its kv head's quantizer, into LDS:
+//   codes[D/4]  codes - 2^(bits-1) as int8, in q_code_pos order
+//   coef[4]     alpha = qs, beta = qz', gamma = qs sum(qc') + D qz',
+//               kappa = C / D, each times scale * log2(e)
+//   sgn[D/32]   QJL sign words
 // where qc' = qc - 2^(bits-1) and qz' = qz + qs 2^(bits-1), so that
 // decode(q) rotated = qs qc' + qz'.
 template <int D, int BITS>
-__global__ __launch_bounds__(64) void tq_query_kernel(const TqArgs a, TqAttendArgs t) {
+__device__ __forceinline__ void wave_encode_query(const TqArgs& a, const TqAttendArgs& t, int b,
+                                                  int qh, int kvh, int lane, float* sres,
+                                                  uint32_t* codes, float* coef, uint32_t* sgw) {
 #pragma clang fp contract(off)
   constexpr int E = D / 64;
-  constexpr int QREC = tq_qrec_words(D);
   constexpr int C0 = 1 << (BITS - 1);
-  __shared__ float sres[D];
-  const int lane = threadIdx.x;
-  const int qh = blockIdx.x, b = blockIdx.y;
-  const int kvh = qh / (t.num_heads / a.heads);
   const size_t qo = ((size_t)b * t.num_heads + qh) * D;
   float x[E], y[E], sgn[E], scale, zero;
   uint32_t code[E];
@@ -337,13 +343,12 @@ __global__ __launch_bounds__(64) void tq_query_kernel(const TqArgs a, TqAttendAr
     x[e] = load_row_elem(t.q, qo + lane + 64 * e, t.q_bf16 != 0);
   }
   wave_encode<D, BITS>(x, sgn, lane, a.norm, y, code, scale, zero);
-  uint32_t* rec = t.qenc + ((size_t)b * t.num_heads + qh) * QREC;
   float sq = 0.0f;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int cc = (int)code[e] - C0;
     sq += (float)cc;
-    ((int8_t*)rec)[q_code_pos<BITS>(lane + 64 * e)] = (int8_t)cc;
+    ((int8_t*)codes)[q_code_pos<BITS>(lane + 64 * e)] = (int8_t)cc;
   }
   sq = wave_sum(sq);
   float c = 0.0f;
@@ -353,16 +358,15 @@ __global__ __launch_bounds__(64) void tq_query_kernel(const TqArgs a, TqAttendAr
   if (a.qjl) c = wave_qjl<D>(code, scale, zero, x, sgn, lane, a.norm, sres, sb);
   if (lane == 0) {
     const float qz = zero + scale * (float)C0;
-    float* rf = (float*)(rec + D / 4);
-    rf[0] = scale * t.scale_log2;
-    rf[1] = qz * t.scale_log2;
-    rf[2] = (scale * sq + (float)D * qz) * t.scale_log2;
-    rf[3] = c / (float)D * t.scale_log2;
+    coef[0] = scale * t.scale_log2;
+    coef[1] = qz * t.scale_log2;
+    coef[2] = (scale * sq + (float)D * qz) * t.scale_log2;
+    coef[3] = c / (float)D * t.scale_log2;
   }
   if (lane < D / 32) {
     uint64_t m = sb[0];
     if constexpr (E == 2) m = (lane >> 1) ? sb[1] : sb[0];
-    rec[D / 4 + 4 + lane] = (uint32_t)((lane & 1) ? (m >> 32) : m);
+    sgw[lane] = (uint32_t)((lane & 1) ? (m >> 32) : m);
   }
 }
 
@@ -421,6 +425,80 @@ __device__ __forceinline__ int p_slot(int r) {
   return r;
 }
 
+// Rows sy[g] (the group's outputs in the rotated domain) back to the model's
+// domain: the butterfly's stages over LDS, then * norm and the signs, written
+// to out. All NT threads of the block take part.
+template <int D, int G, int NT>
+__device__ __forceinline__ void rotate_back(const TqArgs& a, const TqAttendArgs& t, int b,
+                                            int kvh, float (&sy)[G][D]) {
+#pragma clang fp contract(off)
+  constexpr int PER = (G * D + NT - 1) / NT;
+  for (int h = 1; h < D; h *= 2) {
+    float nv[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int e = threadIdx.x + k * NT;
+      if (e < G * D) {
+        const int g = e / D, i = e % D;
+        const float a0 = sy[g][i], a1 = sy[g][i ^ h];
+        nv[k] = (i & h) ? a1 - a0 : a0 + a1;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int e = threadIdx.x + k * NT;
+      if (e < G * D) sy[e / D][e % D] = nv[k];
+    }
+    __syncthreads();
+  }
+  for (int e = threadIdx.x; e < G * D; e += NT) {
+    const int g = e / D, i = e % D;
+    t.out[((size_t)b * t.num_heads + kvh * G + g) * D + i] =
+        sy[g][i] * a.norm * (float)a.signs[(size_t)kvh * D + i];
+  }
+}
+
+// Merge of the split partials of one (kv head, sequence) with more than one
+// split, then the rotation back. One thread per (head, dim); every thread
+// has the (m, l, o) loads of 16 splits in flight at once (the partials were
+// written by workgroups on other XCDs: each round is one memory latency).
+template <int D, int G>
+__global__ __launch_bounds__(G * D) void tq_merge_kernel(const TqArgs a, TqAttendArgs t) {
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int L = a.seq_lens[b] + a.pending;
+  const int nsplit = (L + t.split_rows - 1) / t.split_rows;
+  if (nsplit <= 1) return;  // finished by the attention kernel
+  const int g = threadIdx.x / D, i = threadIdx.x % D;
+  const size_t pstride = (size_t)G * (D + 2);
+  const float* part0 = t.partials + ((size_t)b * a.heads + kvh) * t.max_splits * pstride;
+  float M = -INFINITY, Ls = 0.0f, O = 0.0f;
+  for (int s0 = 0; s0 < nsplit; s0 += 16) {
+    float pm[16], pl[16], po[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float* ps = part0 + (size_t)min(s0 + j, nsplit - 1) * pstride + g * (D + 2);
+      pm[j] = ps[0];
+      pl[j] = ps[1];
+      po[j] = ps[2 + i];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (s0 + j >= nsplit || pm[j] == -INFINITY) continue;
+      const float Mn = fmaxf(M, pm[j]);
+      const float fa = fast_exp2(M - Mn);
+      const float fb = fast_exp2(pm[j] - Mn);
+      Ls = Ls * fa + pl[j] * fb;
+      O = O * fa + po[j] * fb;
+      M = Mn;
+    }
+  }
+  __shared__ float sy[G][D];
+  sy[g][i] = Ls > 0.0f ? O / Ls : 0.0f;
+  __syncthreads();
+  rotate_back<D, G, G * D>(a, t, b, kvh, sy);
+}
+
 // ---- attention ---------------------------------------------------------------
 // Workgroup = (split of split_rows positions, kv head, sequence), NW waves; a
 // wave takes 64-position tiles. Logits: lane = position, the group's heads in
@@ -436,7 +514,6 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   constexpr int NS = D / 4;              // logit steps
   constexpr int DH = D / 64;             // value dim halves
   constexpr int TBW = 2 * BITS;          // V words per dim per tile
-  constexpr int QREC = tq_qrec_words(D);
   constexpr int KOFF = BITS == 8 ? 128 : 0;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -449,25 +526,27 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   const int r1 = min(L, r0 + t.split_rows);
 
   __shared__ uint32_t sqc[NQ * 4][NS];           // query code words (padding heads 0)
+  __shared__ float sqf[G][4];                    // alpha, beta, gamma, kappa
+  __shared__ uint32_t sqs[G][D / 32];            // query QJL sign words
+  __shared__ float sres[NW][D];
   __shared__ _Float16 sp[NW][NQ * 4][64 + 4];    // a wave's P' rows
-  const uint32_t* qrec = t.qenc + ((size_t)b * t.num_heads + kvh * G) * QREC;
-  for (int e = threadIdx.x; e < NQ * 4 * NS; e += 64 * NW) {
-    const int g = e / NS, s = e % NS;
-    sqc[g][s] = g < G ? qrec[g * QREC + s] : 0u;
-  }
+  for (int e = threadIdx.x; e < (NQ * 4 - G) * NS; e += 64 * NW) sqc[G + e / NS][e % NS] = 0u;
+  for (int g = wave; g < G; g += NW)
+    wave_encode_query<D, BITS>(a, t, b, kvh * G + g, kvh, lane, sres[wave], sqc[g], sqf[g],
+                               sqs[g]);
+  __syncthreads();
+  // the query's coefficients and sign words are uniform: scalar registers
   float qa[G], qb[G], qg[G], qk[G];
   uint32_t qs[G][D / 32];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float* rf = (const float*)(qrec + g * QREC + D / 4);
-    qa[g] = rf[0];
-    qb[g] = rf[1];
-    qg[g] = rf[2];
-    qk[g] = rf[3];
+    qa[g] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sqf[g][0])));
+    qb[g] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sqf[g][1])));
+    qg[g] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sqf[g][2])));
+    qk[g] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sqf[g][3])));
 #pragma unroll
-    for (int j = 0; j < D / 32; ++j) qs[g][j] = qrec[g * QREC + D / 4 + 4 + j];
+    for (int j = 0; j < D / 32; ++j) qs[g][j] = __builtin_amdgcn_readfirstlane(sqs[g][j]);
   }
-  __syncthreads();
 
   float m_run[G], l_run[G], z_run[G];
   floatx4_t o_run[NQ][DH];
@@ -627,9 +706,10 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
   }
-  // merge the waves through LDS, then one partial per workgroup
+  // merge the waves through LDS
   __shared__ float sm_m[NW][G], sm_l[NW][G], sm_z[NW][G];
   __shared__ float sm_o[NW][G][D];
+  __shared__ float sy[G][D];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const float lsum = wave_sum(l_run[g]);
@@ -648,7 +728,9 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
       for (int i = 0; i < 4; ++i)
         if (4 * u + i < G) sm_o[wave][4 * u + i][64 * e + lane] = o_run[u][e][i];
   __syncthreads();
-  float* part = t.partials + (((size_t)b * a.heads + kvh) * t.max_splits + split) * (G * (D + 2));
+  const int nsplit = (L + t.split_rows - 1) / t.split_rows;
+  const size_t pstride = (size_t)G * (D + 2);
+  float* part0 = t.partials + ((size_t)b * a.heads + kvh) * t.max_splits * pstride;
   for (int e = threadIdx.x; e < G * D; e += 64 * NW) {
     const int g = e / D, i = e % D;
     float M = -INFINITY;
@@ -662,54 +744,25 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
       Ls += sm_l[w][g] * f;
       O += (sm_o[w][g][i] + sm_z[w][g]) * f;
     }
-    part[g * (D + 2) + 2 + i] = O;
-    if (i == 0) {
-      part[g * (D + 2)] = M;
-      part[g * (D + 2) + 1] = Ls;
+    if (nsplit == 1) {
+      sy[g][i] = Ls > 0.0f ? O / Ls : 0.0f;
+    } else {
+      float* part = part0 + split * pstride + g * (D + 2);
+      part[2 + i] = O;
+      if (i == 0) {
+        part[0] = M;
+        part[1] = Ls;
+      }
     }
   }
-}
-
-// Merge the splits of one (sequence, kv head), rotate back (inverse
-// butterfly through LDS, then the signs) and normalise. One thread per
-// (head, dim).
-template <int D, int G>
-__global__ __launch_bounds__(G * D) void tq_merge_kernel(const TqArgs a, TqAttendArgs t) {
-#pragma clang fp contract(off)
-  const int kvh = blockIdx.x, b = blockIdx.y;
-  const int g = threadIdx.x / D, i = threadIdx.x % D;
-  const int L = a.seq_lens[b] + a.pending;
-  const int nsplit = (L + t.split_rows - 1) / t.split_rows;
-  const float* part = t.partials + ((size_t)b * a.heads + kvh) * t.max_splits * (G * (D + 2));
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part[(size_t)s * (G * (D + 2)) + g * (D + 2)]);
-  float Ls = 0.0f, O = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float* ps = part + (size_t)s * (G * (D + 2)) + g * (D + 2);
-    if (ps[0] == -INFINITY) continue;
-    const float f = fast_exp2(ps[0] - M);
-    Ls += ps[1] * f;
-    O += ps[2 + i] * f;
-  }
-  __shared__ float sy[G][D];
-  sy[g][i] = Ls > 0.0f ? O / Ls : 0.0f;
+  if (nsplit > 1) return;  // tq_merge_kernel finishes
   __syncthreads();
-  // inverse rotation: the same butterfly stages, one element per thread
-  for (int h = 1; h < D; h *= 2) {
-    const float a0 = sy[g][i], a1 = sy[g][i ^ h];
-    __syncthreads();
-    sy[g][i] = (i & h) ? a1 - a0 : a0 + a1;
-    __syncthreads();
-  }
-  const float y = sy[g][i] * a.norm * (float)a.signs[(size_t)kvh * D + i];
-  t.out[((size_t)b * t.num_heads + kvh * G + g) * D + i] = y;
+  rotate_back<D, G, 64 * NW>(a, t, b, kvh, sy);
 }
 
 template <int D, int BITS>
 hipError_t attend_db(const TqArgs& a, const TqAttendArgs& t, int group, int nsplit, int batch,
                      hipStream_t st) {
-  hipLaunchKernelGGL((tq_query_kernel<D, BITS>), dim3(t.num_heads, batch), dim3(64), 0, st, a, t);
-  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   const dim3 grid(nsplit, a.heads, batch);
   switch (group) {
     case 1: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 1, 4>), grid, dim3(256), 0, st, a, t); break;
@@ -719,7 +772,7 @@ hipError_t attend_db(const TqArgs& a, const TqAttendArgs& t, int group, int nspl
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || nsplit <= 1) return e;
   const dim3 mg(a.heads, batch);
   switch (group) {
     case 1: hipLaunchKernelGGL((tq_merge_kernel<D, 1>), mg, dim3(D), 0, st, a, t); break;
