@@ -311,6 +311,13 @@ sai_status sai_tqcache_reset(sai_ctx* ctx, sai_tqcache* cache);
 /* Host view: lens_out[max_batch] committed rows, *pending_out, *batch_out. */
 sai_status sai_tqcache_lengths(const sai_tqcache* cache, int32_t* lens_out, int32_t* pending_out,
                                int32_t* batch_out);
+/* memory_bytes (kv_compression.rs:928-957): *reference_bytes = the
+ * reference's accounting of the committed rows (every layer holding each
+ * sequence's rows: packed codes + 25 bytes per block, sign words + 12 bytes
+ * per residual, K and V); *device_bytes = what this cache holds on the
+ * device at its capacity. Either may be NULL. */
+sai_status sai_tqcache_memory_bytes(const sai_tqcache* cache, uint64_t* reference_bytes,
+                                    uint64_t* device_bytes);
 /* read_k / read_v (kv_compression.rs:862-907): rows [start, start+len) of
  * (layer, sequence b, kv head) decoded to f32, host arrays [len][head_dim]
  * each. Synchronous. */

@@ -87,6 +87,7 @@ EXPORTS = [
     "sai_rope_tables", "sai_copy_rows", "sai_tqcache_create", "sai_tqcache_destroy",
     "sai_tqcache_write", "sai_tqcache_advance", "sai_tqcache_reset", "sai_tqcache_set_lengths",
     "sai_tqcache_lengths", "sai_tqcache_read", "sai_tqcache_read_raw", "sai_tqcache_attend",
+    "sai_tqcache_memory_bytes",
 ]
 ROPE_BHSD = 0
 ROPE_BSHD = 1
@@ -138,6 +139,7 @@ def _declare(L: C.CDLL) -> None:
         "sai_tqcache_read": (i32, [p, p, i32, i32, i32, i32, i32, p, p]),
         "sai_tqcache_read_raw": (i32, [p, p, i32, i32, i32, i32, i32, p, p, p, p, p, p]),
         "sai_tqcache_attend": (i32, [p, p, i32, p, i32, i32, i32, i32, f, p, p]),
+        "sai_tqcache_memory_bytes": (i32, [p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -468,6 +470,14 @@ class TqCache:
         self._L.sai_tqcache_lengths(self.handle, out.ctypes.data_as(C.c_void_p), C.byref(pend),
                                     C.byref(b))
         return out, pend.value, b.value
+
+    def memory_bytes(self):
+        """(the reference's memory_bytes of the committed rows, device bytes held)."""
+        r, d = C.c_uint64(), C.c_uint64()
+        st = self._L.sai_tqcache_memory_bytes(self.handle, C.byref(r), C.byref(d))
+        if st != SAI_OK:
+            raise SaiError(st, "tqcache_memory_bytes")
+        return r.value, d.value
 
     def read(self, layer, b, kv_head, start, n):
         """Decoded rows (read_k, read_v), f32 [n, head_dim] each (synchronous)."""

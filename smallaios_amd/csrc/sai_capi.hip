@@ -1300,6 +1300,32 @@ SAI_API sai_status sai_tqcache_lengths(const sai_tqcache* c, int32_t* lens_out,
   return SAI_OK;
 }
 
+SAI_API sai_status sai_tqcache_memory_bytes(const sai_tqcache* c, uint64_t* reference_bytes,
+                                            uint64_t* device_bytes) {
+  if (!c) return SAI_ERR_NULL;
+  const sai_tqcache_desc& d = c->desc;
+  if (reference_bytes) {
+    // QuantizedBlock: packed data + 4 floats + dim + bits; QJLResidual: sign
+    // words + c + dim (kv_compression.rs:166-168, :352-354), K and V
+    const uint64_t block = ((uint64_t)d.head_dim * d.bits + 7) / 8 + 4 * 4 + 8 + 1;
+    const uint64_t resid = ((uint64_t)d.head_dim + 63) / 64 * 8 + 4 + 8;
+    const uint64_t per_row = 2 * block + (d.qjl ? 2 * resid : 0);
+    uint64_t rows = 0;
+    for (int b = 0; b < d.max_batch; ++b) rows += (uint64_t)c->h_lens[b];
+    *reference_bytes = rows * (uint64_t)d.num_layers * d.num_kv_heads * per_row;
+  }
+  if (device_bytes) {
+    const uint64_t per_layer =
+        (uint64_t)c->rows_total * (c->code_stride + 2 * sizeof(float4) +
+                                   (d.qjl ? 2 * (uint64_t)d.head_dim / 8 : 0)) +
+        (uint64_t)d.num_kv_heads * d.max_batch * c->tiles_cap *
+            sai::tq_vtile_bytes(d.head_dim, d.bits) +
+        (uint64_t)d.num_kv_heads * d.head_dim;
+    *device_bytes = per_layer * d.num_layers + (uint64_t)d.max_batch * sizeof(int32_t);
+  }
+  return SAI_OK;
+}
+
 SAI_API sai_status sai_tqcache_read(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int32_t b,
                                     int32_t head, int32_t start, int32_t len, float* k_out,
                                     float* v_out) {

@@ -203,6 +203,29 @@ def test_attend_long_ragged_splits(rt):
         c.close()
 
 
+def test_memory_bytes(rt):
+    """cache_memory_footprint (kv_compression.rs:1517-1547): 128 rows of D=64,
+    4-bit + QJL stay below the f32 size; the count follows the reference's
+    per-block (packed + 25 B) and per-residual (words * 8 + 12 B) sizes."""
+    import torch
+    d = 64
+    c = S.TqCache(rt, 1, 1, d, 4, True, 1, 128, seed=42)
+    try:
+        pos = np.arange(128, dtype=np.float32)[:, None]
+        k = ((np.arange(d, dtype=np.float32)[None] + pos) * np.float32(0.01)).reshape(1, 128, d)
+        v = ((np.arange(d, dtype=np.float32)[None] + pos + 100) * np.float32(0.01)).reshape(1, 128, d)
+        assert c.memory_bytes()[0] == 0
+        c.write(0, to_dev(k.astype(np.float32), False), to_dev(v.astype(np.float32), False), 1, 128)
+        c.advance()
+        torch.cuda.synchronize()
+        ref, dev = c.memory_bytes()
+        assert ref < 128 * d * 4 * 2
+        assert ref == 128 * (2 * (32 + 25) + 2 * (8 + 12))
+        assert dev >= 128 * (2 * 32 + 32)
+    finally:
+        c.close()
+
+
 def test_errors_and_lifecycle(rt):
     import torch
     with pytest.raises(S.SaiError) as e:
