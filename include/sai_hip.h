@@ -344,6 +344,25 @@ sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, c
                               int32_t dtype, int32_t batch, int32_t num_heads, int32_t has_scale,
                               float scale, float* out, void* stream);
 
+/* The design's two cache primitives of the GQA read path
+ * (docs/kv-compression-design.md section 9, steps 4 and 6), over the
+ * committed + pending rows of `layer`; the reference has not implemented
+ * them yet.
+ * attention_logits: logits[(b * num_heads + h) * ld + t] = the inner-product
+ * estimate <decode(q_h), decode(k_t)> (+ the QJL correction) of query head h
+ * with row t of its kv head, for t < the sequence's rows; q as in
+ * sai_tqcache_attend; unscaled. ld >= the longest sequence. */
+sai_status sai_tqcache_attention_logits(sai_ctx* ctx, sai_tqcache* cache, int32_t layer,
+                                        const void* q, int32_t dtype, int32_t batch,
+                                        int32_t num_heads, float* logits, int32_t ld,
+                                        void* stream);
+/* weighted_value_sum: out[b, h, :] = sum_t weights[(b * num_heads + h) * ld
+ * + t] * decode(v_t) over the sequence's rows (not normalised); weights and
+ * out device f32 (out [batch, 1, num_heads * head_dim]). */
+sai_status sai_tqcache_weighted_value_sum(sai_ctx* ctx, sai_tqcache* cache, int32_t layer,
+                                          const float* weights, int32_t ld, int32_t batch,
+                                          int32_t num_heads, float* out, void* stream);
+
 /* ---- tuning / introspection ------------------------------------------------- */
 /* Tokens per split-K work item of the decode kernel (0 = automatic, else a
  * multiple of 64). Returns the previous value. */

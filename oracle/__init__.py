@@ -99,6 +99,8 @@ def _declare(L: C.CDLL) -> None:
         "sai_or_tq_write_row": (_i, [_p, _i, _i, _p, _i, _p, _p, _p, _p, _p]),
         "sai_or_tq_attend": (_i, [_p, _i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p,
                                   _f, _p]),
+        "sai_or_tq_attention_logits": (_i, [_p, _i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _p, _p]),
+        "sai_or_tq_weighted_value_sum": (None, [_p, _i, _i, _i, _p, _i, _p, _p, _p, _p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -297,6 +299,36 @@ def tq_attend(q, bits, qjl, signs, k, v, scale):
                                 _ptr(np.ascontiguousarray(vc)), _ptr(vs), _ptr(vz),
                                 float(scale), _ptr(out))
     _check(rc, "tq_attend")
+    return out
+
+
+def tq_attention_logits(q, bits, qjl, signs, k):
+    """The design's attention_logits over encoded rows k (tq_write_rows
+    output): [G, rows] unscaled estimates."""
+    q = _f32(q)
+    g, d = q.shape
+    kc, ks, kz, ksb, kcm = k
+    n = kc.shape[0]
+    out = np.zeros((g, n), np.float32)
+    sg = np.ascontiguousarray(signs, np.int8)
+    rc = lib().sai_or_tq_attention_logits(_ptr(q), g, d, bits, int(qjl), _ptr(sg), n,
+                                          _ptr(np.ascontiguousarray(kc)), _ptr(ks), _ptr(kz),
+                                          _ptr(np.ascontiguousarray(ksb)), _ptr(kcm), _ptr(out))
+    _check(rc, "tq_attention_logits")
+    return out
+
+
+def tq_weighted_value_sum(weights, bits, signs, v):
+    """The design's weighted_value_sum: [G, D] = weights [G, rows] x decoded v."""
+    w = _f32(weights)
+    g, n = w.shape
+    vc, vs, vz, _, _ = v
+    d = len(signs)
+    out = np.zeros((g, d), np.float32)
+    sg = np.ascontiguousarray(signs, np.int8)
+    lib().sai_or_tq_weighted_value_sum(_ptr(w), g, d, bits, _ptr(sg), n,
+                                       _ptr(np.ascontiguousarray(vc)), _ptr(vs), _ptr(vz),
+                                       _ptr(out))
     return out
 
 

@@ -961,3 +961,56 @@ int sai_or_tq_attend(const float* q, int G, int dim, int bits, int qjl, const in
   free(qs);
   return rc;
 }
+
+/* The design's attention_logits (docs/kv-compression-design.md section 9,
+ * step 4) with the module's estimator (kv_compression.rs:1254-1288): for
+ * each of the G query heads, q is encoded with the head's quantizer and
+ * logits[h][t] = <decode(q), decode(k_t)> + (qjl ? correction : 0), dot in
+ * dim order. Unscaled. */
+int sai_or_tq_attention_logits(const float* q, int G, int dim, int bits, int qjl,
+                               const int8_t* signs, int rows, const uint8_t* k_codes,
+                               const float* k_scale, const float* k_zero, const uint64_t* k_signs,
+                               const float* k_c, float* logits) {
+  int code_bytes = (dim * bits + 7) / 8, words = (dim + 63) / 64;
+  float* qd = (float*)malloc(sizeof(float) * (size_t)dim);
+  float* kd = (float*)malloc(sizeof(float) * (size_t)dim);
+  uint8_t* qp = (uint8_t*)malloc((size_t)code_bytes);
+  uint64_t* qs = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)words);
+  int rc = OK;
+  for (int h = 0; h < G && rc == OK; ++h) {
+    float qsc, qz, qc = 0.0f;
+    rc = sai_or_tq_write_row(q + (size_t)h * dim, dim, bits, signs, qjl, qp, &qsc, &qz, qs, &qc);
+    if (rc != OK) break;
+    sai_or_tq_decode(qp, dim, bits, qsc, qz, signs, qd);
+    for (int t = 0; t < rows; ++t) {
+      sai_or_tq_decode(k_codes + (size_t)t * code_bytes, dim, bits, k_scale[t], k_zero[t], signs, kd);
+      float dot = 0.0f;
+      for (int i = 0; i < dim; ++i) dot += qd[i] * kd[i];
+      if (qjl) dot += sai_or_qjl_correction(qs, qc, k_signs + (size_t)t * words, k_c[t], dim);
+      logits[(size_t)h * rows + t] = dot;
+    }
+  }
+  free(qd);
+  free(kd);
+  free(qp);
+  free(qs);
+  return rc;
+}
+
+/* The design's weighted_value_sum (section 9, step 6): out[h] = sum_t
+ * weights[h][t] * decode(v_t), rows in order, not normalised. */
+void sai_or_tq_weighted_value_sum(const float* weights, int G, int dim, int bits,
+                                  const int8_t* signs, int rows, const uint8_t* v_codes,
+                                  const float* v_scale, const float* v_zero, float* out) {
+  int code_bytes = (dim * bits + 7) / 8;
+  float* vd = (float*)malloc(sizeof(float) * (size_t)dim);
+  for (int i = 0; i < G * dim; ++i) out[i] = 0.0f;
+  for (int t = 0; t < rows; ++t) {
+    sai_or_tq_decode(v_codes + (size_t)t * code_bytes, dim, bits, v_scale[t], v_zero[t], signs, vd);
+    for (int h = 0; h < G; ++h) {
+      float w = weights[(size_t)h * rows + t];
+      for (int i = 0; i < dim; ++i) out[(size_t)h * dim + i] += w * vd[i];
+    }
+  }
+  free(vd);
+}

@@ -161,4 +161,12 @@ uint64_t sai_or_check_rhe_vs_rint(uint64_t lo, uint64_t hi);
 }
 #endif
 
+int sai_or_tq_attention_logits(const float* q, int G, int dim, int bits, int qjl,
+                               const int8_t* signs, int rows, const uint8_t* k_codes,
+                               const float* k_scale, const float* k_zero, const uint64_t* k_signs,
+                               const float* k_c, float* logits);
+void sai_or_tq_weighted_value_sum(const float* weights, int G, int dim, int bits,
+                                  const int8_t* signs, int rows, const uint8_t* v_codes,
+                                  const float* v_scale, const float* v_zero, float* out);
+
 #endif

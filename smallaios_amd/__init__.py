@@ -87,7 +87,7 @@ EXPORTS = [
     "sai_rope_tables", "sai_copy_rows", "sai_tqcache_create", "sai_tqcache_destroy",
     "sai_tqcache_write", "sai_tqcache_advance", "sai_tqcache_reset", "sai_tqcache_set_lengths",
     "sai_tqcache_lengths", "sai_tqcache_read", "sai_tqcache_read_raw", "sai_tqcache_attend",
-    "sai_tqcache_memory_bytes",
+    "sai_tqcache_memory_bytes", "sai_tqcache_attention_logits", "sai_tqcache_weighted_value_sum",
 ]
 ROPE_BHSD = 0
 ROPE_BSHD = 1
@@ -140,6 +140,8 @@ def _declare(L: C.CDLL) -> None:
         "sai_tqcache_read_raw": (i32, [p, p, i32, i32, i32, i32, i32, p, p, p, p, p, p]),
         "sai_tqcache_attend": (i32, [p, p, i32, p, i32, i32, i32, i32, f, p, p]),
         "sai_tqcache_memory_bytes": (i32, [p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+        "sai_tqcache_attention_logits": (i32, [p, p, i32, p, i32, i32, i32, p, i32, p]),
+        "sai_tqcache_weighted_value_sum": (i32, [p, p, i32, p, i32, i32, i32, p, p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -504,6 +506,20 @@ class TqCache:
             self.rt.handle, self.handle, layer, b, kv_head, start, n, ptr("k_codes"),
             ptr("v_codes"), ptr("k_params"), ptr("v_params"), sk, sv), "tqcache_read_raw")
         return r
+
+    def attention_logits(self, layer, q, logits, ld, batch, num_heads, stream=None, dtype=None):
+        """logits: device f32 [batch * num_heads, ld] (unscaled inner-product estimates)."""
+        dt = dtype if dtype is not None else _dtype_code(q)
+        self.rt.check(self._L.sai_tqcache_attention_logits(
+            self.rt.handle, self.handle, layer, _dev_ptr(q), dt, batch, num_heads,
+            _dev_ptr(logits), int(ld), _stream(stream)), "tqcache_attention_logits")
+
+    def weighted_value_sum(self, layer, weights, ld, out, batch, num_heads, stream=None):
+        """weights: device f32 [batch * num_heads, ld]; out: device f32
+        [batch, 1, num_heads * head_dim]."""
+        self.rt.check(self._L.sai_tqcache_weighted_value_sum(
+            self.rt.handle, self.handle, layer, _dev_ptr(weights), int(ld), batch, num_heads,
+            _dev_ptr(out), _stream(stream)), "tqcache_weighted_value_sum")
 
     def attend(self, layer, q, out, batch, num_heads, scale=None, stream=None, dtype=None):
         """q: device [batch, 1, num_heads*head_dim]; out: device f32, same shape."""

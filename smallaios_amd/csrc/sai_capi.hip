@@ -1424,15 +1424,20 @@ SAI_API sai_status sai_tqcache_read_raw(sai_ctx* ctx, sai_tqcache* c, int32_t la
   return SAI_OK;
 }
 
-SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t layer, const void* q,
-                                      int32_t dtype, int32_t batch, int32_t num_heads,
-                                      int32_t has_scale, float scale, float* out, void* stream) {
-  if (!ctx || !c) return SAI_ERR_NULL;
-  const char* op = "tq_cache_attend";
-  if (!q || !out) return fail(ctx, SAI_ERR_NULL, "%s: missing query/output", op);
+namespace {
+
+// The three read paths over a TurboQuant layer: mode 0 attention, 1 logits,
+// 2 weighted value sum. q / weights / out as the entry points document.
+sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, const void* q,
+                        int32_t dtype, const float* weights, int32_t ld, int32_t batch,
+                        int32_t num_heads, float scale_log2, float* out, void* stream,
+                        const char* op) {
+  if (mode != 2 && !q) return fail(ctx, SAI_ERR_NULL, "%s: missing query", op);
+  if (mode == 2 && !weights) return fail(ctx, SAI_ERR_NULL, "%s: missing weights", op);
+  if (!out) return fail(ctx, SAI_ERR_NULL, "%s: missing output", op);
   if (layer < 0 || layer >= c->desc.num_layers)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: layer_idx %d", op, layer);
-  if (dtype != SAI_DTYPE_F32 && dtype != SAI_DTYPE_BF16)
+  if (mode != 2 && dtype != SAI_DTYPE_F32 && dtype != SAI_DTYPE_BF16)
     return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (want f32 or bf16)", op, dtype);
   const int H = c->desc.num_kv_heads, D = c->desc.head_dim;
   if (num_heads <= 0 || num_heads % H != 0)
@@ -1448,12 +1453,15 @@ SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t laye
   int32_t max_len = 0;
   for (int b = 0; b < batch; ++b) max_len = std::max(max_len, c->h_lens[b] + c->pending);
   if (max_len <= 0) return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: empty cache", op);
+  if (mode != 0 && ld < max_len)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: row stride %d below the %d positions", op, ld,
+                max_len);
   // splits of 1024 rows (16 tiles of 64 per 4-wave workgroup)
   const int32_t split_rows = 1024;
   const int32_t max_splits = (max_len + split_rows - 1) / split_rows;
   const size_t part_floats = (size_t)batch * H * max_splits * G * (D + 2);
   DeviceGuard dg(ctx->device);
-  if (part_floats > ctx->tq_partial_floats) {
+  if (mode != 1 && part_floats > ctx->tq_partial_floats) {
     if (ctx->tq_partials) (void)hipFree(ctx->tq_partials);
     ctx->tq_partials = nullptr;
     ctx->tq_partial_floats = 0;
@@ -1468,10 +1476,43 @@ SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t laye
   t.num_heads = num_heads;
   t.out = out;
   t.partials = ctx->tq_partials;
+  t.weights = weights;
+  t.ld = ld;
+  t.normalize = mode == 0 ? 1 : 0;
   t.split_rows = split_rows;
   t.max_splits = max_splits;
-  t.scale_log2 = (has_scale ? scale : sai_default_scale(D)) * 1.4426950408889634f;
-  const hipError_t e = sai::launch_tq_attend(a, t, G, max_splits, batch, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(ctx, e, "tq_cache_attend launch");
+  t.scale_log2 = scale_log2;
+  const hipError_t e =
+      sai::launch_tq_attend(a, t, mode, G, max_splits, batch, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, op);
   return SAI_OK;
+}
+
+}  // namespace
+
+SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t layer, const void* q,
+                                      int32_t dtype, int32_t batch, int32_t num_heads,
+                                      int32_t has_scale, float scale, float* out, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const float sc = has_scale ? scale : sai_default_scale(c->desc.head_dim);
+  return tq_read_path(ctx, c, layer, 0, q, dtype, nullptr, 0, batch, num_heads,
+                      sc * 1.4426950408889634f, out, stream, "tq_cache_attend");
+}
+
+SAI_API sai_status sai_tqcache_attention_logits(sai_ctx* ctx, sai_tqcache* c, int32_t layer,
+                                                const void* q, int32_t dtype, int32_t batch,
+                                                int32_t num_heads, float* logits, int32_t ld,
+                                                void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  return tq_read_path(ctx, c, layer, 1, q, dtype, nullptr, ld, batch, num_heads, 1.0f, logits,
+                      stream, "tq_cache_attention_logits");
+}
+
+SAI_API sai_status sai_tqcache_weighted_value_sum(sai_ctx* ctx, sai_tqcache* c, int32_t layer,
+                                                  const float* weights, int32_t ld,
+                                                  int32_t batch, int32_t num_heads, float* out,
+                                                  void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  return tq_read_path(ctx, c, layer, 2, nullptr, SAI_DTYPE_F32, weights, ld, batch, num_heads,
+                      1.0f, out, stream, "tq_cache_weighted_value_sum");
 }

@@ -229,6 +229,9 @@ struct TqAttendArgs {
   int num_heads;
   float* out;       // [batch, 1, num_heads * D]
   float* partials;  // [batch][heads][max_splits][G * (D + 2)]
+  const float* weights;  // weighted value sum: [batch * num_heads][ld]
+  int ld;                // row stride of logits / weights
+  int normalize;         // 0: the weighted sum is not divided by the weights' sum
   int split_rows, max_splits;
   float scale_log2;
 };
@@ -238,8 +241,9 @@ hipError_t launch_tq_write(const TqArgs& a, const void* k, const void* v, int bf
                            int s_new, hipStream_t st);
 hipError_t launch_tq_read(const TqArgs& a, int b, int h, int start, int len, float* k_out,
                           float* v_out, hipStream_t st);
-hipError_t launch_tq_attend(const TqArgs& a, const TqAttendArgs& t, int group, int nsplit,
-                            int batch, hipStream_t st);
+// mode 0 attention, 1 logits only, 2 weighted value sum only
+hipError_t launch_tq_attend(const TqArgs& a, const TqAttendArgs& t, int mode, int group,
+                            int nsplit, int batch, hipStream_t st);
 hipError_t launch_copy_rows(const CopyRowsArgs& a, int chunk_bytes, hipStream_t st);
 // Standalone RoPE (rotary.hip): x/y f32 or bf16, tables f32 or bf16.
 hipError_t launch_rotary(const RotaryArgs& a, bool x_bf16, bool table_bf16, bool interleaved,

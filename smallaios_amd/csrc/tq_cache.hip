@@ -494,7 +494,7 @@ __global__ __launch_bounds__(G * D) void tq_merge_kernel(const TqArgs a, TqAtten
     }
   }
   __shared__ float sy[G][D];
-  sy[g][i] = Ls > 0.0f ? O / Ls : 0.0f;
+  sy[g][i] = t.normalize ? (Ls > 0.0f ? O / Ls : 0.0f) : O;
   __syncthreads();
   rotate_back<D, G, G * D>(a, t, b, kvh, sy);
 }
@@ -506,7 +506,12 @@ __global__ __launch_bounds__(G * D) void tq_merge_kernel(const TqArgs a, TqAtten
 // so lane l's result i is head 4u + i at position l). Values: lane = dim
 // (4x4x4 f16 MFMA: A = four heads' weights, B = the lane's dim over four
 // positions, so lane l's result i is head 4u + i at dim 64 e + l).
-template <int D, int BITS, int G, int NW>
+// MODE 0: attention (softmax of scale * logits, weighted value sum, rotated
+// back). MODE 1: the logits alone (the design's attention_logits), written to
+// t.out[(b, head)][position] with row stride t.ld, coefficients at scale 1.
+// MODE 2: the weighted value sum alone (weighted_value_sum) of the weights
+// t.weights[(b, head)][position], not normalised.
+template <int D, int BITS, int G, int NW, int MODE>
 __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAttendArgs t) {
   constexpr int NQ = (G + 3) / 4;
   constexpr int KW = D * BITS / 32;
@@ -530,10 +535,12 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   __shared__ uint32_t sqs[G][D / 32];            // query QJL sign words
   __shared__ float sres[NW][D];
   __shared__ _Float16 sp[NW][NQ * 4][64 + 4];    // a wave's P' rows
-  for (int e = threadIdx.x; e < (NQ * 4 - G) * NS; e += 64 * NW) sqc[G + e / NS][e % NS] = 0u;
-  for (int g = wave; g < G; g += NW)
-    wave_encode_query<D, BITS>(a, t, b, kvh * G + g, kvh, lane, sres[wave], sqc[g], sqf[g],
-                               sqs[g]);
+  if constexpr (MODE != 2) {
+    for (int e = threadIdx.x; e < (NQ * 4 - G) * NS; e += 64 * NW) sqc[G + e / NS][e % NS] = 0u;
+    for (int g = wave; g < G; g += NW)
+      wave_encode_query<D, BITS>(a, t, b, kvh * G + g, kvh, lane, sres[wave], sqc[g], sqf[g],
+                                 sqs[g]);
+  }
   __syncthreads();
   // the query's coefficients and sign words are uniform: scalar registers
   float qa[G], qb[G], qg[G], qk[G];
@@ -552,7 +559,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   floatx4_t o_run[NQ][DH];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    m_run[g] = -INFINITY;
+    m_run[g] = MODE == 2 ? 0.0f : -INFINITY;  // given weights: no running max
     l_run[g] = 0.0f;
     z_run[g] = 0.0f;
   }
@@ -570,7 +577,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
     const size_t rr = rbase + (live ? row : tile0);
     // this lane's K row, its parameters and sign words; V codes of its dims
     uint32_t kc[KWL];
-    {
+    if constexpr (MODE != 2) {
       const uint4* src = (const uint4*)(a.codes_k + rr * a.code_stride);
 #pragma unroll
       for (int j = 0; j < KWL / 4; ++j) {
@@ -584,7 +591,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
     const float4 kp = a.par_k[rr];
     const float4 vp = a.par_v[rr];
     uint32_t ks[D / 32];
-    if (a.qjl) {
+    if (MODE != 2 && a.qjl) {
       const uint4* src = (const uint4*)(a.signs_k + rr * (D / 32));
 #pragma unroll
       for (int j = 0; j < D / 128; ++j) {
@@ -601,7 +608,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
       }
     }
     uint32_t vc[DH][TBW];
-    {
+    if constexpr (MODE != 1) {
       const uint8_t* vt = vbase + (size_t)(tile0 / 64) * tq_vtile_bytes(D, BITS);
 #pragma unroll
       for (int e = 0; e < DH; ++e) {
@@ -614,6 +621,8 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
         }
       }
     }
+    float lg[G];
+    if constexpr (MODE != 2) {
     // logits: exact integer dot products on the int8 MFMA
     intx4_t ip[NQ];
 #pragma unroll
@@ -628,7 +637,6 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
     }
     const float sk = kp.w - (float)(KOFF * D);
     const float kz = kp.y + (float)KOFF * kp.x;
-    float lg[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float ipf = (float)ip[g >> 2][g & 3];
@@ -641,13 +649,20 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
       }
       lg[g] = live ? dot : -INFINITY;
     }
+    }  // MODE != 2
+    if constexpr (MODE == 1) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (live) t.out[((size_t)b * t.num_heads + kvh * G + g) * t.ld + row] = lg[g];
+      continue;
+    }
     // online softmax (log2 domain); the running max moves only when a lane
     // exceeds it
     float alpha[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       alpha[g] = 1.0f;
-      if (__ballot(lg[g] > m_run[g])) {
+      if (MODE == 0 && __ballot(lg[g] > m_run[g])) {
         const float m_new = fmaxf(m_run[g], wave_max(lg[g]));
         alpha[g] = fast_exp2(m_run[g] - m_new);
         m_run[g] = m_new;
@@ -664,7 +679,11 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
     for (int g = 0; g < NQ * 4; ++g) {
       _Float16 ph = (_Float16)0.0f;
       if (g < G) {
-        ph = (_Float16)(fast_exp2(lg[g] - m_run[g]) * vsn);
+        const float pw =
+            MODE == 2 ? (live ? t.weights[((size_t)b * t.num_heads + kvh * G + g) * t.ld + row]
+                              : 0.0f)
+                      : fast_exp2(lg[g] - m_run[g]);
+        ph = (_Float16)(pw * vsn);
         const float p = (float)ph * rvsn;
         l_run[g] = l_run[g] * alpha[g] + p;
         z_run[g] = z_run[g] * alpha[g] + p * vp.y;
@@ -706,6 +725,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
   }
+  if constexpr (MODE == 1) return;
   // merge the waves through LDS
   __shared__ float sm_m[NW][G], sm_l[NW][G], sm_z[NW][G];
   __shared__ float sm_o[NW][G][D];
@@ -745,7 +765,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
       O += (sm_o[w][g][i] + sm_z[w][g]) * f;
     }
     if (nsplit == 1) {
-      sy[g][i] = Ls > 0.0f ? O / Ls : 0.0f;
+      sy[g][i] = MODE == 2 ? O : (Ls > 0.0f ? O / Ls : 0.0f);
     } else {
       float* part = part0 + split * pstride + g * (D + 2);
       part[2 + i] = O;
@@ -760,19 +780,19 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   rotate_back<D, G, 64 * NW>(a, t, b, kvh, sy);
 }
 
-template <int D, int BITS>
+template <int D, int BITS, int MODE>
 hipError_t attend_db(const TqArgs& a, const TqAttendArgs& t, int group, int nsplit, int batch,
                      hipStream_t st) {
   const dim3 grid(nsplit, a.heads, batch);
   switch (group) {
-    case 1: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 1, 4>), grid, dim3(256), 0, st, a, t); break;
-    case 2: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 2, 4>), grid, dim3(256), 0, st, a, t); break;
-    case 4: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 4, 4>), grid, dim3(256), 0, st, a, t); break;
-    case 8: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 8, 4>), grid, dim3(256), 0, st, a, t); break;
+    case 1: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 1, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
+    case 2: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 2, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
+    case 4: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 4, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
+    case 8: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 8, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || nsplit <= 1) return e;
+  if (e != hipSuccess || MODE == 1 || nsplit <= 1) return e;
   const dim3 mg(a.heads, batch);
   switch (group) {
     case 1: hipLaunchKernelGGL((tq_merge_kernel<D, 1>), mg, dim3(D), 0, st, a, t); break;
@@ -824,11 +844,16 @@ hipError_t launch_tq_read(const TqArgs& a, int b, int h, int start, int len, flo
   });
 }
 
-hipError_t launch_tq_attend(const TqArgs& a, const TqAttendArgs& t, int group, int nsplit,
-                            int batch, hipStream_t st) {
+hipError_t launch_tq_attend(const TqArgs& a, const TqAttendArgs& t, int mode, int group,
+                            int nsplit, int batch, hipStream_t st) {
   return dispatch_dbits(a.head_dim, a.bits, [&](auto dd, auto bb) -> hipError_t {
     constexpr int D = decltype(dd)::value, B = decltype(bb)::value;
-    return attend_db<D, B>(a, t, group, nsplit, batch, st);
+    switch (mode) {
+      case 0: return attend_db<D, B, 0>(a, t, group, nsplit, batch, st);
+      case 1: return attend_db<D, B, 1>(a, t, group, nsplit, batch, st);
+      case 2: return attend_db<D, B, 2>(a, t, group, nsplit, batch, st);
+      default: return hipErrorInvalidValue;
+    }
   });
 }
 

@@ -203,6 +203,59 @@ def test_attend_long_ragged_splits(rt):
         c.close()
 
 
+@pytest.mark.parametrize("d,bits,qjl,group", [(128, 4, True, 4), (64, 8, False, 8),
+                                               (128, 3, True, 2)])
+def test_logits_and_weighted_sum(rt, d, bits, qjl, group):
+    """The design's attention_logits and weighted_value_sum over ragged
+    sequences (two splits for one of them). Logits: the integer-exact path
+    differs from the oracle's f32 dot by rounding only. Weighted sum: each
+    weight enters the f16 product with a relative error of at most 2^-11, so
+    |error| <= 2^-11 * sum_t |w_t| |decode(v_t)| (plus f32 rounding)."""
+    import torch
+    log(f"tq logits/wsum d={d} bits={bits} qjl={qjl} G={group}")
+    rng = np.random.default_rng(bits * 7 + group)
+    heads = 2
+    nh = heads * group
+    lens = [1500, 300]
+    batch, rows, ld = len(lens), max(lens), 1536
+    c = S.TqCache(rt, 1, heads, d, bits, qjl, batch, rows, seed=SEED)
+    try:
+        k = rng.standard_normal((batch, rows, heads * d)).astype(np.float32)
+        v = rng.standard_normal((batch, rows, heads * d)).astype(np.float32)
+        c.write(0, to_dev(k, False), to_dev(v, False), batch, rows)
+        c.advance()
+        c.set_lengths(lens)
+        q = rng.standard_normal((batch, 1, nh * d)).astype(np.float32)
+        lg = torch.full((batch * nh, ld), float("nan"), device="cuda")
+        c.attention_logits(0, to_dev(q, False), lg, ld, batch, nh)
+        w = (rng.random((batch * nh, ld)) * 2 - 1).astype(np.float32)
+        out = torch.zeros((batch, 1, nh * d), device="cuda")
+        c.weighted_value_sum(0, to_dev(w, False), ld, out, batch, nh)
+        torch.cuda.synchronize()
+        lg = lg.cpu().numpy().reshape(batch, nh, ld)
+        got = out.cpu().numpy().reshape(batch, nh, d)
+        qq = q.reshape(batch, nh, d)
+        w = w.reshape(batch, nh, ld)
+        for b in range(batch):
+            n = lens[b]
+            assert np.isnan(lg[b, :, n:]).all()
+            for h in range(heads):
+                sg = head_signs(SEED, 0, heads, h, d)
+                ek = O.tq_write_rows(rows_of(k, b, h, heads, d)[:n], bits, sg, qjl)
+                ev = O.tq_write_rows(rows_of(v, b, h, heads, d)[:n], bits, sg, qjl)
+                hs = slice(h * group, (h + 1) * group)
+                want = O.tq_attention_logits(qq[b, hs], bits, qjl, sg, ek)
+                np.testing.assert_allclose(lg[b, hs, :n], want, atol=1e-3, rtol=1e-4)
+                ww = w[b, hs, :n]
+                want = O.tq_weighted_value_sum(ww, bits, sg, ev)
+                vd = np.stack([O.tq_decode(ev[0][t], d, bits, ev[1][t], ev[2][t], sg)
+                               for t in range(n)])
+                bound = 2.0**-11 * (np.abs(ww) @ np.abs(vd)) + 1e-4 * (1 + np.abs(want))
+                assert (np.abs(got[b, hs] - want) <= bound).all(), (b, h)
+    finally:
+        c.close()
+
+
 def test_memory_bytes(rt):
     """cache_memory_footprint (kv_compression.rs:1517-1547): 128 rows of D=64,
     4-bit + QJL stay below the f32 size; the count follows the reference's

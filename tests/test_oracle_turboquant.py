@@ -16,8 +16,10 @@ decodes to within half a step of the rotated value (the quantiser's bound,
 which a wrong rounding or scale breaks); the popcount correction equals
 C_a C_b <s_a, s_b> / D computed from +-1 vectors; the sign vector is
 balanced and seed-specific; the cache seeds follow the reference's mixing
-constant. The attention estimator (sai_or_tq_attend) is checked against a
-numpy evaluation of the same formula built from the pinned pieces.
+constant. The attention estimator (sai_or_tq_attend) and the design's two
+primitives (sai_or_tq_attention_logits, sai_or_tq_weighted_value_sum) are
+checked against numpy evaluations built from the pinned pieces, and the
+attention against softmax(scale * logits) then the weighted sum.
 """
 import numpy as np
 import pytest
@@ -172,3 +174,33 @@ def test_attend_matches_numpy_of_the_pinned_pieces(bits, qjl):
         w = np.exp(0.125 * lg - (0.125 * lg).max())
         want = (w / w.sum()) @ vd
         np.testing.assert_allclose(got[h], want, atol=2e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("bits,qjl", [(4, True), (3, True), (8, False)])
+def test_logits_and_weighted_sum(bits, qjl):
+    rng = np.random.default_rng(10 + bits)
+    d, g, n = 64, 2, 29
+    sg = O.tq_signs(5, d)
+    k = rng.standard_normal((n, d)).astype(np.float32)
+    v = rng.standard_normal((n, d)).astype(np.float32)
+    q = rng.standard_normal((g, d)).astype(np.float32)
+    ek, ev = O.tq_write_rows(k, bits, sg, qjl), O.tq_write_rows(v, bits, sg, qjl)
+    lg = O.tq_attention_logits(q, bits, qjl, sg, ek)
+    eq = O.tq_write_rows(q, bits, sg, qjl)
+    kd = np.stack([O.tq_decode(ek[0][t], d, bits, ek[1][t], ek[2][t], sg) for t in range(n)])
+    vd = np.stack([O.tq_decode(ev[0][t], d, bits, ev[1][t], ev[2][t], sg) for t in range(n)])
+    for h in range(g):
+        qd = O.tq_decode(eq[0][h], d, bits, eq[1][h], eq[2][h], sg).astype(np.float64)
+        want = kd.astype(np.float64) @ qd
+        if qjl:
+            want += [O.qjl_correction(eq[3][h], eq[4][h], ek[3][t], ek[4][t], d) for t in range(n)]
+        np.testing.assert_allclose(lg[h], want, atol=1e-4, rtol=1e-5)
+    w = rng.random((g, n)).astype(np.float32)
+    ws = O.tq_weighted_value_sum(w, bits, sg, ev)
+    np.testing.assert_allclose(ws, w.astype(np.float64) @ vd, atol=1e-4, rtol=1e-5)
+    # attention = weighted sum of softmax(scale * logits)
+    sc = 0.125
+    p = np.exp(sc * (lg - lg.max(1, keepdims=True)))
+    p /= p.sum(1, keepdims=True)
+    np.testing.assert_allclose(O.tq_attend(q, bits, qjl, sg, ek, ev, sc),
+                               O.tq_weighted_value_sum(p, bits, sg, ev), atol=2e-5, rtol=1e-4)
