@@ -105,6 +105,51 @@ def test_write_read_bit_exact(rt, d, bits, qjl, bf16):
         c.close()
 
 
+@pytest.mark.parametrize("d,bits", [(128, 3), (64, 4), (128, 8)])
+def test_writes_across_tile_boundaries(rt, d, bits):
+    """Passes of 70, 1, 130 and 1 rows from unaligned starts: the V tiles
+    are read-modify-written by their owning wave at both ends of a pass, and
+    the rows already there must survive. Every row checked bit for bit, and
+    attention over the result."""
+    import torch
+    log(f"tq tile boundaries d={d} bits={bits}")
+    rng = np.random.default_rng(d + bits)
+    batch, heads = 2, 2
+    c = S.TqCache(rt, 1, heads, d, bits, True, batch, 256, seed=SEED)
+    try:
+        ks, vs = [], []
+        for s in (70, 1, 130, 1):
+            k = rng.standard_normal((batch, s, heads * d)).astype(np.float32)
+            v = rng.standard_normal((batch, s, heads * d)).astype(np.float32)
+            c.write(0, to_dev(k, False), to_dev(v, False), batch, s)
+            c.advance()
+            ks.append(k)
+            vs.append(v)
+        torch.cuda.synchronize()
+        k = np.concatenate(ks, axis=1)
+        v = np.concatenate(vs, axis=1)
+        assert list(c.lengths()[0][:batch]) == [202] * batch
+        for b in range(batch):
+            for h in range(heads):
+                check_rows(c, 0, b, h, 0, rows_of(k, b, h, heads, d), rows_of(v, b, h, heads, d),
+                           heads, d, bits, True, SEED)
+        nh = heads * 4
+        q = rng.standard_normal((batch, 1, nh * d)).astype(np.float32)
+        out = torch.zeros((batch, 1, nh * d), device="cuda")
+        c.attend(0, to_dev(q, False), out, batch, nh)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(batch, nh, d)
+        for b in range(batch):
+            for h in range(heads):
+                sg = head_signs(SEED, 0, heads, h, d)
+                want = oracle_attend(rows_of(k, b, h, heads, d), rows_of(v, b, h, heads, d),
+                                     q.reshape(batch, nh, d)[b, 4 * h:4 * h + 4], bits, True, sg,
+                                     S.default_scale(d))
+                np.testing.assert_allclose(got[b, 4 * h:4 * h + 4], want, atol=2e-3, rtol=1e-2)
+    finally:
+        c.close()
+
+
 def test_constant_and_edge_rows(rt):
     """Constant rows (range 0: scale 1.0), zeros, large magnitudes."""
     import torch
