@@ -465,20 +465,25 @@ def main():
         out = torch.empty((b, 1, hq * d), device="cuda", dtype=torch.float32)
 
         def pre():
-            cache.write(0, k_new, v_new, b, 1, stream=stream)
+            if args.unfused:
+                cache.write(0, k_new, v_new, b, 1, stream=stream)
 
         def kern():
-            cache.attend(0, q, out, b, hq, stream=stream)
+            if args.unfused:
+                cache.attend(0, q, out, b, hq, stream=stream)
+            else:
+                cache.write_attend(0, q, k_new, v_new, out, b, hq, stream=stream)
 
         def step():
-            pre()  # rewrites the pending row: every step sees ctx rows
+            pre()  # each step rewrites the pending row: every step sees ctx rows
             kern()
 
         for _ in range(args.warmup):
             step()
         ms_step = time_steps(torch, step, args.steps)
         kus = event_times(torch, stream, pre, kern, args.steps)   # query + attend + merge
-        wus = event_times(torch, stream, lambda: None, pre, args.steps)
+        wus = event_times(torch, stream, lambda: None,
+                          lambda: cache.write(0, k_new, v_new, b, 1, stream=stream), args.steps)
         per = tq_bytes_per_row_head(d, bits, qjl)
         alg = b * ctx * hkv * per + b * hq * d * (2 + 4)
         k_us = float(np.median(kus))
@@ -492,12 +497,14 @@ def main():
             "data": "synthetic (seeded N(0,1) Q/K/V; no checkpoint)",
             "config": {"workload": "tq4", "batch": b, "q_heads": hq, "kv_heads": hkv,
                        "head_dim": d, "context": ctx, "bits": bits, "qjl": qjl,
-                       "step": "tq_cache_write (1 token, pending) + tq_cache_attend "
-                               "(query encode + attend + merge)"},
+                       "step": ("tq_cache_write (1 token, pending) + tq_cache_attend"
+                                if args.unfused else
+                                "tq_cache_write_attend: the token's store fused into the "
+                                "attention kernel (+ split merge)")},
             "algorithmic_bytes_per_step": alg,
             "bytes_per_row_head": per,
             "attend_us": {"median": round(k_us, 3), "mean": round(float(kus.mean()), 3)},
-            "write_us": {"median": round(float(np.median(wus)), 3)},
+            "separate_write_us": {"median": round(float(np.median(wus)), 3)},
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                          "traffic": None},

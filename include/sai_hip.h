@@ -344,6 +344,16 @@ sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, c
                               int32_t dtype, int32_t batch, int32_t num_heads, int32_t has_scale,
                               float scale, float* out, void* stream);
 
+/* The decode step in one launch (the design's steps 2-6): sai_tqcache_write
+ * of one row per sequence (k_new, v_new [batch, 1, num_kv_heads*head_dim],
+ * F32 or BF16; pending as after sai_tqcache_write) and sai_tqcache_attend
+ * over the rows including it. The workgroup that attends a sequence's last
+ * positions stores its new row first. Errors: those of the two calls. */
+sai_status sai_tqcache_write_attend(sai_ctx* ctx, sai_tqcache* cache, int32_t layer,
+                                    const void* q, int32_t q_dtype, const void* k_new,
+                                    const void* v_new, int32_t kv_dtype, int32_t batch,
+                                    int32_t num_heads, int32_t has_scale, float scale, float* out,
+                                    void* stream);
 /* The design's two cache primitives of the GQA read path
  * (docs/kv-compression-design.md section 9, steps 4 and 6), over the
  * committed + pending rows of `layer`; the reference has not implemented

@@ -88,6 +88,7 @@ EXPORTS = [
     "sai_tqcache_write", "sai_tqcache_advance", "sai_tqcache_reset", "sai_tqcache_set_lengths",
     "sai_tqcache_lengths", "sai_tqcache_read", "sai_tqcache_read_raw", "sai_tqcache_attend",
     "sai_tqcache_memory_bytes", "sai_tqcache_attention_logits", "sai_tqcache_weighted_value_sum",
+    "sai_tqcache_write_attend",
 ]
 ROPE_BHSD = 0
 ROPE_BSHD = 1
@@ -142,6 +143,7 @@ def _declare(L: C.CDLL) -> None:
         "sai_tqcache_memory_bytes": (i32, [p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
         "sai_tqcache_attention_logits": (i32, [p, p, i32, p, i32, i32, i32, p, i32, p]),
         "sai_tqcache_weighted_value_sum": (i32, [p, p, i32, p, i32, i32, i32, p, p]),
+        "sai_tqcache_write_attend": (i32, [p, p, i32, p, i32, p, p, i32, i32, i32, i32, f, p, p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -506,6 +508,16 @@ class TqCache:
             self.rt.handle, self.handle, layer, b, kv_head, start, n, ptr("k_codes"),
             ptr("v_codes"), ptr("k_params"), ptr("v_params"), sk, sv), "tqcache_read_raw")
         return r
+
+    def write_attend(self, layer, q, k_new, v_new, out, batch, num_heads, scale=None,
+                     stream=None, q_dtype=None, kv_dtype=None):
+        """One decode step: store the new row (k_new/v_new [B, 1, Hkv*D]) and attend."""
+        qd = q_dtype if q_dtype is not None else _dtype_code(q)
+        kd = kv_dtype if kv_dtype is not None else _dtype_code(k_new)
+        self.rt.check(self._L.sai_tqcache_write_attend(
+            self.rt.handle, self.handle, layer, _dev_ptr(q), qd, _dev_ptr(k_new), _dev_ptr(v_new),
+            kd, batch, num_heads, int(scale is not None), 0.0 if scale is None else float(scale),
+            _dev_ptr(out), _stream(stream)), "tqcache_write_attend")
 
     def attention_logits(self, layer, q, logits, ld, batch, num_heads, stream=None, dtype=None):
         """logits: device f32 [batch * num_heads, ld] (unscaled inner-product estimates)."""

@@ -1431,7 +1431,8 @@ namespace {
 sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, const void* q,
                         int32_t dtype, const float* weights, int32_t ld, int32_t batch,
                         int32_t num_heads, float scale_log2, float* out, void* stream,
-                        const char* op) {
+                        const char* op, const void* k_new = nullptr, const void* v_new = nullptr,
+                        int32_t kv_dtype = SAI_DTYPE_F32) {
   if (mode != 2 && !q) return fail(ctx, SAI_ERR_NULL, "%s: missing query", op);
   if (mode == 2 && !weights) return fail(ctx, SAI_ERR_NULL, "%s: missing weights", op);
   if (!out) return fail(ctx, SAI_ERR_NULL, "%s: missing output", op);
@@ -1479,6 +1480,9 @@ sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, c
   t.weights = weights;
   t.ld = ld;
   t.normalize = mode == 0 ? 1 : 0;
+  t.k_new = k_new;
+  t.v_new = v_new;
+  t.kv_bf16 = kv_dtype == SAI_DTYPE_BF16 ? 1 : 0;
   t.split_rows = split_rows;
   t.max_splits = max_splits;
   t.scale_log2 = scale_log2;
@@ -1497,6 +1501,42 @@ SAI_API sai_status sai_tqcache_attend(sai_ctx* ctx, sai_tqcache* c, int32_t laye
   const float sc = has_scale ? scale : sai_default_scale(c->desc.head_dim);
   return tq_read_path(ctx, c, layer, 0, q, dtype, nullptr, 0, batch, num_heads,
                       sc * 1.4426950408889634f, out, stream, "tq_cache_attend");
+}
+
+SAI_API sai_status sai_tqcache_write_attend(sai_ctx* ctx, sai_tqcache* c, int32_t layer,
+                                            const void* q, int32_t q_dtype, const void* k_new,
+                                            const void* v_new, int32_t kv_dtype, int32_t batch,
+                                            int32_t num_heads, int32_t has_scale, float scale,
+                                            float* out, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "tq_cache_write_attend";
+  if (!k_new || !v_new) return fail(ctx, SAI_ERR_NULL, "%s: missing key/value", op);
+  if (layer < 0 || layer >= c->desc.num_layers)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: layer_idx %d", op, layer);
+  if (kv_dtype != SAI_DTYPE_F32 && kv_dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (want f32 or bf16)", op, kv_dtype);
+  if (batch <= 0 || batch > c->desc.max_batch)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: batch %d", op, batch);
+  if (c->pending != 0 && (c->pending != 1 || batch != c->batch))
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH,
+                "%s: 1 row x %d sequences, but this pass appends %d x %d", op, batch, c->pending,
+                c->batch);
+  for (int b = 0; b < batch; ++b)
+    if ((int64_t)c->h_lens[b] + 1 > c->desc.max_rows)
+      return fail(ctx, SAI_ERR_OVERFLOW, "%s: position_overflow (sequence %d: %d + 1 > %d)", op,
+                  b, c->h_lens[b], c->desc.max_rows);
+  const int32_t pending = c->pending, pbatch = c->batch;
+  c->pending = 1;
+  c->batch = batch;
+  const float sc = has_scale ? scale : sai_default_scale(c->desc.head_dim);
+  const sai_status st = tq_read_path(ctx, c, layer, 0, q, q_dtype, nullptr, 0, batch, num_heads,
+                                     sc * 1.4426950408889634f, out, stream, op, k_new, v_new,
+                                     kv_dtype);
+  if (st != SAI_OK) {
+    c->pending = pending;
+    c->batch = pbatch;
+  }
+  return st;
 }
 
 SAI_API sai_status sai_tqcache_attention_logits(sai_ctx* ctx, sai_tqcache* c, int32_t layer,

@@ -232,6 +232,9 @@ struct TqAttendArgs {
   const float* weights;  // weighted value sum: [batch * num_heads][ld]
   int ld;                // row stride of logits / weights
   int normalize;         // 0: the weighted sum is not divided by the weights' sum
+  const void* k_new;     // fused step: the pass's new row per (sequence, kv head),
+  const void* v_new;     //   [batch, 1, heads * D], stored before it is attended
+  int kv_bf16;
   int split_rows, max_splits;
   float scale_log2;
 };

@@ -166,6 +166,71 @@ __device__ __forceinline__ float wave_qjl(const uint32_t (&code)[D / 64], float 
   return c;
 }
 
+// Encodes the row x (lane l: dims l + 64 e) as position r of (kv head h,
+// sequence b), K (kind 0) or V (kind 1), and stores it: K codes row-major; V
+// codes into the position's bits of its tile, in the LDS copy `stile` of the
+// tile's words when given, else by read-modify-write of the words in memory
+// (the caller guarantees that no other wave writes that tile meanwhile);
+// then the parameters (scale, zero point, QJL mean, sum of the codes) and the
+// QJL sign words. Orders its LDS use at wave level only.
+template <int D, int BITS>
+__device__ __forceinline__ void wave_store_row(const TqArgs& a, const float (&x)[D / 64],
+                                               const float (&sgn)[D / 64], int lane, int h, int b,
+                                               int r, int kind, uint32_t (*stile)[2 * BITS + 1],
+                                               float* sres, uint32_t* scode) {
+#pragma clang fp contract(off)
+  constexpr int E = D / 64;
+  constexpr int W = D * BITS / 32;  // K code words per row
+  constexpr int TBW = 2 * BITS;     // V words per dim per tile
+  constexpr uint32_t LEVELS = (1u << BITS) - 1u;
+  float y[E], scale, zero;
+  uint32_t code[E];
+  wave_encode<D, BITS>(x, sgn, lane, a.norm, y, code, scale, zero);
+  float csum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) csum += (float)code[e];
+  csum = wave_sum(csum);  // integers below 2^24: exact
+  const size_t row = ((size_t)h * a.batch_cap + b) * a.rows_cap + r;
+  if (kind == 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) scode[lane + 64 * e] = code[e];
+    wave_lds_sync();
+    if (lane < W) {
+      uint32_t wd = 0u;
+      const int i0 = (32 * lane) / BITS, i1 = (32 * lane + 31) / BITS;
+      for (int i = i0; i <= i1; ++i) {
+        const int bp = BITS * i - 32 * lane;
+        wd |= bp >= 0 ? (scode[i] << bp) : (scode[i] >> -bp);
+      }
+      ((uint32_t*)(a.codes_k + row * a.code_stride))[lane] = wd;
+    }
+    wave_lds_sync();  // scode is reused by the wave's next row
+  } else {
+    const int p = (r % 64) * BITS, w = p >> 5, sh = p & 31;
+    uint32_t* vt = (uint32_t*)(a.codes_v + (((size_t)h * a.batch_cap + b) * a.tiles_cap + r / 64) *
+                                               tq_vtile_bytes(D, BITS));
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int d = lane + 64 * e;
+      uint32_t* tw = stile ? stile[d] : vt + d * TBW;
+      tw[w] = (tw[w] & ~(LEVELS << sh)) | (code[e] << sh);
+      if (sh + BITS > 32) tw[w + 1] = (tw[w + 1] & ~(LEVELS >> (32 - sh))) | (code[e] >> (32 - sh));
+    }
+  }
+  float c = 0.0f;
+  if (a.qjl) {
+    uint64_t sb[E];
+    c = wave_qjl<D>(code, scale, zero, x, sgn, lane, a.norm, sres, sb);
+    if (lane < D / 32) {
+      uint64_t m = sb[0];
+      if constexpr (E == 2) m = (lane >> 1) ? sb[1] : sb[0];
+      ((kind ? a.signs_v : a.signs_k) + row * (D / 32))[lane] =
+          (uint32_t)((lane & 1) ? (m >> 32) : m);
+    }
+  }
+  if (lane == 0) (kind ? a.par_v : a.par_k)[row] = make_float4(scale, zero, c, csum);
+}
+
 // ---- write: one wave per (sequence, kv head, K|V, 64-position tile) --------
 // The wave encodes the tile's rows of this pass in order. K rows go out
 // row-major; V codes are merged into the tile's words (read, modified in LDS,
@@ -175,9 +240,7 @@ __global__ __launch_bounds__(64) void tq_write_kernel(const TqArgs a, const void
                                                       int bf16, int s_new) {
 #pragma clang fp contract(off)
   constexpr int E = D / 64;
-  constexpr int W = D * BITS / 32;  // K code words per row
-  constexpr int TBW = 2 * BITS;     // V words per dim per tile
-  constexpr uint32_t LEVELS = (1u << BITS) - 1u;
+  constexpr int TBW = 2 * BITS;  // V words per dim per tile
   const int lane = threadIdx.x;
   const int kind = blockIdx.y & 1, h = blockIdx.y >> 1, b = blockIdx.z;
   const int len = a.seq_lens[b];
@@ -192,7 +255,6 @@ __global__ __launch_bounds__(64) void tq_write_kernel(const TqArgs a, const void
   float sgn[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) sgn[e] = (float)a.signs[(size_t)h * D + lane + 64 * e];
-  const size_t rbase = ((size_t)h * a.batch_cap + b) * a.rows_cap;
   uint32_t* vt = (uint32_t*)(a.codes_v + (((size_t)h * a.batch_cap + b) * a.tiles_cap + tile) *
                                              tq_vtile_bytes(D, BITS));
   const int w_lo = ((r_lo - tile * 64) * BITS) >> 5;
@@ -201,58 +263,17 @@ __global__ __launch_bounds__(64) void tq_write_kernel(const TqArgs a, const void
 #pragma unroll
     for (int e = 0; e < E; ++e)
       for (int w = w_lo; w <= w_hi; ++w) stile[lane + 64 * e][w] = vt[(lane + 64 * e) * TBW + w];
+    wave_lds_sync();
   }
-  float4* par = (kind ? a.par_v : a.par_k) + rbase;
-  uint32_t* sw = (kind ? a.signs_v : a.signs_k) + rbase * (D / 32);
   for (int r = r_lo; r < r_hi; ++r) {
     const size_t in_off = (((size_t)b * s_new + (r - len)) * a.heads + h) * D;
-    float x[E], y[E], scale, zero;
-    uint32_t code[E];
+    float x[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) x[e] = load_row_elem(src, in_off + lane + 64 * e, is_bf16);
-    wave_encode<D, BITS>(x, sgn, lane, a.norm, y, code, scale, zero);
-    float csum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) csum += (float)code[e];
-    csum = wave_sum(csum);  // integers below 2^24: exact
-    if (kind == 0) {
-#pragma unroll
-      for (int e = 0; e < E; ++e) scode[lane + 64 * e] = code[e];
-      __syncthreads();
-      if (lane < W) {
-        uint32_t wd = 0u;
-        const int i0 = (32 * lane) / BITS, i1 = (32 * lane + 31) / BITS;
-        for (int i = i0; i <= i1; ++i) {
-          const int bp = BITS * i - 32 * lane;
-          wd |= bp >= 0 ? (scode[i] << bp) : (scode[i] >> -bp);
-        }
-        ((uint32_t*)(a.codes_k + (rbase + r) * a.code_stride))[lane] = wd;
-      }
-      __syncthreads();
-    } else {
-      const int p = (r - tile * 64) * BITS, w = p >> 5, sh = p & 31;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        uint32_t* tw = stile[lane + 64 * e];
-        tw[w] = (tw[w] & ~(LEVELS << sh)) | (code[e] << sh);
-        if (sh + BITS > 32)
-          tw[w + 1] = (tw[w + 1] & ~(LEVELS >> (32 - sh))) | (code[e] >> (32 - sh));
-      }
-    }
-    float c = 0.0f;
-    if (a.qjl) {
-      uint64_t sb[E];
-      c = wave_qjl<D>(code, scale, zero, x, sgn, lane, a.norm, sres, sb);
-      if (lane < D / 32) {
-        const uint64_t m = sb[0];
-        uint64_t m1 = m;
-        if constexpr (E == 2) m1 = (lane >> 1) ? sb[1] : sb[0];
-        sw[(size_t)r * (D / 32) + lane] = (uint32_t)((lane & 1) ? (m1 >> 32) : m1);
-      }
-    }
-    if (lane == 0) par[r] = make_float4(scale, zero, c, csum);
+    wave_store_row<D, BITS>(a, x, sgn, lane, h, b, r, kind, stile, sres, scode);
   }
   if (kind) {
+    wave_lds_sync();
 #pragma unroll
     for (int e = 0; e < E; ++e)
       for (int w = w_lo; w <= w_hi; ++w) vt[(lane + 64 * e) * TBW + w] = stile[lane + 64 * e][w];
@@ -535,6 +556,23 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   __shared__ uint32_t sqs[G][D / 32];            // query QJL sign words
   __shared__ float sres[NW][D];
   __shared__ _Float16 sp[NW][NQ * 4][64 + 4];    // a wave's P' rows
+  if constexpr (MODE == 0) {
+    // fused step: the last split's workgroup stores the pass's one new row
+    // of this kv head (K by wave 0, V by wave 1) before any wave reads it
+    if (t.k_new != nullptr && r1 == L && wave < 2) {
+      __shared__ uint32_t scode[D];
+      float x[D / 64], sgn[D / 64];
+      const void* src = wave ? t.v_new : t.k_new;
+      const size_t in_off = ((size_t)b * a.heads + kvh) * D;
+#pragma unroll
+      for (int e = 0; e < D / 64; ++e) {
+        sgn[e] = (float)a.signs[(size_t)kvh * D + lane + 64 * e];
+        x[e] = load_row_elem(src, in_off + lane + 64 * e, t.kv_bf16 != 0);
+      }
+      wave_store_row<D, BITS>(a, x, sgn, lane, kvh, b, L - 1, wave, nullptr, sres[wave], scode);
+      __threadfence_block();
+    }
+  }
   if constexpr (MODE != 2) {
     for (int e = threadIdx.x; e < (NQ * 4 - G) * NS; e += 64 * NW) sqc[G + e / NS][e % NS] = 0u;
     for (int g = wave; g < G; g += NW)

@@ -301,6 +301,59 @@ def test_logits_and_weighted_sum(rt, d, bits, qjl, group):
         c.close()
 
 
+@pytest.mark.parametrize("d,bits,qjl,group,bf16", [(128, 4, True, 4, True), (64, 3, True, 8, False),
+                                                    (128, 8, False, 2, False)])
+def test_write_attend_fused_step(rt, d, bits, qjl, group, bf16):
+    """sai_tqcache_write_attend against sai_tqcache_write + sai_tqcache_attend
+    on a twin cache: the same outputs bit for bit and the same stored rows,
+    over ragged lengths (one sequence with three splits, the new row in the
+    last), two layers in one pass, two passes."""
+    import torch
+    log(f"tq fused step d={d} bits={bits} qjl={qjl} G={group} bf16={bf16}")
+    rng = np.random.default_rng(group * 3 + bits)
+    heads, lens = 2, [2100, 77]
+    batch, nh, cap = len(lens), heads * group, 2200
+    twins = [S.TqCache(rt, 2, heads, d, bits, qjl, batch, cap, seed=SEED) for _ in range(2)]
+    try:
+        k0 = rng.standard_normal((batch, max(lens), heads * d)).astype(np.float32)
+        v0 = rng.standard_normal((batch, max(lens), heads * d)).astype(np.float32)
+        for c in twins:
+            for layer in range(2):
+                c.write(layer, to_dev(k0, False), to_dev(v0, False), batch, max(lens))
+            c.advance()
+            c.set_lengths(lens)
+        for step in range(2):
+            outs = [[], []]
+            for layer in range(2):
+                q = to_dev(rng.standard_normal((batch, 1, nh * d)).astype(np.float32), bf16)
+                kn = to_dev(rng.standard_normal((batch, 1, heads * d)).astype(np.float32), bf16)
+                vn = to_dev(rng.standard_normal((batch, 1, heads * d)).astype(np.float32), bf16)
+                for i, c in enumerate(twins):
+                    out = torch.zeros((batch, 1, nh * d), device="cuda")
+                    if i == 0:
+                        c.write(layer, kn, vn, batch, 1)
+                        c.attend(layer, q, out, batch, nh)
+                    else:
+                        c.write_attend(layer, q, kn, vn, out, batch, nh)
+                    outs[i].append(out)
+            for c in twins:
+                c.advance()
+            torch.cuda.synchronize()
+            for a, b_ in zip(*outs):
+                assert torch.equal(a, b_), step
+        assert list(twins[1].lengths()[0][:batch]) == [n + 2 for n in lens]
+        for layer in range(2):
+            for b in range(batch):
+                for h in range(heads):
+                    n = lens[b] + 2
+                    r0, r1 = twins[0].read_raw(layer, b, h, n - 3, 3), twins[1].read_raw(layer, b, h, n - 3, 3)
+                    for key in r0:
+                        assert np.array_equal(r0[key], r1[key]), (layer, b, h, key)
+    finally:
+        for c in twins:
+            c.close()
+
+
 def test_memory_bytes(rt):
     """cache_memory_footprint (kv_compression.rs:1517-1547): 128 rows of D=64,
     4-bit + QJL stay below the f32 size; the count follows the reference's
