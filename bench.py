@@ -323,6 +323,7 @@ def main():
     rt = S.Runtime(0)
     if args.split:
         rt.set_decode_split(args.split)
+        rt.set_tq_split(args.split)
     if args.waves:
         rt.set_decode_waves(args.waves)
     if args.merge != "auto":

@@ -377,6 +377,9 @@ sai_status sai_tqcache_weighted_value_sum(sai_ctx* ctx, sai_tqcache* cache, int3
 /* Tokens per split-K work item of the decode kernel (0 = automatic, else a
  * multiple of 64). Returns the previous value. */
 int32_t sai_set_decode_split(sai_ctx* ctx, int32_t tokens);
+/* TurboQuant attention split in positions (a multiple of 256, 0 = automatic);
+ * returns the previous value. Tuning only. */
+int32_t sai_set_tq_split(sai_ctx* ctx, int32_t rows);
 /* Waves per decode workgroup: 4 or 8, or 0 = automatic (4 for an int8
  * cache, 8 for int4). Returns the previous value. */
 int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves);

@@ -88,7 +88,7 @@ EXPORTS = [
     "sai_tqcache_write", "sai_tqcache_advance", "sai_tqcache_reset", "sai_tqcache_set_lengths",
     "sai_tqcache_lengths", "sai_tqcache_read", "sai_tqcache_read_raw", "sai_tqcache_attend",
     "sai_tqcache_memory_bytes", "sai_tqcache_attention_logits", "sai_tqcache_weighted_value_sum",
-    "sai_tqcache_write_attend",
+    "sai_tqcache_write_attend", "sai_set_tq_split",
 ]
 ROPE_BHSD = 0
 ROPE_BSHD = 1
@@ -121,6 +121,7 @@ def _declare(L: C.CDLL) -> None:
                                   f, i32, p, p]),
         "sai_kvcache_set_layer_window": (i32, [p, p, i32, i32]),
         "sai_set_decode_split": (i32, [p, i32]),
+        "sai_set_tq_split": (i32, [p, i32]),
         "sai_set_decode_waves": (i32, [p, i32]),
         "sai_set_decode_merge": (i32, [p, i32]),
         "sai_last_decode_shape": (i32, [p, C.POINTER(i32), C.POINTER(i32)]),
@@ -226,6 +227,9 @@ class Runtime:
 
     def set_decode_split(self, tokens: int) -> int:
         return int(self._L.sai_set_decode_split(self.handle, tokens))
+
+    def set_tq_split(self, rows: int) -> int:
+        return int(self._L.sai_set_tq_split(self.handle, int(rows)))
 
     def set_decode_waves(self, waves: int) -> int:
         return int(self._L.sai_set_decode_waves(self.handle, waves))

@@ -31,6 +31,7 @@ struct sai_ctx {
   int32_t* counters = nullptr;
   size_t counter_n = 0;
   int32_t decode_split = 0;  // 0 = automatic
+  int32_t tq_split = 0;      // TurboQuant attention split, positions (0 = automatic)
   int32_t decode_waves = 0;  // 0: automatic
   int32_t decode_merge = 0;  // 0: combine kernel, 1: in-kernel merge
   int32_t last_wg = 0;
@@ -260,6 +261,13 @@ SAI_API int32_t sai_set_decode_split(sai_ctx* ctx, int32_t tokens) {
   if (!ctx) return 0;
   int32_t prev = ctx->decode_split;
   if (tokens >= 0 && tokens % 64 == 0 && tokens <= kMaxDecodeSplit) ctx->decode_split = tokens;
+  return prev;
+}
+
+SAI_API int32_t sai_set_tq_split(sai_ctx* ctx, int32_t rows) {
+  if (!ctx) return 0;
+  int32_t prev = ctx->tq_split;
+  if (rows == 0 || (rows >= 256 && rows % 256 == 0 && rows <= 65536)) ctx->tq_split = rows;
   return prev;
 }
 
@@ -1457,8 +1465,16 @@ sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, c
   if (mode != 0 && ld < max_len)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: row stride %d below the %d positions", op, ld,
                 max_len);
-  // splits of 1024 rows (16 tiles of 64 per 4-wave workgroup)
-  const int32_t split_rows = 1024;
+  // automatic split: about 768 workgroups (three 4-wave workgroups per CU,
+  // measured best at 16 x 8192 x 8 kv heads against one, two or four per
+  // CU), in multiples of 256 positions
+  int32_t split_rows = ctx->tq_split;
+  if (split_rows <= 0) {
+    const int64_t units = (int64_t)batch * H;
+    const int64_t want = std::max<int64_t>(1, std::min<int64_t>((768 + units - 1) / units,
+                                                                (max_len + 255) / 256));
+    split_rows = (int32_t)(((max_len + want - 1) / want + 255) / 256 * 256);
+  }
   const int32_t max_splits = (max_len + split_rows - 1) / split_rows;
   const size_t part_floats = (size_t)batch * H * max_splits * G * (D + 2);
   DeviceGuard dg(ctx->device);
