@@ -204,7 +204,7 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, 
 
 template <int D, int G, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParams p) {
-  static_assert(D == 64 || D == 128, "head_dim");
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static_assert(G >= 1 && G <= 8, "group");
   constexpr int KS = D / 64;
   constexpr int JB = D / 16;
@@ -255,9 +255,12 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   __syncthreads();
 
   // cos / sin of position L-1: issued ahead of the first tile, so the query's
-  // RoPE only waits for them and not for the tile
-  float cq[KS][16], sq[KS][16];
-  if (p.do_rotary) {
+  // RoPE only waits for them and not for the tile (head_dim 256 loads them per
+  // chunk in the RoPE loop and its first tile after the query: the registers
+  // of both would not fit)
+  constexpr bool BIG = D > 128;
+  float cq[BIG ? 1 : KS][16], sq[BIG ? 1 : KS][16];
+  if (!BIG && p.do_rotary) {
     const float* cr = p.cos_cache + (size_t)(L - 1) * HALF;
     const float* sr = p.sin_cache + (size_t)(L - 1) * HALF;
 #pragma unroll
@@ -293,7 +296,8 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   if (appender && my_tiles == 1) append();
   const int tile_off = 0;  // splits start on a tile (64-token) boundary
   TileRegs<D> TA;
-  if (tile < n_tiles) load_tile<D>(TA, p.pool, sm_pg + tile_off, tile, p.num_pages, kvh, r, g, n_pages_split);
+  if (!BIG && tile < n_tiles)
+    load_tile<D>(TA, p.pool, sm_pg + tile_off, tile, p.num_pages, kvh, r, g, n_pages_split);
   // The wave's second tile is touched (one dword per 128-byte line) so that
   // it streams into L2 while the query is prepared, instead of the memory
   // pipe idling until the loop issues its load. Its own lines only: the new
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   uint32_t touch[kTouch];
 #pragma unroll
   for (int j = 0; j < kTouch; ++j) touch[j] = 0;
-  if (my_tiles > 1 && !(appender && my_tiles == 2)) {  // uniform over the wave
+  if (!BIG && my_tiles > 1 && !(appender && my_tiles == 2)) {  // uniform over the wave
     const int t1 = tile + NW;
 #pragma unroll
     for (int j = 0; j < kTouch; ++j) {
@@ -333,6 +337,19 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
       for (int i = 0; i < 16; ++i) x[i] = xq[ks][i];
       if (p.do_rotary) {
         float y[16];
+        float cc[16], ss[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if constexpr (BIG) {
+            const int base = p.interleaved ? (c0 >> 1) : (c0 < HALF ? c0 : c0 - HALF);
+            const int idx = base + (p.interleaved ? (i >> 1) : i);
+            cc[i] = p.cos_cache[(size_t)(L - 1) * HALF + idx];
+            ss[i] = p.sin_cache[(size_t)(L - 1) * HALF + idx];
+          } else {
+            cc[i] = cq[ks][i];
+            ss[i] = sq[ks][i];
+          }
+        }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           // split-half partner d +- D/2: the same element of lane g ^ 2 (32
@@ -343,7 +360,7 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
           const float half_partner = __uint_as_float(c0 < HALF ? sw[1] : sw[0]);
           const float partner = p.interleaved ? x[i ^ 1] : half_partner;
           const bool first = p.interleaved ? (i & 1) == 0 : c0 < HALF;
-          y[i] = rope_elem(cq[ks][i], sq[ks][i], x[i], partner, first);
+          y[i] = rope_elem(cc[i], ss[i], x[i], partner, first);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) x[i] = y[i];
@@ -399,18 +416,39 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
 #pragma unroll
   for (int j = 0; j < kTouch; ++j) __asm__ volatile("" ::"v"(touch[j]));
   int k = 0;
-  for (; k + 2 < my_tiles; k += 2) {
-    ld(TB, k + 1);
-    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
-    ld(TA, k + 2);
-    compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
-  }
-  if (k + 1 < my_tiles) {  // two left
-    ld(TB, k + 1);
-    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
-    compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
-  } else if (k < my_tiles) {  // one left
-    compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+  if constexpr (D <= 128) {
+    for (; k + 2 < my_tiles; k += 2) {
+      ld(TB, k + 1);
+      compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+      ld(TA, k + 2);
+      compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+    }
+    if (k + 1 < my_tiles) {  // two left
+      ld(TB, k + 1);
+      compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+      compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+    } else if (k < my_tiles) {  // one left
+      compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+    }
+  } else {
+    // head_dim 256: a tile is ~128 registers, so one buffer; each iteration
+    // touches the wave's next tile (its own tile again on the last one, so
+    // the code stays straight-line) into L2 while the current one computes
+    for (; k < my_tiles; ++k) {
+      ld(TA, k);
+      const int tn = wave + min(k + 1, my_tiles - 1) * NW;
+      uint32_t tch[kTouch];
+#pragma unroll
+      for (int j = 0; j < kTouch; ++j) {
+        const int line = min(lane + 64 * j, 4 * kLines - 1);
+        const int pg = sm_pg[min(tn * 4 + line / kLines, n_pages_split - 1)];
+        tch[j] = *(const uint32_t*)(p.pool + block_offset(pg, kvh, p.num_pages, block_bytes_int8(D)) +
+                                    (size_t)(line % kLines) * 128);
+      }
+      compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+#pragma unroll
+      for (int j = 0; j < kTouch; ++j) __asm__ volatile("" ::"v"(tch[j]));
+    }
   }
 
   // ---- merge the NW waves of the workgroup --------------------------------------
@@ -615,7 +653,10 @@ hipError_t launch_d(const DecodeParams& p, int group, int work_items, bool combi
     case 1: return launch_dg<D, 1>(p, work_items, combine, st);
     case 2: return launch_dg<D, 2>(p, work_items, combine, st);
     case 4: return launch_dg<D, 4>(p, work_items, combine, st);
-    case 8: return launch_dg<D, 8>(p, work_items, combine, st);
+    case 8:
+      // the combine block is one thread per (head, dim): 8 x 256 is past 1024
+      if constexpr (D <= 128) return launch_dg<D, 8>(p, work_items, combine, st);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
@@ -635,6 +676,7 @@ hipError_t launch_decode_combine(const DecodeParams& p, int head_dim, int group,
   };
   if (head_dim == 64) return by_group(std::integral_constant<int, 64>{});
   if (head_dim == 128) return by_group(std::integral_constant<int, 128>{});
+  if (head_dim == 256 && group <= 4) return by_group(std::integral_constant<int, 256>{});
   return hipErrorInvalidValue;
 }
 
@@ -647,6 +689,7 @@ hipError_t launch_gqa_decode(const DecodeParams& p, int head_dim, int group, int
     return hipErrorInvalidValue;
   if (head_dim == 64) return launch_d<64>(p, group, work_items, combine, st);
   if (head_dim == 128) return launch_d<128>(p, group, work_items, combine, st);
+  if (head_dim == 256 && group <= 4) return launch_d<256>(p, group, work_items, combine, st);
   return hipErrorInvalidValue;
 }
 

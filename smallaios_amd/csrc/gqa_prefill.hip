@@ -302,12 +302,15 @@ __device__ __forceinline__ void stage_store4(const TileStage4<D, NT>& S, Prefill
   }
 }
 
+// RB row blocks of 16 attention rows per wave: 2 up to head_dim 128, 1 at
+// 256 (the query pair and the accumulators of two blocks would not fit).
 template <int D, int G, int NW, int Q>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillParams p) {
   constexpr int NT = 64 * NW;
   constexpr int KS = D / 32;      // 32-dim k steps of QK
   constexpr int JB = D / 16;      // 16-dim column blocks of PV
-  constexpr int QT = 32 * NW / G; // query positions per workgroup
+  constexpr int RB = D > 128 ? 1 : 2;
+  constexpr int QT = 16 * RB * NW / G;  // query positions per workgroup
   constexpr bool INT4 = Q == kQuantInt4;
   typedef PrefillTile<D, INT4> Tile;
   constexpr int KROW = Tile::KROW;
@@ -364,11 +367,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   // RoPE(q) * scale * log2(e) as an f16 pair hi + lo (~22 bits: a score's
   // rounding error stays ~2^-20 of its largest term, outlier channels
   // included); lane (r, g) holds dims 32ks + 8g .. +7
-  v8h qB[2][KS], qL[2][KS];
-  int qpos[2];  // absolute position of the row (clamped for dead rows)
+  v8h qB[RB][KS], qL[RB][KS];
+  int qpos[RB];  // absolute position of the row (clamped for dead rows)
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int R = wave * 32 + rb * 16 + r;
+  for (int rb = 0; rb < RB; ++rb) {
+    const int R = wave * (16 * RB) + rb * 16 + r;
     const int il = q0 + R / G;
     const int hq = kvh * G + R % G;
     const int i = il < p.sq ? il : p.sq - 1;
@@ -417,11 +420,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   __syncthreads();
 
   // ---- online softmax state ----------------------------------------------------
-  float m_run[2] = {-INFINITY, -INFINITY};  // lane (row r): row r of block rb
-  float l_run[2] = {0.0f, 0.0f};
-  v4f acc[2][JB];  // lane (dim r of block jb, g): rows 4g+e of block rb
+  float m_run[RB], l_run[RB];  // lane (row r): row r of block rb
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < RB; ++rb) {
+    m_run[rb] = -INFINITY;
+    l_run[rb] = 0.0f;
+  }
+  v4f acc[RB][JB];  // lane (dim r of block jb, g): rows 4g+e of block rb
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int jb = 0; jb < JB; ++jb) acc[rb][jb] = v4f{0.f, 0.f, 0.f, 0.f};
 
@@ -433,11 +440,13 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 
     // S^T for both row blocks: 4 column blocks of 16 tokens; k steps outer so
     // that eight independent accumulation chains interleave on the MFMA pipe
-    float s[2][4][4];
+    float s[RB][4][4];
     {
-      v4f c[4][2];
+      v4f c[4][RB];
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) c[cb][0] = c[cb][1] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) c[cb][rb] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         // one term at a time over all eight accumulators, so that consecutive
@@ -448,19 +457,19 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-          for (int rb = 0; rb < 2; ++rb)
+          for (int rb = 0; rb < RB; ++rb)
             c[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cb], qB[rb][ks], c[cb][rb], 0, 0, 0);
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-          for (int rb = 0; rb < 2; ++rb)
+          for (int rb = 0; rb < RB; ++rb)
             c[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cb], qL[rb][ks], c[cb][rb], 0, 0, 0);
         if constexpr (INT4) {
 #pragma unroll
           for (int cb = 0; cb < 4; ++cb) {
             const v8h al = *(const v8h*)(T.klo + (16 * cb + r) * KROW + 8 * g + 32 * ks);
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
+            for (int rb = 0; rb < RB; ++rb)
               c[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qB[rb][ks], c[cb][rb], 0, 0, 0);
           }
         }
@@ -473,14 +482,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
           skx[0] = skv.x, skx[1] = skv.y, skx[2] = skv.z, skx[3] = skv.w;
         }
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) s[rb][cb][e] = INT4 ? c[cb][rb][e] : c[cb][rb][e] * skx[e];
       }
     }
     if (tile >= full_tiles || tile < lo_full) {
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
@@ -491,10 +500,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
           }
     }
 
-    v8h pa[2][2];
-    float alpha[2];
+    v8h pa[RB][2];
+    float alpha[RB];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
       float mt = -INFINITY;
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb)
@@ -526,9 +535,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 
     // rescale the accumulator rows 4g+e (alpha of row j lives in lane j),
     // unless no row of the wave moved its maximum
-    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.0f || alpha[1] != 1.0f) != 0) {
+    bool moved = false;
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) moved = moved || alpha[rb] != 1.0f;
+    if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
         float ae[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) ae[e] = __shfl(alpha[rb], 4 * g + e, 64);
@@ -543,8 +555,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 #pragma unroll
       for (int jb = 0; jb < JB; ++jb) {
         const v8h bv = *(const v8h*)(T.v + ((size_t)kst * D + 16 * jb + r) * VROW + 8 * g);
-        acc[0][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[0][kst], bv, acc[0][jb], 0, 0, 0);
-        acc[1][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[1][kst], bv, acc[1][jb], 0, 0, 0);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[rb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rb][kst], bv, acc[rb][jb], 0, 0, 0);
       }
 
     if (more) store_stage(sT[(tile + 1) & 1], t0 + 64);
@@ -553,12 +566,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 
   // ---- write O / l ------------------------------------------------------------
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+  for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = 4 * g + e;  // row within the block
       const float l = __shfl(l_run[rb], row, 64);
-      const int R = wave * 32 + rb * 16 + row;
+      const int R = wave * (16 * RB) + rb * 16 + row;
       const int il = q0 + R / G;
       if (il >= p.sq) continue;
       const int hq = kvh * G + R % G;
@@ -572,13 +585,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 
 template <int D, int NW, int Q>
 hipError_t launch_dn(const PrefillParams& p, int group, hipStream_t st) {
+  constexpr int RB = D > 128 ? 1 : 2;  // as in the kernel
   auto grid = [&](int qt) { return dim3((p.sq + qt - 1) / qt, p.kv_heads, p.batch); };
   const dim3 block(64 * NW);
   switch (group) {
-    case 1: hipLaunchKernelGGL((gqa_prefill_kernel<D, 1, NW, Q>), grid(32 * NW), block, 0, st, p); break;
-    case 2: hipLaunchKernelGGL((gqa_prefill_kernel<D, 2, NW, Q>), grid(16 * NW), block, 0, st, p); break;
-    case 4: hipLaunchKernelGGL((gqa_prefill_kernel<D, 4, NW, Q>), grid(8 * NW), block, 0, st, p); break;
-    case 8: hipLaunchKernelGGL((gqa_prefill_kernel<D, 8, NW, Q>), grid(4 * NW), block, 0, st, p); break;
+    case 1: hipLaunchKernelGGL((gqa_prefill_kernel<D, 1, NW, Q>), grid(16 * RB * NW), block, 0, st, p); break;
+    case 2: hipLaunchKernelGGL((gqa_prefill_kernel<D, 2, NW, Q>), grid(8 * RB * NW), block, 0, st, p); break;
+    case 4: hipLaunchKernelGGL((gqa_prefill_kernel<D, 4, NW, Q>), grid(4 * RB * NW), block, 0, st, p); break;
+    case 8: hipLaunchKernelGGL((gqa_prefill_kernel<D, 8, NW, Q>), grid(2 * RB * NW), block, 0, st, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -600,6 +614,7 @@ hipError_t launch_gqa_prefill(const PrefillParams& p, int head_dim, int group, i
   if (quant != kQuantInt8 && quant != kQuantInt4) return hipErrorInvalidValue;
   if (head_dim == 64) return launch_d<64>(p, group, quant, st);
   if (head_dim == 128) return launch_d<128>(p, group, quant, st);
+  if (head_dim == 256 && quant == kQuantInt8) return launch_dn<256, 8, kQuantInt8>(p, group, st);
   return hipErrorInvalidValue;
 }
 

@@ -1,0 +1,113 @@
+"""head_dim 256 (the Gemma 3 attention shape, onnx-rt/src/model_loader/config.rs:695-717:
+8 query heads over 4 kv heads, sliding windows of 1024) through kernels 1-3 on the
+int8 cache, against the oracle. Same bar as the other parity tests: codes and scales
+bit-exact, outputs within 2e-3 abs + 1e-2 rel.
+"""
+import numpy as np
+import pytest
+
+import smallaios_amd as S
+from _gpu_util import Case, assert_close, log
+
+pytestmark = pytest.mark.gpu
+D = 256
+
+
+@pytest.fixture(scope="module")
+def rt():
+    import torch
+    assert torch.cuda.is_available()
+    r = S.Runtime(0)
+    yield r
+    r.close()
+
+
+@pytest.mark.parametrize("interleaved,kv_dtype", [(False, "bf16"), (True, "f32")])
+def test_append_d256_bit_exact(rt, interleaved, kv_dtype):
+    log(f"append d=256 interleaved={interleaved} {kv_dtype}")
+    c = Case(rt, 256 + interleaved, 3, 8, 4, D, [40, 5, 17], 9, theta=1e6, kv_dtype=kv_dtype,
+             permute_pages=True, interleaved=interleaved)
+    c.step_kv()
+    c.check_codes()
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 4), (4, 4), (4, 1)])
+def test_decode_d256_groups(rt, hq, hkv):
+    log(f"decode d=256 hq={hq} hkv={hkv}")
+    c = Case(rt, 300 + hq + hkv, 2, hq, hkv, D, [700, 129], 1, theta=1e6, permute_pages=True)
+    c.step_kv()
+    q = c.query("bf16")
+    assert_close(c.gpu_decode(q, "bf16"), c.oracle_attend(q), f"d=256 group {hq // hkv}")
+    c.check_codes(seqs=[1])
+
+
+@pytest.mark.parametrize("split", [64, 1024])
+def test_decode_d256_split_merge_and_fused(rt, split):
+    """Several split partials through the combine kernel, then the fused
+    append + decode step."""
+    log(f"decode d=256 split={split}")
+    c = Case(rt, 333, 3, 8, 4, D, [2500, 1, 640], 1, theta=1e6, permute_pages=True,
+             extra_tokens=1)
+    prev = rt.set_decode_split(split)
+    try:
+        c.step_kv()
+        q = c.query()
+        assert_close(c.gpu_decode(q), c.oracle_attend(q), f"d=256 split {split}")
+        c.cache.advance()
+        q = c.query()
+        got = c.step_fused(q)
+        assert_close(got, c.oracle_attend(q), f"d=256 fused split {split}")
+        c.check_codes(seqs=[1])
+    finally:
+        rt.set_decode_split(prev)
+
+
+def test_decode_d256_windows(rt):
+    """Gemma 3's sliding layers: a layer window of 1024 and a mask window."""
+    log("decode d=256 windows")
+    c = Case(rt, 345, 2, 8, 4, D, [3000, 700], 1, theta=1e6)
+    c.cache.set_layer_window(0, 1024)
+    c.step_kv()
+    q = c.query()
+    assert_close(c.gpu_decode(q), c.oracle_attend(q, layer_window=1024), "d=256 layer window")
+    assert_close(c.gpu_decode(q, window=300), c.oracle_attend(q, layer_window=1024, mask_window=300),
+                 "d=256 both windows")
+
+
+def test_decode_d256_group8_rejected(rt):
+    c = Case(rt, 346, 1, 8, 1, D, [64], 1)
+    c.step_kv()
+    with pytest.raises(S.SaiError) as e:
+        c.gpu_decode(c.query())
+    assert e.value.kind == "Unsupported"
+
+
+@pytest.mark.parametrize("hq,hkv,past,new,qd", [
+    (8, 4, [300, 0], 150, "bf16"), (8, 1, [100, 37], 70, "f32"), (4, 4, [64, 640], 33, "f32")])
+def test_prefill_d256(rt, hq, hkv, past, new, qd):
+    log(f"prefill d=256 hq={hq} hkv={hkv} past={past} new={new} {qd}")
+    c = Case(rt, 350 + new, len(past), hq, hkv, D, past, new, theta=1e6, permute_pages=True,
+             kv_dtype=qd)
+    c.step_kv()
+    c.check_codes()
+    q = c.query(qd)
+    assert_close(c.gpu_prefill(q, qd), c.oracle_attend(q), "d=256 prefill")
+
+
+def test_prefill_d256_outlier_keys_and_window(rt):
+    """x20 outlier channels (Student-t elsewhere) and a 64-key sliding window."""
+    log("prefill d=256 outlier keys + window")
+
+    def outliers(rng, k):
+        b, n, hd = k.shape
+        t = rng.standard_t(3, size=k.shape).astype(np.float32).reshape(b, n, hd // D, D)
+        t[..., [5, 17, 130, D - 3]] *= 20.0
+        return t.reshape(b, n, hd)
+
+    c = Case(rt, 360, 2, 8, 4, D, [200, 31], 90, theta=1e6, kv_dtype="bf16",
+             k_transform=outliers)
+    c.step_kv()
+    q = c.query("bf16")
+    assert_close(c.gpu_prefill(q, "bf16"), c.oracle_attend(q), "d=256 outlier prefill")
+    assert_close(c.gpu_prefill(q, "bf16", window=64), c.oracle_attend(q, mask_window=64),
+                 "d=256 windowed prefill")
