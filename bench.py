@@ -54,6 +54,8 @@ WORKLOADS = {
     "int4long": dict(kind="decode", batch=4, hq=32, hkv=8, d=128, lens=("uniform", 32768),
                      theta=500000.0, q_dtype="bf16", permute=False, quant="int4",
                      k_dist="outlier_t3"),
+    "gemma4b": dict(kind="decode", batch=16, hq=8, hkv=4, d=256, lens=("uniform", 8192),
+                    theta=1000000.0, q_dtype="bf16", permute=False),
     "ragged": dict(kind="decode", batch=64, hq=32, hkv=8, d=128, lens=("uniform_rand", 128, 16384),
                    theta=500000.0, q_dtype="bf16", permute=True),
     "prefill": dict(kind="prefill", batch=2, hq=32, hkv=8, d=128, past=6144, new=2048,

@@ -88,7 +88,7 @@ int32_t sai_device_supported(int device);
 typedef struct sai_kvcache_desc {
   int32_t num_layers;
   int32_t num_kv_heads;
-  int32_t head_dim;          /* 64 or 128 */
+  int32_t head_dim;          /* 64, 128, or 256 (int8 only; decode groups up to 4) */
   int32_t num_pages;         /* physical pages per layer */
   int32_t max_batch;         /* sequences */
   int32_t max_pages_per_seq; /* page-table width */
