@@ -1085,8 +1085,11 @@ void cpu_layer_kinds_for_gemma() {
 // reset_kv_cache and a fresh pass, each checked against the oracle (RoPE by
 // apply_rope, the int8 cache by kv_append without rotation, attention with
 // both window rules).
-void gpu_session_gemma_graph() {
-  const int L = 4, B = 2, Hq = 8, Hkv = 2, D = 128, W = 24, rows = 160;
+// A Gemma-shaped graph (per layer: RoPE on q and k, then GQA; sliding layers
+// every other one) through GpuSession: prefill and decode passes against the
+// oracle, reset, then the executor's error paths.
+void gemma_graph_session(int Hq, int Hkv, int D, double theta, uint64_t seed) {
+  const int L = 4, B = 2, W = 24, rows = 160;
   SessionConfig cfg;
   cfg.num_hidden_layers = L;
   cfg.num_key_value_heads = Hkv;
@@ -1113,7 +1116,7 @@ void gpu_session_gemma_graph() {
   REQUIRE(session->layer_kinds()[0].tag == LayerKind::Tag::SlidingWindow && session->layer_kinds()[1].tag == LayerKind::Tag::Global,
           "layer kinds");
   std::vector<float> cs, sn;
-  rope_tables(rows, D, 10000.0, cs, sn);
+  rope_tables(rows, D, theta, cs, sn);
   // oracle state per layer: int8 codes of the rotated keys
   const int T = 128;
   struct Lay { std::vector<int8_t> k8, v8; std::vector<float> ks, vs; };
@@ -1125,7 +1128,7 @@ void gpu_session_gemma_graph() {
     }
   };
   clear();
-  std::mt19937_64 gen(61);
+  std::mt19937_64 gen(seed);
   int pos = 0;
   auto pass = [&](int S, const char* what) {
     std::vector<std::pair<std::string, DeviceTensor>> in;
@@ -1188,6 +1191,12 @@ void gpu_session_gemma_graph() {
   REQUIRE(e.to_string() == "execution failed: GPU executor: output tensor 'nothing' not produced", "%s",
           e.to_string().c_str());
 }
+
+void gpu_session_gemma_graph() { gemma_graph_session(8, 2, 128, 10000.0, 61); }
+
+// Gemma 3 4B's attention shape (model_loader/config.rs:695-717): 8 query heads
+// over 4 kv heads, head_dim 256, rope_theta 1e6.
+void gpu_session_gemma3_head256() { gemma_graph_session(8, 4, 256, 1000000.0, 62); }
 
 // test_kv_cache_sliding_window (tests/test_cuda.rs:1275-1334): a global layer
 // and a sliding-window layer of 4; after 6 tokens the global view holds 6,
@@ -1256,6 +1265,7 @@ int main(int argc, char** argv) {
       {"gpu_cpu_op_mha_with_past", true, gpu_cpu_op_mha_with_past},
       {"gpu_cpu_op_kats", true, gpu_cpu_op_kats},
       {"gpu_session_gemma_graph", true, gpu_session_gemma_graph},
+      {"gpu_session_gemma3_head256", true, gpu_session_gemma3_head256},
   };
   std::vector<const Case*> run;
   for (int i = 1; i < argc; ++i) {

@@ -10,8 +10,9 @@ in one child process, the restated reference cache tests
 prefill/decode sessions (global and sliding-window layers, local_window_size)
 checked against the oracle (outputs within 2e-3 abs + 1e-2 rel, cache contents
 bit-exact), the RotaryEmbedding op and dispatcher (bit-exact), the CPU
-attention ops with explicit past/present (present bit-exact), and a
-Gemma-shaped graph run through GpuSession (gqa_session.hpp).
+attention ops with explicit past/present (present bit-exact), and
+Gemma-shaped graphs run through GpuSession (gqa_session.hpp), one of them at
+Gemma 3 4B's head_dim 256.
 """
 import os
 import subprocess
