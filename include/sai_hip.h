@@ -279,7 +279,7 @@ typedef struct sai_tqcache sai_tqcache;
 typedef struct sai_tqcache_desc {
   int32_t num_layers;
   int32_t num_kv_heads;
-  int32_t head_dim;  /* 64 or 128 */
+  int32_t head_dim;  /* 64, 128 or 256 (attention groups up to 4 at 256) */
   int32_t bits;      /* 3, 4 or 8 (kv_quant_bits) */
   int32_t qjl;       /* kv_qjl_residual */
   int32_t max_batch; /* sequences */

@@ -1183,8 +1183,8 @@ SAI_API sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc
   const sai_tqcache_desc& d = *desc;
   if (d.num_layers <= 0 || d.num_kv_heads <= 0 || d.max_batch <= 0 || d.max_rows <= 0)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "tq_cache: zero dimension");
-  if (d.head_dim != 64 && d.head_dim != 128)
-    return fail(ctx, SAI_ERR_UNSUPPORTED, "tq_cache: head_dim %d (64 or 128)", d.head_dim);
+  if (d.head_dim != 64 && d.head_dim != 128 && d.head_dim != 256)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "tq_cache: head_dim %d (64, 128 or 256)", d.head_dim);
   if (d.bits != 3 && d.bits != 4 && d.bits != 8)
     return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE, "bits must be 3, 4, or 8");
   if (d.num_kv_heads > 65535 || d.max_batch > 65535)
@@ -1460,6 +1460,8 @@ sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, c
   const int G = num_heads / H;
   if (G != 1 && G != 2 && G != 4 && G != 8)
     return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: group size %d (supported 1, 2, 4, 8)", op, G);
+  if (D == 256 && G > 4)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: head_dim 256 supports groups of 1, 2 and 4", op);
   const int nb = c->pending > 0 ? c->batch : batch;
   if (batch <= 0 || batch != nb || batch > c->desc.max_batch)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: batch %d does not match the cache's %d", op,

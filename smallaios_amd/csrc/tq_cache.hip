@@ -74,11 +74,16 @@ __device__ __forceinline__ void wave_butterfly(float (&y)[D / 64], int lane, flo
       y[e] = (lane & h) ? p - y[e] : y[e] + p;
     }
   }
-  if constexpr (E == 2) {
-    const float a0 = y[0], a1 = y[1];
-    y[0] = a0 + a1;
-    y[1] = a0 - a1;
-  }
+  // stages 64, 128, ...: pairs of the lane's own dims, (e, e + h/64)
+#pragma unroll
+  for (int hs = 1; hs < E; hs <<= 1)
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if ((e & hs) == 0) {
+        const float a0 = y[e], a1 = y[e + hs];
+        y[e] = a0 + a1;
+        y[e + hs] = a0 - a1;
+      }
 #pragma unroll
   for (int e = 0; e < E; ++e) y[e] *= norm;
 }
@@ -223,7 +228,8 @@ __device__ __forceinline__ void wave_store_row(const TqArgs& a, const float (&x)
     c = wave_qjl<D>(code, scale, zero, x, sgn, lane, a.norm, sres, sb);
     if (lane < D / 32) {
       uint64_t m = sb[0];
-      if constexpr (E == 2) m = (lane >> 1) ? sb[1] : sb[0];
+#pragma unroll
+      for (int e = 1; e < E; ++e) m = (lane >> 1) == e ? sb[e] : m;
       ((kind ? a.signs_v : a.signs_k) + row * (D / 32))[lane] =
           (uint32_t)((lane & 1) ? (m >> 32) : m);
     }
@@ -386,7 +392,8 @@ __device__ __forceinline__ void wave_encode_query(const TqArgs& a, const TqAtten
   }
   if (lane < D / 32) {
     uint64_t m = sb[0];
-    if constexpr (E == 2) m = (lane >> 1) ? sb[1] : sb[0];
+#pragma unroll
+    for (int e = 1; e < E; ++e) m = (lane >> 1) == e ? sb[e] : m;
     sgw[lane] = (uint32_t)((lane & 1) ? (m >> 32) : m);
   }
 }
@@ -639,7 +646,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
         ks[4 * j + 2] = w4.z;
         ks[4 * j + 3] = w4.w;
       }
-      if constexpr (D == 64) {
+      if constexpr (D == 64) {  // two words
         const uint2 w2 = *(const uint2*)(a.signs_k + rr * (D / 32));
         ks[0] = w2.x;
         ks[1] = w2.y;
@@ -826,7 +833,12 @@ hipError_t attend_db(const TqArgs& a, const TqAttendArgs& t, int group, int nspl
     case 1: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 1, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
     case 2: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 2, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
     case 4: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 4, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
-    case 8: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 8, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
+    case 8:
+      if constexpr (D <= 128) {
+        hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 8, 4, MODE>), grid, dim3(256), 0, st, a, t);
+        break;
+      }
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
@@ -836,7 +848,12 @@ hipError_t attend_db(const TqArgs& a, const TqAttendArgs& t, int group, int nspl
     case 1: hipLaunchKernelGGL((tq_merge_kernel<D, 1>), mg, dim3(D), 0, st, a, t); break;
     case 2: hipLaunchKernelGGL((tq_merge_kernel<D, 2>), mg, dim3(2 * D), 0, st, a, t); break;
     case 4: hipLaunchKernelGGL((tq_merge_kernel<D, 4>), mg, dim3(4 * D), 0, st, a, t); break;
-    case 8: hipLaunchKernelGGL((tq_merge_kernel<D, 8>), mg, dim3(8 * D), 0, st, a, t); break;
+    case 8:
+      if constexpr (D <= 128) {
+        hipLaunchKernelGGL((tq_merge_kernel<D, 8>), mg, dim3(8 * D), 0, st, a, t);
+        break;
+      }
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -854,6 +871,7 @@ hipError_t dispatch_dbits(int d, int bits, F&& f) {
   };
   if (d == 64) return by_bits(std::integral_constant<int, 64>{});
   if (d == 128) return by_bits(std::integral_constant<int, 128>{});
+  if (d == 256) return by_bits(std::integral_constant<int, 256>{});
   return hipErrorInvalidValue;
 }
 

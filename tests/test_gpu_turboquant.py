@@ -73,7 +73,9 @@ def check_rows(cache, layer, b, h, t0, x_k, x_v, heads, d, bits, qjl, seed):
 
 @pytest.mark.parametrize("d,bits,qjl,bf16", [(128, 4, True, False), (128, 3, True, True),
                                              (64, 8, False, False), (64, 4, True, True),
-                                             (128, 8, True, False), (64, 3, False, False)])
+                                             (128, 8, True, False), (64, 3, False, False),
+                                             (256, 4, True, True), (256, 3, True, False),
+                                             (256, 8, False, False)])
 def test_write_read_bit_exact(rt, d, bits, qjl, bf16):
     """A prefill pass then a decode pass, two layers; every stored row of
     layer 1 checked."""
@@ -105,7 +107,7 @@ def test_write_read_bit_exact(rt, d, bits, qjl, bf16):
         c.close()
 
 
-@pytest.mark.parametrize("d,bits", [(128, 3), (64, 4), (128, 8)])
+@pytest.mark.parametrize("d,bits", [(128, 3), (64, 4), (128, 8), (256, 4)])
 def test_writes_across_tile_boundaries(rt, d, bits):
     """Passes of 70, 1, 130 and 1 rows from unaligned starts: the V tiles
     are read-modify-written by their owning wave at both ends of a pass, and
@@ -175,7 +177,8 @@ def oracle_attend(cache_rows_k, cache_rows_v, q, bits, qjl, sg, scale):
 
 @pytest.mark.parametrize("d,bits,qjl,group,bf16", [
     (128, 4, True, 4, False), (128, 3, True, 8, True), (64, 8, False, 2, False),
-    (128, 8, True, 1, False), (64, 4, True, 8, True), (64, 3, False, 4, False)])
+    (128, 8, True, 1, False), (64, 4, True, 8, True), (64, 3, False, 4, False),
+    (256, 4, True, 2, True), (256, 3, False, 4, False), (256, 8, True, 1, False)])
 def test_attend_matches_oracle(rt, d, bits, qjl, group, bf16):
     """Prefill 40 rows, then a decode pass whose appended row is attended
     while pending (one split)."""
@@ -249,7 +252,7 @@ def test_attend_long_ragged_splits(rt):
 
 
 @pytest.mark.parametrize("d,bits,qjl,group", [(128, 4, True, 4), (64, 8, False, 8),
-                                               (128, 3, True, 2)])
+                                               (128, 3, True, 2), (256, 4, True, 4)])
 def test_logits_and_weighted_sum(rt, d, bits, qjl, group):
     """The design's attention_logits and weighted_value_sum over ragged
     sequences (two splits for one of them). Logits: the integer-exact path
@@ -302,7 +305,7 @@ def test_logits_and_weighted_sum(rt, d, bits, qjl, group):
 
 
 @pytest.mark.parametrize("d,bits,qjl,group,bf16", [(128, 4, True, 4, True), (64, 3, True, 8, False),
-                                                    (128, 8, False, 2, False)])
+                                                    (128, 8, False, 2, False), (256, 4, True, 2, True)])
 def test_write_attend_fused_step(rt, d, bits, qjl, group, bf16):
     """sai_tqcache_write_attend against sai_tqcache_write + sai_tqcache_attend
     on a twin cache: the same outputs bit for bit and the same stored rows,
@@ -385,6 +388,17 @@ def test_errors_and_lifecycle(rt):
     with pytest.raises(S.SaiError) as e:
         S.TqCache(rt, 1, 2, 96, 4, True, 1, 8)
     assert e.value.kind == "Unsupported"
+    c256 = S.TqCache(rt, 1, 1, 256, 4, True, 1, 8)
+    try:
+        import torch
+        x = torch.randn(1, 1, 256, device="cuda")
+        c256.write(0, x, x, 1, 1)
+        with pytest.raises(S.SaiError) as e:  # group 8 at head_dim 256
+            c256.attend(0, torch.randn(1, 1, 8 * 256, device="cuda"),
+                        torch.zeros(1, 1, 8 * 256, device="cuda"), 1, 8)
+        assert e.value.kind == "Unsupported"
+    finally:
+        c256.close()
     d, heads = 64, 2
     c = S.TqCache(rt, 2, heads, d, 4, False, 2, 8)
     try:
