@@ -8,7 +8,7 @@
 // normalised Walsh-Hadamard butterfly y = H(s*x)/sqrt(D), one min/max
 // quantiser over y (codes of 3, 4 or 8 bits), and, with QJL on (:365-395),
 // the sign bits of r = x - decode(codes) and C = mean|r|. One wave encodes a
-// row, lane l holding dims l and l + 64: every f32 step is the reference's
+// row, lane l holding dims l + 64 e (D = 64, 128 or 256): every f32 step is the reference's
 // (same operands, same order, no contraction, IEEE division; the running
 // sum of |r| is taken in dim order), so codes, scale, zero point, sign bits
 // and C are the reference's bit for bit.
@@ -22,7 +22,8 @@
 // C_q C_t (D - 2 popcount(sq ^ s_t)) / D. The values are summed in the
 // rotated domain on the f16 MFMA (weights p_t vs_t / S in f16, codes as exact
 // f16 subnormals code * 2^-24) and rotated back once per output (inverse
-// butterfly, signs), in the merge kernel.
+// butterfly, signs), by the attention kernel for a single split and by the
+// merge kernel otherwise.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -60,8 +61,8 @@ __device__ __forceinline__ float load_row_elem(const void* p, size_t i, bool bf1
 
 // The reference's butterfly (wht_butterfly_normalize, :81-110) over a row
 // spread across the wave (lane l: dims l + 64 e): stage h pairs dims (j, j+h)
-// into (a + b, a - b); stages below 64 pair lanes l and l ^ h, stage 64 the
-// two dims of a lane. Then * norm.
+// into (a + b, a - b); stages below 64 pair lanes l and l ^ h, stages 64 and
+// up the dims of a lane. Then * norm.
 template <int D>
 __device__ __forceinline__ void wave_butterfly(float (&y)[D / 64], int lane, float norm) {
 #pragma clang fp contract(off)
