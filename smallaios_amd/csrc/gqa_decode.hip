@@ -57,7 +57,8 @@ struct TileRegs {
   float sk, sv;   // K / V scale of (page g, slot r); shared through LDS
 };
 
-template <int D>
+// Parts of a tile load: K codes and both scales (part 1), V codes (part 2).
+template <int D, int PART = 3>
 __device__ __forceinline__ void load_tile(TileRegs<D>& T, const uint8_t* __restrict__ pool,
                                           const int* sm_pg, int tile, int num_pages, int kvh,
                                           int r, int g, int n_pages_split) {
@@ -67,17 +68,23 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& T, const uint8_t* __restr
   const int pg_k = sm_pg[min(tile * 4 + (r >> 2), lp)];
   const uint8_t* blk_g = pool + block_offset(pg_g, kvh, num_pages, BB);
   const uint8_t* blk_k = pool + block_offset(pg_k, kvh, num_pages, BB);
+  if constexpr ((PART & 1) != 0) {
 #pragma unroll
-  for (int blk = 0; blk < 4; ++blk)
+    for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
-    for (int ks = 0; ks < TileRegs<D>::KS; ++ks)
-      T.ka[blk][ks] = __builtin_nontemporal_load(
-          (const v4i*)(blk_k + (size_t)(4 * blk + (r & 3)) * D + (D / 4) * g + 16 * ks));
+      for (int ks = 0; ks < TileRegs<D>::KS; ++ks)
+        T.ka[blk][ks] = __builtin_nontemporal_load(
+            (const v4i*)(blk_k + (size_t)(4 * blk + (r & 3)) * D + (D / 4) * g + 16 * ks));
+  }
+  if constexpr ((PART & 2) != 0) {
 #pragma unroll
-  for (int jb = 0; jb < TileRegs<D>::JB; ++jb)
-    T.vb[jb] = __builtin_nontemporal_load((const v4i*)(blk_g + 16 * D + (16 * jb + r) * 16));
-  T.sk = ((const float*)(blk_g + 32 * D))[r];
-  T.sv = ((const float*)(blk_g + 32 * D + 64))[r];
+    for (int jb = 0; jb < TileRegs<D>::JB; ++jb)
+      T.vb[jb] = __builtin_nontemporal_load((const v4i*)(blk_g + 16 * D + (16 * jb + r) * 16));
+  }
+  if constexpr ((PART & 1) != 0) {
+    T.sk = ((const float*)(blk_g + 32 * D))[r];
+    T.sv = ((const float*)(blk_g + 32 * D + 64))[r];
+  }
 }
 
 template <int D, int G>
@@ -86,11 +93,19 @@ struct WaveState {
   float acc[D / 16][2]; // lane (dim 16*jb + r, group g): heads 2g, 2g+1
 };
 
-template <int D, int G>
+struct NoHook {
+  __device__ void operator()() const {}
+};
+
+// after_qk runs once the tile's K codes and scales are consumed (the QK
+// MFMAs issued, the scales in LDS), after_pv once its V codes are: a caller
+// with one tile buffer loads the next tile's K and V there.
+template <int D, int G, class H1 = NoHook, class H2 = NoHook>
 __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, G>& st,
                                              const v4i (&qB)[D / 64], float q_own, float q_oth,
                                              int tok0, int t_lo, int t_end, bool is_hi, bool live,
-                                             int g, float* sm_sc) {
+                                             int g, float* sm_sc, H1 after_qk = H1{},
+                                             H2 after_pv = H2{}) {
   constexpr int KS = D / 64;
   constexpr int JB = D / 16;
   // QK^T on the matrix cores
@@ -106,6 +121,7 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, 
   const int lane = threadIdx.x & 63;
   sm_sc[lane] = T.sk;
   sm_sc[64 + lane] = T.sv;
+  after_qk();
   __builtin_amdgcn_wave_barrier();  // LDS ops of a wave run in order; keep the compiler from hoisting
   float skv[16], svv[16];
 #pragma unroll
@@ -200,6 +216,7 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, 
     st.acc[jb][0] = st.acc[jb][0] * a0 + ((float)co[0] * s0 + (float)co[1] * s0l);
     st.acc[jb][1] = st.acc[jb][1] * a1 + ((float)co[2] * s1 + (float)co[3] * s1l);
   }
+  after_pv();
 }
 
 template <int D, int G, int NW>
@@ -431,23 +448,21 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
       compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
     }
   } else {
-    // head_dim 256: a tile is ~128 registers, so one buffer; each iteration
-    // touches the wave's next tile (its own tile again on the last one, so
-    // the code stays straight-line) into L2 while the current one computes
+    // head_dim 256: a tile is ~128 registers, so one buffer, refilled by
+    // phase: the next tile's K (and scales) load as soon as this tile's QK is
+    // issued, its V as soon as this tile's PV is (the last tile reloads
+    // itself, so the code stays straight-line)
+    if (my_tiles > 0) ld(TA, 0);
     for (; k < my_tiles; ++k) {
-      ld(TA, k);
-      const int tn = wave + min(k + 1, my_tiles - 1) * NW;
-      uint32_t tch[kTouch];
-#pragma unroll
-      for (int j = 0; j < kTouch; ++j) {
-        const int line = min(lane + 64 * j, 4 * kLines - 1);
-        const int pg = sm_pg[min(tn * 4 + line / kLines, n_pages_split - 1)];
-        tch[j] = *(const uint32_t*)(p.pool + block_offset(pg, kvh, p.num_pages, block_bytes_int8(D)) +
-                                    (size_t)(line % kLines) * 128);
-      }
-      compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
-#pragma unroll
-      for (int j = 0; j < kTouch; ++j) __asm__ volatile("" ::"v"(tch[j]));
+      const int kn = wave + min(k + 1, my_tiles - 1) * NW;
+      compute_tile<D, G>(
+          TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave],
+          [&]() {
+            load_tile<D, 1>(TA, p.pool, sm_pg + tile_off, kn, p.num_pages, kvh, r, g, n_pages_split);
+          },
+          [&]() {
+            load_tile<D, 2>(TA, p.pool, sm_pg + tile_off, kn, p.num_pages, kvh, r, g, n_pages_split);
+          });
     }
   }
 
