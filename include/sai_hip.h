@@ -192,8 +192,8 @@ sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, c
 /* ---- kernel 3: prefill chunk (f16 MFMA) ---------------------------------------
  * Same contract as sai_gqa_decode for a chunk of sq == pending query tokens per
  * sequence (the reference's op_group_query_attention with Sq > 1, causal with
- * past_sk = seq_len[b], microsoft.rs:1156 and :331-337), over an int8 or int4
- * cache (head_dim 64 or 128).
+ * past_sk = seq_len[b], microsoft.rs:1156 and :331-337), over an int8 cache
+ * (head_dim 64, 128 or 256) or an int4 one (64 or 128).
  * q: device [batch, sq, num_heads*D]; out: device [batch, sq, num_heads*D] f32.
  * window and sliding-window layers as for sai_gqa_decode, applied to every
  * query row at its own position (gpu_gqa's mask, attention.rs:79, :111). */
