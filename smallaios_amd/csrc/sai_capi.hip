@@ -1187,8 +1187,9 @@ SAI_API sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc
     return fail(ctx, SAI_ERR_UNSUPPORTED, "tq_cache: head_dim %d (64, 128 or 256)", d.head_dim);
   if (d.bits != 3 && d.bits != 4 && d.bits != 8)
     return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE, "bits must be 3, 4, or 8");
-  if (d.num_kv_heads > 65535 || d.max_batch > 65535)
-    return fail(ctx, SAI_ERR_UNSUPPORTED, "tq_cache: more than 65535 heads or sequences");
+  // the write grid's y is 2 x heads (K and V), its z the sequences
+  if (d.num_kv_heads > 32767 || d.max_batch > 65535)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "tq_cache: more than 32767 heads or 65535 sequences");
   DeviceGuard dg(ctx->device);
   sai_tqcache* c = new (std::nothrow) sai_tqcache();
   if (!c) return fail(ctx, SAI_ERR_ALLOC, "tq_cache: host");
