@@ -357,6 +357,54 @@ def test_write_attend_fused_step(rt, d, bits, qjl, group, bf16):
             c.close()
 
 
+def test_attend_full_size_sampled(rt):
+    """The tq4 workload at full size: 16 sequences x 8192 positions, 32 query
+    heads over 8 kv heads, head_dim 128, 4-bit + QJL, bf16 queries; the cache
+    filled in 1024-position passes, then the fused write + attend step. The
+    outputs of sampled (sequence, kv head) pairs against the oracle, and the
+    last stored rows bit for bit."""
+    import torch
+    log("tq attend full size 16 x 8192, 32Q/8KV, 4-bit + QJL (sampled)")
+    batch, heads, group, d, bits, ctx = 16, 8, 4, 128, 4, 8192
+    nh = heads * group
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(20261202)
+    c = S.TqCache(rt, 1, heads, d, bits, True, batch, ctx, seed=SEED)
+    try:
+        ks, vs = [], []
+        for _ in range(ctx // 1024):
+            k = torch.randn((batch, 1024, heads * d), generator=gen, device="cuda")
+            v = torch.randn((batch, 1024, heads * d), generator=gen, device="cuda")
+            c.write(0, k, v, batch, 1024)
+            c.advance()
+            ks.append(k)
+            vs.append(v)
+        c.set_lengths([ctx - 1] * batch)
+        kn = torch.randn((batch, 1, heads * d), generator=gen, device="cuda").to(torch.bfloat16)
+        vn = torch.randn((batch, 1, heads * d), generator=gen, device="cuda").to(torch.bfloat16)
+        q = torch.randn((batch, 1, nh * d), generator=gen, device="cuda").to(torch.bfloat16)
+        out = torch.zeros((batch, 1, nh * d), device="cuda")
+        c.write_attend(0, q, kn, vn, out, batch, nh)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(batch, nh, d)
+        k = torch.cat(ks, dim=1)[:, :ctx - 1].float().cpu().numpy()
+        v = torch.cat(vs, dim=1)[:, :ctx - 1].float().cpu().numpy()
+        k = np.concatenate([k, kn.float().cpu().numpy()], axis=1)
+        v = np.concatenate([v, vn.float().cpu().numpy()], axis=1)
+        qq = q.float().cpu().numpy().reshape(batch, nh, d)
+        for b, h in [(0, 0), (7, 5), (15, 7)]:
+            sg = head_signs(SEED, 0, heads, h, d)
+            want = oracle_attend(rows_of(k, b, h, heads, d), rows_of(v, b, h, heads, d),
+                                 qq[b, h * group:(h + 1) * group], bits, True, sg,
+                                 S.default_scale(d))
+            np.testing.assert_allclose(got[b, h * group:(h + 1) * group], want, atol=2e-3,
+                                       rtol=1e-2)
+            check_rows(c, 0, b, h, ctx - 4, rows_of(k, b, h, heads, d)[ctx - 4:],
+                       rows_of(v, b, h, heads, d)[ctx - 4:], heads, d, bits, True, SEED)
+    finally:
+        c.close()
+
+
 def test_memory_bytes(rt):
     """cache_memory_footprint (kv_compression.rs:1517-1547): 128 rows of D=64,
     4-bit + QJL stay below the f32 size; the count follows the reference's
