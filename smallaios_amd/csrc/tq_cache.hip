@@ -556,6 +556,13 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   const int split = blockIdx.x;
   const int L = a.seq_lens[b] + a.pending;
   const int r0 = split * t.split_rows;
+  if (L == 0) {
+    // no rows: the reference's zero row (sdpa_write_zero_row, microsoft.rs:322-326)
+    if (MODE != 1 && split == 0)
+      for (int e = threadIdx.x; e < G * D; e += 64 * NW)
+        t.out[((size_t)b * t.num_heads + kvh * G + e / D) * D + e % D] = 0.0f;
+    return;
+  }
   if (r0 >= L) return;  // uniform: this split is past the sequence
   const int r1 = min(L, r0 + t.split_rows);
 

@@ -405,6 +405,33 @@ def test_attend_full_size_sampled(rt):
         c.close()
 
 
+def test_empty_sequence_gives_zero_rows(rt):
+    """A sequence with no rows in the batch (set_lengths 0, nothing pending):
+    attention and the weighted sum write zero rows for it, as the reference's
+    SDPA does for a row with no visible key; the other sequence is unaffected."""
+    import torch
+    d, heads, group = 128, 2, 4
+    nh = heads * group
+    c = S.TqCache(rt, 1, heads, d, 4, True, 2, 64, seed=SEED)
+    try:
+        x = torch.randn(2, 10, heads * d, device="cuda")
+        c.write(0, x, x, 2, 10)
+        c.advance()
+        c.set_lengths([10, 0])
+        q = torch.randn(2, 1, nh * d, device="cuda")
+        out = torch.full((2, 1, nh * d), float("nan"), device="cuda")
+        c.attend(0, q, out, 2, nh)
+        w = torch.ones(2 * nh, 16, device="cuda")
+        ws = torch.full((2, 1, nh * d), float("nan"), device="cuda")
+        c.weighted_value_sum(0, w, 16, ws, 2, nh)
+        torch.cuda.synchronize()
+        assert torch.equal(out[1], torch.zeros_like(out[1]))
+        assert torch.equal(ws[1], torch.zeros_like(ws[1]))
+        assert torch.isfinite(out[0]).all() and torch.isfinite(ws[0]).all()
+    finally:
+        c.close()
+
+
 def test_memory_bytes(rt):
     """cache_memory_footprint (kv_compression.rs:1517-1547): 128 rows of D=64,
     4-bit + QJL stay below the f32 size; the count follows the reference's
