@@ -36,7 +36,7 @@ def test_reference_wht_kats():
     assert np.abs(back - x).max() < 1e-4
 
 
-@pytest.mark.parametrize("n", [4, 16, 64, 128])
+@pytest.mark.parametrize("n", [4, 16, 64, 128, 256])
 def test_wht_is_the_sylvester_hadamard(n):
     norm = O.wht(np.eye(n, dtype=np.float32)[1], [1] * n)[0] * 1.0  # scale of one entry
     s = 1.0 / np.sqrt(n)
