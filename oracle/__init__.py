@@ -101,6 +101,9 @@ def _declare(L: C.CDLL) -> None:
                                   _f, _p]),
         "sai_or_tq_attention_logits": (_i, [_p, _i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _p, _p]),
         "sai_or_tq_weighted_value_sum": (None, [_p, _i, _i, _i, _p, _i, _p, _p, _p, _p]),
+        "sai_or_lr_decompose": (_i, [_p, _i, _i, _i, _p, _p]),
+        "sai_or_lr_reconstruct": (None, [_p, _p, _i, _i, _i, _p]),
+        "sai_or_lr_update": (None, [_p, _p, _p, _i, _p, _p, _p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -330,6 +333,55 @@ def tq_weighted_value_sum(weights, bits, signs, v):
                                        _ptr(np.ascontiguousarray(vc)), _ptr(vs), _ptr(vz),
                                        _ptr(out))
     return out
+
+
+class LowRankK:
+    """LowRankK (kv_compression.rs:425-445) with LowRankKeyDecomposer's
+    decompose / update / reconstruct (:470-577); u_s kept with room for
+    `capacity` rows."""
+
+    def __init__(self, k, rank: int, capacity: int | None = None):
+        k = _f32(k)
+        rows, cols = k.shape
+        cap = max(rows, capacity or rows)
+        r = max(1, rank)
+        self.u_s = np.zeros(cap * r, np.float32)
+        self.vt = np.zeros(r * cols, np.float32)
+        self.rank = int(lib().sai_or_lr_decompose(_ptr(np.ascontiguousarray(k)), rows, cols, rank,
+                                                  _ptr(self.u_s), _ptr(self.vt)))
+        self.rows, self.cols, self.write_counter = rows, cols, 0
+
+    def update(self, row):
+        row = _f32(row)
+        assert row.size == self.cols
+        if (self.rows + 1) * self.rank > self.u_s.size:
+            self.u_s = np.concatenate([self.u_s, np.zeros(self.u_s.size + self.rank, np.float32)])
+        rows, rank, wc = C.c_int(self.rows), C.c_int(self.rank), C.c_int(self.write_counter)
+        lib().sai_or_lr_update(_ptr(self.u_s), _ptr(self.vt), C.byref(rows), self.cols,
+                               C.byref(rank), C.byref(wc), _ptr(row))
+        self.rows, self.rank, self.write_counter = rows.value, rank.value, wc.value
+
+    def factors(self):
+        """(U_S [rows, rank], Vt [rank, cols])."""
+        return (self.u_s[:self.rows * self.rank].reshape(self.rows, self.rank).copy(),
+                self.vt[:self.rank * self.cols].reshape(self.rank, self.cols).copy())
+
+    def reconstruct(self):
+        out = np.zeros((self.rows, self.cols), np.float32)
+        lib().sai_or_lr_reconstruct(_ptr(self.u_s), _ptr(self.vt), self.rows, self.cols,
+                                    self.rank, _ptr(out))
+        return out
+
+
+def tq_lowrank_rows(k, rank: int) -> LowRankK:
+    """CompressedKVCache::write_kv's low-rank K state (kv_compression.rs:840-852)
+    after rows k [n, D] in order: the first row decomposed alone, the rest
+    appended by update."""
+    k = _f32(k)
+    lr = LowRankK(k[:1], rank, capacity=k.shape[0])
+    for t in range(1, k.shape[0]):
+        lr.update(k[t])
+    return lr
 
 
 # ------------------------------------------------------------ RoPE / SDPA ---

@@ -1014,3 +1014,118 @@ void sai_or_tq_weighted_value_sum(const float* weights, int G, int dim, int bits
   }
   free(vd);
 }
+
+/* --- LowRankKeyDecomposer (kv_compression.rs:420-690) ------------------- */
+
+/* norm_vec (:674-680): sum of squares in index order, then sqrt_approx. */
+static float lr_norm(const float* v, int n) {
+  float s = 0.0f;
+  for (int i = 0; i < n; ++i) s += v[i] * v[i];
+  return sai_or_sqrt_approx(s);
+}
+
+/* normalize_vec (:683-690): divided by the norm when it exceeds 1e-30. */
+static void lr_normalize(float* v, int n) {
+  float nv = lr_norm(v, n);
+  if (nv > 1e-30f)
+    for (int i = 0; i < n; ++i) v[i] /= nv;
+}
+
+/* power_iteration_svd (:583-671) on a (m x n, row-major; deflated in place):
+ * per component r, v starts at +-1 ((j + r) even: +1) normalised, ten rounds
+ * of u = A v, v = A^T u (rows accumulated in order), v normalised; then
+ * u = A v, sigma = |u|; sigma < 1e-12 ends the loop (the remaining columns
+ * stay zero); U_S[:, r] = (u / sigma) * sigma, Vt[r] = v; A -= sigma u v^T. */
+static void lr_power_svd(float* a, int m, int n, int rank, float* u_s, float* vt) {
+  float* v = (float*)malloc(sizeof(float) * (size_t)n);
+  float* u = (float*)malloc(sizeof(float) * (size_t)m);
+  for (int i = 0; i < m * rank; ++i) u_s[i] = 0.0f;
+  for (int i = 0; i < rank * n; ++i) vt[i] = 0.0f;
+  for (int r = 0; r < rank; ++r) {
+    for (int j = 0; j < n; ++j) v[j] = (j + r) % 2 == 0 ? 1.0f : -1.0f;
+    lr_normalize(v, n);
+    for (int it = 0; it < 10; ++it) {
+      for (int i = 0; i < m; ++i) {
+        float dot = 0.0f;
+        for (int j = 0; j < n; ++j) dot += a[(size_t)i * n + j] * v[j];
+        u[i] = dot;
+      }
+      for (int j = 0; j < n; ++j) v[j] = 0.0f;
+      for (int i = 0; i < m; ++i)
+        for (int j = 0; j < n; ++j) v[j] += a[(size_t)i * n + j] * u[i];
+      lr_normalize(v, n);
+    }
+    for (int i = 0; i < m; ++i) {
+      float dot = 0.0f;
+      for (int j = 0; j < n; ++j) dot += a[(size_t)i * n + j] * v[j];
+      u[i] = dot;
+    }
+    float sigma = lr_norm(u, m);
+    if (sigma < 1e-12f) break;
+    for (int i = 0; i < m; ++i) u[i] /= sigma;
+    for (int i = 0; i < m; ++i) u_s[(size_t)i * rank + r] = u[i] * sigma;
+    for (int j = 0; j < n; ++j) vt[(size_t)r * n + j] = v[j];
+    for (int i = 0; i < m; ++i)
+      for (int j = 0; j < n; ++j) a[(size_t)i * n + j] -= sigma * u[i] * v[j];
+  }
+  free(v);
+  free(u);
+}
+
+/* decompose (:470-498): rank 0 counts as 1 (new, :461-465); the kept rank is
+ * min(rank, rows, cols), returned; u_s [rows][kept], vt [kept][cols]. An
+ * empty matrix keeps the requested rank with no factors. */
+int sai_or_lr_decompose(const float* k, int rows, int cols, int rank, float* u_s, float* vt) {
+  if (rank <= 0) rank = 1;
+  if (rows == 0 || cols == 0) return rank;
+  int kept = rank < rows ? rank : rows;
+  if (cols < kept) kept = cols;
+  float* a = (float*)malloc(sizeof(float) * (size_t)rows * cols);
+  memcpy(a, k, sizeof(float) * (size_t)rows * cols);
+  lr_power_svd(a, rows, cols, kept, u_s, vt);
+  free(a);
+  return kept;
+}
+
+/* reconstruct (:502-523): out[i][j] = sum over r in order of
+ * u_s[i][r] * vt[r][j], from 0.0. */
+void sai_or_lr_reconstruct(const float* u_s, const float* vt, int rows, int cols, int rank,
+                           float* out) {
+  for (int i = 0; i < rows; ++i)
+    for (int j = 0; j < cols; ++j) {
+      float s = 0.0f;
+      for (int r = 0; r < rank; ++r) s += u_s[(size_t)i * rank + r] * vt[(size_t)r * cols + j];
+      out[(size_t)i * cols + j] = rank > 0 ? s : 0.0f;
+    }
+}
+
+/* update (:529-561) and reorthogonalize (:564-577): appends the row's
+ * coefficients new_row . Vt[r] (u_s holds room for one more row), counts the
+ * write, and every 512th write with rows > rank rebuilds U_S Vt and
+ * decomposes it again at min(rank, rows, cols). */
+void sai_or_lr_update(float* u_s, float* vt, int* rows, int cols, int* rank, int* write_counter,
+                      const float* new_row) {
+  int rk = *rank;
+  if (rk == 0 || cols == 0) {
+    *rows += 1;
+    return;
+  }
+  for (int r = 0; r < rk; ++r) {
+    float dot = 0.0f;
+    for (int c = 0; c < cols; ++c) dot += new_row[c] * vt[(size_t)r * cols + c];
+    u_s[(size_t)(*rows) * rk + r] = dot;
+  }
+  *rows += 1;
+  *write_counter += 1;
+  if (*write_counter % 512 == 0 && *rows > rk) {
+    int m = *rows;
+    int kept = rk < m ? rk : m;
+    if (cols < kept) kept = cols;
+    float* a = (float*)malloc(sizeof(float) * (size_t)m * cols);
+    sai_or_lr_reconstruct(u_s, vt, m, cols, rk, a);
+    lr_power_svd(a, m, cols, kept, u_s, vt);
+    free(a);
+    *rank = kept;
+    *write_counter = 0;
+  }
+}

@@ -169,4 +169,11 @@ void sai_or_tq_weighted_value_sum(const float* weights, int G, int dim, int bits
                                   const int8_t* signs, int rows, const uint8_t* v_codes,
                                   const float* v_scale, const float* v_zero, float* out);
 
+/* LowRankKeyDecomposer (kv_compression.rs:451-671). */
+int sai_or_lr_decompose(const float* k, int rows, int cols, int rank, float* u_s, float* vt);
+void sai_or_lr_reconstruct(const float* u_s, const float* vt, int rows, int cols, int rank,
+                           float* out);
+void sai_or_lr_update(float* u_s, float* vt, int* rows, int cols, int* rank, int* write_counter,
+                      const float* new_row);
+
 #endif
