@@ -285,6 +285,11 @@ typedef struct sai_tqcache_desc {
   int32_t max_batch; /* sequences */
   int32_t max_rows;  /* rows per sequence */
   uint64_t seed;     /* KVCacheConfig::seed */
+  /* kv_lowrank_k: 0 = None; r >= 1 = Some(r) (Some(0) means Some(1),
+   * LowRankKeyDecomposer::new, kv_compression.rs:461-465). The cache
+   * decomposes each head's first K row alone, so the kept rank is 1 for any
+   * r (:840-852); read_k then reconstructs K from it. */
+  int32_t lowrank_k;
 } sai_tqcache_desc;
 /* Allocates the layers' storage and uploads the rotation signs. Synchronous.
  * Errors: SHAPE_MISMATCH (zero sizes), UNSUPPORTED (head_dim),
@@ -293,8 +298,11 @@ sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc, sai_tq
 void sai_tqcache_destroy(sai_tqcache* cache);
 /* CompressedKVCache::write_kv for every kv head of `layer`: k, v device
  * [batch, s_new, num_kv_heads*head_dim] (F32 or BF16) become rows
- * len[b] .. len[b] + s_new - 1 (pending). Errors: SHAPE_MISMATCH (layer,
- * sizes, a pass mixing row counts), OVERFLOW (past max_rows), UNSUPPORTED. */
+ * len[b] .. len[b] + s_new - 1 (pending); a low-rank K takes the rows in
+ * order (LowRankKeyDecomposer decompose / update, :840-852), once per layer
+ * and pass. Errors: SHAPE_MISMATCH (layer, sizes, a pass mixing row counts),
+ * OVERFLOW (past max_rows), UNSUPPORTED (dtype; a layer's low-rank K written
+ * twice in one pass). */
 sai_status sai_tqcache_write(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, const void* k,
                              const void* v, int32_t dtype, int32_t batch, int32_t s_new,
                              void* stream);
@@ -303,7 +311,8 @@ sai_status sai_tqcache_write(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, co
 sai_status sai_tqcache_advance(sai_ctx* ctx, sai_tqcache* cache, void* stream);
 /* Committed lengths of sequences 0..batch-1 (<= max_rows; rows beyond a
  * length are ignored), dropping anything pending; the next pass has `batch`
- * sequences. Synchronous. Errors: SHAPE_MISMATCH, OVERFLOW. */
+ * sequences. Synchronous. Errors: SHAPE_MISMATCH, OVERFLOW, UNSUPPORTED (a
+ * low-rank K, whose state follows the rows written: use reset). */
 sai_status sai_tqcache_set_lengths(sai_ctx* ctx, sai_tqcache* cache, const int32_t* lens,
                                    int32_t batch);
 /* All lengths back to 0 (storage kept). Synchronous. */
@@ -320,7 +329,8 @@ sai_status sai_tqcache_memory_bytes(const sai_tqcache* cache, uint64_t* referenc
                                     uint64_t* device_bytes);
 /* read_k / read_v (kv_compression.rs:862-907): rows [start, start+len) of
  * (layer, sequence b, kv head) decoded to f32, host arrays [len][head_dim]
- * each. Synchronous. */
+ * each; with a low-rank K, k_out is its reconstruction 0 + U_S[t] Vt, as
+ * read_k prefers it. Synchronous. */
 sai_status sai_tqcache_read(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, int32_t b,
                             int32_t head, int32_t start, int32_t len, float* k_out,
                             float* v_out);
@@ -328,6 +338,13 @@ sai_status sai_tqcache_read(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, int
  * [len][head_dim*bits/8] packed LSB first, params [len][3] f32 (scale,
  * zero point, QJL mean), QJL sign words [len][head_dim/64] u64 (qjl only).
  * Synchronous. */
+/* The low-rank K state of (layer, sequence b, kv head) (LowRankK,
+ * kv_compression.rs:425-438, rank 1): u_s [len] = U_S of rows
+ * [start, start+len), vt [head_dim] (either may be NULL). Synchronous.
+ * Errors: UNSUPPORTED (no low-rank K), SHAPE_MISMATCH. */
+sai_status sai_tqcache_read_lowrank(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, int32_t b,
+                                    int32_t head, int32_t start, int32_t len, float* u_s,
+                                    float* vt);
 sai_status sai_tqcache_read_raw(sai_ctx* ctx, sai_tqcache* cache, int32_t layer, int32_t b,
                                 int32_t head, int32_t start, int32_t len, void* k_codes,
                                 void* v_codes, float* k_params, float* v_params, void* k_signs,

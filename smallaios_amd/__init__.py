@@ -50,7 +50,7 @@ class _TqDesc(C.Structure):
     _fields_ = [
         ("num_layers", C.c_int32), ("num_kv_heads", C.c_int32), ("head_dim", C.c_int32),
         ("bits", C.c_int32), ("qjl", C.c_int32), ("max_batch", C.c_int32),
-        ("max_rows", C.c_int32), ("seed", C.c_uint64),
+        ("max_rows", C.c_int32), ("seed", C.c_uint64), ("lowrank_k", C.c_int32),
     ]
 
 
@@ -88,7 +88,7 @@ EXPORTS = [
     "sai_tqcache_write", "sai_tqcache_advance", "sai_tqcache_reset", "sai_tqcache_set_lengths",
     "sai_tqcache_lengths", "sai_tqcache_read", "sai_tqcache_read_raw", "sai_tqcache_attend",
     "sai_tqcache_memory_bytes", "sai_tqcache_attention_logits", "sai_tqcache_weighted_value_sum",
-    "sai_tqcache_write_attend", "sai_set_tq_split",
+    "sai_tqcache_write_attend", "sai_set_tq_split", "sai_tqcache_read_lowrank",
 ]
 ROPE_BHSD = 0
 ROPE_BSHD = 1
@@ -140,6 +140,7 @@ def _declare(L: C.CDLL) -> None:
         "sai_tqcache_lengths": (i32, [p, p, p, p]),
         "sai_tqcache_read": (i32, [p, p, i32, i32, i32, i32, i32, p, p]),
         "sai_tqcache_read_raw": (i32, [p, p, i32, i32, i32, i32, i32, p, p, p, p, p, p]),
+        "sai_tqcache_read_lowrank": (i32, [p, p, i32, i32, i32, i32, i32, p, p]),
         "sai_tqcache_attend": (i32, [p, p, i32, p, i32, i32, i32, i32, f, p, p]),
         "sai_tqcache_memory_bytes": (i32, [p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
         "sai_tqcache_attention_logits": (i32, [p, p, i32, p, i32, i32, i32, p, i32, p]),
@@ -429,11 +430,13 @@ class TqCache:
     kv_compression.rs) on the device."""
 
     def __init__(self, rt: Runtime, num_layers, num_kv_heads, head_dim, bits, qjl, max_batch,
-                 max_rows, seed=0):
+                 max_rows, seed=0, lowrank_k=None):
+        """lowrank_k: KVCacheConfig::kv_lowrank_k (None, or a rank; 0 counts as 1)."""
         self.rt = rt
         self._L = rt._L
+        lr = 0 if lowrank_k is None else max(1, int(lowrank_k))
         self.desc = _TqDesc(num_layers, num_kv_heads, head_dim, bits, int(bool(qjl)), max_batch,
-                            max_rows, seed & (2**64 - 1))
+                            max_rows, seed & (2**64 - 1), lr)
         h = C.c_void_p()
         rt.check(self._L.sai_tqcache_create(rt.handle, C.byref(self.desc), C.byref(h)),
                  "tqcache_create")
@@ -495,6 +498,15 @@ class TqCache:
                                                start, n, k.ctypes.data_as(C.c_void_p),
                                                v.ctypes.data_as(C.c_void_p)), "tqcache_read")
         return k, v
+
+    def read_lowrank(self, layer, b, kv_head, start, n):
+        """The low-rank K state (rank 1): (U_S [n] of rows start.., Vt [D])."""
+        us = np.zeros(n, np.float32)
+        vt = np.zeros(self.head_dim, np.float32)
+        self.rt.check(self._L.sai_tqcache_read_lowrank(
+            self.rt.handle, self.handle, layer, b, kv_head, start, n,
+            us.ctypes.data_as(C.c_void_p), vt.ctypes.data_as(C.c_void_p)), "tqcache_read_lowrank")
+        return us, vt
 
     def read_raw(self, layer, b, kv_head, start, n):
         """Stored rows: dict of k/v codes [n, D*bits/8] u8, params [n, 3] f32

@@ -57,6 +57,10 @@ struct sai_tqcache {
     uint32_t* sg_k = nullptr;
     uint32_t* sg_v = nullptr;
     int8_t* rot = nullptr;  // rotation signs [heads][D]
+    float* lr_us = nullptr;  // low-rank K: U_S per row, Vt, u scratch
+    float* lr_vt = nullptr;
+    float* lr_u = nullptr;
+    bool lr_written = false;  // its low-rank state took this pass's rows
   };
   std::vector<Layer> layers;
   int32_t* d_lens = nullptr;
@@ -1160,6 +1164,9 @@ sai::TqArgs tq_args(const sai_tqcache* c, int32_t layer) {
   a.qjl = c->desc.qjl;
   a.code_stride = c->code_stride;
   a.norm = c->norm;
+  a.lr_us = L.lr_us;
+  a.lr_vt = L.lr_vt;
+  a.lr_u = L.lr_u;
   return a;
 }
 
@@ -1169,7 +1176,8 @@ SAI_API void sai_tqcache_destroy(sai_tqcache* c) {
   if (!c) return;
   for (auto& L : c->layers) {
     for (void* p : {(void*)L.codes_k, (void*)L.codes_v, (void*)L.par_k, (void*)L.par_v,
-                    (void*)L.sg_k, (void*)L.sg_v, (void*)L.rot})
+                    (void*)L.sg_k, (void*)L.sg_v, (void*)L.rot, (void*)L.lr_us, (void*)L.lr_vt,
+                    (void*)L.lr_u})
       if (p) (void)hipFree(p);
   }
   if (c->d_lens) (void)hipFree(c->d_lens);
@@ -1190,6 +1198,8 @@ SAI_API sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc
   // the write grid's y is 2 x heads (K and V), its z the sequences
   if (d.num_kv_heads > 32767 || d.max_batch > 65535)
     return fail(ctx, SAI_ERR_UNSUPPORTED, "tq_cache: more than 32767 heads or 65535 sequences");
+  if (d.lowrank_k < 0)
+    return fail(ctx, SAI_ERR_INVALID_ATTRIBUTE, "tq_cache: lowrank_k %d", d.lowrank_k);
   DeviceGuard dg(ctx->device);
   sai_tqcache* c = new (std::nothrow) sai_tqcache();
   if (!c) return fail(ctx, SAI_ERR_ALLOC, "tq_cache: host");
@@ -1213,6 +1223,10 @@ SAI_API sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc
     if (e == hipSuccess && c->desc.qjl) e = hipMalloc(&L.sg_k, c->rows_total * d.head_dim / 8);
     if (e == hipSuccess && c->desc.qjl) e = hipMalloc(&L.sg_v, c->rows_total * d.head_dim / 8);
     if (e == hipSuccess) e = hipMalloc(&L.rot, rot.size());
+    if (e == hipSuccess && d.lowrank_k > 0) e = hipMalloc(&L.lr_us, c->rows_total * sizeof(float));
+    if (e == hipSuccess && d.lowrank_k > 0) e = hipMalloc(&L.lr_u, c->rows_total * sizeof(float));
+    if (e == hipSuccess && d.lowrank_k > 0)
+      e = hipMalloc(&L.lr_vt, (size_t)d.num_kv_heads * d.max_batch * d.head_dim * sizeof(float));
     if (e == hipSuccess) {
       for (int h = 0; h < d.num_kv_heads; ++h)
         tq_rotation_signs(d.seed, l, d.num_kv_heads, h, d.head_dim, rot.data() + (size_t)h * d.head_dim);
@@ -1252,11 +1266,17 @@ SAI_API sai_status sai_tqcache_write(sai_ctx* ctx, sai_tqcache* c, int32_t layer
     if ((int64_t)c->h_lens[b] + s_new > c->desc.max_rows)
       return fail(ctx, SAI_ERR_OVERFLOW, "%s: position_overflow (sequence %d: %d + %d > %d)", op,
                   b, c->h_lens[b], s_new, c->desc.max_rows);
+  if (c->layers[layer].lr_written)
+    return fail(ctx, SAI_ERR_UNSUPPORTED,
+                "%s: layer %d's low-rank K already took this pass's rows", op, layer);
   DeviceGuard dg(ctx->device);
   sai::TqArgs a = tq_args(c, layer);
-  const hipError_t e = sai::launch_tq_write(a, k, v, dtype == SAI_DTYPE_BF16 ? 1 : 0, batch, s_new,
-                                            (hipStream_t)stream);
+  const int bf = dtype == SAI_DTYPE_BF16 ? 1 : 0;
+  hipError_t e = sai::launch_tq_write(a, k, v, bf, batch, s_new, (hipStream_t)stream);
+  if (e == hipSuccess && a.lr_us)
+    e = sai::launch_tq_lowrank(a, k, bf, batch, s_new, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "tq_cache_write launch");
+  if (a.lr_us) c->layers[layer].lr_written = true;
   c->pending = s_new;
   c->batch = batch;
   return SAI_OK;
@@ -1270,6 +1290,7 @@ SAI_API sai_status sai_tqcache_advance(sai_ctx* ctx, sai_tqcache* c, void* strea
   if (e != hipSuccess) return hip_fail(ctx, e, "tq_cache_advance");
   for (int b = 0; b < c->batch; ++b) c->h_lens[b] += c->pending;
   c->pending = 0;
+  for (auto& L : c->layers) L.lr_written = false;
   return SAI_OK;
 }
 
@@ -1281,6 +1302,7 @@ SAI_API sai_status sai_tqcache_reset(sai_ctx* ctx, sai_tqcache* c) {
   std::fill(c->h_lens.begin(), c->h_lens.end(), 0);
   c->pending = 0;
   c->batch = 0;
+  for (auto& L : c->layers) L.lr_written = false;
   return SAI_OK;
 }
 
@@ -1289,6 +1311,9 @@ SAI_API sai_status sai_tqcache_set_lengths(sai_ctx* ctx, sai_tqcache* c, const i
   if (!ctx || !c || !lens) return SAI_ERR_NULL;
   if (batch <= 0 || batch > c->desc.max_batch)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "tq_cache_set_lengths: batch %d", batch);
+  if (c->desc.lowrank_k > 0)
+    return fail(ctx, SAI_ERR_UNSUPPORTED,
+                "tq_cache_set_lengths: the low-rank K state follows the rows written; reset instead");
   for (int b = 0; b < batch; ++b)
     if (lens[b] < 0 || lens[b] > c->desc.max_rows)
       return fail(ctx, SAI_ERR_OVERFLOW, "tq_cache_set_lengths: length %d of sequence %d exceeds %d",
@@ -1324,9 +1349,17 @@ SAI_API sai_status sai_tqcache_memory_bytes(const sai_tqcache* c, uint64_t* refe
     const uint64_t block = ((uint64_t)d.head_dim * d.bits + 7) / 8 + 4 * 4 + 8 + 1;
     const uint64_t resid = ((uint64_t)d.head_dim + 63) / 64 * 8 + 4 + 8;
     const uint64_t per_row = 2 * block + (d.qjl ? 2 * resid : 0);
-    uint64_t rows = 0;
-    for (int b = 0; b < d.max_batch; ++b) rows += (uint64_t)c->h_lens[b];
+    uint64_t rows = 0, started = 0;
+    for (int b = 0; b < d.max_batch; ++b) {
+      rows += (uint64_t)c->h_lens[b];
+      started += c->h_lens[b] > 0 ? 1 : 0;
+    }
     *reference_bytes = rows * (uint64_t)d.num_layers * d.num_kv_heads * per_row;
+    // LowRankK::memory_bytes (:441-444): (rows * 1 + 1 * D) floats + 32 per
+    // (layer, head) holding rows
+    if (d.lowrank_k > 0)
+      *reference_bytes += (uint64_t)d.num_layers * d.num_kv_heads *
+                          (rows * 4 + started * ((uint64_t)d.head_dim * 4 + 32));
   }
   if (device_bytes) {
     const uint64_t per_layer =
@@ -1334,7 +1367,10 @@ SAI_API sai_status sai_tqcache_memory_bytes(const sai_tqcache* c, uint64_t* refe
                                    (d.qjl ? 2 * (uint64_t)d.head_dim / 8 : 0)) +
         (uint64_t)d.num_kv_heads * d.max_batch * c->tiles_cap *
             sai::tq_vtile_bytes(d.head_dim, d.bits) +
-        (uint64_t)d.num_kv_heads * d.head_dim;
+        (uint64_t)d.num_kv_heads * d.head_dim +
+        (d.lowrank_k > 0 ? (uint64_t)c->rows_total * 8 +
+                               (uint64_t)d.num_kv_heads * d.max_batch * d.head_dim * 4
+                         : 0);
     *device_bytes = per_layer * d.num_layers + (uint64_t)d.max_batch * sizeof(int32_t);
   }
   return SAI_OK;
@@ -1361,6 +1397,30 @@ SAI_API sai_status sai_tqcache_read(sai_ctx* ctx, sai_tqcache* c, int32_t layer,
   if (e == hipSuccess) e = hipMemcpy(k_out, dk, n * sizeof(float), hipMemcpyDeviceToHost);
   if (e == hipSuccess) e = hipMemcpy(v_out, dk + n, n * sizeof(float), hipMemcpyDeviceToHost);
   (void)hipFree(dk);
+  if (e != hipSuccess) return hip_fail(ctx, e, op);
+  return SAI_OK;
+}
+
+SAI_API sai_status sai_tqcache_read_lowrank(sai_ctx* ctx, sai_tqcache* c, int32_t layer,
+                                            int32_t b, int32_t head, int32_t start, int32_t len,
+                                            float* u_s, float* vt) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "tq_cache_read_lowrank";
+  if (c->desc.lowrank_k <= 0) return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: no low-rank K", op);
+  if (layer < 0 || layer >= c->desc.num_layers || b < 0 || b >= c->desc.max_batch || head < 0 ||
+      head >= c->desc.num_kv_heads || start < 0 || len < 0 ||
+      (int64_t)start + len > (int64_t)c->h_lens[b] + (b < c->batch ? c->pending : 0))
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: range out of the written rows", op);
+  DeviceGuard dg(ctx->device);
+  const sai_tqcache::Layer& L = c->layers[layer];
+  const size_t hb = (size_t)head * c->desc.max_batch + b;
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess && u_s && len > 0)
+    e = hipMemcpy(u_s, L.lr_us + hb * c->desc.max_rows + start, (size_t)len * sizeof(float),
+                  hipMemcpyDeviceToHost);
+  if (e == hipSuccess && vt)
+    e = hipMemcpy(vt, L.lr_vt + hb * c->desc.head_dim, (size_t)c->desc.head_dim * sizeof(float),
+                  hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_fail(ctx, e, op);
   return SAI_OK;
 }
@@ -1549,13 +1609,22 @@ SAI_API sai_status sai_tqcache_write_attend(sai_ctx* ctx, sai_tqcache* c, int32_
     if ((int64_t)c->h_lens[b] + 1 > c->desc.max_rows)
       return fail(ctx, SAI_ERR_OVERFLOW, "%s: position_overflow (sequence %d: %d + 1 > %d)", op,
                   b, c->h_lens[b], c->desc.max_rows);
+  if (c->layers[layer].lr_written)
+    return fail(ctx, SAI_ERR_UNSUPPORTED,
+                "%s: layer %d's low-rank K already took this pass's rows", op, layer);
   const int32_t pending = c->pending, pbatch = c->batch;
   c->pending = 1;
   c->batch = batch;
   const float sc = has_scale ? scale : sai_default_scale(c->desc.head_dim);
-  const sai_status st = tq_read_path(ctx, c, layer, 0, q, q_dtype, nullptr, 0, batch, num_heads,
-                                     sc * 1.4426950408889634f, out, stream, op, k_new, v_new,
-                                     kv_dtype);
+  sai_status st = tq_read_path(ctx, c, layer, 0, q, q_dtype, nullptr, 0, batch, num_heads,
+                               sc * 1.4426950408889634f, out, stream, op, k_new, v_new, kv_dtype);
+  if (st == SAI_OK && c->layers[layer].lr_us) {
+    const hipError_t e = sai::launch_tq_lowrank(tq_args(c, layer), k_new,
+                                                kv_dtype == SAI_DTYPE_BF16 ? 1 : 0, batch, 1,
+                                                (hipStream_t)stream);
+    if (e != hipSuccess) st = hip_fail(ctx, e, op);
+    else c->layers[layer].lr_written = true;
+  }
   if (st != SAI_OK) {
     c->pending = pending;
     c->batch = pbatch;

@@ -221,6 +221,12 @@ struct TqArgs {
   int heads, batch_cap, rows_cap, tiles_cap, head_dim, bits, qjl;
   size_t code_stride;  // bytes per row of K codes (multiple of 16)
   float norm;          // 1 / sqrt_approx(head_dim)
+  // low-rank K (rank 1), null when the cache keeps none: U_S per row
+  // [heads][batch_cap][rows_cap], Vt [heads][batch_cap][D], and the
+  // re-decomposition's u vector, laid out as U_S
+  float* lr_us;
+  float* lr_vt;
+  float* lr_u;
 };
 
 struct TqAttendArgs {
@@ -242,6 +248,8 @@ struct TqAttendArgs {
 // Launchers (return hipError_t of the launch).
 hipError_t launch_tq_write(const TqArgs& a, const void* k, const void* v, int bf16, int batch,
                            int s_new, hipStream_t st);
+hipError_t launch_tq_lowrank(const TqArgs& a, const void* k, int bf16, int batch, int s_new,
+                             hipStream_t st);
 hipError_t launch_tq_read(const TqArgs& a, int b, int h, int start, int len, float* k_out,
                           float* v_out, hipStream_t st);
 // mode 0 attention, 1 logits only, 2 weighted value sum only

@@ -309,6 +309,14 @@ __global__ __launch_bounds__(64) void tq_read_kernel(const TqArgs a, int b, int 
   const int kind = idx & 1;
   const int t = idx >> 1;
   const size_t row = ((size_t)h * a.batch_cap + b) * a.rows_cap + start + t;
+  if (kind == 0 && a.lr_us) {
+    // read_k prefers the low-rank K (:871-881): reconstruct's 0 + U_S Vt
+    const float u = a.lr_us[row];
+    const float* vt = a.lr_vt + ((size_t)h * a.batch_cap + b) * D;
+    float* out = k_out + (size_t)t * D;
+    for (int i = 0; i < D; ++i) out[i] = 0.0f + u * vt[i];
+    return;
+  }
   const float4 par = (kind ? a.par_v : a.par_k)[row];
   const uint8_t* kc = a.codes_k + row * a.code_stride;
   float y[D];
@@ -335,6 +343,185 @@ __global__ __launch_bounds__(64) void tq_read_kernel(const TqArgs a, int b, int 
   const int8_t* sg = a.signs + (size_t)h * D;
   float* out = (kind ? v_out : k_out) + (size_t)t * D;
   for (int i = 0; i < D; ++i) out[i] = y[i] * a.norm * (float)sg[i];
+}
+
+// ---- Low-rank K (LowRankKeyDecomposer, kv_compression.rs:451-690) ----
+// CompressedKVCache::write_kv (:840-852) decomposes a head's first K row on
+// its own, so the kept rank is min(rank, 1, D) = 1, and update (:529-561)
+// and reorthogonalize (:564-577) keep it: U_S is one float per row, Vt one
+// row of D. Per row after the first, U_S[r] = k_r . Vt; when the write
+// counter (rows - 1 mod 512) reaches 512, i.e. at rows 513, 1025, ...,
+// U_S Vt is rebuilt and decomposed again by power iteration. Every dot
+// product and norm is summed serially in the reference's index order with
+// the product and the sum rounded apart (contraction off), so the state
+// matches the reference bit for bit. One workgroup per (kv head, sequence)
+// walks the pass's rows in order.
+constexpr int LR_THREADS = 256;
+constexpr int LR_CHUNK = 1024;
+
+// sqrt_approx (onnx-rt/src/operators.rs:3311-3320): ten Newton steps from x.
+__device__ __forceinline__ float lr_sqrt_approx(float x) {
+  if (x <= 0.0f) return 0.0f;
+  float s = x;
+  for (int i = 0; i < 10; ++i) s = 0.5f * (s + x / s);
+  return s;
+}
+
+// normalize_vec (:683-690) of v_s[D]: thread 0 sums the squares in order.
+template <int D>
+__device__ void lr_normalize(float* v_s, float* bc) {
+#pragma clang fp contract(off)
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    float s = 0.0f;
+    for (int j = 0; j < D; ++j) s = s + v_s[j] * v_s[j];
+    *bc = lr_sqrt_approx(s);
+  }
+  __syncthreads();
+  const float n = *bc;
+  if (n > 1e-30f && tid < D) v_s[tid] = v_s[tid] / n;
+  __syncthreads();
+}
+
+// v_s = the +-1 start of component 0 ((j + 0) even: +1), normalised.
+template <int D>
+__device__ void lr_start(float* v_s, float* bc) {
+  if (threadIdx.x < D) v_s[threadIdx.x] = (threadIdx.x & 1) == 0 ? 1.0f : -1.0f;
+  __syncthreads();
+  lr_normalize<D>(v_s, bc);
+}
+
+// u[i] = sum_j (0 + us[i] vt_s[j]) v_s[j] for rows i < R: the rank-1
+// reconstruction times v, each row's sum serial over j.
+template <int D>
+__device__ void lr_upass(const float* us, float* u, int R, const float* vt_s, const float* v_s) {
+#pragma clang fp contract(off)
+  for (int i = threadIdx.x; i < R; i += LR_THREADS) {
+    const float ui = us[i];
+    float dot = 0.0f;
+    for (int j = 0; j < D; ++j) {
+      const float x = 0.0f + ui * vt_s[j];
+      dot = dot + x * v_s[j];
+    }
+    u[i] = dot;
+  }
+  __syncthreads();
+}
+
+// Re-decomposition of rows [0, R) (reorthogonalize + power_iteration_svd,
+// :564-671, rank 1). vt_s holds the current Vt on entry and the new one on
+// exit; us[0..R) is rewritten.
+template <int D>
+__device__ void lr_redecompose(float* us, float* u, int R, float* vt_s, float* v_s, float* c_us,
+                               float* c_u, float* bc) {
+#pragma clang fp contract(off)
+  const int tid = threadIdx.x;
+  lr_start<D>(v_s, bc);
+  for (int it = 0; it < 10; ++it) {
+    lr_upass<D>(us, u, R, vt_s, v_s);
+    // v[j] = sum_i x_ij u[i], rows in order: thread j, rows staged in LDS
+    float acc = 0.0f;
+    for (int i0 = 0; i0 < R; i0 += LR_CHUNK) {
+      const int n = min(LR_CHUNK, R - i0);
+      for (int i = tid; i < n; i += LR_THREADS) {
+        c_us[i] = us[i0 + i];
+        c_u[i] = u[i0 + i];
+      }
+      __syncthreads();
+      if (tid < D) {
+        const float vj = vt_s[tid];
+        for (int i = 0; i < n; ++i) {
+          const float x = 0.0f + c_us[i] * vj;
+          acc = acc + x * c_u[i];
+        }
+      }
+      __syncthreads();
+    }
+    if (tid < D) v_s[tid] = acc;
+    __syncthreads();
+    lr_normalize<D>(v_s, bc);
+  }
+  lr_upass<D>(us, u, R, vt_s, v_s);
+  // sigma = norm_vec(u), rows in order
+  float s = 0.0f;
+  for (int i0 = 0; i0 < R; i0 += LR_CHUNK) {
+    const int n = min(LR_CHUNK, R - i0);
+    for (int i = tid; i < n; i += LR_THREADS) c_u[i] = u[i0 + i];
+    __syncthreads();
+    if (tid == 0)
+      for (int i = 0; i < n; ++i) s = s + c_u[i] * c_u[i];
+    __syncthreads();
+  }
+  if (tid == 0) *bc = lr_sqrt_approx(s);
+  __syncthreads();
+  const float sigma = *bc;
+  const bool zero = sigma < 1e-12f;  // the loop breaks: factors stay zero
+  for (int i = tid; i < R; i += LR_THREADS) us[i] = zero ? 0.0f : (u[i] / sigma) * sigma;
+  if (tid < D) vt_s[tid] = zero ? 0.0f : v_s[tid];
+  __syncthreads();
+}
+
+template <int D>
+__global__ __launch_bounds__(LR_THREADS) void tq_lowrank_kernel(const TqArgs a, const void* k,
+                                                               int bf16, int s_new) {
+#pragma clang fp contract(off)
+  __shared__ float vt_s[D], v_s[D], row_s[D], c_us[LR_CHUNK], c_u[LR_CHUNK];
+  __shared__ float bc;
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int r0 = a.seq_lens[b];
+  const size_t hb = (size_t)h * a.batch_cap + b;
+  float* us = a.lr_us + hb * a.rows_cap;
+  float* u = a.lr_u + hb * a.rows_cap;
+  float* vtg = a.lr_vt + hb * D;
+  const bool is_bf16 = bf16 != 0;
+  auto in_off = [&](int t) { return (((size_t)b * s_new + t) * a.heads + h) * D; };
+  if (tid < D) vt_s[tid] = r0 > 0 ? vtg[tid] : 0.0f;
+  int t = 0;
+  if (r0 == 0) {
+    // decompose(k, 1, D) (:470-498): power iteration on the single row
+    if (tid < D) row_s[tid] = load_row_elem(k, in_off(0) + tid, is_bf16);
+    lr_start<D>(v_s, &bc);
+    for (int it = 0; it < 10; ++it) {
+      if (tid == 0) {
+        float dot = 0.0f;
+        for (int j = 0; j < D; ++j) dot = dot + row_s[j] * v_s[j];
+        bc = dot;
+      }
+      __syncthreads();
+      const float u0 = bc;
+      __syncthreads();
+      if (tid < D) v_s[tid] = 0.0f + row_s[tid] * u0;
+      __syncthreads();
+      lr_normalize<D>(v_s, &bc);
+    }
+    if (tid == 0) {
+      float dot = 0.0f;
+      for (int j = 0; j < D; ++j) dot = dot + row_s[j] * v_s[j];
+      const float sigma = lr_sqrt_approx(0.0f + dot * dot);
+      const bool zero = sigma < 1e-12f;
+      us[0] = zero ? 0.0f : (dot / sigma) * sigma;
+      bc = zero ? 0.0f : 1.0f;
+    }
+    __syncthreads();
+    if (tid < D) vt_s[tid] = bc != 0.0f ? v_s[tid] : 0.0f;
+    __syncthreads();
+    t = 1;
+  }
+  while (t < s_new) {
+    const int r = r0 + t;                       // >= 1
+    const int rr = (r + 511) / 512 * 512;       // the next row whose write re-decomposes
+    const int t_end = min(s_new, rr - r0 + 1);  // rows [t, t_end) project onto this Vt
+    for (int tt = t + tid; tt < t_end; tt += LR_THREADS) {
+      const size_t off = in_off(tt);
+      float dot = 0.0f;
+      for (int c = 0; c < D; ++c) dot = dot + load_row_elem(k, off + c, is_bf16) * vt_s[c];
+      us[r0 + tt] = dot;
+    }
+    __syncthreads();
+    if (r0 + t_end - 1 == rr) lr_redecompose<D>(us, u, rr + 1, vt_s, v_s, c_us, c_u, &bc);
+    t = t_end;
+  }
+  if (tid < D) vtg[tid] = vt_s[tid];
 }
 
 // Byte position of dim d's code in a query record: the order in which the
@@ -895,6 +1082,26 @@ hipError_t launch_tq_write(const TqArgs& a, const void* k, const void* v, int bf
     hipLaunchKernelGGL((tq_write_kernel<D, B>), grid, dim3(64), 0, st, a, k, v, bf16, s_new);
     return hipGetLastError();
   });
+}
+
+hipError_t launch_tq_lowrank(const TqArgs& a, const void* k, int bf16, int batch, int s_new,
+                             hipStream_t st) {
+  if (batch <= 0 || s_new <= 0 || !a.lr_us) return hipSuccess;
+  const dim3 grid(a.heads, batch);
+  switch (a.head_dim) {
+    case 64:
+      hipLaunchKernelGGL(tq_lowrank_kernel<64>, grid, dim3(LR_THREADS), 0, st, a, k, bf16, s_new);
+      break;
+    case 128:
+      hipLaunchKernelGGL(tq_lowrank_kernel<128>, grid, dim3(LR_THREADS), 0, st, a, k, bf16, s_new);
+      break;
+    case 256:
+      hipLaunchKernelGGL(tq_lowrank_kernel<256>, grid, dim3(LR_THREADS), 0, st, a, k, bf16, s_new);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_tq_read(const TqArgs& a, int b, int h, int start, int len, float* k_out,
