@@ -358,6 +358,7 @@ __global__ __launch_bounds__(64) void tq_read_kernel(const TqArgs a, int b, int 
 // walks the pass's rows in order.
 constexpr int LR_THREADS = 256;
 constexpr int LR_CHUNK = 1024;
+constexpr int LR_ROW_FLOATS = 16384;  // LDS for staged K rows, stride D + 1
 
 // sqrt_approx (onnx-rt/src/operators.rs:3311-3320): ten Newton steps from x.
 __device__ __forceinline__ float lr_sqrt_approx(float x) {
@@ -374,6 +375,7 @@ __device__ void lr_normalize(float* v_s, float* bc) {
   const int tid = threadIdx.x;
   if (tid == 0) {
     float s = 0.0f;
+#pragma unroll 16
     for (int j = 0; j < D; ++j) s = s + v_s[j] * v_s[j];
     *bc = lr_sqrt_approx(s);
   }
@@ -430,6 +432,7 @@ __device__ void lr_redecompose(float* us, float* u, int R, float* vt_s, float* v
       __syncthreads();
       if (tid < D) {
         const float vj = vt_s[tid];
+#pragma unroll 8
         for (int i = 0; i < n; ++i) {
           const float x = 0.0f + c_us[i] * vj;
           acc = acc + x * c_u[i];
@@ -448,8 +451,10 @@ __device__ void lr_redecompose(float* us, float* u, int R, float* vt_s, float* v
     const int n = min(LR_CHUNK, R - i0);
     for (int i = tid; i < n; i += LR_THREADS) c_u[i] = u[i0 + i];
     __syncthreads();
-    if (tid == 0)
+    if (tid == 0) {
+#pragma unroll 8
       for (int i = 0; i < n; ++i) s = s + c_u[i] * c_u[i];
+    }
     __syncthreads();
   }
   if (tid == 0) *bc = lr_sqrt_approx(s);
@@ -465,7 +470,9 @@ template <int D>
 __global__ __launch_bounds__(LR_THREADS) void tq_lowrank_kernel(const TqArgs a, const void* k,
                                                                int bf16, int s_new) {
 #pragma clang fp contract(off)
+  constexpr int NR = LR_ROW_FLOATS / (D + 1) < LR_THREADS ? LR_ROW_FLOATS / (D + 1) : LR_THREADS;
   __shared__ float vt_s[D], v_s[D], row_s[D], c_us[LR_CHUNK], c_u[LR_CHUNK];
+  __shared__ float rows_s[NR * (D + 1)];
   __shared__ float bc;
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int r0 = a.seq_lens[b];
@@ -484,6 +491,7 @@ __global__ __launch_bounds__(LR_THREADS) void tq_lowrank_kernel(const TqArgs a, 
     for (int it = 0; it < 10; ++it) {
       if (tid == 0) {
         float dot = 0.0f;
+#pragma unroll 16
         for (int j = 0; j < D; ++j) dot = dot + row_s[j] * v_s[j];
         bc = dot;
       }
@@ -496,6 +504,7 @@ __global__ __launch_bounds__(LR_THREADS) void tq_lowrank_kernel(const TqArgs a, 
     }
     if (tid == 0) {
       float dot = 0.0f;
+#pragma unroll 16
       for (int j = 0; j < D; ++j) dot = dot + row_s[j] * v_s[j];
       const float sigma = lr_sqrt_approx(0.0f + dot * dot);
       const bool zero = sigma < 1e-12f;
@@ -511,13 +520,23 @@ __global__ __launch_bounds__(LR_THREADS) void tq_lowrank_kernel(const TqArgs a, 
     const int r = r0 + t;                       // >= 1
     const int rr = (r + 511) / 512 * 512;       // the next row whose write re-decomposes
     const int t_end = min(s_new, rr - r0 + 1);  // rows [t, t_end) project onto this Vt
-    for (int tt = t + tid; tt < t_end; tt += LR_THREADS) {
-      const size_t off = in_off(tt);
-      float dot = 0.0f;
-      for (int c = 0; c < D; ++c) dot = dot + load_row_elem(k, off + c, is_bf16) * vt_s[c];
-      us[r0 + tt] = dot;
+    // rows staged in LDS by coalesced loads, then one thread per row
+    for (int t0 = t; t0 < t_end; t0 += NR) {
+      const int nr = min(NR, t_end - t0);
+      for (int e = tid; e < nr * D; e += LR_THREADS) {
+        const int q = e / D, c = e - q * D;
+        rows_s[q * (D + 1) + c] = load_row_elem(k, in_off(t0 + q) + c, is_bf16);
+      }
+      __syncthreads();
+      if (tid < nr) {
+        const float* x = rows_s + tid * (D + 1);
+        float dot = 0.0f;
+#pragma unroll 16
+        for (int c = 0; c < D; ++c) dot = dot + x[c] * vt_s[c];
+        us[r0 + t0 + tid] = dot;
+      }
+      __syncthreads();
     }
-    __syncthreads();
     if (r0 + t_end - 1 == rr) lr_redecompose<D>(us, u, rr + 1, vt_s, v_s, c_us, c_u, &bc);
     t = t_end;
   }
