@@ -21,8 +21,10 @@
 //         (head j>>1, term j&1: 0 = hi, 1 = lo). The result lands with lane
 //         (j, g) holding head-term j for all 16 slots of page g -- exactly the
 //         A-operand layout the PV product needs, so no LDS transpose.
-//         k index: lane group g, k step ks <-> dims (D/4)*g + 16*ks + [0,16),
-//         so one row's 4 lane groups read one contiguous 128-byte line.
+//         k index: lane group g, k step ks <-> dims kdim0(g, ks) + [0,16):
+//         (D/4)*g + 16*ks up to head_dim 128, so one row's 4 lane groups read
+//         one contiguous 128-byte line; 16*g + 64*ks at 256, so they read 64
+//         contiguous bytes of the row's two lines per load instruction.
 //   PV  : O = P' * V.  A = P' codes (row = head-term, k = slots of page g),
 //         B = V codes read dim-major from the page (column = dim).
 //   Online softmax in the log2 domain; cross-page reductions are two
@@ -58,6 +60,18 @@ struct TileRegs {
 };
 
 // Parts of a tile load: K codes and both scales (part 1), V codes (part 2).
+// First head dim of lane group g's 16-dim chunk at k step ks (K codes and Q
+// terms alike). At head_dim 256, (D/4)*g + 16*ks would spread a load
+// instruction's four 16-byte pieces of a row over both of its lines (32
+// lines per instruction, 32 bytes used of each); 16*g + 64*ks reads 64
+// contiguous bytes (16 lines) and took the gemma-shaped decode from 68.2 to
+// 52.3 us. At 128 the same change measured slower (50.2 -> 52.7 us: the
+// partner chunk held for RoPE spills registers).
+template <int D>
+__device__ __forceinline__ constexpr int kdim0(int g, int ks) {
+  return D > 128 ? 16 * g + 64 * ks : (D / 4) * g + 16 * ks;
+}
+
 template <int D, int PART = 3>
 __device__ __forceinline__ void load_tile(TileRegs<D>& T, const uint8_t* __restrict__ pool,
                                           const int* sm_pg, int tile, int num_pages, int kvh,
@@ -74,7 +88,7 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& T, const uint8_t* __restr
 #pragma unroll
       for (int ks = 0; ks < TileRegs<D>::KS; ++ks)
         T.ka[blk][ks] = __builtin_nontemporal_load(
-            (const v4i*)(blk_k + (size_t)(4 * blk + (r & 3)) * D + (D / 4) * g + 16 * ks));
+            (const v4i*)(blk_k + (size_t)(4 * blk + (r & 3)) * D + kdim0<D>(g, ks)));
   }
   if constexpr ((PART & 2) != 0) {
 #pragma unroll
@@ -262,7 +276,7 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   const size_t qbase = ((size_t)b * Hq + kvh * G + (live ? h : 0)) * D;
   float xq[KS][16];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) load16(p.q, qbase + (D / 4) * g + 16 * ks, p.q_dtype, xq[ks]);
+  for (int ks = 0; ks < KS; ++ks) load16(p.q, qbase + kdim0<D>(g, ks), p.q_dtype, xq[ks]);
   const int t_begin = origin + split * p.split_tokens;
   const int t_end = min(L, t_begin + p.split_tokens);
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
@@ -282,7 +296,7 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
     const float* sr = p.sin_cache + (size_t)(L - 1) * HALF;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const int c0 = (D / 4) * g + 16 * ks;
+      const int c0 = kdim0<D>(g, ks);
       const int base = p.interleaved ? (c0 >> 1) : (c0 < HALF ? c0 : c0 - HALF);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -348,7 +362,7 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
     float amax = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const int c0 = (D / 4) * g + 16 * ks;  // first dim of this lane's chunk
+      const int c0 = kdim0<D>(g, ks);  // first dim of this lane's chunk
       float x[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) x[i] = xq[ks][i];
@@ -369,12 +383,18 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          // split-half partner d +- D/2: the same element of lane g ^ 2 (32
-          // lanes away); permlane32_swap(x, x) gives [0] = lanes 0-31's x,
-          // [1] = lanes 32-63's x on both halves
-          auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i]), __float_as_uint(x[i]),
-                                                     false, false);
-          const float half_partner = __uint_as_float(c0 < HALF ? sw[1] : sw[0]);
+          // split-half partner d +- D/2: up to head_dim 128 the same element
+          // of lane g ^ 2 (32 lanes away; permlane32_swap(x, x) gives [0] =
+          // lanes 0-31's x, [1] = lanes 32-63's x on both halves); at 256 the
+          // same lane's chunk ks ^ 2
+          float half_partner;
+          if constexpr (BIG) {
+            half_partner = xq[ks ^ 2][i];
+          } else {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i]),
+                                                       __float_as_uint(x[i]), false, false);
+            half_partner = __uint_as_float(c0 < HALF ? sw[1] : sw[0]);
+          }
           const float partner = p.interleaved ? x[i ^ 1] : half_partner;
           const bool first = p.interleaved ? (i & 1) == 0 : c0 < HALF;
           y[i] = rope_elem(cc[i], ss[i], x[i], partner, first);
