@@ -157,10 +157,6 @@ int sai_or_gqa_cached_window(const float* query, int b, int sq, int num_heads, i
  * pattern u in [lo, hi) (hi <= 2^32). Returns the number of mismatches. */
 uint64_t sai_or_check_rhe_vs_rint(uint64_t lo, uint64_t hi);
 
-#ifdef __cplusplus
-}
-#endif
-
 int sai_or_tq_attention_logits(const float* q, int G, int dim, int bits, int qjl,
                                const int8_t* signs, int rows, const uint8_t* k_codes,
                                const float* k_scale, const float* k_zero, const uint64_t* k_signs,
@@ -175,5 +171,9 @@ void sai_or_lr_reconstruct(const float* u_s, const float* vt, int rows, int cols
                            float* out);
 void sai_or_lr_update(float* u_s, float* vt, int* rows, int cols, int* rank, int* write_counter,
                       const float* new_row);
+
+#ifdef __cplusplus
+}
+#endif
 
 #endif

@@ -87,7 +87,7 @@ def build_host() -> str:
     _run([CXX, "-std=c++17", "-O2", "-fPIC", "-shared", "-ffp-contract=off", "-Wall", "-Wextra",
           "-D__HIP_PLATFORM_AMD__", "-I", INCLUDE, "-I", "/opt/rocm/include",
           os.path.join(HERE, "host", "gqa_host.cpp"), os.path.join(HERE, "host", "gqa_session.cpp"),
-          "-o", tmp,
+          os.path.join(HERE, "host", "kv_compression.cpp"), "-o", tmp,
           "-L", HERE, "-lsai_hip", "-L", "/opt/rocm/lib", "-lamdhip64",
           "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib"])
     os.replace(tmp, HOST_LIB)

@@ -23,6 +23,7 @@
 #include "../../oracle/sai_oracle.h"
 #include "../../smallaios_amd/host/gqa_host.hpp"
 #include "../../smallaios_amd/host/gqa_session.hpp"
+#include "../../smallaios_amd/host/kv_compression.hpp"
 
 using namespace sai::rocm;
 
@@ -1198,6 +1199,107 @@ void gpu_session_gemma_graph() { gemma_graph_session(8, 2, 128, 10000.0, 61); }
 // over 4 kv heads, head_dim 256, rope_theta 1e6.
 void gpu_session_gemma3_head256() { gemma_graph_session(8, 4, 256, 1000000.0, 62); }
 
+// GpuCompressedKvCache (CompressedKVCache, kv_compression.rs:738-963) with the
+// low-rank K on: two sequences x two kv heads, head_dim 128, 4-bit + QJL, a
+// 520-row pass (the low-rank state re-decomposes at row 513) and a fused
+// one-row step. read_v is bit-exact with the oracle's encode + decode,
+// read_k with the oracle's low-rank reconstruction, the attention within
+// 2e-3 + 1e-2 relative of the oracle's estimator; errors map to OpError.
+void gpu_compressed_kv_cache() {
+  const int B = 2, H = 2, D = 128, S = 520, Hq = 4, G = Hq / H, BITS = 4;
+  KVCacheConfig cfg;
+  cfg.kv_quant_bits = BITS;
+  cfg.num_kv_heads = H;
+  cfg.head_dim = D;
+  cfg.kv_lowrank_k = 4;
+  GpuCompressedKvCache c = must(GpuCompressedKvCache::create(runtime(), cfg, B, 600), "create");
+  std::mt19937 rng(71);
+  std::normal_distribution<float> nd;
+  auto randv = [&](size_t n) {
+    std::vector<float> v(n);
+    for (float& x : v) x = nd(rng);
+    return v;
+  };
+  const std::vector<float> k = randv((size_t)B * S * H * D), v = randv(k.size());
+  must(c.write_kv(0, must(DeviceTensor::from_f32(k, shp({B, S, H * D})), "k"),
+                  must(DeviceTensor::from_f32(v, shp({B, S, H * D})), "v")), "write_kv");
+  must(c.advance(), "advance");
+  const std::vector<float> q = randv((size_t)B * Hq * D), k1 = randv((size_t)B * H * D),
+                           v1 = randv(k1.size());
+  DeviceTensor out = must(c.write_attend(0, must(DeviceTensor::from_f32(q, shp({B, 1, Hq * D})), "q"),
+                                         must(DeviceTensor::from_f32(k1, shp({B, 1, H * D})), "k1"),
+                                         must(DeviceTensor::from_f32(v1, shp({B, 1, H * D})), "v1"),
+                                         Hq), "write_attend");
+  must(c.advance(), "advance 2");
+  REQUIRE(c.seq_len(0) == S + 1 && c.seq_len(1) == S + 1, "seq_len %zu", c.seq_len(0));
+  const std::vector<float> got = must(out.to_host_f32(), "out");
+  const int R = S + 1, cb = D * BITS / 8, W = D / 64;
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < H; ++h) {
+      std::vector<int8_t> sg(D);
+      sai_or_tq_signs(sai_or_tq_head_seed(cfg.seed, 0, H, h), D, sg.data());
+      std::vector<float> kr((size_t)R * D), vr((size_t)R * D);
+      for (int t = 0; t < R; ++t)
+        for (int d = 0; d < D; ++d) {
+          const size_t src = t < S ? (((size_t)b * S + t) * H + h) * D + d : ((size_t)b * H + h) * D + d;
+          kr[(size_t)t * D + d] = t < S ? k[src] : k1[src];
+          vr[(size_t)t * D + d] = t < S ? v[src] : v1[src];
+        }
+      std::vector<uint8_t> kc((size_t)R * cb), vc((size_t)R * cb);
+      std::vector<float> ks(R), kz(R), kcm(R), vs(R), vz(R), vcm(R);
+      std::vector<uint64_t> ksb((size_t)R * W), vsb((size_t)R * W);
+      for (int t = 0; t < R; ++t) {
+        REQUIRE(sai_or_tq_write_row(&kr[(size_t)t * D], D, BITS, sg.data(), 1, &kc[(size_t)t * cb],
+                                    &ks[t], &kz[t], &ksb[(size_t)t * W], &kcm[t]) == 0, "k row");
+        REQUIRE(sai_or_tq_write_row(&vr[(size_t)t * D], D, BITS, sg.data(), 1, &vc[(size_t)t * cb],
+                                    &vs[t], &vz[t], &vsb[(size_t)t * W], &vcm[t]) == 0, "v row");
+      }
+      // read_v: rows 500 .. 520, bit for bit
+      const std::vector<float> gv = must(c.read_v(0, b, h, 500, R - 500), "read_v");
+      std::vector<float> want(D);
+      for (int t = 500; t < R; ++t) {
+        sai_or_tq_decode(&vc[(size_t)t * cb], D, BITS, vs[t], vz[t], sg.data(), want.data());
+        REQUIRE(std::memcmp(&gv[(size_t)(t - 500) * D], want.data(), D * 4) == 0, "read_v row %d", t);
+      }
+      // read_k: the low-rank reconstruction, bit for bit
+      std::vector<float> us(R), vt(D);
+      int rows = 1, rank = sai_or_lr_decompose(kr.data(), 1, D, 4, us.data(), vt.data()), wc = 0;
+      REQUIRE(rank == 1, "rank %d", rank);
+      for (int t = 1; t < R; ++t)
+        sai_or_lr_update(us.data(), vt.data(), &rows, D, &rank, &wc, &kr[(size_t)t * D]);
+      std::vector<float> rec((size_t)R * D);
+      sai_or_lr_reconstruct(us.data(), vt.data(), R, D, rank, rec.data());
+      const std::vector<float> gk = must(c.read_k(0, b, h, 500, R - 500), "read_k");
+      REQUIRE(std::memcmp(gk.data(), &rec[(size_t)500 * D], gk.size() * 4) == 0, "read_k b%d h%d", b, h);
+      // the fused step's attention for this kv head's query heads
+      std::vector<float> wo((size_t)G * D);
+      REQUIRE(sai_or_tq_attend(&q[((size_t)b * Hq + h * G) * D], G, D, BITS, 1, sg.data(), R,
+                               kc.data(), ks.data(), kz.data(), ksb.data(), kcm.data(), vc.data(),
+                               vs.data(), vz.data(), 1.0f / std::sqrt((float)D), wo.data()) == 0,
+              "oracle attend");
+      for (int i = 0; i < G * D; ++i) {
+        const float g = got[((size_t)b * Hq + h * G) * D + i], w = wo[i];
+        REQUIRE(std::fabs(g - w) <= 2e-3f + 1e-2f * std::fabs(w), "attend b%d h%d i%d %g vs %g", b,
+                h, i, g, w);
+      }
+    }
+  // reference accounting: blocks + residuals per row, plus the low-rank state
+  const size_t per_row = 2 * (cb + 25) + 2 * (W * 8 + 12);
+  const size_t want_bytes = (size_t)B * R * H * per_row + (size_t)B * H * (R * 4 + D * 4 + 32);
+  REQUIRE(c.memory_bytes() == want_bytes, "memory_bytes %zu vs %zu", c.memory_bytes(), want_bytes);
+  KVCacheConfig bad = cfg;
+  bad.kv_quant_bits = 5;
+  OpError e = must_fail(GpuCompressedKvCache::create(runtime(), bad, 1, 8), "bits 5");
+  REQUIRE(e.kind == OpError::Kind::InvalidAttribute, "kind");
+  bad = cfg;
+  bad.head_dim = 96;
+  e = must_fail(GpuCompressedKvCache::create(runtime(), bad, 1, 8), "head_dim 96");
+  REQUIRE(e.kind == OpError::Kind::UnsupportedOp, "kind");
+  e = must_fail(c.write_kv(0, must(DeviceTensor::from_f32(k1, shp({B, H * D})), "k2"),
+                           must(DeviceTensor::from_f32(v1, shp({B, H * D})), "v2")), "rank-2 K");
+  REQUIRE(e.kind == OpError::Kind::ShapeMismatch, "kind");
+}
+
 // test_kv_cache_sliding_window (tests/test_cuda.rs:1275-1334): a global layer
 // and a sliding-window layer of 4; after 6 tokens the global view holds 6,
 // the local view the last 4 (positions 2..5), read back by value.
@@ -1238,6 +1340,7 @@ int main(int argc, char** argv) {
     std::function<void()> fn;
   };
   const std::vector<Case> cases = {
+      {"gpu_compressed_kv_cache", true, gpu_compressed_kv_cache},
       {"cpu_attrs", false, cpu_attrs},
       {"cpu_validate", false, cpu_validate},
       {"cpu_errors_and_types", false, cpu_errors_and_types},

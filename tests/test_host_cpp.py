@@ -12,7 +12,9 @@ checked against the oracle (outputs within 2e-3 abs + 1e-2 rel, cache contents
 bit-exact), the RotaryEmbedding op and dispatcher (bit-exact), the CPU
 attention ops with explicit past/present (present bit-exact), and
 Gemma-shaped graphs run through GpuSession (gqa_session.hpp), one of them at
-Gemma 3 4B's head_dim 256.
+Gemma 3 4B's head_dim 256, and the TurboQuant cache's C++ mirror
+(kv_compression.hpp) against the oracle (read_v and the low-rank read_k
+bit-exact, attention within tolerance).
 """
 import os
 import subprocess
