@@ -329,7 +329,7 @@ def main():
     if args.waves:
         rt.set_decode_waves(args.waves)
     if args.merge != "auto":
-        rt.set_decode_merge(args.merge == "inkernel")
+        rt.set_decode_merge(1 if args.merge == "inkernel" else 0)
     b, hq, hkv, d = w["batch"], w["hq"], w.get("hkv", 0), w["d"]
     qdt = torch.bfloat16 if w.get("q_dtype", "bf16") == "bf16" else torch.float32
     stream = torch.cuda.Stream()  # default priority

@@ -134,7 +134,11 @@ sai_status sai_kvcache_read(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, int
                             int32_t kv_head, int32_t t0, int32_t n_tokens, void* k_codes,
                             void* v_codes, void* k_params, void* v_params);
 /* Raw pool of one layer (device pointer and size in bytes) and the bytes of
- * one (page, kv head) block; the block layout is documented in DESIGN.md. */
+ * one (page, kv head) block. Block (page p, kv head h) starts at
+ * (h * num_pages + p) * block_bytes; INT8 block: K codes [16][D] int8, V codes
+ * [D][16] int8, K scales [16] f32, V scales [16] f32 (32*D + 128 bytes); INT4
+ * block: K codes [16][D/2], V codes [D][8] (LSB-first along slots), K then V
+ * (scale, zero) binary16 [16][D/32][2] (20*D bytes). */
 sai_status sai_kvcache_pool(const sai_kvcache* cache, int32_t layer, void** dev_ptr,
                             size_t* bytes, size_t* block_bytes);
 
@@ -144,9 +148,10 @@ sai_status sai_kvcache_pool(const sai_kvcache* cache, int32_t layer, void** dev_
  * QuantizeLinear of the KV scheme. k, v: device [batch, s_new, Hkv*D] of
  * `dtype` (F32 or BF16), pre-RoPE K. Token s of sequence b goes to position
  * seq_len[b] + s; RoPE (when do_rotary) uses that position in cos/sin
- * ([cache_rows, D/2] f32, device). Leaves s_new tokens pending; the same
- * s_new must be used for every layer of a forward pass, and appending a layer
- * twice before advance rewrites the same slots.
+ * ([cache_rows, D/2] f32, device, 16-byte aligned; the same tables and
+ * alignment for every attention entry point below). Leaves s_new tokens
+ * pending; the same s_new must be used for every layer of a forward pass, and
+ * appending a layer twice before advance rewrites the same slots.
  * Errors: SHAPE_MISMATCH (dims, unmapped page, position >= cache_rows),
  * OVERFLOW (past the page table), UNSUPPORTED (dtype/head_dim). */
 sai_status sai_kv_append(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* k,
@@ -400,17 +405,20 @@ int32_t sai_set_tq_split(sai_ctx* ctx, int32_t rows);
 /* Waves per decode workgroup: 4 or 8, or 0 = automatic (4 for an int8
  * cache, 8 for int4). Returns the previous value. */
 int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves);
-/* Split merge of the decode kernel: 0 = separate combine kernel (default),
- * 1 = the last workgroup of a (sequence, kv head) merges in-kernel (int8; every
- * wave then releases its partials with an agent-scope fence, which writes back
- * its XCD's L2, so this is slower at the Llama layer shape). Returns the
- * previous value. */
+/* Split merge of the decode kernel: 0 = separate combine kernel, 1 = the
+ * last workgroup of a (sequence, kv head) merges in-kernel (int8 cache; the
+ * partials are handed over with agent-scope stores and loads, one ticket
+ * counter per (sequence, kv head)), 2 = automatic (the default: in-kernel
+ * when every sequence of the launch has the same split count, else the
+ * combine kernel; int4 always uses the combine kernel). Returns the previous
+ * value; other values are ignored. */
 int32_t sai_set_decode_merge(sai_ctx* ctx, int32_t in_kernel);
 /* Number of workgroups and split size of the last decode launch on ctx. */
 sai_status sai_last_decode_shape(const sai_ctx* ctx, int32_t* workgroups, int32_t* split_tokens);
 /* Kernel timing of the decode step: with slots > 0, every sai_gqa_decode /
  * sai_gqa_with_cache call records two HIP events on its stream around the
- * decode kernel alone (not the split merge that follows it), in a ring of
+ * decode kernel alone (not a combine kernel that follows it; an in-kernel
+ * merge is part of the decode kernel), in a ring of
  * `slots` event pairs (at most 4096), so back-to-back calls are timed without
  * synchronizing between them. 0 turns timing off. Returns the previous slot
  * count. */

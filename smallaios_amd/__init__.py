@@ -235,8 +235,9 @@ class Runtime:
     def set_decode_waves(self, waves: int) -> int:
         return int(self._L.sai_set_decode_waves(self.handle, waves))
 
-    def set_decode_merge(self, in_kernel: bool) -> int:
-        return int(self._L.sai_set_decode_merge(self.handle, int(in_kernel)))
+    def set_decode_merge(self, mode) -> int:
+        """0 / False: combine kernel, 1 / True: in-kernel merge, 2: automatic."""
+        return int(self._L.sai_set_decode_merge(self.handle, int(mode)))
 
     def last_decode_shape(self):
         wg, sp = C.c_int32(), C.c_int32()

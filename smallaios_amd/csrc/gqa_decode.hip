@@ -101,36 +101,61 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& T, const uint8_t* __restr
   }
 }
 
+// Heads of a group are taken four at a time (a "pass"): column j = 4*hq + t
+// of the QK product is term t of head 4*pass + hq, so the four lanes of a
+// DPP quad hold the terms of one head.
+template <int G>
+struct Passes {
+  static constexpr int N = G > 4 ? 2 : 1;
+};
+
 template <int D, int G>
 struct WaveState {
-  float m_run, l_run;   // per head (lanes of head-term j), log2 domain
-  float acc[D / 16][2]; // lane (dim 16*jb + r, group g): heads 2g, 2g+1
+  static constexpr int NP = Passes<G>::N;
+  float m_run[NP], l_run[NP];  // this lane's head of each pass, log2 domain
+  float acc[NP][D / 16];       // lane (dim 16*jb + r, group g): head 4*pass + g
 };
 
 struct NoHook {
   __device__ void operator()() const {}
 };
 
+// sum over the four lanes of a DPP quad; every lane gets the same bits
+// (x0 + x1) + (x2 + x3), since f32 addition commutes
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+  return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));
+}
+
+// One 64-token tile. qB[pass] holds this lane's query term (t = r & 3 of head
+// 4*pass + (r >> 2); t = 3 is zero) and qw[pass] its weight, so that
+//   score(t, h) = s_k[t] * sum over the quad of qw * <k_t, term>.
 // after_qk runs once the tile's K codes and scales are consumed (the QK
 // MFMAs issued, the scales in LDS), after_pv once its V codes are: a caller
 // with one tile buffer loads the next tile's K and V there.
 template <int D, int G, class H1 = NoHook, class H2 = NoHook>
 __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, G>& st,
-                                             const v4i (&qB)[D / 64], float q_own, float q_oth,
-                                             int tok0, int t_lo, int t_end, bool is_hi, bool live,
-                                             int g, float* sm_sc, H1 after_qk = H1{},
+                                             const v4i (&qB)[Passes<G>::N][D / 64],
+                                             const float (&qw)[Passes<G>::N],
+                                             int tok0, int t_lo, int t_end, int r, int g,
+                                             float* sm_sc, H1 after_qk = H1{},
                                              H2 after_pv = H2{}) {
   constexpr int KS = D / 64;
   constexpr int JB = D / 16;
-  // QK^T on the matrix cores
+  constexpr int NP = Passes<G>::N;
+  // QK^T of a pass on the matrix cores (the first pass's before the scales
+  // are exchanged, the second's when its turn comes: one set of results live)
   v4i cs[4];
+  auto qk = [&](int ps) {
 #pragma unroll
-  for (int blk = 0; blk < 4; ++blk) {
-    cs[blk] = v4i{0, 0, 0, 0};
+    for (int blk = 0; blk < 4; ++blk) {
+      cs[blk] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      cs[blk] = __builtin_amdgcn_mfma_i32_16x16x64_i8(T.ka[blk][ks], qB[ks], cs[blk], 0, 0, 0);
-  }
+      for (int ks = 0; ks < KS; ++ks)
+        cs[blk] = __builtin_amdgcn_mfma_i32_16x16x64_i8(T.ka[blk][ks], qB[ps][ks], cs[blk], 0, 0, 0);
+    }
+  };
+  qk(0);
   // scales of page g, slots 0..15 (this wave's LDS slot; lane 16g + r wrote slot r)
   const int lane = threadIdx.x & 63;
   sm_sc[lane] = T.sk;
@@ -151,90 +176,93 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, 
   const int nlow = t_lo - tok0;
   const bool full =
       __builtin_amdgcn_readfirstlane(t_end - (tok0 - 16 * g) >= 64 && tok0 - 16 * g >= t_lo);
-  float s[16];
-#pragma unroll
-  for (int blk = 0; blk < 4; ++blk)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int slot = 4 * blk + e;
-      const int own = cs[blk][e];
-      const int oth = swap_pair(own);
-      s[slot] = (q_own * (float)own + q_oth * (float)oth) * skv[slot];
-    }
   if (!full) {
 #pragma unroll
+    for (int i = 0; i < 16; ++i) svv[i] = i < nvalid && i >= nlow ? svv[i] : 0.0f;
+  }
+  const int t = r & 3;
+#pragma unroll
+  for (int ps = 0; ps < NP; ++ps) {
+    const bool live = 4 * ps + (r >> 2) < G;
+    if (ps > 0) qk(ps);
+    float s[16];
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int slot = 4 * blk + e;
+        s[slot] = quad_sum(qw[ps] * (float)cs[blk][e]) * skv[slot];
+      }
+    if (!full) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] = i < nvalid && i >= nlow ? s[i] : -INFINITY;
+    }
+    float mt = s[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mt = fmaxf(mt, s[i]);
+    mt = xgroup_max(mt);
+    const float m_new = fmaxf(st.m_run[ps], mt);
+    const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+    const float alpha = fast_exp2(st.m_run[ps] - m_use);
+    float psum = 0.0f, pmax = 0.0f;
+    float pv[16];
+#pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const bool vis = i < nvalid && i >= nlow;
-      s[i] = vis ? s[i] : -INFINITY;
-      svv[i] = vis ? svv[i] : 0.0f;
+      const float pe = fast_exp2(s[i] - m_use);
+      psum += pe;
+      pv[i] = pe * svv[i];
+      pmax = fmaxf(pmax, pv[i]);
     }
-  }
-  float mt = s[0];
-#pragma unroll
-  for (int i = 1; i < 16; ++i) mt = fmaxf(mt, s[i]);
-  mt = xgroup_max(mt);
-  const float m_new = fmaxf(st.m_run, mt);
-  const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-  const float alpha = fast_exp2(st.m_run - m_use);
-  float psum = 0.0f, pmax = 0.0f;
-  float pv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float pe = fast_exp2(s[i] - m_use);
-    psum += pe;
-    pv[i] = pe * svv[i];
-    pmax = fmaxf(pmax, pv[i]);
-  }
-  psum = xgroup_sum(psum);
-  pmax = xgroup_max(pmax);
-  st.l_run = st.l_run * alpha + psum;
-  st.m_run = m_new;
+    psum = xgroup_sum(psum);
+    pmax = xgroup_max(pmax);
+    st.l_run[ps] = st.l_run[ps] * alpha + psum;
+    st.m_run[ps] = m_new;
 
-  // P' -> int8 (hi, lo) terms; this lane's term is its row of the PV A operand
-  const float sp = pmax * (1.0f / 127.0f);
-  const float inv_sp = pmax > 0.0f ? 127.0f / pmax : 0.0f;
-  int pc[16];
+    // P' -> int8 (hi, lo) terms: term t = 0 / 1 of the quad is its row of
+    // the PV A operand (rows 4*hq + 2, 4*hq + 3 are zero)
+    const float sp = pmax * (1.0f / 127.0f);
+    const float inv_sp = pmax > 0.0f ? 127.0f / pmax : 0.0f;
+    int pc[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float hi = rintf(pv[i] * inv_sp);
-    const float lo = fminf(fmaxf(rintf((pv[i] - hi * sp) * (254.0f * inv_sp)), -127.0f), 127.0f);
-    pc[i] = live ? (int)(is_hi ? hi : lo) : 0;
-  }
-  v4i pa;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) pa[w] = pack4(pc[4 * w], pc[4 * w + 1], pc[4 * w + 2], pc[4 * w + 3]);
-
-  // rescale factors of the heads this lane accumulates (2g, 2g+1); head h's
-  // softmax state sits in lanes with head-term 2h (read from lane 2h)
-  float a0 = 0.0f, a1 = 0.0f, s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-  for (int h2 = 0; h2 < (G + 1) / 2; ++h2) {
-    const int ah0 = __builtin_amdgcn_readlane(__float_as_int(alpha), 4 * h2);
-    const int sh0 = __builtin_amdgcn_readlane(__float_as_int(sp), 4 * h2);
-    const int ah1 = G > 2 * h2 + 1 ? __builtin_amdgcn_readlane(__float_as_int(alpha), 4 * h2 + 2) : 0;
-    const int sh1 = G > 2 * h2 + 1 ? __builtin_amdgcn_readlane(__float_as_int(sp), 4 * h2 + 2) : 0;
-    if (g == h2) {
-      a0 = __int_as_float(ah0);
-      s0 = __int_as_float(sh0);
-      a1 = __int_as_float(ah1);
-      s1 = __int_as_float(sh1);
+    for (int i = 0; i < 16; ++i) {
+      const float hi = rintf(pv[i] * inv_sp);
+      const float lo =
+          fminf(fmaxf(rintf((pv[i] - hi * sp) * (254.0f * inv_sp)), -127.0f), 127.0f);
+      pc[i] = live && t < 2 ? (int)(t == 0 ? hi : lo) : 0;
     }
-  }
-  const float s0l = s0 * (1.0f / 254.0f);
-  const float s1l = s1 * (1.0f / 254.0f);
-
-  // P' V on the matrix cores
+    v4i pa;
 #pragma unroll
-  for (int jb = 0; jb < JB; ++jb) {
-    const v4i co = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, T.vb[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
-    st.acc[jb][0] = st.acc[jb][0] * a0 + ((float)co[0] * s0 + (float)co[1] * s0l);
-    st.acc[jb][1] = st.acc[jb][1] * a1 + ((float)co[2] * s1 + (float)co[3] * s1l);
+    for (int w = 0; w < 4; ++w) pa[w] = pack4(pc[4 * w], pc[4 * w + 1], pc[4 * w + 2], pc[4 * w + 3]);
+
+    // rescale factor and P' scale of the head this lane accumulates
+    // (4*ps + g); head 4*ps + hq's softmax state sits in lanes r = 4*hq + t
+    float a_g = 0.0f, sp_g = 0.0f;
+#pragma unroll
+    for (int hq = 0; hq < 4; ++hq) {
+      if (4 * ps + hq >= G) break;
+      const float ah = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), 4 * hq));
+      const float sh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sp), 4 * hq));
+      a_g = g == hq ? ah : a_g;
+      sp_g = g == hq ? sh : sp_g;
+    }
+    const float sp_gl = sp_g * (1.0f / 254.0f);
+
+    // P' V on the matrix cores: output rows 4g .. 4g + 3 are head 4*ps + g's terms
+#pragma unroll
+    for (int jb = 0; jb < JB; ++jb) {
+      const v4i co = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, T.vb[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+      st.acc[ps][jb] = st.acc[ps][jb] * a_g + ((float)co[0] * sp_g + (float)co[1] * sp_gl);
+    }
   }
   after_pv();
 }
 
+// Two waves per SIMD, except group 8 at head_dim 128: its two passes of query
+// terms and accumulators do not fit beside two tile buffers in 256 registers,
+// so it runs one wave per SIMD with the whole register file.
 template <int D, int G, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_decode_int8_kernel(
+    DecodeParams p) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static_assert(G >= 1 && G <= 8, "group");
   constexpr int KS = D / 64;
@@ -252,31 +280,28 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   decode_work_item(p, work, lane, b, split, nsplit, split_base);
   if (b < 0 || b >= p.batch) return;  // uniform over the workgroup
 
-  // page ids of the split, loaded before the length is known (the page-table
-  // row has max_pages entries; the split's range is clamped to it)
-  const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
-  // length first; then the page ids of the split and the query, in flight
-  // across the barrier
-  const int L = p.seq_lens[b] + p.pending;
-  // sliding window: keys [k_lo, L) visible, splits from the tile holding k_lo
-  const int k_lo = window_first_key(L, p.window);
-  const int origin = (k_lo / 64) * 64;
-  const int first_page = origin / kPageTokens + split * (p.split_tokens / kPageTokens);
+  // length and the split's page ids (the page-table row has max_pages
+  // entries; the split's range is clamped to it), then the query, all in
+  // flight across the barrier. Sliding window: keys [k_lo, L) visible, splits
+  // from the tile holding k_lo.
   __shared__ int sm_pg[kMaxSplitPages];
-  const int split_pages = p.split_tokens / kPageTokens;
-  for (int i = threadIdx.x; i < split_pages; i += 64 * NW)
-    sm_pg[i] = pt[min(first_page + i, p.max_pages - 1)];
+  int L, k_lo, first_page;
+  stage_split_pages<64 * NW>(p, b, split, sm_pg, L, k_lo, first_page);
+  const int origin = (k_lo / 64) * 64;
 
   constexpr int HALF = D / 2;
-  const int hterm = r;  // column j of the QK product
-  const int h = hterm >> 1;
-  const bool is_hi = (hterm & 1) == 0;
-  const bool live = h < G;
+  constexpr int NP = Passes<G>::N;
+  // column r = 4*hq + t of the QK product: term t of head 4*pass + hq
+  const int tq = r & 3;
   const int Hq = p.kv_heads * G;
-  const size_t qbase = ((size_t)b * Hq + kvh * G + (live ? h : 0)) * D;
-  float xq[KS][16];
+  float xq[NP][KS][16];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) load16(p.q, qbase + kdim0<D>(g, ks), p.q_dtype, xq[ks]);
+  for (int ps = 0; ps < NP; ++ps) {
+    const int h = 4 * ps + (r >> 2);
+    const size_t qbase = ((size_t)b * Hq + kvh * G + (h < G ? h : 0)) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) load16(p.q, qbase + kdim0<D>(g, ks), p.q_dtype, xq[ps][ks]);
+  }
   const int t_begin = origin + split * p.split_tokens;
   const int t_end = min(L, t_begin + p.split_tokens);
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
@@ -290,21 +315,12 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   // chunk in the RoPE loop and its first tile after the query: the registers
   // of both would not fit)
   constexpr bool BIG = D > 128;
-  float cq[BIG ? 1 : KS][16], sq[BIG ? 1 : KS][16];
+  float4 cq[BIG ? 1 : KS][4], sq[BIG ? 1 : KS][4];
   if (!BIG && p.do_rotary) {
     const float* cr = p.cos_cache + (size_t)(L - 1) * HALF;
     const float* sr = p.sin_cache + (size_t)(L - 1) * HALF;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int c0 = kdim0<D>(g, ks);
-      const int base = p.interleaved ? (c0 >> 1) : (c0 < HALF ? c0 : c0 - HALF);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int idx = base + (p.interleaved ? (i >> 1) : i);
-        cq[ks][i] = cr[idx];
-        sq[ks][i] = sr[idx];
-      }
-    }
+    for (int ks = 0; ks < KS; ++ks) rope_load16<D>(cr, sr, kdim0<D>(g, ks), p.interleaved, cq[ks], sq[ks]);
   }
 
   // ---- fused append by the last tile's owner: before its first load if that
@@ -354,10 +370,16 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   }
   if (appender && my_tiles > 1) append();
 
-  // ---- Q: RoPE at position L-1, split into int8 (hi, lo) terms -------------
-  v4i qB[KS];
-  float sq_hi;
-  {
+  // ---- Q: RoPE at position L-1, split into three int8 terms ------------------
+  // y = sq * (hi + mid / 254 + lo / 254^2), sq = max|y| / 127 over the head:
+  // ~24 significant bits, about f32's own. (Two terms, ~16 bits, put keys
+  // with x20 outlier channels at 0.96 of the output tolerance: their score
+  // terms reach the hundreds.) Each lane packs its own term t; t = 3 is zero.
+  v4i qB[NP][KS];
+  float qw[NP];
+#pragma unroll
+  for (int ps = 0; ps < NP; ++ps) {
+    const bool live = 4 * ps + (r >> 2) < G;
     float qv[KS][16];
     float amax = 0.0f;
 #pragma unroll
@@ -365,21 +387,17 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
       const int c0 = kdim0<D>(g, ks);  // first dim of this lane's chunk
       float x[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x[i] = xq[ks][i];
+      for (int i = 0; i < 16; ++i) x[i] = xq[ps][ks][i];
       if (p.do_rotary) {
         float y[16];
         float cc[16], ss[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          if constexpr (BIG) {
-            const int base = p.interleaved ? (c0 >> 1) : (c0 < HALF ? c0 : c0 - HALF);
-            const int idx = base + (p.interleaved ? (i >> 1) : i);
-            cc[i] = p.cos_cache[(size_t)(L - 1) * HALF + idx];
-            ss[i] = p.sin_cache[(size_t)(L - 1) * HALF + idx];
-          } else {
-            cc[i] = cq[ks][i];
-            ss[i] = sq[ks][i];
-          }
+        if constexpr (BIG) {
+          float4 lc[4], ls[4];
+          rope_load16<D>(p.cos_cache + (size_t)(L - 1) * HALF, p.sin_cache + (size_t)(L - 1) * HALF,
+                         c0, p.interleaved, lc, ls);
+          rope_pick_all<0>(lc, ls, p.interleaved != 0, cc, ss);
+        } else {
+          rope_pick_all<0>(cq[ks], sq[ks], p.interleaved != 0, cc, ss);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -389,7 +407,7 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
           // same lane's chunk ks ^ 2
           float half_partner;
           if constexpr (BIG) {
-            half_partner = xq[ks ^ 2][i];
+            half_partner = xq[ps][ks ^ 2][i];
           } else {
             auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i]),
                                                        __float_as_uint(x[i]), false, false);
@@ -409,35 +427,41 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
       }
     }
     amax = xgroup_max(amax);
-    sq_hi = amax > 0.0f ? amax * (1.0f / 127.0f) : 1.0f;
-    const float inv_sq = 1.0f / sq_hi;
+    const float s0 = amax > 0.0f ? amax * (1.0f / 127.0f) : 1.0f;
+    const float inv = 1.0f / s0;
+    const float s1 = s0 * (1.0f / 254.0f);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       int c[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float y = qv[ks][i];
-        const float hi = fminf(fmaxf(rintf(y * inv_sq), -127.0f), 127.0f);
-        const float lo = fminf(fmaxf(rintf((y - hi * sq_hi) * (254.0f * inv_sq)), -127.0f), 127.0f);
-        c[i] = live ? (int)(is_hi ? hi : lo) : 0;
+        const float hi = fminf(fmaxf(rintf(y * inv), -127.0f), 127.0f);
+        const float r1 = y - hi * s0;
+        const float mid = fminf(fmaxf(rintf(r1 * (254.0f * inv)), -127.0f), 127.0f);
+        const float r2 = r1 - mid * s1;
+        const float lo = fminf(fmaxf(rintf(r2 * (64516.0f * inv)), -127.0f), 127.0f);
+        c[i] = live && tq < 3 ? (int)(tq == 0 ? hi : (tq == 1 ? mid : lo)) : 0;
       }
 #pragma unroll
-      for (int w = 0; w < 4; ++w) qB[ks][w] = pack4(c[4 * w], c[4 * w + 1], c[4 * w + 2], c[4 * w + 3]);
+      for (int w = 0; w < 4; ++w)
+        qB[ps][ks][w] = pack4(c[4 * w], c[4 * w + 1], c[4 * w + 2], c[4 * w + 3]);
     }
+    // the softmax scale (log2 domain) rides on the term weights
+    const float w0 = s0 * p.scale_log2;
+    qw[ps] = tq == 0 ? w0 : (tq == 1 ? w0 * (1.0f / 254.0f) : (tq == 2 ? w0 * (1.0f / 64516.0f) : 0.0f));
   }
-  // the softmax scale (log2 domain) rides on the Q term scales
-  const float sq_hi_s = sq_hi * p.scale_log2;
-  const float sq_lo_s = sq_hi_s * (1.0f / 254.0f);
-  const float q_own = is_hi ? sq_hi_s : sq_lo_s;
-  const float q_oth = is_hi ? sq_lo_s : sq_hi_s;
   __shared__ float sm_sc[NW][128];
 
   // ---- stream the split's tiles, double-buffered --------------------------------
   WaveState<D, G> st;
-  st.m_run = -INFINITY;
-  st.l_run = 0.0f;
 #pragma unroll
-  for (int jb = 0; jb < JB; ++jb) st.acc[jb][0] = st.acc[jb][1] = 0.0f;
+  for (int ps = 0; ps < NP; ++ps) {
+    st.m_run[ps] = -INFINITY;
+    st.l_run[ps] = 0.0f;
+#pragma unroll
+    for (int jb = 0; jb < JB; ++jb) st.acc[ps][jb] = 0.0f;
+  }
 
   // Ping-pong over this wave's tiles wave, wave+NW, ... Every prefetch inside
   // the loop is unconditional (straight-line code), so the compiler's wait
@@ -456,16 +480,16 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   if constexpr (D <= 128) {
     for (; k + 2 < my_tiles; k += 2) {
       ld(TB, k + 1);
-      compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+      compute_tile<D, G>(TA, st, qB, qw, tok0(k), k_lo, t_end, r, g, sm_sc[wave]);
       ld(TA, k + 2);
-      compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+      compute_tile<D, G>(TB, st, qB, qw, tok0(k + 1), k_lo, t_end, r, g, sm_sc[wave]);
     }
     if (k + 1 < my_tiles) {  // two left
       ld(TB, k + 1);
-      compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
-      compute_tile<D, G>(TB, st, qB, q_own, q_oth, tok0(k + 1), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+      compute_tile<D, G>(TA, st, qB, qw, tok0(k), k_lo, t_end, r, g, sm_sc[wave]);
+      compute_tile<D, G>(TB, st, qB, qw, tok0(k + 1), k_lo, t_end, r, g, sm_sc[wave]);
     } else if (k < my_tiles) {  // one left
-      compute_tile<D, G>(TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave]);
+      compute_tile<D, G>(TA, st, qB, qw, tok0(k), k_lo, t_end, r, g, sm_sc[wave]);
     }
   } else {
     // head_dim 256: a tile is ~128 registers, so one buffer, refilled by
@@ -476,7 +500,7 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
     for (; k < my_tiles; ++k) {
       const int kn = wave + min(k + 1, my_tiles - 1) * NW;
       compute_tile<D, G>(
-          TA, st, qB, q_own, q_oth, tok0(k), k_lo, t_end, is_hi, live, g, sm_sc[wave],
+          TA, st, qB, qw, tok0(k), k_lo, t_end, r, g, sm_sc[wave],
           [&]() {
             load_tile<D, 1>(TA, p.pool, sm_pg + tile_off, kn, p.num_pages, kvh, r, g, n_pages_split);
           },
@@ -490,17 +514,18 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   __shared__ float sm_m[NW][G];
   __shared__ float sm_l[NW][G];
   __shared__ float sm_o[NW][G][D];
-  if (g == 0 && is_hi && live) {
-    sm_m[wave][h] = st.m_run;
-    sm_l[wave][h] = st.l_run;
-  }
 #pragma unroll
-  for (int jb = 0; jb < JB; ++jb)
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int hd = 2 * g + hh;
-      if (hd < G) sm_o[wave][hd][16 * jb + r] = st.acc[jb][hh];
+  for (int ps = 0; ps < NP; ++ps) {
+    const int h = 4 * ps + (r >> 2);
+    if (g == 0 && tq == 0 && h < G) {
+      sm_m[wave][h] = st.m_run[ps];
+      sm_l[wave][h] = st.l_run[ps];
     }
+    const int hd = 4 * ps + g;
+#pragma unroll
+    for (int jb = 0; jb < JB; ++jb)
+      if (hd < G) sm_o[wave][hd][16 * jb + r] = st.acc[ps][jb];
+  }
   __syncthreads();
 
   float* part = p.partials + ((size_t)(split_base + split) * p.kv_heads + kvh) * (G * (D + 2));
@@ -528,6 +553,12 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
     mO[k] = O;
     if (nsplit == 1) {
       p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+    } else if (p.merge_in_kernel) {
+      store_partial(part + hd * (D + 2) + 2 + d, O);
+      if (d == 0) {
+        store_partial(part + hd * (D + 2), M);
+        store_partial(part + hd * (D + 2) + 1, Ls);
+      }
     } else {
       part[hd * (D + 2) + 2 + d] = O;
       if (d == 0) {
@@ -547,19 +578,16 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
   }
   if (nsplit == 1) return;
 
-  // ---- in-kernel merge: the last workgroup of (b, kvh) to finish merges -------
-  // Every thread releases its own partial stores at agent scope (the splits
-  // run on different XCDs, whose L2s are not coherent with each other), the
-  // barrier orders those releases before thread 0's counter increment, and
-  // the last workgroup acquires before reading. The counter resets itself.
+  // ---- in-kernel merge: the workgroup with the last ticket of (b, kvh) -------
+  // Its partial stores are agent-scope, so once they have completed (every
+  // wave waits for its own, then the barrier) they are visible to the other
+  // XCDs; thread 0 then takes a ticket. The last workgroup loads the other
+  // splits' partials with agent-scope loads and writes the output.
   __shared__ int sm_last;
-  __threadfence();
+  partials_complete();
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&p.counters[b * p.kv_heads + kvh], 1);
-    sm_last = (prev == nsplit - 1);
-    if (sm_last) __threadfence();
-  }
+  int* counter = &p.counters[b * p.kv_heads + kvh];
+  if (threadIdx.x == 0) sm_last = last_ticket(counter, nsplit);
   __syncthreads();
   if (!sm_last) return;
   const size_t stride = (size_t)p.kv_heads * (G * (D + 2));
@@ -570,31 +598,16 @@ __global__ __launch_bounds__(64 * NW, 2) void gqa_decode_int8_kernel(DecodeParam
     if (G * D % (64 * NW) != 0 && t >= G * D) break;
     const int hd = t / D, d = t % D;
     float M = mM[k], Ls = mL[k], O = mO[k];
-    // the other splits' (m, l, o), up to 16 loads in flight per round
-    for (int s0 = 0; s0 < nsplit; s0 += 16) {
-      float pm[16], pl[16], po[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const float* ps = p0 + (size_t)min(s0 + j, nsplit - 1) * stride + hd * (D + 2);
-        pm[j] = ps[0];
-        pl[j] = ps[1];
-        po[j] = ps[2 + d];
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int sidx = s0 + j;
-        if (sidx >= nsplit || sidx == split || pm[j] == -INFINITY) continue;
-        const float Mn = fmaxf(M, pm[j]);
-        const float fa = fast_exp2(M - Mn);
-        const float fb = fast_exp2(pm[j] - Mn);
-        Ls = Ls * fa + pl[j] * fb;
-        O = O * fa + po[j] * fb;
-        M = Mn;
-      }
-    }
+    const float* ph = p0 + hd * (D + 2);
+    if (nsplit <= 2)
+      merge_partials<2>(ph, stride, d, nsplit, split, M, Ls, O);
+    else if (nsplit <= 4)
+      merge_partials<4>(ph, stride, d, nsplit, split, M, Ls, O);
+    else
+      merge_partials<8>(ph, stride, d, nsplit, split, M, Ls, O);
     p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
   }
-  if (threadIdx.x == 0) atomicExch(&p.counters[b * p.kv_heads + kvh], 0);
+  if (threadIdx.x == 0) reset_ticket(counter);
 }
 
 // Merge of the split partials of one (sequence, kv head): grid (batch, Hkv),
@@ -672,8 +685,12 @@ hipError_t launch_combine_dg(const DecodeParams& p, hipStream_t st) {
 template <int D, int G>
 hipError_t launch_dg(const DecodeParams& p, int work_items, bool combine, hipStream_t st) {
   const dim3 grid(work_items, p.kv_heads);
-  if (p.waves == 8)
-    hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, 8>), grid, dim3(512), 0, st, p);
+  // group 8 at head_dim 128 needs one wave per SIMD (see the kernel), which
+  // an 8-wave workgroup cannot give: always 4 waves there
+  constexpr bool kEightWaves = !(G > 4 && D == 128);
+  if (kEightWaves && p.waves == 8)
+    hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, kEightWaves ? 8 : 4>), grid,
+                       dim3(kEightWaves ? 512 : 256), 0, st, p);
   else
     hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, 4>), grid, dim3(256), 0, st, p);
   hipError_t e = hipGetLastError();

@@ -264,16 +264,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   // length first; then the page ids of the split; then the query and the
   // cos / sin of position L-1, all in flight across the barrier and ahead
   // of the first tile
-  const int L = p.seq_lens[b] + p.pending;
-  const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
+  // (without a window the page-id loads go out beside the length's)
   // sliding window: keys [k_lo, L) visible, splits from the tile holding k_lo
-  const int k_lo = window_first_key(L, p.window);
-  const int origin = (k_lo / 64) * 64;
-  const int first_page = origin / kPageTokens + split * (p.split_tokens / kPageTokens);
   __shared__ int sm_pg[kMaxSplitPages];
-  const int split_pages = p.split_tokens / kPageTokens;
-  for (int i = threadIdx.x; i < split_pages; i += 64 * NW)
-    sm_pg[i] = pt[min(first_page + i, p.max_pages - 1)];
+  int L, k_lo, first_page;
+  stage_split_pages<64 * NW>(p, b, split, sm_pg, L, k_lo, first_page);
+  const int origin = (k_lo / 64) * 64;
 
   // lane (j = 4*hh + G', g) holds the 32 dims of group g of head 4*qd + hh
   const int gp = r & 3;
@@ -297,18 +293,13 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
       for (int i = 0; i < 32; ++i) x[qd][i] = 0.0f;
     }
   }
-  float cq[32], sq[32];
+  // cos / sin of dims 32g .. 32g + 31 of the lane, as two runs of 16
+  float4 cq4[2][4], sq4[2][4];
   if (p.do_rotary) {
-    const int c0 = p.interleaved ? 16 * g : (g < 2 ? 32 * g : 32 * g - kD / 2);
-    const float* cr = p.cos_cache + (size_t)(L - 1) * (kD / 2) + c0;
-    const float* sr = p.sin_cache + (size_t)(L - 1) * (kD / 2) + c0;
-    // interleaved: pair i >> 1 of the lane's 32 dims, 16 values
+    const float* cr = p.cos_cache + (size_t)(L - 1) * (kD / 2);
+    const float* sr = p.sin_cache + (size_t)(L - 1) * (kD / 2);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const int ci = p.interleaved ? (i >> 1) : i;
-      cq[i] = cr[ci];
-      sq[i] = sr[ci];
-    }
+    for (int hf = 0; hf < 2; ++hf) rope_load16<kD>(cr, sr, 32 * g + 16 * hf, p.interleaved, cq4[hf], sq4[hf]);
   }
 
   const int t_begin = origin + split * p.split_tokens;
@@ -346,7 +337,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
 #pragma unroll
   for (int qd = 0; qd < HT; ++qd) {
     if (p.do_rotary) {
-      float y[32];
+      float y[32], cq[32], sq[32];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        float c16[16], s16[16];
+        rope_pick_all<0>(cq4[hf], sq4[hf], p.interleaved != 0, c16, s16);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          cq[16 * hf + i] = c16[i];
+          sq[16 * hf + i] = s16[i];
+        }
+      }
       if (p.interleaved) {
 #pragma unroll
         for (int i = 0; i < 32; ++i)

@@ -33,7 +33,7 @@ struct sai_ctx {
   int32_t decode_split = 0;  // 0 = automatic
   int32_t tq_split = 0;      // TurboQuant attention split, positions (0 = automatic)
   int32_t decode_waves = 0;  // 0: automatic
-  int32_t decode_merge = 0;  // 0: combine kernel, 1: in-kernel merge
+  int32_t decode_merge = 2;  // 0: combine kernel, 1: in-kernel merge, 2: automatic
   int32_t last_wg = 0;
   int32_t last_split = 0;
   // decode-kernel timing ring: event pairs of the last `slots` calls
@@ -166,6 +166,10 @@ sai_status check_rope(sai_ctx* ctx, const sai_kvcache* c, int32_t batch, int32_t
   if (!cos_cache || !sin_cache)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: do_rotary=1 but cos_cache/sin_cache is missing",
                 op);
+  // the kernels read a table row in 16-byte pieces
+  if ((((uintptr_t)cos_cache | (uintptr_t)sin_cache) & 15u) != 0)
+    return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: cos_cache/sin_cache must be 16-byte aligned",
+                op);
   int32_t maxlen = 0;
   for (int i = 0; i < batch; ++i) maxlen = std::max(maxlen, c->h_seq_lens[i] + extra);
   if (maxlen > cache_rows)
@@ -287,7 +291,7 @@ SAI_API int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves) {
 SAI_API int32_t sai_set_decode_merge(sai_ctx* ctx, int32_t in_kernel) {
   if (!ctx) return 0;
   int32_t prev = ctx->decode_merge;
-  ctx->decode_merge = in_kernel ? 1 : 0;
+  if (in_kernel >= 0 && in_kernel <= 2) ctx->decode_merge = in_kernel;
   return prev;
 }
 
@@ -734,7 +738,12 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   p.max_nsplit = (int)n_max;
   p.partials = ctx->partials;
   p.seq_info = ctx->seq_info;
-  p.merge_in_kernel = ctx->decode_merge;
+  // automatic: the last workgroup merges when every sequence has the same
+  // split count (one ticket per (sequence, kv head), measured faster at 16 x
+  // 8k); ragged batches use the combine kernel (measured faster there). The
+  // int4 kernel always uses the combine kernel.
+  p.merge_in_kernel = c->desc.quant == SAI_KV_INT8 &&
+                      (ctx->decode_merge == 1 || (ctx->decode_merge == 2 && uniform));
   p.counters = ctx->counters;
   p.k_new = k_new;
   p.v_new = v_new;
@@ -755,8 +764,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
     if (e != hipSuccess) return hip_fail(ctx, e, "gqa_decode timing event");
     ++ctx->timed_calls;
   }
-  const bool in_kernel = c->desc.quant == SAI_KV_INT8 && p.merge_in_kernel;
-  if (multi && !in_kernel) {
+  if (multi && !p.merge_in_kernel) {
     e = sai::launch_decode_combine(p, D, G, hs);
     if (e != hipSuccess) return hip_fail(ctx, e, "gqa_decode combine launch");
   }

@@ -172,6 +172,26 @@ class Case:
                                   mask_window=mask_window)
 
 
+def err_tol_ratio(got, ref):
+    """max over elements of |got - ref| / (ATOL + RTOL |ref|): 1.0 is the edge
+    of the tolerance."""
+    return float((np.abs(got - ref) / (ATOL + RTOL * np.abs(ref))).max())
+
+
+def outlier_keys(d, channels=(7, 31, 64, 100), factor=20.0):
+    """k_transform: Student-t (df 3) keys with `channels` of every head of
+    head_dim d scaled by `factor` (heavy tails plus the fixed outlier
+    channels of real models' keys)."""
+
+    def tf(rng, k):
+        b, n, hd = k.shape
+        t = rng.standard_t(3, size=k.shape).astype(np.float32).reshape(b, n, hd // d, d)
+        t[..., list(channels)] *= np.float32(factor)
+        return t.reshape(b, n, hd)
+
+    return tf
+
+
 def assert_close(got, ref, what=""):
     err = np.abs(got - ref)
     tol = ATOL + RTOL * np.abs(ref)

@@ -1,0 +1,79 @@
+"""int8 decode parity on heavy-tailed keys with outlier channels.
+
+The int8 decode kernel holds the rotated query, and each tile's softmax
+weights p * s_v, as two int8 terms (hi + residual / 254) relative to their
+maximum, about 16 significant bits. Keys drawn from a Student-t (df 3) with
+four channels per head scaled x20 (the outlier channels of real models' keys)
+make the largest score terms, and so that representation error, hundreds of
+times larger than N(0, 1) keys do. These cases pin the kernel there, through
+both entry points (sai_gqa_decode after sai_kv_append, and the fused
+sai_gqa_with_cache), at head_dim 128 (groups 4 and 8) and 256 (groups 2 and
+4), with many small splits and with one or two large ones. Each case logs its
+worst error as a fraction of the 2e-3 abs + 1e-2 rel tolerance.
+
+Reference semantics being matched: scaled_dot_product_attention
+(onnx-rt/src/ops/microsoft.rs:241-299, :380-438) over the dequantised cache.
+"""
+import numpy as np
+import pytest
+
+import smallaios_amd as S
+from _gpu_util import Case, assert_close, err_tol_ratio, log, outlier_keys
+
+pytestmark = pytest.mark.gpu
+
+PAST = [6000, 1500, 700, 129]
+
+
+@pytest.fixture(scope="module")
+def rt():
+    import torch
+    assert torch.cuda.is_available()
+    r = S.Runtime(0)
+    yield r
+    r.close()
+
+
+def channels_for(d):
+    return (7, 31, 64, 100) if d == 128 else (7, 63, 130, 200)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("split", [64, 4096])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 128), (16, 4, 256), (8, 4, 256)])
+def test_decode_int8_outlier_keys(rt, hq, hkv, d, split, fused):
+    if d == 256 and hq // hkv == 2 and (split == 64 or fused):
+        pytest.skip("group 2 at head_dim 256: one case (split 4096, unfused) is enough")
+    log(f"int8 decode outlier K: hq={hq} hkv={hkv} d={d} split={split} fused={fused} past={PAST}")
+    prev = rt.set_decode_split(split)
+    try:
+        c = Case(rt, 0x0B7 + hq + d + split, len(PAST), hq, hkv, d, PAST, 1,
+                 theta=5e5, kv_dtype="bf16", permute_pages=True,
+                 k_transform=outlier_keys(d, channels_for(d)), extra_tokens=1)
+        q = c.query("bf16")
+        if fused:
+            got = c.step_fused(q, "bf16")
+        else:
+            c.step_kv()
+            got = c.gpu_decode(q, "bf16")
+        ref = c.oracle_attend(q)
+        ratio = err_tol_ratio(got, ref)
+        log(f"  worst err/tol {ratio:.4f}")
+        assert_close(got, ref, f"outlier K d={d} G={hq // hkv} split={split} fused={fused}")
+        c.check_codes(seqs=[3])
+    finally:
+        rt.set_decode_split(prev)
+
+
+def test_decode_int8_outlier_keys_llama_full_size(rt):
+    """The Llama-3-8B decode layer (B=16, 8k context, 32Q/8KV) with outlier
+    keys, through the fused step at the automatic split."""
+    log("int8 decode outlier K full size: B=16 ctx 8192 32Q/8KV D=128, fused")
+    c = Case(rt, 0x5A1A00F1, 16, 32, 8, 128, [8191] * 16, 1, theta=5e5,
+             k_transform=outlier_keys(128), extra_tokens=1)
+    q = c.query("bf16")
+    got = c.step_fused(q, "bf16")
+    ref = c.oracle_attend(q)
+    ratio = err_tol_ratio(got, ref)
+    log(f"  worst err/tol {ratio:.4f}")
+    assert_close(got, ref, "c2 shape, outlier K")

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import smallaios_amd as S
-from _gpu_util import Case, assert_close, log, outlier_student_t
+from _gpu_util import Case, assert_close, err_tol_ratio, log, outlier_student_t
 
 pytestmark = pytest.mark.gpu
 
@@ -131,14 +131,15 @@ def test_decode_split_merge(rt, split):
         rt.set_decode_split(prev)
 
 
-@pytest.mark.parametrize("merge_in_kernel", [False, True])
+@pytest.mark.parametrize("merge", [0, 1, 2])
 @pytest.mark.parametrize("split", [64, 4096])
-def test_decode_fused_step(rt, merge_in_kernel, split):
+def test_decode_fused_step(rt, merge, split):
     """sai_gqa_with_cache: the decode kernel appends the token itself (codes
-    bit-exact with the standalone append) and merges splits in-kernel or in the
-    combine kernel; repeated steps advance the cache."""
-    log(f"fused decode step merge_in_kernel={merge_in_kernel} split={split}")
-    prev_m = rt.set_decode_merge(merge_in_kernel)
+    bit-exact with the standalone append) and merges splits in the combine
+    kernel (0), in-kernel (1) or as chosen automatically (2); repeated steps
+    advance the cache."""
+    log(f"fused decode step merge={merge} split={split}")
+    prev_m = rt.set_decode_merge(merge)
     prev_s = rt.set_decode_split(split)
     try:
         c = Case(rt, 91, 3, 32, 8, 128, [700, 5, 4100], 1, theta=5e5, kv_dtype="bf16",
@@ -198,7 +199,7 @@ def test_decode_llama_layer_full_size(rt):
     got = c.gpu_decode(q, "bf16")
     ref = c.oracle_attend(q)
     err = assert_close(got, ref, "c2 decode")
-    log(f"  max abs err {err:.2e}")
+    log(f"  max abs err {err:.2e}, worst err/tol {err_tol_ratio(got, ref):.4f}")
     c.check_codes(seqs=[0, 15])
 
 
