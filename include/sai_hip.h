@@ -16,6 +16,13 @@
  * Threading: a sai_ctx and the caches created from it are thread-compatible,
  * not thread-safe. The reference holds its cache behind Arc<Mutex<_>>
  * (onnx-rt/src/session.rs:377); callers do the same.
+ *
+ * Streams: each cache (sai_kvcache, sai_tqcache) owns the device scratch its
+ * attention launches use, sized when it is created, so different caches may
+ * run on different streams at once. The launches on one cache must be
+ * ordered by the caller (one stream, or events between streams), as the
+ * cache's contents already require. Calls documented as synchronous wait for
+ * all work on the device first.
  */
 #ifndef SAI_HIP_H
 #define SAI_HIP_H

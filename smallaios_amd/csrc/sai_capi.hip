@@ -24,12 +24,6 @@ struct sai_ctx {
   int device = 0;
   int num_cus = 0;
   std::string err;
-  float* partials = nullptr;
-  size_t partial_floats = 0;
-  int32_t* seq_info = nullptr;
-  size_t seq_info_n = 0;
-  int32_t* counters = nullptr;
-  size_t counter_n = 0;
   int32_t decode_split = 0;  // 0 = automatic
   int32_t tq_split = 0;      // TurboQuant attention split, positions (0 = automatic)
   int32_t decode_waves = 0;  // 0: automatic
@@ -39,9 +33,20 @@ struct sai_ctx {
   // decode-kernel timing ring: event pairs of the last `slots` calls
   std::vector<hipEvent_t> ev_start, ev_end;
   int64_t timed_calls = 0;
-  // TurboQuant attention workspace
-  float* tq_partials = nullptr;
-  size_t tq_partial_floats = 0;
+};
+
+// Device scratch of the decode kernels: split partials (m, l, o), per-sequence
+// split ranges for the combine kernel, and the in-kernel merge's ticket
+// counters (zero between launches: each launch's last workgroup resets its
+// counter). Each cache owns one, sized when the cache is created, so that
+// caches used from different streams never share one.
+struct DecodeWorkspace {
+  float* partials = nullptr;
+  size_t partial_floats = 0;
+  int32_t* seq_info = nullptr;
+  size_t seq_info_n = 0;
+  int32_t* counters = nullptr;
+  size_t counter_n = 0;
 };
 
 struct sai_tqcache {
@@ -68,6 +73,9 @@ struct sai_tqcache {
   int32_t batch = 0;
   int32_t pending = 0;
   float norm = 0.0f;
+  // attention split partials, sized at creation
+  float* partials = nullptr;
+  size_t partial_floats = 0;
 };
 
 struct sai_kvcache {
@@ -83,6 +91,7 @@ struct sai_kvcache {
   int32_t batch = 0;
   int32_t pending = 0;
   std::vector<int32_t> layer_window;  // per layer: last keys visible (0: global)
+  DecodeWorkspace ws;
 };
 
 namespace {
@@ -191,39 +200,65 @@ int32_t visible_span(int32_t layer_window, int32_t window) {
   return (int32_t)std::min<int64_t>(w, 0x7FFFFFFF);
 }
 
-sai_status ensure_workspace(sai_ctx* ctx, size_t partial_floats, size_t seq_info,
-                            size_t counters) {
-  if (counters > ctx->counter_n) {
-    if (ctx->counters) (void)hipFree(ctx->counters);
-    ctx->counters = nullptr;
-    ctx->counter_n = 0;
-    size_t n = std::max(counters, (size_t)4096);
-    hipError_t e = hipMalloc(&ctx->counters, n * sizeof(int32_t));
+void release_workspace(DecodeWorkspace& w) {
+  if (w.partials) (void)hipFree(w.partials);
+  if (w.seq_info) (void)hipFree(w.seq_info);
+  if (w.counters) (void)hipFree(w.counters);
+  w = DecodeWorkspace{};
+}
+
+// Grows w to hold at least the given sizes. A buffer that must grow is freed
+// and allocated again after the device is idle (no launch still uses it);
+// counters start at zero.
+sai_status reserve_workspace(sai_ctx* ctx, DecodeWorkspace& w, size_t partial_floats,
+                             size_t seq_info, size_t counters) {
+  if (partial_floats <= w.partial_floats && seq_info <= w.seq_info_n && counters <= w.counter_n)
+    return SAI_OK;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(ctx, e, "decode workspace: sync");
+  if (counters > w.counter_n) {
+    if (w.counters) (void)hipFree(w.counters);
+    w.counters = nullptr;
+    w.counter_n = 0;
+    e = hipMalloc(&w.counters, counters * sizeof(int32_t));
     if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "decode counters: %s", hipGetErrorString(e));
-    e = hipMemset(ctx->counters, 0, n * sizeof(int32_t));
+    e = hipMemset(w.counters, 0, counters * sizeof(int32_t));
     if (e != hipSuccess) return hip_fail(ctx, e, "decode counters memset");
-    ctx->counter_n = n;
+    w.counter_n = counters;
   }
-  if (partial_floats > ctx->partial_floats) {
-    if (ctx->partials) (void)hipFree(ctx->partials);
-    ctx->partials = nullptr;
-    ctx->partial_floats = 0;
-    size_t n = std::max(partial_floats, (size_t)1 << 20);
-    hipError_t e = hipMalloc(&ctx->partials, n * sizeof(float));
+  if (partial_floats > w.partial_floats) {
+    if (w.partials) (void)hipFree(w.partials);
+    w.partials = nullptr;
+    w.partial_floats = 0;
+    e = hipMalloc(&w.partials, partial_floats * sizeof(float));
     if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "decode workspace: %s", hipGetErrorString(e));
-    ctx->partial_floats = n;
+    w.partial_floats = partial_floats;
   }
-  if (seq_info > ctx->seq_info_n) {
-    if (ctx->seq_info) (void)hipFree(ctx->seq_info);
-    ctx->seq_info = nullptr;
-    ctx->seq_info_n = 0;
-    size_t n = std::max(seq_info, (size_t)4096);
-    hipError_t e = hipMalloc(&ctx->seq_info, n * sizeof(int32_t));
+  if (seq_info > w.seq_info_n) {
+    if (w.seq_info) (void)hipFree(w.seq_info);
+    w.seq_info = nullptr;
+    w.seq_info_n = 0;
+    e = hipMalloc(&w.seq_info, seq_info * sizeof(int32_t));
     if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "decode sequence info: %s", hipGetErrorString(e));
-    ctx->seq_info_n = n;
+    w.seq_info_n = seq_info;
   }
   return SAI_OK;
 }
+
+// (sequence, split) work items one decode launch can have at the automatic
+// split (decode_split_tokens): the split is at least 256 tokens and at least
+// (tokens x kv heads) / CUs, except for ragged batches, where it may be capped
+// at 2048; so the items number at most CUs / kv heads, or total tokens / 2048,
+// plus one rounding item per sequence. Total tokens are bounded by the pages
+// (unless sequences share pages; a launch that needs more grows the workspace).
+size_t decode_work_bound(const sai_ctx* ctx, const sai_kvcache_desc& d) {
+  const size_t by_cus = ((size_t)ctx->num_cus + d.num_kv_heads - 1) / d.num_kv_heads + 1;
+  const size_t by_pages = ((size_t)d.num_pages * SAI_PAGE_TOKENS + 2047) / 2048;
+  return std::max(by_cus, by_pages) + (size_t)d.max_batch;
+}
+
+// Largest query group a cache of this head_dim serves in decode.
+int max_decode_group(int head_dim) { return head_dim > 128 ? 4 : 8; }
 
 }  // namespace
 
@@ -246,10 +281,6 @@ SAI_API sai_status sai_init(int device, sai_ctx** out) {
 SAI_API void sai_destroy(sai_ctx* ctx) {
   if (!ctx) return;
   DeviceGuard dg(ctx->device);
-  if (ctx->tq_partials) (void)hipFree(ctx->tq_partials);
-  if (ctx->partials) (void)hipFree(ctx->partials);
-  if (ctx->seq_info) (void)hipFree(ctx->seq_info);
-  if (ctx->counters) (void)hipFree(ctx->counters);
   for (hipEvent_t e : ctx->ev_start) (void)hipEventDestroy(e);
   for (hipEvent_t e : ctx->ev_end) (void)hipEventDestroy(e);
   delete ctx;
@@ -383,6 +414,15 @@ SAI_API sai_status sai_kvcache_create(sai_ctx* ctx, const sai_kvcache_desc* desc
   c->h_mapped.assign(d.max_batch, 0);
   c->h_seq_lens.assign(d.max_batch, 0);
   c->layer_window.assign(d.num_layers, 0);
+  // the decode workspace for every launch at the automatic split
+  const size_t work = decode_work_bound(ctx, d);
+  sai_status st = reserve_workspace(
+      ctx, c->ws, work * d.num_kv_heads * max_decode_group(d.head_dim) * (d.head_dim + 2),
+      (size_t)d.max_batch * 2, (size_t)d.max_batch * d.num_kv_heads);
+  if (st != SAI_OK) {
+    sai_kvcache_destroy(c);
+    return st;
+  }
   *out = c;
   return SAI_OK;
 }
@@ -405,6 +445,7 @@ SAI_API void sai_kvcache_destroy(sai_kvcache* c) {
     if (p) (void)hipFree(p);
   if (c->d_page_table) (void)hipFree(c->d_page_table);
   if (c->d_seq_lens) (void)hipFree(c->d_seq_lens);
+  release_workspace(c->ws);
   delete c;
 }
 
@@ -528,6 +569,11 @@ SAI_API sai_status sai_kvcache_read(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
   if ((int64_t)t0 + n_tokens > (int64_t)c->h_mapped[b] * SAI_PAGE_TOKENS)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "kvcache_read: tokens beyond the mapped pages");
   DeviceGuard dg(ctx->device);
+  {
+    // synchronous: the tokens of every append already enqueued on any stream
+    const hipError_t es = hipDeviceSynchronize();
+    if (es != hipSuccess) return hip_fail(ctx, es, "kvcache_read");
+  }
   const int D = d.head_dim;
   std::vector<uint8_t> blk(c->block_bytes);
   const int NG = D / 32;
@@ -708,8 +754,10 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   if (work <= 0 || work > 0x7FFFFFFF)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: bad work size", op);
   DeviceGuard dg(ctx->device);
-  sai_status st = ensure_workspace(ctx, (size_t)work * kvh * G * (D + 2), (size_t)batch * 2,
-                                   (size_t)batch * kvh);
+  // the cache's own workspace (sized at creation for the automatic split; a
+  // smaller split set for tuning may grow it once, synchronously)
+  sai_status st = reserve_workspace(ctx, c->ws, (size_t)work * kvh * G * (D + 2),
+                                    (size_t)batch * 2, (size_t)batch * kvh);
   if (st != SAI_OK) return st;
 
   sai::DecodeParams p{};
@@ -736,15 +784,15 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   p.waves = ctx->decode_waves ? ctx->decode_waves : (c->desc.quant == SAI_KV_INT4 ? 8 : 4);
   p.uniform_nsplit = uniform ? (int)n_first : 0;
   p.max_nsplit = (int)n_max;
-  p.partials = ctx->partials;
-  p.seq_info = ctx->seq_info;
+  p.partials = c->ws.partials;
+  p.seq_info = c->ws.seq_info;
   // automatic: the last workgroup merges when every sequence has the same
   // split count (one ticket per (sequence, kv head), measured faster at 16 x
   // 8k); ragged batches use the combine kernel (measured faster there). The
   // int4 kernel always uses the combine kernel.
   p.merge_in_kernel = c->desc.quant == SAI_KV_INT8 &&
                       (ctx->decode_merge == 1 || (ctx->decode_merge == 2 && uniform));
-  p.counters = ctx->counters;
+  p.counters = c->ws.counters;
   p.k_new = k_new;
   p.v_new = v_new;
   p.kv_dtype = kv_dtype;
@@ -1189,6 +1237,7 @@ SAI_API void sai_tqcache_destroy(sai_tqcache* c) {
       if (p) (void)hipFree(p);
   }
   if (c->d_lens) (void)hipFree(c->d_lens);
+  if (c->partials) (void)hipFree(c->partials);
   delete c;
 }
 
@@ -1248,6 +1297,17 @@ SAI_API sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc
     return fail(ctx, SAI_ERR_ALLOC, "tq_cache: %s", hipGetErrorString(e));
   }
   c->h_lens.assign(d.max_batch, 0);
+  // attention partials at the automatic split: about 768 workgroups plus one
+  // rounding split per (sequence, kv head), groups up to 8 (4 at head_dim 256)
+  {
+    const size_t units = (size_t)d.max_batch * d.num_kv_heads;
+    const size_t n = (768 + 2 * units) * (d.head_dim > 128 ? 4 : 8) * (d.head_dim + 2);
+    if (hipMalloc(&c->partials, n * sizeof(float)) != hipSuccess) {
+      sai_tqcache_destroy(c);
+      return fail(ctx, SAI_ERR_ALLOC, "tq_cache: workspace");
+    }
+    c->partial_floats = n;
+  }
   *out = c;
   return SAI_OK;
 }
@@ -1305,7 +1365,9 @@ SAI_API sai_status sai_tqcache_advance(sai_ctx* ctx, sai_tqcache* c, void* strea
 SAI_API sai_status sai_tqcache_reset(sai_ctx* ctx, sai_tqcache* c) {
   if (!ctx || !c) return SAI_ERR_NULL;
   DeviceGuard dg(ctx->device);
-  const hipError_t e = hipMemset(c->d_lens, 0, (size_t)c->desc.max_batch * sizeof(int32_t));
+  // synchronous: after every launch already enqueued on any stream
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemset(c->d_lens, 0, (size_t)c->desc.max_batch * sizeof(int32_t));
   if (e != hipSuccess) return hip_fail(ctx, e, "tq_cache_reset");
   std::fill(c->h_lens.begin(), c->h_lens.end(), 0);
   c->pending = 0;
@@ -1398,7 +1460,10 @@ SAI_API sai_status sai_tqcache_read(sai_ctx* ctx, sai_tqcache* c, int32_t layer,
   DeviceGuard dg(ctx->device);
   const size_t n = (size_t)len * c->desc.head_dim;
   float* dk = nullptr;
-  hipError_t e = hipMalloc(&dk, 2 * n * sizeof(float));
+  // synchronous: the rows of every write already enqueued on any stream
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(ctx, e, op);
+  e = hipMalloc(&dk, 2 * n * sizeof(float));
   if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "%s: %s", op, hipGetErrorString(e));
   sai::TqArgs a = tq_args(c, layer);
   e = sai::launch_tq_read(a, b, head, start, len, dk, dk + n, nullptr);
@@ -1445,6 +1510,11 @@ SAI_API sai_status sai_tqcache_read_raw(sai_ctx* ctx, sai_tqcache* c, int32_t la
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: range out of the written rows", op);
   if (len == 0) return SAI_OK;
   DeviceGuard dg(ctx->device);
+  {
+    // synchronous: the rows of every write already enqueued on any stream
+    const hipError_t es = hipDeviceSynchronize();
+    if (es != hipSuccess) return hip_fail(ctx, es, op);
+  }
   const sai_tqcache::Layer& L = c->layers[layer];
   const size_t row0 = ((size_t)head * c->desc.max_batch + b) * c->desc.max_rows + start;
   const size_t cb = (size_t)c->desc.head_dim * c->desc.bits / 8;
@@ -1554,13 +1624,17 @@ sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, c
   const int32_t max_splits = (max_len + split_rows - 1) / split_rows;
   const size_t part_floats = (size_t)batch * H * max_splits * G * (D + 2);
   DeviceGuard dg(ctx->device);
-  if (mode != 1 && part_floats > ctx->tq_partial_floats) {
-    if (ctx->tq_partials) (void)hipFree(ctx->tq_partials);
-    ctx->tq_partials = nullptr;
-    ctx->tq_partial_floats = 0;
-    if (hipMalloc(&ctx->tq_partials, part_floats * sizeof(float)) != hipSuccess)
+  // the cache's partials are sized at creation for the automatic split; a
+  // smaller split set for tuning may grow them once, after the device is idle
+  if (mode != 1 && part_floats > c->partial_floats) {
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(ctx, e, op);
+    if (c->partials) (void)hipFree(c->partials);
+    c->partials = nullptr;
+    c->partial_floats = 0;
+    if (hipMalloc(&c->partials, part_floats * sizeof(float)) != hipSuccess)
       return fail(ctx, SAI_ERR_ALLOC, "%s: workspace", op);
-    ctx->tq_partial_floats = part_floats;
+    c->partial_floats = part_floats;
   }
   sai::TqArgs a = tq_args(c, layer);
   sai::TqAttendArgs t{};
@@ -1568,7 +1642,7 @@ sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, c
   t.q_bf16 = dtype == SAI_DTYPE_BF16 ? 1 : 0;
   t.num_heads = num_heads;
   t.out = out;
-  t.partials = ctx->tq_partials;
+  t.partials = c->partials;
   t.weights = weights;
   t.ld = ld;
   t.normalize = mode == 0 ? 1 : 0;

@@ -239,6 +239,12 @@ size_t DeviceTensor::byte_size() const {
   return n * es;
 }
 
+bool DeviceTensor::holds_shape() const {
+  const size_t n = byte_size();
+  if (n == std::numeric_limits<size_t>::max()) return false;
+  return buffer.size() >= n && (n == 0 || buffer.as_ptr() != nullptr);
+}
+
 Result<DeviceTensor, HipError> DeviceTensor::alloc(std::vector<int64_t> shape, DataType dtype) {
   DeviceTensor t;
   t.shape = std::move(shape);
@@ -403,7 +409,8 @@ Result<Unit, HipError> GpuKvCache::append(size_t layer_idx, const DeviceTensor& 
     sn = 1;
   }
   if (b == 0 || new_v.shape != new_k.shape ||
-      new_k.byte_size() != b * sn * num_kv_heads_ * head_dim_ * element_size(new_k.dtype))
+      new_k.byte_size() != b * sn * num_kv_heads_ * head_dim_ * element_size(new_k.dtype) ||
+      !new_k.holds_shape() || !new_v.holds_shape())
     return HipError::runtime("kv_cache_append:tensor_byte_size_mismatch");
   auto ck = check_append(b, sn);
   if (!ck) return ck;
@@ -639,6 +646,8 @@ Result<int32_t, OpError> check_rope_tables(const DeviceTensor& cos, const Device
   const int64_t rows = std::min(cos.shape[0], sin.shape[0]);
   if (rows < 0 || rows > std::numeric_limits<int32_t>::max())
     return OpError::shape("apply_rope_in_place: cos/sin caches must be rank-2");
+  if (!cos.holds_shape() || !sin.holds_shape())
+    return OpError::shape("apply_rope_in_place: cos/sin buffer does not hold its shape");
   return (int32_t)rows;
 }
 
@@ -713,8 +722,7 @@ Result<std::vector<DeviceTensor>, OpError> dispatch_gqa(
     return OpError::shape("GroupQueryAttention requires Float or BFloat16 input");
   if (q.byte_size() != g.batch * g.seq * g.q_hidden * element_size(q.dtype) ||
       k.byte_size() != g.batch * g.seq * g.kv_heads * g.head_dim * element_size(k.dtype) ||
-      !(q.buffer.as_ptr() || q.byte_size() == 0) || !(k.buffer.as_ptr() || k.byte_size() == 0) ||
-      !(v.buffer.as_ptr() || v.byte_size() == 0))
+      !q.holds_shape() || !k.holds_shape() || !v.holds_shape())
     return OpError::shape("GroupQueryAttention: input buffer does not hold its shape");
 
   // RoPE tables (inputs 7 and 8, gqa_apply_rotary, ops/microsoft.rs:1004-1020)
@@ -815,6 +823,9 @@ Result<std::vector<DeviceTensor>, OpError> dispatch_rotary_embedding(
     if (!(cos = slot(inputs, 1))) return missing("cos_cache");
     if (!(sin = slot(inputs, 2))) return missing("sin_cache");
   }
+  if (!x->holds_shape() || !cos->holds_shape() || !sin->holds_shape() ||
+      (pos && !pos->holds_shape()))
+    return OpError::shape("GPU RotaryEmbedding: input buffer does not hold its shape");
   const AttributeProto* il = find_attr(attrs, "interleaved");
   const bool interleaved = il && il->i != 0;
   // pick_rotary_position / read_first_i64_position (gpu_executor.rs:747-771)
@@ -909,6 +920,9 @@ Result<DeviceTensor, OpError> op_rotary_embedding(RocmRuntime& runtime,
   if (!cos) return OpError::shape("RotaryEmbedding: missing cos_cache");
   const DeviceTensor* sin = slot(inputs, 3);
   if (!sin) return OpError::shape("RotaryEmbedding: missing sin_cache");
+  if (!input->holds_shape() || !position_ids->holds_shape() || !cos->holds_shape() ||
+      !sin->holds_shape())
+    return OpError::shape("RotaryEmbedding: input buffer does not hold its shape");
   if (input->dtype != DataType::Float) return OpError::shape("RotaryEmbedding requires Float input");
   // rank 3 is read as [B, num_heads, S, D] over the same bytes (microsoft.rs:578-600)
   std::vector<int64_t> view;
@@ -1022,6 +1036,8 @@ Result<size_t, OpError> validate_past_kv(const DeviceTensor* past, size_t batch,
   if (past->shape[0] != (int64_t)batch || past->shape[1] != (int64_t)heads ||
       past->shape[3] != (int64_t)head_dim || past->shape[2] < 0)
     return OpError::shape("GQA/MHA: past cache batch/heads/head_dim mismatch");
+  if (!past->holds_shape())
+    return OpError::shape("GQA/MHA: past cache buffer does not hold its shape");
   return (size_t)past->shape[2];
 }
 
@@ -1150,6 +1166,8 @@ Result<AttentionOutputs, OpError> op_group_query_attention(
   const DeviceTensor* sin = slot(inputs, 8);
   if (q->dtype != DataType::Float || k->dtype != DataType::Float || v->dtype != DataType::Float)
     return OpError::shape("GroupQueryAttention requires Float input");
+  if (!q->holds_shape() || !k->holds_shape() || !v->holds_shape())
+    return OpError::shape("GroupQueryAttention: input buffer does not hold its shape");
   // gqa_validate (microsoft.rs:933-984) takes rank-3 Q/K/V only
   if (q->shape.size() != 3 || k->shape.size() != 3 || v->shape.size() != 3) {
     if (num_heads <= 0 || kv_num_heads <= 0)
@@ -1208,6 +1226,8 @@ Result<AttentionOutputs, OpError> op_multi_head_attention(
   const DeviceTensor* past_value = slot(inputs, 7);
   if (q->dtype != DataType::Float || k->dtype != DataType::Float || v->dtype != DataType::Float)
     return OpError::shape("MultiHeadAttention requires Float input");
+  if (!q->holds_shape() || !k->holds_shape() || !v->holds_shape())
+    return OpError::shape("MultiHeadAttention: input buffer does not hold its shape");
   if (num_heads <= 0) return OpError::attribute("MultiHeadAttention: num_heads must be > 0");
   if (q->shape.size() != 3 || k->shape.size() != 3 || v->shape.size() != 3)
     return OpError::shape("MultiHeadAttention: Q/K/V must be rank-3 (B, Sq, hidden)");

@@ -185,6 +185,10 @@ struct DeviceTensor {
 
   size_t total_elements() const;  // 0 when any dim is negative
   size_t byte_size() const;
+  // The buffer holds at least byte_size() bytes (and a device pointer when
+  // that is not 0): shape and buffer are separate fields, and every entry
+  // point checks this before a kernel reads or writes the tensor.
+  bool holds_shape() const;
   // Uninitialised device tensor of `shape` and `dtype`.
   static Result<DeviceTensor, HipError> alloc(std::vector<int64_t> shape, DataType dtype);
   // Device copy of little-endian host bytes (Tensor::raw_data). The byte

@@ -92,6 +92,8 @@ Result<Unit, OpError> GpuCompressedKvCache::write_kv(size_t layer, const DeviceT
       k.shape[1] <= 0 || !fits_i32((size_t)k.shape[0]) || !fits_i32((size_t)k.shape[1]) ||
       !fits_i32(layer))
     return OpError::shape(pre + "K/V must be [batch, rows, kv_heads * head_dim]");
+  if (!k.holds_shape() || !v.holds_shape())
+    return OpError::shape(pre + "K/V buffer does not hold its shape");
   const sai_status st =
       sai_tqcache_write(rt_->raw(), cache_, (int32_t)layer, k.buffer.as_ptr(), v.buffer.as_ptr(),
                         *dt, (int32_t)k.shape[0], (int32_t)k.shape[1], stream);
@@ -170,6 +172,7 @@ Result<DeviceTensor, OpError> GpuCompressedKvCache::attend(size_t layer, const D
       !fits_i32(num_heads) || !fits_i32(layer) ||
       q.shape[2] != (int64_t)(num_heads * cfg_.head_dim))
     return OpError::shape(pre + "query must be [batch, 1, num_heads * head_dim]");
+  if (!q.holds_shape()) return OpError::shape(pre + "query buffer does not hold its shape");
   auto out = DeviceTensor::alloc(q.shape, DataType::Float);
   if (!out) return OpError::internal(pre + out.error().to_string());
   const sai_status st = sai_tqcache_attend(rt_->raw(), cache_, (int32_t)layer, q.buffer.as_ptr(),
@@ -193,6 +196,8 @@ Result<DeviceTensor, OpError> GpuCompressedKvCache::write_attend(
       q.shape[2] != (int64_t)(num_heads * cfg_.head_dim) || k_new.shape != v_new.shape ||
       k_new.shape != std::vector<int64_t>{q.shape[0], 1, hidden})
     return OpError::shape(pre + "Q [batch, 1, Hq*D] and K/V [batch, 1, Hkv*D] expected");
+  if (!q.holds_shape() || !k_new.holds_shape() || !v_new.holds_shape())
+    return OpError::shape(pre + "Q/K/V buffer does not hold its shape");
   auto out = DeviceTensor::alloc(q.shape, DataType::Float);
   if (!out) return OpError::internal(pre + out.error().to_string());
   const sai_status st = sai_tqcache_write_attend(

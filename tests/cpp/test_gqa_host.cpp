@@ -197,6 +197,10 @@ void cpu_errors_and_types() {
   t.shape = shp({2, 3, 4});
   t.dtype = DataType::BFloat16;
   REQUIRE(t.total_elements() == 24 && t.byte_size() == 48, "sizes");
+  // a shape with no buffer behind it is rejected by every entry point
+  REQUIRE(!t.holds_shape(), "shape without a buffer");
+  t.shape = shp({2, 0, 4});
+  REQUIRE(t.holds_shape(), "empty shape needs no buffer");
   HipError e = must_fail_hip(RocmRuntime::init(1 << 20), "device out of range");
   REQUIRE(e.kind == HipError::Kind::NoDevice, "%s", e.to_string().c_str());
 }
@@ -418,6 +422,33 @@ void gpu_dispatch_errors() {
   expect(dispatch_gqa(rt, {&q, &k, &k, nullptr, nullptr, nullptr, nullptr, &cs, nullptr}, heads,
                       nullptr),
          OpError::Kind::ShapeMismatch, "do_rotary=1 but sin_cache is missing", "cos without sin");
+  // a tensor whose shape claims more than its buffer holds
+  DeviceTensor short_k = f32_tensor(std::vector<float>(64, 0.5f), shp({1, 1, 64}));
+  short_k.shape = s3kv;
+  expect(dispatch_gqa(rt, {&q, &short_k, &k}, heads, nullptr), OpError::Kind::ShapeMismatch,
+         "input buffer does not hold its shape", "K buffer shorter than its shape");
+  DeviceTensor short_q = f32_tensor(std::vector<float>(128, 0.5f), shp({1, 1, 128}));
+  short_q.shape = s3;
+  expect(dispatch_gqa(rt, {&short_q, &k, &k}, heads, nullptr), OpError::Kind::ShapeMismatch,
+         "input buffer does not hold its shape", "Q buffer shorter than its shape");
+  OpError eo = must_fail(op_group_query_attention(rt, {&short_q, &k, &k}, 4, 2, std::nullopt, -1,
+                                                  false, false),
+                         "CPU-op Q buffer shorter than its shape");
+  REQUIRE(eo.kind == OpError::Kind::ShapeMismatch &&
+              eo.message.find("does not hold its shape") != std::string::npos,
+          "%s", eo.to_string().c_str());
+  DeviceTensor short_cs = f32_tensor(std::vector<float>(16, 1.0f), shp({1, 16}));
+  short_cs.shape = shp({8, 32});
+  expect(dispatch_gqa(rt, {&q, &k, &k, nullptr, nullptr, nullptr, nullptr, &short_cs, &cs}, heads,
+                      nullptr),
+         OpError::Kind::ShapeMismatch, "cos/sin buffer does not hold its shape",
+         "cos buffer shorter than its shape");
+  GpuKvCache cache = must(GpuKvCache::allocate(rt, 1, 2, 64, 32, KvQuant::Int8,
+                                               std::vector<LayerKind>(1, LayerKind::global())),
+                          "cache");
+  HipError he = must_fail_hip(cache.append(0, short_k, k, nullptr), "append short K");
+  REQUIRE(he.to_string().find("tensor_byte_size_mismatch") != std::string::npos, "%s",
+          he.to_string().c_str());
 }
 
 }  // namespace
@@ -1224,6 +1255,17 @@ void gpu_compressed_kv_cache() {
   must(c.write_kv(0, must(DeviceTensor::from_f32(k, shp({B, S, H * D})), "k"),
                   must(DeviceTensor::from_f32(v, shp({B, S, H * D})), "v")), "write_kv");
   must(c.advance(), "advance");
+  {
+    // shapes that claim more than their buffers hold are rejected
+    DeviceTensor short_k = must(DeviceTensor::from_f32(std::vector<float>((size_t)H * D), shp({1, 1, H * D})), "short");
+    short_k.shape = shp({B, 1, H * D});
+    OpError e = must_fail(c.write_kv(0, short_k, short_k), "write_kv short K");
+    REQUIRE(e.kind == OpError::Kind::ShapeMismatch, "%s", e.to_string().c_str());
+    DeviceTensor short_q = must(DeviceTensor::from_f32(std::vector<float>((size_t)Hq * D), shp({1, 1, Hq * D})), "short q");
+    short_q.shape = shp({B, 1, Hq * D});
+    e = must_fail(c.attend(0, short_q, Hq), "attend short Q");
+    REQUIRE(e.kind == OpError::Kind::ShapeMismatch, "%s", e.to_string().c_str());
+  }
   const std::vector<float> q = randv((size_t)B * Hq * D), k1 = randv((size_t)B * H * D),
                            v1 = randv(k1.size());
   DeviceTensor out = must(c.write_attend(0, must(DeviceTensor::from_f32(q, shp({B, 1, Hq * D})), "q"),
