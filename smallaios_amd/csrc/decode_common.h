@@ -133,10 +133,10 @@ __device__ __forceinline__ void reset_ticket(int* counter) {
   __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Online merge of C splits' (m, l, o) entries for one (head, dim) into
-// (M, Ls, O), skipping split `own` (whose values the caller already holds) and
-// splits with no visible key; `ph` points at split 0's (m, l, o[...]) block of
-// this head, `stride` floats apart per split, `d` the dim.
+// Online merge of the splits' (m, l, o) entries for one (head, dim) into
+// (M, Ls, O), C splits per round trip, in split order, skipping split `own`
+// (-1: none) and splits with no visible key; `ph` points at split 0's (m, l,
+// o[...]) block of this head, `stride` floats apart per split, `d` the dim.
 template <int C>
 __device__ __forceinline__ void merge_partials(const float* ph, size_t stride, int d, int nsplit,
                                                int own, float& M, float& Ls, float& O) {

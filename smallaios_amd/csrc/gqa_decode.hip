@@ -531,7 +531,6 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
   float* part = p.partials + ((size_t)(split_base + split) * p.kv_heads + kvh) * (G * (D + 2));
   // (m, l, o) of this split for the (head, dim) entries t = threadIdx.x + k*64*NW
   constexpr int PER = (G * D + 64 * NW - 1) / (64 * NW);
-  float mM[PER], mL[PER], mO[PER];
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int t = threadIdx.x + k * 64 * NW;
@@ -548,9 +547,6 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
       Ls += sm_l[w][hd] * f;
       O += sm_o[w][hd][d] * f;
     }
-    mM[k] = M;
-    mL[k] = Ls;
-    mO[k] = O;
     if (nsplit == 1) {
       p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
     } else if (p.merge_in_kernel) {
@@ -592,19 +588,21 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
   if (!sm_last) return;
   const size_t stride = (size_t)p.kv_heads * (G * (D + 2));
   const float* p0 = p.partials + ((size_t)split_base * p.kv_heads + kvh) * (G * (D + 2));
+  // every split's partial, this workgroup's own included, in split order: the
+  // result does not depend on which workgroup finished last
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int t = threadIdx.x + k * 64 * NW;
     if (G * D % (64 * NW) != 0 && t >= G * D) break;
     const int hd = t / D, d = t % D;
-    float M = mM[k], Ls = mL[k], O = mO[k];
+    float M = -INFINITY, Ls = 0.0f, O = 0.0f;
     const float* ph = p0 + hd * (D + 2);
     if (nsplit <= 2)
-      merge_partials<2>(ph, stride, d, nsplit, split, M, Ls, O);
+      merge_partials<2>(ph, stride, d, nsplit, -1, M, Ls, O);
     else if (nsplit <= 4)
-      merge_partials<4>(ph, stride, d, nsplit, split, M, Ls, O);
+      merge_partials<4>(ph, stride, d, nsplit, -1, M, Ls, O);
     else
-      merge_partials<8>(ph, stride, d, nsplit, split, M, Ls, O);
+      merge_partials<8>(ph, stride, d, nsplit, -1, M, Ls, O);
     p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
   }
   if (threadIdx.x == 0) reset_ticket(counter);
