@@ -201,6 +201,28 @@ sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, c
                               int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
                               float scale, int32_t window, float* out, void* stream);
 
+/* ---- the fused decode step without allocation ---------------------------------
+ * No counterpart in the reference: this is for callers that cannot allocate
+ * device memory during a step (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation). Same contract, arguments and
+ * results as sai_gqa_with_cache, but the step's scratch (split partials,
+ * split ranges, merge tickets) lives in one fixed 16 MiB array per GPU that
+ * the library sets up in sai_init and holds until the process ends, instead
+ * of the cache's own workspace; nothing is allocated or freed. Limits: at
+ * most 65536 (sequence x kv head) pairs, 32768 sequences, and 4,063,232
+ * partial floats, i.e. sequence-splits x kv heads x group x (head_dim + 2)
+ * (the Llama-3-8B layer at 16 x 8k uses 133,120); a larger step fails with
+ * UNSUPPORTED. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads, other contexts) race. */
+sai_status sai_gqa_with_cache_noalloc(sai_ctx* ctx, sai_kvcache* cache, int32_t layer,
+                                      const void* q, int32_t q_dtype, const void* k_new,
+                                      const void* v_new, int32_t kv_dtype, int32_t batch,
+                                      int32_t num_heads, const float* cos_cache,
+                                      const float* sin_cache, int32_t cache_rows,
+                                      int32_t do_rotary, int32_t rotary_interleaved,
+                                      int32_t has_scale, float scale, int32_t window, float* out,
+                                      void* stream);
+
 /* ---- kernel 3: prefill chunk (f16 MFMA) ---------------------------------------
  * Same contract as sai_gqa_decode for a chunk of sq == pending query tokens per
  * sequence (the reference's op_group_query_attention with Sq > 1, causal with

@@ -81,7 +81,8 @@ EXPORTS = [
     "sai_kvcache_set_seq_lens", "sai_kvcache_advance", "sai_kvcache_reset",
     "sai_kvcache_lengths", "sai_kvcache_read", "sai_kvcache_pool", "sai_kv_append",
     "sai_kvcache_set_layer_window",
-    "sai_gqa_decode", "sai_gqa_with_cache", "sai_gqa_prefill", "sai_set_decode_split",
+    "sai_gqa_decode", "sai_gqa_with_cache", "sai_gqa_with_cache_noalloc", "sai_gqa_prefill",
+    "sai_set_decode_split",
     "sai_set_decode_waves", "sai_set_decode_merge", "sai_last_decode_shape",
     "sai_set_decode_timing", "sai_decode_kernel_times", "sai_rotary_embedding",
     "sai_rope_tables", "sai_copy_rows", "sai_tqcache_create", "sai_tqcache_destroy",
@@ -116,6 +117,8 @@ def _declare(L: C.CDLL) -> None:
         "sai_gqa_decode": (i32, [p, p, i32, p, i32, i32, i32, p, p, i32, i32, i32, i32, f, i32,
                                  p, p]),
         "sai_gqa_with_cache": (i32, [p, p, i32, p, i32, p, p, i32, i32, i32, p, p, i32, i32,
+                                     i32, i32, f, i32, p, p]),
+        "sai_gqa_with_cache_noalloc": (i32, [p, p, i32, p, i32, p, p, i32, i32, i32, p, p, i32, i32,
                                      i32, i32, f, i32, p, p]),
         "sai_gqa_prefill": (i32, [p, p, i32, p, i32, i32, i32, i32, p, p, i32, i32, i32, i32,
                                   f, i32, p, p]),
@@ -415,6 +418,19 @@ class KvCache:
             kd, batch, num_heads, _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary),
             int(interleaved), int(scale is not None), 0.0 if scale is None else float(scale),
             int(window), _dev_ptr(out), _stream(stream)), "gqa_with_cache")
+
+    def decode_with_cache_noalloc(self, layer, q, k_new, v_new, out, batch, num_heads, cos=None,
+                                  sin=None, cache_rows=0, do_rotary=True, interleaved=False,
+                                  scale=None, stream=None, q_dtype=None, kv_dtype=None, window=0):
+        """decode_with_cache over the library's fixed per-GPU scratch (no
+        device allocation; calls overlapping on one GPU race)."""
+        qd = q_dtype if q_dtype is not None else _dtype_code(q)
+        kd = kv_dtype if kv_dtype is not None else _dtype_code(k_new)
+        self.rt.check(self._L.sai_gqa_with_cache_noalloc(
+            self.rt.handle, self.handle, layer, _dev_ptr(q), qd, _dev_ptr(k_new), _dev_ptr(v_new),
+            kd, batch, num_heads, _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary),
+            int(interleaved), int(scale is not None), 0.0 if scale is None else float(scale),
+            int(window), _dev_ptr(out), _stream(stream)), "gqa_with_cache_noalloc")
 
     def prefill(self, layer, q, out, batch, sq, num_heads, cos=None, sin=None, cache_rows=0,
                 do_rotary=True, interleaved=False, scale=None, stream=None, dtype=None, window=0):

@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -48,6 +49,30 @@ struct DecodeWorkspace {
   int32_t* counters = nullptr;
   size_t counter_n = 0;
 };
+
+// Scratch of sai_gqa_with_cache_noalloc, for callers that cannot allocate
+// device memory: one fixed array per GPU, held until the process ends,
+// holding the same three parts as a DecodeWorkspace (merge ticket counters,
+// split ranges, split partials, in that order). Its device address on each
+// GPU is taken once, in sai_init, with that GPU current (g_scratch below);
+// host code never passes `scratch` itself to a kernel (on the host that name
+// is only a stand-in for the symbol).
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+constexpr size_t kScratchCounters = 65536;  // int32: sequences x kv heads
+constexpr size_t kScratchSeqInfo = 65536;   // int32: two per sequence
+constexpr size_t kScratchPartialFloats =
+    (kScratchBytes - sizeof(int32_t) * (kScratchCounters + kScratchSeqInfo)) / sizeof(float);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// Per device: the scratch's device address (0 until sai_init has set it up
+// on that device) and whether that set-up failed.
+constexpr int kMaxScratchDevices = 64;
+struct ScratchSlot {
+  void* ptr = nullptr;
+  bool failed = false;
+};
+std::mutex g_scratch_mu;
+ScratchSlot g_scratch[kMaxScratchDevices];
 
 struct sai_tqcache {
   sai_tqcache_desc desc{};
@@ -274,6 +299,25 @@ SAI_API sai_status sai_init(int device, sai_ctx** out) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess) ctx->num_cus = prop.multiProcessorCount;
   if (ctx->num_cus <= 0) ctx->num_cus = 256;
+  // the no-allocation scratch of this device: its address, once, with the
+  // device current; its ticket counters must start at zero (every launch
+  // that merges in-kernel leaves them at zero again)
+  if (device < kMaxScratchDevices) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    ScratchSlot& sl = g_scratch[device];
+    if (!sl.ptr && !sl.failed) {
+      DeviceGuard dg(device);
+      void* ptr = nullptr;
+      hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e == hipSuccess && ptr)
+        e = hipMemset(ptr, 0, kScratchCounters * sizeof(int32_t));
+      if (e == hipSuccess) e = hipDeviceSynchronize();
+      if (e == hipSuccess && ptr)
+        sl.ptr = ptr;
+      else
+        sl.failed = true;
+    }
+  }
   *out = ctx;
   return SAI_OK;
 }
@@ -704,7 +748,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
                          const float* sin_cache, int32_t cache_rows, int32_t do_rotary,
                          int32_t rotary_interleaved, int32_t has_scale, float scale,
                          int32_t window, float* out, const void* k_new, const void* v_new,
-                         int32_t kv_dtype, void* stream) {
+                         int32_t kv_dtype, void* stream, DecodeWorkspace* fixed_ws = nullptr) {
   const char* op = "gqa_decode";
   const int32_t W = visible_span(c->layer_window[layer], window);
   const int D = c->desc.head_dim;
@@ -755,10 +799,24 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: bad work size", op);
   DeviceGuard dg(ctx->device);
   // the cache's own workspace (sized at creation for the automatic split; a
-  // smaller split set for tuning may grow it once, synchronously)
-  sai_status st = reserve_workspace(ctx, c->ws, (size_t)work * kvh * G * (D + 2),
-                                    (size_t)batch * 2, (size_t)batch * kvh);
-  if (st != SAI_OK) return st;
+  // smaller split set for tuning may grow it once, synchronously), or a fixed
+  // one that cannot grow
+  const size_t need_partials = (size_t)work * kvh * G * (D + 2);
+  DecodeWorkspace* ws = &c->ws;
+  if (fixed_ws) {
+    if (need_partials > fixed_ws->partial_floats || (size_t)batch * 2 > fixed_ws->seq_info_n ||
+        (size_t)batch * kvh > fixed_ws->counter_n)
+      return fail(ctx, SAI_ERR_UNSUPPORTED,
+                  "%s: the step needs %zu partial floats, %d sequences and %d sequence x kv head "
+                  "tickets; the fixed scratch holds %zu, %zu and %zu",
+                  op, need_partials, batch, batch * kvh, fixed_ws->partial_floats,
+                  fixed_ws->seq_info_n / 2, fixed_ws->counter_n);
+    ws = fixed_ws;
+  } else {
+    sai_status st = reserve_workspace(ctx, c->ws, need_partials, (size_t)batch * 2,
+                                      (size_t)batch * kvh);
+    if (st != SAI_OK) return st;
+  }
 
   sai::DecodeParams p{};
   p.q = q;
@@ -784,15 +842,15 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   p.waves = ctx->decode_waves ? ctx->decode_waves : (c->desc.quant == SAI_KV_INT4 ? 8 : 4);
   p.uniform_nsplit = uniform ? (int)n_first : 0;
   p.max_nsplit = (int)n_max;
-  p.partials = c->ws.partials;
-  p.seq_info = c->ws.seq_info;
+  p.partials = ws->partials;
+  p.seq_info = ws->seq_info;
   // automatic: the last workgroup merges when every sequence has the same
   // split count (one ticket per (sequence, kv head), measured faster at 16 x
   // 8k); ragged batches use the combine kernel (measured faster there). The
   // int4 kernel always uses the combine kernel.
   p.merge_in_kernel = c->desc.quant == SAI_KV_INT8 &&
                       (ctx->decode_merge == 1 || (ctx->decode_merge == 2 && uniform));
-  p.counters = c->ws.counters;
+  p.counters = ws->counters;
   p.k_new = k_new;
   p.v_new = v_new;
   p.kv_dtype = kv_dtype;
@@ -839,16 +897,15 @@ SAI_API sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, c
                        nullptr, SAI_DTYPE_F32, stream);
 }
 
-SAI_API sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
-                                      const void* q, int32_t q_dtype, const void* k_new,
-                                      const void* v_new, int32_t kv_dtype, int32_t batch,
-                                      int32_t num_heads, const float* cos_cache,
-                                      const float* sin_cache, int32_t cache_rows,
-                                      int32_t do_rotary, int32_t rotary_interleaved,
-                                      int32_t has_scale, float scale, int32_t window, float* out,
-                                      void* stream) {
-  if (!ctx || !c) return SAI_ERR_NULL;
-  const char* op = "gqa_with_cache";
+namespace {
+
+sai_status gqa_with_cache_impl(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
+                               int32_t q_dtype, const void* k_new, const void* v_new,
+                               int32_t kv_dtype, int32_t batch, int32_t num_heads,
+                               const float* cos_cache, const float* sin_cache,
+                               int32_t cache_rows, int32_t do_rotary, int32_t rotary_interleaved,
+                               int32_t has_scale, float scale, int32_t window, float* out,
+                               void* stream, const char* op, DecodeWorkspace* fixed_ws) {
   if (!k_new || !v_new) return fail(ctx, SAI_ERR_NULL, "%s: missing key/value", op);
   if (kv_dtype != SAI_DTYPE_F32 && kv_dtype != SAI_DTYPE_BF16)
     return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (want f32 or bf16)", op, kv_dtype);
@@ -864,9 +921,57 @@ SAI_API sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* c, int32_t laye
   if (st == SAI_OK)
     st = launch_decode(ctx, c, layer, q, q_dtype, batch, G, cos_cache, sin_cache, cache_rows,
                        do_rotary, rotary_interleaved, has_scale, scale, window, out, k_new,
-                       v_new, kv_dtype, stream);
+                       v_new, kv_dtype, stream, fixed_ws);
   if (st != SAI_OK) c->pending = prev_pending;
   return st;
+}
+
+}  // namespace
+
+SAI_API sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
+                                      const void* q, int32_t q_dtype, const void* k_new,
+                                      const void* v_new, int32_t kv_dtype, int32_t batch,
+                                      int32_t num_heads, const float* cos_cache,
+                                      const float* sin_cache, int32_t cache_rows,
+                                      int32_t do_rotary, int32_t rotary_interleaved,
+                                      int32_t has_scale, float scale, int32_t window, float* out,
+                                      void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  return gqa_with_cache_impl(ctx, c, layer, q, q_dtype, k_new, v_new, kv_dtype, batch, num_heads,
+                             cos_cache, sin_cache, cache_rows, do_rotary, rotary_interleaved,
+                             has_scale, scale, window, out, stream, "gqa_with_cache", nullptr);
+}
+
+SAI_API sai_status sai_gqa_with_cache_noalloc(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
+                                              const void* q, int32_t q_dtype, const void* k_new,
+                                              const void* v_new, int32_t kv_dtype, int32_t batch,
+                                              int32_t num_heads, const float* cos_cache,
+                                              const float* sin_cache, int32_t cache_rows,
+                                              int32_t do_rotary, int32_t rotary_interleaved,
+                                              int32_t has_scale, float scale, int32_t window,
+                                              float* out, void* stream) {
+  if (!ctx || !c) return SAI_ERR_NULL;
+  const char* op = "gqa_with_cache_noalloc";
+  void* base = nullptr;
+  if (ctx->device < kMaxScratchDevices) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    base = g_scratch[ctx->device].ptr;
+  }
+  if (!base)
+    return fail(ctx, SAI_ERR_HIP, "%s: the device scratch of device %d is not set up", op,
+                ctx->device);
+  // counters, then split ranges, then partials (the counters' region was
+  // cleared when the scratch was set up and is left at zero by every launch)
+  DecodeWorkspace ws;
+  ws.counters = (int32_t*)base;
+  ws.counter_n = kScratchCounters;
+  ws.seq_info = (int32_t*)base + kScratchCounters;
+  ws.seq_info_n = kScratchSeqInfo;
+  ws.partials = (float*)((int32_t*)base + kScratchCounters + kScratchSeqInfo);
+  ws.partial_floats = kScratchPartialFloats;
+  return gqa_with_cache_impl(ctx, c, layer, q, q_dtype, k_new, v_new, kv_dtype, batch, num_heads,
+                             cos_cache, sin_cache, cache_rows, do_rotary, rotary_interleaved,
+                             has_scale, scale, window, out, stream, op, &ws);
 }
 
 SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
