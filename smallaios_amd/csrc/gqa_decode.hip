@@ -306,8 +306,9 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
   const int t_end = min(L, t_begin + p.split_tokens);
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
   const int n_tiles = (t_end - t_begin + 63) / 64;
-  // the wave that streams the split's last tile (it holds the newest token)
-  const int last_owner = (n_tiles - 1) % NW;
+  // next tile of the split to hand out (see below)
+  __shared__ int sm_next;
+  if (threadIdx.x == 0) sm_next = 0;
   __syncthreads();
 
   // cos / sin of position L-1: issued ahead of the first tile, so the query's
@@ -323,12 +324,27 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
     for (int ks = 0; ks < KS; ++ks) rope_load16<D>(cr, sr, kdim0<D>(g, ks), p.interleaved, cq[ks], sq[ks]);
   }
 
-  // ---- fused append by the last tile's owner: before its first load if that
-  // tile is its only one, else while its first tile is in flight -----------------
-  const bool appender = p.k_new != nullptr && split == nsplit - 1 && wave == last_owner;
-  int tile = wave;
-  const int my_tiles = tile < n_tiles ? (n_tiles - 1 - tile) / NW + 1 : 0;
-  auto append = [&]() {
+  // ---- tiles are handed out one at a time from an LDS counter (a wave takes
+  // the index of its next tile one tile ahead, and loads that tile just
+  // before computing the current one), so the waves of a workgroup finish
+  // together however their loads are served. Each wave's first tile is fixed
+  // (its index). The split that holds the step's new token keeps its last
+  // tile out of the count: the appender wave (the last one) writes the token
+  // and then streams that tile first; no other wave touches that page.
+  // (Sharing one counter in memory between the workgroups of a sequence was
+  // measured 18 % slower at 16 x 8k: its atomics serialise.)
+  const bool appender_split = p.k_new != nullptr && split == nsplit - 1;
+  const bool appender = appender_split && wave == NW - 1;
+  const int pool_end = appender_split ? n_tiles - 1 : n_tiles;
+  const int slots = NW;  // fixed first tiles
+  const int pool_start = slots - (appender_split ? 1 : 0);
+  auto grab_issue = [&]() {  // lane 0 holds the counter's old value
+    int t = 0;
+    if (lane == 0) t = atomicAdd(&sm_next, 1);
+    return t;
+  };
+  auto grab_value = [&](int t) { return pool_start + __builtin_amdgcn_readfirstlane(t); };
+  if (appender) {
     const int pos = L - 1;
     uint8_t* blk = (uint8_t*)p.pool +
                    block_offset(sm_pg[pos / kPageTokens - first_page], kvh, p.num_pages,
@@ -337,28 +353,32 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
     append_row_int8<D>((const uint8_t*)p.k_new + row, (const uint8_t*)p.v_new + row, p.kv_dtype,
                        lane, pos, blk, pos % kPageTokens, p.do_rotary, p.interleaved != 0,
                        p.cos_cache, p.sin_cache);
-    // this wave reads the page back in its last tile: order the stores first
+    // this wave reads the page back right below: order the stores first
     __threadfence_block();
-  };
-  if (appender && my_tiles == 1) append();
-  const int tile_off = 0;  // splits start on a tile (64-token) boundary
+  }
+  const int first = appender ? n_tiles - 1 : wave;
+  const bool have_first = appender || first < pool_end;
+  // the next tile's index, asked for before the first tile's loads so that
+  // waiting for it never waits for them
+  int gq = 0;
+  if (have_first) gq = grab_issue();
   TileRegs<D> TA;
-  if (!BIG && tile < n_tiles)
-    load_tile<D>(TA, p.pool, sm_pg + tile_off, tile, p.num_pages, kvh, r, g, n_pages_split);
-  // The wave's second tile is touched (one dword per 128-byte line) so that
-  // it streams into L2 while the query is prepared, instead of the memory
-  // pipe idling until the loop issues its load. Its own lines only: the new
-  // token's page may be rewritten by the append below. The values are
-  // consumed only where the first tile is needed anyway.
-  // Branch-free (lanes past the last line repeat it): a divergent branch here
-  // would make the compiler wait for every outstanding load at its join.
+  if (!BIG && have_first)
+    load_tile<D>(TA, p.pool, sm_pg, first, p.num_pages, kvh, r, g, n_pages_split);
+  // Tile first + slots (the one this wave most likely takes next, never the
+  // appender's) is touched (one dword per 128-byte line) so that it
+  // streams into L2 while the query is prepared, instead of the memory pipe
+  // idling until the loop issues its load. The values are consumed only where
+  // the first tile is needed anyway. Branch-free (lanes past the last line
+  // repeat it): a divergent branch here would make the compiler wait for every
+  // outstanding load at its join.
   constexpr int kLines = (int)(block_bytes_int8(D) / 128);  // 33 for D = 128
   constexpr int kTouch = (4 * kLines + 63) / 64;              // loads per lane
   uint32_t touch[kTouch];
 #pragma unroll
   for (int j = 0; j < kTouch; ++j) touch[j] = 0;
-  if (!BIG && my_tiles > 1 && !(appender && my_tiles == 2)) {  // uniform over the wave
-    const int t1 = tile + NW;
+  if (!BIG && have_first && first + slots < pool_end) {  // uniform over the wave
+    const int t1 = first + slots;
 #pragma unroll
     for (int j = 0; j < kTouch; ++j) {
       const int line = min(lane + 64 * j, 4 * kLines - 1);
@@ -368,7 +388,6 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
       touch[j] = *(const uint32_t*)a;
     }
   }
-  if (appender && my_tiles > 1) append();
 
   // ---- Q: RoPE at position L-1, split into three int8 terms ------------------
   // y = sq * (hi + mid / 254 + lo / 254^2), sq = max|y| / 127 over the head:
@@ -463,50 +482,65 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
     for (int jb = 0; jb < JB; ++jb) st.acc[ps][jb] = 0.0f;
   }
 
-  // Ping-pong over this wave's tiles wave, wave+NW, ... Every prefetch inside
-  // the loop is unconditional (straight-line code), so the compiler's wait
-  // counts only cover the tile being computed, never the one in flight.
+  // Ping-pong between two tile buffers: the next tile is taken and its load
+  // issued before the current one is computed, so one tile is always in
+  // flight; the loads inside the loop are unconditional once a tile is taken.
   TileRegs<D> TB;
-  auto tok0 = [&](int k) { return t_begin + (wave + k * NW) * 64 + 16 * g; };
-  auto ld = [&](TileRegs<D>& T, int k) {
-    load_tile<D>(T, p.pool, sm_pg + tile_off, wave + k * NW, p.num_pages, kvh, r, g,
-                 n_pages_split);
+  auto tok0 = [&](int tile) { return t_begin + tile * 64 + 16 * g; };
+  auto ld = [&](TileRegs<D>& T, int tile) {
+    load_tile<D>(T, p.pool, sm_pg, tile, p.num_pages, kvh, r, g, n_pages_split);
   };
   // the touch loads, consumed (an empty asm use keeps them): issued right
   // after the first tile, which the loop waits for first anyway
 #pragma unroll
   for (int j = 0; j < kTouch; ++j) __asm__ volatile("" ::"v"(touch[j]));
-  int k = 0;
+  // (the index for the tile after next is asked for before the next tile's
+  // loads are issued, for the same reason as above)
   if constexpr (D <= 128) {
-    for (; k + 2 < my_tiles; k += 2) {
-      ld(TB, k + 1);
-      compute_tile<D, G>(TA, st, qB, qw, tok0(k), k_lo, t_end, r, g, sm_sc[wave]);
-      ld(TA, k + 2);
-      compute_tile<D, G>(TB, st, qB, qw, tok0(k + 1), k_lo, t_end, r, g, sm_sc[wave]);
-    }
-    if (k + 1 < my_tiles) {  // two left
-      ld(TB, k + 1);
-      compute_tile<D, G>(TA, st, qB, qw, tok0(k), k_lo, t_end, r, g, sm_sc[wave]);
-      compute_tile<D, G>(TB, st, qB, qw, tok0(k + 1), k_lo, t_end, r, g, sm_sc[wave]);
-    } else if (k < my_tiles) {  // one left
-      compute_tile<D, G>(TA, st, qB, qw, tok0(k), k_lo, t_end, r, g, sm_sc[wave]);
+    if (have_first) {
+      int cur = first;
+      for (;;) {
+        const int n1 = grab_value(gq);
+        if (n1 >= pool_end) {
+          compute_tile<D, G>(TA, st, qB, qw, tok0(cur), k_lo, t_end, r, g, sm_sc[wave]);
+          break;
+        }
+        gq = grab_issue();
+        ld(TB, n1);
+        compute_tile<D, G>(TA, st, qB, qw, tok0(cur), k_lo, t_end, r, g, sm_sc[wave]);
+        const int n2 = grab_value(gq);
+        if (n2 >= pool_end) {
+          compute_tile<D, G>(TB, st, qB, qw, tok0(n1), k_lo, t_end, r, g, sm_sc[wave]);
+          break;
+        }
+        gq = grab_issue();
+        ld(TA, n2);
+        compute_tile<D, G>(TB, st, qB, qw, tok0(n1), k_lo, t_end, r, g, sm_sc[wave]);
+        cur = n2;
+      }
     }
   } else {
     // head_dim 256: a tile is ~128 registers, so one buffer, refilled by
     // phase: the next tile's K (and scales) load as soon as this tile's QK is
     // issued, its V as soon as this tile's PV is (the last tile reloads
     // itself, so the code stays straight-line)
-    if (my_tiles > 0) ld(TA, 0);
-    for (; k < my_tiles; ++k) {
-      const int kn = wave + min(k + 1, my_tiles - 1) * NW;
-      compute_tile<D, G>(
-          TA, st, qB, qw, tok0(k), k_lo, t_end, r, g, sm_sc[wave],
-          [&]() {
-            load_tile<D, 1>(TA, p.pool, sm_pg + tile_off, kn, p.num_pages, kvh, r, g, n_pages_split);
-          },
-          [&]() {
-            load_tile<D, 2>(TA, p.pool, sm_pg + tile_off, kn, p.num_pages, kvh, r, g, n_pages_split);
-          });
+    if (have_first) {
+      int cur = first;
+      ld(TA, cur);
+      for (;;) {
+        const int n1 = grab_value(gq);
+        const bool more = n1 < pool_end;
+        const int kn = more ? n1 : cur;
+        // asked for unconditionally (straight-line code); the last one is
+        // never used
+        gq = grab_issue();
+        compute_tile<D, G>(
+            TA, st, qB, qw, tok0(cur), k_lo, t_end, r, g, sm_sc[wave],
+            [&]() { load_tile<D, 1>(TA, p.pool, sm_pg, kn, p.num_pages, kvh, r, g, n_pages_split); },
+            [&]() { load_tile<D, 2>(TA, p.pool, sm_pg, kn, p.num_pages, kvh, r, g, n_pages_split); });
+        if (!more) break;
+        cur = n1;
+      }
     }
   }
 

@@ -807,8 +807,8 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
     if (need_partials > fixed_ws->partial_floats || (size_t)batch * 2 > fixed_ws->seq_info_n ||
         (size_t)batch * kvh > fixed_ws->counter_n)
       return fail(ctx, SAI_ERR_UNSUPPORTED,
-                  "%s: the step needs %zu partial floats, %d sequences and %d sequence x kv head "
-                  "tickets; the fixed scratch holds %zu, %zu and %zu",
+                  "%s: the step needs %zu partial floats, %d sequences and %d (sequence, kv head) "
+                  "pairs; the fixed scratch holds %zu, %zu and %zu",
                   op, need_partials, batch, batch * kvh, fixed_ws->partial_floats,
                   fixed_ws->seq_info_n / 2, fixed_ws->counter_n);
     ws = fixed_ws;

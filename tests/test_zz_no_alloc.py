@@ -4,9 +4,9 @@ per-GPU scratch instead of the cache's workspace.
 Two calls in a row through the C ABI, the second with a smaller input (so the
 scratch still holds the first call's contents): each against
 sai_gqa_with_cache on an identical cache (same seeded inputs), to the path's
-bar (2e-3 abs + 1e-2 rel; the two run the same kernels, so the outputs are
-expected to be equal), against the oracle, and with the appended token's codes
-bit-exact. A step whose partials exceed the scratch is rejected with
+bar (2e-3 abs + 1e-2 rel; the two run the same kernels, but tiles go to waves
+in the order the waves ask for them, so the last bits may differ), against the
+oracle, and with the appended token's codes bit-exact. A step whose partials exceed the scratch is rejected with
 UNSUPPORTED and leaves the cache as it was.
 """
 import numpy as np
@@ -55,7 +55,6 @@ def test_noalloc_matches_with_cache(rt, call):
     got = fused(cases[1], q[1], *kv[1], noalloc=True)
     assert_close(got, want, f"noalloc vs with_cache, call {call}")
     log(f"  bit-identical to sai_gqa_with_cache: {np.array_equal(got, want)}")
-    assert np.array_equal(got, want), "same kernels, same merge order: equal outputs"
     c = cases[1]
     c.ocache.append(*kv[1], c.cos, c.sin, c.do_rotary, c.interleaved)
     assert_close(got, c.oracle_attend(q[1]), f"noalloc vs oracle, call {call}")
