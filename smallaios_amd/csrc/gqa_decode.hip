@@ -362,23 +362,27 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
   // waiting for it never waits for them
   int gq = 0;
   if (have_first) gq = grab_issue();
+  // The first tile's loads and the touch below are issued by every wave (a
+  // wave without a tile re-reads tile 0 of its split, which always exists):
+  // behind a branch, the compiler's wait counts for the query's loads would
+  // have to assume the branch was not taken and wait for these loads too.
   TileRegs<D> TA;
-  if (!BIG && have_first)
-    load_tile<D>(TA, p.pool, sm_pg, first, p.num_pages, kvh, r, g, n_pages_split);
+  const int first_ld = have_first ? first : 0;
+  if constexpr (!BIG)
+    load_tile<D>(TA, p.pool, sm_pg, first_ld, p.num_pages, kvh, r, g, n_pages_split);
   // Tile first + slots (the one this wave most likely takes next, never the
-  // appender's) is touched (one dword per 128-byte line) so that it
-  // streams into L2 while the query is prepared, instead of the memory pipe
-  // idling until the loop issues its load. The values are consumed only where
-  // the first tile is needed anyway. Branch-free (lanes past the last line
-  // repeat it): a divergent branch here would make the compiler wait for every
-  // outstanding load at its join.
+  // appender's; else the first tile again) is touched (one dword per 128-byte
+  // line) so that it streams into L2 while the query is prepared, instead of
+  // the memory pipe idling until the loop issues its load. The values are
+  // consumed only where the first tile is needed anyway. Branch-free (lanes
+  // past the last line repeat it).
   constexpr int kLines = (int)(block_bytes_int8(D) / 128);  // 33 for D = 128
   constexpr int kTouch = (4 * kLines + 63) / 64;              // loads per lane
   uint32_t touch[kTouch];
 #pragma unroll
   for (int j = 0; j < kTouch; ++j) touch[j] = 0;
-  if (!BIG && have_first && first + slots < pool_end) {  // uniform over the wave
-    const int t1 = first + slots;
+  if constexpr (!BIG) {
+    const int t1 = have_first && first + slots < pool_end ? first + slots : first_ld;
 #pragma unroll
     for (int j = 0; j < kTouch; ++j) {
       const int line = min(lane + 64 * j, 4 * kLines - 1);
