@@ -99,6 +99,18 @@ def prefill_flops(batch, hq, d, past, new):
     return 4 * d * hq * keys * batch
 
 
+def append_roofline(b, new, hkv, d, us):
+    """HBM roofline of the int8 append of `new` bf16 tokens per sequence:
+    K and V rows read (2 bytes an element), codes and two f32 scales per
+    (token, kv head) written, and one cos and one sin row of D/2 f32 per
+    position read."""
+    rows = b * new * hkv
+    alg = rows * d * 2 * 2 + rows * (2 * d + 8) + b * new * d * 4
+    gbps = alg / (us * 1e-6) / 1e9
+    return {"median_us": round(us, 2), "algorithmic_bytes": alg, "achieved_gbps": round(gbps, 1),
+            "peak_gbps": HBM_PEAK_GBPS, "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
 def traffic_from_profile(workload):
     """HBM bytes per decode-kernel launch measured with rocprofv3 --pmc
     (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of known size), if the
@@ -553,7 +565,7 @@ def main():
                        "step": "kv_append (2048 tokens) + gqa_prefill"},
             "tokens_per_s": round(b * new / (ms_step * 1e-3), 1),
             "prefill_kernel": {"median_us": round(k_us, 2), "flops": flops},
-            "append_kernel": {"median_us": round(float(np.median(aus)), 2)},
+            "append_kernel": append_roofline(b, new, hkv, d, float(np.median(aus))),
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},

@@ -20,6 +20,9 @@ namespace sai {
 
 namespace {
 
+// appends of at least this many tokens per sequence go by page blocks
+constexpr int kPageAppendMin = 4;
+
 template <int D>
 __device__ __forceinline__ void decode_row(const AppendParams& p, long row, int& b, int& s,
                                            int& h) {
@@ -46,6 +49,257 @@ __global__ __launch_bounds__(256) void kv_append_int8_kernel(AppendParams p) {
   append_row_int8<D>((const uint8_t*)p.k + src * esz, (const uint8_t*)p.v + src * esz, p.dtype,
                      lane, pos, blk, pos % kPageTokens, p.do_rotary, p.interleaved != 0,
                      p.cos_cache, p.sin_cache);
+}
+
+// ---------------------------------------------------- int8, page blocks ----
+// Multi-token appends: one workgroup per (sequence b, page, kv head h) block
+// that receives new tokens, W = D/32 waves. Each wave takes G = 64/L slots,
+// one per group of L = D/8 lanes (wave w, group g: slot g*W + w). Lane c of
+// a group holds dims [4c, 4c+4) and [D/2 + 4c, D/2 + 4c + 4): both elements
+// of every split-half RoPE pair, and whole interleaved pairs, so RoPE needs
+// no other lane; a token's absolute maximum is a reduction over its group
+// (DPP within rows of 16 lanes, permlane16_swap across two rows). The codes
+// are staged in LDS (K rows with a 16-byte pad, V as one 16-byte column per
+// dim, placed so that one instruction's writes fall in distinct banks) and
+// leave it in 16-byte stores, one per thread: K rows as contiguous pieces of
+// the block, V columns whole, with the old bytes of slots outside the
+// appended range kept. Per element the arithmetic is append_row_int8's (the
+// quotient by the scale as in quant4_int8), so the codes and
+// scales are the same bits.
+// Four consecutive elements (f32 or bf16) at byte offset `off` of `base`.
+template <bool BF16>
+__device__ __forceinline__ void load4(const uint8_t* base, uint32_t off, float (&x)[4]) {
+  if constexpr (BF16) {
+    const uint2 w = *(const uint2*)(base + off);
+    x[0] = __uint_as_float(w.x << 16), x[1] = __uint_as_float(w.x & 0xFFFF0000u);
+    x[2] = __uint_as_float(w.y << 16), x[3] = __uint_as_float(w.y & 0xFFFF0000u);
+  } else {
+    const float4 v = *(const float4*)(base + off);
+    x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w;
+  }
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t max_dpp(uint32_t v) {
+  const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+  return v > o ? v : o;
+}
+
+// Maximum over aligned groups of L lanes (8, 16 or 32) of a non-negative,
+// non-NaN float: its bits order as unsigned integers, and the maximum is
+// order-free, so this equals wave_max over the same elements.
+template <int L>
+__device__ __forceinline__ float group_max(float x) {
+  uint32_t v = __float_as_uint(x);
+  v = max_dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = max_dpp<0x4E>(v);   // quad_perm [2,3,0,1]: every quad holds its maximum
+  v = max_dpp<0x141>(v);  // row_half_mirror: the other quad of each 8
+  if constexpr (L >= 16) v = max_dpp<0x140>(v);  // row_mirror: the other 8 of 16
+  if constexpr (L >= 32) {
+    // rows 0 and 1 (2 and 3) meet: one copy in each result
+    const auto sw = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = sw[0] > sw[1] ? sw[0] : sw[1];
+  }
+  return __uint_as_float(v);
+}
+
+// The quotient x / s of append_row_int8 (s = fl(m / 127) for the row's
+// maximum m >= |x|), taken without the division. r = 1/s from v_rcp_f32
+// (within 1 ulp) when s is a normal finite float, NaN otherwise. Then
+// |x / s| <= 127 (1 + 2^-23), x * r is within 1.5 * 2^-23 relative (2.3e-5)
+// of x / s, and the correctly rounded quotient fl(x / s) within another
+// 3.8e-6 (half an ulp at 128). Where x * r lies farther than 2^-14 from
+// every half-integer, fl(x / s) falls in the same unit interval around the
+// same integer n = rintf(x * r), which is then rintf(fl(x / s)), a code in
+// [-127, 127]. quant4_fast returns those codes (packed LSB first) and flags
+// the other elements (near a half-integer, or NaN) in `near`.
+__device__ __forceinline__ uint32_t quant4_fast(const float (&x)[4], float r, bool (&near)[4]) {
+#pragma clang fp contract(off)
+  uint32_t w = 0u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float a = x[j] * r;
+    const float n = rintf(a);
+    near[j] = !(fabsf(a - n) < 0.5f - 0x1p-14f);       // NaN too
+    w |= ((uint32_t)(int32_t)n & 0xFFu) << (8 * j);  // a flagged element is redone
+  }
+  return w;
+}
+
+// Code of an element quant4_fast flagged. Near the half-integer h (|h| >= 1,
+// s within [2^-100, 2^100]) it is settled exactly from e = fma(-h, s, x):
+// its sign is that of x / s - h, and u = s * ulp(h)/2 is exact, so |e| < u
+// means |x / s - h| < ulp(h)/2, fl(x / s) == h and the code is rintf(h)
+// (the even neighbour); |e| > u means fl(x / s) lies beyond h on the side of
+// e, inside the unit interval, and the code is h -+ 1/2. Everything else
+// (|e| == u, NaN, tiny h, extreme scales) takes append_row_int8's own steps:
+// the correctly rounded division, rintf, the saturating cast and the clamp
+// (in float first, which gives the same integer; NaN gives 0).
+__device__ __forceinline__ uint32_t quant_settle(float x, float s, float r) {
+#pragma clang fp contract(off)
+  const float a = x * r;
+  const float h = floorf(a) + 0.5f;
+  const float e = fmaf(-h, s, x);
+  const float p2 = __uint_as_float(__float_as_uint(h) & 0x7F800000u);  // 2^exponent(h)
+  const float u = s * p2 * 0x1p-24f;
+  const bool ok = s >= 0x1p-100f && s <= 0x1p100f && fabsf(h) >= 1.0f && e == e;
+  float code = fabsf(e) < u ? rintf(h) : (e > 0.0f ? h + 0.5f : h - 0.5f);
+  if (!(ok && fabsf(e) != u)) code = rintf(x / s);
+  const int32_t q = code == code ? (int32_t)fminf(fmaxf(code, -128.0f), 127.0f) : 0;
+  return (uint32_t)q & 0xFFu;
+}
+
+// quant4_fast, then quant_settle for the flagged elements (a branch each,
+// taken only when some lane flagged that element).
+__device__ __forceinline__ uint32_t quant4_int8(const float (&x)[4], float s, float r) {
+  bool near[4];
+  uint32_t w = quant4_fast(x, r, near);
+  if (near[0] | near[1] | near[2] | near[3]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (near[j]) w = (w & ~(0xFFu << (8 * j))) | (quant_settle(x[j], s, r) << (8 * j));
+  }
+  return w;
+}
+
+// ROPE: 0 none, 1 split halves (d, d + D/2), 2 interleaved (2i, 2i + 1).
+// Grid (kv_heads, pages_per_seq, batch). The launch keeps s_new * kv_heads *
+// D * 4 (the byte offset of a row within a sequence's new K or V) below 2^31.
+template <int D, bool BF16, int ROPE>
+__global__ __launch_bounds__(2 * D) void kv_append_page_int8_kernel(AppendParams p) {
+  constexpr int L = D / 8;            // lanes per token
+  constexpr int W = D / 32;           // waves: kPageTokens / (64 / L)
+  constexpr int HALF = D / 2;
+  constexpr int KS = D + 16;          // LDS K row stride (bytes)
+  constexpr uint32_t ESZ = BF16 ? 2 : 4;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = blockIdx.x, b = blockIdx.z;
+  const int start = p.seq_lens[b];
+  const int page_idx = start / kPageTokens + (int)blockIdx.y;
+  const int t0 = page_idx * kPageTokens;  // position of slot 0
+  const int lo = max(start, t0) - t0;     // new slots [lo, hi)
+  const int hi = min(start + p.s_new, t0 + kPageTokens) - t0;
+  if (lo >= hi) return;  // a page past the new tokens (the whole workgroup)
+  const int page = p.page_table[(size_t)b * p.max_pages + page_idx];
+  uint8_t* blk = p.pool + block_offset(page, h, p.num_pages, block_bytes_int8(D));
+  const bool partial = lo > 0 || hi < kPageTokens;
+
+  // threads D .. 2D-1 (waves W/2 ..) store V column tid - D: the old column
+  // of a partial page first, so that its latency overlaps the work below
+  uint4 vold = uint4{0u, 0u, 0u, 0u};
+  if (partial && w >= W / 2) vold = *(const uint4*)(blk + (size_t)16 * D + (size_t)(tid - D) * 16);
+
+  const int c = lane % L, g = lane / L;
+  const int t = g * W + w;  // this group's slot
+  // a slot outside the new range reads the nearest new row (its codes are
+  // never stored), so every address stays inside the inputs
+  const uint32_t srow = (uint32_t)min(max(t0 + t - start, 0), p.s_new - 1);
+  const size_t row0 = ((size_t)b * p.s_new * p.kv_heads + h) * D * ESZ;  // (b, token 0, h)
+  const uint8_t* kbase = (const uint8_t*)p.k + row0;
+  const uint8_t* vbase = (const uint8_t*)p.v + row0;
+  const uint32_t off = (srow * (uint32_t)p.kv_heads * D + 4 * c) * ESZ;  // bytes
+  float xa[4], xb[4], va[4], vb[4];
+  load4<BF16>(kbase, off, xa);
+  load4<BF16>(kbase, off + HALF * ESZ, xb);
+  load4<BF16>(vbase, off, va);
+  load4<BF16>(vbase, off + HALF * ESZ, vb);
+  // the tables' rows from position start on
+  const uint8_t* cos0 = (const uint8_t*)(p.cos_cache + (size_t)start * HALF);
+  const uint8_t* sin0 = (const uint8_t*)(p.sin_cache + (size_t)start * HALF);
+  if constexpr (ROPE == 1) {
+    // dims 4c + j and HALF + 4c + j share table entry 4c + j
+    const uint32_t o = (srow * HALF + 4 * c) * 4;
+    const float4 cv = *(const float4*)(cos0 + o);
+    const float4 sv = *(const float4*)(sin0 + o);
+    const float ca[4] = {cv.x, cv.y, cv.z, cv.w}, sa[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x0 = xa[j], x1 = xb[j];
+      xa[j] = rope_pair_elem(ca[j], sa[j], x0, x1, true);
+      xb[j] = rope_pair_elem(ca[j], sa[j], x1, x0, false);
+    }
+  } else if constexpr (ROPE == 2) {
+    // pair (2i, 2i + 1) uses entry i: 2c, 2c + 1 and HALF/2 + 2c, + 1
+    const uint32_t o = (srow * HALF + 2 * c) * 4;
+    const float2 c0 = *(const float2*)(cos0 + o);
+    const float2 s0 = *(const float2*)(sin0 + o);
+    const float2 c1 = *(const float2*)(cos0 + o + HALF * 2);
+    const float2 s1 = *(const float2*)(sin0 + o + HALF * 2);
+    const float ca[2] = {c0.x, c0.y}, sa[2] = {s0.x, s0.y};
+    const float cb[2] = {c1.x, c1.y}, sb[2] = {s1.x, s1.y};
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float x0 = xa[2 * e], x1 = xa[2 * e + 1];
+      xa[2 * e] = rope_pair_elem(ca[e], sa[e], x0, x1, true);
+      xa[2 * e + 1] = rope_pair_elem(ca[e], sa[e], x1, x0, false);
+      x0 = xb[2 * e], x1 = xb[2 * e + 1];
+      xb[2 * e] = rope_pair_elem(cb[e], sb[e], x0, x1, true);
+      xb[2 * e + 1] = rope_pair_elem(cb[e], sb[e], x1, x0, false);
+    }
+  }
+  // fmaxf from 0 skips NaN elements, as in append_row_int8: the lane maxima
+  // are non-negative and never NaN
+  float ak = 0.0f, av = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ak = fmaxf(ak, fmaxf(fabsf(xa[j]), fabsf(xb[j])));
+    av = fmaxf(av, fmaxf(fabsf(va[j]), fabsf(vb[j])));
+  }
+  ak = group_max<L>(ak);
+  av = group_max<L>(av);
+  const float sk = (ak > 0.0f) ? ak / 127.0f : 1.0f;
+  const float sv = (av > 0.0f) ? av / 127.0f : 1.0f;
+  const float rk = (sk >= 0x1p-126f && sk <= 0x1.fffffep127f) ? __builtin_amdgcn_rcpf(sk)
+                                                              : __builtin_nanf("");
+  const float rv = (sv >= 0x1p-126f && sv <= 0x1.fffffep127f) ? __builtin_amdgcn_rcpf(sv)
+                                                              : __builtin_nanf("");
+  const uint32_t ka = quant4_int8(xa, sk, rk), kb = quant4_int8(xb, sk, rk);
+  const uint32_t qa = quant4_int8(va, sv, rv), qb = quant4_int8(vb, sv, rv);
+
+  __shared__ __align__(16) uint8_t sm_k[kPageTokens * KS];
+  __shared__ __align__(16) uint8_t sm_v[kPageTokens * D];  // column d at 16 d
+  *(uint32_t*)&sm_k[t * KS + 4 * c] = ka;
+  *(uint32_t*)&sm_k[t * KS + HALF + 4 * c] = kb;
+  uint8_t* vcol = &sm_v[64 * c + t];  // dim 4c, slot t
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    vcol[16 * j] = (uint8_t)(qa >> (8 * j));
+    vcol[16 * (HALF + j)] = (uint8_t)(qb >> (8 * j));
+  }
+  if (t >= lo && t < hi) {
+    if (c == 0) ((float*)(blk + 32 * D))[t] = sk;
+    if (c == 1) ((float*)(blk + 32 * D + 64))[t] = sv;
+  }
+  __syncthreads();
+
+  if (w < W / 2) {
+    // K: 16-byte piece tid of the 16 rows, stored when its row is new
+    constexpr int CHUNKS = D / 16;  // pieces of a row
+    const int tr = tid / CHUNKS;
+    const uint4 v = *(const uint4*)&sm_k[tr * KS + 16 * (tid % CHUNKS)];
+    if (tr >= lo && tr < hi) *(uint4*)(blk + (size_t)tid * 16) = v;
+  } else {
+    // V: column d (16 slots), new slots from the tile, on a partial page the
+    // others kept
+    const int d = tid - D;
+    uint4 v = *(const uint4*)&sm_v[16 * d];
+    if (partial) {
+      // byte k of word q is slot 4q + k: 0xFF where the slot keeps its code
+      const uint32_t fresh = (1u << hi) - (1u << lo);  // bits lo .. hi-1
+      uint32_t keep[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t nib = (~fresh >> (4 * q)) & 15u;
+        keep[q] = ((nib * 0x00204081u) & 0x01010101u) * 0xFFu;
+      }
+      v.x = (v.x & ~keep[0]) | (vold.x & keep[0]);
+      v.y = (v.y & ~keep[1]) | (vold.y & keep[1]);
+      v.z = (v.z & ~keep[2]) | (vold.z & keep[2]);
+      v.w = (v.w & ~keep[3]) | (vold.w & keep[3]);
+    }
+    *(uint4*)(blk + (size_t)16 * D + (size_t)d * 16) = v;
+  }
 }
 
 // ---------------------------------------------------------------- int4 ----
@@ -139,9 +393,48 @@ __global__ void seq_advance_kernel(int32_t* seq_lens, int batch, int pending) {
   if (i < batch) seq_lens[i] += pending;
 }
 
+template <int D, bool BF16>
+void launch_page_int8_dt(dim3 grid, hipStream_t st, const AppendParams& p, int rope) {
+  if (rope == 0)
+    hipLaunchKernelGGL((kv_append_page_int8_kernel<D, BF16, 0>), grid, dim3(2 * D), 0, st, p);
+  else if (rope == 1)
+    hipLaunchKernelGGL((kv_append_page_int8_kernel<D, BF16, 1>), grid, dim3(2 * D), 0, st, p);
+  else
+    hipLaunchKernelGGL((kv_append_page_int8_kernel<D, BF16, 2>), grid, dim3(2 * D), 0, st, p);
+}
+
+template <int D>
+void launch_page_int8(dim3 grid, hipStream_t st, const AppendParams& p, bool bf, int rope) {
+  if (bf)
+    launch_page_int8_dt<D, true>(grid, st, p, rope);
+  else
+    launch_page_int8_dt<D, false>(grid, st, p, rope);
+}
+
 }  // namespace
 
 hipError_t launch_kv_append(const AppendParams& p, int head_dim, int quant, hipStream_t st) {
+  // the page kernel reads 8 or 16 bytes of a row at once: rows must start
+  // 16-byte aligned; its grid is (kv_heads, pages, batch) and its in-sequence
+  // row offsets are 32-bit
+  const bool aligned = (((uintptr_t)p.k | (uintptr_t)p.v) & 15u) == 0;
+  const int pages = (p.s_new + kPageTokens - 1) / kPageTokens + 1;  // any start
+  const bool fits = pages <= 65535 && p.batch <= 65535 &&
+                    (long)p.s_new * p.kv_heads * head_dim * 4 < (1L << 31);
+  if (quant == kQuantInt8 && p.s_new >= kPageAppendMin && aligned && fits) {
+    const dim3 grid((unsigned)p.kv_heads, (unsigned)pages, (unsigned)p.batch);
+    const bool bf = p.dtype == kDtypeBf16;
+    const int rope = !p.do_rotary ? 0 : (p.interleaved ? 2 : 1);
+    if (head_dim == 64)
+      launch_page_int8<64>(grid, st, p, bf, rope);
+    else if (head_dim == 128)
+      launch_page_int8<128>(grid, st, p, bf, rope);
+    else if (head_dim == 256)
+      launch_page_int8<256>(grid, st, p, bf, rope);
+    else
+      return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   if (quant == kQuantInt8) {
     const long rows = (long)p.batch * p.s_new * p.kv_heads;
     const dim3 grid((unsigned)((rows + 3) / 4));

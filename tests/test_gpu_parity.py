@@ -44,6 +44,48 @@ def test_append_variants_bit_exact(rt, d, interleaved, rot, kv_dtype):
     c.check_codes()
 
 
+@pytest.mark.parametrize("d,interleaved,kv_dtype", [
+    (64, False, "f32"), (64, True, "bf16"), (128, False, "bf16"), (128, True, "f32"),
+    (256, False, "bf16"), (256, True, "f32")])
+def test_append_page_blocks_bit_exact(rt, d, interleaved, kv_dtype):
+    """Multi-token appends take the page-block kernel (one wave per page
+    block): 20 new tokens from starts 13, 0, 31 and 16 span two or three
+    pages, first and last page partial or whole; the slots before the start
+    keep their codes. 3 tokens take the per-row kernel, and the results of
+    both meet bit-exact in one cache."""
+    log(f"append page blocks d={d} interleaved={interleaved} {kv_dtype}")
+    c = Case(rt, 0xB10C + d, 4, 8, 2, d, [13, 0, 31, 16], 20, theta=5e5, kv_dtype=kv_dtype,
+             permute_pages=True, interleaved=interleaved, extra_tokens=3)
+    c.step_kv()
+    c.check_codes()
+    c.cache.advance()
+    k, v = c.kv(3)
+    c.append_both(k, v)
+    c.check_codes()
+
+
+def test_append_unaligned_rows_bit_exact(rt):
+    """Rows that do not start 16-byte aligned (a view 4 bytes into its
+    buffer) are appended by the per-row kernel, with the same codes."""
+    import torch
+    log("append: 4-byte-offset K/V views, 12 tokens")
+    c = Case(rt, 0xA11, 2, 8, 2, 128, [5, 22], 12, theta=5e5, permute_pages=True)
+    k, v = c.kv(12)
+
+    def offset_view(x):
+        flat = torch.zeros(x.size + 1, dtype=torch.float32, device="cuda")
+        flat[1:] = torch.from_numpy(x.reshape(-1)).cuda()
+        view = flat[1:].view(x.shape)
+        assert view.data_ptr() % 16 == 4
+        return view
+
+    kd, vd = offset_view(k), offset_view(v)
+    c.cache.append(0, kd, vd, c.batch, 12, c.cos_d, c.sin_d, c.cos.shape[0], True, False)
+    c.ocache.append(k, v, c.cos, c.sin, True, False)
+    torch.cuda.synchronize()
+    c.check_codes()
+
+
 def test_append_special_values(rt):
     """Zero rows, huge/tiny magnitudes, inf and NaN keep the codes bit-exact."""
     log("append special values")
