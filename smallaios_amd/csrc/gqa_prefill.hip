@@ -20,10 +20,11 @@
 //            read from LDS serves both row blocks of the wave.
 //   PV       A = P * s_v (f16), B = V (LDS f16); each V fragment serves both
 //            row blocks.
-// Scores: s = <q', k> * s_k[t], online softmax in the log2 domain. Only tiles
+// Scores: s = <q', k> * s_k[t], online softmax in the log2 domain against a
+// per-row reference point that moves only when a tile's scores rise more than
+// kMaxLead above it (so most tiles skip the accumulator rescale). Only tiles
 // that cross the causal diagonal (or the end of the sequence), or the first
-// key of a sliding window, apply the mask;
-// the accumulator rescale is skipped when no row maximum moved.
+// key of a sliding window, apply the mask.
 #include <type_traits>
 
 #include "sai_internal.h"
@@ -72,6 +73,11 @@ __device__ __forceinline__ float xgroup_sum(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// How far (log2 units) a row's scores may rise above its reference point
+// before the reference moves: softmax weights stay <= 2^kMaxLead = 4, so
+// p * s_v stays inside binary16 for V rows up to |v| ~ 2e6.
+constexpr float kMaxLead = 2.0f;
 
 template <int D, bool KLO = false>
 struct PrefillTile {
@@ -420,10 +426,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   __syncthreads();
 
   // ---- online softmax state ----------------------------------------------------
+  // m_run: the row's reference point (set from its first visible keys; 0 only
+  // while the row has seen none), l_run: sum of exp2(score - m_run)
   float m_run[RB], l_run[RB];  // lane (row r): row r of block rb
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    m_run[rb] = -INFINITY;
+    m_run[rb] = 0.0f;
     l_run[rb] = 0.0f;
   }
   v4f acc[RB][JB];  // lane (dim r of block jb, g): rows 4g+e of block rb
@@ -439,7 +447,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
     if (more) load_stage(t0 + 64);
 
     // S^T for both row blocks: 4 column blocks of 16 tokens; k steps outer so
-    // that eight independent accumulation chains interleave on the MFMA pipe
+    // that eight independent accumulation chains interleave on the MFMA pipe.
+    // s holds each score relative to its row's running maximum:
+    // s = <q', k> * s_k - m_run
     float s[RB][4][4];
     {
       v4f c[4][RB];
@@ -484,7 +494,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s[rb][cb][e] = INT4 ? c[cb][rb][e] : c[cb][rb][e] * skx[e];
+          for (int e = 0; e < 4; ++e)
+            s[rb][cb][e] = INT4 ? c[cb][rb][e] - m_run[rb]
+                                : __builtin_fmaf(c[cb][rb][e], skx[e], -m_run[rb]);
       }
     }
     if (tile >= full_tiles || tile < lo_full) {
@@ -500,8 +512,13 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
           }
     }
 
-    v8h pa[RB][2];
-    float alpha[RB];
+    // The running maximum only moves when a row's tile maximum exceeds it by
+    // more than kMaxLead (or on the row's first visible keys), so p = exp2(s)
+    // stays <= 2^kMaxLead and most tiles skip the accumulator rescale.
+    // Any reference point gives the same softmax; it only has to keep p and
+    // the sums in range.
+    float lead[RB];
+    bool move = false;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       float mt = -INFINITY;
@@ -510,9 +527,34 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 #pragma unroll
         for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[rb][cb][e]);
       mt = xgroup_max(mt);
-      const float m_new = fmaxf(m_run[rb], mt);
-      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      alpha[rb] = fast_exp2(m_run[rb] - m_use);
+      const bool row_moves = mt > kMaxLead || (l_run[rb] == 0.0f && mt != -INFINITY);
+      lead[rb] = row_moves ? mt : 0.0f;
+      move = move || row_moves;
+    }
+    if (__builtin_amdgcn_ballot_w64(move) != 0) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        m_run[rb] += lead[rb];
+        const float alpha = fast_exp2(-lead[rb]);  // 1 for rows that keep their max
+        l_run[rb] *= alpha;
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[rb][cb][e] -= lead[rb];
+        // accumulator rows 4g+e: the alpha of row j lives in lane j
+        float ae[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ae[e] = __shfl(alpha, 4 * g + e, 64);
+#pragma unroll
+        for (int jb = 0; jb < JB; ++jb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[rb][jb][e] *= ae[e];
+      }
+    }
+
+    v8h pa[RB][2];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
       float psum = 0.0f;
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
@@ -523,32 +565,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float pe = fast_exp2(s[rb][cb][e] - m_use);
+          const float pe = fast_exp2(s[rb][cb][e]);
           psum += pe;
           pa[rb][cb >> 1][(cb & 1) * 4 + e] = (_Float16)(INT4 ? pe : pe * svx[e]);
         }
       }
-      psum = xgroup_sum(psum);
-      l_run[rb] = l_run[rb] * alpha[rb] + psum;
-      m_run[rb] = m_new;
-    }
-
-    // rescale the accumulator rows 4g+e (alpha of row j lives in lane j),
-    // unless no row of the wave moved its maximum
-    bool moved = false;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) moved = moved || alpha[rb] != 1.0f;
-    if (__builtin_amdgcn_ballot_w64(moved) != 0) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        float ae[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ae[e] = __shfl(alpha[rb], 4 * g + e, 64);
-#pragma unroll
-        for (int jb = 0; jb < JB; ++jb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[rb][jb][e] *= ae[e];
-      }
+      l_run[rb] += xgroup_sum(psum);
     }
 #pragma unroll
     for (int kst = 0; kst < 2; ++kst)
