@@ -79,6 +79,10 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // p * s_v stays inside binary16 for V rows up to |v| ~ 2e6.
 constexpr float kMaxLead = 2.0f;
 
+// V fragments read ahead of the PV MFMAs that consume them
+constexpr int kVPrefetch = 6;
+constexpr int kVPrefetchInt4 = 3;  // int4 keeps its K lo tile reads and has fewer spare registers
+
 template <int D, bool KLO = false>
 struct PrefillTile {
   static constexpr int KROW = D + 8;      // padded f16 row of the K tile
@@ -105,10 +109,41 @@ struct TileStage {
   float sc;
 };
 
+// Page ids (pool blocks) a thread's staging loads of one 64-token tile touch:
+// chunk i of the K and V loads (c = tid + NT i) lies in local page c / D for
+// int8, and in c / (16 * D/32) (K) and c / D (V) for int4; the first 128
+// threads (int8) also load one scale of token tid & 63. They are loaded one
+// tile ahead, so the tile's code loads never wait on a page-table read.
+template <int D, int NT, bool INT4>
+struct StagePages {
+  static constexpr int KN = INT4 ? 64 * (D / 32) : 64 * (D / 16);  // K chunks of a tile
+  static constexpr int VN = 4 * D;                                  // V chunks of a tile
+  static constexpr int KC = (KN + NT - 1) / NT;
+  static constexpr int VC = (VN + NT - 1) / NT;
+  int k[KC];
+  int v[VC];
+  int s;
+
+  __device__ __forceinline__ void load(const int32_t* pt, int tile, int last_page, int tid) {
+#pragma unroll
+    for (int i = 0; i < KC; ++i) {
+      const int c = min(tid + NT * i, KN - 1);
+      const int lp = INT4 ? c / (16 * (D / 32)) : c / D;
+      k[i] = pt[min(4 * tile + lp, last_page)];
+    }
+#pragma unroll
+    for (int i = 0; i < VC; ++i) {
+      const int c = min(tid + NT * i, VN - 1);
+      v[i] = pt[min(4 * tile + c / D, last_page)];
+    }
+    s = INT4 ? 0 : pt[min(4 * tile + (tid & 63) / kPageTokens, last_page)];
+  }
+};
+
 template <int D, int NT>
 __device__ __forceinline__ void stage_load(TileStage<D, NT>& S, const PrefillParams& p,
-                                           const int32_t* pt, int kvh, int t0, int last_page,
-                                           int total, int tid) {
+                                           const StagePages<D, NT, false>& P, int kvh, int t0,
+                                           int tid) {
   constexpr size_t BB = block_bytes_int8(D);
 #pragma unroll
   for (int i = 0; i < TileStage<D, NT>::KC; ++i) {
@@ -116,33 +151,31 @@ __device__ __forceinline__ void stage_load(TileStage<D, NT>& S, const PrefillPar
     if (TileStage<D, NT>::KN % NT != 0 && c >= TileStage<D, NT>::KN) break;
     const int tok = c / (D / 16);
     const int dp = c % (D / 16);
-    const int pg = min((t0 + tok) / kPageTokens, last_page);
-    const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
+    const uint8_t* blk = p.pool + block_offset(P.k[i], kvh, p.num_pages, BB);
     S.kc[i] = *(const uint4*)(blk + (size_t)((t0 + tok) % kPageTokens) * D + 16 * dp);
   }
 #pragma unroll
   for (int i = 0; i < TileStage<D, NT>::VC; ++i) {
     const int c = tid + NT * i;
     if (TileStage<D, NT>::VN % NT != 0 && c >= TileStage<D, NT>::VN) break;
-    const int cb = c / D;
     const int d = c % D;
-    const int pg = min(t0 / kPageTokens + cb, last_page);
-    const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
+    const uint8_t* blk = p.pool + block_offset(P.v[i], kvh, p.num_pages, BB);
     S.vc[i] = *(const uint4*)(blk + 16 * D + (size_t)d * 16);
   }
+  // the first 128 threads load one scale each; tokens past the sequence end
+  // are zeroed when the tile is stored (a select here would wait for the load)
   S.sc = 0.0f;
   if (tid < 128) {
     const int which = tid >> 6;
     const int tok = tid & 63;
-    const int pg = min((t0 + tok) / kPageTokens, last_page);
-    const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
-    const float v = ((const float*)(blk + 32 * D + 64 * which))[(t0 + tok) % kPageTokens];
-    S.sc = t0 + tok < total ? v : 0.0f;
+    const uint8_t* blk = p.pool + block_offset(P.s, kvh, p.num_pages, BB);
+    S.sc = ((const float*)(blk + 32 * D + 64 * which))[(t0 + tok) % kPageTokens];
   }
 }
 
 template <int D, int NT, class Tile>
-__device__ __forceinline__ void stage_store(const TileStage<D, NT>& S, Tile& T, int tid) {
+__device__ __forceinline__ void stage_store(const TileStage<D, NT>& S, Tile& T, int t0, int total,
+                                            int tid) {
   constexpr int KROW = Tile::KROW;
   constexpr int VROW = Tile::VROW;
 #pragma unroll
@@ -179,10 +212,11 @@ __device__ __forceinline__ void stage_store(const TileStage<D, NT>& S, Tile& T, 
     }
   }
   if (tid < 128) {
+    const float sc = t0 + (tid & 63) < total ? S.sc : 0.0f;
     if (tid < 64)
-      T.sk[tid] = S.sc;
+      T.sk[tid] = sc;
     else
-      T.sv[tid - 64] = S.sc;
+      T.sv[tid - 64] = sc;
   }
 }
 
@@ -214,17 +248,18 @@ __device__ __forceinline__ float half_hi(uint32_t w) {
 
 template <int D, int NT>
 __device__ __forceinline__ void stage_load4(TileStage4<D, NT>& S, const PrefillParams& p,
-                                            const int32_t* pt, int kvh, int t0, int last_page,
+                                            const StagePages<D, NT, true>& P, int kvh, int t0,
                                             int tid) {
   constexpr size_t BB = block_bytes_int4(D);
   constexpr int NG = D / 32;
+  static_assert(StagePages<D, NT, true>::KC == TileStage4<D, NT>::KC &&
+                StagePages<D, NT, true>::VC == TileStage4<D, NT>::VC, "chunk counts");
 #pragma unroll
   for (int i = 0; i < TileStage4<D, NT>::KC; ++i) {
     const int c = min(tid + NT * i, TileStage4<D, NT>::KN - 1);  // spare threads repeat the last
     const int tok = c / NG;
     const int grp = c % NG;
-    const int pg = min((t0 + tok) / kPageTokens, last_page);
-    const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
+    const uint8_t* blk = p.pool + block_offset(P.k[i], kvh, p.num_pages, BB);
     const int slot = (t0 + tok) % kPageTokens;
     S.kc[i] = *(const uint4*)(blk + (size_t)slot * (D / 2) + 16 * grp);
     S.kp[i] = *(const uint32_t*)(blk + 16 * D + (size_t)(slot * NG + grp) * 4);
@@ -232,10 +267,8 @@ __device__ __forceinline__ void stage_load4(TileStage4<D, NT>& S, const PrefillP
 #pragma unroll
   for (int i = 0; i < TileStage4<D, NT>::VC; ++i) {
     const int c = min(tid + NT * i, TileStage4<D, NT>::VN - 1);
-    const int cb = c / D;
     const int d = c % D;
-    const int pg = min(t0 / kPageTokens + cb, last_page);
-    const uint8_t* blk = p.pool + block_offset(pt[pg], kvh, p.num_pages, BB);
+    const uint8_t* blk = p.pool + block_offset(P.v[i], kvh, p.num_pages, BB);
     S.vc[i] = *(const uint2*)(blk + 8 * D + (size_t)d * 8);
     const uint8_t* par = blk + 16 * D + 64 * NG + (size_t)(d / 32) * 4;
 #pragma unroll
@@ -323,7 +356,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   constexpr int VROW = Tile::VROW;
   constexpr int HALF = D / 2;
 
-  __shared__ Tile sT[2];
+  // int8 at head_dim <= 128 keeps four tiles in LDS and computes two per
+  // barrier (4 x 38.4 KB at 128); the larger int4 and head_dim-256 tiles keep two
+  constexpr int NSLOT = (!INT4 && D <= 128) ? 4 : 2;
+  constexpr int PER_BARRIER = NSLOT / 2;
+  __shared__ Tile sT[NSLOT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -355,19 +392,23 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   // first tile in flight while Q is prepared
   typedef typename std::conditional<INT4, TileStage4<D, NT>, TileStage<D, NT>>::type Stage;
   Stage S;
+  StagePages<D, NT, INT4> pages;  // page ids of the next tile to load
   auto load_stage = [&](int t0) {
     if constexpr (INT4)
-      stage_load4<D, NT>(S, p, pt, kvh, t0, last_page, tid);
+      stage_load4<D, NT>(S, p, pages, kvh, t0, tid);
     else
-      stage_load<D, NT>(S, p, pt, kvh, t0, last_page, total, tid);
+      stage_load<D, NT>(S, p, pages, kvh, t0, tid);
   };
   auto store_stage = [&](Tile& T, int t0) {
     if constexpr (INT4)
       stage_store4<D, NT>(S, T, t0, total, tid);
     else
-      stage_store<D, NT>(S, T, tid);
+      stage_store<D, NT>(S, T, t0, total, tid);
   };
+  auto slot = [&](int tile) -> Tile& { return sT[(tile - tile_lo) & (NSLOT - 1)]; };
+  pages.load(pt, tile_lo, last_page, tid);
   load_stage(tile_lo * 64);
+  pages.load(pt, tile_lo + 1, last_page, tid);
 
   // ---- Q^T operand: rows R = wave*32 + rb*16 + r -> (position, head) -------
   // RoPE(q) * scale * log2(e) as an f16 pair hi + lo (~22 bits: a score's
@@ -422,7 +463,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       }
   }
 
-  store_stage(sT[tile_lo & 1], tile_lo * 64);
+  store_stage(slot(tile_lo), tile_lo * 64);
+  if (PER_BARRIER == 2 && tile_lo + 1 < n_tiles) {
+    load_stage((tile_lo + 1) * 64);
+    pages.load(pt, tile_lo + 2, last_page, tid);
+    store_stage(slot(tile_lo + 1), (tile_lo + 1) * 64);
+  }
   __syncthreads();
 
   // ---- online softmax state ----------------------------------------------------
@@ -440,11 +486,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 #pragma unroll
     for (int jb = 0; jb < JB; ++jb) acc[rb][jb] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int tile = tile_lo; tile < n_tiles; ++tile) {
+  // one tile: QK^T, mask, softmax, PV against the tile in LDS slot T
+  auto process = [&](const Tile& T, int tile) __attribute__((always_inline)) {
     const int t0 = tile * 64;
-    const Tile& T = sT[tile & 1];
-    const bool more = tile + 1 < n_tiles;
-    if (more) load_stage(t0 + 64);
 
     // S^T for both row blocks: 4 column blocks of 16 tokens; k steps outer so
     // that eight independent accumulation chains interleave on the MFMA pipe.
@@ -457,23 +501,33 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) c[cb][rb] = v4f{0.f, 0.f, 0.f, 0.f};
+      // K fragments of k step ks + 1 are read while the MFMAs of step ks run
+      // (the fence keeps the reads ahead of them)
+      v8h kf[2][4];
+      auto kfrag = [&](int ks, int cb) {
+        return *(const v8h*)(T.k + (16 * cb + r) * KROW + 8 * g + 32 * ks);
+      };
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) kf[0][cb] = kfrag(0, cb);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) {
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb) kf[(ks + 1) & 1][cb] = kfrag(ks + 1, cb);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         // one term at a time over all eight accumulators, so that consecutive
         // MFMAs never wait for each other's result
-        v8h a[4];
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) a[cb] = *(const v8h*)(T.k + (16 * cb + r) * KROW + 8 * g + 32 * ks);
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb)
-            c[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cb], qB[rb][ks], c[cb][rb], 0, 0, 0);
+            c[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[ks & 1][cb], qB[rb][ks], c[cb][rb], 0, 0, 0);
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb)
-            c[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cb], qL[rb][ks], c[cb][rb], 0, 0, 0);
+            c[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[ks & 1][cb], qL[rb][ks], c[cb][rb], 0, 0, 0);
         if constexpr (INT4) {
 #pragma unroll
           for (int cb = 0; cb < 4; ++cb) {
@@ -572,17 +626,51 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       }
       l_run[rb] += xgroup_sum(psum);
     }
+    // PV over the 2 x JB V fragments, kVPrefetch of them in flight ahead of
+    // the MFMAs that consume them (the scheduler fence keeps each read ahead
+    // of its consumer by that many MFMA pairs, so the LDS latency is covered)
+    {
+      constexpr int NV = 2 * JB;
+      constexpr int PF = INT4 ? kVPrefetchInt4 : kVPrefetch;
+      v8h vf[NV];
+      auto vfrag = [&](int i) {
+        const int kst = i / JB, jb = i % JB;
+        return *(const v8h*)(T.v + ((size_t)kst * D + 16 * jb + r) * VROW + 8 * g);
+      };
 #pragma unroll
-    for (int kst = 0; kst < 2; ++kst)
+      for (int i = 0; i < PF && i < NV; ++i) vf[i] = vfrag(i);
 #pragma unroll
-      for (int jb = 0; jb < JB; ++jb) {
-        const v8h bv = *(const v8h*)(T.v + ((size_t)kst * D + 16 * jb + r) * VROW + 8 * g);
+      for (int i = 0; i < NV; ++i) {
+        if (i + PF < NV) vf[i + PF] = vfrag(i + PF);
+        const int kst = i / JB, jb = i % JB;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
-          acc[rb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rb][kst], bv, acc[rb][jb], 0, 0, 0);
+          acc[rb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rb][kst], vf[i], acc[rb][jb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    }
 
-    if (more) store_stage(sT[(tile + 1) & 1], t0 + 64);
+  };
+
+  // PER_BARRIER tiles between barriers; each stages the tile PER_BARRIER
+  // ahead into the slot the previous round finished reading (its global loads
+  // in flight while the tile is computed, the page ids of the one after)
+  for (int tile = tile_lo; tile < n_tiles; tile += PER_BARRIER) {
+    // not unrolled: one copy of the tile body keeps the register budget
+#pragma nounroll
+    for (int h = 0; h < PER_BARRIER; ++h) {
+      const int tt = tile + h;
+      if (tt < n_tiles) {
+        const int nxt = tt + PER_BARRIER;
+        const bool more = nxt < n_tiles;
+        if (more) {
+          load_stage(nxt * 64);
+          pages.load(pt, nxt + 1, last_page, tid);  // consumed by the next stage
+        }
+        process(slot(tt), tt);
+        if (more) store_stage(slot(nxt), nxt * 64);
+      }
+    }
     __syncthreads();
   }
 
