@@ -396,7 +396,9 @@ def test_prefill_outlier_keys(rt, quant, hq, hkv, d, past, new, qd):
     c.check_codes()
     q = c.query(qd)
     got = c.gpu_prefill(q, qd)
-    err = assert_close(got, c.oracle_attend(q), "outlier-K prefill")
+    ref = c.oracle_attend(q)
+    log(f"  worst err/tol {err_tol_ratio(got, ref):.4f}")
+    err = assert_close(got, ref, "outlier-K prefill")
     log(f"  max abs err {err:.2e}")
 
 
