@@ -179,7 +179,8 @@ sai_status sai_kv_append(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const 
  * window: gpu_gqa_with_cache's `window` (the node's local_window_size when
  * > 0): the query at position p sees keys [p - window, p]; <= 0 = off. A
  * sliding-window layer (sai_kvcache_set_layer_window) sees its last w keys;
- * with both, the narrower span applies. */
+ * with both, the narrower span applies. Head dims: int8 64, 128 and 256
+ * (groups up to 4 at 256), int4 64 and 128; UNSUPPORTED otherwise. */
 sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
                           int32_t dtype, int32_t batch, int32_t num_heads,
                           const float* cos_cache, const float* sin_cache, int32_t cache_rows,

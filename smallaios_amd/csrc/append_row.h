@@ -150,22 +150,24 @@ __device__ __forceinline__ void quant_int4_elem(float x, uint32_t& q, uint16_t& 
 }
 
 // Full K+V append of one (token, kv head) row into an int4 page block, one
-// wave. K is packed LSB-first along D; V is dim-major and shares each byte
-// with the neighbouring slot, whose nibble is kept (read-modify-write; the
-// caller guarantees no other wave writes that byte concurrently). Every load
-// is issued before the first store.
-__device__ __forceinline__ void append_row_int4_d128(const void* k_row, const void* v_row,
-                                                     int dtype, int lane, int pos, uint8_t* blk,
-                                                     int slot, int do_rotary, bool interleaved,
-                                                     const float* cos_cache,
-                                                     const float* sin_cache) {
-  constexpr int D = 128;
+// wave (head_dim 64 or 128: element lane + 64 j, a group of 32 = a half-wave).
+// K is packed LSB-first along D; V is dim-major and shares each byte with the
+// neighbouring slot, whose nibble is kept (read-modify-write; the caller
+// guarantees no other wave writes that byte concurrently). Every load is
+// issued before the first store.
+template <int D>
+__device__ __forceinline__ void append_row_int4(const void* k_row, const void* v_row, int dtype,
+                                                int lane, int pos, uint8_t* blk, int slot,
+                                                int do_rotary, bool interleaved,
+                                                const float* cos_cache, const float* sin_cache) {
+  static_assert(D == 64 || D == 128, "int4 row append: head_dim 64 or 128");
   constexpr int NG = D / 32;
-  float xk[2], xv[2];
-  uint8_t* vdst[2];
-  uint8_t vcur[2];
+  constexpr int J = D / 64;
+  float xk[J], xv[J];
+  uint8_t* vdst[J];
+  uint8_t vcur[J];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < J; ++j) {
     const int e = lane + 64 * j;
     xk[j] = load_elem(k_row, e, dtype);
     xv[j] = load_elem(v_row, e, dtype);
@@ -177,7 +179,7 @@ __device__ __forceinline__ void append_row_int4_d128(const void* k_row, const vo
   for (int which = 0; which < 2; ++which) {
     uint16_t* sz = (uint16_t*)(blk + 16 * D + 64 * NG * which) + (size_t)slot * NG * 2;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < J; ++j) {
       uint32_t q;
       uint16_t s16, z16;
       quant_int4_elem(which == 0 ? xk[j] : xv[j], q, s16, z16);

@@ -1,6 +1,7 @@
 // Kernel 2, int4 cache: split-K flash decode over pages of 4-bit asymmetric
 // codes with a binary16 (scale, zero) per (token, kv head, group of 32 dims).
-// head_dim 128 (4 groups), GQA group G <= 8.
+// head_dim 128 (4 groups) or 64 (2 groups: lane groups 2 and 3 carry zero query
+// dims and zero group parameters, so they add nothing), GQA group G <= 8.
 //
 // Same work split, prologue, double-buffered tile stream and split merge as
 // the int8 kernel (gqa_decode.hip); what changes is the math:
@@ -46,36 +47,48 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-constexpr int kD = 128;
-constexpr int kNG = kD / 32;  // groups of 32 along head_dim
-constexpr int kJB = kD / 16;  // 16-dim column blocks of PV
-constexpr size_t kBB = block_bytes_int4(kD);
+constexpr int kChunks = 4;  // 8-dim chunks of a lane's 32 dims (one group)
 constexpr float kTwo20 = 1048576.0f;          // 2^20
 constexpr float kTwo24 = 16777216.0f;         // 2^24
 
+template <int D>
 struct Tile4 {
-  v4u ka[4];     // K: token (page r>>2, slot 4*blk + (r&3)), dims 32g .. 32g+31
-  v2u vb[kJB];   // V: slots 0..15 of dim 16*jb + r in page g
-  uint4 kp, vp;  // (scale, zero) x 4 groups, f16, of (page g, slot r)
+  v4u ka[4];       // K: token (page r>>2, slot 4*blk + (r&3)), dims 32g .. 32g+31
+  v2u vb[D / 16];  // V: slots 0..15 of dim 16*jb + r in page g
+  uint4 kp, vp;    // (scale, zero) x D/32 groups, f16, of (page g, slot r); zero padded
 };
 
-__device__ __forceinline__ void load_tile4(Tile4& T, const uint8_t* __restrict__ pool,
+template <int D>
+__device__ __forceinline__ void load_tile4(Tile4<D>& T, const uint8_t* __restrict__ pool,
                                            const int* sm_pg, int tile, int num_pages, int kvh,
                                            int r, int g, int n_pages_split) {
+  constexpr int NG = D / 32;
+  constexpr size_t BB = block_bytes_int4(D);
+  // at head_dim 64 lane groups 2 and 3 re-read group 1's K bytes: their query
+  // dims are zero, and the nibbles are finite, so they add exactly nothing
+  const int gk = min(g, NG - 1);
   const int lp = n_pages_split - 1;
   const int pg_g = sm_pg[min(tile * 4 + g, lp)];
   const int pg_k = sm_pg[min(tile * 4 + (r >> 2), lp)];
-  const uint8_t* blk_g = pool + block_offset(pg_g, kvh, num_pages, kBB);
-  const uint8_t* blk_k = pool + block_offset(pg_k, kvh, num_pages, kBB);
+  const uint8_t* blk_g = pool + block_offset(pg_g, kvh, num_pages, BB);
+  const uint8_t* blk_k = pool + block_offset(pg_k, kvh, num_pages, BB);
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk)
     T.ka[blk] = __builtin_nontemporal_load(
-        (const v4u*)(blk_k + (size_t)(4 * blk + (r & 3)) * (kD / 2) + 16 * g));
+        (const v4u*)(blk_k + (size_t)(4 * blk + (r & 3)) * (D / 2) + 16 * gk));
 #pragma unroll
-  for (int jb = 0; jb < kJB; ++jb)
-    T.vb[jb] = __builtin_nontemporal_load((const v2u*)(blk_g + 8 * kD + (16 * jb + r) * 8));
-  T.kp = *(const uint4*)(blk_g + 16 * kD + 16 * r);
-  T.vp = *(const uint4*)(blk_g + 16 * kD + 64 * kNG + 16 * r);
+  for (int jb = 0; jb < D / 16; ++jb)
+    T.vb[jb] = __builtin_nontemporal_load((const v2u*)(blk_g + 8 * D + (16 * jb + r) * 8));
+  if constexpr (NG == 4) {
+    T.kp = *(const uint4*)(blk_g + 16 * D + 16 * r);
+    T.vp = *(const uint4*)(blk_g + 16 * D + 64 * NG + 16 * r);
+  } else {
+    // two groups: 8 bytes per slot, the upper (scale, zero) pairs zero
+    const uint2 k2 = *(const uint2*)(blk_g + 16 * D + 8 * r);
+    const uint2 v2 = *(const uint2*)(blk_g + 16 * D + 64 * NG + 8 * r);
+    T.kp = uint4{k2.x, k2.y, 0u, 0u};
+    T.vp = uint4{v2.x, v2.y, 0u, 0u};
+  }
 }
 
 // 8 nibbles (one dword, element k at bits 4k..4k+3) -> f16 subnormals in the
@@ -98,25 +111,26 @@ __device__ __forceinline__ float quad_sum(float v) {
   return v;
 }
 
-template <int G>
+template <int D, int G>
 struct State4 {
   static constexpr int HT = (G + 3) / 4;  // quads of heads
   float m_run[HT], l_run[HT];  // per lane (j, g): head 4*qd + j/4, log2 domain
   float zacc[HT];              // sum_t p_t z_v,tG' of (head 4*qd + j/4, G' = j&3)
-  float acc[HT][kJB];          // lane (dim 16*jb + r, g): head 4*qd + g, x 2^-24
+  float acc[HT][D / 16];       // lane (dim 16*jb + r, g): head 4*qd + g, x 2^-24
 };
 
 // One 64-token tile: lane (r, g) owns page g of the tile (slots 0..15) for
 // column j = r. MASK: the tile crosses the end of the split (t_end) or the
 // first key of a sliding window (t_lo).
-template <int G, bool MASK>
-__device__ __forceinline__ void compute_tile4(const Tile4& T, State4<G>& st,
-                                              const v8h (&Bh)[State4<G>::HT][kNG],
-                                              const v8h (&Bl)[State4<G>::HT][kNG],
-                                              const float (&qsn)[State4<G>::HT],
-                                              const float (&q_scale)[State4<G>::HT], int tok0,
+template <int D, int G, bool MASK>
+__device__ __forceinline__ void compute_tile4(const Tile4<D>& T, State4<D, G>& st,
+                                              const v8h (&Bh)[State4<D, G>::HT][kChunks],
+                                              const v8h (&Bl)[State4<D, G>::HT][kChunks],
+                                              const float (&qsn)[State4<D, G>::HT],
+                                              const float (&q_scale)[State4<D, G>::HT], int tok0,
                                               int t_lo, int t_end, int r, int g, uint4* sm_p) {
-  constexpr int HT = State4<G>::HT;
+  constexpr int HT = State4<D, G>::HT;
+  constexpr int JB = D / 16;
   const int lane = threadIdx.x & 63;
   const int gp = r & 3;
   // (scale, zero) of every slot of the tile through this wave's LDS slot
@@ -234,7 +248,7 @@ __device__ __forceinline__ void compute_tile4(const Tile4& T, State4<G>& st,
   }
   // P V on the matrix cores; lane (dim, g) reads row (head g, group of dim)
 #pragma unroll
-  for (int jb = 0; jb < kJB; ++jb) {
+  for (int jb = 0; jb < JB; ++jb) {
     const v8h b0 = unpack_sub(T.vb[jb].x);
     const v8h b1 = unpack_sub(T.vb[jb].y);
 #pragma unroll
@@ -247,9 +261,12 @@ __device__ __forceinline__ void compute_tile4(const Tile4& T, State4<G>& st,
   }
 }
 
-template <int G, int NW>
+template <int D, int G, int NW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(DecodeParams p) {
-  constexpr int HT = State4<G>::HT;
+  constexpr int HT = State4<D, G>::HT;
+  constexpr int NG = D / 32;
+  constexpr int JB = D / 16;
+  constexpr size_t BB = block_bytes_int4(D);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r = lane & 15;
@@ -279,8 +296,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
 #pragma unroll
   for (int qd = 0; qd < HT; ++qd) {
     const int h = 4 * qd + hh;
-    if (h < G) {
-      const size_t qbase = ((size_t)b * Hq + kvh * G + h) * kD + 32 * g;
+    if (h < G && g < NG) {
+      const size_t qbase = ((size_t)b * Hq + kvh * G + h) * D + 32 * g;
       float t[16];
       load16(p.q, qbase, p.q_dtype, t);
 #pragma unroll
@@ -296,10 +313,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   // cos / sin of dims 32g .. 32g + 31 of the lane, as two runs of 16
   float4 cq4[2][4], sq4[2][4];
   if (p.do_rotary) {
-    const float* cr = p.cos_cache + (size_t)(L - 1) * (kD / 2);
-    const float* sr = p.sin_cache + (size_t)(L - 1) * (kD / 2);
+    const float* cr = p.cos_cache + (size_t)(L - 1) * (D / 2);
+    const float* sr = p.sin_cache + (size_t)(L - 1) * (D / 2);
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) rope_load16<kD>(cr, sr, 32 * g + 16 * hf, p.interleaved, cq4[hf], sq4[hf]);
+    for (int hf = 0; hf < 2; ++hf)
+      rope_load16<D>(cr, sr, 32 * min(g, NG - 1) + 16 * hf, p.interleaved, cq4[hf], sq4[hf]);
   }
 
   const int t_begin = origin + split * p.split_tokens;
@@ -318,21 +336,21 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   auto append = [&]() {
     const int pos = L - 1;
     uint8_t* blk = (uint8_t*)p.pool +
-                   block_offset(sm_pg[pos / kPageTokens - first_page], kvh, p.num_pages, kBB);
-    const size_t row = ((size_t)b * p.kv_heads + kvh) * kD * (p.kv_dtype == kDtypeBf16 ? 2 : 4);
-    append_row_int4_d128((const uint8_t*)p.k_new + row, (const uint8_t*)p.v_new + row,
+                   block_offset(sm_pg[pos / kPageTokens - first_page], kvh, p.num_pages, BB);
+    const size_t row = ((size_t)b * p.kv_heads + kvh) * D * (p.kv_dtype == kDtypeBf16 ? 2 : 4);
+    append_row_int4<D>((const uint8_t*)p.k_new + row, (const uint8_t*)p.v_new + row,
                          p.kv_dtype, lane, pos, blk, pos % kPageTokens, p.do_rotary,
                          p.interleaved != 0, p.cos_cache, p.sin_cache);
     // the page is read back by this wave's last tile
     __threadfence_block();
   };
   if (appender && my_tiles == 1) append();
-  Tile4 TA;
+  Tile4<D> TA;
   if (tile < n_tiles) load_tile4(TA, p.pool, sm_pg, tile, p.num_pages, kvh, r, g, n_pages_split);
   if (appender && my_tiles > 1) append();
 
   // ---- Q: RoPE at position L-1, normalised by the head's max|Q| ----
-  v8h Bh[HT][kNG], Bl[HT][kNG];
+  v8h Bh[HT][kChunks], Bl[HT][kChunks];
   float qsn[HT], q_scale[HT];
 #pragma unroll
   for (int qd = 0; qd < HT; ++qd) {
@@ -353,15 +371,20 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
         for (int i = 0; i < 32; ++i)
           y[i] = rope_elem(cq[i], sq[i], x[qd][i], x[qd][i ^ 1], (i & 1) == 0);
       } else {
-        // partner d +- 64: group g ^ 2, the lane 32 away
-        const bool first = g < 2;
+        // partner d +- D/2: group g ^ (NG/2), the lane 16 * NG / 2 away
+        const bool first = g < NG / 2;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-          // permlane32_swap(x, x): [0] = lanes 0-31's x on both halves, [1] =
-          // lanes 32-63's x on both halves
-          auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[qd][i]),
-                                                     __float_as_uint(x[qd][i]), false, false);
-          const float xp = __uint_as_float(first ? sw[1] : sw[0]);
+          float xp;
+          if constexpr (NG == 4) {
+            // permlane32_swap(x, x): [0] = lanes 0-31's x on both halves, [1] =
+            // lanes 32-63's x on both halves
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[qd][i]),
+                                                       __float_as_uint(x[qd][i]), false, false);
+            xp = __uint_as_float(first ? sw[1] : sw[0]);
+          } else {
+            xp = __shfl_xor(x[qd][i], 16, 64);
+          }
           y[i] = rope_elem(cq[i], sq[i], x[qd][i], xp, first);
         }
       }
@@ -404,29 +427,29 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   __shared__ uint4 sm_par[NW][128];
 
   // ---- stream the split's tiles, ping-pong; the last one may be partial ----
-  State4<G> st;
+  State4<D, G> st;
 #pragma unroll
   for (int qd = 0; qd < HT; ++qd) {
     st.m_run[qd] = -INFINITY;
     st.l_run[qd] = 0.0f;
     st.zacc[qd] = 0.0f;
 #pragma unroll
-    for (int jb = 0; jb < kJB; ++jb) st.acc[qd][jb] = 0.0f;
+    for (int jb = 0; jb < JB; ++jb) st.acc[qd][jb] = 0.0f;
   }
 
-  Tile4 TB;
+  Tile4<D> TB;
   auto tok0 = [&](int k) { return t_begin + (wave + k * NW) * 64 + 16 * g; };
-  auto ld = [&](Tile4& T, int k) {
+  auto ld = [&](Tile4<D>& T, int k) {
     load_tile4(T, p.pool, sm_pg, wave + k * NW, p.num_pages, kvh, r, g, n_pages_split);
   };
   // tiles before the split's last one are full
   const bool last_partial = (t_end - t_begin) % 64 != 0;
-  auto run = [&](const Tile4& T, int k) {
+  auto run = [&](const Tile4<D>& T, int k) {
     const bool partial = last_partial && wave + k * NW == n_tiles - 1;
     if (__builtin_amdgcn_readfirstlane(partial))
-      compute_tile4<G, true>(T, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
+      compute_tile4<D, G, true>(T, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
     else
-      compute_tile4<G, false>(T, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
+      compute_tile4<D, G, false>(T, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
   };
   int k = 0;
   // the window's first key inside the split's first tile (wave 0's tile 0):
@@ -435,23 +458,23 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   if (wave == 0 && k_lo > t_begin) {  // uniform over the wave
     if (my_tiles > 1) {
       ld(TB, 1);
-      compute_tile4<G, true>(TA, st, Bh, Bl, qsn, q_scale, tok0(0), k_lo, t_end, r, g, sm_par[wave]);
+      compute_tile4<D, G, true>(TA, st, Bh, Bl, qsn, q_scale, tok0(0), k_lo, t_end, r, g, sm_par[wave]);
       TA = TB;
       k = 1;
     } else {
-      compute_tile4<G, true>(TA, st, Bh, Bl, qsn, q_scale, tok0(0), k_lo, t_end, r, g, sm_par[wave]);
+      compute_tile4<D, G, true>(TA, st, Bh, Bl, qsn, q_scale, tok0(0), k_lo, t_end, r, g, sm_par[wave]);
       k = 1;
     }
   }
   for (; k + 2 < my_tiles; k += 2) {
     ld(TB, k + 1);
-    compute_tile4<G, false>(TA, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
+    compute_tile4<D, G, false>(TA, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
     ld(TA, k + 2);
-    compute_tile4<G, false>(TB, st, Bh, Bl, qsn, q_scale, tok0(k + 1), k_lo, t_end, r, g, sm_par[wave]);
+    compute_tile4<D, G, false>(TB, st, Bh, Bl, qsn, q_scale, tok0(k + 1), k_lo, t_end, r, g, sm_par[wave]);
   }
   if (k + 1 < my_tiles) {
     ld(TB, k + 1);
-    compute_tile4<G, false>(TA, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
+    compute_tile4<D, G, false>(TA, st, Bh, Bl, qsn, q_scale, tok0(k), k_lo, t_end, r, g, sm_par[wave]);
     run(TB, k + 1);
   } else if (k < my_tiles) {
     run(TA, k);
@@ -460,13 +483,13 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   // ---- merge the NW waves; zero-point sums join per (head, dim group) ----
   __shared__ float sm_m[NW][G];
   __shared__ float sm_l[NW][G];
-  __shared__ float sm_z[NW][G][kNG];
-  __shared__ float sm_o[NW][G][kD];
+  __shared__ float sm_z[NW][G][NG];
+  __shared__ float sm_o[NW][G][D];
 #pragma unroll
   for (int qd = 0; qd < HT; ++qd) {
     const int h = 4 * qd + hh;
     if (g == 0 && h < G) {
-      sm_z[wave][h][gp] = st.zacc[qd];
+      if (gp < NG) sm_z[wave][h][gp] = st.zacc[qd];
       if (gp == 0) {
         sm_m[wave][h] = st.m_run[qd];
         sm_l[wave][h] = st.l_run[qd];
@@ -475,14 +498,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
     const int hd = 4 * qd + g;
     if (hd < G) {
 #pragma unroll
-      for (int jb = 0; jb < kJB; ++jb) sm_o[wave][hd][16 * jb + r] = st.acc[qd][jb] * kTwo24;
+      for (int jb = 0; jb < JB; ++jb) sm_o[wave][hd][16 * jb + r] = st.acc[qd][jb] * kTwo24;
     }
   }
   __syncthreads();
 
-  float* part = p.partials + ((size_t)(split_base + split) * p.kv_heads + kvh) * (G * (kD + 2));
-  for (int t = threadIdx.x; t < G * kD; t += 64 * NW) {
-    const int hd = t / kD, d = t % kD;
+  float* part = p.partials + ((size_t)(split_base + split) * p.kv_heads + kvh) * (G * (D + 2));
+  for (int t = threadIdx.x; t < G * D; t += 64 * NW) {
+    const int hd = t / D, d = t % D;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w) M = fmaxf(M, sm_m[w][hd]);
@@ -495,12 +518,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
       O += (sm_o[w][hd][d] + sm_z[w][hd][d >> 5]) * f;
     }
     if (nsplit == 1) {
-      p.out[((size_t)b * Hq + kvh * G + hd) * kD + d] = Ls > 0.0f ? O / Ls : 0.0f;
+      p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
     } else {
-      part[hd * (kD + 2) + 2 + d] = O;
+      part[hd * (D + 2) + 2 + d] = O;
       if (d == 0) {
-        part[hd * (kD + 2)] = M;
-        part[hd * (kD + 2) + 1] = Ls;
+        part[hd * (D + 2)] = M;
+        part[hd * (D + 2) + 1] = Ls;
       }
     }
   }
@@ -510,34 +533,41 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   }
 }
 
-template <int G>
+template <int D, int G>
 hipError_t launch_g(const DecodeParams& p, int work_items, bool combine, hipStream_t st) {
   if (p.waves == 8)
-    hipLaunchKernelGGL((gqa_decode_int4_kernel<G, 8>), dim3(work_items, p.kv_heads), dim3(512), 0,
-                       st, p);
+    hipLaunchKernelGGL((gqa_decode_int4_kernel<D, G, 8>), dim3(work_items, p.kv_heads), dim3(512),
+                       0, st, p);
   else
-    hipLaunchKernelGGL((gqa_decode_int4_kernel<G, 4>), dim3(work_items, p.kv_heads), dim3(256), 0,
-                       st, p);
+    hipLaunchKernelGGL((gqa_decode_int4_kernel<D, G, 4>), dim3(work_items, p.kv_heads), dim3(256),
+                       0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !combine) return e;
-  return launch_decode_combine(p, kD, G, st);
+  return launch_decode_combine(p, D, G, st);
+}
+
+template <int D>
+hipError_t launch_d(const DecodeParams& p, int group, int work_items, bool combine,
+                    hipStream_t st) {
+  switch (group) {
+    case 1: return launch_g<D, 1>(p, work_items, combine, st);
+    case 2: return launch_g<D, 2>(p, work_items, combine, st);
+    case 4: return launch_g<D, 4>(p, work_items, combine, st);
+    case 8: return launch_g<D, 8>(p, work_items, combine, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
 
 hipError_t launch_gqa_decode_int4(const DecodeParams& p, int head_dim, int group, int work_items,
                                   bool combine, hipStream_t st) {
-  if (head_dim != kD) return hipErrorInvalidValue;
   if (p.split_tokens <= 0 || p.split_tokens % 64 != 0 ||
       p.split_tokens > kMaxSplitPages * kPageTokens)
     return hipErrorInvalidValue;
-  switch (group) {
-    case 1: return launch_g<1>(p, work_items, combine, st);
-    case 2: return launch_g<2>(p, work_items, combine, st);
-    case 4: return launch_g<4>(p, work_items, combine, st);
-    case 8: return launch_g<8>(p, work_items, combine, st);
-    default: return hipErrorInvalidValue;
-  }
+  if (head_dim == 128) return launch_d<128>(p, group, work_items, combine, st);
+  if (head_dim == 64) return launch_d<64>(p, group, work_items, combine, st);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace sai

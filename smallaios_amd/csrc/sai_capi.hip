@@ -752,8 +752,9 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   const char* op = "gqa_decode";
   const int32_t W = visible_span(c->layer_window[layer], window);
   const int D = c->desc.head_dim;
-  if (c->desc.quant == SAI_KV_INT4 && D != 128)
-    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: int4 decode needs head_dim 128 (got %d)", op, D);
+  if (c->desc.quant == SAI_KV_INT4 && D != 128 && D != 64)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: int4 decode needs head_dim 64 or 128 (got %d)", op,
+                D);
   if (D == 256 && G > 4)
     return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: head_dim 256 supports groups of 1, 2 and 4 (got %d)",
                 op, G);
