@@ -95,7 +95,7 @@ int32_t sai_device_supported(int device);
 typedef struct sai_kvcache_desc {
   int32_t num_layers;
   int32_t num_kv_heads;
-  int32_t head_dim;          /* 64, 128, or 256 (int8 only; decode groups up to 4) */
+  int32_t head_dim;          /* 64, 128 or 256 (decode groups up to 4 at 256) */
   int32_t num_pages;         /* physical pages per layer */
   int32_t max_batch;         /* sequences */
   int32_t max_pages_per_seq; /* page-table width */
@@ -179,8 +179,8 @@ sai_status sai_kv_append(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const 
  * window: gpu_gqa_with_cache's `window` (the node's local_window_size when
  * > 0): the query at position p sees keys [p - window, p]; <= 0 = off. A
  * sliding-window layer (sai_kvcache_set_layer_window) sees its last w keys;
- * with both, the narrower span applies. Head dims: int8 64, 128 and 256
- * (groups up to 4 at 256), int4 64 and 128; UNSUPPORTED otherwise. */
+ * with both, the narrower span applies. Head dims 64, 128 and 256 for int8
+ * and int4 (groups up to 4 at 256); UNSUPPORTED otherwise. */
 sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
                           int32_t dtype, int32_t batch, int32_t num_heads,
                           const float* cos_cache, const float* sin_cache, int32_t cache_rows,
@@ -228,7 +228,7 @@ sai_status sai_gqa_with_cache_noalloc(sai_ctx* ctx, sai_kvcache* cache, int32_t 
  * Same contract as sai_gqa_decode for a chunk of sq == pending query tokens per
  * sequence (the reference's op_group_query_attention with Sq > 1, causal with
  * past_sk = seq_len[b], microsoft.rs:1156 and :331-337), over an int8 cache
- * (head_dim 64, 128 or 256) or an int4 one (64 or 128).
+ * or an int4 one (head_dim 64, 128 or 256).
  * q: device [batch, sq, num_heads*D]; out: device [batch, sq, num_heads*D] f32.
  * window and sliding-window layers as for sai_gqa_decode, applied to every
  * query row at its own position (gpu_gqa's mask, attention.rs:79, :111). */

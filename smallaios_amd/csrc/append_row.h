@@ -150,7 +150,7 @@ __device__ __forceinline__ void quant_int4_elem(float x, uint32_t& q, uint16_t& 
 }
 
 // Full K+V append of one (token, kv head) row into an int4 page block, one
-// wave (head_dim 64 or 128: element lane + 64 j, a group of 32 = a half-wave).
+// wave (head_dim 64, 128 or 256: element lane + 64 j, a group of 32 = a half-wave).
 // K is packed LSB-first along D; V is dim-major and shares each byte with the
 // neighbouring slot, whose nibble is kept (read-modify-write; the caller
 // guarantees no other wave writes that byte concurrently). Every load is
@@ -160,7 +160,7 @@ __device__ __forceinline__ void append_row_int4(const void* k_row, const void* v
                                                 int lane, int pos, uint8_t* blk, int slot,
                                                 int do_rotary, bool interleaved,
                                                 const float* cos_cache, const float* sin_cache) {
-  static_assert(D == 64 || D == 128, "int4 row append: head_dim 64 or 128");
+  static_assert(D == 64 || D == 128 || D == 256, "int4 row append: head_dim 64, 128 or 256");
   constexpr int NG = D / 32;
   constexpr int J = D / 64;
   float xk[J], xv[J];

@@ -1,7 +1,9 @@
 // Kernel 2, int4 cache: split-K flash decode over pages of 4-bit asymmetric
 // codes with a binary16 (scale, zero) per (token, kv head, group of 32 dims).
-// head_dim 128 (4 groups) or 64 (2 groups: lane groups 2 and 3 carry zero query
-// dims and zero group parameters, so they add nothing), GQA group G <= 8.
+// head_dim 128 (4 groups), 64 (2 groups: lane groups 2 and 3 carry zero query
+// dims and zero group parameters, so they add nothing) or 256 (two halves of 128
+// dims, each in the 128 layout, their group-scaled dots summed before the
+// softmax), GQA group G <= 8 (<= 4 at 256).
 //
 // Same work split, prologue, double-buffered tile stream and split merge as
 // the int8 kernel (gqa_decode.hip); what changes is the math:
@@ -51,11 +53,21 @@ constexpr int kChunks = 4;  // 8-dim chunks of a lane's 32 dims (one group)
 constexpr float kTwo20 = 1048576.0f;          // 2^20
 constexpr float kTwo24 = 16777216.0f;         // 2^24
 
+// Halves of 128 dims (two at head_dim 256) and the 32-dim groups of a half.
+template <int D>
+struct Shape4 {
+  static constexpr int NG = D / 32;              // groups of a row
+  static constexpr int NH = D > 128 ? D / 128 : 1;
+  static constexpr int NGH = NG / NH;            // groups of a half: 2 (D = 64) or 4
+  static constexpr int JB = D / 16;              // 16-dim column blocks of PV
+};
+
 template <int D>
 struct Tile4 {
-  v4u ka[4];       // K: token (page r>>2, slot 4*blk + (r&3)), dims 32g .. 32g+31
-  v2u vb[D / 16];  // V: slots 0..15 of dim 16*jb + r in page g
-  uint4 kp, vp;    // (scale, zero) x D/32 groups, f16, of (page g, slot r); zero padded
+  static constexpr int NH = Shape4<D>::NH;
+  v4u ka[NH][4];     // K: token (page r>>2, slot 4*blk + (r&3)), dims 128 hf + 32g .. +31
+  v2u vb[D / 16];    // V: slots 0..15 of dim 16*jb + r in page g
+  uint4 kp[NH], vp[NH];  // (scale, zero) of the half's groups, f16, of (page g, slot r)
 };
 
 template <int D>
@@ -63,31 +75,39 @@ __device__ __forceinline__ void load_tile4(Tile4<D>& T, const uint8_t* __restric
                                            const int* sm_pg, int tile, int num_pages, int kvh,
                                            int r, int g, int n_pages_split) {
   constexpr int NG = D / 32;
+  constexpr int NH = Shape4<D>::NH;
+  constexpr int NGH = Shape4<D>::NGH;
   constexpr size_t BB = block_bytes_int4(D);
   // at head_dim 64 lane groups 2 and 3 re-read group 1's K bytes: their query
   // dims are zero, and the nibbles are finite, so they add exactly nothing
-  const int gk = min(g, NG - 1);
+  const int gk = min(g, NGH - 1);
   const int lp = n_pages_split - 1;
   const int pg_g = sm_pg[min(tile * 4 + g, lp)];
   const int pg_k = sm_pg[min(tile * 4 + (r >> 2), lp)];
   const uint8_t* blk_g = pool + block_offset(pg_g, kvh, num_pages, BB);
   const uint8_t* blk_k = pool + block_offset(pg_k, kvh, num_pages, BB);
 #pragma unroll
-  for (int blk = 0; blk < 4; ++blk)
-    T.ka[blk] = __builtin_nontemporal_load(
-        (const v4u*)(blk_k + (size_t)(4 * blk + (r & 3)) * (D / 2) + 16 * gk));
+  for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+      T.ka[hf][blk] = __builtin_nontemporal_load(
+          (const v4u*)(blk_k + (size_t)(4 * blk + (r & 3)) * (D / 2) + 64 * hf + 16 * gk));
 #pragma unroll
   for (int jb = 0; jb < D / 16; ++jb)
     T.vb[jb] = __builtin_nontemporal_load((const v2u*)(blk_g + 8 * D + (16 * jb + r) * 8));
-  if constexpr (NG == 4) {
-    T.kp = *(const uint4*)(blk_g + 16 * D + 16 * r);
-    T.vp = *(const uint4*)(blk_g + 16 * D + 64 * NG + 16 * r);
+  if constexpr (NGH == 4) {
+    // half hf: groups 4 hf .. 4 hf + 3, 16 bytes of the slot's 4 NG
+#pragma unroll
+    for (int hf = 0; hf < NH; ++hf) {
+      T.kp[hf] = *(const uint4*)(blk_g + 16 * D + 4 * NG * r + 16 * hf);
+      T.vp[hf] = *(const uint4*)(blk_g + 16 * D + 64 * NG + 4 * NG * r + 16 * hf);
+    }
   } else {
     // two groups: 8 bytes per slot, the upper (scale, zero) pairs zero
     const uint2 k2 = *(const uint2*)(blk_g + 16 * D + 8 * r);
     const uint2 v2 = *(const uint2*)(blk_g + 16 * D + 64 * NG + 8 * r);
-    T.kp = uint4{k2.x, k2.y, 0u, 0u};
-    T.vp = uint4{v2.x, v2.y, 0u, 0u};
+    T.kp[0] = uint4{k2.x, k2.y, 0u, 0u};
+    T.vp[0] = uint4{v2.x, v2.y, 0u, 0u};
   }
 }
 
@@ -115,7 +135,7 @@ template <int D, int G>
 struct State4 {
   static constexpr int HT = (G + 3) / 4;  // quads of heads
   float m_run[HT], l_run[HT];  // per lane (j, g): head 4*qd + j/4, log2 domain
-  float zacc[HT];              // sum_t p_t z_v,tG' of (head 4*qd + j/4, G' = j&3)
+  float zacc[Shape4<D>::NH][HT];  // sum_t p_t z_v,tG' of (head 4*qd + j/4, G' = j&3) per half
   float acc[HT][D / 16];       // lane (dim 16*jb + r, g): head 4*qd + g, x 2^-24
 };
 
@@ -124,53 +144,70 @@ struct State4 {
 // first key of a sliding window (t_lo).
 template <int D, int G, bool MASK>
 __device__ __forceinline__ void compute_tile4(const Tile4<D>& T, State4<D, G>& st,
-                                              const v8h (&Bh)[State4<D, G>::HT][kChunks],
-                                              const v8h (&Bl)[State4<D, G>::HT][kChunks],
-                                              const float (&qsn)[State4<D, G>::HT],
+                                              const v8h (&Bh)[Shape4<D>::NH][State4<D, G>::HT][kChunks],
+                                              const v8h (&Bl)[Shape4<D>::NH][State4<D, G>::HT][kChunks],
+                                              const float (&qsn)[Shape4<D>::NH][State4<D, G>::HT],
                                               const float (&q_scale)[State4<D, G>::HT], int tok0,
                                               int t_lo, int t_end, int r, int g, uint4* sm_p) {
   constexpr int HT = State4<D, G>::HT;
+  constexpr int NH = Shape4<D>::NH;
   constexpr int JB = D / 16;
+  constexpr int JBH = JB / NH;  // column blocks of a half
   const int lane = threadIdx.x & 63;
   const int gp = r & 3;
-  // (scale, zero) of every slot of the tile through this wave's LDS slot
-  sm_p[lane] = T.kp;
-  sm_p[64 + lane] = T.vp;
+  // (scale, zero) of every slot of the tile through this wave's LDS slot:
+  // K halves, then V halves, 64 lanes each
+#pragma unroll
+  for (int hf = 0; hf < NH; ++hf) {
+    sm_p[64 * hf + lane] = T.kp[hf];
+    sm_p[64 * (NH + hf) + lane] = T.vp[hf];
+  }
   __builtin_amdgcn_wave_barrier();
   const uint32_t* sm_w = (const uint32_t*)sm_p;
 
-  // QK^T: per 16-token block, accumulate the four 8-dim chunks (hi and lo)
-  v4f cs[HT][4];
+  // QK^T: per half and 16-token block, accumulate the four 8-dim chunks (hi
+  // and lo)
+  v4f cs[NH][HT][4];
 #pragma unroll
-  for (int blk = 0; blk < 4; ++blk) {
-    v8h ka[4];
+  for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) ka[c] = unpack_sub(T.ka[blk][c]);
+    for (int blk = 0; blk < 4; ++blk) {
+      v8h ka[4];
 #pragma unroll
-    for (int qd = 0; qd < HT; ++qd) {
-      v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < 4; ++c) ka[c] = unpack_sub(T.ka[hf][blk][c]);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[c], Bh[qd][c], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[c], Bl[qd][c], acc, 0, 0, 0);
+      for (int qd = 0; qd < HT; ++qd) {
+        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[c], Bh[hf][qd][c], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[c], Bl[hf][qd][c], acc, 0, 0, 0);
+        }
+        cs[hf][qd][blk] = acc;
       }
-      cs[qd][blk] = acc;
     }
-  }
   // MASK: slots [nlow, nvalid) of page g are visible (split end, window start)
   const int nvalid = t_end - tok0;
   const int nlow = t_lo - tok0;
-  // u = sum_G' (s_G' * dot_G' + z_G' * qsn); score (log2) = q_scale * u
+  // u = sum_G' (s_G' * dot_G' + z_G' * qsn) over the groups of every half;
+  // score (log2) = q_scale * u
   float u[HT][16];
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int slot = 4 * blk + e;
-      const v2h sz = __builtin_bit_cast(v2h, sm_w[(16 * g + slot) * 4 + gp]);
 #pragma unroll
-      for (int qd = 0; qd < HT; ++qd)
-        u[qd][slot] = quad_sum(fmaf((float)sz[0], cs[qd][blk][e], (float)sz[1] * qsn[qd]));
+      for (int qd = 0; qd < HT; ++qd) {
+        float t = 0.0f;
+#pragma unroll
+        for (int hf = 0; hf < NH; ++hf) {
+          const v2h sz = __builtin_bit_cast(v2h, sm_w[(64 * hf + 16 * g + slot) * 4 + gp]);
+          const float th = fmaf((float)sz[0], cs[hf][qd][blk][e], (float)sz[1] * qsn[hf][qd]);
+          t = hf == 0 ? th : t + th;
+        }
+        u[qd][slot] = quad_sum(t);
+      }
     }
   if (MASK) {
 #pragma unroll
@@ -204,37 +241,46 @@ __device__ __forceinline__ void compute_tile4(const Tile4<D>& T, State4<D, G>& s
     st.m_run[qd] = m_new;
   }
 
-  // A operand of P V: row j = p(head) * s_v of group G' = j&3, slots of each
-  // half in the V unpack order; zero-point sums of the same (head, G')
-  v8h pa[HT][2];
-  float ze[HT], zo[HT];
+  // A operand of P V, per half of the dims: row j = p(head) * s_v of group
+  // G' = j&3 of the half, slots of each half-page in the V unpack order;
+  // zero-point sums of the same (head, G')
+  v8h pa[NH][HT][2];
+  float ze[NH][HT], zo[NH][HT];
 #pragma unroll
-  for (int qd = 0; qd < HT; ++qd) ze[qd] = zo[qd] = 0.0f;
+  for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-  for (int half = 0; half < 2; ++half)
+    for (int qd = 0; qd < HT; ++qd) ze[hf][qd] = zo[hf][qd] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int slot = 8 * half + sub_elem(i);
-      const v2h sz = __builtin_bit_cast(v2h, sm_w[(64 + 16 * g + slot) * 4 + gp]);
+  for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-      for (int qd = 0; qd < HT; ++qd) {
-        float a = p[qd][slot] * (float)sz[0];
-        float z = p[qd][slot] * (float)sz[1];
-        if (MASK) {
-          // masked slots may hold stale parameters: select, do not multiply
-          a = (slot < nvalid && slot >= nlow) ? a : 0.0f;
-          z = (slot < nvalid && slot >= nlow) ? z : 0.0f;
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int slot = 8 * half + sub_elem(i);
+        const v2h sz =
+            __builtin_bit_cast(v2h, sm_w[(64 * (NH + hf) + 16 * g + slot) * 4 + gp]);
+#pragma unroll
+        for (int qd = 0; qd < HT; ++qd) {
+          float a = p[qd][slot] * (float)sz[0];
+          float z = p[qd][slot] * (float)sz[1];
+          if (MASK) {
+            // masked slots may hold stale parameters: select, do not multiply
+            a = (slot < nvalid && slot >= nlow) ? a : 0.0f;
+            z = (slot < nvalid && slot >= nlow) ? z : 0.0f;
+          }
+          pa[hf][qd][half][i] = (_Float16)a;
+          if (slot & 1)
+            zo[hf][qd] += z;
+          else
+            ze[hf][qd] += z;
         }
-        pa[qd][half][i] = (_Float16)a;
-        if (slot & 1)
-          zo[qd] += z;
-        else
-          ze[qd] += z;
       }
-    }
 #pragma unroll
-  for (int qd = 0; qd < HT; ++qd)
-    st.zacc[qd] = st.zacc[qd] * alpha[qd] + xgroup_sum(fmaf(zo[qd], 16.0f, ze[qd]));
+  for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+    for (int qd = 0; qd < HT; ++qd)
+      st.zacc[hf][qd] =
+          st.zacc[hf][qd] * alpha[qd] + xgroup_sum(fmaf(zo[hf][qd], 16.0f, ze[hf][qd]));
 
   // rescale factor of the head this lane accumulates in P V (4*qd + g)
   float apv[HT];
@@ -247,24 +293,31 @@ __device__ __forceinline__ void compute_tile4(const Tile4<D>& T, State4<D, G>& s
     apv[qd] = __int_as_float(g == 0 ? a0 : (g == 1 ? a1 : (g == 2 ? a2 : a3)));
   }
   // P V on the matrix cores; lane (dim, g) reads row (head g, group of dim)
+  // from the A operand of the dim's half
 #pragma unroll
   for (int jb = 0; jb < JB; ++jb) {
+    const int hf = jb / JBH;
     const v8h b0 = unpack_sub(T.vb[jb].x);
     const v8h b1 = unpack_sub(T.vb[jb].y);
 #pragma unroll
     for (int qd = 0; qd < HT; ++qd) {
       v4f co = v4f{0.f, 0.f, 0.f, 0.f};
-      co = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[qd][0], b0, co, 0, 0, 0);
-      co = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[qd][1], b1, co, 0, 0, 0);
-      st.acc[qd][jb] = st.acc[qd][jb] * apv[qd] + co[jb >> 1];
+      co = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[hf][qd][0], b0, co, 0, 0, 0);
+      co = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[hf][qd][1], b1, co, 0, 0, 0);
+      st.acc[qd][jb] = st.acc[qd][jb] * apv[qd] + co[(jb % JBH) >> 1];
     }
   }
 }
 
+// head_dim 256 runs one wave per SIMD with the whole register file (two
+// halves of tiles, query terms and dots)
 template <int D, int G, int NW>
-__global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * NW, D > 128 ? 1 : 8 / NW) void gqa_decode_int4_kernel(
+    DecodeParams p) {
   constexpr int HT = State4<D, G>::HT;
   constexpr int NG = D / 32;
+  constexpr int NH = Shape4<D>::NH;
+  constexpr int NGH = Shape4<D>::NGH;
   constexpr int JB = D / 16;
   constexpr size_t BB = block_bytes_int4(D);
   const int lane = threadIdx.x & 63;
@@ -292,32 +345,38 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   const int gp = r & 3;
   const int hh = r >> 2;
   const int Hq = p.kv_heads * G;
-  float x[HT][32];
+  // lane (r, g) holds dims 128 hf + 32g .. +31 of head 4*qd + hh
+  float x[NH][HT][32];
 #pragma unroll
-  for (int qd = 0; qd < HT; ++qd) {
-    const int h = 4 * qd + hh;
-    if (h < G && g < NG) {
-      const size_t qbase = ((size_t)b * Hq + kvh * G + h) * D + 32 * g;
-      float t[16];
-      load16(p.q, qbase, p.q_dtype, t);
+  for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x[qd][i] = t[i];
-      load16(p.q, qbase + 16, p.q_dtype, t);
+    for (int qd = 0; qd < HT; ++qd) {
+      const int h = 4 * qd + hh;
+      if (h < G && g < NGH) {
+        const size_t qbase = ((size_t)b * Hq + kvh * G + h) * D + 128 * hf + 32 * g;
+        float t[16];
+        load16(p.q, qbase, p.q_dtype, t);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x[qd][16 + i] = t[i];
-    } else {
+        for (int i = 0; i < 16; ++i) x[hf][qd][i] = t[i];
+        load16(p.q, qbase + 16, p.q_dtype, t);
 #pragma unroll
-      for (int i = 0; i < 32; ++i) x[qd][i] = 0.0f;
+        for (int i = 0; i < 16; ++i) x[hf][qd][16 + i] = t[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[hf][qd][i] = 0.0f;
+      }
     }
-  }
-  // cos / sin of dims 32g .. 32g + 31 of the lane, as two runs of 16
-  float4 cq4[2][4], sq4[2][4];
+  // cos / sin of the lane's dims of each half, as two runs of 16
+  float4 cq4[NH][2][4], sq4[NH][2][4];
   if (p.do_rotary) {
     const float* cr = p.cos_cache + (size_t)(L - 1) * (D / 2);
     const float* sr = p.sin_cache + (size_t)(L - 1) * (D / 2);
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
-      rope_load16<D>(cr, sr, 32 * min(g, NG - 1) + 16 * hf, p.interleaved, cq4[hf], sq4[hf]);
+    for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+        rope_load16<D>(cr, sr, 128 * hf + 32 * min(g, NGH - 1) + 16 * h2, p.interleaved,
+                       cq4[hf][h2], sq4[hf][h2]);
   }
 
   const int t_begin = origin + split * p.split_tokens;
@@ -350,81 +409,101 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   if (appender && my_tiles > 1) append();
 
   // ---- Q: RoPE at position L-1, normalised by the head's max|Q| ----
-  v8h Bh[HT][kChunks], Bl[HT][kChunks];
-  float qsn[HT], q_scale[HT];
+  v8h Bh[NH][HT][kChunks], Bl[NH][HT][kChunks];
+  float qsn[NH][HT], q_scale[HT];
 #pragma unroll
   for (int qd = 0; qd < HT; ++qd) {
     if (p.do_rotary) {
-      float y[32], cq[32], sq[32];
+      float y[NH][32], cq[NH][32], sq[NH][32];
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        float c16[16], s16[16];
-        rope_pick_all<0>(cq4[hf], sq4[hf], p.interleaved != 0, c16, s16);
+      for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          cq[16 * hf + i] = c16[i];
-          sq[16 * hf + i] = s16[i];
+        for (int h2 = 0; h2 < 2; ++h2) {
+          float c16[16], s16[16];
+          rope_pick_all<0>(cq4[hf][h2], sq4[hf][h2], p.interleaved != 0, c16, s16);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            cq[hf][16 * h2 + i] = c16[i];
+            sq[hf][16 * h2 + i] = s16[i];
+          }
         }
-      }
       if (p.interleaved) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i)
-          y[i] = rope_elem(cq[i], sq[i], x[qd][i], x[qd][i ^ 1], (i & 1) == 0);
+        for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+          for (int i = 0; i < 32; ++i)
+            y[hf][i] = rope_elem(cq[hf][i], sq[hf][i], x[hf][qd][i], x[hf][qd][i ^ 1], (i & 1) == 0);
+      } else if constexpr (NH == 2) {
+        // partner d +- 128: the other half, same lane and element
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int i = 0; i < 32; ++i)
+            y[hf][i] = rope_elem(cq[hf][i], sq[hf][i], x[hf][qd][i], x[hf ^ 1][qd][i], hf == 0);
       } else {
-        // partner d +- D/2: group g ^ (NG/2), the lane 16 * NG / 2 away
-        const bool first = g < NG / 2;
+        // partner d +- D/2: group g ^ (NGH/2), the lane 16 * NGH / 2 away
+        const bool first = g < NGH / 2;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
           float xp;
-          if constexpr (NG == 4) {
+          if constexpr (NGH == 4) {
             // permlane32_swap(x, x): [0] = lanes 0-31's x on both halves, [1] =
             // lanes 32-63's x on both halves
-            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[qd][i]),
-                                                       __float_as_uint(x[qd][i]), false, false);
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[0][qd][i]),
+                                                       __float_as_uint(x[0][qd][i]), false, false);
             xp = __uint_as_float(first ? sw[1] : sw[0]);
           } else {
-            xp = __shfl_xor(x[qd][i], 16, 64);
+            xp = __shfl_xor(x[0][qd][i], 16, 64);
           }
-          y[i] = rope_elem(cq[i], sq[i], x[qd][i], xp, first);
+          y[0][i] = rope_elem(cq[0][i], sq[0][i], x[0][qd][i], xp, first);
         }
       }
 #pragma unroll
-      for (int i = 0; i < 32; ++i) x[qd][i] = y[i];
-    }
-    float amax = 0.0f, sum = 0.0f;
+      for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      amax = fmaxf(amax, fabsf(x[qd][i]));
-      sum += x[qd][i];
+        for (int i = 0; i < 32; ++i) x[hf][qd][i] = y[hf][i];
+    }
+    float amax = 0.0f, sum[NH];
+#pragma unroll
+    for (int hf = 0; hf < NH; ++hf) {
+      sum[hf] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        amax = fmaxf(amax, fabsf(x[hf][qd][i]));
+        sum[hf] += x[hf][qd][i];
+      }
     }
     amax = xgroup_max(amax);
     const float norm = amax > 0.0f ? amax : 1.0f;
     const float inv = 1.0f / norm;
     // dots come out x 2^-20 (see the unpack), folded into the score scale
     q_scale[qd] = norm * p.scale_log2 * kTwo20;
-    // sum over group G' = j&3 of this head: held by lane (j, G')
-    const float gsum = __shfl(sum, r + 16 * gp, 64);
-    qsn[qd] = gsum * inv * (1.0f / kTwo20);
     const v8h zero = v8h{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      v8h qh, ql;
+    for (int hf = 0; hf < NH; ++hf) {
+      // sum over group G' = j&3 of the half for this head: held by lane (j, G')
+      const float gsum = __shfl(sum[hf], r + 16 * gp, 64);
+      qsn[hf][qd] = gsum * inv * (1.0f / kTwo20);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float yv = x[qd][8 * c + sub_elem(i)] * inv * (sub_small(i) ? 16.0f : 1.0f);
-        // hi and lo must split one f32 value; without this barrier the
-        // backend may fold the product into one of the two f16 conversions
-        // only (v_fma_mixlo_f16, a single rounding) and hi + lo drifts
-        __asm__("" : "+v"(yv));
-        const _Float16 hi = (_Float16)yv;
-        qh[i] = hi;
-        ql[i] = (_Float16)(yv - (float)hi);
+      for (int c = 0; c < 4; ++c) {
+        v8h qh, ql;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float yv = x[hf][qd][8 * c + sub_elem(i)] * inv * (sub_small(i) ? 16.0f : 1.0f);
+          // hi and lo must split one f32 value; without this barrier the
+          // backend may fold the product into one of the two f16 conversions
+          // only (v_fma_mixlo_f16, a single rounding) and hi + lo drifts
+          __asm__("" : "+v"(yv));
+          const _Float16 hi = (_Float16)yv;
+          qh[i] = hi;
+          ql[i] = (_Float16)(yv - (float)hi);
+        }
+        Bh[hf][qd][c] = g == gp ? qh : zero;
+        Bl[hf][qd][c] = g == gp ? ql : zero;
       }
-      Bh[qd][c] = g == gp ? qh : zero;
-      Bl[qd][c] = g == gp ? ql : zero;
     }
   }
-  __shared__ uint4 sm_par[NW][128];
+  __shared__ uint4 sm_par[NW][128 * NH];
 
   // ---- stream the split's tiles, ping-pong; the last one may be partial ----
   State4<D, G> st;
@@ -432,7 +511,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   for (int qd = 0; qd < HT; ++qd) {
     st.m_run[qd] = -INFINITY;
     st.l_run[qd] = 0.0f;
-    st.zacc[qd] = 0.0f;
+#pragma unroll
+    for (int hf = 0; hf < NH; ++hf) st.zacc[hf][qd] = 0.0f;
 #pragma unroll
     for (int jb = 0; jb < JB; ++jb) st.acc[qd][jb] = 0.0f;
   }
@@ -489,7 +569,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
   for (int qd = 0; qd < HT; ++qd) {
     const int h = 4 * qd + hh;
     if (g == 0 && h < G) {
-      if (gp < NG) sm_z[wave][h][gp] = st.zacc[qd];
+#pragma unroll
+      for (int hf = 0; hf < NH; ++hf)
+        if (gp < NGH) sm_z[wave][h][NGH * hf + gp] = st.zacc[hf][qd];
       if (gp == 0) {
         sm_m[wave][h] = st.m_run[qd];
         sm_l[wave][h] = st.l_run[qd];
@@ -535,10 +617,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_decode_int4_kernel(Decode
 
 template <int D, int G>
 hipError_t launch_g(const DecodeParams& p, int work_items, bool combine, hipStream_t st) {
-  if (p.waves == 8)
-    hipLaunchKernelGGL((gqa_decode_int4_kernel<D, G, 8>), dim3(work_items, p.kv_heads), dim3(512),
-                       0, st, p);
-  else
+  // head_dim 256: four waves (one per SIMD)
+  bool eight = false;
+  if constexpr (D <= 128) {
+    eight = p.waves == 8;
+    if (eight)
+      hipLaunchKernelGGL((gqa_decode_int4_kernel<D, G, 8>), dim3(work_items, p.kv_heads),
+                         dim3(512), 0, st, p);
+  }
+  if (!eight)
     hipLaunchKernelGGL((gqa_decode_int4_kernel<D, G, 4>), dim3(work_items, p.kv_heads), dim3(256),
                        0, st, p);
   hipError_t e = hipGetLastError();
@@ -553,7 +640,9 @@ hipError_t launch_d(const DecodeParams& p, int group, int work_items, bool combi
     case 1: return launch_g<D, 1>(p, work_items, combine, st);
     case 2: return launch_g<D, 2>(p, work_items, combine, st);
     case 4: return launch_g<D, 4>(p, work_items, combine, st);
-    case 8: return launch_g<D, 8>(p, work_items, combine, st);
+    case 8:
+      if constexpr (D <= 128) return launch_g<D, 8>(p, work_items, combine, st);
+      return hipErrorInvalidValue;  // head_dim 256: groups up to 4
     default: return hipErrorInvalidValue;
   }
 }
@@ -567,6 +656,7 @@ hipError_t launch_gqa_decode_int4(const DecodeParams& p, int head_dim, int group
     return hipErrorInvalidValue;
   if (head_dim == 128) return launch_d<128>(p, group, work_items, combine, st);
   if (head_dim == 64) return launch_d<64>(p, group, work_items, combine, st);
+  if (head_dim == 256 && group <= 4) return launch_d<256>(p, group, work_items, combine, st);
   return hipErrorInvalidValue;
 }
 

@@ -357,9 +357,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   constexpr int HALF = D / 2;
 
   // int8 at head_dim <= 128 keeps four tiles in LDS and computes two per
-  // barrier (4 x 38.4 KB at 128); the larger int4 and head_dim-256 tiles keep two
-  constexpr int NSLOT = (!INT4 && D <= 128) ? 4 : 2;
-  constexpr int PER_BARRIER = NSLOT / 2;
+  // barrier (4 x 38.4 KB at 128); int4 up to 128 and int8 at 256 keep two;
+  // int4 at 256 (an f16 hi + lo K tile and the V tile, 109 KB) keeps one and
+  // stages behind a second barrier
+  constexpr int NSLOT = (!INT4 && D <= 128) ? 4 : ((INT4 && D > 128) ? 1 : 2);
+  constexpr int PER_BARRIER = NSLOT == 4 ? 2 : 1;
   __shared__ Tile sT[NSLOT];
 
   const int tid = threadIdx.x;
@@ -655,23 +657,41 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   // PER_BARRIER tiles between barriers; each stages the tile PER_BARRIER
   // ahead into the slot the previous round finished reading (its global loads
   // in flight while the tile is computed, the page ids of the one after)
-  for (int tile = tile_lo; tile < n_tiles; tile += PER_BARRIER) {
-    // not unrolled: one copy of the tile body keeps the register budget
-#pragma nounroll
-    for (int h = 0; h < PER_BARRIER; ++h) {
-      const int tt = tile + h;
-      if (tt < n_tiles) {
-        const int nxt = tt + PER_BARRIER;
-        const bool more = nxt < n_tiles;
-        if (more) {
-          load_stage(nxt * 64);
-          pages.load(pt, nxt + 1, last_page, tid);  // consumed by the next stage
-        }
-        process(slot(tt), tt);
-        if (more) store_stage(slot(nxt), nxt * 64);
+  if constexpr (NSLOT == 1) {
+    // one slot: the next tile's loads are in flight while this one is
+    // computed, and it is stored once every wave has finished reading
+    for (int tile = tile_lo; tile < n_tiles; ++tile) {
+      const bool more = tile + 1 < n_tiles;
+      if (more) {
+        load_stage((tile + 1) * 64);
+        pages.load(pt, tile + 2, last_page, tid);
+      }
+      process(sT[0], tile);
+      __syncthreads();
+      if (more) {
+        store_stage(sT[0], (tile + 1) * 64);
+        __syncthreads();
       }
     }
-    __syncthreads();
+  } else {
+    for (int tile = tile_lo; tile < n_tiles; tile += PER_BARRIER) {
+      // not unrolled: one copy of the tile body keeps the register budget
+#pragma nounroll
+      for (int h = 0; h < PER_BARRIER; ++h) {
+        const int tt = tile + h;
+        if (tt < n_tiles) {
+          const int nxt = tt + PER_BARRIER;
+          const bool more = nxt < n_tiles;
+          if (more) {
+            load_stage(nxt * 64);
+            pages.load(pt, nxt + 1, last_page, tid);  // consumed by the next stage
+          }
+          process(slot(tt), tt);
+          if (more) store_stage(slot(nxt), nxt * 64);
+        }
+      }
+      __syncthreads();
+    }
   }
 
   // ---- write O / l ------------------------------------------------------------
@@ -724,7 +744,9 @@ hipError_t launch_gqa_prefill(const PrefillParams& p, int head_dim, int group, i
   if (quant != kQuantInt8 && quant != kQuantInt4) return hipErrorInvalidValue;
   if (head_dim == 64) return launch_d<64>(p, group, quant, st);
   if (head_dim == 128) return launch_d<128>(p, group, quant, st);
-  if (head_dim == 256 && quant == kQuantInt8) return launch_dn<256, 8, kQuantInt8>(p, group, st);
+  if (head_dim == 256)
+    return quant == kQuantInt8 ? launch_dn<256, 8, kQuantInt8>(p, group, st)
+                               : launch_dn<256, 8, kQuantInt4>(p, group, st);
   return hipErrorInvalidValue;
 }
 

@@ -457,6 +457,8 @@ hipError_t launch_kv_append(const AppendParams& p, int head_dim, int quant, hipS
       hipLaunchKernelGGL(kv_append_int4_kernel<64>, grid, dim3(256), 0, st, p, pairs);
     else if (head_dim == 128)
       hipLaunchKernelGGL(kv_append_int4_kernel<128>, grid, dim3(256), 0, st, p, pairs);
+    else if (head_dim == 256)
+      hipLaunchKernelGGL(kv_append_int4_kernel<256>, grid, dim3(256), 0, st, p, pairs);
     else
       return hipErrorInvalidValue;
     return hipGetLastError();

@@ -153,10 +153,10 @@ float sqrt_f32_newton(float x) {
 // Largest decode split (the kernel stages a split's page ids in LDS).
 constexpr int32_t kMaxDecodeSplit = 16384;
 
-// int8: head_dim 64, 128 and 256 (Gemma 3); int4: 64 and 128.
+// int8 and int4: head_dim 64, 128 and 256 (Gemma 3).
 bool supported_dims(int head_dim, int quant) {
-  if (quant == SAI_KV_INT8) return head_dim == 64 || head_dim == 128 || head_dim == 256;
-  if (quant == SAI_KV_INT4) return head_dim == 64 || head_dim == 128;
+  if (quant == SAI_KV_INT8 || quant == SAI_KV_INT4)
+    return head_dim == 64 || head_dim == 128 || head_dim == 256;
   return false;
 }
 
@@ -752,9 +752,6 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   const char* op = "gqa_decode";
   const int32_t W = visible_span(c->layer_window[layer], window);
   const int D = c->desc.head_dim;
-  if (c->desc.quant == SAI_KV_INT4 && D != 128 && D != 64)
-    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: int4 decode needs head_dim 64 or 128 (got %d)", op,
-                D);
   if (D == 256 && G > 4)
     return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: head_dim 256 supports groups of 1, 2 and 4 (got %d)",
                 op, G);
