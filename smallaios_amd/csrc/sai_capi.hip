@@ -98,9 +98,12 @@ struct sai_tqcache {
   int32_t batch = 0;
   int32_t pending = 0;
   float norm = 0.0f;
-  // attention split partials, sized at creation
+  // attention split partials, sized at creation, and the split tickets of
+  // each (sequence, kv head) (zero between launches: the workgroup that takes
+  // the last ticket resets it)
   float* partials = nullptr;
   size_t partial_floats = 0;
+  int32_t* counters = nullptr;
 };
 
 struct sai_kvcache {
@@ -1341,6 +1344,7 @@ SAI_API void sai_tqcache_destroy(sai_tqcache* c) {
   }
   if (c->d_lens) (void)hipFree(c->d_lens);
   if (c->partials) (void)hipFree(c->partials);
+  if (c->counters) (void)hipFree(c->counters);
   delete c;
 }
 
@@ -1405,7 +1409,9 @@ SAI_API sai_status sai_tqcache_create(sai_ctx* ctx, const sai_tqcache_desc* desc
   {
     const size_t units = (size_t)d.max_batch * d.num_kv_heads;
     const size_t n = (768 + 2 * units) * (d.head_dim > 128 ? 4 : 8) * (d.head_dim + 2);
-    if (hipMalloc(&c->partials, n * sizeof(float)) != hipSuccess) {
+    const size_t nc = units * sizeof(int32_t);
+    if (hipMalloc(&c->partials, n * sizeof(float)) != hipSuccess ||
+        hipMalloc(&c->counters, nc) != hipSuccess || hipMemset(c->counters, 0, nc) != hipSuccess) {
       sai_tqcache_destroy(c);
       return fail(ctx, SAI_ERR_ALLOC, "tq_cache: workspace");
     }
@@ -1714,13 +1720,14 @@ sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, c
   if (mode != 0 && ld < max_len)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: row stride %d below the %d positions", op, ld,
                 max_len);
-  // automatic split: about 768 workgroups (three 4-wave workgroups per CU,
-  // measured best at 16 x 8192 x 8 kv heads against one, two or four per
-  // CU), in multiples of 256 positions
+  // automatic split: about 512 workgroups (two 4-wave workgroups per CU; at
+  // 16 x 8192 x 8 kv heads with the cache streamed from HBM, 2048 positions
+  // per split measured 4-6 % faster than 1536 or 2816 and 20 % faster than
+  // 1024), in multiples of 256 positions
   int32_t split_rows = ctx->tq_split;
   if (split_rows <= 0) {
     const int64_t units = (int64_t)batch * H;
-    const int64_t want = std::max<int64_t>(1, std::min<int64_t>((768 + units - 1) / units,
+    const int64_t want = std::max<int64_t>(1, std::min<int64_t>((512 + units - 1) / units,
                                                                 (max_len + 255) / 256));
     split_rows = (int32_t)(((max_len + want - 1) / want + 255) / 256 * 256);
   }
@@ -1746,6 +1753,7 @@ sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, c
   t.num_heads = num_heads;
   t.out = out;
   t.partials = c->partials;
+  t.counters = c->counters;
   t.weights = weights;
   t.ld = ld;
   t.normalize = mode == 0 ? 1 : 0;

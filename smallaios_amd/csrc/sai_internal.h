@@ -235,13 +235,14 @@ struct TqAttendArgs {
   int num_heads;
   float* out;       // [batch, 1, num_heads * D]
   float* partials;  // [batch][heads][max_splits][G * (D + 2)]
+  int* counters;    // [batch][heads] split tickets, zero between launches
   const float* weights;  // weighted value sum: [batch * num_heads][ld]
   int ld;                // row stride of logits / weights
   int normalize;         // 0: the weighted sum is not divided by the weights' sum
   const void* k_new;     // fused step: the pass's new row per (sequence, kv head),
   const void* v_new;     //   [batch, 1, heads * D], stored before it is attended
   int kv_bf16;
-  int split_rows, max_splits;
+  int split_rows, max_splits;  // max_splits: the launch grid's splits per sequence
   float scale_log2;
 };
 

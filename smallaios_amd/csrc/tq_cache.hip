@@ -22,8 +22,8 @@
 // C_q C_t (D - 2 popcount(sq ^ s_t)) / D. The values are summed in the
 // rotated domain on the f16 MFMA (weights p_t vs_t / S in f16, codes as exact
 // f16 subnormals code * 2^-24) and rotated back once per output (inverse
-// butterfly, signs), by the attention kernel for a single split and by the
-// merge kernel otherwise.
+// butterfly, signs) by the attention kernel: for a single split by its
+// workgroup, otherwise by the workgroup that stores the last split partial.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -44,19 +44,88 @@ __device__ __forceinline__ float round_half_away(float x) {
 #pragma clang fp contract(off)
   const float t = (float)sat_i32(x);
   const float f = x - t;
-  if (f >= 0.5f) return t + 1.0f;
-  if (f <= -0.5f) return t - 1.0f;
-  return t;
+  // selects, not branches (the values are the same)
+  const float up = t + 1.0f, dn = t - 1.0f;
+  return f >= 0.5f ? up : (f <= -0.5f ? dn : t);
 }
 
+// The value of lane `lane ^ H`, on VALU lane moves rather than LDS permutes:
+// DPP quad_perm (H = 1, 2), row_shl / row_shr by 4 (lane i reads i + 4 or
+// i - 4 within its row of 16; H = 4), row_ror by 8 (H = 8), and the gfx950
+// lane-swap instructions (H = 16, 32; swap(x, x) returns the even and the odd
+// halves, rows, each on both).
+template <int H>
+__device__ __forceinline__ float lane_xor(float v, int lane) {
+  const int x = __float_as_int(v);
+  if constexpr (H == 1) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
+  } else if constexpr (H == 2) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+  } else if constexpr (H == 4) {
+    const int up = __builtin_amdgcn_mov_dpp(x, 0x104, 0xF, 0xF, false);
+    const int dn = __builtin_amdgcn_mov_dpp(x, 0x114, 0xF, 0xF, false);
+    return __int_as_float((lane & 4) ? dn : up);
+  } else if constexpr (H == 8) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false));
+  } else if constexpr (H == 16) {
+    const auto s = __builtin_amdgcn_permlane16_swap((uint32_t)x, (uint32_t)x, false, false);
+    return __uint_as_float((lane & 16) ? s[0] : s[1]);
+  } else {
+    static_assert(H == 32, "lane_xor: H is a power of two up to 32");
+    const auto s = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)x, false, false);
+    return __uint_as_float((lane & 32) ? s[0] : s[1]);
+  }
+}
+
+// Wave reductions over lane_xor (the same partners, hence the same results,
+// as the __shfl_xor forms).
 __device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
-  return v;
+  const int lane = threadIdx.x & 63;
+  v = fminf(v, lane_xor<32>(v, lane));
+  v = fminf(v, lane_xor<16>(v, lane));
+  v = fminf(v, lane_xor<8>(v, lane));
+  v = fminf(v, lane_xor<4>(v, lane));
+  v = fminf(v, lane_xor<2>(v, lane));
+  return fminf(v, lane_xor<1>(v, lane));
+}
+__device__ __forceinline__ float tq_wave_max(float v) {
+  const int lane = threadIdx.x & 63;
+  v = fmaxf(v, lane_xor<32>(v, lane));
+  v = fmaxf(v, lane_xor<16>(v, lane));
+  v = fmaxf(v, lane_xor<8>(v, lane));
+  v = fmaxf(v, lane_xor<4>(v, lane));
+  v = fmaxf(v, lane_xor<2>(v, lane));
+  return fmaxf(v, lane_xor<1>(v, lane));
+}
+__device__ __forceinline__ float tq_wave_sum(float v) {
+  const int lane = threadIdx.x & 63;
+  v += lane_xor<32>(v, lane);
+  v += lane_xor<16>(v, lane);
+  v += lane_xor<8>(v, lane);
+  v += lane_xor<4>(v, lane);
+  v += lane_xor<2>(v, lane);
+  return v + lane_xor<1>(v, lane);
 }
 
+// Element i of an f32 or bf16 row. One aligned dword load either way (for
+// bf16 the word holding elements i & ~1 and i | 1) and a select, no branch:
+// the compiler then counts the load's place among later loads exactly and
+// waits for it alone.
 __device__ __forceinline__ float load_row_elem(const void* p, size_t i, bool bf16) {
-  return bf16 ? __uint_as_float((uint32_t)((const uint16_t*)p)[i] << 16) : ((const float*)p)[i];
+  const uint32_t w = *(const uint32_t*)((const char*)p + (bf16 ? (i * 2) & ~(size_t)3 : i * 4));
+  return __uint_as_float(bf16 ? ((i & 1) ? (w & 0xFFFF0000u) : (w << 16)) : w);
+}
+
+// One butterfly stage below 64: dims l and l ^ H of each lane pair into
+// (a + b, a - b), the sum at the lower dim.
+template <int H, int E>
+__device__ __forceinline__ void butterfly_stage(float (&y)[E], int lane) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float p = lane_xor<H>(y[e], lane);
+    y[e] = (lane & H) ? p - y[e] : y[e] + p;
+  }
 }
 
 // The reference's butterfly (wht_butterfly_normalize, :81-110) over a row
@@ -67,14 +136,12 @@ template <int D>
 __device__ __forceinline__ void wave_butterfly(float (&y)[D / 64], int lane, float norm) {
 #pragma clang fp contract(off)
   constexpr int E = D / 64;
-#pragma unroll
-  for (int h = 1; h < 64; h <<= 1) {
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float p = __shfl_xor(y[e], h, 64);
-      y[e] = (lane & h) ? p - y[e] : y[e] + p;
-    }
-  }
+  butterfly_stage<1>(y, lane);
+  butterfly_stage<2>(y, lane);
+  butterfly_stage<4>(y, lane);
+  butterfly_stage<8>(y, lane);
+  butterfly_stage<16>(y, lane);
+  butterfly_stage<32>(y, lane);
   // stages 64, 128, ...: pairs of the lane's own dims, (e, e + h/64)
 #pragma unroll
   for (int hs = 1; hs < E; hs <<= 1)
@@ -108,7 +175,7 @@ __device__ __forceinline__ void wave_encode(const float (&x)[D / 64], const floa
     mx = fmaxf(mx, y[e]);
   }
   mn = wave_min(mn);
-  mx = wave_max(mx);
+  mx = tq_wave_max(mx);
   if (mn == 0.0f) {
     // the reference keeps the first minimum in dim order: with a zero
     // minimum, the sign of the first zero
@@ -140,9 +207,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // QJLResidualEncoder::encode (:365-395) of x against decode(code): the sign
-// words (uniform, word j = dims 32j .. 32j+31) and C = sum|r| / D, summed in
-// dim order by lane 0. sres: the wave's D floats of LDS.
-template <int D>
+// words (uniform, word j = dims 32j .. 32j+31) and C = sum|r| / D. Stored rows
+// (DIM_ORDER) sum in dim order on lane 0, as the reference does, through
+// sres (the wave's D floats of LDS); the attention's query, whose C only
+// scales its logit correction, sums by a wave reduction.
+template <int D, bool DIM_ORDER = true>
 __device__ __forceinline__ float wave_qjl(const uint32_t (&code)[D / 64], float scale, float zero,
                                           const float (&x)[D / 64], const float (&sgn)[D / 64],
                                           int lane, float norm, float* sres,
@@ -153,12 +222,21 @@ __device__ __forceinline__ float wave_qjl(const uint32_t (&code)[D / 64], float 
 #pragma unroll
   for (int e = 0; e < E; ++e) y[e] = (float)code[e] * scale + zero;
   wave_butterfly<D>(y, lane, norm);
+  float ra[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const float r = x[e] - y[e] * sgn[e];
     sbits[e] = __ballot(r >= 0.0f);
-    sres[lane + 64 * e] = fabsf(r);
+    ra[e] = fabsf(r);
   }
+  if constexpr (!DIM_ORDER) {
+    float part = ra[0];
+#pragma unroll
+    for (int e = 1; e < E; ++e) part += ra[e];
+    return tq_wave_sum(part) / (float)D;
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) sres[lane + 64 * e] = ra[e];
   wave_lds_sync();
   float c = 0.0f;
   if (lane == 0) {
@@ -167,7 +245,7 @@ __device__ __forceinline__ float wave_qjl(const uint32_t (&code)[D / 64], float 
     for (int i = 0; i < D; ++i) sum += sres[i];
     c = sum / (float)D;
   }
-  c = __shfl(c, 0, 64);
+  c = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(c)));
   wave_lds_sync();  // sres is reused by the wave's next row
   return c;
 }
@@ -195,7 +273,7 @@ __device__ __forceinline__ void wave_store_row(const TqArgs& a, const float (&x)
   float csum = 0.0f;
 #pragma unroll
   for (int e = 0; e < E; ++e) csum += (float)code[e];
-  csum = wave_sum(csum);  // integers below 2^24: exact
+  csum = tq_wave_sum(csum);  // integers below 2^24: exact
   const size_t row = ((size_t)h * a.batch_cap + b) * a.rows_cap + r;
   if (kind == 0) {
 #pragma unroll
@@ -560,22 +638,19 @@ __device__ __forceinline__ int q_code_pos(int d) {
 //               kappa = C / D, each times scale * log2(e)
 //   sgn[D/32]   QJL sign words
 // where qc' = qc - 2^(bits-1) and qz' = qz + qs 2^(bits-1), so that
-// decode(q) rotated = qs qc' + qz'.
+// decode(q) rotated = qs qc' + qz'. x: the query row (lane l: dims l + 64 e),
+// sgn: the kv head's signs, both loaded by the caller.
 template <int D, int BITS>
-__device__ __forceinline__ void wave_encode_query(const TqArgs& a, const TqAttendArgs& t, int b,
-                                                  int qh, int kvh, int lane, float* sres,
-                                                  uint32_t* codes, float* coef, uint32_t* sgw) {
+__device__ __forceinline__ void wave_encode_query(const TqArgs& a, const TqAttendArgs& t,
+                                                  const float (&x)[D / 64],
+                                                  const float (&sgn)[D / 64], int lane,
+                                                  float* sres, uint32_t* codes, float* coef,
+                                                  uint32_t* sgw) {
 #pragma clang fp contract(off)
   constexpr int E = D / 64;
   constexpr int C0 = 1 << (BITS - 1);
-  const size_t qo = ((size_t)b * t.num_heads + qh) * D;
-  float x[E], y[E], sgn[E], scale, zero;
+  float y[E], scale, zero;
   uint32_t code[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    sgn[e] = (float)a.signs[(size_t)kvh * D + lane + 64 * e];
-    x[e] = load_row_elem(t.q, qo + lane + 64 * e, t.q_bf16 != 0);
-  }
   wave_encode<D, BITS>(x, sgn, lane, a.norm, y, code, scale, zero);
   float sq = 0.0f;
 #pragma unroll
@@ -584,12 +659,12 @@ __device__ __forceinline__ void wave_encode_query(const TqArgs& a, const TqAtten
     sq += (float)cc;
     ((int8_t*)codes)[q_code_pos<BITS>(lane + 64 * e)] = (int8_t)cc;
   }
-  sq = wave_sum(sq);
+  sq = tq_wave_sum(sq);
   float c = 0.0f;
   uint64_t sb[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) sb[e] = 0;
-  if (a.qjl) c = wave_qjl<D>(code, scale, zero, x, sgn, lane, a.norm, sres, sb);
+  if (a.qjl) c = wave_qjl<D, false>(code, scale, zero, x, sgn, lane, a.norm, sres, sb);
   if (lane == 0) {
     const float qz = zero + scale * (float)C0;
     coef[0] = scale * t.scale_log2;
@@ -694,47 +769,78 @@ __device__ __forceinline__ void rotate_back(const TqArgs& a, const TqAttendArgs&
   }
 }
 
-// Merge of the split partials of one (kv head, sequence) with more than one
-// split, then the rotation back. One thread per (head, dim); every thread
-// has the (m, l, o) loads of 16 splits in flight at once (the partials were
-// written by workgroups on other XCDs: each round is one memory latency).
-template <int D, int G>
-__global__ __launch_bounds__(G * D) void tq_merge_kernel(const TqArgs a, TqAttendArgs t) {
-  const int kvh = blockIdx.x, b = blockIdx.y;
-  const int L = a.seq_lens[b] + a.pending;
-  const int nsplit = (L + t.split_rows - 1) / t.split_rows;
-  if (nsplit <= 1) return;  // finished by the attention kernel
-  const int g = threadIdx.x / D, i = threadIdx.x % D;
-  const size_t pstride = (size_t)G * (D + 2);
-  const float* part0 = t.partials + ((size_t)b * a.heads + kvh) * t.max_splits * pstride;
-  float M = -INFINITY, Ls = 0.0f, O = 0.0f;
-  for (int s0 = 0; s0 < nsplit; s0 += 16) {
-    float pm[16], pl[16], po[16];
+// ---- attention ---------------------------------------------------------------
+// One lane's share of a 64-position tile: its position's K codes, parameters
+// and sign words, and the V codes of its dims over the tile's positions.
+template <int D, int BITS, int MODE>
+struct TqTile {
+  static constexpr int KWL = (D * BITS / 32 + 3) / 4 * 4;  // K words loaded
+  static constexpr int DH = D / 64;
+  static constexpr int TBW = 2 * BITS;  // V words per dim per tile
+  uint32_t kc[MODE != 2 ? KWL : 1];
+  uint32_t ks[D / 32];
+  uint32_t vc[DH][MODE != 1 ? TBW : 1];
+  float4 kp, vp;
+};
+
+// Loads tile tile0's share for this lane (positions past r1 read the tile's
+// first row, a valid one; the caller masks them). Branch-free, so that the
+// compiler knows at every later use how many loads were issued after each
+// one: without QJL the sign-word loads read K code bytes instead (rows of
+// code_stride >= D/8 bytes), whose values are never used.
+template <int D, int BITS, int MODE>
+__device__ __forceinline__ void tq_load_tile(const TqArgs& a, size_t rbase, const uint8_t* vbase,
+                                             int tile0, int r1, int lane,
+                                             TqTile<D, BITS, MODE>& T) {
+  using Tl = TqTile<D, BITS, MODE>;
+  const int row = tile0 + lane;
+  const size_t rr = rbase + (row < r1 ? row : tile0);
+  if constexpr (MODE != 2) {
+    const uint4* src = (const uint4*)(a.codes_k + rr * a.code_stride);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float* ps = part0 + (size_t)min(s0 + j, nsplit - 1) * pstride + g * (D + 2);
-      pm[j] = ps[0];
-      pl[j] = ps[1];
-      po[j] = ps[2 + i];
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (s0 + j >= nsplit || pm[j] == -INFINITY) continue;
-      const float Mn = fmaxf(M, pm[j]);
-      const float fa = fast_exp2(M - Mn);
-      const float fb = fast_exp2(pm[j] - Mn);
-      Ls = Ls * fa + pl[j] * fb;
-      O = O * fa + po[j] * fb;
-      M = Mn;
+    for (int j = 0; j < Tl::KWL / 4; ++j) {
+      const uint4 w4 = src[j];
+      T.kc[4 * j] = w4.x;
+      T.kc[4 * j + 1] = w4.y;
+      T.kc[4 * j + 2] = w4.z;
+      T.kc[4 * j + 3] = w4.w;
     }
   }
-  __shared__ float sy[G][D];
-  sy[g][i] = t.normalize ? (Ls > 0.0f ? O / Ls : 0.0f) : O;
-  __syncthreads();
-  rotate_back<D, G, G * D>(a, t, b, kvh, sy);
+  T.kp = a.par_k[rr];
+  T.vp = a.par_v[rr];
+  if constexpr (MODE != 2) {
+    const uint8_t* sbase = a.qjl ? (const uint8_t*)a.signs_k : a.codes_k;
+    const size_t sstride = a.qjl ? (size_t)(D / 8) : a.code_stride;
+    const uint8_t* srow = sbase + rr * sstride;
+#pragma unroll
+    for (int j = 0; j < D / 128; ++j) {
+      const uint4 w4 = ((const uint4*)srow)[j];
+      T.ks[4 * j] = w4.x;
+      T.ks[4 * j + 1] = w4.y;
+      T.ks[4 * j + 2] = w4.z;
+      T.ks[4 * j + 3] = w4.w;
+    }
+    if constexpr (D == 64) {  // two words
+      const uint2 w2 = *(const uint2*)srow;
+      T.ks[0] = w2.x;
+      T.ks[1] = w2.y;
+    }
+  }
+  if constexpr (MODE != 1) {
+    const uint8_t* vt = vbase + (size_t)(tile0 / 64) * tq_vtile_bytes(D, BITS);
+#pragma unroll
+    for (int e = 0; e < Tl::DH; ++e) {
+      const uint2* src = (const uint2*)(vt + (size_t)(64 * e + lane) * (8 * BITS));
+#pragma unroll
+      for (int j = 0; j < Tl::TBW / 2; ++j) {
+        const uint2 w2 = src[j];
+        T.vc[e][2 * j] = w2.x;
+        T.vc[e][2 * j + 1] = w2.y;
+      }
+    }
+  }
 }
 
-// ---- attention ---------------------------------------------------------------
 // Workgroup = (split of split_rows positions, kv head, sequence), NW waves; a
 // wave takes 64-position tiles. Logits: lane = position, the group's heads in
 // quads (4x4x4 int8 MFMA: A = four heads' query codes, B = the lane's K row,
@@ -747,7 +853,8 @@ __global__ __launch_bounds__(G * D) void tq_merge_kernel(const TqArgs a, TqAtten
 // MODE 2: the weighted value sum alone (weighted_value_sum) of the weights
 // t.weights[(b, head)][position], not normalised.
 template <int D, int BITS, int G, int NW, int MODE>
-__global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAttendArgs t) {
+__global__ __launch_bounds__(64 * NW, (G <= 4 && D * BITS <= 512) ? 3 : 1) void tq_attend_kernel(
+    const TqArgs a, TqAttendArgs t) {
   constexpr int NQ = (G + 3) / 4;
   constexpr int KW = D * BITS / 32;
   constexpr int KWL = (KW + 3) / 4 * 4;  // words loaded (within code_stride)
@@ -756,10 +863,10 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   constexpr int TBW = 2 * BITS;          // V words per dim per tile
   constexpr int KOFF = BITS == 8 ? 128 : 0;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
-  const int split = blockIdx.x;
   const int L = a.seq_lens[b] + a.pending;
   const int r0 = split * t.split_rows;
   if (L == 0) {
@@ -771,6 +878,37 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   }
   if (r0 >= L) return;  // uniform: this split is past the sequence
   const int r1 = min(L, r0 + t.split_rows);
+  const size_t rbase = ((size_t)kvh * a.batch_cap + b) * a.rows_cap;
+  const uint8_t* vbase =
+      a.codes_v + ((size_t)kvh * a.batch_cap + b) * a.tiles_cap * tq_vtile_bytes(D, BITS);
+  // The group's query rows (one wave per head) and the kv head's signs are
+  // loaded first: the prologue waits for them, and loads complete in order.
+  constexpr int HPW = (G + NW - 1) / NW;  // query heads per wave
+  float qx[HPW][D / 64], qsg[D / 64];
+  // Every load below is unconditional (a wave without a head or a tile reads
+  // a valid one it does not use): the compiler's wait before each use then
+  // counts exactly the loads issued after it, on every path.
+  if constexpr (MODE != 2) {
+#pragma unroll
+    for (int e = 0; e < D / 64; ++e) qsg[e] = (float)a.signs[(size_t)kvh * D + lane + 64 * e];
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+      const int g = min(wave + NW * h, G - 1);
+#pragma unroll
+      for (int e = 0; e < D / 64; ++e)
+        qx[h][e] = load_row_elem(t.q, ((size_t)b * t.num_heads + kvh * G + g) * D + lane + 64 * e,
+                                 t.q_bf16 != 0);
+    }
+  }
+  // Two tile buffers: a wave loads its next tile before it computes the
+  // current one. The first tile's loads follow the query's, before the
+  // prologue (the query's wait then counts them as later loads). In the
+  // workgroup that stores the pass's new row, the wave whose first tile holds
+  // that row loads it again after the store.
+  TqTile<D, BITS, MODE> tb[2];
+  const bool fused_store = MODE == 0 && t.k_new != nullptr && r1 == L;
+  const int first = r0 + wave * 64;
+  tq_load_tile<D, BITS, MODE>(a, rbase, vbase, first < r1 ? first : r0, r1, lane, tb[0]);
 
   __shared__ uint32_t sqc[NQ * 4][NS];           // query code words (padding heads 0)
   __shared__ float sqf[G][4];                    // alpha, beta, gamma, kappa
@@ -796,11 +934,16 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   }
   if constexpr (MODE != 2) {
     for (int e = threadIdx.x; e < (NQ * 4 - G) * NS; e += 64 * NW) sqc[G + e / NS][e % NS] = 0u;
-    for (int g = wave; g < G; g += NW)
-      wave_encode_query<D, BITS>(a, t, b, kvh * G + g, kvh, lane, sres[wave], sqc[g], sqf[g],
-                                 sqs[g]);
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+      const int g = wave + NW * h;
+      if (g < G)
+        wave_encode_query<D, BITS>(a, t, qx[h], qsg, lane, sres[wave], sqc[g], sqf[g], sqs[g]);
+    }
   }
   __syncthreads();
+  if (fused_store && first < r1 && first + 64 >= L)
+    tq_load_tile<D, BITS, MODE>(a, rbase, vbase, first, r1, lane, tb[0]);
   // the query's coefficients and sign words are uniform: scalar registers
   float qa[G], qb[G], qg[G], qk[G];
   uint32_t qs[G][D / 32];
@@ -827,59 +970,12 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
 #pragma unroll
     for (int e = 0; e < DH; ++e) o_run[u][e] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const size_t rbase = ((size_t)kvh * a.batch_cap + b) * a.rows_cap;
-  const uint8_t* vbase =
-      a.codes_v + ((size_t)kvh * a.batch_cap + b) * a.tiles_cap * tq_vtile_bytes(D, BITS);
-  for (int tile0 = r0 + wave * 64; tile0 < r1; tile0 += 64 * NW) {
+  // one tile of this wave: logits, online softmax, value sums
+  auto process = [&](const TqTile<D, BITS, MODE>& T, int tile0) __attribute__((always_inline)) {
     const int row = tile0 + lane;
     const bool live = row < r1;
-    const size_t rr = rbase + (live ? row : tile0);
-    // this lane's K row, its parameters and sign words; V codes of its dims
-    uint32_t kc[KWL];
-    if constexpr (MODE != 2) {
-      const uint4* src = (const uint4*)(a.codes_k + rr * a.code_stride);
-#pragma unroll
-      for (int j = 0; j < KWL / 4; ++j) {
-        const uint4 w4 = src[j];
-        kc[4 * j] = w4.x;
-        kc[4 * j + 1] = w4.y;
-        kc[4 * j + 2] = w4.z;
-        kc[4 * j + 3] = w4.w;
-      }
-    }
-    const float4 kp = a.par_k[rr];
-    const float4 vp = a.par_v[rr];
-    uint32_t ks[D / 32];
-    if (MODE != 2 && a.qjl) {
-      const uint4* src = (const uint4*)(a.signs_k + rr * (D / 32));
-#pragma unroll
-      for (int j = 0; j < D / 128; ++j) {
-        const uint4 w4 = src[j];
-        ks[4 * j] = w4.x;
-        ks[4 * j + 1] = w4.y;
-        ks[4 * j + 2] = w4.z;
-        ks[4 * j + 3] = w4.w;
-      }
-      if constexpr (D == 64) {  // two words
-        const uint2 w2 = *(const uint2*)(a.signs_k + rr * (D / 32));
-        ks[0] = w2.x;
-        ks[1] = w2.y;
-      }
-    }
-    uint32_t vc[DH][TBW];
-    if constexpr (MODE != 1) {
-      const uint8_t* vt = vbase + (size_t)(tile0 / 64) * tq_vtile_bytes(D, BITS);
-#pragma unroll
-      for (int e = 0; e < DH; ++e) {
-        const uint2* src = (const uint2*)(vt + (size_t)(64 * e + lane) * (8 * BITS));
-#pragma unroll
-        for (int j = 0; j < TBW / 2; ++j) {
-          const uint2 w2 = src[j];
-          vc[e][2 * j] = w2.x;
-          vc[e][2 * j + 1] = w2.y;
-        }
-      }
-    }
+    const float4 kp = T.kp;
+    const float4 vp = T.vp;
     float lg[G];
     if constexpr (MODE != 2) {
     // logits: exact integer dot products on the int8 MFMA
@@ -888,7 +984,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
     for (int u = 0; u < NQ; ++u) ip[u] = intx4_t{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const int kb = k_operand<BITS, KWL>(kc, s);
+      const int kb = k_operand<BITS, KWL>(T.kc, s);
 #pragma unroll
       for (int u = 0; u < NQ; ++u)
         ip[u] = __builtin_amdgcn_mfma_i32_4x4x4i8((int)sqc[4 * u + (lane & 3)][s], kb, ip[u], 0, 0,
@@ -903,7 +999,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
       if (a.qjl) {
         int pop = 0;
 #pragma unroll
-        for (int j = 0; j < D / 32; ++j) pop += __popc(qs[g][j] ^ ks[j]);
+        for (int j = 0; j < D / 32; ++j) pop += __popc(qs[g][j] ^ T.ks[j]);
         dot += qk[g] * kp.z * (float)(D - 2 * pop);
       }
       lg[g] = live ? dot : -INFINITY;
@@ -913,8 +1009,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
 #pragma unroll
       for (int g = 0; g < G; ++g)
         if (live) t.out[((size_t)b * t.num_heads + kvh * G + g) * t.ld + row] = lg[g];
-      continue;
-    }
+    } else {
     // online softmax (log2 domain); the running max moves only when a lane
     // exceeds it
     float alpha[G];
@@ -922,7 +1017,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
     for (int g = 0; g < G; ++g) {
       alpha[g] = 1.0f;
       if (MODE == 0 && __ballot(lg[g] > m_run[g])) {
-        const float m_new = fmaxf(m_run[g], wave_max(lg[g]));
+        const float m_new = fmaxf(m_run[g], tq_wave_max(lg[g]));
         alpha[g] = fast_exp2(m_run[g] - m_new);
         m_run[g] = m_new;
       }
@@ -930,7 +1025,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
     // weights: P' = f16(p vs / S); the row's whole value (vs code + vz) and
     // the normaliser take the same rounded weight p' = P' S / vs, so the
     // f16 rounding perturbs each weight instead of splitting the row
-    const float vsmax = wave_max(live ? vp.x : 0.0f);
+    const float vsmax = tq_wave_max(live ? vp.x : 0.0f);
     const float vsn = vp.x / vsmax;
     const float rvsn = vsmax / vp.x;
     const int slot = p_slot<BITS>(lane);
@@ -965,7 +1060,7 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
       for (int u = 0; u < NQ; ++u) pa[u] = *(const half4_t*)&sp[wave][4 * u + (lane & 3)][4 * s];
 #pragma unroll
       for (int e = 0; e < DH; ++e) {
-        const half4_t vb = v_operand<BITS, TBW>(vc[e], s);
+        const half4_t vb = v_operand<BITS, TBW>(T.vc[e], s);
 #pragma unroll
         for (int u = 0; u < NQ; ++u)
           mf[u][e] = __builtin_amdgcn_mfma_f32_4x4x4f16(pa[u], vb, mf[u][e], 0, 0, 0);
@@ -983,6 +1078,19 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
         }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    }  // MODE != 1
+  };
+  // The next tile's loads are issued unconditionally: past the split's end
+  // they re-read the current tile (cache hits), so no branch separates a
+  // load from its use.
+  for (int tile0 = first; tile0 < r1; tile0 += 128 * NW) {
+    const int t1 = tile0 + 64 * NW;
+    tq_load_tile<D, BITS, MODE>(a, rbase, vbase, t1 < r1 ? t1 : tile0, r1, lane, tb[1]);
+    process(tb[0], tile0);
+    if (t1 >= r1) break;
+    const int t2 = t1 + 64 * NW;
+    tq_load_tile<D, BITS, MODE>(a, rbase, vbase, t2 < r1 ? t2 : t1, r1, lane, tb[0]);
+    process(tb[1], t1);
   }
   if constexpr (MODE == 1) return;
   // merge the waves through LDS
@@ -991,8 +1099,8 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
   __shared__ float sy[G][D];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float lsum = wave_sum(l_run[g]);
-    const float zsum = wave_sum(z_run[g]);
+    const float lsum = tq_wave_sum(l_run[g]);
+    const float zsum = tq_wave_sum(z_run[g]);
     if (lane == 0) {
       sm_m[wave][g] = m_run[g];
       sm_l[wave][g] = lsum;
@@ -1027,14 +1135,39 @@ __global__ __launch_bounds__(64 * NW) void tq_attend_kernel(const TqArgs a, TqAt
       sy[g][i] = MODE == 2 ? O : (Ls > 0.0f ? O / Ls : 0.0f);
     } else {
       float* part = part0 + split * pstride + g * (D + 2);
-      part[2 + i] = O;
+      store_partial(part + 2 + i, O);
       if (i == 0) {
-        part[0] = M;
-        part[1] = Ls;
+        store_partial(part, M);
+        store_partial(part + 1, Ls);
       }
     }
   }
-  if (nsplit > 1) return;  // tq_merge_kernel finishes
+  if (nsplit > 1) {
+    // The workgroup with the last ticket of (sequence, kv head) merges every
+    // split's partial, its own included, in split order (the result does not
+    // depend on which one finished last). The partial stores are agent-scope
+    // and complete before the ticket is taken, so the other XCDs see them.
+    __shared__ int sm_last;
+    partials_complete();
+    __syncthreads();
+    int* counter = t.counters + (size_t)b * a.heads + kvh;
+    if (threadIdx.x == 0) sm_last = last_ticket(counter, nsplit);
+    __syncthreads();
+    if (!sm_last) return;
+    for (int e = threadIdx.x; e < G * D; e += 64 * NW) {
+      const int g = e / D, i = e % D;
+      float M = -INFINITY, Ls = 0.0f, O = 0.0f;
+      const float* ph = part0 + g * (D + 2);
+      if (nsplit <= 4)
+        merge_partials<4>(ph, pstride, i, nsplit, -1, M, Ls, O);
+      else if (nsplit <= 8)
+        merge_partials<8>(ph, pstride, i, nsplit, -1, M, Ls, O);
+      else
+        merge_partials<16>(ph, pstride, i, nsplit, -1, M, Ls, O);
+      sy[g][i] = MODE == 2 ? O : (Ls > 0.0f ? O / Ls : 0.0f);
+    }
+    if (threadIdx.x == 0) reset_ticket(counter);
+  }
   __syncthreads();
   rotate_back<D, G, 64 * NW>(a, t, b, kvh, sy);
 }
@@ -1050,21 +1183,6 @@ hipError_t attend_db(const TqArgs& a, const TqAttendArgs& t, int group, int nspl
     case 8:
       if constexpr (D <= 128) {
         hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 8, 4, MODE>), grid, dim3(256), 0, st, a, t);
-        break;
-      }
-      return hipErrorInvalidValue;
-    default: return hipErrorInvalidValue;
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || MODE == 1 || nsplit <= 1) return e;
-  const dim3 mg(a.heads, batch);
-  switch (group) {
-    case 1: hipLaunchKernelGGL((tq_merge_kernel<D, 1>), mg, dim3(D), 0, st, a, t); break;
-    case 2: hipLaunchKernelGGL((tq_merge_kernel<D, 2>), mg, dim3(2 * D), 0, st, a, t); break;
-    case 4: hipLaunchKernelGGL((tq_merge_kernel<D, 4>), mg, dim3(4 * D), 0, st, a, t); break;
-    case 8:
-      if constexpr (D <= 128) {
-        hipLaunchKernelGGL((tq_merge_kernel<D, 8>), mg, dim3(8 * D), 0, st, a, t);
         break;
       }
       return hipErrorInvalidValue;
