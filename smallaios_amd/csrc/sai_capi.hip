@@ -1720,16 +1720,18 @@ sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, c
   if (mode != 0 && ld < max_len)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: row stride %d below the %d positions", op, ld,
                 max_len);
-  // automatic split: about 512 workgroups (two 4-wave workgroups per CU; at
-  // 16 x 8192 x 8 kv heads with the cache streamed from HBM, 2048 positions
-  // per split measured 4-6 % faster than 1536 or 2816 and 20 % faster than
-  // 1024), in multiples of 256 positions
+  // automatic split: about one workgroup per CU (256; 8 waves each up to
+  // head_dim 128, 4 at 256), in multiples of one 64-position tile per wave.
+  // A second workgroup on a CU starts its stream late: its loads queue behind
+  // the first one's. At 16 x 8192 x 8 kv heads, streamed from HBM, 2 splits of
+  // 8 waves measured 40.1 us per step against 44.3 for 4 splits of 4 waves.
   int32_t split_rows = ctx->tq_split;
   if (split_rows <= 0) {
     const int64_t units = (int64_t)batch * H;
-    const int64_t want = std::max<int64_t>(1, std::min<int64_t>((512 + units - 1) / units,
-                                                                (max_len + 255) / 256));
-    split_rows = (int32_t)(((max_len + want - 1) / want + 255) / 256 * 256);
+    const int64_t quantum = D <= 128 ? 512 : 256;
+    const int64_t want = std::max<int64_t>(
+        1, std::min<int64_t>((256 + units - 1) / units, (max_len + quantum - 1) / quantum));
+    split_rows = (int32_t)(((max_len + want - 1) / want + quantum - 1) / quantum * quantum);
   }
   const int32_t max_splits = (max_len + split_rows - 1) / split_rows;
   const size_t part_floats = (size_t)batch * H * max_splits * G * (D + 2);

@@ -853,7 +853,7 @@ __device__ __forceinline__ void tq_load_tile(const TqArgs& a, size_t rbase, cons
 // MODE 2: the weighted value sum alone (weighted_value_sum) of the weights
 // t.weights[(b, head)][position], not normalised.
 template <int D, int BITS, int G, int NW, int MODE>
-__global__ __launch_bounds__(64 * NW, (G <= 4 && D * BITS <= 512) ? 3 : 1) void tq_attend_kernel(
+__global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
     const TqArgs a, TqAttendArgs t) {
   constexpr int NQ = (G + 3) / 4;
   constexpr int KW = D * BITS / 32;
@@ -1172,17 +1172,26 @@ __global__ __launch_bounds__(64 * NW, (G <= 4 && D * BITS <= 512) ? 3 : 1) void 
   rotate_back<D, G, 64 * NW>(a, t, b, kvh, sy);
 }
 
+// Waves per workgroup: 8 (two per SIMD, one workgroup per CU) up to head_dim
+// 128; at 256 the tile buffers need more registers than two waves per SIMD
+// leave, so 4.
+template <int D>
+constexpr int tq_attend_waves() {
+  return D <= 128 ? 8 : 4;
+}
+
 template <int D, int BITS, int MODE>
 hipError_t attend_db(const TqArgs& a, const TqAttendArgs& t, int group, int nsplit, int batch,
                      hipStream_t st) {
-  const dim3 grid(nsplit, a.heads, batch);
+  constexpr int NW = tq_attend_waves<D>();
+  const dim3 grid(nsplit, a.heads, batch), block(64 * NW);
   switch (group) {
-    case 1: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 1, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
-    case 2: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 2, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
-    case 4: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 4, 4, MODE>), grid, dim3(256), 0, st, a, t); break;
+    case 1: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 1, NW, MODE>), grid, block, 0, st, a, t); break;
+    case 2: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 2, NW, MODE>), grid, block, 0, st, a, t); break;
+    case 4: hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 4, NW, MODE>), grid, block, 0, st, a, t); break;
     case 8:
       if constexpr (D <= 128) {
-        hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 8, 4, MODE>), grid, dim3(256), 0, st, a, t);
+        hipLaunchKernelGGL((tq_attend_kernel<D, BITS, 8, NW, MODE>), grid, block, 0, st, a, t);
         break;
       }
       return hipErrorInvalidValue;
