@@ -941,6 +941,10 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
         wave_encode_query<D, BITS>(a, t, qx[h], qsg, lane, sres[wave], sqc[g], sqf[g], sqs[g]);
     }
   }
+  // tiles past each wave's first are handed out from this counter, one
+  // index at a time
+  __shared__ int sm_next;
+  if (threadIdx.x == 0) sm_next = 0;
   __syncthreads();
   if (fused_store && first < r1 && first + 64 >= L)
     tq_load_tile<D, BITS, MODE>(a, rbase, vbase, first, r1, lane, tb[0]);
@@ -1080,17 +1084,41 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
     __builtin_amdgcn_wave_barrier();
     }  // MODE != 1
   };
-  // The next tile's loads are issued unconditionally: past the split's end
-  // they re-read the current tile (cache hits), so no branch separates a
-  // load from its use.
-  for (int tile0 = first; tile0 < r1; tile0 += 128 * NW) {
-    const int t1 = tile0 + 64 * NW;
-    tq_load_tile<D, BITS, MODE>(a, rbase, vbase, t1 < r1 ? t1 : tile0, r1, lane, tb[1]);
-    process(tb[0], tile0);
-    if (t1 >= r1) break;
-    const int t2 = t1 + 64 * NW;
-    tq_load_tile<D, BITS, MODE>(a, rbase, vbase, t2 < r1 ? t2 : t1, r1, lane, tb[0]);
-    process(tb[1], t1);
+  // Wave w's first tile is tile w of the split; the rest are taken from the
+  // workgroup's counter, each index asked for one tile ahead, so the waves
+  // of a workgroup finish together however their loads are served (with a
+  // fixed share, the last wave of a workgroup ended ~6 us after the first).
+  // The next tile's loads are issued before the current tile is computed;
+  // only the loop's exits branch around a load.
+  const int ntile = (r1 - r0 + 63) / 64;
+  auto grab_issue = [&]() {  // lane 0 holds the counter's old value
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&sm_next, 1);
+    return v;
+  };
+  auto grab_value = [&](int v) { return NW + __builtin_amdgcn_readfirstlane(v); };
+  if (wave < ntile) {
+    int cur = wave;
+    int gq = grab_issue();
+    for (;;) {
+      const int n1 = grab_value(gq);
+      if (n1 >= ntile) {
+        process(tb[0], r0 + 64 * cur);
+        break;
+      }
+      gq = grab_issue();
+      tq_load_tile<D, BITS, MODE>(a, rbase, vbase, r0 + 64 * n1, r1, lane, tb[1]);
+      process(tb[0], r0 + 64 * cur);
+      const int n2 = grab_value(gq);
+      if (n2 >= ntile) {
+        process(tb[1], r0 + 64 * n1);
+        break;
+      }
+      gq = grab_issue();
+      tq_load_tile<D, BITS, MODE>(a, rbase, vbase, r0 + 64 * n2, r1, lane, tb[0]);
+      process(tb[1], r0 + 64 * n1);
+      cur = n2;
+    }
   }
   if constexpr (MODE == 1) return;
   // merge the waves through LDS
