@@ -601,6 +601,12 @@ __global__ __launch_bounds__(64 * NW, D > 128 ? 1 : 8 / NW) void gqa_decode_int4
     }
     if (nsplit == 1) {
       p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+    } else if (p.merge_in_kernel) {
+      store_partial(part + hd * (D + 2) + 2 + d, O);
+      if (d == 0) {
+        store_partial(part + hd * (D + 2), M);
+        store_partial(part + hd * (D + 2) + 1, Ls);
+      }
     } else {
       part[hd * (D + 2) + 2 + d] = O;
       if (d == 0) {
@@ -609,10 +615,43 @@ __global__ __launch_bounds__(64 * NW, D > 128 ? 1 : 8 / NW) void gqa_decode_int4
       }
     }
   }
-  if (split == 0 && threadIdx.x == 0 && kvh == 0) {
-    p.seq_info[2 * b] = split_base;
-    p.seq_info[2 * b + 1] = nsplit;
+  if (!p.merge_in_kernel) {
+    // every sequence records its split range, single-split ones included, so
+    // the combine kernel never reads a previous launch's entry
+    if (split == 0 && threadIdx.x == 0 && kvh == 0) {
+      p.seq_info[2 * b] = split_base;
+      p.seq_info[2 * b + 1] = nsplit;
+    }
+    return;
   }
+  if (nsplit == 1) return;
+
+  // ---- in-kernel merge, as in the int8 kernel: the partial stores are
+  // agent-scope and complete (each wave waits for its own, then the barrier)
+  // before thread 0 takes a ticket of (b, kvh); the workgroup with the last
+  // ticket loads every split's partial in split order and writes the output
+  __shared__ int sm_last;
+  partials_complete();
+  __syncthreads();
+  int* counter = &p.counters[b * p.kv_heads + kvh];
+  if (threadIdx.x == 0) sm_last = last_ticket(counter, nsplit);
+  __syncthreads();
+  if (!sm_last) return;
+  const size_t stride = (size_t)p.kv_heads * (G * (D + 2));
+  const float* p0 = p.partials + ((size_t)split_base * p.kv_heads + kvh) * (G * (D + 2));
+  for (int t = threadIdx.x; t < G * D; t += 64 * NW) {
+    const int hd = t / D, d = t % D;
+    float M = -INFINITY, Ls = 0.0f, O = 0.0f;
+    const float* ph = p0 + hd * (D + 2);
+    if (nsplit <= 2)
+      merge_partials<2>(ph, stride, d, nsplit, -1, M, Ls, O);
+    else if (nsplit <= 4)
+      merge_partials<4>(ph, stride, d, nsplit, -1, M, Ls, O);
+    else
+      merge_partials<8>(ph, stride, d, nsplit, -1, M, Ls, O);
+    p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+  }
+  if (threadIdx.x == 0) reset_ticket(counter);
 }
 
 template <int D, int G>
@@ -629,7 +668,7 @@ hipError_t launch_g(const DecodeParams& p, int work_items, bool combine, hipStre
     hipLaunchKernelGGL((gqa_decode_int4_kernel<D, G, 4>), dim3(work_items, p.kv_heads), dim3(256),
                        0, st, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || !combine) return e;
+  if (e != hipSuccess || !combine || p.merge_in_kernel) return e;
   return launch_decode_combine(p, D, G, st);
 }
 

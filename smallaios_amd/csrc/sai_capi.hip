@@ -847,10 +847,9 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   p.seq_info = ws->seq_info;
   // automatic: the last workgroup merges when every sequence has the same
   // split count (one ticket per (sequence, kv head), measured faster at 16 x
-  // 8k); ragged batches use the combine kernel (measured faster there). The
-  // int4 kernel always uses the combine kernel.
-  p.merge_in_kernel = c->desc.quant == SAI_KV_INT8 &&
-                      (ctx->decode_merge == 1 || (ctx->decode_merge == 2 && uniform));
+  // 8k, int8, and at 4 x 32k, int4); ragged batches use the combine kernel
+  // (measured faster there).
+  p.merge_in_kernel = ctx->decode_merge == 1 || (ctx->decode_merge == 2 && uniform);
   p.counters = ws->counters;
   p.k_new = k_new;
   p.v_new = v_new;
