@@ -418,7 +418,9 @@ hipError_t launch_kv_append(const AppendParams& p, int head_dim, int quant, hipS
   // 16-byte aligned; its grid is (kv_heads, pages, batch) and its in-sequence
   // row offsets are 32-bit
   const bool aligned = (((uintptr_t)p.k | (uintptr_t)p.v) & 15u) == 0;
-  const int pages = (p.s_new + kPageTokens - 1) / kPageTokens + 1;  // any start
+  // the host's exact count when given, else one more than s_new spans (any
+  // start)
+  const int pages = p.pages > 0 ? p.pages : (p.s_new + kPageTokens - 1) / kPageTokens + 1;
   const bool fits = pages <= 65535 && p.batch <= 65535 &&
                     (long)p.s_new * p.kv_heads * head_dim * 4 < (1L << 31);
   if (quant == kQuantInt8 && p.s_new >= kPageAppendMin && aligned && fits) {

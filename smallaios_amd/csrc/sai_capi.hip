@@ -702,6 +702,13 @@ SAI_API sai_status sai_kv_append(sai_ctx* ctx, sai_kvcache* c, int32_t layer, co
   p.max_pages = c->desc.max_pages_per_seq;
   p.pool = c->pools[layer];
   p.num_pages = c->desc.num_pages;
+  // pages the new rows span, from the committed lengths (h_seq_lens mirrors
+  // the device's)
+  int32_t pages = 0;
+  for (int b = 0; b < batch; ++b)
+    pages = std::max(pages, (c->h_seq_lens[b] % SAI_PAGE_TOKENS + s_new + SAI_PAGE_TOKENS - 1) /
+                                SAI_PAGE_TOKENS);
+  p.pages = pages;
   hipError_t e = sai::launch_kv_append(p, c->desc.head_dim, c->desc.quant, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "kv_append launch");
   c->pending = s_new;

@@ -102,6 +102,9 @@ struct AppendParams {
   int max_pages;
   uint8_t* pool;
   int num_pages;
+  // pages the new tokens touch in the sequence that touches most (the page
+  // kernel's grid); 0: s_new / 16 + 1, which covers any start
+  int pages;
 };
 
 struct DecodeParams {
