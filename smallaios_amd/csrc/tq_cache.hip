@@ -917,18 +917,21 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
   __shared__ _Float16 sp[NW][NQ * 4][64 + 4];    // a wave's P' rows
   if constexpr (MODE == 0) {
     // fused step: the last split's workgroup stores the pass's one new row
-    // of this kv head (K by wave 0, V by wave 1) before any wave reads it
-    if (t.k_new != nullptr && r1 == L && wave < 2) {
+    // of this kv head (K by wave NW - 2, V by wave NW - 1: with 8 waves and
+    // up to 4 query heads, waves that encode no query head) before any wave
+    // reads it
+    if (t.k_new != nullptr && r1 == L && wave >= NW - 2) {
       __shared__ uint32_t scode[D];
       float x[D / 64], sgn[D / 64];
-      const void* src = wave ? t.v_new : t.k_new;
+      const int kind = wave - (NW - 2);  // 0: K, 1: V
+      const void* src = kind ? t.v_new : t.k_new;
       const size_t in_off = ((size_t)b * a.heads + kvh) * D;
 #pragma unroll
       for (int e = 0; e < D / 64; ++e) {
         sgn[e] = (float)a.signs[(size_t)kvh * D + lane + 64 * e];
         x[e] = load_row_elem(src, in_off + lane + 64 * e, t.kv_bf16 != 0);
       }
-      wave_store_row<D, BITS>(a, x, sgn, lane, kvh, b, L - 1, wave, nullptr, sres[wave], scode);
+      wave_store_row<D, BITS>(a, x, sgn, lane, kvh, b, L - 1, kind, nullptr, sres[wave], scode);
       __threadfence_block();
     }
   }
