@@ -900,14 +900,41 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
                                  t.q_bf16 != 0);
     }
   }
+  // Tiles of the split: wave w starts with tile w, the rest come from a
+  // workgroup counter. In a fused step the last split's workgroup stores the
+  // pass's new row, which lies in its last tile T. One wave (T's holder, else
+  // the last wave, whose own first tile then goes to the counter) stores the
+  // row's K and V after the prologue barrier, while the other waves already
+  // stream, and then computes T first; no other wave touches T. Stored in the
+  // prologue instead, the row held the whole workgroup at the barrier, and
+  // that split's loop ended 2-3 us after the others.
+  const int ntile = (r1 - r0 + 63) / 64;
+  const int T = ntile - 1;
+  const bool fused_store = MODE == 0 && t.k_new != nullptr && r1 == L;
+  const int store_wave = T < NW ? T : NW - 1;
+  const bool storer = fused_store && wave == store_wave;
+  const bool t_pooled = fused_store && T >= NW;  // tile NW - 1 goes to the counter
+  const int first_tile = storer ? T : wave;
+  // the new row's K and V elements, loaded by every wave with the query's
+  // (branch-free; without a fused row they read the query, unused)
+  float xnk[D / 64], xnv[D / 64];
+  if constexpr (MODE == 0) {
+    const bool have = t.k_new != nullptr;
+    const void* kn = have ? t.k_new : t.q;
+    const void* vn = have ? t.v_new : t.q;
+    const bool bf = have ? t.kv_bf16 != 0 : t.q_bf16 != 0;
+    const size_t in_off = ((size_t)b * a.heads + kvh) * D;
+#pragma unroll
+    for (int e = 0; e < D / 64; ++e) {
+      xnk[e] = load_row_elem(kn, in_off + lane + 64 * e, bf);
+      xnv[e] = load_row_elem(vn, in_off + lane + 64 * e, bf);
+    }
+  }
   // Two tile buffers: a wave loads its next tile before it computes the
   // current one. The first tile's loads follow the query's, before the
-  // prologue (the query's wait then counts them as later loads). In the
-  // workgroup that stores the pass's new row, the wave whose first tile holds
-  // that row loads it again after the store.
+  // prologue (the query's wait then counts them as later loads).
   TqTile<D, BITS, MODE> tb[2];
-  const bool fused_store = MODE == 0 && t.k_new != nullptr && r1 == L;
-  const int first = r0 + wave * 64;
+  const int first = r0 + first_tile * 64;
   tq_load_tile<D, BITS, MODE>(a, rbase, vbase, first < r1 ? first : r0, r1, lane, tb[0]);
 
   __shared__ uint32_t sqc[NQ * 4][NS];           // query code words (padding heads 0)
@@ -915,26 +942,6 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
   __shared__ uint32_t sqs[G][D / 32];            // query QJL sign words
   __shared__ float sres[NW][D];
   __shared__ _Float16 sp[NW][NQ * 4][64 + 4];    // a wave's P' rows
-  if constexpr (MODE == 0) {
-    // fused step: the last split's workgroup stores the pass's one new row
-    // of this kv head (K by wave NW - 2, V by wave NW - 1: with 8 waves and
-    // up to 4 query heads, waves that encode no query head) before any wave
-    // reads it
-    if (t.k_new != nullptr && r1 == L && wave >= NW - 2) {
-      __shared__ uint32_t scode[D];
-      float x[D / 64], sgn[D / 64];
-      const int kind = wave - (NW - 2);  // 0: K, 1: V
-      const void* src = kind ? t.v_new : t.k_new;
-      const size_t in_off = ((size_t)b * a.heads + kvh) * D;
-#pragma unroll
-      for (int e = 0; e < D / 64; ++e) {
-        sgn[e] = (float)a.signs[(size_t)kvh * D + lane + 64 * e];
-        x[e] = load_row_elem(src, in_off + lane + 64 * e, t.kv_bf16 != 0);
-      }
-      wave_store_row<D, BITS>(a, x, sgn, lane, kvh, b, L - 1, kind, nullptr, sres[wave], scode);
-      __threadfence_block();
-    }
-  }
   if constexpr (MODE != 2) {
     for (int e = threadIdx.x; e < (NQ * 4 - G) * NS; e += 64 * NW) sqc[G + e / NS][e % NS] = 0u;
 #pragma unroll
@@ -949,8 +956,18 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
   __shared__ int sm_next;
   if (threadIdx.x == 0) sm_next = 0;
   __syncthreads();
-  if (fused_store && first < r1 && first + 64 >= L)
-    tq_load_tile<D, BITS, MODE>(a, rbase, vbase, first, r1, lane, tb[0]);
+  if constexpr (MODE == 0) {
+    if (storer) {
+      __shared__ uint32_t scode[D];
+      float sgn[D / 64];
+#pragma unroll
+      for (int e = 0; e < D / 64; ++e) sgn[e] = (float)a.signs[(size_t)kvh * D + lane + 64 * e];
+      wave_store_row<D, BITS>(a, xnk, sgn, lane, kvh, b, L - 1, 0, nullptr, sres[wave], scode);
+      wave_store_row<D, BITS>(a, xnv, sgn, lane, kvh, b, L - 1, 1, nullptr, sres[wave], scode);
+      __threadfence_block();
+      tq_load_tile<D, BITS, MODE>(a, rbase, vbase, first, r1, lane, tb[0]);
+    }
+  }
   // the query's coefficients and sign words are uniform: scalar registers
   float qa[G], qb[G], qg[G], qk[G];
   uint32_t qs[G][D / 32];
@@ -1093,19 +1110,24 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
   // fixed share, the last wave of a workgroup ended ~6 us after the first).
   // The next tile's loads are issued before the current tile is computed;
   // only the loop's exits branch around a load.
-  const int ntile = (r1 - r0 + 63) / 64;
   auto grab_issue = [&]() {  // lane 0 holds the counter's old value
     int v = 0;
     if (lane == 0) v = atomicAdd(&sm_next, 1);
     return v;
   };
-  auto grab_value = [&](int v) { return NW + __builtin_amdgcn_readfirstlane(v); };
-  if (wave < ntile) {
-    int cur = wave;
+  // counter value c: tile NW + c, or with T kept out, NW - 1 first, then
+  // NW + c - 1 (T itself is never handed out: the values stop at T)
+  auto grab_value = [&](int v) {
+    const int c = __builtin_amdgcn_readfirstlane(v);
+    return t_pooled ? (c == 0 ? NW - 1 : NW + c - 1) : NW + c;
+  };
+  const int pool_end = t_pooled ? T : ntile;  // grab values from here on stop
+  if (first_tile < ntile) {
+    int cur = first_tile;
     int gq = grab_issue();
     for (;;) {
       const int n1 = grab_value(gq);
-      if (n1 >= ntile) {
+      if (n1 >= pool_end) {
         process(tb[0], r0 + 64 * cur);
         break;
       }
@@ -1113,7 +1135,7 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
       tq_load_tile<D, BITS, MODE>(a, rbase, vbase, r0 + 64 * n1, r1, lane, tb[1]);
       process(tb[0], r0 + 64 * cur);
       const int n2 = grab_value(gq);
-      if (n2 >= ntile) {
+      if (n2 >= pool_end) {
         process(tb[1], r0 + 64 * n1);
         break;
       }
