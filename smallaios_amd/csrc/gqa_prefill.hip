@@ -72,12 +72,28 @@ __device__ __forceinline__ float xgroup_sum(float v) {
   auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
+// max over the whole wave: within each row of 16 lanes on DPP moves (quad
+// swaps, then rotations by 4 and 8), then across the four rows
+__device__ __forceinline__ float wave_max(float v) {
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value,
+                                                      0xF, 0xF, false));
+  };
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm 1,0,3,2
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm 2,3,0,1
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x124>{}));  // row_ror:4
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x128>{}));  // row_ror:8
+  return xgroup_max(v);
+}
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // How far (log2 units) a row's scores may rise above its reference point
 // before the reference moves: softmax weights stay <= 2^kMaxLead = 4, so
 // p * s_v stays inside binary16 for V rows up to |v| ~ 2e6.
 constexpr float kMaxLead = 2.0f;
+// Fast-path bounds: p * s_v <= kFastSum (inside binary16), row sums <= kFastCap
+constexpr float kFastSum = 32768.0f;
+constexpr float kFastCap = 1048576.0f;
 
 // V fragments read ahead of the PV MFMAs that consume them
 constexpr int kVPrefetch = 6;
@@ -93,6 +109,7 @@ struct PrefillTile {
   alignas(16) _Float16 v[2 * D * VROW];
   alignas(16) float sk[64];
   alignas(16) float sv[64];
+  float svmax;  // largest V scale of the tile (int8)
 };
 
 // Codes and scales of one 64-token tile, held in registers between the load
@@ -217,6 +234,11 @@ __device__ __forceinline__ void stage_store(const TileStage<D, NT>& S, Tile& T, 
       T.sk[tid] = sc;
     else
       T.sv[tid - 64] = sc;
+    // the second wave holds the 64 V scales: their maximum bounds p * s_v
+    if (__builtin_amdgcn_readfirstlane(tid >> 6) == 1) {
+      const float m = wave_max(sc);
+      if (tid == 64) T.svmax = m;
+    }
   }
 }
 
@@ -494,10 +516,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 
     // S^T for both row blocks: 4 column blocks of 16 tokens; k steps outer so
     // that eight independent accumulation chains interleave on the MFMA pipe.
-    // s holds each score relative to its row's running maximum:
-    // s = <q', k> * s_k - m_run
-    float s[RB][4][4];
-    {
+    // s holds each score relative to its row's reference point:
+    // s = <q', k> * s_k - m_run (masked keys: -inf)
+    auto scores = [&](float (&s)[RB][4][4]) __attribute__((always_inline)) {
       v4f c[4][RB];
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb)
@@ -554,64 +575,107 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
             s[rb][cb][e] = INT4 ? c[cb][rb][e] - m_run[rb]
                                 : __builtin_fmaf(c[cb][rb][e], skx[e], -m_run[rb]);
       }
-    }
-    if (tile >= full_tiles || tile < lo_full) {
+      if (tile >= full_tiles || tile < lo_full) {
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int t = t0 + 16 * cb + 4 * g + e;
+              const bool vis = t <= qpos[rb] && (W <= 0 || t > qpos[rb] - W);
+              s[rb][cb][e] = vis ? s[rb][cb][e] : -INFINITY;
+            }
+      }
+    };
+    // s -> p = exp2(s) in place; rsum = the row's sum over the tile
+    auto weights = [&](float (&s)[RB][4][4], float (&rsum)[RB]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        float psum = 0.0f;
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int t = t0 + 16 * cb + 4 * g + e;
-            const bool vis = t <= qpos[rb] && (W <= 0 || t > qpos[rb] - W);
-            s[rb][cb][e] = vis ? s[rb][cb][e] : -INFINITY;
+            s[rb][cb][e] = fast_exp2(s[rb][cb][e]);
+            psum += s[rb][cb][e];
           }
-    }
+        rsum[rb] = xgroup_sum(psum);
+      }
+    };
 
-    // The running maximum only moves when a row's tile maximum exceeds it by
-    // more than kMaxLead (or on the row's first visible keys), so p = exp2(s)
-    // stays <= 2^kMaxLead and most tiles skip the accumulator rescale.
-    // Any reference point gives the same softmax; it only has to keep p and
-    // the sums in range.
-    float lead[RB];
-    bool move = false;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      float mt = -INFINITY;
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[rb][cb][e]);
-      mt = xgroup_max(mt);
-      const bool row_moves = mt > kMaxLead || (l_run[rb] == 0.0f && mt != -INFINITY);
-      lead[rb] = row_moves ? mt : 0.0f;
-      move = move || row_moves;
-    }
-    if (__builtin_amdgcn_ballot_w64(move) != 0) {
+    // The reference point moves when a row's tile maximum exceeds it by more
+    // than kMaxLead (or on the row's first visible keys), so p = exp2(s) stays
+    // <= 2^kMaxLead. Any reference point gives the same softmax; it only has
+    // to keep p and the sums in range.
+    float s[RB][4][4];
+    float rsum[RB];
+    auto settle = [&]() __attribute__((always_inline)) {
+      scores(s);
+      float lead[RB];
+      bool move = false;
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        m_run[rb] += lead[rb];
-        const float alpha = fast_exp2(-lead[rb]);  // 1 for rows that keep their max
-        l_run[rb] *= alpha;
+        float mt = -INFINITY;
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s[rb][cb][e] -= lead[rb];
-        // accumulator rows 4g+e: the alpha of row j lives in lane j
-        float ae[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ae[e] = __shfl(alpha, 4 * g + e, 64);
-#pragma unroll
-        for (int jb = 0; jb < JB; ++jb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[rb][jb][e] *= ae[e];
+          for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[rb][cb][e]);
+        mt = xgroup_max(mt);
+        const bool row_moves = mt > kMaxLead || (l_run[rb] == 0.0f && mt != -INFINITY);
+        lead[rb] = row_moves ? mt : 0.0f;
+        move = move || row_moves;
       }
+      if (__builtin_amdgcn_ballot_w64(move) != 0) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          m_run[rb] += lead[rb];
+          const float alpha = fast_exp2(-lead[rb]);  // 1 for rows that keep their max
+          l_run[rb] *= alpha;
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[rb][cb][e] -= lead[rb];
+          // accumulator rows 4g+e: the alpha of row j lives in lane j
+          float ae[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ae[e] = __shfl(alpha, 4 * g + e, 64);
+#pragma unroll
+          for (int jb = 0; jb < JB; ++jb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[rb][jb][e] *= ae[e];
+        }
+      }
+      weights(s, rsum);
+    };
+    if constexpr (INT4) {
+      settle();
+    } else {
+      // Fast path (int8): the weights against the current reference point are
+      // kept when they provably fit: a row sum <= kFastSum / max(s_v) bounds
+      // every p * s_v (the PV operand, binary16) by kFastSum, the cap bounds
+      // the running sums, and a row that has seen no keys yet needs a sum >= 1
+      // (its largest weight is then >= 1/64, so the reference is not far above
+      // its scores). Otherwise (a row's first keys, scores that rose far above
+      // the reference, inf or NaN) the tile is settled as above, its scores
+      // recomputed from the tile still in LDS.
+      scores(s);
+      weights(s, rsum);
+      const float svm = T.svmax;
+      bool bad = false;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const bool ok = rsum[rb] <= kFastCap && rsum[rb] * svm <= kFastSum &&
+                        (l_run[rb] > 0.0f || rsum[rb] >= 1.0f);
+        bad = bad || !ok;
+      }
+      if (__builtin_amdgcn_ballot_w64(bad) != 0) settle();
     }
 
     v8h pa[RB][2];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      float psum = 0.0f;
+      l_run[rb] += rsum[rb];
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
         float svx[4] = {1.0f, 1.0f, 1.0f, 1.0f};
@@ -620,13 +684,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
           svx[0] = svv.x, svx[1] = svv.y, svx[2] = svv.z, svx[3] = svv.w;
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float pe = fast_exp2(s[rb][cb][e]);
-          psum += pe;
-          pa[rb][cb >> 1][(cb & 1) * 4 + e] = (_Float16)(INT4 ? pe : pe * svx[e]);
-        }
+        for (int e = 0; e < 4; ++e)
+          pa[rb][cb >> 1][(cb & 1) * 4 + e] =
+              (_Float16)(INT4 ? s[rb][cb][e] : s[rb][cb][e] * svx[e]);
       }
-      l_run[rb] += xgroup_sum(psum);
     }
     // PV over the 2 x JB V fragments, kVPrefetch of them in flight ahead of
     // the MFMAs that consume them (the scheduler fence keeps each read ahead
