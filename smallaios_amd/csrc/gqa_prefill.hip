@@ -157,27 +157,37 @@ struct StagePages {
   }
 };
 
+// A kv head's page blocks are contiguous in the pool (block_offset), so a
+// block's address is the head's base plus page * block bytes: one 32 x 32 ->
+// 64-bit multiply-add (page ids are non-negative). Tiles start at multiples of
+// 64 tokens, so a tile token's slot in its page is token & 15.
+__device__ __forceinline__ const uint8_t* head_blocks(const PrefillParams& p, int kvh, size_t bb) {
+  return p.pool + block_offset(0, kvh, p.num_pages, bb);
+}
+__device__ __forceinline__ const uint8_t* page_block(const uint8_t* head, int page, size_t bb) {
+  return head + (uint64_t)(uint32_t)page * bb;
+}
+
 template <int D, int NT>
 __device__ __forceinline__ void stage_load(TileStage<D, NT>& S, const PrefillParams& p,
                                            const StagePages<D, NT, false>& P, int kvh, int t0,
                                            int tid) {
   constexpr size_t BB = block_bytes_int8(D);
+  const uint8_t* head = head_blocks(p, kvh, BB);
 #pragma unroll
   for (int i = 0; i < TileStage<D, NT>::KC; ++i) {
     const int c = tid + NT * i;
     if (TileStage<D, NT>::KN % NT != 0 && c >= TileStage<D, NT>::KN) break;
     const int tok = c / (D / 16);
     const int dp = c % (D / 16);
-    const uint8_t* blk = p.pool + block_offset(P.k[i], kvh, p.num_pages, BB);
-    S.kc[i] = *(const uint4*)(blk + (size_t)((t0 + tok) % kPageTokens) * D + 16 * dp);
+    S.kc[i] = *(const uint4*)(page_block(head, P.k[i], BB) + (tok & 15) * D + 16 * dp);
   }
 #pragma unroll
   for (int i = 0; i < TileStage<D, NT>::VC; ++i) {
     const int c = tid + NT * i;
     if (TileStage<D, NT>::VN % NT != 0 && c >= TileStage<D, NT>::VN) break;
     const int d = c % D;
-    const uint8_t* blk = p.pool + block_offset(P.v[i], kvh, p.num_pages, BB);
-    S.vc[i] = *(const uint4*)(blk + 16 * D + (size_t)d * 16);
+    S.vc[i] = *(const uint4*)(page_block(head, P.v[i], BB) + 16 * D + d * 16);
   }
   // the first 128 threads load one scale each; tokens past the sequence end
   // are zeroed when the tile is stored (a select here would wait for the load)
@@ -185,8 +195,7 @@ __device__ __forceinline__ void stage_load(TileStage<D, NT>& S, const PrefillPar
   if (tid < 128) {
     const int which = tid >> 6;
     const int tok = tid & 63;
-    const uint8_t* blk = p.pool + block_offset(P.s, kvh, p.num_pages, BB);
-    S.sc = ((const float*)(blk + 32 * D + 64 * which))[(t0 + tok) % kPageTokens];
+    S.sc = ((const float*)(page_block(head, P.s, BB) + 32 * D + 64 * which))[tok & 15];
   }
 }
 
@@ -276,23 +285,24 @@ __device__ __forceinline__ void stage_load4(TileStage4<D, NT>& S, const PrefillP
   constexpr int NG = D / 32;
   static_assert(StagePages<D, NT, true>::KC == TileStage4<D, NT>::KC &&
                 StagePages<D, NT, true>::VC == TileStage4<D, NT>::VC, "chunk counts");
+  const uint8_t* head = head_blocks(p, kvh, BB);
 #pragma unroll
   for (int i = 0; i < TileStage4<D, NT>::KC; ++i) {
     const int c = min(tid + NT * i, TileStage4<D, NT>::KN - 1);  // spare threads repeat the last
     const int tok = c / NG;
     const int grp = c % NG;
-    const uint8_t* blk = p.pool + block_offset(P.k[i], kvh, p.num_pages, BB);
-    const int slot = (t0 + tok) % kPageTokens;
-    S.kc[i] = *(const uint4*)(blk + (size_t)slot * (D / 2) + 16 * grp);
-    S.kp[i] = *(const uint32_t*)(blk + 16 * D + (size_t)(slot * NG + grp) * 4);
+    const uint8_t* blk = page_block(head, P.k[i], BB);
+    const int slot = tok & 15;
+    S.kc[i] = *(const uint4*)(blk + slot * (D / 2) + 16 * grp);
+    S.kp[i] = *(const uint32_t*)(blk + 16 * D + (slot * NG + grp) * 4);
   }
 #pragma unroll
   for (int i = 0; i < TileStage4<D, NT>::VC; ++i) {
     const int c = min(tid + NT * i, TileStage4<D, NT>::VN - 1);
     const int d = c % D;
-    const uint8_t* blk = p.pool + block_offset(P.v[i], kvh, p.num_pages, BB);
-    S.vc[i] = *(const uint2*)(blk + 8 * D + (size_t)d * 8);
-    const uint8_t* par = blk + 16 * D + 64 * NG + (size_t)(d / 32) * 4;
+    const uint8_t* blk = page_block(head, P.v[i], BB);
+    S.vc[i] = *(const uint2*)(blk + 8 * D + d * 8);
+    const uint8_t* par = blk + 16 * D + 64 * NG + (d / 32) * 4;
 #pragma unroll
     for (int sl = 0; sl < 16; ++sl) S.vp[i][sl] = *(const uint32_t*)(par + (size_t)sl * NG * 4);
   }
