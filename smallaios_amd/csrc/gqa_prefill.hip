@@ -108,10 +108,7 @@ struct PrefillTile {
   alignas(16) _Float16 klo[KLO ? 64 * KROW : 8];  // int4: K - f16(K), hi + lo hold K to ~22 bits
   alignas(16) _Float16 v[2 * D * VROW];
   alignas(16) float sk[64];
-  // int8 V scales as binary16, in the order of the PV A operand: token
-  // 16 cb + 4 g + e at [g][cb >> 1][(cb & 1) * 4 + e], so lane group g reads
-  // its 16 with two 16-byte loads
-  alignas(16) _Float16 svh[64];
+  alignas(16) float sv[64];
   float svmax;  // largest V scale of the tile (int8)
 };
 
@@ -242,12 +239,10 @@ __device__ __forceinline__ void stage_store(const TileStage<D, NT>& S, Tile& T, 
   }
   if (tid < 128) {
     const float sc = t0 + (tid & 63) < total ? S.sc : 0.0f;
-    if (tid < 64) {
+    if (tid < 64)
       T.sk[tid] = sc;
-    } else {
-      const int tk = tid - 64, cb = tk >> 4;
-      T.svh[((tk >> 2) & 3) * 16 + (cb >> 1) * 8 + (cb & 1) * 4 + (tk & 3)] = (_Float16)sc;
-    }
+    else
+      T.sv[tid - 64] = sc;
     // the second wave holds the 64 V scales: their maximum bounds p * s_v
     if (__builtin_amdgcn_readfirstlane(tid >> 6) == 1) {
       const float m = wave_max(sc);
@@ -603,25 +598,18 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
             }
       }
     };
-    // p = exp2(s) as binary16 into the PV A operand (token 16 cb + 4 g + e at
-    // pa[rb][cb >> 1][(cb & 1) * 4 + e]); rsum = the row's sum of the rounded
-    // weights, as PV uses them, two per dot product
-    v8h pa[RB][2];
-    auto weights = [&](const float (&s)[RB][4][4], float (&rsum)[RB]) __attribute__((always_inline)) {
+    // s -> p = exp2(s) in place; rsum = the row's sum over the tile
+    auto weights = [&](float (&s)[RB][4][4], float (&rsum)[RB]) __attribute__((always_inline)) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
+        float psum = 0.0f;
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            pa[rb][cb >> 1][(cb & 1) * 4 + e] = (_Float16)fast_exp2(s[rb][cb][e]);
-        float psum = 0.0f;
-#pragma unroll
-        for (int kst = 0; kst < 2; ++kst)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            psum = __builtin_amdgcn_fdot2(v2h{pa[rb][kst][2 * i], pa[rb][kst][2 * i + 1]},
-                                          v2h{(_Float16)1.0f, (_Float16)1.0f}, psum, false);
+          for (int e = 0; e < 4; ++e) {
+            s[rb][cb][e] = fast_exp2(s[rb][cb][e]);
+            psum += s[rb][cb][e];
+          }
         rsum[rb] = xgroup_sum(psum);
       }
     };
@@ -675,9 +663,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
     } else {
       // Fast path (int8): the weights against the current reference point are
       // kept when they provably fit: a row sum <= kFastSum / max(s_v) bounds
-      // every p * s_v (the PV operand, binary16) by kFastSum (a weight beyond
-      // binary16 makes the sum inf), the cap bounds the running sums, and a
-      // row that has seen no keys yet needs a sum >= 1
+      // every p * s_v (the PV operand, binary16) by kFastSum, the cap bounds
+      // the running sums, and a row that has seen no keys yet needs a sum >= 1
       // (its largest weight is then >= 1/64, so the reference is not far above
       // its scores). Otherwise (a row's first keys, scores that rose far above
       // the reference, inf or NaN) the tile is settled as above, its scores
@@ -695,18 +682,23 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       if (__builtin_amdgcn_ballot_w64(bad) != 0) settle();
     }
 
-    // int8: A = p * s_v (binary16 products; the V tile holds the codes)
-    if constexpr (!INT4) {
-      const v8h sv0 = *(const v8h*)(T.svh + 16 * g);
-      const v8h sv1 = *(const v8h*)(T.svh + 16 * g + 8);
+    v8h pa[RB][2];
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        pa[rb][0] *= sv0;
-        pa[rb][1] *= sv1;
+    for (int rb = 0; rb < RB; ++rb) {
+      l_run[rb] += rsum[rb];
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        float svx[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (!INT4) {
+          const float4 svv = *(const float4*)(T.sv + 16 * cb + 4 * g);
+          svx[0] = svv.x, svx[1] = svv.y, svx[2] = svv.z, svx[3] = svv.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          pa[rb][cb >> 1][(cb & 1) * 4 + e] =
+              (_Float16)(INT4 ? s[rb][cb][e] : s[rb][cb][e] * svx[e]);
       }
     }
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) l_run[rb] += rsum[rb];
     // PV over the 2 x JB V fragments, kVPrefetch of them in flight ahead of
     // the MFMAs that consume them (the scheduler fence keeps each read ahead
     // of its consumer by that many MFMA pairs, so the LDS latency is covered)

@@ -54,7 +54,7 @@ class Case:
     def __init__(self, rt, seed, batch, hq, hkv, d, past_lens, new_tokens, theta=10000.0,
                  quant=S.KV_INT8, kv_dtype="f32", permute_pages=False, do_rotary=True,
                  interleaved=False, k_transform=None, extra_pages=3, max_pages_per_seq=None,
-                 extra_tokens=0):
+                 extra_tokens=0, v_transform=None):
         self.rng = np.random.default_rng(seed)
         self.rt = rt
         self.batch, self.hq, self.hkv, self.d = batch, hq, hkv, d
@@ -64,6 +64,7 @@ class Case:
         self.kv_dtype = kv_dtype
         self.do_rotary, self.interleaved = do_rotary, interleaved
         self.k_transform = k_transform
+        self.v_transform = v_transform
         total = int(self.past_lens.max()) + new_tokens + extra_tokens
         self.t_cap = total
         self.max_pages = max_pages_per_seq or (total + S.PAGE_TOKENS - 1) // S.PAGE_TOKENS
@@ -92,6 +93,8 @@ class Case:
         v = self.rng.standard_normal(shape, dtype=np.float32)
         if self.k_transform is not None:
             k = self.k_transform(self.rng, k)
+        if self.v_transform is not None:
+            v = self.v_transform(self.rng, v)
         if self.kv_dtype == "bf16":
             k, v = to_bf16_f32(k), to_bf16_f32(v)
         return k, v

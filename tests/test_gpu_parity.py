@@ -402,6 +402,37 @@ def test_prefill_outlier_keys(rt, quant, hq, hkv, d, past, new, qd):
     log(f"  max abs err {err:.2e}")
 
 
+@pytest.mark.parametrize("vscale", [1.0, 1.0e5])
+def test_prefill_reference_moves(rt, vscale):
+    """int8 prefill whose weights leave the fast path's bounds mid-sequence: keys
+    at past positions 300-339 are scaled x6, so their scores rise tens of log2
+    units above the reference point the first tiles set (their weights would
+    overflow binary16), and with vscale 1e5 the V rows reach |v| ~ 4e5, so the
+    row-sum bound r * max(s_v) <= 32768 fails on ordinary tiles too. Those tiles
+    are settled (scores recomputed, reference moved); codes bit-exact, outputs
+    within tolerance of the oracle in units of the V scale (scaling V by c scales
+    the output by c; the outputs here are averages of +-4e5 values that cancel
+    down to ~1e3, so an absolute 2e-3 would ask binary16 weights for ~1e-8
+    relative accuracy)."""
+    log(f"prefill reference moves: keys x6 at 300-339, V x{vscale:g}")
+
+    def jump(rng, k):
+        if k.shape[1] >= 340:
+            k[:, 300:340] *= 6.0
+        return k
+
+    c = Case(rt, 0x5E77, 2, 16, 4, 128, [700, 450], 130, theta=5e5, permute_pages=True,
+             k_transform=jump, v_transform=lambda rng, v: v * np.float32(vscale))
+    c.step_kv()
+    c.check_codes()
+    q = c.query("f32")
+    got = c.gpu_prefill(q, "f32")
+    ref = c.oracle_attend(q)
+    got, ref = got / np.float32(vscale), ref / np.float32(vscale)
+    log(f"  worst err/tol {err_tol_ratio(got, ref):.4f}")
+    assert_close(got, ref, "prefill, reference moves")
+
+
 # ------------------------------------------------------------- introspection ---
 def test_decode_kernel_timing_ring(rt):
     """sai_set_decode_timing / sai_decode_kernel_times: events around the decode
