@@ -1050,8 +1050,10 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
     // the normaliser take the same rounded weight p' = P' S / vs, so the
     // f16 rounding perturbs each weight instead of splitting the row
     const float vsmax = tq_wave_max(live ? vp.x : 0.0f);
-    const float vsn = vp.x / vsmax;
-    const float rvsn = vsmax / vp.x;
+    // hardware reciprocals (1 ulp) instead of IEEE divisions: the two ratios
+    // only need to be each other's inverse far below the f16 rounding of P'
+    const float vsn = vp.x * __builtin_amdgcn_rcpf(vsmax);
+    const float rvsn = vsmax * __builtin_amdgcn_rcpf(vp.x);
     const int slot = p_slot<BITS>(lane);
 #pragma unroll
     for (int g = 0; g < NQ * 4; ++g) {
