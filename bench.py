@@ -15,7 +15,8 @@ every step (append without advance), so the context stays fixed.
 Other workloads (--workload, for the per-configuration table): `batch1`
 (8Q/2KV, head_dim 64, context 512), `int4long` (4 sequences of 32768 tokens,
 int4 KV with f16 (scale, zero) per group of 32 dims, K Student-t df 3 with
-four x20 outlier channels), `ragged` (64 sequences with seeded lengths
+four x20 outlier channels), `gemma4b` and `gemma4b_int4` (Gemma 3 4B's 8Q/4KV at
+head_dim 256, 16 sequences of 8192 tokens, int8 and int4 KV), `ragged` (64 sequences with seeded lengths
 U[128, 16384], randomly permuted page table), `prefill` (2 x 2048 new
 tokens appended to a 6144-token cache, then causal MFMA attention) and `rope`
 (the standalone RotaryEmbedding op over that chunk's queries: [2, 2048,
@@ -56,6 +57,9 @@ WORKLOADS = {
                      k_dist="outlier_t3"),
     "gemma4b": dict(kind="decode", batch=16, hq=8, hkv=4, d=256, lens=("uniform", 8192),
                     theta=1000000.0, q_dtype="bf16", permute=False),
+    "gemma4b_int4": dict(kind="decode", batch=16, hq=8, hkv=4, d=256, lens=("uniform", 8192),
+                         theta=1000000.0, q_dtype="bf16", permute=False, quant="int4",
+                         k_dist="outlier_t3"),
     "ragged": dict(kind="decode", batch=64, hq=32, hkv=8, d=128, lens=("uniform_rand", 128, 16384),
                    theta=500000.0, q_dtype="bf16", permute=True),
     "prefill": dict(kind="prefill", batch=2, hq=32, hkv=8, d=128, past=6144, new=2048,
