@@ -309,12 +309,33 @@ def test_logits_and_weighted_sum(rt, d, bits, qjl, group):
 def test_write_attend_fused_step(rt, d, bits, qjl, group, bf16):
     """sai_tqcache_write_attend against sai_tqcache_write + sai_tqcache_attend
     on a twin cache: the same outputs bit for bit and the same stored rows,
-    over ragged lengths (one sequence with three splits, the new row in the
+    over ragged lengths (one sequence with several splits, the new row in the
     last), two layers in one pass, two passes."""
+    fused_step_case(rt, d, bits, qjl, group, bf16, [2100, 77], 0)
+
+
+def test_write_attend_fused_step_long_last_split(rt):
+    """As above with a 1024-position split: the last split of the first
+    sequence holds 14 tiles, more than the workgroup's 8 waves, so the wave
+    that stores the new row is the last one, and its own first tile goes to
+    the workgroup's tile counter instead. Tiles past a wave's first are
+    handed out at run time, so which wave sums which tile can differ between
+    any two launches, and each wave rounds its weights to binary16 against
+    its own running maximum: the outputs agree to the weights' rounding
+    (2^-11 relative; atol 1e-4, rtol 1e-3 here), the stored rows bit for
+    bit."""
+    prev = rt.set_tq_split(1024)
+    try:
+        fused_step_case(rt, 128, 4, True, 4, True, [1900, 77], 1024, exact=False)
+    finally:
+        rt.set_tq_split(prev)
+
+
+def fused_step_case(rt, d, bits, qjl, group, bf16, lens, split, exact=True):
     import torch
-    log(f"tq fused step d={d} bits={bits} qjl={qjl} G={group} bf16={bf16}")
+    log(f"tq fused step d={d} bits={bits} qjl={qjl} G={group} bf16={bf16} lens={lens} split={split}")
     rng = np.random.default_rng(group * 3 + bits)
-    heads, lens = 2, [2100, 77]
+    heads = 2
     batch, nh, cap = len(lens), heads * group, 2200
     twins = [S.TqCache(rt, 2, heads, d, bits, qjl, batch, cap, seed=SEED) for _ in range(2)]
     try:
@@ -343,7 +364,11 @@ def test_write_attend_fused_step(rt, d, bits, qjl, group, bf16):
                 c.advance()
             torch.cuda.synchronize()
             for a, b_ in zip(*outs):
-                assert torch.equal(a, b_), step
+                if exact:
+                    assert torch.equal(a, b_), step
+                else:
+                    log(f"  step {step}: max abs diff {(a - b_).abs().max().item():.3e}")
+                    assert torch.allclose(a, b_, rtol=1e-3, atol=1e-4), step
         assert list(twins[1].lengths()[0][:batch]) == [n + 2 for n in lens]
         for layer in range(2):
             for b in range(batch):
