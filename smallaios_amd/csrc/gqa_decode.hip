@@ -221,7 +221,9 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, 
     // P' -> int8 (hi, lo) terms: term t = 0 / 1 of the quad is its row of
     // the PV A operand (rows 4*hq + 2, 4*hq + 3 are zero)
     const float sp = pmax * (1.0f / 127.0f);
-    const float inv_sp = pmax > 0.0f ? 127.0f / pmax : 0.0f;
+    // hardware reciprocal (1 ulp): hi stays within +-127 (rint of at most
+    // 127 (1 + 2^-22)), and lo takes up the difference
+    const float inv_sp = pmax > 0.0f ? 127.0f * __builtin_amdgcn_rcpf(pmax) : 0.0f;
     int pc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
