@@ -466,7 +466,14 @@ def main():
         k_us = float(np.median(kus))
         d_us = float(np.mean(dus))
         value = alg / (ms_step * 1e-3) / 1e9
-        achieved = alg / (d_us * 1e-6) / 1e9
+        # one launch per step (the fused step merging its splits in-kernel):
+        # the step clock, over back-to-back launches, prices the decode kernel
+        # itself; HIP events around single launches add dispatch latency.
+        # Otherwise (a combine kernel or a separate append follows or precedes
+        # it) the events around the decode kernel alone.
+        single_launch = not args.unfused and rt.last_decode_launches() == 1
+        kernel_us = ms_step * 1e3 if single_launch else d_us
+        achieved = alg / (kernel_us * 1e-6) / 1e9
         result = {
             "metric": METRIC if args.workload == "llama8k" else
             f"{args.workload} decode attention HBM GB/s, {quant} KV, 1 MI355X",
@@ -498,9 +505,13 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                          "traffic": traffic_from_profile(args.workload),
-                         "basis": "mean of HIP events recorded on the launch stream around "
-                                  "each decode launch (they include a few us of dispatch "
-                                  "latency, so rocprof's kernel duration is shorter)"},
+                         "kernel_us": round(kernel_us, 3),
+                         "basis": ("step clock over back-to-back steps of one decode launch "
+                                   "each (the fused step, splits merged in-kernel)"
+                                   if single_launch else
+                                   "mean of HIP events recorded on the launch stream around "
+                                   "each decode launch (they include a few us of dispatch "
+                                   "latency)")},
         }
         if rotated is not None:
             result["rotated_two_caches"] = rotated

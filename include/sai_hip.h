@@ -174,8 +174,11 @@ sai_status sai_kv_append(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const 
  * tokens of each sequence (ragged lengths allowed), GQA head grouping
  * kh = qh / (Hq/Hkv). Requires pending == 1.
  * q: device [batch, 1, num_heads*D] of `dtype` (F32 or BF16);
- * out: device [batch, 1, num_heads*D] f32. scale: used when has_scale != 0,
- * else sai_default_scale(D).
+ * out: device [batch, 1, num_heads*D] of out_dtype: F32, or BF16 rounded to
+ * nearest even from the f32 result (the reference's GPU attention returns
+ * Q's dtype, attention.rs:835 and :877-901, and the bf16 GEMM after it takes
+ * only bf16 x bf16, gpu_executor.rs:1024-1031); UNSUPPORTED otherwise.
+ * scale: used when has_scale != 0, else sai_default_scale(D).
  * window: gpu_gqa_with_cache's `window` (the node's local_window_size when
  * > 0): the query at position p sees keys [p - window, p]; <= 0 = off. A
  * sliding-window layer (sai_kvcache_set_layer_window) sees its last w keys;
@@ -185,7 +188,8 @@ sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const
                           int32_t dtype, int32_t batch, int32_t num_heads,
                           const float* cos_cache, const float* sin_cache, int32_t cache_rows,
                           int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
-                          float scale, int32_t window, float* out, void* stream);
+                          float scale, int32_t window, void* out, int32_t out_dtype,
+                          void* stream);
 
 /* ---- kernels 1 + 2 fused: one decode step in one launch ----------------------
  * Replaces gpu_gqa_with_cache (onnx-rt/src/cuda/kernels/attention.rs:1260-1295),
@@ -200,7 +204,8 @@ sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, c
                               int32_t kv_dtype, int32_t batch, int32_t num_heads,
                               const float* cos_cache, const float* sin_cache, int32_t cache_rows,
                               int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
-                              float scale, int32_t window, float* out, void* stream);
+                              float scale, int32_t window, void* out, int32_t out_dtype,
+                              void* stream);
 
 /* ---- the fused decode step without allocation ---------------------------------
  * No counterpart in the reference: this is for callers that cannot allocate
@@ -214,29 +219,34 @@ sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, c
  * partial floats, i.e. sequence-splits x kv heads x group x (head_dim + 2)
  * (the Llama-3-8B layer at 16 x 8k uses 133,120); a larger step fails with
  * UNSUPPORTED. Every call on one GPU shares that GPU's array: calls that
- * overlap on one GPU (other streams, other threads, other contexts) race. */
+ * overlap on one GPU (other streams, other threads, other contexts) race, and
+ * their outputs are undefined. Each call first clears its merge tickets with
+ * a small fill kernel on `stream` (no memset node under graph capture), so
+ * what a racing call left behind does not reach the calls after it. */
 sai_status sai_gqa_with_cache_noalloc(sai_ctx* ctx, sai_kvcache* cache, int32_t layer,
                                       const void* q, int32_t q_dtype, const void* k_new,
                                       const void* v_new, int32_t kv_dtype, int32_t batch,
                                       int32_t num_heads, const float* cos_cache,
                                       const float* sin_cache, int32_t cache_rows,
                                       int32_t do_rotary, int32_t rotary_interleaved,
-                                      int32_t has_scale, float scale, int32_t window, float* out,
-                                      void* stream);
+                                      int32_t has_scale, float scale, int32_t window, void* out,
+                                      int32_t out_dtype, void* stream);
 
 /* ---- kernel 3: prefill chunk (f16 MFMA) ---------------------------------------
  * Same contract as sai_gqa_decode for a chunk of sq == pending query tokens per
  * sequence (the reference's op_group_query_attention with Sq > 1, causal with
  * past_sk = seq_len[b], microsoft.rs:1156 and :331-337), over an int8 cache
  * or an int4 one (head_dim 64, 128 or 256).
- * q: device [batch, sq, num_heads*D]; out: device [batch, sq, num_heads*D] f32.
+ * q: device [batch, sq, num_heads*D]; out: device [batch, sq, num_heads*D] of
+ * out_dtype (F32 or BF16, as for sai_gqa_decode).
  * window and sliding-window layers as for sai_gqa_decode, applied to every
  * query row at its own position (gpu_gqa's mask, attention.rs:79, :111). */
 sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
                            int32_t dtype, int32_t batch, int32_t sq, int32_t num_heads,
                            const float* cos_cache, const float* sin_cache, int32_t cache_rows,
                            int32_t do_rotary, int32_t rotary_interleaved, int32_t has_scale,
-                           float scale, int32_t window, float* out, void* stream);
+                           float scale, int32_t window, void* out, int32_t out_dtype,
+                           void* stream);
 
 /* ---- standalone rotary embedding ----------------------------------------------
  * Replaces op_rotary_embedding (onnx-rt/src/ops/microsoft.rs:556-652, through
@@ -435,16 +445,20 @@ int32_t sai_set_tq_split(sai_ctx* ctx, int32_t rows);
 /* Waves per decode workgroup: 4 or 8, or 0 = automatic (4 for an int8
  * cache, 8 for int4). Returns the previous value. */
 int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves);
-/* Split merge of the decode kernel: 0 = separate combine kernel, 1 = the
- * last workgroup of a (sequence, kv head) merges in-kernel (int8 cache; the
- * partials are handed over with agent-scope stores and loads, one ticket
- * counter per (sequence, kv head)), 2 = automatic (the default: in-kernel
- * when every sequence of the launch has the same split count, else the
- * combine kernel; int4 always uses the combine kernel). Returns the previous
- * value; other values are ignored. */
+/* Split merge of the decode kernels (int8 and int4 caches): 0 = separate
+ * combine kernel, 1 = the last workgroup of a (sequence, kv head) merges
+ * in-kernel (the partials are handed over with agent-scope stores and loads,
+ * one ticket counter per (sequence, kv head)), 2 = automatic (the default:
+ * in-kernel when every sequence of the launch has the same split count, else
+ * the combine kernel). Returns the previous value; other values are
+ * ignored. */
 int32_t sai_set_decode_merge(sai_ctx* ctx, int32_t in_kernel);
 /* Number of workgroups and split size of the last decode launch on ctx. */
 sai_status sai_last_decode_shape(const sai_ctx* ctx, int32_t* workgroups, int32_t* split_tokens);
+/* Kernel launches of the last decode call on ctx: 1 (the decode kernel,
+ * splits merged in-kernel or a single split) or 2 (the combine kernel
+ * after it); 0 before any. */
+int32_t sai_last_decode_launches(const sai_ctx* ctx);
 /* Kernel timing of the decode step: with slots > 0, every sai_gqa_decode /
  * sai_gqa_with_cache call records two HIP events on its stream around the
  * decode kernel alone (not a combine kernel that follows it; an in-kernel

@@ -84,6 +84,7 @@ EXPORTS = [
     "sai_gqa_decode", "sai_gqa_with_cache", "sai_gqa_with_cache_noalloc", "sai_gqa_prefill",
     "sai_set_decode_split",
     "sai_set_decode_waves", "sai_set_decode_merge", "sai_last_decode_shape",
+    "sai_last_decode_launches",
     "sai_set_decode_timing", "sai_decode_kernel_times", "sai_rotary_embedding",
     "sai_rope_tables", "sai_copy_rows", "sai_tqcache_create", "sai_tqcache_destroy",
     "sai_tqcache_write", "sai_tqcache_advance", "sai_tqcache_reset", "sai_tqcache_set_lengths",
@@ -115,19 +116,20 @@ def _declare(L: C.CDLL) -> None:
         "sai_kvcache_pool": (i32, [p, i32, pp, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
         "sai_kv_append": (i32, [p, p, i32, p, p, i32, i32, i32, p, p, i32, i32, i32, p]),
         "sai_gqa_decode": (i32, [p, p, i32, p, i32, i32, i32, p, p, i32, i32, i32, i32, f, i32,
-                                 p, p]),
+                                 p, i32, p]),
         "sai_gqa_with_cache": (i32, [p, p, i32, p, i32, p, p, i32, i32, i32, p, p, i32, i32,
-                                     i32, i32, f, i32, p, p]),
-        "sai_gqa_with_cache_noalloc": (i32, [p, p, i32, p, i32, p, p, i32, i32, i32, p, p, i32, i32,
-                                     i32, i32, f, i32, p, p]),
+                                     i32, i32, f, i32, p, i32, p]),
+        "sai_gqa_with_cache_noalloc": (i32, [p, p, i32, p, i32, p, p, i32, i32, i32, p, p, i32,
+                                             i32, i32, i32, f, i32, p, i32, p]),
         "sai_gqa_prefill": (i32, [p, p, i32, p, i32, i32, i32, i32, p, p, i32, i32, i32, i32,
-                                  f, i32, p, p]),
+                                  f, i32, p, i32, p]),
         "sai_kvcache_set_layer_window": (i32, [p, p, i32, i32]),
         "sai_set_decode_split": (i32, [p, i32]),
         "sai_set_tq_split": (i32, [p, i32]),
         "sai_set_decode_waves": (i32, [p, i32]),
         "sai_set_decode_merge": (i32, [p, i32]),
         "sai_last_decode_shape": (i32, [p, C.POINTER(i32), C.POINTER(i32)]),
+        "sai_last_decode_launches": (i32, [p]),
         "sai_set_decode_timing": (i32, [p, i32]),
         "sai_decode_kernel_times": (i32, [p, C.POINTER(C.c_float), i32]),
         "sai_rotary_embedding": (i32, [p, p, p, i32, i32, i32, i32, i32, i32, p, C.c_int64,
@@ -246,6 +248,11 @@ class Runtime:
         wg, sp = C.c_int32(), C.c_int32()
         self._L.sai_last_decode_shape(self.handle, C.byref(wg), C.byref(sp))
         return wg.value, sp.value
+
+    def last_decode_launches(self) -> int:
+        """Kernel launches of the last decode call: 1 (decode kernel) or 2
+        (plus the combine kernel)."""
+        return int(self._L.sai_last_decode_launches(self.handle))
 
     def set_decode_timing(self, slots: int) -> int:
         """HIP events around the decode kernel alone for the last `slots`
@@ -404,8 +411,8 @@ class KvCache:
         self.rt.check(self._L.sai_gqa_decode(
             self.rt.handle, self.handle, layer, _dev_ptr(q), dt, batch, num_heads, _dev_ptr(cos),
             _dev_ptr(sin), cache_rows, int(do_rotary), int(interleaved), int(scale is not None),
-            0.0 if scale is None else float(scale), int(window), _dev_ptr(out), _stream(stream)),
-            "gqa_decode")
+            0.0 if scale is None else float(scale), int(window), _dev_ptr(out),
+            _dtype_code(out), _stream(stream)), "gqa_decode")
 
     def decode_with_cache(self, layer, q, k_new, v_new, out, batch, num_heads, cos=None,
                           sin=None, cache_rows=0, do_rotary=True, interleaved=False, scale=None,
@@ -417,7 +424,7 @@ class KvCache:
             self.rt.handle, self.handle, layer, _dev_ptr(q), qd, _dev_ptr(k_new), _dev_ptr(v_new),
             kd, batch, num_heads, _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary),
             int(interleaved), int(scale is not None), 0.0 if scale is None else float(scale),
-            int(window), _dev_ptr(out), _stream(stream)), "gqa_with_cache")
+            int(window), _dev_ptr(out), _dtype_code(out), _stream(stream)), "gqa_with_cache")
 
     def decode_with_cache_noalloc(self, layer, q, k_new, v_new, out, batch, num_heads, cos=None,
                                   sin=None, cache_rows=0, do_rotary=True, interleaved=False,
@@ -430,7 +437,8 @@ class KvCache:
             self.rt.handle, self.handle, layer, _dev_ptr(q), qd, _dev_ptr(k_new), _dev_ptr(v_new),
             kd, batch, num_heads, _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary),
             int(interleaved), int(scale is not None), 0.0 if scale is None else float(scale),
-            int(window), _dev_ptr(out), _stream(stream)), "gqa_with_cache_noalloc")
+            int(window), _dev_ptr(out), _dtype_code(out), _stream(stream)),
+            "gqa_with_cache_noalloc")
 
     def prefill(self, layer, q, out, batch, sq, num_heads, cos=None, sin=None, cache_rows=0,
                 do_rotary=True, interleaved=False, scale=None, stream=None, dtype=None, window=0):
@@ -439,7 +447,7 @@ class KvCache:
             self.rt.handle, self.handle, layer, _dev_ptr(q), dt, batch, sq, num_heads,
             _dev_ptr(cos), _dev_ptr(sin), cache_rows, int(do_rotary), int(interleaved),
             int(scale is not None), 0.0 if scale is None else float(scale), int(window),
-            _dev_ptr(out), _stream(stream)), "gqa_prefill")
+            _dev_ptr(out), _dtype_code(out), _stream(stream)), "gqa_prefill")
 
 
 class TqCache:

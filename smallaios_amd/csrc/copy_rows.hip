@@ -60,7 +60,20 @@ __global__ __launch_bounds__(kThreads) void copy_rows_kernel(const CopyRowsArgs 
   *dst = *src;
 }
 
+__global__ __launch_bounds__(kThreads) void fill_i32_kernel(int32_t* p, uint32_t n, int32_t v) {
+  const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 }  // namespace
+
+hipError_t launch_fill_i32(int32_t* p, size_t n, int32_t v, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  if (n > 0xFFFFFFFFull - kThreads) return hipErrorInvalidValue;
+  const dim3 g((uint32_t)((n + kThreads - 1) / kThreads)), t(kThreads);
+  hipLaunchKernelGGL(fill_i32_kernel, g, t, 0, st, p, (uint32_t)n, v);
+  return hipGetLastError();
+}
 
 hipError_t launch_copy_rows(const CopyRowsArgs& a, int chunk_bytes, hipStream_t st) {
   if (a.total == 0) return hipSuccess;

@@ -186,13 +186,19 @@ __device__ __forceinline__ void load16(const void* base, size_t off, int dtype, 
   }
 }
 
-// (sequence, split) of a decode workgroup. Uniform split count: direct
-// mapping; otherwise a prefix scan over the per-sequence split counts of
-// seq_lens[b] + pending tokens. Returns b = -1 past the last work item.
+// (sequence, split) of a decode workgroup and its split's length in 64-token
+// tiles. Uniform split count: direct mapping, splits of split_tokens.
+// Ragged: a prefix scan over the per-sequence split counts of seq_lens[b] +
+// pending tokens (in p.order when given), and a sequence's streamed tiles
+// dealt evenly to its splits (ceil(T / nsplit) each, the last split taking
+// the rest, never none), so no split is a short remainder. Returns b = -1
+// past the last work item.
 __device__ __forceinline__ void decode_work_item(const DecodeParams& p, int work, int lane, int& b,
-                                                 int& split, int& nsplit, int& split_base) {
+                                                 int& split, int& nsplit, int& split_base,
+                                                 int& tps) {
   b = -1;
   split = nsplit = split_base = 0;
+  tps = p.split_tokens / 64;
   if (p.uniform_nsplit > 0) {
     nsplit = p.uniform_nsplit;
     b = work / nsplit;
@@ -203,8 +209,10 @@ __device__ __forceinline__ void decode_work_item(const DecodeParams& p, int work
   int base = 0;
   for (int c0 = 0; c0 < p.batch; c0 += 64) {
     const int bi = c0 + lane;
-    const int Lb = bi < p.batch ? p.seq_lens[bi] + p.pending : 0;
-    const int n = (Lb - window_origin(Lb, p.window) + p.split_tokens - 1) / p.split_tokens;
+    const int sb = bi < p.batch ? (p.ordered ? (int)p.order[bi] : bi) : 0;
+    const int Lb = bi < p.batch ? p.seq_lens[sb] + p.pending : 0;
+    const int span = Lb - window_origin(Lb, p.window);
+    const int n = (span + p.split_tokens - 1) / p.split_tokens;
     int incl = n;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -215,17 +223,17 @@ __device__ __forceinline__ void decode_work_item(const DecodeParams& p, int work
     if (work < base + total) {
       const unsigned long long m = __ballot(base + incl > work);
       const int first = __ffsll((long long)m) - 1;
-      b = c0 + first;
+      b = __shfl(sb, first, 64);
       split_base = base + __shfl(incl - n, first, 64);
       nsplit = __shfl(n, first, 64);
+      const int tiles = (__shfl(span, first, 64) + 63) / 64;
+      tps = (tiles + nsplit - 1) / nsplit;
       split = work - split_base;
       return;
     }
     base += total;
   }
 }
-
-
 
 // The length of sequence b (seq_lens[b] + pending) and the split's page ids,
 // staged into sm_pg (page slot i of the split = sm_pg[i]). The length is a
@@ -235,12 +243,12 @@ __device__ __forceinline__ void decode_work_item(const DecodeParams& p, int work
 // first tile. With a window the split starts at the tile holding the first
 // visible key, which needs the length first. NT = threads of the workgroup.
 template <int NT>
-__device__ __forceinline__ void stage_split_pages(const DecodeParams& p, int b, int split,
+__device__ __forceinline__ void stage_split_pages(const DecodeParams& p, int b, int split, int tps,
                                                   int* sm_pg, int& L, int& k_lo,
                                                   int& first_page) {
   b = __builtin_amdgcn_readfirstlane(b);
   const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
-  const int split_pages = p.split_tokens / kPageTokens;
+  const int split_pages = tps * (64 / kPageTokens);
   const int len = p.seq_lens[b];
   if (p.window <= 0) {
     first_page = split * split_pages;

@@ -8,19 +8,22 @@
 // token-head at 80 % of 8 TB/s). Instead the int8 codes go straight from HBM
 // into v_mfma_i32_16x16x64_i8 operands and the per-token scales are applied to
 // the 32-bit dot products:
-//   score(t, h) = s_k[t] * (sq_hi[h] * <k_t, qhi_h> + sq_lo[h] * <k_t, qlo_h>)
+//   score(t, h) = s_k[t] * sq[h] * (<k_t, qhi_h> + <k_t, qmid_h>/254 + <k_t, qlo_h>/254^2)
 //   out(h, :)   = sum_t p'(t, h) * v_t,   p' = p * s_v[t] = sp[h]*(phi + plo/254)
-// Q (after RoPE) and P' are split into two int8 terms (hi + residual/254), so
-// their representation error is ~1/64516 of the row maximum; both terms ride
-// in spare MFMA rows/columns, so the split costs no extra MFMA issue.
+// Q (after RoPE) is split into three int8 terms (~24 significant bits, so
+// keys with large outlier channels do not amplify its rounding) and each
+// tile's P' into two (hi + residual/254, error ~1/64516 of the tile's
+// maximum); the terms ride in spare MFMA rows/columns (a DPP quad holds one
+// head's terms), so the split costs no extra MFMA issue.
 //
 // Wave layout (lane = r + 16 g, r = lane & 15, g = lane >> 4). A tile is 64
 // tokens = 4 pages; lane group g of a tile works on page g.
 //   QK  : S^T = K * Q^T.  A = K codes, row i of MFMA #blk is token
 //         (page i>>2, slot 4*blk + (i&3)); B = Q terms, column j = head-term
-//         (head j>>1, term j&1: 0 = hi, 1 = lo). The result lands with lane
-//         (j, g) holding head-term j for all 16 slots of page g -- exactly the
-//         A-operand layout the PV product needs, so no LDS transpose.
+//         (head j>>2, term j&3: 0 = hi, 1 = mid, 2 = lo, 3 = zero). The
+//         result lands with lane (j, g) holding head-term j for all 16 slots
+//         of page g -- exactly the A-operand layout the PV product needs (its
+//         rows j = hi and lo terms of P'), so no LDS transpose.
 //         k index: lane group g, k step ks <-> dims kdim0(g, ks) + [0,16):
 //         (D/4)*g + 16*ks up to head_dim 128, so one row's 4 lane groups read
 //         one contiguous 128-byte line; 16*g + 64*ks at 256, so they read 64
@@ -36,10 +39,12 @@
 //
 // Work split: grid.x enumerates (sequence, split) pairs over ragged lengths
 // (each wave finds its pair by a prefix scan over seq_lens), grid.y is the kv
-// head. NW waves of a workgroup take interleaved tiles of the split and merge
-// through LDS. A sequence with one split writes its output directly; with
-// several, every workgroup writes a partial (m, l, o) and the combine kernel
-// (a second launch, so no cross-workgroup fences) merges them.
+// head. The NW waves of a workgroup take the split's tiles from an LDS
+// counter and merge through LDS. A sequence with one split writes its output
+// directly; with several, every workgroup writes a partial (m, l, o), and
+// either the workgroup that takes the last ticket of its (sequence, kv head)
+// merges them (agent-scope stores and loads, below) or the combine kernel, a
+// second launch, does.
 #include <type_traits>
 
 #include "append_row.h"
@@ -278,8 +283,8 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
   const int work = blockIdx.x;
 
   // ---- (sequence, split) of this workgroup ------------------------------------
-  int b, split, nsplit, split_base;
-  decode_work_item(p, work, lane, b, split, nsplit, split_base);
+  int b, split, nsplit, split_base, tps;
+  decode_work_item(p, work, lane, b, split, nsplit, split_base, tps);
   if (b < 0 || b >= p.batch) return;  // uniform over the workgroup
 
   // length and the split's page ids (the page-table row has max_pages
@@ -288,7 +293,7 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
   // from the tile holding k_lo.
   __shared__ int sm_pg[kMaxSplitPages];
   int L, k_lo, first_page;
-  stage_split_pages<64 * NW>(p, b, split, sm_pg, L, k_lo, first_page);
+  stage_split_pages<64 * NW>(p, b, split, tps, sm_pg, L, k_lo, first_page);
   const int origin = (k_lo / 64) * 64;
 
   constexpr int HALF = D / 2;
@@ -304,8 +309,8 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) load16(p.q, qbase + kdim0<D>(g, ks), p.q_dtype, xq[ps][ks]);
   }
-  const int t_begin = origin + split * p.split_tokens;
-  const int t_end = min(L, t_begin + p.split_tokens);
+  const int t_begin = origin + split * tps * 64;
+  const int t_end = min(L, t_begin + tps * 64);
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
   const int n_tiles = (t_end - t_begin + 63) / 64;
   // next tile of the split to hand out (see below)
@@ -588,7 +593,7 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
       O += sm_o[w][hd][d] * f;
     }
     if (nsplit == 1) {
-      p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+      store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * D + d, Ls > 0.0f ? O / Ls : 0.0f, p.out_bf16);
     } else if (p.merge_in_kernel) {
       store_partial(part + hd * (D + 2) + 2 + d, O);
       if (d == 0) {
@@ -643,7 +648,7 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
       merge_partials<4>(ph, stride, d, nsplit, -1, M, Ls, O);
     else
       merge_partials<8>(ph, stride, d, nsplit, -1, M, Ls, O);
-    p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+    store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * D + d, Ls > 0.0f ? O / Ls : 0.0f, p.out_bf16);
   }
   if (threadIdx.x == 0) reset_ticket(counter);
 }
@@ -700,7 +705,7 @@ __global__ __launch_bounds__(G * D) void gqa_decode_combine_kernel(DecodeParams 
     }
     M = mb;
   }
-  p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+  store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * D + d, Ls > 0.0f ? O / Ls : 0.0f, p.out_bf16);
 }
 
 template <int D, int G>

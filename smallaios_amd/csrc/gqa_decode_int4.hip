@@ -309,10 +309,15 @@ __device__ __forceinline__ void compute_tile4(const Tile4<D>& T, State4<D, G>& s
   }
 }
 
-// head_dim 256 runs one wave per SIMD with the whole register file (two
-// halves of tiles, query terms and dots)
+// head_dim 256 (two halves of tiles, query terms and dots) and group 8 at 128 (two
+// quads of heads: twice the query terms, dots and accumulators) run one wave
+// per SIMD with the whole register file; at two waves per SIMD group 8 spilled
+// ~400 bytes per lane
+template <int D, int G>
+constexpr bool kOneWavePerSimd = D > 128 || (G > 4 && D == 128);
+
 template <int D, int G, int NW>
-__global__ __launch_bounds__(64 * NW, D > 128 ? 1 : 8 / NW) void gqa_decode_int4_kernel(
+__global__ __launch_bounds__(64 * NW, (kOneWavePerSimd<D, G>) ? 1 : 8 / NW) void gqa_decode_int4_kernel(
     DecodeParams p) {
   constexpr int HT = State4<D, G>::HT;
   constexpr int NG = D / 32;
@@ -327,8 +332,8 @@ __global__ __launch_bounds__(64 * NW, D > 128 ? 1 : 8 / NW) void gqa_decode_int4
   const int kvh = blockIdx.y;
   const int work = blockIdx.x;
 
-  int b, split, nsplit, split_base;
-  decode_work_item(p, work, lane, b, split, nsplit, split_base);
+  int b, split, nsplit, split_base, tps;
+  decode_work_item(p, work, lane, b, split, nsplit, split_base, tps);
   if (b < 0 || b >= p.batch) return;  // uniform over the workgroup
 
   // length first; then the page ids of the split; then the query and the
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(64 * NW, D > 128 ? 1 : 8 / NW) void gqa_decode_int4
   // sliding window: keys [k_lo, L) visible, splits from the tile holding k_lo
   __shared__ int sm_pg[kMaxSplitPages];
   int L, k_lo, first_page;
-  stage_split_pages<64 * NW>(p, b, split, sm_pg, L, k_lo, first_page);
+  stage_split_pages<64 * NW>(p, b, split, tps, sm_pg, L, k_lo, first_page);
   const int origin = (k_lo / 64) * 64;
 
   // lane (j = 4*hh + G', g) holds the 32 dims of group g of head 4*qd + hh
@@ -379,8 +384,8 @@ __global__ __launch_bounds__(64 * NW, D > 128 ? 1 : 8 / NW) void gqa_decode_int4
                        cq4[hf][h2], sq4[hf][h2]);
   }
 
-  const int t_begin = origin + split * p.split_tokens;
-  const int t_end = min(L, t_begin + p.split_tokens);
+  const int t_begin = origin + split * tps * 64;
+  const int t_end = min(L, t_begin + tps * 64);
   const int n_pages_split = (t_end - 1) / kPageTokens - first_page + 1;
   const int n_tiles = (t_end - t_begin + 63) / 64;
   const int last_owner = (n_tiles - 1) % NW;
@@ -600,7 +605,7 @@ __global__ __launch_bounds__(64 * NW, D > 128 ? 1 : 8 / NW) void gqa_decode_int4
       O += (sm_o[w][hd][d] + sm_z[w][hd][d >> 5]) * f;
     }
     if (nsplit == 1) {
-      p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+      store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * D + d, Ls > 0.0f ? O / Ls : 0.0f, p.out_bf16);
     } else if (p.merge_in_kernel) {
       store_partial(part + hd * (D + 2) + 2 + d, O);
       if (d == 0) {
@@ -649,16 +654,16 @@ __global__ __launch_bounds__(64 * NW, D > 128 ? 1 : 8 / NW) void gqa_decode_int4
       merge_partials<4>(ph, stride, d, nsplit, -1, M, Ls, O);
     else
       merge_partials<8>(ph, stride, d, nsplit, -1, M, Ls, O);
-    p.out[((size_t)b * Hq + kvh * G + hd) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+    store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * D + d, Ls > 0.0f ? O / Ls : 0.0f, p.out_bf16);
   }
   if (threadIdx.x == 0) reset_ticket(counter);
 }
 
 template <int D, int G>
 hipError_t launch_g(const DecodeParams& p, int work_items, bool combine, hipStream_t st) {
-  // head_dim 256: four waves (one per SIMD)
+  // head_dim 256 and group 8: four waves (one per SIMD)
   bool eight = false;
-  if constexpr (D <= 128) {
+  if constexpr (!kOneWavePerSimd<D, G>) {
     eight = p.waves == 8;
     if (eight)
       hipLaunchKernelGGL((gqa_decode_int4_kernel<D, G, 8>), dim3(work_items, p.kv_heads),

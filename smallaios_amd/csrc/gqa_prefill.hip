@@ -88,12 +88,30 @@ __device__ __forceinline__ float wave_max(float v) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // How far (log2 units) a row's scores may rise above its reference point
-// before the reference moves: softmax weights stay <= 2^kMaxLead = 4, so
-// p * s_v stays inside binary16 for V rows up to |v| ~ 2e6.
+// before the reference moves: softmax weights stay <= 2^kMaxLead = 4.
 constexpr float kMaxLead = 2.0f;
-// Fast-path bounds: p * s_v <= kFastSum (inside binary16), row sums <= kFastCap
+// Fast-path bounds: the PV operand (p * s_v, or p * s_v / max(s_v) on a
+// large-V tile) <= kFastSum (inside binary16), row sums <= kFastCap
 constexpr float kFastSum = 32768.0f;
 constexpr float kFastCap = 1048576.0f;
+// int8 tiles whose largest V scale exceeds this (|v| above 32) take the
+// exact-weight PV: the operand is p * s_v / max(s_v) (at most p, whatever
+// the V magnitude) split into binary16 hi + lo (~22 significant bits instead
+// of 11), and the tile's product is scaled by max(s_v) in f32. A single
+// binary16 weight's 2^-11 rounding times |v| would otherwise dominate the
+// error of outputs that cancel far below |v|.
+constexpr float kBigVScale = 0.25f;
+// int4 V is staged as f16 of v * 2^-5 and the weights as f16 of p * 2^5:
+// |v| <= 16 * 65504 for binary16 (scale, zero), so the staged values stay
+// finite, and the product p * v is unchanged.
+constexpr float kInt4VDown = 0.03125f;
+constexpr float kInt4PUp = 32.0f;
+// The precise pass takes its weights 2^kPrecLift larger (an exact shift of the
+// scores, undone in the row sums and at the output): its PV operand p * s_v /
+// 2^vexp then spans up to 2^kPrecLift instead of 1, so the lo half of a
+// small weight stays a normal binary16 rather than falling to the 2^-24
+// subnormal step, which times |v| ~ 2^vexp would dominate the error.
+constexpr int kPrecLift = 12;
 
 // V fragments read ahead of the PV MFMAs that consume them
 constexpr int kVPrefetch = 6;
@@ -109,7 +127,11 @@ struct PrefillTile {
   alignas(16) _Float16 v[2 * D * VROW];
   alignas(16) float sk[64];
   alignas(16) float sv[64];
-  float svmax;  // largest V scale of the tile (int8)
+  // int8: the V scales above are divided by the tile's power of two vsig
+  // (1 unless the largest scale exceeds kBigVScale), svmax is their largest
+  // (at most kBigVScale) and vexp = log2(vsig)
+  float svmax;
+  int vexp;
 };
 
 // Codes and scales of one 64-token tile, held in registers between the load
@@ -239,14 +261,19 @@ __device__ __forceinline__ void stage_store(const TileStage<D, NT>& S, Tile& T, 
   }
   if (tid < 128) {
     const float sc = t0 + (tid & 63) < total ? S.sc : 0.0f;
-    if (tid < 64)
+    if (tid < 64) {
       T.sk[tid] = sc;
-    else
-      T.sv[tid - 64] = sc;
-    // the second wave holds the 64 V scales: their maximum bounds p * s_v
-    if (__builtin_amdgcn_readfirstlane(tid >> 6) == 1) {
+    } else if (__builtin_amdgcn_readfirstlane(tid >> 6) == 1) {
+      // the second wave holds the 64 V scales: their maximum m bounds the
+      // PV operand. Above kBigVScale they are divided by the power of two
+      // 2^e >= m / kBigVScale (exact), so the operand stays <= p * kBigVScale
       const float m = wave_max(sc);
-      if (tid == 64) T.svmax = m;
+      const int e = m > kBigVScale ? __builtin_amdgcn_frexp_expf(m * (1.0f / kBigVScale)) : 0;
+      T.sv[tid - 64] = __builtin_ldexpf(sc, -e);
+      if (tid == 64) {
+        T.svmax = __builtin_ldexpf(m, -e);
+        T.vexp = e;
+      }
     }
   }
 }
@@ -357,7 +384,9 @@ __device__ __forceinline__ void stage_store4(const TileStage4<D, NT>& S, Prefill
     for (int sl = 0; sl < 16; ++sl) {
       const uint32_t nib = (w[sl >> 3] >> (4 * (sl & 7))) & 0xF;
       const bool valid = t0 + 16 * cb + sl < total;
-      val[sl] = valid ? (float)nib * half_lo(S.vp[i][sl]) + half_hi(S.vp[i][sl]) : 0.0f;
+      // exact power-of-two scaling after the f32 dequantisation
+      val[sl] = valid ? ((float)nib * half_lo(S.vp[i][sl]) + half_hi(S.vp[i][sl])) * kInt4VDown
+                      : 0.0f;
     }
     // slot s of page cb: k step cb>>1, group s>>2, element (cb&1)*4 + (s&3)
     _Float16* row = T.v + ((size_t)(cb >> 1) * D + d) * VROW;
@@ -375,7 +404,9 @@ __device__ __forceinline__ void stage_store4(const TileStage4<D, NT>& S, Prefill
 
 // RB row blocks of 16 attention rows per wave: 2 up to head_dim 128, 1 at
 // 256 (the query pair and the accumulators of two blocks would not fit).
-template <int D, int G, int NW, int Q>
+// PREC: the int8 precise pass (see the tile loop below): only workgroups
+// whose flag the fast pass set run, from their first tile.
+template <int D, int G, int NW, int Q, bool PREC>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillParams p) {
   constexpr int NT = 64 * NW;
   constexpr int KS = D / 32;      // 32-dim k steps of QK
@@ -403,6 +434,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   const int g = lane >> 4;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
+  // the workgroup's large-V flag: set by the fast pass, taken (and cleared,
+  // so the flags are zero between launches) by the precise pass
+  int32_t* const prec_flag =
+      p.prec_flags + ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  if constexpr (PREC) {
+    if (__builtin_amdgcn_readfirstlane(*prec_flag) == 0) return;  // uniform
+    __syncthreads();  // every wave has read it
+    if (tid == 0) *prec_flag = 0;
+  }
   const int n_qt = (p.sq + QT - 1) / QT;
   const int qtile = n_qt - 1 - (int)blockIdx.x;  // longest rows first
   const int q0 = qtile * QT;
@@ -519,15 +559,39 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int jb = 0; jb < JB; ++jb) acc[rb][jb] = v4f{0.f, 0.f, 0.f, 0.f};
+  // int8: acc holds sum p * v in units of 2^vexp_run, the largest V-scale
+  // exponent of the tiles so far (0 while every tile's V is small; uniform)
+  int vexp_run = 0;
 
   // one tile: QK^T, mask, softmax, PV against the tile in LDS slot T
   auto process = [&](const Tile& T, int tile) __attribute__((always_inline)) {
     const int t0 = tile * 64;
+    // int8 large V: a tile whose exponent passes the running one raises it
+    // (acc rescaled by an exact power of two); a tile below it has its
+    // weights taken 2^(vexp_tile - vexp_run) smaller, and the precise pass's
+    // 2^kPrecLift larger: p' = p * 2^dexp (dexp added to every score), so
+    // that p' * (s_v / 2^vexp_tile) = p * s_v * 2^(kPrecLift - vexp_run)
+    int dexp = 0;
+    float svm = 1.0f;  // largest V scale of the tile, / 2^vexp_tile
+    if constexpr (!INT4) {
+      const int et = PREC ? __builtin_amdgcn_readfirstlane(T.vexp) : 0;  // fast pass: 0
+      if (PREC && et > vexp_run) {
+        const float f = __builtin_ldexpf(1.0f, vexp_run - et);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int jb = 0; jb < JB; ++jb) acc[rb][jb] *= f;
+        vexp_run = et;
+      }
+      dexp = et - vexp_run + (PREC ? kPrecLift : 0);
+      svm = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, T.svmax)));
+    }
+    const float lc = (float)dexp;
 
     // S^T for both row blocks: 4 column blocks of 16 tokens; k steps outer so
     // that eight independent accumulation chains interleave on the MFMA pipe.
     // s holds each score relative to its row's reference point:
-    // s = <q', k> * s_k - m_run (masked keys: -inf)
+    // s = <q', k> * s_k - m_run + dexp (masked keys: -inf)
     auto scores = [&](float (&s)[RB][4][4]) __attribute__((always_inline)) {
       v4f c[4][RB];
 #pragma unroll
@@ -571,6 +635,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
           }
         }
       }
+      float mref[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) mref[rb] = INT4 ? m_run[rb] : m_run[rb] - lc;
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
         float skx[4] = {1.0f, 1.0f, 1.0f, 1.0f};
@@ -582,8 +649,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            s[rb][cb][e] = INT4 ? c[cb][rb][e] - m_run[rb]
-                                : __builtin_fmaf(c[cb][rb][e], skx[e], -m_run[rb]);
+            s[rb][cb][e] = INT4 ? c[cb][rb][e] - mref[rb]
+                                : __builtin_fmaf(c[cb][rb][e], skx[e], -mref[rb]);
       }
       if (tile >= full_tiles || tile < lo_full) {
 #pragma unroll
@@ -631,7 +698,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[rb][cb][e]);
-        mt = xgroup_max(mt);
+        mt = xgroup_max(mt) - lc;  // relative to the reference point
         const bool row_moves = mt > kMaxLead || (l_run[rb] == 0.0f && mt != -INFINITY);
         lead[rb] = row_moves ? mt : 0.0f;
         move = move || row_moves;
@@ -640,7 +707,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
           m_run[rb] += lead[rb];
-          const float alpha = fast_exp2(-lead[rb]);  // 1 for rows that keep their max
+          // 1 for rows that keep their reference; 0 for rows with no history
+          // (their first keys may sit far below 0, where exp2(-lead) is inf
+          // and would turn the zero sums into NaN)
+          const float alpha = l_run[rb] > 0.0f ? fast_exp2(-lead[rb]) : 0.0f;
           l_run[rb] *= alpha;
 #pragma unroll
           for (int cb = 0; cb < 4; ++cb)
@@ -663,53 +733,59 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
     } else {
       // Fast path (int8): the weights against the current reference point are
       // kept when they provably fit: a row sum <= kFastSum / max(s_v) bounds
-      // every p * s_v (the PV operand, binary16) by kFastSum, the cap bounds
-      // the running sums, and a row that has seen no keys yet needs a sum >= 1
+      // every PV operand p * s_v by kFastSum (binary16), the cap bounds the
+      // running sums, and a row that has seen no keys yet needs a sum >= 1
       // (its largest weight is then >= 1/64, so the reference is not far above
       // its scores). Otherwise (a row's first keys, scores that rose far above
       // the reference, inf or NaN) the tile is settled as above, its scores
-      // recomputed from the tile still in LDS.
+      // recomputed from the tile still in LDS. (The sums here are 2^dexp of
+      // the weights' own.)
       scores(s);
       weights(s, rsum);
-      const float svm = T.svmax;
+      const float cap = __builtin_ldexpf(kFastCap, dexp);
+      const float one = __builtin_ldexpf(1.0f, dexp);
       bool bad = false;
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        const bool ok = rsum[rb] <= kFastCap && rsum[rb] * svm <= kFastSum &&
-                        (l_run[rb] > 0.0f || rsum[rb] >= 1.0f);
+        const bool ok = rsum[rb] <= cap && rsum[rb] * svm <= kFastSum &&
+                        (l_run[rb] > 0.0f || rsum[rb] >= one);
         bad = bad || !ok;
       }
       if (__builtin_amdgcn_ballot_w64(bad) != 0) settle();
     }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      l_run[rb] += INT4 ? rsum[rb] : __builtin_ldexpf(rsum[rb], -dexp);
 
-    v8h pa[RB][2];
+    auto vfrag = [&](int i) {
+      const int kst = i / JB, jb = i % JB;
+      return *(const v8h*)(T.v + ((size_t)kst * D + 16 * jb + r) * VROW + 8 * g);
+    };
+    // PV operand: p (x 2^dexp) * s_v (/ 2^vexp_tile) for int8, p * 2^5 for int4
+    auto operand = [&](int rb, int cb, int e, const float (&svx)[4]) {
+      return s[rb][cb][e] * (INT4 ? kInt4PUp : svx[e]);
+    };
+    if constexpr (!PREC) {
+      v8h pa[RB][2];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      l_run[rb] += rsum[rb];
+      for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
-        float svx[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-        if constexpr (!INT4) {
-          const float4 svv = *(const float4*)(T.sv + 16 * cb + 4 * g);
-          svx[0] = svv.x, svx[1] = svv.y, svx[2] = svv.z, svx[3] = svv.w;
+        for (int cb = 0; cb < 4; ++cb) {
+          float svx[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+          if constexpr (!INT4) {
+            const float4 svv = *(const float4*)(T.sv + 16 * cb + 4 * g);
+            svx[0] = svv.x, svx[1] = svv.y, svx[2] = svv.z, svx[3] = svv.w;
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pa[rb][cb >> 1][(cb & 1) * 4 + e] = (_Float16)operand(rb, cb, e, svx);
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          pa[rb][cb >> 1][(cb & 1) * 4 + e] =
-              (_Float16)(INT4 ? s[rb][cb][e] : s[rb][cb][e] * svx[e]);
       }
-    }
-    // PV over the 2 x JB V fragments, kVPrefetch of them in flight ahead of
-    // the MFMAs that consume them (the scheduler fence keeps each read ahead
-    // of its consumer by that many MFMA pairs, so the LDS latency is covered)
-    {
+      // PV over the 2 x JB V fragments, kVPrefetch of them in flight ahead of
+      // the MFMAs that consume them (the scheduler fence keeps each read ahead
+      // of its consumer by that many MFMA pairs, so the LDS latency is covered)
       constexpr int NV = 2 * JB;
       constexpr int PF = INT4 ? kVPrefetchInt4 : kVPrefetch;
       v8h vf[NV];
-      auto vfrag = [&](int i) {
-        const int kst = i / JB, jb = i % JB;
-        return *(const v8h*)(T.v + ((size_t)kst * D + 16 * jb + r) * VROW + 8 * g);
-      };
 #pragma unroll
       for (int i = 0; i < PF && i < NV; ++i) vf[i] = vfrag(i);
 #pragma unroll
@@ -721,17 +797,66 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
           acc[rb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rb][kst], vf[i], acc[rb][jb], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
+    } else {
+      // int8 with large V (some tile's V scales above kBigVScale): the
+      // operand as binary16 hi + lo (~22 significant bits), both against the
+      // same V fragment
+      v8h ph[RB][2], pl[RB][2];
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const float4 svv = *(const float4*)(T.sv + 16 * cb + 4 * g);
+        const float svx[4] = {svv.x, svv.y, svv.z, svv.w};
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float w = operand(rb, cb, e, svx);
+            // one rounded product feeds both halves of the split
+            __asm__("" : "+v"(w));
+            const _Float16 hi = (_Float16)w;
+            ph[rb][cb >> 1][(cb & 1) * 4 + e] = hi;
+            pl[rb][cb >> 1][(cb & 1) * 4 + e] = (_Float16)(w - (float)hi);
+          }
+      }
+#pragma unroll
+      for (int i = 0; i < 2 * JB; ++i) {
+        const v8h vf = vfrag(i);
+        const int kst = i / JB, jb = i % JB;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[rb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[rb][kst], vf, acc[rb][jb], 0, 0, 0);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[rb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[rb][kst], vf, acc[rb][jb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-
   };
 
-  // PER_BARRIER tiles between barriers; each stages the tile PER_BARRIER
-  // ahead into the slot the previous round finished reading (its global loads
-  // in flight while the tile is computed, the page ids of the one after)
+  // Tiles in order. PER_BARRIER tiles between barriers; each stages the
+  // tile PER_BARRIER ahead into the slot the previous round finished reading
+  // (its global loads in flight while the tile is computed, the page ids of
+  // the one after). The fast pass (every int4 tile; int8 while every V
+  // scale so far is at most kBigVScale) gives up at the first int8 tile with
+  // large V: it flags the workgroup and returns before writing anything, and
+  // the precise pass (a second launch of this kernel) recomputes the
+  // workgroup with the large-V bookkeeping. As a separate kernel the
+  // bookkeeping costs the fast pass no registers.
+  auto big = [&](const Tile& T) {
+    if constexpr (INT4 || PREC) return false;
+    else return __builtin_amdgcn_readfirstlane(T.vexp) > 0;
+  };
+  // the loops end early (their bound drops to the current tile) when the fast
+  // pass gives up: one loop exit, as without the check
+  int t_stop = n_tiles;
   if constexpr (NSLOT == 1) {
     // one slot: the next tile's loads are in flight while this one is
     // computed, and it is stored once every wave has finished reading
-    for (int tile = tile_lo; tile < n_tiles; ++tile) {
+    for (int tile = tile_lo; tile < t_stop; ++tile) {
+      if (big(sT[0])) {  // every wave sees the same tile
+        t_stop = tile;
+        break;
+      }
       const bool more = tile + 1 < n_tiles;
       if (more) {
         load_stage((tile + 1) * 64);
@@ -745,7 +870,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       }
     }
   } else {
-    for (int tile = tile_lo; tile < n_tiles; tile += PER_BARRIER) {
+    for (int tile = tile_lo; tile < t_stop; tile += PER_BARRIER) {
+      // the tiles of this round are in LDS (the barrier below orders them)
+      bool any_big = big(slot(tile));
+      if (PER_BARRIER == 2 && tile + 1 < n_tiles) any_big = any_big || big(slot(tile + 1));
+      if (any_big) {
+        t_stop = tile;
+        break;
+      }
       // not unrolled: one copy of the tile body keeps the register budget
 #pragma nounroll
       for (int h = 0; h < PER_BARRIER; ++h) {
@@ -765,6 +897,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
     }
   }
 
+  if (!PREC && t_stop < n_tiles) {
+    if (tid == 0) *prec_flag = 1;
+    return;
+  }
+
   // ---- write O / l ------------------------------------------------------------
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
@@ -776,27 +913,44 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       const int il = q0 + R / G;
       if (il >= p.sq) continue;
       const int hq = kvh * G + R % G;
-      float* o = p.out + (((size_t)b * p.sq + il) * Hq + hq) * D;
-      const float f = l > 0.0f ? 1.0f / l : 0.0f;
+      const size_t o = (((size_t)b * p.sq + il) * Hq + hq) * D;
+      // acc is in units of 2^(vexp_run - kPrecLift) in the precise pass (exact)
+      const float f =
+          l > 0.0f ? __builtin_ldexpf(1.0f / l, PREC ? vexp_run - kPrecLift : 0) : 0.0f;
 #pragma unroll
-      for (int jb = 0; jb < JB; ++jb) o[16 * jb + r] = acc[rb][jb][e] * f;
+      for (int jb = 0; jb < JB; ++jb) store_out(p.out, o + 16 * jb + r, acc[rb][jb][e] * f, p.out_bf16);
     }
   }
 }
 
-template <int D, int NW, int Q>
-hipError_t launch_dn(const PrefillParams& p, int group, hipStream_t st) {
+// Rows per workgroup (query positions x heads of one kv head) and the grid.
+template <int D, int NW>
+dim3 prefill_grid(const PrefillParams& p, int group) {
   constexpr int RB = D > 128 ? 1 : 2;  // as in the kernel
-  auto grid = [&](int qt) { return dim3((p.sq + qt - 1) / qt, p.kv_heads, p.batch); };
+  const int qt = 16 * RB * NW / group;
+  return dim3((p.sq + qt - 1) / qt, p.kv_heads, p.batch);
+}
+
+template <int D, int NW, int Q, bool PREC>
+hipError_t launch_pass(const PrefillParams& p, int group, hipStream_t st) {
+  const dim3 grid = prefill_grid<D, NW>(p, group);
   const dim3 block(64 * NW);
   switch (group) {
-    case 1: hipLaunchKernelGGL((gqa_prefill_kernel<D, 1, NW, Q>), grid(16 * RB * NW), block, 0, st, p); break;
-    case 2: hipLaunchKernelGGL((gqa_prefill_kernel<D, 2, NW, Q>), grid(8 * RB * NW), block, 0, st, p); break;
-    case 4: hipLaunchKernelGGL((gqa_prefill_kernel<D, 4, NW, Q>), grid(4 * RB * NW), block, 0, st, p); break;
-    case 8: hipLaunchKernelGGL((gqa_prefill_kernel<D, 8, NW, Q>), grid(2 * RB * NW), block, 0, st, p); break;
+    case 1: hipLaunchKernelGGL((gqa_prefill_kernel<D, 1, NW, Q, PREC>), grid, block, 0, st, p); break;
+    case 2: hipLaunchKernelGGL((gqa_prefill_kernel<D, 2, NW, Q, PREC>), grid, block, 0, st, p); break;
+    case 4: hipLaunchKernelGGL((gqa_prefill_kernel<D, 4, NW, Q, PREC>), grid, block, 0, st, p); break;
+    case 8: hipLaunchKernelGGL((gqa_prefill_kernel<D, 8, NW, Q, PREC>), grid, block, 0, st, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// The fast pass, then (int8) the precise pass over the workgroups it flagged.
+template <int D, int NW, int Q>
+hipError_t launch_dn(const PrefillParams& p, int group, hipStream_t st) {
+  hipError_t e = launch_pass<D, NW, Q, false>(p, group, st);
+  if (e != hipSuccess || Q != kQuantInt8) return e;
+  return launch_pass<D, NW, Q, true>(p, group, st);
 }
 
 // 8 waves (256 rows) per workgroup: the staged K/V tile serves twice the rows
@@ -809,6 +963,11 @@ hipError_t launch_d(const PrefillParams& p, int group, int quant, hipStream_t st
 }
 
 }  // namespace
+
+size_t prefill_workgroups(const PrefillParams& p, int head_dim, int group) {
+  const dim3 g = head_dim > 128 ? prefill_grid<256, 8>(p, group) : prefill_grid<128, 8>(p, group);
+  return (size_t)g.x * g.y * g.z;
+}
 
 hipError_t launch_gqa_prefill(const PrefillParams& p, int head_dim, int group, int quant,
                               hipStream_t st) {

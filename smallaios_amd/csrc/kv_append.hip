@@ -302,6 +302,228 @@ __global__ __launch_bounds__(2 * D) void kv_append_page_int8_kernel(AppendParams
   }
 }
 
+// ---------------------------------------------------- int4, page blocks ----
+// Multi-token int4 appends, one workgroup per (sequence b, page, kv head h)
+// block, the int8 page kernel's thread layout: lane c of a token's L = D/8
+// lanes holds dims [4c, 4c+4) and [D/2 + 4c, D/2 + 4c + 4), so a group of 32
+// dims is 8 aligned lanes (its min/max: DPP within half-rows of 8) and RoPE
+// stays in-lane. Per element the arithmetic is quant_int4_elem's (min/max
+// over the group, scale and zero point rounded to binary16, the correctly
+// rounded quotient and round_f32), so codes and parameters are the same
+// bits. Codes are staged in LDS (K rows; V one byte per (dim, slot)) and
+// leave in 16-byte stores: K rows of the new slots, V two dims' packed
+// columns per thread with the nibbles of slots outside the appended range
+// kept, and the (scale, zero) pairs of the new slots.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// min and max over the 8 aligned lanes of a group (quad swaps, then the other
+// quad of the half-row); exact and order-free
+__device__ __forceinline__ void group8_minmax(float& mn, float& mx) {
+  mn = fminf(mn, dpp_f<0xB1>(mn));
+  mx = fmaxf(mx, dpp_f<0xB1>(mx));
+  mn = fminf(mn, dpp_f<0x4E>(mn));
+  mx = fmaxf(mx, dpp_f<0x4E>(mx));
+  mn = fminf(mn, dpp_f<0x141>(mn));  // row_half_mirror
+  mx = fmaxf(mx, dpp_f<0x141>(mx));
+}
+
+// Codes of this lane's 4 elements of a group held by 8 lanes, and the
+// group's binary16 (scale, zero) as one word (scale in the low half).
+__device__ __forceinline__ uint32_t quant4_int4(const float (&x)[4], uint32_t& sz) {
+#pragma clang fp contract(off)
+  // NaN never wins a `<` / `>` comparison in the reference loop
+  float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    mn = fminf(mn, x[j] != x[j] ? INFINITY : x[j]);
+    mx = fmaxf(mx, x[j] != x[j] ? -INFINITY : x[j]);
+  }
+  group8_minmax(mn, mx);
+  const float range = mx - mn;
+  const float scale = (range > 0.0f) ? range / 15.0f : 1.0f;
+  const _Float16 hs = (_Float16)scale;  // round to nearest even
+  const _Float16 hz = (_Float16)mn;
+  const float sf = (float)hs;
+  const float zf = (float)hz;
+  uint32_t w = 0u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t v = 0u;
+    if (sf > 0.0f) {
+      // round_f32 of onnx-rt/src/kv_compression.rs:27-37, then `as u32`
+      const float t = (x[j] - zf) / sf;
+      const float tr = (float)sat_i32(t);
+      const float fr = t - tr;
+      const float rr = (fr >= 0.5f) ? tr + 1.0f : ((fr <= -0.5f) ? tr - 1.0f : tr);
+      v = sat_u32(rr);
+    }
+    w |= (v < 15u ? v : 15u) << (4 * j);  // codes packed LSB first
+  }
+  sz = (uint32_t)__builtin_bit_cast(uint16_t, hs) | ((uint32_t)__builtin_bit_cast(uint16_t, hz) << 16);
+  return w;
+}
+
+// The 16 one-byte codes of a V column (slot s at byte s) as 8 bytes of
+// nibble pairs, slot 2i in the low nibble of byte i.
+__device__ __forceinline__ uint2 pack_column(const uint4 c) {
+  auto pk = [](uint32_t a, uint32_t b) {
+    const uint32_t u = (a | (a >> 4)) & 0x00FF00FFu;  // bytes 0, 2: slot pairs of a
+    const uint32_t v = (b | (b >> 4)) & 0x00FF00FFu;
+    return (u & 0xFFu) | ((u >> 8) & 0xFF00u) | ((v & 0xFFu) << 16) | ((v << 8) & 0xFF000000u);
+  };
+  return uint2{pk(c.x, c.y), pk(c.z, c.w)};
+}
+
+template <int D, bool BF16, int ROPE>
+__global__ __launch_bounds__(2 * D) void kv_append_page_int4_kernel(AppendParams p) {
+  constexpr int L = D / 8;    // lanes per token
+  constexpr int W = D / 32;   // waves: kPageTokens / (64 / L)
+  constexpr int HALF = D / 2;
+  constexpr int NG = D / 32;  // groups of a row
+  constexpr int KS = D / 2 + 16;  // LDS K row stride (bytes)
+  constexpr uint32_t ESZ = BF16 ? 2 : 4;
+  constexpr int PB = D / 8 < 16 ? D / 8 : 16;  // bytes of a (scale, zero) piece
+  constexpr int PPS = (D / 8) / PB;            // pieces per slot
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = blockIdx.x, b = blockIdx.z;
+  const int start = p.seq_lens[b];
+  const int page_idx = start / kPageTokens + (int)blockIdx.y;
+  const int t0 = page_idx * kPageTokens;  // position of slot 0
+  const int lo = max(start, t0) - t0;     // new slots [lo, hi)
+  const int hi = min(start + p.s_new, t0 + kPageTokens) - t0;
+  if (lo >= hi) return;  // a page past the new tokens (the whole workgroup)
+  const int page = p.page_table[(size_t)b * p.max_pages + page_idx];
+  uint8_t* blk = p.pool + block_offset(page, h, p.num_pages, block_bytes_int4(D));
+  const bool partial = lo > 0 || hi < kPageTokens;
+
+  // threads D/2 .. D-1 store V dims 2j, 2j + 1 (j = tid - D/2): the old
+  // columns of a partial page first, so that their latency overlaps the work
+  const bool vstore = tid >= D / 2 && tid < D;
+  uint4 vold = uint4{0u, 0u, 0u, 0u};
+  if (partial && vstore) vold = *(const uint4*)(blk + (size_t)8 * D + (size_t)(tid - D / 2) * 16);
+
+  const int c = lane % L, g = lane / L;
+  const int t = g * W + w;  // this group's slot
+  // a slot outside the new range reads the nearest new row (its codes are
+  // never stored), so every address stays inside the inputs
+  const uint32_t srow = (uint32_t)min(max(t0 + t - start, 0), p.s_new - 1);
+  const size_t row0 = ((size_t)b * p.s_new * p.kv_heads + h) * D * ESZ;  // (b, token 0, h)
+  const uint8_t* kbase = (const uint8_t*)p.k + row0;
+  const uint8_t* vbase = (const uint8_t*)p.v + row0;
+  const uint32_t off = (srow * (uint32_t)p.kv_heads * D + 4 * c) * ESZ;  // bytes
+  float xa[4], xb[4], va[4], vb[4];
+  load4<BF16>(kbase, off, xa);
+  load4<BF16>(kbase, off + HALF * ESZ, xb);
+  load4<BF16>(vbase, off, va);
+  load4<BF16>(vbase, off + HALF * ESZ, vb);
+  const uint8_t* cos0 = (const uint8_t*)(p.cos_cache + (size_t)start * HALF);
+  const uint8_t* sin0 = (const uint8_t*)(p.sin_cache + (size_t)start * HALF);
+  if constexpr (ROPE == 1) {
+    const uint32_t o = (srow * HALF + 4 * c) * 4;
+    const float4 cv = *(const float4*)(cos0 + o);
+    const float4 sv = *(const float4*)(sin0 + o);
+    const float ca[4] = {cv.x, cv.y, cv.z, cv.w}, sa[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x0 = xa[j], x1 = xb[j];
+      xa[j] = rope_pair_elem(ca[j], sa[j], x0, x1, true);
+      xb[j] = rope_pair_elem(ca[j], sa[j], x1, x0, false);
+    }
+  } else if constexpr (ROPE == 2) {
+    const uint32_t o = (srow * HALF + 2 * c) * 4;
+    const float2 c0 = *(const float2*)(cos0 + o);
+    const float2 s0 = *(const float2*)(sin0 + o);
+    const float2 c1 = *(const float2*)(cos0 + o + HALF * 2);
+    const float2 s1 = *(const float2*)(sin0 + o + HALF * 2);
+    const float ca[2] = {c0.x, c0.y}, sa[2] = {s0.x, s0.y};
+    const float cb[2] = {c1.x, c1.y}, sb[2] = {s1.x, s1.y};
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float x0 = xa[2 * e], x1 = xa[2 * e + 1];
+      xa[2 * e] = rope_pair_elem(ca[e], sa[e], x0, x1, true);
+      xa[2 * e + 1] = rope_pair_elem(ca[e], sa[e], x1, x0, false);
+      x0 = xb[2 * e], x1 = xb[2 * e + 1];
+      xb[2 * e] = rope_pair_elem(cb[e], sb[e], x0, x1, true);
+      xb[2 * e + 1] = rope_pair_elem(cb[e], sb[e], x1, x0, false);
+    }
+  }
+  uint32_t pka, pkb, pva, pvb;  // (scale, zero) of the groups of xa, xb, va, vb
+  const uint32_t ka = quant4_int4(xa, pka), kb = quant4_int4(xb, pkb);
+  const uint32_t qa = quant4_int4(va, pva), qb = quant4_int4(vb, pvb);
+
+  __shared__ __align__(16) uint8_t sm_k[kPageTokens * KS];
+  __shared__ __align__(16) uint8_t sm_v[kPageTokens * D];      // column d at 16 d, one byte per slot
+  __shared__ __align__(16) uint32_t sm_p[2][kPageTokens][NG];  // K, V (scale, zero) per slot
+  // K: the 4 codes of dims 4c.. (already nibbles, LSB first) are bytes 2c,
+  // 2c + 1 of the row; those of D/2 + 4c.. bytes D/4 + 2c, + 1
+  *(uint16_t*)&sm_k[t * KS + 2 * c] = (uint16_t)ka;
+  *(uint16_t*)&sm_k[t * KS + D / 4 + 2 * c] = (uint16_t)kb;
+  uint8_t* vcol = &sm_v[64 * c + t];  // dim 4c, slot t
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    vcol[16 * j] = (uint8_t)((qa >> (4 * j)) & 0xFu);
+    vcol[16 * (HALF + j)] = (uint8_t)((qb >> (4 * j)) & 0xFu);
+  }
+  if ((c & 7) == 0) {  // the group's first lane: groups c/8 and NG/2 + c/8
+    sm_p[0][t][c / 8] = pka;
+    sm_p[0][t][NG / 2 + c / 8] = pkb;
+    sm_p[1][t][c / 8] = pva;
+    sm_p[1][t][NG / 2 + c / 8] = pvb;
+  }
+  __syncthreads();
+
+  if (tid < D / 2) {
+    // K: 16-byte piece tid of the 16 rows (D/32 per row), stored when its row is new
+    constexpr int CHUNKS = D / 32;
+    const int tr = tid / CHUNKS;
+    const uint4 v = *(const uint4*)&sm_k[tr * KS + 16 * (tid % CHUNKS)];
+    if (tr >= lo && tr < hi) *(uint4*)(blk + (size_t)tid * 16) = v;
+  } else if (vstore) {
+    // V: dims 2j, 2j + 1 (16 contiguous bytes), new slots from the tile, on a
+    // partial page the other nibbles kept
+    const int j = tid - D / 2;
+    const uint2 c0 = pack_column(*(const uint4*)&sm_v[16 * (2 * j)]);
+    const uint2 c1 = pack_column(*(const uint4*)&sm_v[16 * (2 * j + 1)]);
+    uint4 v = uint4{c0.x, c0.y, c1.x, c1.y};
+    if (partial) {
+      // nibble s of a column's 64 bits is slot s: 0xF where the slot keeps its code
+      const uint32_t fresh = (1u << hi) - (1u << lo);  // slots lo .. hi-1
+      uint32_t keep[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t bits = (~fresh >> (8 * q)) & 0xFFu;  // slots 8q .. 8q+7
+        uint32_t m = 0u;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) m |= ((bits >> k) & 1u) * (0xFu << (4 * k));
+        keep[q] = m;
+      }
+      v.x = (v.x & ~keep[0]) | (vold.x & keep[0]);
+      v.y = (v.y & ~keep[1]) | (vold.y & keep[1]);
+      v.z = (v.z & ~keep[0]) | (vold.z & keep[0]);
+      v.w = (v.w & ~keep[1]) | (vold.w & keep[1]);
+    }
+    *(uint4*)(blk + (size_t)8 * D + (size_t)j * 16) = v;
+  } else if (tid < D + 2 * kPageTokens * PPS) {
+    // (scale, zero) pairs: K then V, PB-byte pieces, PPS per slot
+    const int i = tid - D;
+    const int which = i / (kPageTokens * PPS);
+    const int slot = (i % (kPageTokens * PPS)) / PPS;
+    const int piece = i % PPS;
+    uint8_t* dst = blk + 16 * D + 64 * NG * which + (size_t)slot * (D / 8) + piece * PB;
+    const uint8_t* src = (const uint8_t*)&sm_p[which][slot][0] + piece * PB;
+    if (slot >= lo && slot < hi) {
+      if constexpr (PB == 16)
+        *(uint4*)dst = *(const uint4*)src;
+      else
+        *(uint2*)dst = *(const uint2*)src;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- int4 ----
 // One wave per (b, token pair, h): the two tokens of a pair share the bytes of
 // the dim-major V block, so one wave owns both nibbles of every byte it
@@ -411,6 +633,24 @@ void launch_page_int8(dim3 grid, hipStream_t st, const AppendParams& p, bool bf,
     launch_page_int8_dt<D, false>(grid, st, p, rope);
 }
 
+template <int D, bool BF16>
+void launch_page_int4_dt(dim3 grid, hipStream_t st, const AppendParams& p, int rope) {
+  if (rope == 0)
+    hipLaunchKernelGGL((kv_append_page_int4_kernel<D, BF16, 0>), grid, dim3(2 * D), 0, st, p);
+  else if (rope == 1)
+    hipLaunchKernelGGL((kv_append_page_int4_kernel<D, BF16, 1>), grid, dim3(2 * D), 0, st, p);
+  else
+    hipLaunchKernelGGL((kv_append_page_int4_kernel<D, BF16, 2>), grid, dim3(2 * D), 0, st, p);
+}
+
+template <int D>
+void launch_page_int4(dim3 grid, hipStream_t st, const AppendParams& p, bool bf, int rope) {
+  if (bf)
+    launch_page_int4_dt<D, true>(grid, st, p, rope);
+  else
+    launch_page_int4_dt<D, false>(grid, st, p, rope);
+}
+
 }  // namespace
 
 hipError_t launch_kv_append(const AppendParams& p, int head_dim, int quant, hipStream_t st) {
@@ -423,19 +663,24 @@ hipError_t launch_kv_append(const AppendParams& p, int head_dim, int quant, hipS
   const int pages = p.pages > 0 ? p.pages : (p.s_new + kPageTokens - 1) / kPageTokens + 1;
   const bool fits = pages <= 65535 && p.batch <= 65535 &&
                     (long)p.s_new * p.kv_heads * head_dim * 4 < (1L << 31);
-  if (quant == kQuantInt8 && p.s_new >= kPageAppendMin && aligned && fits) {
+  if (p.s_new >= kPageAppendMin && aligned && fits && (quant == kQuantInt8 || quant == kQuantInt4)) {
     const dim3 grid((unsigned)p.kv_heads, (unsigned)pages, (unsigned)p.batch);
     const bool bf = p.dtype == kDtypeBf16;
     const int rope = !p.do_rotary ? 0 : (p.interleaved ? 2 : 1);
-    if (head_dim == 64)
-      launch_page_int8<64>(grid, st, p, bf, rope);
-    else if (head_dim == 128)
-      launch_page_int8<128>(grid, st, p, bf, rope);
-    else if (head_dim == 256)
-      launch_page_int8<256>(grid, st, p, bf, rope);
-    else
-      return hipErrorInvalidValue;
-    return hipGetLastError();
+    auto by_dim = [&](auto launch64, auto launch128, auto launch256) {
+      if (head_dim == 64)
+        launch64(grid, st, p, bf, rope);
+      else if (head_dim == 128)
+        launch128(grid, st, p, bf, rope);
+      else if (head_dim == 256)
+        launch256(grid, st, p, bf, rope);
+      else
+        return hipErrorInvalidValue;
+      return hipGetLastError();
+    };
+    if (quant == kQuantInt8)
+      return by_dim(launch_page_int8<64>, launch_page_int8<128>, launch_page_int8<256>);
+    return by_dim(launch_page_int4<64>, launch_page_int4<128>, launch_page_int4<256>);
   }
   if (quant == kQuantInt8) {
     const long rows = (long)p.batch * p.s_new * p.kv_heads;

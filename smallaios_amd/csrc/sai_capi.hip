@@ -31,6 +31,7 @@ struct sai_ctx {
   int32_t decode_merge = 2;  // 0: combine kernel, 1: in-kernel merge, 2: automatic
   int32_t last_wg = 0;
   int32_t last_split = 0;
+  int32_t last_launches = 0;  // kernels of the last decode call (decode, + combine)
   // decode-kernel timing ring: event pairs of the last `slots` calls
   std::vector<hipEvent_t> ev_start, ev_end;
   int64_t timed_calls = 0;
@@ -48,6 +49,10 @@ struct DecodeWorkspace {
   size_t seq_info_n = 0;
   int32_t* counters = nullptr;
   size_t counter_n = 0;
+  // prefill: one large-V flag per workgroup (zero between launches: the
+  // precise pass clears what the fast pass set)
+  int32_t* prec_flags = nullptr;
+  size_t prec_flags_n = 0;
 };
 
 // Scratch of sai_gqa_with_cache_noalloc, for callers that cannot allocate
@@ -232,7 +237,26 @@ void release_workspace(DecodeWorkspace& w) {
   if (w.partials) (void)hipFree(w.partials);
   if (w.seq_info) (void)hipFree(w.seq_info);
   if (w.counters) (void)hipFree(w.counters);
+  if (w.prec_flags) (void)hipFree(w.prec_flags);
   w = DecodeWorkspace{};
+}
+
+// Grows the prefill flags to n (zeroed, after the device is idle).
+sai_status reserve_prec_flags(sai_ctx* ctx, DecodeWorkspace& w, size_t n) {
+  if (n <= w.prec_flags_n) return SAI_OK;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(ctx, e, "prefill flags: sync");
+  if (w.prec_flags) (void)hipFree(w.prec_flags);
+  w.prec_flags = nullptr;
+  w.prec_flags_n = 0;
+  e = hipMalloc(&w.prec_flags, n * sizeof(int32_t));
+  if (e != hipSuccess) return fail(ctx, SAI_ERR_ALLOC, "prefill flags: %s", hipGetErrorString(e));
+  e = hipMemset(w.prec_flags, 0, n * sizeof(int32_t));
+  if (e != hipSuccess) return hip_fail(ctx, e, "prefill flags memset");
+  e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(ctx, e, "prefill flags: sync");
+  w.prec_flags_n = n;
+  return SAI_OK;
 }
 
 // Grows w to hold at least the given sizes. A buffer that must grow is freed
@@ -421,6 +445,10 @@ SAI_API sai_status sai_last_decode_shape(const sai_ctx* ctx, int32_t* workgroups
   if (workgroups) *workgroups = ctx->last_wg;
   if (split_tokens) *split_tokens = ctx->last_split;
   return SAI_OK;
+}
+
+SAI_API int32_t sai_last_decode_launches(const sai_ctx* ctx) {
+  return ctx ? ctx->last_launches : 0;
 }
 
 // ------------------------------------------------------------------ cache ---
@@ -720,8 +748,11 @@ namespace {
 sai_status attention_common(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
                             int32_t dtype, int32_t batch, int32_t sq, int32_t num_heads,
                             const float* cos_cache, const float* sin_cache, int32_t cache_rows,
-                            int32_t do_rotary, float* out, const char* op, int32_t* group) {
+                            int32_t do_rotary, const void* out, int32_t out_dtype,
+                            const char* op, int32_t* group) {
   if (!q || !out) return fail(ctx, SAI_ERR_NULL, "%s: missing query/output", op);
+  if (out_dtype != SAI_DTYPE_F32 && out_dtype != SAI_DTYPE_BF16)
+    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: output dtype %d (want f32 or bf16)", op, out_dtype);
   if (layer < 0 || layer >= c->desc.num_layers)
     return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: layer_idx %d", op, layer);
   if (dtype != SAI_DTYPE_F32 && dtype != SAI_DTYPE_BF16)
@@ -757,8 +788,9 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
                          int32_t dtype, int32_t batch, int32_t G, const float* cos_cache,
                          const float* sin_cache, int32_t cache_rows, int32_t do_rotary,
                          int32_t rotary_interleaved, int32_t has_scale, float scale,
-                         int32_t window, float* out, const void* k_new, const void* v_new,
-                         int32_t kv_dtype, void* stream, DecodeWorkspace* fixed_ws = nullptr) {
+                         int32_t window, void* out, int32_t out_dtype, const void* k_new,
+                         const void* v_new, int32_t kv_dtype, void* stream,
+                         DecodeWorkspace* fixed_ws = nullptr) {
   const char* op = "gqa_decode";
   const int32_t W = visible_span(c->layer_window[layer], window);
   const int D = c->desc.head_dim;
@@ -830,6 +862,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   p.q = q;
   p.q_dtype = dtype;
   p.out = out;
+  p.out_bf16 = out_dtype == SAI_DTYPE_BF16 ? 1 : 0;
   p.pool = c->pools[layer];
   p.kv_heads = kvh;
   p.num_pages = c->desc.num_pages;
@@ -857,6 +890,22 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   // 8k, int8, and at 4 x 32k, int4); ragged batches use the combine kernel
   // (measured faster there).
   p.merge_in_kernel = ctx->decode_merge == 1 || (ctx->decode_merge == 2 && uniform);
+  // ragged: work items go to the sequences with the longest splits first
+  // (each sequence's tiles are dealt evenly to its splits, so this orders the
+  // work items longest first), which the in-order dispatch of workgroups to
+  // CUs then balances as a longest-processing-time list schedule
+  p.ordered = 0;
+  if (!uniform && batch <= sai::kDecodeOrder) {
+    std::vector<std::pair<int64_t, int>> key((size_t)batch);
+    for (int b = 0; b < batch; ++b) {
+      const int64_t tiles = (streamed(b) + 63) / 64;
+      const int64_t n = (streamed(b) + split - 1) / split;
+      key[b] = {-((tiles + n - 1) / n), b};
+    }
+    std::stable_sort(key.begin(), key.end());
+    for (int i = 0; i < batch; ++i) p.order[i] = (uint16_t)key[i].second;
+    p.ordered = 1;
+  }
   p.counters = ws->counters;
   p.k_new = k_new;
   p.v_new = v_new;
@@ -883,6 +932,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   }
   ctx->last_wg = (int32_t)(work * kvh);
   ctx->last_split = split;
+  ctx->last_launches = (multi && !p.merge_in_kernel) ? 2 : 1;
   return SAI_OK;
 }
 
@@ -893,15 +943,16 @@ SAI_API sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, c
                                   const float* cos_cache, const float* sin_cache,
                                   int32_t cache_rows, int32_t do_rotary,
                                   int32_t rotary_interleaved, int32_t has_scale, float scale,
-                                  int32_t window, float* out, void* stream) {
+                                  int32_t window, void* out, int32_t out_dtype, void* stream) {
   if (!ctx || !c) return SAI_ERR_NULL;
   int32_t G = 0;
   sai_status st = attention_common(ctx, c, layer, q, dtype, batch, 1, num_heads, cos_cache,
-                                   sin_cache, cache_rows, do_rotary, out, "gqa_decode", &G);
+                                   sin_cache, cache_rows, do_rotary, out, out_dtype, "gqa_decode",
+                                   &G);
   if (st != SAI_OK) return st;
   return launch_decode(ctx, c, layer, q, dtype, batch, G, cos_cache, sin_cache, cache_rows,
-                       do_rotary, rotary_interleaved, has_scale, scale, window, out, nullptr,
-                       nullptr, SAI_DTYPE_F32, stream);
+                       do_rotary, rotary_interleaved, has_scale, scale, window, out, out_dtype,
+                       nullptr, nullptr, SAI_DTYPE_F32, stream);
 }
 
 namespace {
@@ -911,8 +962,9 @@ sai_status gqa_with_cache_impl(sai_ctx* ctx, sai_kvcache* c, int32_t layer, cons
                                int32_t kv_dtype, int32_t batch, int32_t num_heads,
                                const float* cos_cache, const float* sin_cache,
                                int32_t cache_rows, int32_t do_rotary, int32_t rotary_interleaved,
-                               int32_t has_scale, float scale, int32_t window, float* out,
-                               void* stream, const char* op, DecodeWorkspace* fixed_ws) {
+                               int32_t has_scale, float scale, int32_t window, void* out,
+                               int32_t out_dtype, void* stream, const char* op,
+                               DecodeWorkspace* fixed_ws) {
   if (!k_new || !v_new) return fail(ctx, SAI_ERR_NULL, "%s: missing key/value", op);
   if (kv_dtype != SAI_DTYPE_F32 && kv_dtype != SAI_DTYPE_BF16)
     return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: dtype %d (want f32 or bf16)", op, kv_dtype);
@@ -924,11 +976,11 @@ sai_status gqa_with_cache_impl(sai_ctx* ctx, sai_kvcache* c, int32_t layer, cons
   c->pending = 1;
   int32_t G = 0;
   sai_status st = attention_common(ctx, c, layer, q, q_dtype, batch, 1, num_heads, cos_cache,
-                                   sin_cache, cache_rows, do_rotary, out, op, &G);
+                                   sin_cache, cache_rows, do_rotary, out, out_dtype, op, &G);
   if (st == SAI_OK)
     st = launch_decode(ctx, c, layer, q, q_dtype, batch, G, cos_cache, sin_cache, cache_rows,
-                       do_rotary, rotary_interleaved, has_scale, scale, window, out, k_new,
-                       v_new, kv_dtype, stream, fixed_ws);
+                       do_rotary, rotary_interleaved, has_scale, scale, window, out, out_dtype,
+                       k_new, v_new, kv_dtype, stream, fixed_ws);
   if (st != SAI_OK) c->pending = prev_pending;
   return st;
 }
@@ -941,12 +993,13 @@ SAI_API sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* c, int32_t laye
                                       int32_t num_heads, const float* cos_cache,
                                       const float* sin_cache, int32_t cache_rows,
                                       int32_t do_rotary, int32_t rotary_interleaved,
-                                      int32_t has_scale, float scale, int32_t window, float* out,
-                                      void* stream) {
+                                      int32_t has_scale, float scale, int32_t window, void* out,
+                                      int32_t out_dtype, void* stream) {
   if (!ctx || !c) return SAI_ERR_NULL;
   return gqa_with_cache_impl(ctx, c, layer, q, q_dtype, k_new, v_new, kv_dtype, batch, num_heads,
                              cos_cache, sin_cache, cache_rows, do_rotary, rotary_interleaved,
-                             has_scale, scale, window, out, stream, "gqa_with_cache", nullptr);
+                             has_scale, scale, window, out, out_dtype, stream, "gqa_with_cache",
+                             nullptr);
 }
 
 SAI_API sai_status sai_gqa_with_cache_noalloc(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
@@ -956,7 +1009,7 @@ SAI_API sai_status sai_gqa_with_cache_noalloc(sai_ctx* ctx, sai_kvcache* c, int3
                                               const float* sin_cache, int32_t cache_rows,
                                               int32_t do_rotary, int32_t rotary_interleaved,
                                               int32_t has_scale, float scale, int32_t window,
-                                              float* out, void* stream) {
+                                              void* out, int32_t out_dtype, void* stream) {
   if (!ctx || !c) return SAI_ERR_NULL;
   const char* op = "gqa_with_cache_noalloc";
   void* base = nullptr;
@@ -967,8 +1020,10 @@ SAI_API sai_status sai_gqa_with_cache_noalloc(sai_ctx* ctx, sai_kvcache* c, int3
   if (!base)
     return fail(ctx, SAI_ERR_HIP, "%s: the device scratch of device %d is not set up", op,
                 ctx->device);
-  // counters, then split ranges, then partials (the counters' region was
-  // cleared when the scratch was set up and is left at zero by every launch)
+  // counters, then split ranges, then partials. Every launch that merges
+  // in-kernel leaves its counters at zero; they are cleared again on the
+  // caller's stream before each call anyway, so that what an overlapping
+  // (racing) call left behind cannot reach a later one.
   DecodeWorkspace ws;
   ws.counters = (int32_t*)base;
   ws.counter_n = kScratchCounters;
@@ -976,9 +1031,15 @@ SAI_API sai_status sai_gqa_with_cache_noalloc(sai_ctx* ctx, sai_kvcache* c, int3
   ws.seq_info_n = kScratchSeqInfo;
   ws.partials = (float*)((int32_t*)base + kScratchCounters + kScratchSeqInfo);
   ws.partial_floats = kScratchPartialFloats;
+  if (batch > 0 && (size_t)batch * c->desc.num_kv_heads <= kScratchCounters) {
+    DeviceGuard dg(ctx->device);
+    const hipError_t e = sai::launch_fill_i32(ws.counters, (size_t)batch * c->desc.num_kv_heads,
+                                              0, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "gqa_with_cache_noalloc: counter clear");
+  }
   return gqa_with_cache_impl(ctx, c, layer, q, q_dtype, k_new, v_new, kv_dtype, batch, num_heads,
                              cos_cache, sin_cache, cache_rows, do_rotary, rotary_interleaved,
-                             has_scale, scale, window, out, stream, op, &ws);
+                             has_scale, scale, window, out, out_dtype, stream, op, &ws);
 }
 
 SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void* q,
@@ -986,13 +1047,13 @@ SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, 
                                    const float* cos_cache, const float* sin_cache,
                                    int32_t cache_rows, int32_t do_rotary,
                                    int32_t rotary_interleaved, int32_t has_scale, float scale,
-                                   int32_t window, float* out, void* stream) {
+                                   int32_t window, void* out, int32_t out_dtype, void* stream) {
   if (!ctx || !c) return SAI_ERR_NULL;
   const char* op = "gqa_prefill";
   if (sq <= 0) return fail(ctx, SAI_ERR_SHAPE_MISMATCH, "%s: sq must be > 0", op);
   int32_t G = 0;
   sai_status st = attention_common(ctx, c, layer, q, dtype, batch, sq, num_heads, cos_cache,
-                                   sin_cache, cache_rows, do_rotary, out, op, &G);
+                                   sin_cache, cache_rows, do_rotary, out, out_dtype, op, &G);
   if (st != SAI_OK) return st;
   const int D = c->desc.head_dim;
   DeviceGuard dg(ctx->device);
@@ -1000,6 +1061,7 @@ SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, 
   p.q = q;
   p.q_dtype = dtype;
   p.out = out;
+  p.out_bf16 = out_dtype == SAI_DTYPE_BF16 ? 1 : 0;
   p.pool = c->pools[layer];
   p.kv_heads = c->desc.num_kv_heads;
   p.num_pages = c->desc.num_pages;
@@ -1016,6 +1078,9 @@ SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, 
   const float sc = has_scale ? scale : sai_default_scale(D);
   p.scale_log2 = sc * 1.4426950408889634f;
   p.window = visible_span(c->layer_window[layer], window);
+  st = reserve_prec_flags(ctx, c->ws, sai::prefill_workgroups(p, D, G));
+  if (st != SAI_OK) return st;
+  p.prec_flags = c->ws.prec_flags;
   hipError_t e = sai::launch_gqa_prefill(p, D, G, c->desc.quant, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gqa_prefill launch");
   return SAI_OK;

@@ -64,6 +64,22 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
 
+// f32 -> bf16 bits, round to nearest even; a NaN stays a quiet NaN of the same
+// sign (f32_to_bf16, onnx-rt/src/tensor.rs:312-329).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float v) {
+  const uint32_t bits = __float_as_uint(v);
+  if (v != v) return (uint16_t)((bits >> 16) | 0x0040u);
+  return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
+}
+
+// Element idx of an attention output of f32, or of bf16 when out_bf16.
+__device__ __forceinline__ void store_out(void* out, size_t idx, float v, int out_bf16) {
+  if (out_bf16)
+    ((uint16_t*)out)[idx] = f32_to_bf16_rne(v);
+  else
+    ((float*)out)[idx] = v;
+}
+
 // Element i of a row stored as f32 or bf16.
 // Element i of an f32 or bf16 row (base 4-byte aligned). Branch-free: one
 // dword load for either type, so a run of these issues back to back instead
@@ -107,10 +123,15 @@ struct AppendParams {
   int pages;
 };
 
+// Sequences whose work items a ragged decode launch can order (longest
+// splits first); the order rides in the kernel arguments.
+constexpr int kDecodeOrder = 256;
+
 struct DecodeParams {
   const void* q;  // [batch, 1, Hq*D]
   int q_dtype;
-  float* out;  // [batch, 1, Hq*D]
+  void* out;     // [batch, 1, Hq*D], f32 or (out_bf16) bf16
+  int out_bf16;
   const uint8_t* pool;
   int kv_heads, num_pages;
   const int32_t* seq_lens;  // device [batch] committed
@@ -134,12 +155,18 @@ struct DecodeParams {
   const void* v_new;
   int kv_dtype;
   int window;           // visible keys per query (0: all); see window_first_key
+  // ragged launches (uniform_nsplit == 0) with batch <= kDecodeOrder: work
+  // items go to the sequences in this order (ordered != 0), each sequence's
+  // splits in turn
+  int ordered;
+  uint16_t order[kDecodeOrder];
 };
 
 struct PrefillParams {
   const void* q;  // [batch, sq, Hq*D]
   int q_dtype;
-  float* out;  // [batch, sq, Hq*D]
+  void* out;     // [batch, sq, Hq*D], f32 or (out_bf16) bf16
+  int out_bf16;
   const uint8_t* pool;
   int kv_heads, num_pages;
   const int32_t* seq_lens;  // committed; total = seq_lens[b] + sq, queries at seq_lens[b] + i
@@ -152,6 +179,9 @@ struct PrefillParams {
   int cache_rows, do_rotary, interleaved;
   float scale_log2;
   int window;  // visible keys per query (0: all)
+  // one int per workgroup (prefill_workgroups), zero between launches: the
+  // int8 fast pass flags the workgroups the precise pass recomputes
+  int32_t* prec_flags;
 };
 
 // Sliding windows: a query at position L-1 sees keys [L - W, L-1] (W > 0)
@@ -260,6 +290,9 @@ hipError_t launch_tq_read(const TqArgs& a, int b, int h, int start, int len, flo
 hipError_t launch_tq_attend(const TqArgs& a, const TqAttendArgs& t, int mode, int group,
                             int nsplit, int batch, hipStream_t st);
 hipError_t launch_copy_rows(const CopyRowsArgs& a, int chunk_bytes, hipStream_t st);
+// p[0, n) = v on the stream (a kernel, so that graph capture records no memset
+// node; copy_rows.hip).
+hipError_t launch_fill_i32(int32_t* p, size_t n, int32_t v, hipStream_t st);
 // Standalone RoPE (rotary.hip): x/y f32 or bf16, tables f32 or bf16.
 hipError_t launch_rotary(const RotaryArgs& a, bool x_bf16, bool table_bf16, bool interleaved,
                          hipStream_t st);
@@ -272,6 +305,8 @@ hipError_t launch_gqa_decode(const DecodeParams& p, int head_dim, int group, int
                              int work_items, bool combine, hipStream_t s);
 hipError_t launch_gqa_prefill(const PrefillParams& p, int head_dim, int group, int quant,
                               hipStream_t s);
+// Workgroups of one prefill launch (the size of PrefillParams::prec_flags).
+size_t prefill_workgroups(const PrefillParams& p, int head_dim, int group);
 // Split-partial merge of the decode kernels (gqa_decode.hip).
 hipError_t launch_decode_combine(const DecodeParams& p, int head_dim, int group, hipStream_t st);
 // int4 decode (gqa_decode_int4.hip): head_dim 128; merges through the combine

@@ -664,8 +664,11 @@ Result<DeviceTensor, OpError> gqa_over_cache(RocmRuntime& rt, GpuKvCache& cache,
                                              const std::string& prefix) {
   if (g.kv_heads != cache.num_kv_heads() || g.head_dim != cache.head_dim())
     return OpError::shape(prefix + "K/V heads or head_dim differ from the cache's");
+  // attn_out takes Q's dtype, as the reference's GPU attention does
+  // (gpu_gqa's dt = q.dtype and its bf16 PV GEMM + gqa_merge_heads_bf16,
+  // cuda/kernels/attention.rs:835, :877-901, :495-520)
   auto out = DeviceTensor::alloc({(int64_t)g.batch, (int64_t)g.seq, (int64_t)g.q_hidden},
-                                 DataType::Float);
+                                 q.dtype);
   if (!out) return OpError::internal(prefix + out.error().to_string());
   if (g.batch == 0 || g.seq == 0) return std::move(out).value();
   const float* cs = rope ? rope->cos : nullptr;
@@ -681,14 +684,15 @@ Result<DeviceTensor, OpError> gqa_over_cache(RocmRuntime& rt, GpuKvCache& cache,
                              ? (int32_t)std::min<int64_t>(a.local_window_size,
                                                           std::numeric_limits<int32_t>::max())
                              : 0;
-  float* o = (float*)out.value().buffer.as_ptr();
+  void* o = out.value().buffer.as_ptr();
+  const int32_t odt = sai_dtype(q.dtype);
   if (g.seq == 1) {
     auto ck = cache.check_append(g.batch, 1);
     if (!ck) return OpError::internal(prefix + ck.error().to_string());
     const sai_status st = sai_gqa_with_cache(
         rt.raw(), cache.raw(), (int32_t)layer, q.buffer.as_ptr(), sai_dtype(q.dtype),
         k.buffer.as_ptr(), v.buffer.as_ptr(), sai_dtype(k.dtype), (int32_t)g.batch,
-        (int32_t)g.num_heads, cs, sn, rows, rot, il, has_scale, scale, window, o, nullptr);
+        (int32_t)g.num_heads, cs, sn, rows, rot, il, has_scale, scale, window, o, odt, nullptr);
     if (st != SAI_OK) return from_status(st, prefix, rt);
     return std::move(out).value();
   }
@@ -697,7 +701,7 @@ Result<DeviceTensor, OpError> gqa_over_cache(RocmRuntime& rt, GpuKvCache& cache,
   const sai_status st = sai_gqa_prefill(rt.raw(), cache.raw(), (int32_t)layer, q.buffer.as_ptr(),
                                         sai_dtype(q.dtype), (int32_t)g.batch, (int32_t)g.seq,
                                         (int32_t)g.num_heads, cs, sn, rows, rot, il, has_scale,
-                                        scale, window, o, nullptr);
+                                        scale, window, o, odt, nullptr);
   if (st != SAI_OK) return from_status(st, prefix, rt);
   return std::move(out).value();
 }
@@ -757,7 +761,7 @@ Result<std::vector<DeviceTensor>, OpError> dispatch_gqa(
   const std::string prefix = "ROCm GroupQueryAttention: ";
   if (g.batch == 0 || g.seq == 0) {
     auto out = DeviceTensor::alloc({(int64_t)g.batch, (int64_t)g.seq, (int64_t)g.q_hidden},
-                                   DataType::Float);
+                                   q.dtype);
     if (!out) return OpError::internal(prefix + out.error().to_string());
     std::vector<DeviceTensor> outs;
     outs.push_back(std::move(out).value());

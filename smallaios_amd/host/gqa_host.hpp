@@ -372,8 +372,9 @@ Result<GqaShape, OpError> gqa_validate(const std::vector<int64_t>& q_shape,
 // gpu_executor.rs:944-970. Inputs by slot: 0 query, 1 key, 2 value, 3/4
 // past_key/past_value (unused: the cache holds the past), 5/6 seqlens_k /
 // total_sequence_length (advisory, unused as on the CPU), 7 cos_cache,
-// 8 sin_cache. Returns { attn_out [B, S, Hq*D] f32 }; present K/V stay in the
-// cache. With kv_cache_ctx, the node uses layer next_layer_idx (then
+// 8 sin_cache. Returns { attn_out [B, S, Hq*D] } in Q's dtype (f32, or bf16
+// rounded to nearest even, as gpu_gqa returns, attention.rs:835, :877-901);
+// present K/V stay in the cache. With kv_cache_ctx, the node uses layer next_layer_idx (then
 // incremented, also on error, as in the reference); S = 1 runs the fused
 // append + split-K decode, S > 1 appends S tokens then runs the prefill
 // kernel. Without kv_cache_ctx the node attends over its own K/V only

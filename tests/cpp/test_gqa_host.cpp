@@ -116,6 +116,31 @@ void close(const std::vector<float>& got, const std::vector<float>& want, const 
   }
 }
 
+// A bf16 attention output against the f32 oracle: the same bar widened by
+// bf16's round-to-nearest (2^-9 of the value, on both sides).
+void close_bf16(const std::vector<float>& got, const std::vector<float>& want, const char* what) {
+  REQUIRE(got.size() == want.size(), "%s: %zu vs %zu elements", what, got.size(), want.size());
+  for (size_t i = 0; i < got.size(); ++i) {
+    const float tol = 2e-3f + (1e-2f + 1.0f / 256.0f) * std::fabs(want[i]);
+    REQUIRE(std::isfinite(got[i]) && std::fabs(got[i] - want[i]) <= tol,
+            "%s: element %zu got %.7g want %.7g", what, i, got[i], want[i]);
+  }
+}
+
+// The values of an f32 or bf16 device tensor, as f32.
+std::vector<float> host_values(const DeviceTensor& t) {
+  if (t.dtype == DataType::Float) return must(t.to_host_f32(), "to_host_f32");
+  REQUIRE(t.dtype == DataType::BFloat16, "dtype %d", (int)t.dtype);
+  const std::vector<uint8_t> raw = must(t.to_host(), "to_host");
+  std::vector<float> v(raw.size() / 2);
+  for (size_t i = 0; i < v.size(); ++i) {
+    uint16_t b;
+    std::memcpy(&b, raw.data() + 2 * i, 2);
+    v[i] = sai_or_bf16_to_f32(b);
+  }
+  return v;
+}
+
 // ------------------------------------------------------------- CPU cases ---
 void cpu_attrs() {
   GqaAttrs d = parse_gqa_attrs({});
@@ -853,7 +878,9 @@ static void session(KvQuant quant, bool bf16, int B, int Hq, int Hkv, int D, int
                                     attrs, &ctx),
                        "dispatch_gqa");
       REQUIRE(ctx.next_layer_idx == (size_t)layer + 1, "layer counter");
-      std::vector<float> got = must(outs[0].to_host_f32(), "download");
+      // attn_out in Q's dtype (gpu_gqa: dt = q.dtype, attention.rs:835)
+      REQUIRE(outs[0].dtype == (bf16 ? DataType::BFloat16 : DataType::Float), "attn_out dtype");
+      std::vector<float> got = host_values(outs[0]);
       // oracle
       Logical& l = lc[layer];
       std::vector<int32_t> start(B, pos), lens(B, pos + S);
@@ -875,7 +902,10 @@ static void session(KvQuant quant, bool bf16, int B, int Hq, int Hkv, int D, int
               "oracle gqa");
       char what[96];
       std::snprintf(what, sizeof what, "pass %d layer %d output", pass, layer);
-      close(got, want, what);
+      if (bf16)
+        close_bf16(got, want, what);
+      else
+        close(got, want, what);
       // the cache holds exactly the oracle's codes: dequantised values agree bit for bit
       for (int b = 0; b < B; ++b)
         for (int h = 0; h < Hkv; ++h) {
@@ -1226,6 +1256,100 @@ void gemma_graph_session(int Hq, int Hkv, int D, double theta, uint64_t seed) {
 
 void gpu_session_gemma_graph() { gemma_graph_session(8, 2, 128, 10000.0, 61); }
 
+// A bf16 graph whose attention outputs feed the next layer: layer l's
+// RotaryEmbedding takes attn(l-1) as its x. attn_out comes back in Q's
+// dtype (bf16, as gpu_gqa returns it, attention.rs:835 and :877-901), which
+// is what a bf16 consumer needs: the reference's next op, the bf16 o_proj
+// GEMM, takes only bf16 x bf16 (pick_gemm_dtype, gpu_executor.rs:1024-1031),
+// and the RotaryEmbedding node here takes it unchanged. Each layer is checked
+// against the oracle from the input the GPU actually fed it (the previous
+// layer's bf16 output): RoPE bit for bit after rounding to bf16, attention
+// within the bf16-widened tolerance, over a prefill pass and decode passes.
+void gpu_session_bf16_chain() {
+  const int L = 3, B = 2, Hq = 8, Hkv = 2, D = 128, rows = 96, T = 64;
+  SessionConfig cfg;
+  cfg.num_hidden_layers = L;
+  cfg.num_key_value_heads = Hkv;
+  cfg.head_dim = D;
+  cfg.max_seq_len = T;
+  cfg.max_batch = B;
+  std::vector<ExecutionNode> graph;
+  std::vector<std::string> outs;
+  for (int l = 0; l < L; ++l) {
+    const std::string i = std::to_string(l);
+    const std::string x = l == 0 ? "q0" : "attn" + std::to_string(l - 1);
+    graph.push_back({"rope_q" + i, "RotaryEmbedding", {x, "cos", "sin"}, {"qr" + i},
+                     {AttributeProto::make_int("rotary_embedding_dim", D), AttributeProto::make_int("interleaved", 0)}});
+    graph.push_back({"rope_k" + i, "RotaryEmbedding", {"k" + i, "cos", "sin"}, {"kr" + i},
+                     {AttributeProto::make_int("rotary_embedding_dim", D), AttributeProto::make_int("interleaved", 0)}});
+    graph.push_back({"gqa" + i, "GroupQueryAttention", {"qr" + i, "kr" + i, "v" + i, "", ""},
+                     {"attn" + i, "present_k" + i, "present_v" + i},
+                     {AttributeProto::make_int("num_heads", Hq), AttributeProto::make_int("kv_num_heads", Hkv)}});
+    outs.push_back("attn" + i);
+  }
+  auto session = must(GpuSession::create(0, cfg, graph, outs), "GpuSession::create");
+  std::vector<float> cs, sn;
+  rope_tables(rows, D, 10000.0, cs, sn);
+  struct Lay { std::vector<int8_t> k8, v8; std::vector<float> ks, vs; };
+  std::vector<Lay> lay(L);
+  for (Lay& x : lay) {
+    x.k8.assign((size_t)B * Hkv * T * D, 0); x.v8.assign(x.k8.size(), 0);
+    x.ks.assign((size_t)B * Hkv * T, 0.0f); x.vs.assign(x.ks.size(), 0.0f);
+  }
+  auto round_bf16 = [](std::vector<float>& x) {
+    for (float& e : x) e = sai_or_bf16_to_f32(sai_or_f32_to_bf16(e));
+  };
+  std::mt19937_64 gen(63);
+  int pos = 0;
+  auto pass = [&](int S, const char* what) {
+    std::vector<std::pair<std::string, DeviceTensor>> in;
+    in.emplace_back("cos", f32_tensor(cs, shp({rows, D / 2})));
+    in.emplace_back("sin", f32_tensor(sn, shp({rows, D / 2})));
+    std::vector<float> q0 = gauss(gen, (size_t)B * S * Hq * D);
+    in.emplace_back("q0", bf16_tensor(q0, shp({B, S, (int64_t)Hq * D})));  // q0: the bf16 values
+    std::vector<std::vector<float>> ks(L), vs(L);
+    for (int l = 0; l < L; ++l) {
+      const std::string i = std::to_string(l);
+      ks[l] = gauss(gen, (size_t)B * S * Hkv * D);
+      vs[l] = gauss(gen, (size_t)B * S * Hkv * D);
+      in.emplace_back("k" + i, bf16_tensor(ks[l], shp({B, S, (int64_t)Hkv * D})));
+      in.emplace_back("v" + i, bf16_tensor(vs[l], shp({B, S, (int64_t)Hkv * D})));
+    }
+    auto got = must(session->run(std::move(in)), what);
+    REQUIRE(got.size() == (size_t)L, "%s: outputs", what);
+    std::vector<float> x = q0;  // layer l's RoPE input as the GPU saw it
+    for (int l = 0; l < L; ++l) {
+      REQUIRE(got[l].dtype == DataType::BFloat16, "%s layer %d: attn_out is not bf16", what, l);
+      std::vector<float> q = x, k = ks[l];
+      oracle_rope_bshd(q, B, S, Hq, D, pos, cs, sn, rows);
+      oracle_rope_bshd(k, B, S, Hkv, D, pos, cs, sn, rows);
+      round_bf16(q);  // the bf16 RotaryEmbedding outputs the GQA node reads
+      round_bf16(k);
+      std::vector<int32_t> start(B, pos), lens(B, pos + S);
+      REQUIRE(sai_or_kv_append(k.data(), vs[l].data(), B, S, Hkv, D, start.data(), nullptr, nullptr, 0, 0, 0, 1,
+                               T, lay[l].k8.data(), lay[l].v8.data(), lay[l].ks.data(), lay[l].vs.data(), nullptr,
+                               nullptr) == 0,
+              "oracle append");
+      std::vector<float> kd((size_t)B * Hkv * T * D), vd(kd.size());
+      REQUIRE(sai_or_kv_dequant(B, Hkv, D, 1, T, lens.data(), lay[l].k8.data(), lay[l].v8.data(), lay[l].ks.data(),
+                                lay[l].vs.data(), nullptr, nullptr, kd.data(), vd.data()) == 0,
+              "oracle dequant");
+      std::vector<float> want((size_t)B * S * Hq * D);
+      REQUIRE(sai_or_gqa_cached_window(q.data(), B, S, Hq, Hkv, D, lens.data(), T, kd.data(), vd.data(), nullptr,
+                                       nullptr, 0, 0, 0, 0, 0.0f, 0, -1, want.data()) == 0,
+              "oracle attention");
+      const std::vector<float> a = host_values(got[l]);
+      char w[96];
+      std::snprintf(w, sizeof w, "%s layer %d", what, l);
+      close_bf16(a, want, w);
+      x = a;  // the next layer's RotaryEmbedding reads this output
+    }
+    pos += S;
+  };
+  pass(21, "bf16 chain prefill");
+  for (int step = 0; step < 3; ++step) pass(1, "bf16 chain decode");
+}
+
 // Gemma 3 4B's attention shape (model_loader/config.rs:695-717): 8 query heads
 // over 4 kv heads, head_dim 256, rope_theta 1e6.
 void gpu_session_gemma3_head256() { gemma_graph_session(8, 4, 256, 1000000.0, 62); }
@@ -1410,6 +1534,7 @@ int main(int argc, char** argv) {
       {"gpu_cpu_op_mha_with_past", true, gpu_cpu_op_mha_with_past},
       {"gpu_cpu_op_kats", true, gpu_cpu_op_kats},
       {"gpu_session_gemma_graph", true, gpu_session_gemma_graph},
+      {"gpu_session_bf16_chain", true, gpu_session_bf16_chain},
       {"gpu_session_gemma3_head256", true, gpu_session_gemma3_head256},
   };
   std::vector<const Case*> run;

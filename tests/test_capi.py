@@ -60,7 +60,10 @@ def test_null_handles_are_rejected():
     assert L.sai_kvcache_create(None, None, None) == -7
     assert L.sai_kv_append(None, None, 0, None, None, 1, 1, 1, None, None, 0, 0, 0, None) == -7
     assert L.sai_gqa_decode(None, None, 0, None, 1, 1, 1, None, None, 0, 0, 0, 0, 0.0, 0, None,
-                            None) == -7
+                            1, None) == -7
+    assert L.sai_gqa_prefill(None, None, 0, None, 1, 1, 1, 1, None, None, 0, 0, 0, 0, 0.0, 0,
+                             None, 16, None) == -7
+    assert L.sai_last_decode_launches(None) == 0
     assert L.sai_kvcache_set_layer_window(None, None, 0, 4) == -7
     assert L.sai_kvcache_advance(None, None, None) == -7
     assert L.sai_last_error(None) == b""

@@ -1,11 +1,12 @@
 """int8 decode parity on heavy-tailed keys with outlier channels.
 
-The int8 decode kernel holds the rotated query, and each tile's softmax
-weights p * s_v, as two int8 terms (hi + residual / 254) relative to their
-maximum, about 16 significant bits. Keys drawn from a Student-t (df 3) with
-four channels per head scaled x20 (the outlier channels of real models' keys)
-make the largest score terms, and so that representation error, hundreds of
-times larger than N(0, 1) keys do. These cases pin the kernel there, through
+The int8 decode kernel holds the rotated query as three int8 terms (hi +
+mid / 254 + lo / 254^2, ~24 significant bits) and each tile's softmax weights
+p * s_v as two (hi + residual / 254, ~16 bits), relative to their maxima.
+Keys drawn from a Student-t (df 3) with four channels per head scaled x20 (the
+outlier channels of real models' keys) make the largest score terms, and so
+the query's representation error, hundreds of times larger than N(0, 1) keys
+do (two query terms measured 0.96 of the tolerance here; three, 0.06). These cases pin the kernel there, through
 both entry points (sai_gqa_decode after sai_kv_append, and the fused
 sai_gqa_with_cache), at head_dim 128 (groups 4 and 8) and 256 (groups 2 and
 4), with many small splits and with one or two large ones. Each case logs its

@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 import smallaios_amd as S
-from _gpu_util import Case, assert_close, err_tol_ratio, log, outlier_student_t
+from _gpu_util import (Case, assert_close, assert_close_weighted, dev, err_tol_ratio, log,
+                       outlier_student_t, weighted_abs_v)
 
 pytestmark = pytest.mark.gpu
 
@@ -44,18 +45,23 @@ def test_append_variants_bit_exact(rt, d, interleaved, rot, kv_dtype):
     c.check_codes()
 
 
+@pytest.mark.parametrize("quant", [S.KV_INT8, S.KV_INT4])
 @pytest.mark.parametrize("d,interleaved,kv_dtype", [
     (64, False, "f32"), (64, True, "bf16"), (128, False, "bf16"), (128, True, "f32"),
     (256, False, "bf16"), (256, True, "f32")])
-def test_append_page_blocks_bit_exact(rt, d, interleaved, kv_dtype):
-    """Multi-token appends take the page-block kernel (one wave per page
-    block): 20 new tokens from starts 13, 0, 31 and 16 span two or three
-    pages, first and last page partial or whole; the slots before the start
-    keep their codes. 3 tokens take the per-row kernel, and the results of
-    both meet bit-exact in one cache."""
-    log(f"append page blocks d={d} interleaved={interleaved} {kv_dtype}")
+def test_append_page_blocks_bit_exact(rt, d, interleaved, kv_dtype, quant):
+    """Multi-token appends take the page-block kernel (one workgroup per page
+    block, 16-byte stores): 20 new tokens from starts 13, 0, 31 and 16 span
+    two or three pages, first and last page partial or whole; the slots
+    before the start keep their codes (int4: the other nibble of each V
+    byte). 3 tokens take the per-row (int4: per-pair) kernel, and the results
+    of both meet bit-exact in one cache. K with x20 outlier channels and
+    heavy tails, so the int4 groups' ranges differ widely."""
+    log(f"append page blocks quant={quant} d={d} interleaved={interleaved} {kv_dtype}")
+    from _gpu_util import outlier_keys
     c = Case(rt, 0xB10C + d, 4, 8, 2, d, [13, 0, 31, 16], 20, theta=5e5, kv_dtype=kv_dtype,
-             permute_pages=True, interleaved=interleaved, extra_tokens=3)
+             permute_pages=True, interleaved=interleaved, extra_tokens=3, quant=quant,
+             k_transform=outlier_keys(d, channels=(5, 17, d - 3)))
     c.step_kv()
     c.check_codes()
     c.cache.advance()
@@ -86,9 +92,12 @@ def test_append_unaligned_rows_bit_exact(rt):
     c.check_codes()
 
 
-def test_append_special_values(rt):
-    """Zero rows, huge/tiny magnitudes, inf and NaN keep the codes bit-exact."""
-    log("append special values")
+@pytest.mark.parametrize("quant", [S.KV_INT8, S.KV_INT4])
+def test_append_special_values(rt, quant):
+    """Zero rows, huge/tiny magnitudes, inf and NaN keep the codes (and int4's
+    binary16 group parameters) bit-exact; 8 tokens take the page-block
+    kernel."""
+    log(f"append special values quant={quant}")
 
     def poison(rng, k):
         k = k.copy()
@@ -101,7 +110,7 @@ def test_append_special_values(rt):
         k[0, 6, 64:128] = np.float32(-np.inf)
         return k
 
-    c = Case(rt, 11, 1, 4, 2, 64, [0], 8, k_transform=poison, do_rotary=False)
+    c = Case(rt, 11, 1, 4, 2, 64, [0], 8, k_transform=poison, do_rotary=False, quant=quant)
     c.step_kv()
     c.check_codes()
 
@@ -197,6 +206,47 @@ def test_decode_fused_step(rt, merge, split):
         rt.set_decode_split(prev_s)
 
 
+@pytest.mark.parametrize("quant,vscale", [
+    (S.KV_INT8, 1.0e5), (S.KV_INT8, 1.0e7), (S.KV_INT4, 1.0e4),
+])
+@pytest.mark.parametrize("split", [256, 0])
+def test_decode_large_v(rt, quant, vscale, split):
+    """The fused decode step (sai_gqa_with_cache) with V rows of |v| ~ 4e5 or
+    4e7 and keys at 300-339 scaled x6 (weights concentrated on a few keys
+    whose V rows cancel far below |v|), one split and many. int8 P' is two
+    int8 terms against its 64-token tile's maximum, int4 P' one binary16
+    value per (head, group); both are scale-free, so the outputs are checked
+    against the bound of that representation (decode_weight_bounds) plus the
+    oracle's expf_approx error, on top of 2e-3 + 1e-2|ref| (the oracle's
+    expf_approx alone moves such outputs by more than 2e-3). int4 runs at
+    1e4 (|v| ~ 4e4): its zero point, the group minimum, is stored as
+    binary16, so V beyond 65504 is outside the scheme (inf in the oracle
+    too)."""
+    from _gpu_util import assert_close_decode_bound, decode_weight_bounds
+    log(f"decode large V: quant {quant} V x{vscale:g} split {split}")
+
+    def jump(rng, k):
+        if k.shape[1] >= 340:
+            k[:, 300:340] *= 6.0
+        return k
+
+    prev_s = rt.set_decode_split(split)
+    try:
+        c = Case(rt, 0x1A6E, 3, 32, 8, 128, [700, 450, 3000], 1, theta=5e5, quant=quant,
+                 kv_dtype="bf16", permute_pages=True, k_transform=jump,
+                 v_transform=lambda rng, v: v * np.float32(vscale))
+        q = c.query("bf16")
+        got = c.step_fused(q, "bf16")
+        c.check_codes(seqs=[1])
+        ref = c.oracle_attend(q)
+        assert np.isfinite(got).all()
+        wabs, rep = decode_weight_bounds(c, q)
+        r = assert_close_decode_bound(got, ref, wabs, rep, "decode, large V")
+        log(f"  worst err / bound {r:.4f}")
+    finally:
+        rt.set_decode_split(prev_s)
+
+
 def test_decode_first_token_equals_v(rt):
     """One visible key: the output is that key's dequantised V (cf. the
     reference's test_gpu_gqa_first_token_no_history)."""
@@ -232,6 +282,33 @@ def test_decode_ragged_paged_batch(rt):
     assert_close(c.gpu_decode(q), c.oracle_attend(q), "ragged decode")
 
 
+@pytest.mark.parametrize("merge", [0, 1])
+@pytest.mark.parametrize("quant", [S.KV_INT8, S.KV_INT4])
+def test_decode_ragged_balanced_splits(rt, quant, merge):
+    """Ragged batches deal each sequence's tiles evenly to its splits and hand
+    the work items to the sequences with the longest splits first (batches of
+    up to 256 sequences; the order rides in the kernel arguments). 300
+    sequences (past the ordered limit: scan order) and 40 (ordered), lengths
+    from 1 to 1200 tokens, split 256 (1 to 5 splits each, lengths like 257 and
+    513 that would leave a one-token remainder), merged by the combine kernel
+    (0) and in-kernel (1)."""
+    log(f"decode ragged balanced splits quant={quant} merge={merge}")
+    prev_s = rt.set_decode_split(256)
+    prev_m = rt.set_decode_merge(merge)
+    try:
+        for n, seed in ((300, 0xBA1A), (40, 0xBA1B)):
+            lens = np.random.default_rng(seed).integers(1, 1200, size=n).astype(np.int32)
+            lens[:4] = [256, 512, 257, 1]
+            c = Case(rt, seed, n, 8, 2, 64 if quant == S.KV_INT8 else 128, lens - 1, 1,
+                     theta=1e4, quant=quant, permute_pages=True)
+            q = c.query("bf16")
+            got = c.step_fused(q, "bf16")
+            assert_close(got, c.oracle_attend(q), f"ragged {n} sequences")
+    finally:
+        rt.set_decode_split(prev_s)
+        rt.set_decode_merge(prev_m)
+
+
 def test_decode_llama_layer_full_size(rt):
     """Full Llama-3-8B decode layer: B=16, 8k context, bf16 Q, int8 KV."""
     log("decode full size: B=16 ctx 8192 32Q/8KV D=128")
@@ -243,6 +320,74 @@ def test_decode_llama_layer_full_size(rt):
     err = assert_close(got, ref, "c2 decode")
     log(f"  max abs err {err:.2e}, worst err/tol {err_tol_ratio(got, ref):.4f}")
     c.check_codes(seqs=[0, 15])
+
+
+@pytest.mark.parametrize("quant", [S.KV_INT8, S.KV_INT4])
+def test_decode_bf16_output(rt, quant):
+    """Attention output in bf16 (the reference's GPU GQA returns Q's dtype,
+    attention.rs:835 and :877-901): the Llama-3-8B layer shape with 8k
+    contexts (4 sequences), the fused step and the no-alloc step with bf16
+    Q and bf16 output, against the f32 oracle within the tolerance widened
+    by bf16 rounding; the decoded step's codes stay bit-exact. Split merges
+    in-kernel (uniform) and through the combine kernel (ragged)."""
+    log(f"decode bf16 output: quant {quant}")
+    from _gpu_util import bf16_tol_close
+    c = Case(rt, 0x5A1A0B16, 4, 32, 8, 128, [8191] * 4, 1, theta=5e5, quant=quant,
+             kv_dtype="bf16", extra_tokens=3)
+    q = c.query("bf16")
+    got = c.step_fused(q, "bf16", out_dtype="bf16")
+    ref = c.oracle_attend(q)
+    r = bf16_tol_close(got, ref, "bf16 fused step")
+    log(f"  uniform 8k: worst err/tol {r:.4f}")
+    c.check_codes(seqs=[2])
+    c.cache.advance()
+    # ragged lengths: the combine kernel's store
+    c.cache.set_seq_lens(np.array([8192, 3000, 777, 5000], np.int32))
+    c.ocache.seq_len = np.array([8192, 3000, 777, 5000], np.int32)
+    q = c.query("bf16")
+    got = c.step_fused(q, "bf16", out_dtype="bf16")
+    r = bf16_tol_close(got, c.oracle_attend(q), "bf16 fused step, ragged")
+    log(f"  ragged: worst err/tol {r:.4f}")
+
+
+def test_prefill_bf16_output(rt):
+    """The prefill chunk at its workload's per-sequence shape (32Q/8KV, 2048
+    new tokens over 6144 cached, bf16 Q/K/V), one sequence, with bf16 output:
+    bit for bit the f32 output rounded to nearest even (prefill is
+    deterministic), and within the bf16-widened tolerance of the oracle on
+    sampled rows."""
+    import copy
+    from _gpu_util import bf16_tol_close, to_bf16_f32
+    log("prefill bf16 output: B=1 past 6144 new 2048")
+    c = Case(rt, 0x5A1A0B17, 1, 32, 8, 128, [6144], 2048, theta=5e5, kv_dtype="bf16")
+    c.step_kv()
+    q = c.query("bf16")
+    got32 = c.gpu_prefill(q, "bf16")
+    got16 = c.gpu_prefill(q, "bf16", out_dtype="bf16")
+    np.testing.assert_array_equal(got16.view(np.uint32), to_bf16_f32(got32).view(np.uint32))
+    deq = c.ocache.dequant()
+    for i in [0, 1000, 2047]:
+        oc = copy.copy(c.ocache)
+        oc.seq_len = np.array([6144 + i + 1], dtype=np.int32)
+        ref = oc.attend(q[:, i:i + 1], 32, c.cos, c.sin, deq=deq)
+        bf16_tol_close(got16[:, i:i + 1], ref, f"bf16 prefill row {i}")
+
+
+def test_output_dtype_errors(rt):
+    """An output dtype other than f32/bf16 is UNSUPPORTED at every attention
+    entry point."""
+    import torch
+    c = Case(rt, 0x0D7E, 1, 8, 2, 64, [40], 1)
+    c.step_kv()
+    q = dev(c.query())
+    for bad in (torch.float16,):
+        out = torch.zeros((1, 1, 8 * 64), dtype=bad, device="cuda")
+        with pytest.raises(S.SaiError) as e:
+            c.cache.decode(0, q, out, 1, 8, c.cos_d, c.sin_d, c.cos.shape[0])
+        assert e.value.status == -3 and "output dtype" in str(e.value)
+        with pytest.raises(S.SaiError) as e:
+            c.cache.prefill(0, q, out, 1, 1, 8, c.cos_d, c.sin_d, c.cos.shape[0])
+        assert e.value.status == -3
 
 
 # ------------------------------------------------------------ int4 decode ---
@@ -402,35 +547,73 @@ def test_prefill_outlier_keys(rt, quant, hq, hkv, d, past, new, qd):
     log(f"  max abs err {err:.2e}")
 
 
-@pytest.mark.parametrize("vscale", [1.0, 1.0e5])
-def test_prefill_reference_moves(rt, vscale):
-    """int8 prefill whose weights leave the fast path's bounds mid-sequence: keys
+@pytest.mark.parametrize("quant,vscale", [
+    (S.KV_INT8, 1.0), (S.KV_INT8, 1.0e5), (S.KV_INT8, 1.0e7), (S.KV_INT4, 1.0e4),
+])
+def test_prefill_reference_moves(rt, quant, vscale):
+    """Prefill whose weights leave the fast path's bounds mid-sequence: keys
     at past positions 300-339 are scaled x6, so their scores rise tens of log2
-    units above the reference point the first tiles set (their weights would
-    overflow binary16), and with vscale 1e5 the V rows reach |v| ~ 4e5, so the
-    row-sum bound r * max(s_v) <= 32768 fails on ordinary tiles too. Those tiles
-    are settled (scores recomputed, reference moved); codes bit-exact, outputs
-    within tolerance of the oracle in units of the V scale (scaling V by c scales
-    the output by c; the outputs here are averages of +-4e5 values that cancel
-    down to ~1e3, so an absolute 2e-3 would ask binary16 weights for ~1e-8
-    relative accuracy)."""
-    log(f"prefill reference moves: keys x6 at 300-339, V x{vscale:g}")
+    units above the reference point the first tiles set. With vscale 1e5 and
+    1e7 the V rows reach |v| ~ 4e5 and 4e7 (int4: 1e4, as its binary16 zero
+    point allows): int8 tiles with V scales above
+    the large-V threshold go to the precise pass (binary16 hi + lo weights
+    normalised by a power of two, so nothing overflows binary16; 1e7 put
+    p * s_v past 65504 before), int4 V is staged scaled by 2^-5. Codes
+    bit-exact. The outputs cancel to ~1e3 against |v| ~ 4e5, where the
+    oracle's own expf_approx (3.5e-5 relative) already moves them by more than
+    2e-3, so large V is checked against the weighted bound
+    2e-3 + 1e-2|ref| + kappa sum p|v| / sum p: kappa 2^-12 for the precise
+    int8 pass, 2^-9 for int4 (binary16 weights and V values)."""
+    log(f"prefill reference moves: quant {quant}, keys x6 at 300-339, V x{vscale:g}")
 
     def jump(rng, k):
         if k.shape[1] >= 340:
             k[:, 300:340] *= 6.0
         return k
 
-    c = Case(rt, 0x5E77, 2, 16, 4, 128, [700, 450], 130, theta=5e5, permute_pages=True,
-             k_transform=jump, v_transform=lambda rng, v: v * np.float32(vscale))
+    c = Case(rt, 0x5E77, 2, 16, 4, 128, [700, 450], 130, theta=5e5, quant=quant,
+             permute_pages=True, k_transform=jump,
+             v_transform=lambda rng, v: v * np.float32(vscale))
     c.step_kv()
     c.check_codes()
     q = c.query("f32")
     got = c.gpu_prefill(q, "f32")
     ref = c.oracle_attend(q)
-    got, ref = got / np.float32(vscale), ref / np.float32(vscale)
-    log(f"  worst err/tol {err_tol_ratio(got, ref):.4f}")
-    assert_close(got, ref, "prefill, reference moves")
+    assert np.isfinite(got).all()
+    if vscale == 1.0:
+        log(f"  worst err/tol {err_tol_ratio(got, ref):.4f}")
+        assert_close(got, ref, "prefill, reference moves")
+        return
+    kappa = 2.0 ** -12 if quant == S.KV_INT8 else 2.0 ** -9
+    r = assert_close_weighted(got, ref, weighted_abs_v(c, q), kappa, "prefill, large V")
+    log(f"  worst err / weighted bound {r:.4f}")
+
+
+@pytest.mark.parametrize("quant", [S.KV_INT8, S.KV_INT4])
+def test_prefill_first_key_far_below(rt, quant):
+    """Row 0 of a fresh prompt sees one key; its query is -20 x that key, so
+    its only score is ~ -330 (log2 units). The reference point then moves
+    down by 330 on the row's first keys, where exp2(330) is inf: the row must
+    still come out as v0 (it came out NaN when the rescale of the empty
+    accumulator was exp2(-lead)). Also rows at a window edge that see only
+    that key."""
+    log(f"prefill first key far below: quant {quant}")
+    c = Case(rt, 0xF1F0, 2, 8, 2, 128, [0, 0], 64, theta=1e4, quant=quant)
+    c.step_kv()
+    c.check_codes()
+    q = c.query("f32")
+    k0 = c.ocache.dequant()[0][:, :, 0, :]  # [B, Hkv, D] (position 0: RoPE is the identity)
+    for b in range(2):
+        for h in range(8):
+            q[b, 0, h * 128:(h + 1) * 128] = -20.0 * k0[b, h // 4]
+    got = c.gpu_prefill(q, "f32")
+    ref = c.oracle_attend(q)
+    assert np.isfinite(got).all(), "NaN/inf in the prefill output"
+    assert_close(got, ref, "prefill, first key far below")
+    got_w = c.gpu_prefill(q, "f32", window=1)
+    ref_w = c.oracle_attend(q, mask_window=1)
+    assert np.isfinite(got_w).all()
+    assert_close(got_w, ref_w, "prefill, window 1")
 
 
 # ------------------------------------------------------------- introspection ---
