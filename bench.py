@@ -142,7 +142,10 @@ def build_cache(S, torch, rt, w, past_lens, extra_tokens, cos_d, sin_d, seed):
     cache.set_page_table(ids.reshape(b, pages))
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
-    past, done, chunk = int(past_lens.max()), 0, 1024
+    # chunks of ~131k (token, kv head) rows per append call, the Llama-3-8B
+    # layer's 16 x 1024 (at least 1024 tokens)
+    chunk = max(1024, (131072 // (b * hkv)) // PAGE * PAGE)
+    past, done = int(past_lens.max()), 0
     while done < past:
         n = min(chunk, past - done)
         k = torch.randn((b, n, hkv * d), generator=g, device="cuda")

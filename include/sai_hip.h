@@ -95,7 +95,7 @@ int32_t sai_device_supported(int device);
 typedef struct sai_kvcache_desc {
   int32_t num_layers;
   int32_t num_kv_heads;
-  int32_t head_dim;          /* 64, 128 or 256 (decode groups up to 4 at 256) */
+  int32_t head_dim;          /* 64, 128 or 256 (int4 decode: groups up to 4 at 256) */
   int32_t num_pages;         /* physical pages per layer */
   int32_t max_batch;         /* sequences */
   int32_t max_pages_per_seq; /* page-table width */
@@ -183,7 +183,8 @@ sai_status sai_kv_append(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const 
  * > 0): the query at position p sees keys [p - window, p]; <= 0 = off. A
  * sliding-window layer (sai_kvcache_set_layer_window) sees its last w keys;
  * with both, the narrower span applies. Head dims 64, 128 and 256 for int8
- * and int4 (groups up to 4 at 256); UNSUPPORTED otherwise. */
+ * and int4, groups 1, 2, 4 and 8 (int4 at 256: up to 4); UNSUPPORTED
+ * otherwise. */
 sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
                           int32_t dtype, int32_t batch, int32_t num_heads,
                           const float* cos_cache, const float* sin_cache, int32_t cache_rows,

@@ -264,11 +264,14 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, 
   after_pv();
 }
 
-// Two waves per SIMD, except group 8 at head_dim 128: its two passes of query
-// terms and accumulators do not fit beside two tile buffers in 256 registers,
-// so it runs one wave per SIMD with the whole register file.
+// Two waves per SIMD, except group 8 at head_dim 128 and 256: its two passes
+// of query terms and accumulators do not fit beside the tile buffers in 256
+// registers, so it runs one wave per SIMD with the whole register file.
+template <int D, int G>
+constexpr bool kInt8OneWavePerSimd = G > 4 && D >= 128;
+
 template <int D, int G, int NW>
-__global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_decode_int8_kernel(
+__global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void gqa_decode_int8_kernel(
     DecodeParams p) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static_assert(G >= 1 && G <= 8, "group");
@@ -660,8 +663,11 @@ __global__ __launch_bounds__(64 * NW, (G > 4 && D == 128) ? 1 : 2) void gqa_deco
 // them online (C = the split count rounded up to 2, 4, 8 or 16, so a 2-split
 // merge is one round trip of 6 loads); with a uniform split count the range
 // comes from the launch, not from seq_info.
+template <int D, int G>
+constexpr int kCombineThreads = G * D < 1024 ? G * D : 1024;
+
 template <int D, int G, int C>
-__global__ __launch_bounds__(G * D) void gqa_decode_combine_kernel(DecodeParams p) {
+__global__ __launch_bounds__((kCombineThreads<D, G>)) void gqa_decode_combine_kernel(DecodeParams p) {
   const int b = blockIdx.x;
   const int kvh = blockIdx.y;
   int split_base, nsplit;
@@ -676,7 +682,8 @@ __global__ __launch_bounds__(G * D) void gqa_decode_combine_kernel(DecodeParams 
   const int Hq = p.kv_heads * G;
   const size_t stride = (size_t)p.kv_heads * (G * (D + 2));
   const float* p0 = p.partials + ((size_t)split_base * p.kv_heads + kvh) * (G * (D + 2));
-  const int t = threadIdx.x;
+  // (head, dim) entries t, t + 1024, ... (8 x 256 entries take two rounds)
+  for (int t = threadIdx.x; t < G * D; t += kCombineThreads<D, G>) {
   const int hd = t / D, d = t % D;
   const float* ph = p0 + hd * (D + 2);
   float M = -INFINITY, Ls = 0.0f, O = 0.0f;
@@ -706,6 +713,7 @@ __global__ __launch_bounds__(G * D) void gqa_decode_combine_kernel(DecodeParams 
     M = mb;
   }
   store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * D + d, Ls > 0.0f ? O / Ls : 0.0f, p.out_bf16);
+  }
 }
 
 template <int D, int G>
@@ -713,7 +721,7 @@ hipError_t launch_combine_dg(const DecodeParams& p, hipStream_t st) {
   // the largest split count decides the batch width (uniform: the launch's;
   // ragged: bounded by the longest sequence)
   const int n = p.uniform_nsplit > 0 ? p.uniform_nsplit : p.max_nsplit;
-  const dim3 grid(p.batch, p.kv_heads), block(G * D);
+  const dim3 grid(p.batch, p.kv_heads), block(kCombineThreads<D, G>);
   if (n <= 2)
     hipLaunchKernelGGL((gqa_decode_combine_kernel<D, G, 2>), grid, block, 0, st, p);
   else if (n <= 4)
@@ -728,9 +736,9 @@ hipError_t launch_combine_dg(const DecodeParams& p, hipStream_t st) {
 template <int D, int G>
 hipError_t launch_dg(const DecodeParams& p, int work_items, bool combine, hipStream_t st) {
   const dim3 grid(work_items, p.kv_heads);
-  // group 8 at head_dim 128 needs one wave per SIMD (see the kernel), which
-  // an 8-wave workgroup cannot give: always 4 waves there
-  constexpr bool kEightWaves = !(G > 4 && D == 128);
+  // group 8 at head_dim 128 and 256 needs one wave per SIMD (see the kernel),
+  // which an 8-wave workgroup cannot give: always 4 waves there
+  constexpr bool kEightWaves = !kInt8OneWavePerSimd<D, G>;
   if (kEightWaves && p.waves == 8)
     hipLaunchKernelGGL((gqa_decode_int8_kernel<D, G, kEightWaves ? 8 : 4>), grid,
                        dim3(kEightWaves ? 512 : 256), 0, st, p);
@@ -748,10 +756,7 @@ hipError_t launch_d(const DecodeParams& p, int group, int work_items, bool combi
     case 1: return launch_dg<D, 1>(p, work_items, combine, st);
     case 2: return launch_dg<D, 2>(p, work_items, combine, st);
     case 4: return launch_dg<D, 4>(p, work_items, combine, st);
-    case 8:
-      // the combine block is one thread per (head, dim): 8 x 256 is past 1024
-      if constexpr (D <= 128) return launch_dg<D, 8>(p, work_items, combine, st);
-      return hipErrorInvalidValue;
+    case 8: return launch_dg<D, 8>(p, work_items, combine, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -771,7 +776,7 @@ hipError_t launch_decode_combine(const DecodeParams& p, int head_dim, int group,
   };
   if (head_dim == 64) return by_group(std::integral_constant<int, 64>{});
   if (head_dim == 128) return by_group(std::integral_constant<int, 128>{});
-  if (head_dim == 256 && group <= 4) return by_group(std::integral_constant<int, 256>{});
+  if (head_dim == 256) return by_group(std::integral_constant<int, 256>{});
   return hipErrorInvalidValue;
 }
 
@@ -784,7 +789,7 @@ hipError_t launch_gqa_decode(const DecodeParams& p, int head_dim, int group, int
     return hipErrorInvalidValue;
   if (head_dim == 64) return launch_d<64>(p, group, work_items, combine, st);
   if (head_dim == 128) return launch_d<128>(p, group, work_items, combine, st);
-  if (head_dim == 256 && group <= 4) return launch_d<256>(p, group, work_items, combine, st);
+  if (head_dim == 256) return launch_d<256>(p, group, work_items, combine, st);
   return hipErrorInvalidValue;
 }
 

@@ -348,17 +348,34 @@ __device__ __forceinline__ uint32_t quant4_int4(const float (&x)[4], uint32_t& s
   const _Float16 hz = (_Float16)mn;
   const float sf = (float)hs;
   const float zf = (float)hz;
+  // the quotient t = (x - z) / s from the reciprocal: a = (x - z) * rcp(s) is
+  // within 2 ulps of the correctly rounded t (1 ulp of v_rcp_f32, half of the
+  // product, half of the division), i.e. within 4e-6 for |t| <= 16. The code
+  // round_f32 then takes (half away from zero, `as u32`, min 15) depends only
+  // on which side of a half-integer t lies, so where a is farther than 2^-14
+  // from every half-integer it is rint-up of a, clamped to [0, 15]; anything
+  // else (near a tie, NaN, inf) takes the reference's own steps below
+  const float rf = __builtin_amdgcn_rcpf(sf);
   uint32_t w = 0u;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     uint32_t v = 0u;
     if (sf > 0.0f) {
-      // round_f32 of onnx-rt/src/kv_compression.rs:27-37, then `as u32`
-      const float t = (x[j] - zf) / sf;
-      const float tr = (float)sat_i32(t);
-      const float fr = t - tr;
-      const float rr = (fr >= 0.5f) ? tr + 1.0f : ((fr <= -0.5f) ? tr - 1.0f : tr);
-      v = sat_u32(rr);
+      const float d = x[j] - zf;
+      const float a = d * rf;
+      const float fl = floorf(a);
+      const float fa = a - fl;
+      if (fabsf(fa - 0.5f) >= 0x1p-14f) {
+        const float c = fa > 0.5f ? fl + 1.0f : fl;
+        v = c <= 0.0f ? 0u : (c >= 15.0f ? 15u : (uint32_t)c);
+      } else {
+        // round_f32 of onnx-rt/src/kv_compression.rs:27-37, then `as u32`
+        const float t = d / sf;
+        const float tr = (float)sat_i32(t);
+        const float fr = t - tr;
+        const float rr = (fr >= 0.5f) ? tr + 1.0f : ((fr <= -0.5f) ? tr - 1.0f : tr);
+        v = sat_u32(rr);
+      }
     }
     w |= (v < 15u ? v : 15u) << (4 * j);  // codes packed LSB first
   }

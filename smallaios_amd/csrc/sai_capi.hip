@@ -310,7 +310,10 @@ size_t decode_work_bound(const sai_ctx* ctx, const sai_kvcache_desc& d) {
 }
 
 // Largest query group a cache of this head_dim serves in decode.
-int max_decode_group(int head_dim) { return head_dim > 128 ? 4 : 8; }
+// (int8 decodes groups up to 8 at every head dim; int4 at head_dim 256 up to 4)
+int max_decode_group(int head_dim, int quant) {
+  return head_dim > 128 && quant == SAI_KV_INT4 ? 4 : 8;
+}
 
 }  // namespace
 
@@ -492,7 +495,7 @@ SAI_API sai_status sai_kvcache_create(sai_ctx* ctx, const sai_kvcache_desc* desc
   // the decode workspace for every launch at the automatic split
   const size_t work = decode_work_bound(ctx, d);
   sai_status st = reserve_workspace(
-      ctx, c->ws, work * d.num_kv_heads * max_decode_group(d.head_dim) * (d.head_dim + 2),
+      ctx, c->ws, work * d.num_kv_heads * max_decode_group(d.head_dim, d.quant) * (d.head_dim + 2),
       (size_t)d.max_batch * 2, (size_t)d.max_batch * d.num_kv_heads);
   if (st != SAI_OK) {
     sai_kvcache_destroy(c);
@@ -794,8 +797,9 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   const char* op = "gqa_decode";
   const int32_t W = visible_span(c->layer_window[layer], window);
   const int D = c->desc.head_dim;
-  if (D == 256 && G > 4)
-    return fail(ctx, SAI_ERR_UNSUPPORTED, "%s: head_dim 256 supports groups of 1, 2 and 4 (got %d)",
+  if (D == 256 && G > 4 && c->desc.quant == SAI_KV_INT4)
+    return fail(ctx, SAI_ERR_UNSUPPORTED,
+                "%s: int4 at head_dim 256 supports groups of 1, 2 and 4 (got %d)",
                 op, G);
   const int kvh = c->desc.num_kv_heads;
 

@@ -81,12 +81,36 @@ def test_decode_d256_windows(rt, quant):
                  "d=256 both windows")
 
 
-def test_decode_d256_group8_rejected(rt, quant):
-    c = Case(rt, 346, 1, 8, 1, D, [64], 1, quant=quant)
+def test_decode_d256_group8(rt, quant):
+    """Group 8 at head_dim 256: int8 decodes it (one wave per SIMD, the
+    combine kernel over 2048 (head, dim) entries in two rounds of 1024
+    threads), through one split, many splits merged in-kernel and by the
+    combine kernel, and the fused step, with outlier keys; int4 rejects it
+    as Unsupported."""
+    log(f"decode d=256 group 8 quant={quant}")
+    c = Case(rt, 346, 3, 16, 2, D, [64, 2100, 900], 1, quant=quant, theta=1e6,
+             permute_pages=True, extra_tokens=1, k_transform=outlier_keys(D))
     c.step_kv()
-    with pytest.raises(S.SaiError) as e:
-        c.gpu_decode(c.query())
-    assert e.value.kind == "Unsupported"
+    if quant == S.KV_INT4:
+        with pytest.raises(S.SaiError) as e:
+            c.gpu_decode(c.query())
+        assert e.value.kind == "Unsupported"
+        return
+    q = c.query("bf16")
+    ref = c.oracle_attend(q)
+    for split, merge in ((0, 2), (256, 0), (256, 1)):
+        prev_s, prev_m = rt.set_decode_split(split), rt.set_decode_merge(merge)
+        try:
+            got = c.gpu_decode(q, "bf16")
+        finally:
+            rt.set_decode_split(prev_s)
+            rt.set_decode_merge(prev_m)
+        log(f"  split {split} merge {merge}: worst err/tol {err_tol_ratio(got, ref):.4f}")
+        assert_close(got, ref, f"d=256 group 8 split {split} merge {merge}")
+    c.cache.advance()
+    q = c.query("bf16")
+    assert_close(c.step_fused(q, "bf16"), c.oracle_attend(q), "d=256 group 8 fused")
+    c.check_codes(seqs=[1])
 
 
 @pytest.mark.parametrize("hq,hkv,past,new,qd", [
