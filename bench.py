@@ -115,11 +115,11 @@ def append_roofline(b, new, hkv, d, us):
             "peak_gbps": HBM_PEAK_GBPS, "frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
-def traffic_from_profile(workload):
-    """HBM bytes per decode-kernel launch measured with rocprofv3 --pmc
-    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of known size), if the
-    workload's summary is present."""
-    path = os.path.join(ROOT, "profiles", f"gqa_decode_{workload}_pmc.txt")
+def traffic_from_profile(workload, kernel="gqa_decode"):
+    """HBM bytes per launch of the workload's dominant kernel measured with
+    rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of
+    known size), if the workload's summary is present."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_pmc.txt")
     try:
         with open(path) as f:
             m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read(), re.M)
@@ -659,7 +659,7 @@ def main():
             "separate_write_us": {"median": round(float(np.median(wus)), 3)},
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                         "traffic": None,
+                         "traffic": traffic_from_profile(args.workload, "tq_attend"),
                          "basis": "median of HIP events around each attention launch "
                                   "(query encoding + attention + split merge)"},
         }
