@@ -16,7 +16,8 @@ Other workloads (--workload, for the per-configuration table): `batch1`
 (8Q/2KV, head_dim 64, context 512), `int4long` (4 sequences of 32768 tokens,
 int4 KV with f16 (scale, zero) per group of 32 dims, K Student-t df 3 with
 four x20 outlier channels), `gemma4b` and `gemma4b_int4` (Gemma 3 4B's 8Q/4KV at
-head_dim 256, 16 sequences of 8192 tokens, int8 and int4 KV), `ragged` (64 sequences with seeded lengths
+head_dim 256, 16 sequences of 8192 tokens, int8 and int4 KV), `gemma31b` (Gemma 4
+31B's 32Q/8KV at head_dim 168, stored 192 wide, 16 x 8192, int8), `ragged` (64 sequences with seeded lengths
 U[128, 16384], randomly permuted page table), `prefill` (2 x 2048 new
 tokens appended to a 6144-token cache, then causal MFMA attention) and `rope`
 (the standalone RotaryEmbedding op over that chunk's queries: [2, 2048,
@@ -60,6 +61,8 @@ WORKLOADS = {
     "gemma4b_int4": dict(kind="decode", batch=16, hq=8, hkv=4, d=256, lens=("uniform", 8192),
                          theta=1000000.0, q_dtype="bf16", permute=False, quant="int4",
                          k_dist="outlier_t3"),
+    "gemma31b": dict(kind="decode", batch=16, hq=32, hkv=8, d=168, lens=("uniform", 8192),
+                     theta=1000000.0, q_dtype="bf16", permute=False),
     "ragged": dict(kind="decode", batch=64, hq=32, hkv=8, d=128, lens=("uniform_rand", 128, 16384),
                    theta=500000.0, q_dtype="bf16", permute=True),
     "prefill": dict(kind="prefill", batch=2, hq=32, hkv=8, d=128, past=6144, new=2048,
@@ -84,16 +87,25 @@ def decode_lengths(w, seed=0x5A1A0003):
     return rng.integers(w["lens"][1], w["lens"][2] + 1, size=w["batch"]).astype(np.int64)
 
 
-def kv_bytes_per_token_head(d, quant):
+def stored_dim(d):
+    """Row width the cache stores: head_dim 168 is kept 192 wide (each 84-dim
+    half of the split-half RoPE pairing followed by 12 zero dims)."""
+    return 192 if d == 168 else d
+
+
+def kv_bytes_per_token_head(d, quant, stored=True):
     """int8: K+V codes (2d) and two f32 scales; int4: K+V nibbles (d) and an
-    f16 (scale, zero) per group of 32 dims for K and for V (d/4)."""
+    f16 (scale, zero) per group of 32 dims for K and for V (d/4). d is the
+    stored width unless `stored` is False (the caller's head_dim)."""
+    d = stored_dim(d) if stored else d
     return 2 * d + 8 if quant == "int8" else d + d // 4
 
 
-def decode_bytes(lens, hq, hkv, d, q_bytes, quant="int8"):
+def decode_bytes(lens, hq, hkv, d, q_bytes, quant="int8", stored=True):
     """Algorithmic bytes of one decode step: the K+V codes and quantisation
-    parameters of every visible token, the query and the f32 output."""
-    kv = int(lens.sum()) * hkv * kv_bytes_per_token_head(d, quant)
+    parameters of every visible token (at the stored row width, or the
+    caller's head_dim when `stored` is False), the query and the f32 output."""
+    kv = int(lens.sum()) * hkv * kv_bytes_per_token_head(d, quant, stored)
     return kv + len(lens) * hq * d * q_bytes + len(lens) * hq * d * 4
 
 
@@ -518,6 +530,14 @@ def main():
         }
         if rotated is not None:
             result["rotated_two_caches"] = rotated
+        if stored_dim(d) != d:
+            # the caller's bytes (168-dim rows) moved per second: the padding
+            # of the stored rows is traffic this layout adds
+            lg = decode_bytes(lens, hq, hkv, d, 2 if qdt == torch.bfloat16 else 4, quant,
+                              stored=False)
+            result["stored_head_dim"] = stored_dim(d)
+            result["logical_bytes_per_step"] = lg
+            result["logical_gbps"] = round(lg / (ms_step * 1e-3) / 1e9, 1)
         if w["lens"][0] != "uniform":
             result["split_balance"] = split_balance(lens, split, hkv)
     elif w["kind"] == "rotary":

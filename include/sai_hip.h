@@ -95,7 +95,8 @@ int32_t sai_device_supported(int device);
 typedef struct sai_kvcache_desc {
   int32_t num_layers;
   int32_t num_kv_heads;
-  int32_t head_dim;          /* 64, 128 or 256 (int4 decode: groups up to 4 at 256) */
+  int32_t head_dim;          /* 64, 128, 256, or 168 for int8 (Gemma 4 31B); int4
+                                decode: groups up to 4 at 256 */
   int32_t num_pages;         /* physical pages per layer */
   int32_t max_batch;         /* sequences */
   int32_t max_pages_per_seq; /* page-table width */
@@ -145,7 +146,10 @@ sai_status sai_kvcache_read(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, int
  * (h * num_pages + p) * block_bytes; INT8 block: K codes [16][D] int8, V codes
  * [D][16] int8, K scales [16] f32, V scales [16] f32 (32*D + 128 bytes); INT4
  * block: K codes [16][D/2], V codes [D][8] (LSB-first along slots), K then V
- * (scale, zero) binary16 [16][D/32][2] (20*D bytes). */
+ * (scale, zero) binary16 [16][D/32][2] (20*D bytes). D is the stored row
+ * width: head_dim, except 192 for head_dim 168, whose dims 0-83 sit at 0-83
+ * and 84-167 at 96-179 (split-half RoPE pairs (i, i + 96)), the rest 0.
+ * sai_kvcache_read returns the head_dim codes of a row. */
 sai_status sai_kvcache_pool(const sai_kvcache* cache, int32_t layer, void** dev_ptr,
                             size_t* bytes, size_t* block_bytes);
 
@@ -183,8 +187,8 @@ sai_status sai_kv_append(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const 
  * > 0): the query at position p sees keys [p - window, p]; <= 0 = off. A
  * sliding-window layer (sai_kvcache_set_layer_window) sees its last w keys;
  * with both, the narrower span applies. Head dims 64, 128 and 256 for int8
- * and int4, groups 1, 2, 4 and 8 (int4 at 256: up to 4); UNSUPPORTED
- * otherwise. */
+ * and int4, and 168 for int8; groups 1, 2, 4 and 8 (int4 at 256: up to 4);
+ * UNSUPPORTED otherwise. */
 sai_status sai_gqa_decode(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
                           int32_t dtype, int32_t batch, int32_t num_heads,
                           const float* cos_cache, const float* sin_cache, int32_t cache_rows,
@@ -217,7 +221,8 @@ sai_status sai_gqa_with_cache(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, c
  * the library sets up in sai_init and holds until the process ends, instead
  * of the cache's own workspace; nothing is allocated or freed. Limits: at
  * most 65536 (sequence x kv head) pairs, 32768 sequences, and 4,063,232
- * partial floats, i.e. sequence-splits x kv heads x group x (head_dim + 2)
+ * partial floats, i.e. sequence-splits x kv heads x group x (D + 2), D the
+ * stored row width (sai_kvcache_pool)
  * (the Llama-3-8B layer at 16 x 8k uses 133,120); a larger step fails with
  * UNSUPPORTED. Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (other streams, other threads, other contexts) race, and
@@ -237,7 +242,7 @@ sai_status sai_gqa_with_cache_noalloc(sai_ctx* ctx, sai_kvcache* cache, int32_t 
  * Same contract as sai_gqa_decode for a chunk of sq == pending query tokens per
  * sequence (the reference's op_group_query_attention with Sq > 1, causal with
  * past_sk = seq_len[b], microsoft.rs:1156 and :331-337), over an int8 cache
- * or an int4 one (head_dim 64, 128 or 256).
+ * (head_dim 64, 128, 168 or 256) or an int4 one (head_dim 64, 128 or 256).
  * q: device [batch, sq, num_heads*D]; out: device [batch, sq, num_heads*D] of
  * out_dtype (F32 or BF16, as for sai_gqa_decode).
  * window and sliding-window layers as for sai_gqa_decode, applied to every

@@ -29,7 +29,21 @@ __device__ __forceinline__ float rope_pair_elem(float c, float s, float own, flo
   return a + (first ? -b : b);
 }
 
-// x[j] = element lane + 64*j of the row; rotates in place at position `pos`.
+// Stored dim of a row held by lane `lane` as its element j. Up to head_dim
+// 256 that is lane + 64 j. At the stored width 192 (head_dim 168) element 0
+// is dim lane and element 1 its split-half partner lane + 96, while element 2
+// is dim 64 + lane on lanes 0-31 and 128 + lane on lanes 32-63 (dims 64-95
+// and 160-191), whose partners are 32 lanes apart.
+template <int D>
+__device__ __forceinline__ int row_elem(int lane, int j) {
+  if constexpr (D == 192)
+    return j == 0 ? lane : (j == 1 ? lane + 96 : (lane < 32 ? 64 + lane : 128 + lane));
+  else
+    return lane + 64 * j;
+}
+
+// x[j] = element j of the row (row_elem); rotates in place at position `pos`
+// with tables of kLogicalDim<D> / 2 entries per position. Padding dims stay 0.
 // The cos / sin loads come first so that they overlap the row's own loads.
 template <int D>
 __device__ __forceinline__ void rope_row_wave(float (&x)[D / 64], int lane, int pos,
@@ -38,15 +52,18 @@ __device__ __forceinline__ void rope_row_wave(float (&x)[D / 64], int lane, int 
                                               bool interleaved) {
   constexpr int J = D / 64;
   constexpr int HALF = D / 2;
-  const float* cr = cos_cache + (size_t)pos * HALF;
-  const float* sr = sin_cache + (size_t)pos * HALF;
+  constexpr int HL = kLogicalDim<D> / 2;  // table entries per position
+  const float* cr = cos_cache + (size_t)pos * HL;
+  const float* sr = sin_cache + (size_t)pos * HL;
   float c[J], s[J];
-  bool first[J];
+  bool first[J], pad[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int e = lane + 64 * j;
+    const int e = row_elem<D>(lane, j);
+    const int el = logical_dim<D>(e);
     first[j] = interleaved ? (e & 1) == 0 : e < HALF;
-    const int i = interleaved ? (e >> 1) : (first[j] ? e : e - HALF);
+    pad[j] = el < 0;
+    const int i = pad[j] ? 0 : (interleaved ? (el >> 1) : (first[j] ? e : e - HALF));
     c[j] = cr[i];
     s[j] = sr[i];
   }
@@ -54,6 +71,10 @@ __device__ __forceinline__ void rope_row_wave(float (&x)[D / 64], int lane, int 
   if (interleaved) {
 #pragma unroll
     for (int j = 0; j < J; ++j) xp[j] = __shfl_xor(x[j], 1, 64);
+  } else if constexpr (D == 192) {
+    xp[0] = x[1];
+    xp[1] = x[0];
+    xp[2] = __shfl_xor(x[2], 32, 64);
   } else if constexpr (HALF >= 64) {
 #pragma unroll
     for (int j = 0; j < J; ++j) xp[j] = x[j ^ (HALF / 64)];
@@ -62,7 +83,8 @@ __device__ __forceinline__ void rope_row_wave(float (&x)[D / 64], int lane, int 
     for (int j = 0; j < J; ++j) xp[j] = __shfl_xor(x[j], HALF, 64);
   }
 #pragma unroll
-  for (int j = 0; j < J; ++j) x[j] = rope_pair_elem(c[j], s[j], x[j], xp[j], first[j]);
+  for (int j = 0; j < J; ++j)
+    x[j] = pad[j] ? 0.0f : rope_pair_elem(c[j], s[j], x[j], xp[j], first[j]);
 }
 
 // Quantise one row (int8, symmetric, per row) and store it into the page
@@ -81,7 +103,7 @@ __device__ __forceinline__ void quant_store_row_int8(float (&x)[D / 64], int lan
   for (int j = 0; j < J; ++j) {
     int32_t q = sat_i32(rintf(x[j] / sc));
     q = q < -128 ? -128 : (q > 127 ? 127 : q);
-    const int e = lane + 64 * j;
+    const int e = row_elem<D>(lane, j);
     if (which == 0)
       blk[(size_t)slot * D + e] = (uint8_t)(int8_t)q;
     else
@@ -91,8 +113,9 @@ __device__ __forceinline__ void quant_store_row_int8(float (&x)[D / 64], int lan
 }
 
 // Full K+V append of one (token, kv head) row. k_row / v_row point at the
-// row's D elements (f32 or bf16). Every load is issued before the first
-// store, so the row costs one memory round trip.
+// row's kLogicalDim<D> elements (f32 or bf16); padding dims are stored as 0.
+// Every load is issued before the first store, so the row costs one memory
+// round trip.
 template <int D>
 __device__ __forceinline__ void append_row_int8(const void* k_row, const void* v_row, int dtype,
                                                 int lane, int pos, uint8_t* blk, int slot,
@@ -102,8 +125,11 @@ __device__ __forceinline__ void append_row_int8(const void* k_row, const void* v
   float xk[J], xv[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    xk[j] = load_elem(k_row, lane + 64 * j, dtype);
-    xv[j] = load_elem(v_row, lane + 64 * j, dtype);
+    const int el = logical_dim<D>(row_elem<D>(lane, j));
+    const int ec = el < 0 ? 0 : el;
+    xk[j] = load_elem(k_row, ec, dtype);
+    xv[j] = load_elem(v_row, ec, dtype);
+    if (el < 0) xk[j] = xv[j] = 0.0f;
   }
   if (do_rotary) rope_row_wave<D>(xk, lane, pos, cos_cache, sin_cache, interleaved);
   quant_store_row_int8<D>(xk, lane, blk, slot, 0);

@@ -26,8 +26,11 @@
 //         rows j = hi and lo terms of P'), so no LDS transpose.
 //         k index: lane group g, k step ks <-> dims kdim0(g, ks) + [0,16):
 //         (D/4)*g + 16*ks up to head_dim 128, so one row's 4 lane groups read
-//         one contiguous 128-byte line; 16*g + 64*ks at 256, so they read 64
-//         contiguous bytes of the row's two lines per load instruction.
+//         one contiguous 128-byte line; 16*g + 64*ks at the stored widths 192
+//         and 256, so they read 64 contiguous bytes of a longer row per load
+//         instruction. (head_dim 168 runs at the stored width 192: each
+//         84-dim half padded to 96 with zeros; the query, RoPE tables and the
+//         output go through that mapping.)
 //   PV  : O = P' * V.  A = P' codes (row = head-term, k = slots of page g),
 //         B = V codes read dim-major from the page (column = dim).
 //   Online softmax in the log2 domain; cross-page reductions are two
@@ -71,10 +74,58 @@ struct TileRegs {
 // lines per instruction, 32 bytes used of each); 16*g + 64*ks reads 64
 // contiguous bytes (16 lines) and took the gemma-shaped decode from 68.2 to
 // 52.3 us. At 128 the same change measured slower (50.2 -> 52.7 us: the
-// partner chunk held for RoPE spills registers).
+// partner chunk held for RoPE spills registers). The stored width 192 (rows
+// of 1.5 lines) takes 16*g + 64*ks too: 57.5 % of HBM with (D/4)*g + 16*ks.
 template <int D>
 __device__ __forceinline__ constexpr int kdim0(int g, int ks) {
   return D > 128 ? 16 * g + 64 * ks : (D / 4) * g + 16 * ks;
+}
+
+// The 16 query elements of stored dims [c0, c0 + 16) of a row of the caller's
+// kLogicalDim<D> elements (qrow: element offset of the row). At the stored
+// width 192 a chunk may hold padding dims, loaded as 0, and its real dims
+// start at an element offset that is only a multiple of 4: four loads of 4
+// elements each.
+template <int D>
+__device__ __forceinline__ void load_q16(const void* q, size_t qrow, int c0, int dtype,
+                                         float (&x)[16]) {
+  if constexpr (kLogicalDim<D> == D) {
+    load16(q, qrow + c0, dtype, x);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int el = logical_dim<D>(c0 + 4 * k);  // 4 dims, all real or all padding
+      const size_t at = qrow + (el < 0 ? 0 : el);
+      float v[4];
+      if (dtype == kDtypeBf16) {
+        const uint2 w = *(const uint2*)((const uint16_t*)q + at);
+        v[0] = __uint_as_float(w.x << 16), v[1] = __uint_as_float(w.x & 0xFFFF0000u);
+        v[2] = __uint_as_float(w.y << 16), v[3] = __uint_as_float(w.y & 0xFFFF0000u);
+      } else {
+        const float4 f = *(const float4*)((const float*)q + at);
+        v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[4 * k + i] = el < 0 ? 0.0f : v[i];
+    }
+  }
+}
+
+// Per-dim cos / sin of stored dims [c0, c0 + 16) at the stored width 192
+// (tables of 84 entries per position): one load each, padding dims read
+// entry 0 (their values are 0 and stay 0).
+template <int D>
+__device__ __forceinline__ void rope_table16_padded(const float* cr, const float* sr, int c0,
+                                                    bool interleaved, float (&c)[16],
+                                                    float (&s)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int e = c0 + i;
+    const int el = logical_dim<D>(e);
+    const int t = el < 0 ? 0 : (interleaved ? (el >> 1) : (e < D / 2 ? e : e - D / 2));
+    c[i] = cr[t];
+    s[i] = sr[t];
+  }
 }
 
 template <int D, int PART = 3>
@@ -273,10 +324,11 @@ constexpr bool kInt8OneWavePerSimd = G > 4 && D >= 128;
 template <int D, int G, int NW>
 __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void gqa_decode_int8_kernel(
     DecodeParams p) {
-  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
+  static_assert(D == 64 || D == 128 || D == 192 || D == 256, "stored head_dim");
   static_assert(G >= 1 && G <= 8, "group");
   constexpr int KS = D / 64;
   constexpr int JB = D / 16;
+  constexpr int DL = kLogicalDim<D>;  // the caller's rows (q, k_new, v_new, out)
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -300,6 +352,7 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
   const int origin = (k_lo / 64) * 64;
 
   constexpr int HALF = D / 2;
+  constexpr int HL = DL / 2;  // table entries per position
   constexpr int NP = Passes<G>::N;
   // column r = 4*hq + t of the QK product: term t of head 4*pass + hq
   const int tq = r & 3;
@@ -308,9 +361,9 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
 #pragma unroll
   for (int ps = 0; ps < NP; ++ps) {
     const int h = 4 * ps + (r >> 2);
-    const size_t qbase = ((size_t)b * Hq + kvh * G + (h < G ? h : 0)) * D;
+    const size_t qbase = ((size_t)b * Hq + kvh * G + (h < G ? h : 0)) * DL;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) load16(p.q, qbase + kdim0<D>(g, ks), p.q_dtype, xq[ps][ks]);
+    for (int ks = 0; ks < KS; ++ks) load_q16<D>(p.q, qbase, kdim0<D>(g, ks), p.q_dtype, xq[ps][ks]);
   }
   const int t_begin = origin + split * tps * 64;
   const int t_end = min(L, t_begin + tps * 64);
@@ -322,14 +375,15 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
   __syncthreads();
 
   // cos / sin of position L-1: issued ahead of the first tile, so the query's
-  // RoPE only waits for them and not for the tile (head_dim 256 loads them per
-  // chunk in the RoPE loop and its first tile after the query: the registers
-  // of both would not fit)
+  // RoPE only waits for them and not for the tile (the stored widths 192 and
+  // 256 load them per chunk in the RoPE loop and their first tile after the
+  // query: the registers of both would not fit)
   constexpr bool BIG = D > 128;
+  constexpr bool WIDE = D == 256;  // split-half partners in the lane's own chunks
   float4 cq[BIG ? 1 : KS][4], sq[BIG ? 1 : KS][4];
   if (!BIG && p.do_rotary) {
-    const float* cr = p.cos_cache + (size_t)(L - 1) * HALF;
-    const float* sr = p.sin_cache + (size_t)(L - 1) * HALF;
+    const float* cr = p.cos_cache + (size_t)(L - 1) * HL;
+    const float* sr = p.sin_cache + (size_t)(L - 1) * HL;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) rope_load16<D>(cr, sr, kdim0<D>(g, ks), p.interleaved, cq[ks], sq[ks]);
   }
@@ -359,7 +413,7 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
     uint8_t* blk = (uint8_t*)p.pool +
                    block_offset(sm_pg[pos / kPageTokens - first_page], kvh, p.num_pages,
                                 block_bytes_int8(D));
-    const size_t row = ((size_t)b * p.kv_heads + kvh) * D * (p.kv_dtype == kDtypeBf16 ? 2 : 4);
+    const size_t row = ((size_t)b * p.kv_heads + kvh) * DL * (p.kv_dtype == kDtypeBf16 ? 2 : 4);
     append_row_int8<D>((const uint8_t*)p.k_new + row, (const uint8_t*)p.v_new + row, p.kv_dtype,
                        lane, pos, blk, pos % kPageTokens, p.do_rotary, p.interleaved != 0,
                        p.cos_cache, p.sin_cache);
@@ -424,7 +478,10 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
       if (p.do_rotary) {
         float y[16];
         float cc[16], ss[16];
-        if constexpr (BIG) {
+        if constexpr (DL != D) {
+          rope_table16_padded<D>(p.cos_cache + (size_t)(L - 1) * HL,
+                                 p.sin_cache + (size_t)(L - 1) * HL, c0, p.interleaved != 0, cc, ss);
+        } else if constexpr (BIG) {
           float4 lc[4], ls[4];
           rope_load16<D>(p.cos_cache + (size_t)(L - 1) * HALF, p.sin_cache + (size_t)(L - 1) * HALF,
                          c0, p.interleaved, lc, ls);
@@ -435,12 +492,19 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           // split-half partner d +- D/2: up to head_dim 128 the same element
-          // of lane g ^ 2 (32 lanes away; permlane32_swap(x, x) gives [0] =
-          // lanes 0-31's x, [1] = lanes 32-63's x on both halves); at 256 the
-          // same lane's chunk ks ^ 2
+          // of lane g ^ 2 (32 lanes away; permlane32_swap(a, b) gives [1] =
+          // a of lanes 32-63 on lanes 0-31, [0] = b of lanes 0-31 on lanes
+          // 32-63); at 256 the same lane's chunk ks ^ 2; at the stored width
+          // 192 chunk (ks + 1) % 3 of lane group g + 2 for g < 2 and chunk
+          // (ks + 2) % 3 of lane group g - 2 for g >= 2
           float half_partner;
-          if constexpr (BIG) {
+          if constexpr (WIDE) {
             half_partner = xq[ps][ks ^ 2][i];
+          } else if constexpr (D == 192) {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(xq[ps][(ks + 1) % 3][i]),
+                                                       __float_as_uint(xq[ps][(ks + 2) % 3][i]),
+                                                       false, false);
+            half_partner = __uint_as_float(g < 2 ? sw[1] : sw[0]);
           } else {
             auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i]),
                                                        __float_as_uint(x[i]), false, false);
@@ -449,6 +513,8 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
           const float partner = p.interleaved ? x[i ^ 1] : half_partner;
           const bool first = p.interleaved ? (i & 1) == 0 : c0 < HALF;
           y[i] = rope_elem(cc[i], ss[i], x[i], partner, first);
+          // padding dims stay 0 whatever the table holds
+          if constexpr (DL != D) y[i] = logical_dim<D>(c0 + i) < 0 ? 0.0f : y[i];
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) x[i] = y[i];
@@ -595,8 +661,11 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
       Ls += sm_l[w][hd] * f;
       O += sm_o[w][hd][d] * f;
     }
+    const int dl = logical_dim<D>(d);  // -1: a padding dim, not written
     if (nsplit == 1) {
-      store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * D + d, Ls > 0.0f ? O / Ls : 0.0f, p.out_bf16);
+      if (dl >= 0)
+        store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * DL + dl, Ls > 0.0f ? O / Ls : 0.0f,
+                  p.out_bf16);
     } else if (p.merge_in_kernel) {
       store_partial(part + hd * (D + 2) + 2 + d, O);
       if (d == 0) {
@@ -651,7 +720,10 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
       merge_partials<4>(ph, stride, d, nsplit, -1, M, Ls, O);
     else
       merge_partials<8>(ph, stride, d, nsplit, -1, M, Ls, O);
-    store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * D + d, Ls > 0.0f ? O / Ls : 0.0f, p.out_bf16);
+    const int dl = logical_dim<D>(d);
+    if (dl >= 0)
+      store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * DL + dl, Ls > 0.0f ? O / Ls : 0.0f,
+                p.out_bf16);
   }
   if (threadIdx.x == 0) reset_ticket(counter);
 }
@@ -712,7 +784,10 @@ __global__ __launch_bounds__((kCombineThreads<D, G>)) void gqa_decode_combine_ke
     }
     M = mb;
   }
-  store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * D + d, Ls > 0.0f ? O / Ls : 0.0f, p.out_bf16);
+  const int dl = logical_dim<D>(d);
+  if (dl >= 0)
+    store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * kLogicalDim<D> + dl,
+              Ls > 0.0f ? O / Ls : 0.0f, p.out_bf16);
   }
 }
 
@@ -777,6 +852,7 @@ hipError_t launch_decode_combine(const DecodeParams& p, int head_dim, int group,
   if (head_dim == 64) return by_group(std::integral_constant<int, 64>{});
   if (head_dim == 128) return by_group(std::integral_constant<int, 128>{});
   if (head_dim == 256) return by_group(std::integral_constant<int, 256>{});
+  if (head_dim == 168) return by_group(std::integral_constant<int, 192>{});
   return hipErrorInvalidValue;
 }
 
@@ -790,6 +866,7 @@ hipError_t launch_gqa_decode(const DecodeParams& p, int head_dim, int group, int
   if (head_dim == 64) return launch_d<64>(p, group, work_items, combine, st);
   if (head_dim == 128) return launch_d<128>(p, group, work_items, combine, st);
   if (head_dim == 256) return launch_d<256>(p, group, work_items, combine, st);
+  if (head_dim == 168) return launch_d<192>(p, group, work_items, combine, st);
   return hipErrorInvalidValue;
 }
 

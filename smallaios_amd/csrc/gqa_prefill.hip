@@ -403,7 +403,8 @@ __device__ __forceinline__ void stage_store4(const TileStage4<D, NT>& S, Prefill
 }
 
 // RB row blocks of 16 attention rows per wave: 2 up to head_dim 128, 1 at
-// 256 (the query pair and the accumulators of two blocks would not fit).
+// the stored widths 192 and 256 (the query pair and the accumulators of two
+// blocks would not fit).
 // PREC: the int8 precise pass (see the tile loop below): only workgroups
 // whose flag the fast pass set run, from their first tile.
 template <int D, int G, int NW, int Q, bool PREC>
@@ -418,6 +419,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   constexpr int KROW = Tile::KROW;
   constexpr int VROW = Tile::VROW;
   constexpr int HALF = D / 2;
+  constexpr int DL = kLogicalDim<D>;  // the caller's rows (q, out)
+  constexpr int HL = DL / 2;          // table entries per position
 
   // int8 at head_dim <= 128 keeps four tiles in LDS and computes two per
   // barrier (4 x 38.4 KB at 128); int4 up to 128 and int8 at 256 keep two;
@@ -498,12 +501,18 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
     const int i = il < p.sq ? il : p.sq - 1;
     const int pos = past + i;
     qpos[rb] = il < p.sq ? pos : -1;
-    const size_t qbase = (((size_t)b * p.sq + i) * Hq + hq) * D;
+    const size_t qbase = (((size_t)b * p.sq + i) * Hq + hq) * DL;
     float x[KS][8];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[ks][e] = load_elem(p.q, qbase + 32 * ks + 8 * g + e, p.q_dtype);
+      for (int e = 0; e < 8; ++e) {
+        // stored dim -> the caller's dim (padding dims of the stored width
+        // 192 are 0)
+        const int dl = logical_dim<D>(32 * ks + 8 * g + e);
+        x[ks][e] = load_elem(p.q, qbase + (dl < 0 ? 0 : dl), p.q_dtype);
+        if (dl < 0) x[ks][e] = 0.0f;
+      }
     if (p.do_rotary) {
       // partners: interleaved d ^ 1 (same chunk); split-half d +- D/2 (chunk
       // ks +- KS/2, the same lane)
@@ -513,11 +522,13 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int d = 32 * ks + 8 * g + e;
+          const int dl = logical_dim<D>(d);
           const bool first = p.interleaved ? (e & 1) == 0 : d < HALF;
-          const int pi = p.interleaved ? (d >> 1) : (first ? d : d - HALF);
+          const int pi = dl < 0 ? 0 : (p.interleaved ? (dl >> 1) : (first ? d : d - HALF));
           const float partner = p.interleaved ? x[ks][e ^ 1] : x[(ks + KS / 2) % KS][e];
-          y[ks][e] = rope_elem(p.cos_cache[(size_t)pos * HALF + pi],
-                               p.sin_cache[(size_t)pos * HALF + pi], x[ks][e], partner, first);
+          y[ks][e] = rope_elem(p.cos_cache[(size_t)pos * HL + pi],
+                               p.sin_cache[(size_t)pos * HL + pi], x[ks][e], partner, first);
+          if (dl < 0) y[ks][e] = 0.0f;
         }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
@@ -913,12 +924,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       const int il = q0 + R / G;
       if (il >= p.sq) continue;
       const int hq = kvh * G + R % G;
-      const size_t o = (((size_t)b * p.sq + il) * Hq + hq) * D;
+      const size_t o = (((size_t)b * p.sq + il) * Hq + hq) * DL;
       // acc is in units of 2^(vexp_run - kPrecLift) in the precise pass (exact)
       const float f =
           l > 0.0f ? __builtin_ldexpf(1.0f / l, PREC ? vexp_run - kPrecLift : 0) : 0.0f;
 #pragma unroll
-      for (int jb = 0; jb < JB; ++jb) store_out(p.out, o + 16 * jb + r, acc[rb][jb][e] * f, p.out_bf16);
+      for (int jb = 0; jb < JB; ++jb) {
+        const int dl = logical_dim<D>(16 * jb + r);  // -1: padding, not written
+        if (dl >= 0) store_out(p.out, o + dl, acc[rb][jb][e] * f, p.out_bf16);
+      }
     }
   }
 }
@@ -977,6 +991,8 @@ hipError_t launch_gqa_prefill(const PrefillParams& p, int head_dim, int group, i
   if (head_dim == 256)
     return quant == kQuantInt8 ? launch_dn<256, 8, kQuantInt8>(p, group, st)
                                : launch_dn<256, 8, kQuantInt4>(p, group, st);
+  // head_dim 168: the stored width 192, int8 only
+  if (head_dim == 168 && quant == kQuantInt8) return launch_dn<192, 8, kQuantInt8>(p, group, st);
   return hipErrorInvalidValue;
 }
 

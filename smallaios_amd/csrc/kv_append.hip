@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void kv_append_int8_kernel(AppendParams p) {
   const int pos = p.seq_lens[b] + s;
   const int page = p.page_table[(size_t)b * p.max_pages + pos / kPageTokens];
   uint8_t* blk = p.pool + block_offset(page, h, p.num_pages, block_bytes_int8(D));
-  const size_t src = (size_t)row * D;  // [b][s][h][D] == row * D
+  const size_t src = (size_t)row * kLogicalDim<D>;  // [b][s][h][head_dim]
   const size_t esz = p.dtype == kDtypeBf16 ? 2 : 4;
   append_row_int8<D>((const uint8_t*)p.k + src * esz, (const uint8_t*)p.v + src * esz, p.dtype,
                      lane, pos, blk, pos % kPageTokens, p.do_rotary, p.interleaved != 0,
@@ -53,12 +53,14 @@ __global__ __launch_bounds__(256) void kv_append_int8_kernel(AppendParams p) {
 
 // ---------------------------------------------------- int8, page blocks ----
 // Multi-token appends: one workgroup per (sequence b, page, kv head h) block
-// that receives new tokens, W = D/32 waves. Each wave takes G = 64/L slots,
-// one per group of L = D/8 lanes (wave w, group g: slot g*W + w). Lane c of
-// a group holds dims [4c, 4c+4) and [D/2 + 4c, D/2 + 4c + 4): both elements
-// of every split-half RoPE pair, and whole interleaved pairs, so RoPE needs
-// no other lane; a token's absolute maximum is a reduction over its group
-// (DPP within rows of 16 lanes, permlane16_swap across two rows). The codes
+// that receives new tokens, W = 16 L / 64 waves. Each wave takes 64/L slots,
+// one per group of L lanes (wave w, group g: slot g*W + w); L = D/8, or 32 at
+// the stored width 192. Lane c of a group holds stored dims [4c, 4c+4) and
+// [D/2 + 4c, D/2 + 4c + 4): both elements of every split-half RoPE pair, and
+// whole interleaved pairs, so RoPE needs no other lane (at width 192, lanes
+// 21-23 hold the padding dims as zeros and lanes 24-31 nothing); a token's
+// absolute maximum is a reduction over its group (DPP within rows of 16
+// lanes, permlane16_swap across two rows). The codes
 // are staged in LDS (K rows with a 16-byte pad, V as one 16-byte column per
 // dim, placed so that one instruction's writes fall in distinct banks) and
 // leave it in 16-byte stores, one per thread: K rows as contiguous pieces of
@@ -165,12 +167,21 @@ __device__ __forceinline__ uint32_t quant4_int8(const float (&x)[4], float s, fl
 // ROPE: 0 none, 1 split halves (d, d + D/2), 2 interleaved (2i, 2i + 1).
 // Grid (kv_heads, pages_per_seq, batch). The launch keeps s_new * kv_heads *
 // D * 4 (the byte offset of a row within a sequence's new K or V) below 2^31.
+template <int D>
+constexpr int kPageLanes = D == 192 ? 32 : D / 8;  // lanes per token (a power of two)
+template <int D>
+constexpr int kPageThreads = kPageTokens * kPageLanes<D>;  // 2 D up to 256, 512 at 192
+
 template <int D, bool BF16, int ROPE>
-__global__ __launch_bounds__(2 * D) void kv_append_page_int8_kernel(AppendParams p) {
-  constexpr int L = D / 8;            // lanes per token
-  constexpr int W = D / 32;           // waves: kPageTokens / (64 / L)
+__global__ __launch_bounds__(kPageThreads<D>) void kv_append_page_int8_kernel(AppendParams p) {
+  constexpr int L = kPageLanes<D>;
+  constexpr int W = kPageThreads<D> / 64;  // waves: kPageTokens / (64 / L)
+  constexpr int DL = kLogicalDim<D>;        // the caller's row width
   constexpr int HALF = D / 2;
-  constexpr int KS = D + 16;          // LDS K row stride (bytes)
+  constexpr int HL = DL / 2;                // table entries per position
+  constexpr int CS = D / 8;                 // lanes holding stored dims
+  constexpr int CL = DL / 8;                // lanes holding the caller's dims
+  constexpr int KS = D + 16;                // LDS K row stride (bytes)
   constexpr uint32_t ESZ = BF16 ? 2 : 4;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -185,31 +196,35 @@ __global__ __launch_bounds__(2 * D) void kv_append_page_int8_kernel(AppendParams
   uint8_t* blk = p.pool + block_offset(page, h, p.num_pages, block_bytes_int8(D));
   const bool partial = lo > 0 || hi < kPageTokens;
 
-  // threads D .. 2D-1 (waves W/2 ..) store V column tid - D: the old column
-  // of a partial page first, so that its latency overlaps the work below
+  // threads D .. 2D-1 (waves from D/64 on) store V column tid - D: the old
+  // column of a partial page first, so that its latency overlaps the work below
+  const bool v_thread = tid >= D && tid < 2 * D;  // wave-uniform
   uint4 vold = uint4{0u, 0u, 0u, 0u};
-  if (partial && w >= W / 2) vold = *(const uint4*)(blk + (size_t)16 * D + (size_t)(tid - D) * 16);
+  if (partial && v_thread) vold = *(const uint4*)(blk + (size_t)16 * D + (size_t)(tid - D) * 16);
 
   const int c = lane % L, g = lane / L;
   const int t = g * W + w;  // this group's slot
+  // lanes past the caller's dims read lane CL-1's (and then hold zeros)
+  const bool real = c < CL;
+  const int cr = real ? c : CL - 1;
   // a slot outside the new range reads the nearest new row (its codes are
   // never stored), so every address stays inside the inputs
   const uint32_t srow = (uint32_t)min(max(t0 + t - start, 0), p.s_new - 1);
-  const size_t row0 = ((size_t)b * p.s_new * p.kv_heads + h) * D * ESZ;  // (b, token 0, h)
+  const size_t row0 = ((size_t)b * p.s_new * p.kv_heads + h) * DL * ESZ;  // (b, token 0, h)
   const uint8_t* kbase = (const uint8_t*)p.k + row0;
   const uint8_t* vbase = (const uint8_t*)p.v + row0;
-  const uint32_t off = (srow * (uint32_t)p.kv_heads * D + 4 * c) * ESZ;  // bytes
+  const uint32_t off = (srow * (uint32_t)p.kv_heads * DL + 4 * cr) * ESZ;  // bytes
   float xa[4], xb[4], va[4], vb[4];
   load4<BF16>(kbase, off, xa);
-  load4<BF16>(kbase, off + HALF * ESZ, xb);
+  load4<BF16>(kbase, off + HL * ESZ, xb);
   load4<BF16>(vbase, off, va);
-  load4<BF16>(vbase, off + HALF * ESZ, vb);
+  load4<BF16>(vbase, off + HL * ESZ, vb);
   // the tables' rows from position start on
-  const uint8_t* cos0 = (const uint8_t*)(p.cos_cache + (size_t)start * HALF);
-  const uint8_t* sin0 = (const uint8_t*)(p.sin_cache + (size_t)start * HALF);
+  const uint8_t* cos0 = (const uint8_t*)(p.cos_cache + (size_t)start * HL);
+  const uint8_t* sin0 = (const uint8_t*)(p.sin_cache + (size_t)start * HL);
   if constexpr (ROPE == 1) {
     // dims 4c + j and HALF + 4c + j share table entry 4c + j
-    const uint32_t o = (srow * HALF + 4 * c) * 4;
+    const uint32_t o = (srow * HL + 4 * cr) * 4;
     const float4 cv = *(const float4*)(cos0 + o);
     const float4 sv = *(const float4*)(sin0 + o);
     const float ca[4] = {cv.x, cv.y, cv.z, cv.w}, sa[4] = {sv.x, sv.y, sv.z, sv.w};
@@ -220,12 +235,12 @@ __global__ __launch_bounds__(2 * D) void kv_append_page_int8_kernel(AppendParams
       xb[j] = rope_pair_elem(ca[j], sa[j], x1, x0, false);
     }
   } else if constexpr (ROPE == 2) {
-    // pair (2i, 2i + 1) uses entry i: 2c, 2c + 1 and HALF/2 + 2c, + 1
-    const uint32_t o = (srow * HALF + 2 * c) * 4;
+    // pair (2i, 2i + 1) uses entry i: 2c, 2c + 1 and HL/2 + 2c, + 1
+    const uint32_t o = (srow * HL + 2 * cr) * 4;
     const float2 c0 = *(const float2*)(cos0 + o);
     const float2 s0 = *(const float2*)(sin0 + o);
-    const float2 c1 = *(const float2*)(cos0 + o + HALF * 2);
-    const float2 s1 = *(const float2*)(sin0 + o + HALF * 2);
+    const float2 c1 = *(const float2*)(cos0 + o + HL * 2);
+    const float2 s1 = *(const float2*)(sin0 + o + HL * 2);
     const float ca[2] = {c0.x, c0.y}, sa[2] = {s0.x, s0.y};
     const float cb[2] = {c1.x, c1.y}, sb[2] = {s1.x, s1.y};
 #pragma unroll
@@ -236,6 +251,12 @@ __global__ __launch_bounds__(2 * D) void kv_append_page_int8_kernel(AppendParams
       x0 = xb[2 * e], x1 = xb[2 * e + 1];
       xb[2 * e] = rope_pair_elem(cb[e], sb[e], x0, x1, true);
       xb[2 * e + 1] = rope_pair_elem(cb[e], sb[e], x1, x0, false);
+    }
+  }
+  if constexpr (CL < L) {
+    if (!real) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xa[j] = xb[j] = va[j] = vb[j] = 0.0f;
     }
   }
   // fmaxf from 0 skips NaN elements, as in append_row_int8: the lane maxima
@@ -259,13 +280,15 @@ __global__ __launch_bounds__(2 * D) void kv_append_page_int8_kernel(AppendParams
 
   __shared__ __align__(16) uint8_t sm_k[kPageTokens * KS];
   __shared__ __align__(16) uint8_t sm_v[kPageTokens * D];  // column d at 16 d
-  *(uint32_t*)&sm_k[t * KS + 4 * c] = ka;
-  *(uint32_t*)&sm_k[t * KS + HALF + 4 * c] = kb;
-  uint8_t* vcol = &sm_v[64 * c + t];  // dim 4c, slot t
+  if (CS == L || c < CS) {
+    *(uint32_t*)&sm_k[t * KS + 4 * c] = ka;
+    *(uint32_t*)&sm_k[t * KS + HALF + 4 * c] = kb;
+    uint8_t* vcol = &sm_v[64 * c + t];  // dim 4c, slot t
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    vcol[16 * j] = (uint8_t)(qa >> (8 * j));
-    vcol[16 * (HALF + j)] = (uint8_t)(qb >> (8 * j));
+    for (int j = 0; j < 4; ++j) {
+      vcol[16 * j] = (uint8_t)(qa >> (8 * j));
+      vcol[16 * (HALF + j)] = (uint8_t)(qb >> (8 * j));
+    }
   }
   if (t >= lo && t < hi) {
     if (c == 0) ((float*)(blk + 32 * D))[t] = sk;
@@ -273,13 +296,13 @@ __global__ __launch_bounds__(2 * D) void kv_append_page_int8_kernel(AppendParams
   }
   __syncthreads();
 
-  if (w < W / 2) {
+  if (tid < D) {
     // K: 16-byte piece tid of the 16 rows, stored when its row is new
     constexpr int CHUNKS = D / 16;  // pieces of a row
     const int tr = tid / CHUNKS;
     const uint4 v = *(const uint4*)&sm_k[tr * KS + 16 * (tid % CHUNKS)];
     if (tr >= lo && tr < hi) *(uint4*)(blk + (size_t)tid * 16) = v;
-  } else {
+  } else if (v_thread) {
     // V: column d (16 slots), new slots from the tile, on a partial page the
     // others kept
     const int d = tid - D;
@@ -635,11 +658,11 @@ __global__ void seq_advance_kernel(int32_t* seq_lens, int batch, int pending) {
 template <int D, bool BF16>
 void launch_page_int8_dt(dim3 grid, hipStream_t st, const AppendParams& p, int rope) {
   if (rope == 0)
-    hipLaunchKernelGGL((kv_append_page_int8_kernel<D, BF16, 0>), grid, dim3(2 * D), 0, st, p);
+    hipLaunchKernelGGL((kv_append_page_int8_kernel<D, BF16, 0>), grid, dim3(kPageThreads<D>), 0, st, p);
   else if (rope == 1)
-    hipLaunchKernelGGL((kv_append_page_int8_kernel<D, BF16, 1>), grid, dim3(2 * D), 0, st, p);
+    hipLaunchKernelGGL((kv_append_page_int8_kernel<D, BF16, 1>), grid, dim3(kPageThreads<D>), 0, st, p);
   else
-    hipLaunchKernelGGL((kv_append_page_int8_kernel<D, BF16, 2>), grid, dim3(2 * D), 0, st, p);
+    hipLaunchKernelGGL((kv_append_page_int8_kernel<D, BF16, 2>), grid, dim3(kPageThreads<D>), 0, st, p);
 }
 
 template <int D>
@@ -695,6 +718,10 @@ hipError_t launch_kv_append(const AppendParams& p, int head_dim, int quant, hipS
         return hipErrorInvalidValue;
       return hipGetLastError();
     };
+    if (quant == kQuantInt8 && head_dim == 168) {
+      launch_page_int8<192>(grid, st, p, bf, rope);
+      return hipGetLastError();
+    }
     if (quant == kQuantInt8)
       return by_dim(launch_page_int8<64>, launch_page_int8<128>, launch_page_int8<256>);
     return by_dim(launch_page_int4<64>, launch_page_int4<128>, launch_page_int4<256>);
@@ -708,6 +735,8 @@ hipError_t launch_kv_append(const AppendParams& p, int head_dim, int quant, hipS
       hipLaunchKernelGGL(kv_append_int8_kernel<128>, grid, dim3(256), 0, st, p);
     else if (head_dim == 256)
       hipLaunchKernelGGL(kv_append_int8_kernel<256>, grid, dim3(256), 0, st, p);
+    else if (head_dim == 168)
+      hipLaunchKernelGGL(kv_append_int8_kernel<192>, grid, dim3(256), 0, st, p);
     else
       return hipErrorInvalidValue;
     return hipGetLastError();

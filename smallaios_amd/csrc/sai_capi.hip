@@ -161,10 +161,13 @@ float sqrt_f32_newton(float x) {
 // Largest decode split (the kernel stages a split's page ids in LDS).
 constexpr int32_t kMaxDecodeSplit = 16384;
 
-// int8 and int4: head_dim 64, 128 and 256 (Gemma 3).
+// int8 and int4: head_dim 64, 128 and 256 (Gemma 3); int8 also 168 (Gemma 4
+// 31B), stored as 192 (sai::stored_head_dim). int4's groups of 32 do not
+// divide 168.
 bool supported_dims(int head_dim, int quant) {
   if (quant == SAI_KV_INT8 || quant == SAI_KV_INT4)
-    return head_dim == 64 || head_dim == 128 || head_dim == 256;
+    return head_dim == 64 || head_dim == 128 || head_dim == 256 ||
+           (head_dim == 168 && quant == SAI_KV_INT8);
   return false;
 }
 
@@ -470,8 +473,8 @@ SAI_API sai_status sai_kvcache_create(sai_ctx* ctx, const sai_kvcache_desc* desc
   sai_kvcache* c = new (std::nothrow) sai_kvcache();
   if (!c) return fail(ctx, SAI_ERR_ALLOC, "kv_cache_allocate: host");
   c->desc = d;
-  c->block_bytes = d.quant == SAI_KV_INT8 ? sai::block_bytes_int8(d.head_dim)
-                                          : sai::block_bytes_int4(d.head_dim);
+  const int ds = sai::stored_head_dim(d.head_dim);
+  c->block_bytes = d.quant == SAI_KV_INT8 ? sai::block_bytes_int8(ds) : sai::block_bytes_int4(ds);
   c->pool_bytes = (size_t)d.num_pages * d.num_kv_heads * c->block_bytes;
   c->pools.assign(d.num_layers, nullptr);
   hipError_t e = hipSuccess;
@@ -495,7 +498,7 @@ SAI_API sai_status sai_kvcache_create(sai_ctx* ctx, const sai_kvcache_desc* desc
   // the decode workspace for every launch at the automatic split
   const size_t work = decode_work_bound(ctx, d);
   sai_status st = reserve_workspace(
-      ctx, c->ws, work * d.num_kv_heads * max_decode_group(d.head_dim, d.quant) * (d.head_dim + 2),
+      ctx, c->ws, work * d.num_kv_heads * max_decode_group(d.head_dim, d.quant) * (ds + 2),
       (size_t)d.max_batch * 2, (size_t)d.max_batch * d.num_kv_heads);
   if (st != SAI_OK) {
     sai_kvcache_destroy(c);
@@ -653,6 +656,7 @@ SAI_API sai_status sai_kvcache_read(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
     if (es != hipSuccess) return hip_fail(ctx, es, "kvcache_read");
   }
   const int D = d.head_dim;
+  const int DS = sai::stored_head_dim(D);  // the block's row width
   std::vector<uint8_t> blk(c->block_bytes);
   const int NG = D / 32;
   for (int t = t0; t < t0 + n_tokens; ++t) {
@@ -667,11 +671,15 @@ SAI_API sai_status sai_kvcache_read(sai_ctx* ctx, sai_kvcache* c, int32_t layer,
       if (e != hipSuccess) return hip_fail(ctx, e, "kvcache_read");
     }
     if (d.quant == SAI_KV_INT8) {
-      if (k_codes) std::memcpy((int8_t*)k_codes + (size_t)i * D, blk.data() + (size_t)slot * D, D);
-      if (v_codes)
-        for (int e = 0; e < D; ++e) ((int8_t*)v_codes)[(size_t)i * D + e] = (int8_t)blk[16 * D + e * 16 + slot];
-      if (k_params) std::memcpy((float*)k_params + i, blk.data() + 32 * D + 4 * slot, 4);
-      if (v_params) std::memcpy((float*)v_params + i, blk.data() + 32 * D + 64 + 4 * slot, 4);
+      // stored dim e -> the caller's dim (padding dims of the width 192 skipped)
+      for (int e = 0; e < DS; ++e) {
+        const int el = DS == D ? e : sai::logical_dim<192>(e);
+        if (el < 0) continue;
+        if (k_codes) ((int8_t*)k_codes)[(size_t)i * D + el] = (int8_t)blk[(size_t)slot * DS + e];
+        if (v_codes) ((int8_t*)v_codes)[(size_t)i * D + el] = (int8_t)blk[16 * DS + e * 16 + slot];
+      }
+      if (k_params) std::memcpy((float*)k_params + i, blk.data() + 32 * DS + 4 * slot, 4);
+      if (v_params) std::memcpy((float*)v_params + i, blk.data() + 32 * DS + 64 + 4 * slot, 4);
     } else {
       if (k_codes) std::memcpy((uint8_t*)k_codes + (size_t)i * (D / 2), blk.data() + (size_t)slot * (D / 2), D / 2);
       if (v_codes) {
@@ -845,7 +853,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   // the cache's own workspace (sized at creation for the automatic split; a
   // smaller split set for tuning may grow it once, synchronously), or a fixed
   // one that cannot grow
-  const size_t need_partials = (size_t)work * kvh * G * (D + 2);
+  const size_t need_partials = (size_t)work * kvh * G * (sai::stored_head_dim(D) + 2);
   DecodeWorkspace* ws = &c->ws;
   if (fixed_ws) {
     if (need_partials > fixed_ws->partial_floats || (size_t)batch * 2 > fixed_ws->seq_info_n ||

@@ -5,7 +5,7 @@
 // form one contiguous stream for the decode workgroup that reads them:
 //   block(p, h) = pool + (h * num_pages + p) * block_bytes
 //
-// INT8 block, D = head_dim, 16 tokens:
+// INT8 block, D = stored_head_dim(head_dim) (below), 16 tokens:
 //   [0,        16*D)        K codes, row-major [slot][D]        (int8)
 //   [16*D,     32*D)        V codes, transposed [D][slot]       (int8)
 //   [32*D,     32*D+64)     K scales [slot]                     (f32)
@@ -35,6 +35,32 @@ constexpr int kQuantInt4 = 2;
 constexpr int kDtypeF32 = 1;
 constexpr int kDtypeF16 = 10;
 constexpr int kDtypeBf16 = 16;
+
+// Stored width of a head's rows in the cache and in the kernels' tiles.
+// head_dim 168 (Gemma 4 31B) is stored as 192: each 84-dim half of the
+// split-half RoPE pairing gets 12 zero dims after it, so the kernels keep
+// whole 16-dim chunks, the pair (i, i + 84) sits at (i, i + 96), interleaved
+// pairs stay adjacent, and the zeros change neither a row's int8 scale nor
+// any dot product. Every other head_dim is stored as it is.
+__host__ __device__ constexpr int stored_head_dim(int head_dim) {
+  return head_dim == 168 ? 192 : head_dim;
+}
+// The head_dim a stored width D serves.
+template <int D>
+constexpr int kLogicalDim = D == 192 ? 168 : D;
+// Dim of the caller's row held by stored dim e of a D-wide row; -1 for a
+// padding dim.
+template <int D>
+__host__ __device__ constexpr int logical_dim(int e) {
+  constexpr int DL = kLogicalDim<D>;
+  if constexpr (DL == D) {
+    return e;
+  } else {
+    const int h = e >= D / 2 ? 1 : 0;
+    const int i = e - h * (D / 2);
+    return i < DL / 2 ? i + h * (DL / 2) : -1;
+  }
+}
 
 __host__ __device__ constexpr size_t block_bytes_int8(int d) { return (size_t)32 * d + 128; }
 __host__ __device__ constexpr size_t block_bytes_int4(int d) { return (size_t)20 * d; }

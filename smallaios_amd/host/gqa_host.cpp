@@ -317,7 +317,9 @@ Result<GpuKvCache, HipError> GpuKvCache::allocate(RocmRuntime& rt, size_t num_la
   const sai_status st = sai_kvcache_create(rt.raw(), &d, &c.cache_);
   if (st == SAI_ERR_UNSUPPORTED) return HipError::runtime("kv_cache_allocate:unsupported_head_dim", st);
   if (st == SAI_ERR_ALLOC) {
-    const size_t per = quant == KvQuant::Int8 ? 32 * head_dim + 128 : 20 * head_dim;
+    // block bytes at the stored row width (head_dim 168 is stored 192 wide)
+    const size_t sd = head_dim == 168 ? 192 : head_dim;
+    const size_t per = quant == KvQuant::Int8 ? 32 * sd + 128 : 20 * sd;
     return HipError::alloc_failed(num_layers * (size_t)d.num_pages * num_kv_heads * per, st);
   }
   if (st != SAI_OK) return HipError::runtime("kv_cache_allocate", st);

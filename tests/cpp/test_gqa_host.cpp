@@ -334,6 +334,9 @@ void gpu_cache_errors() {
                               "window")) == "kv_cache_allocate:sliding_window", "sliding_window 0");
   REQUIRE(op_of(must_fail_hip(GpuKvCache::allocate(rt, 1, 2, 16, 8, KvQuant::Int8, {LayerKind::global()}),
                               "head_dim")) == "kv_cache_allocate:unsupported_head_dim", "head_dim");
+  // int4's groups of 32 do not divide 168 (int8 takes it)
+  REQUIRE(op_of(must_fail_hip(GpuKvCache::allocate(rt, 1, 2, 168, 8, KvQuant::Int4, {LayerKind::global()}),
+                              "int4 168")) == "kv_cache_allocate:unsupported_head_dim", "int4 head_dim 168");
   GpuKvCache cache = must(GpuKvCache::allocate(rt, 1, 2, 64, 2, KvQuant::Int8, {LayerKind::global()}),
                           "allocate");
   DeviceTensor k = fill_tensor(2, 64, 1.0f);
@@ -1354,6 +1357,15 @@ void gpu_session_bf16_chain() {
 // over 4 kv heads, head_dim 256, rope_theta 1e6.
 void gpu_session_gemma3_head256() { gemma_graph_session(8, 4, 256, 1000000.0, 62); }
 
+// Gemma 4 31B's attention shape (model_loader/config.rs:720-737): 32 query
+// heads over 8 kv heads, head_dim 168 (the cache stores it 192 wide),
+// rope_theta 1e6; and the CPU op's cache path at head_dim 168.
+void gpu_session_gemma4_head168() { gemma_graph_session(32, 8, 168, 1000000.0, 63); }
+void gpu_cpu_op_gqa_head168() {
+  cpu_op_case(false, 2, 32, 8, 168, 1, 37, true, false, false, 45);   // decode step
+  cpu_op_case(false, 1, 32, 8, 168, 40, 70, true, true, false, 46);   // chunk over a past
+}
+
 // GpuCompressedKvCache (CompressedKVCache, kv_compression.rs:738-963) with the
 // low-rank K on: two sequences x two kv heads, head_dim 128, 4-bit + QJL, a
 // 520-row pass (the low-rank state re-decomposes at row 513) and a fused
@@ -1536,6 +1548,8 @@ int main(int argc, char** argv) {
       {"gpu_session_gemma_graph", true, gpu_session_gemma_graph},
       {"gpu_session_bf16_chain", true, gpu_session_bf16_chain},
       {"gpu_session_gemma3_head256", true, gpu_session_gemma3_head256},
+      {"gpu_session_gemma4_head168", true, gpu_session_gemma4_head168},
+      {"gpu_cpu_op_gqa_head168", true, gpu_cpu_op_gqa_head168},
   };
   std::vector<const Case*> run;
   for (int i = 1; i < argc; ++i) {
