@@ -387,6 +387,8 @@ def main():
     ap.add_argument("--waves", type=int, default=0, help="waves per decode workgroup (4 or 8)")
     ap.add_argument("--unfused", action="store_true",
                     help="decode: sai_kv_append + sai_gqa_decode instead of sai_gqa_with_cache")
+    ap.add_argument("--tile-order", choices=["auto", "fixed", "dynamic"], default="auto",
+                    help="int8 decode tile order (fixed: bit-reproducible outputs)")
     ap.add_argument("--merge", choices=["auto", "combine", "inkernel"], default="auto",
                     help="decode split merge: combine kernel or last-workgroup merge")
     args = ap.parse_args()
@@ -409,6 +411,8 @@ def main():
         rt.set_decode_waves(args.waves)
     if args.merge != "auto":
         rt.set_decode_merge(1 if args.merge == "inkernel" else 0)
+    if args.tile_order != "auto":
+        rt.set_decode_reproducible(1 if args.tile_order == "fixed" else 0)
     b, hq, hkv, d = w["batch"], w["hq"], w.get("hkv", 0), w["d"]
     qdt = torch.bfloat16 if w.get("q_dtype", "bf16") == "bf16" else torch.float32
     stream = torch.cuda.Stream()  # default priority

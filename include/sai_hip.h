@@ -459,6 +459,17 @@ int32_t sai_set_decode_waves(sai_ctx* ctx, int32_t waves);
  * the combine kernel). Returns the previous value; other values are
  * ignored. */
 int32_t sai_set_decode_merge(sai_ctx* ctx, int32_t in_kernel);
+/* Tile order of the int8 decode kernel and the TurboQuant attention. Fixed:
+ * each wave of a workgroup takes tiles w, w + waves, ..., so repeated calls on
+ * the same inputs give bit-identical outputs (the int4 decode always does).
+ * Run time: tiles are handed out from a workgroup counter, which balances the
+ * waves; outputs then vary between calls within rounding. mode 1: fixed in
+ * both; 0: run time in both; 2 (the default): fixed in the int8 decode
+ * (~0.5 % slower at the Llama-3-8B layer shape), run time in the TurboQuant
+ * attention (fixed is 6-10 % slower there). Returns the previous mode; other
+ * values are ignored. No counterpart in the reference (its path is
+ * deterministic). */
+int32_t sai_set_decode_reproducible(sai_ctx* ctx, int32_t mode);
 /* Number of workgroups and split size of the last decode launch on ctx. */
 sai_status sai_last_decode_shape(const sai_ctx* ctx, int32_t* workgroups, int32_t* split_tokens);
 /* Kernel launches of the last decode call on ctx: 1 (the decode kernel,

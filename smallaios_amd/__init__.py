@@ -83,7 +83,8 @@ EXPORTS = [
     "sai_kvcache_set_layer_window",
     "sai_gqa_decode", "sai_gqa_with_cache", "sai_gqa_with_cache_noalloc", "sai_gqa_prefill",
     "sai_set_decode_split",
-    "sai_set_decode_waves", "sai_set_decode_merge", "sai_last_decode_shape",
+    "sai_set_decode_waves", "sai_set_decode_merge", "sai_set_decode_reproducible",
+    "sai_last_decode_shape",
     "sai_last_decode_launches",
     "sai_set_decode_timing", "sai_decode_kernel_times", "sai_rotary_embedding",
     "sai_rope_tables", "sai_copy_rows", "sai_tqcache_create", "sai_tqcache_destroy",
@@ -128,6 +129,7 @@ def _declare(L: C.CDLL) -> None:
         "sai_set_tq_split": (i32, [p, i32]),
         "sai_set_decode_waves": (i32, [p, i32]),
         "sai_set_decode_merge": (i32, [p, i32]),
+        "sai_set_decode_reproducible": (i32, [p, i32]),
         "sai_last_decode_shape": (i32, [p, C.POINTER(i32), C.POINTER(i32)]),
         "sai_last_decode_launches": (i32, [p]),
         "sai_set_decode_timing": (i32, [p, i32]),
@@ -243,6 +245,12 @@ class Runtime:
     def set_decode_merge(self, mode) -> int:
         """0 / False: combine kernel, 1 / True: in-kernel merge, 2: automatic."""
         return int(self._L.sai_set_decode_merge(self.handle, int(mode)))
+
+    def set_decode_reproducible(self, mode) -> int:
+        """Tile order of the int8 decode and the TurboQuant attention: 1 / True
+        fixed in both (bit-identical outputs across calls), 0 / False run-time
+        hand-out in both, 2 (the default) fixed in the int8 decode only."""
+        return int(self._L.sai_set_decode_reproducible(self.handle, int(mode)))
 
     def last_decode_shape(self):
         wg, sp = C.c_int32(), C.c_int32()

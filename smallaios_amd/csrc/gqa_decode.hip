@@ -402,12 +402,23 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
   const int pool_end = appender_split ? n_tiles - 1 : n_tiles;
   const int slots = NW;  // fixed first tiles
   const int pool_start = slots - (appender_split ? 1 : 0);
-  auto grab_issue = [&]() {  // lane 0 holds the counter's old value
+  // Static order (p.static_tiles): wave w takes tiles w, w + NW, w + 2 NW, ...
+  // (the appender wave NW - 1, 2 NW - 1, ... after the new token's tile), so
+  // every launch accumulates the same tiles in the same order in each wave
+  // and the output is bit-reproducible.
+  const int static_base = appender ? NW - 1 : wave + NW;
+  int grabs = 0;
+  auto grab_issue = [&]() {  // dynamic: lane 0 holds the counter's old value
     int t = 0;
-    if (lane == 0) t = atomicAdd(&sm_next, 1);
+    if (p.static_tiles)
+      t = grabs++;
+    else if (lane == 0)
+      t = atomicAdd(&sm_next, 1);
     return t;
   };
-  auto grab_value = [&](int t) { return pool_start + __builtin_amdgcn_readfirstlane(t); };
+  auto grab_value = [&](int t) {
+    return p.static_tiles ? static_base + NW * t : pool_start + __builtin_amdgcn_readfirstlane(t);
+  };
   if (appender) {
     const int pos = L - 1;
     uint8_t* blk = (uint8_t*)p.pool +

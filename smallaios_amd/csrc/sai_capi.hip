@@ -29,6 +29,11 @@ struct sai_ctx {
   int32_t tq_split = 0;      // TurboQuant attention split, positions (0 = automatic)
   int32_t decode_waves = 0;  // 0: automatic
   int32_t decode_merge = 2;  // 0: combine kernel, 1: in-kernel merge, 2: automatic
+  // tile order of the int8 decode and the TurboQuant attention: 1 fixed in
+  // both (bit-reproducible), 0 handed out at run time in both, 2 fixed in
+  // the int8 decode only (measured ~0.5 % slower there at 16 x 8k, but 6-10 %
+  // slower in the TurboQuant attention)
+  int32_t reproducible = 2;
   int32_t last_wg = 0;
   int32_t last_split = 0;
   int32_t last_launches = 0;  // kernels of the last decode call (decode, + combine)
@@ -400,6 +405,13 @@ SAI_API int32_t sai_set_decode_merge(sai_ctx* ctx, int32_t in_kernel) {
   if (!ctx) return 0;
   int32_t prev = ctx->decode_merge;
   if (in_kernel >= 0 && in_kernel <= 2) ctx->decode_merge = in_kernel;
+  return prev;
+}
+
+SAI_API int32_t sai_set_decode_reproducible(sai_ctx* ctx, int32_t mode) {
+  if (!ctx) return -1;
+  const int32_t prev = ctx->reproducible;
+  if (mode >= 0 && mode <= 2) ctx->reproducible = mode;
   return prev;
 }
 
@@ -902,6 +914,7 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
   // 8k, int8, and at 4 x 32k, int4); ragged batches use the combine kernel
   // (measured faster there).
   p.merge_in_kernel = ctx->decode_merge == 1 || (ctx->decode_merge == 2 && uniform);
+  p.static_tiles = ctx->reproducible != 0;
   // ragged: work items go to the sequences with the longest splits first
   // (each sequence's tiles are dealt evenly to its splits, so this orders the
   // work items longest first), which the in-order dispatch of workgroups to
@@ -1848,6 +1861,7 @@ sai_status tq_read_path(sai_ctx* ctx, sai_tqcache* c, int32_t layer, int mode, c
   t.split_rows = split_rows;
   t.max_splits = max_splits;
   t.scale_log2 = scale_log2;
+  t.static_tiles = ctx->reproducible == 1;
   const hipError_t e =
       sai::launch_tq_attend(a, t, mode, G, max_splits, batch, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, e, op);

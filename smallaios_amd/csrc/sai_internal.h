@@ -106,7 +106,6 @@ __device__ __forceinline__ void store_out(void* out, size_t idx, float v, int ou
     ((float*)out)[idx] = v;
 }
 
-// Element i of a row stored as f32 or bf16.
 // Element i of an f32 or bf16 row (base 4-byte aligned). Branch-free: one
 // dword load for either type, so a run of these issues back to back instead
 // of waiting at the join of two load paths.
@@ -181,6 +180,7 @@ struct DecodeParams {
   const void* v_new;
   int kv_dtype;
   int window;           // visible keys per query (0: all); see window_first_key
+  int static_tiles;     // 1: fixed tile order per wave (bit-reproducible output)
   // ragged launches (uniform_nsplit == 0) with batch <= kDecodeOrder: work
   // items go to the sequences in this order (ordered != 0), each sequence's
   // splits in turn
@@ -303,6 +303,7 @@ struct TqAttendArgs {
   int kv_bf16;
   int split_rows, max_splits;  // max_splits: the launch grid's splits per sequence
   float scale_log2;
+  int static_tiles;  // 1: fixed tile order per wave (bit-reproducible output)
 };
 
 // Launchers (return hipError_t of the launch).

@@ -1112,14 +1112,23 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
   // fixed share, the last wave of a workgroup ended ~6 us after the first).
   // The next tile's loads are issued before the current tile is computed;
   // only the loop's exits branch around a load.
-  auto grab_issue = [&]() {  // lane 0 holds the counter's old value
+  // With t.static_tiles the order is fixed instead: wave w takes tiles w,
+  // w + NW, ... (a storer whose first tile went to the pool takes NW - 1,
+  // 2 NW - 1, ... after T), so repeated launches give bit-identical outputs.
+  const int static_base = storer && t_pooled ? NW - 1 : wave + NW;
+  int grabs = 0;
+  auto grab_issue = [&]() {  // dynamic: lane 0 holds the counter's old value
     int v = 0;
-    if (lane == 0) v = atomicAdd(&sm_next, 1);
+    if (t.static_tiles)
+      v = grabs++;
+    else if (lane == 0)
+      v = atomicAdd(&sm_next, 1);
     return v;
   };
   // counter value c: tile NW + c, or with T kept out, NW - 1 first, then
   // NW + c - 1 (T itself is never handed out: the values stop at T)
   auto grab_value = [&](int v) {
+    if (t.static_tiles) return static_base + NW * v;
     const int c = __builtin_amdgcn_readfirstlane(v);
     return t_pooled ? (c == 0 ? NW - 1 : NW + c - 1) : NW + c;
   };

@@ -634,3 +634,33 @@ def test_decode_kernel_timing_ring(rt):
     finally:
         rt.set_decode_timing(prev)
     assert rt.decode_kernel_times(8) == []
+
+
+@pytest.mark.parametrize("merge", [1, 0])
+def test_decode_reproducible_tile_order(rt, merge):
+    """With the fixed tile order (sai_set_decode_reproducible) repeated decode
+    calls over the same cache give bit-identical outputs (the Llama-3-8B layer
+    shape, 4 x 8k, many splits merged in-kernel and by the combine kernel),
+    within tolerance of the oracle; the run-time order stays within tolerance
+    too."""
+    log(f"decode reproducible tile order, merge {merge}")
+    c = Case(rt, 0x5A1A0F1E, 4, 32, 8, 128, [8191, 8191, 5000, 8191], 1, theta=5e5,
+             kv_dtype="bf16")
+    c.step_kv()
+    q = c.query("bf16")
+    ref = c.oracle_attend(q)
+    prev_r = rt.set_decode_reproducible(1)
+    prev_s, prev_m = rt.set_decode_split(512), rt.set_decode_merge(merge)
+    try:
+        outs = [c.gpu_decode(q, "bf16") for _ in range(4)]
+        rt.set_decode_reproducible(0)
+        dyn = c.gpu_decode(q, "bf16")
+    finally:
+        rt.set_decode_reproducible(prev_r)
+        rt.set_decode_split(prev_s)
+        rt.set_decode_merge(prev_m)
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), "fixed order differs"
+    assert_close(outs[0], ref, "fixed tile order")
+    assert_close(dyn, ref, "run-time tile order")
+    log(f"  fixed vs run-time: max |diff| {np.abs(outs[0] - dyn).max():.3e}")

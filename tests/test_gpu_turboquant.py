@@ -530,3 +530,42 @@ def test_errors_and_lifecycle(rt):
         assert e.value.kind == "ShapeMismatch"
     finally:
         c.close()
+
+
+def test_attend_reproducible_tile_order(rt):
+    """sai_set_decode_reproducible(1) fixes the attention's tile order too:
+    repeated calls over one cache (1024-position splits of 16 tiles over 8
+    waves, so most tiles are past the waves' first) give bit-identical
+    outputs; the default run-time order stays within the weights' rounding
+    of them."""
+    import torch
+    log("tq attend: fixed tile order, repeated calls")
+    rng = np.random.default_rng(0x7A11)
+    d, bits, qjl, group, heads = 128, 4, True, 4, 2
+    lens = [1900, 1500, 77]
+    batch, nh = len(lens), heads * group
+    c = S.TqCache(rt, 1, heads, d, bits, qjl, batch, 2048, seed=SEED)
+    prev_s = rt.set_tq_split(1024)
+    prev_r = rt.set_decode_reproducible(1)
+    try:
+        k0 = rng.standard_normal((batch, max(lens), heads * d)).astype(np.float32)
+        v0 = rng.standard_normal((batch, max(lens), heads * d)).astype(np.float32)
+        c.write(0, to_dev(k0, False), to_dev(v0, False), batch, max(lens))
+        c.advance()
+        c.set_lengths(lens)
+        q = to_dev(rng.standard_normal((batch, 1, nh * d)).astype(np.float32), True)
+        outs = []
+        for mode in (1, 1, 1, 0):
+            rt.set_decode_reproducible(mode)
+            out = torch.zeros((batch, 1, nh * d), device="cuda")
+            c.attend(0, q, out, batch, nh)
+            outs.append(out)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+        diff = (outs[3] - outs[0]).abs().max().item()
+        log(f"  run-time vs fixed order: max abs diff {diff:.3e}")
+        assert torch.allclose(outs[3], outs[0], rtol=1e-3, atol=1e-4)
+    finally:
+        rt.set_decode_reproducible(prev_r)
+        rt.set_tq_split(prev_s)
+        c.close()
