@@ -524,8 +524,14 @@ __global__ __launch_bounds__(64 * NW, (kOneWavePerSimd<D, G>) ? 1 : 8 / NW) void
 
   Tile4<D> TB;
   auto tok0 = [&](int k) { return t_begin + (wave + k * NW) * 64 + 16 * g; };
+  // With one wave per SIMD the next tile's loads are kept ahead of the
+  // current tile's work (the scheduler would otherwise sink them a third of
+  // the way into it): 43.5 -> 39.6 us per step at the Gemma-3-4B int4 shape.
+  // With two waves per SIMD the other wave covers the latency, and the
+  // pinned order measured 3 % slower at 4 x 32k.
   auto ld = [&](Tile4<D>& T, int k) {
     load_tile4(T, p.pool, sm_pg, wave + k * NW, p.num_pages, kvh, r, g, n_pages_split);
+    if constexpr (kOneWavePerSimd<D, G>) __builtin_amdgcn_sched_barrier(0);
   };
   // tiles before the split's last one are full
   const bool last_partial = (t_end - t_begin) % 64 != 0;
