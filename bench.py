@@ -492,6 +492,11 @@ def main():
         # it) the events around the decode kernel alone.
         single_launch = not args.unfused and rt.last_decode_launches() == 1
         kernel_us = ms_step * 1e3 if single_launch else d_us
+        # a step that fits the Infinity Cache is priced on the loop that
+        # alternates two caches, so the roofline is that of the HBM stream
+        hbm_clock = single_launch and rotated is not None
+        if hbm_clock:
+            kernel_us = rotated["ms_per_step"] * 1e3
         achieved = alg / (kernel_us * 1e-6) / 1e9
         result = {
             "metric": METRIC if args.workload == "llama8k" else
@@ -526,6 +531,9 @@ def main():
                          "traffic": traffic_from_profile(args.workload),
                          "kernel_us": round(kernel_us, 3),
                          "basis": ("step clock over back-to-back steps of one decode launch "
+                                   "each, alternating two caches so the stream comes from HBM"
+                                   if hbm_clock else
+                                   "step clock over back-to-back steps of one decode launch "
                                    "each (the fused step, splits merged in-kernel)"
                                    if single_launch else
                                    "mean of HIP events recorded on the launch stream around "
@@ -663,7 +671,12 @@ def main():
                        "note": "steps alternate between two caches (2x the step's bytes, "
                                "above the 256 MB Infinity Cache)"}
         k_us = float(np.median(kus))
-        achieved = alg / (k_us * 1e-6) / 1e9
+        # the fused step is one launch: with two caches alternating (the
+        # stream from HBM, not the Infinity Cache) its step clock prices the
+        # kernel; otherwise the events around each attention launch
+        hbm_clock = not args.unfused and rotated is not None
+        kernel_us = rotated["ms_per_step"] * 1e3 if hbm_clock else k_us
+        achieved = alg / (kernel_us * 1e-6) / 1e9
         result = {
             "metric": "TurboQuant decode attention HBM GB/s (% of peak), 1 MI355X",
             "value": round(alg / (ms_step * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
@@ -684,8 +697,12 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                          "traffic": traffic_from_profile(args.workload, "tq_attend"),
-                         "basis": "median of HIP events around each attention launch "
-                                  "(query encoding + attention + split merge)"},
+                         "kernel_us": round(kernel_us, 3),
+                         "basis": ("step clock over back-to-back steps of one launch each "
+                                   "(query encoding + attention + split merge), alternating "
+                                   "two caches so the stream comes from HBM" if hbm_clock else
+                                   "median of HIP events around each attention launch "
+                                   "(query encoding + attention + split merge)")},
         }
         if rotated is not None:
             result["rotated_two_caches"] = rotated
