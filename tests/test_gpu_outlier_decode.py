@@ -43,8 +43,6 @@ def channels_for(d):
 @pytest.mark.parametrize("split", [64, 4096])
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 128), (16, 4, 256), (8, 4, 256)])
 def test_decode_int8_outlier_keys(rt, hq, hkv, d, split, fused):
-    if d == 256 and hq // hkv == 2 and (split == 64 or fused):
-        pytest.skip("group 2 at head_dim 256: one case (split 4096, unfused) is enough")
     log(f"int8 decode outlier K: hq={hq} hkv={hkv} d={d} split={split} fused={fused} past={PAST}")
     prev = rt.set_decode_split(split)
     try:

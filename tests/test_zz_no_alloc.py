@@ -82,3 +82,23 @@ def test_noalloc_rejects_a_step_beyond_its_scratch(rt):
     got = fused(c, q, k, v, noalloc=True)
     c.ocache.append(k, v, c.cos, c.sin, c.do_rotary, c.interleaved)
     assert_close(got, c.oracle_attend(q), "noalloc after a rejected step")
+
+
+def test_noalloc_head168(rt):
+    """head_dim 168 (Gemma 4 31B, stored 192 wide): the fixed scratch holds
+    the split partials at the stored width; bit-identical to
+    sai_gqa_with_cache, within the oracle's tolerance, codes bit-exact."""
+    log("noalloc head_dim 168: 4 sequences, 32Q/8KV, ragged")
+    past = [3000, 17, 900, 4095]
+    cases = [Case(rt, 0xA1168, 4, 32, 8, 168, past, 1, theta=1e6, kv_dtype="bf16",
+                  permute_pages=True, extra_tokens=1) for _ in range(2)]
+    q = [c.query("bf16") for c in cases]
+    kv = [c.kv(1) for c in cases]
+    want = fused(cases[0], q[0], *kv[0], noalloc=False)
+    got = fused(cases[1], q[1], *kv[1], noalloc=True)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+        f"noalloc differs from with_cache at head_dim 168: max |diff| {np.abs(got - want).max():.3e}"
+    c = cases[1]
+    c.ocache.append(*kv[1], c.cos, c.sin, c.do_rotary, c.interleaved)
+    assert_close(got, c.oracle_attend(q[1]), "noalloc head_dim 168 vs oracle")
+    c.check_codes(seqs=[0, 3])
