@@ -371,13 +371,13 @@ __device__ __forceinline__ uint32_t quant4_int4(const float (&x)[4], uint32_t& s
   const _Float16 hz = (_Float16)mn;
   const float sf = (float)hs;
   const float zf = (float)hz;
-  // the quotient t = (x - z) / s from the reciprocal: a = (x - z) * rcp(s) is
-  // within 2 ulps of the correctly rounded t (1 ulp of v_rcp_f32, half of the
-  // product, half of the division), i.e. within 4e-6 for |t| <= 16. The code
-  // round_f32 then takes (half away from zero, `as u32`, min 15) depends only
-  // on which side of a half-integer t lies, so where a is farther than 2^-14
-  // from every half-integer it is rint-up of a, clamped to [0, 15]; anything
-  // else (near a tie, NaN, inf) takes the reference's own steps below
+  // The code round_f32 takes (half away from zero, `as u32`, min 15) is
+  // floor(t + 1/2) clamped to [0, 15] for the correctly rounded quotient
+  // t = (x - z) / s (t <= -1/2 gives 0 either way). y = fma(x - z, rcp(s),
+  // 1/2) is within 3.4e-6 of t + 1/2 for |t| <= 16 (1 ulp of v_rcp_f32, the
+  // division's half ulp, the fma's half ulp), so where y is farther than
+  // 2^-14 from every integer the code is med3(floor(y), 0, 15). Anything else
+  // (near a tie, NaN, inf) takes the reference's own steps below.
   const float rf = __builtin_amdgcn_rcpf(sf);
   uint32_t w = 0u;
 #pragma unroll
@@ -385,22 +385,22 @@ __device__ __forceinline__ uint32_t quant4_int4(const float (&x)[4], uint32_t& s
     uint32_t v = 0u;
     if (sf > 0.0f) {
       const float d = x[j] - zf;
-      const float a = d * rf;
-      const float fl = floorf(a);
-      const float fa = a - fl;
-      if (fabsf(fa - 0.5f) >= 0x1p-14f) {
-        const float c = fa > 0.5f ? fl + 1.0f : fl;
-        v = c <= 0.0f ? 0u : (c >= 15.0f ? 15u : (uint32_t)c);
+      const float y = __builtin_fmaf(d, rf, 0.5f);
+      const float c = floorf(y);
+      const float fr = y - c;  // exact
+      if (fr >= 0x1p-14f && fr <= 1.0f - 0x1p-14f) {  // false for NaN
+        v = (uint32_t)__builtin_amdgcn_fmed3f(c, 0.0f, 15.0f);
       } else {
         // round_f32 of onnx-rt/src/kv_compression.rs:27-37, then `as u32`
         const float t = d / sf;
         const float tr = (float)sat_i32(t);
-        const float fr = t - tr;
-        const float rr = (fr >= 0.5f) ? tr + 1.0f : ((fr <= -0.5f) ? tr - 1.0f : tr);
+        const float fr2 = t - tr;
+        const float rr = (fr2 >= 0.5f) ? tr + 1.0f : ((fr2 <= -0.5f) ? tr - 1.0f : tr);
         v = sat_u32(rr);
+        v = v < 15u ? v : 15u;
       }
     }
-    w |= (v < 15u ? v : 15u) << (4 * j);  // codes packed LSB first
+    w |= v << (4 * j);  // codes packed LSB first
   }
   sz = (uint32_t)__builtin_bit_cast(uint16_t, hs) | ((uint32_t)__builtin_bit_cast(uint16_t, hz) << 16);
   return w;
