@@ -155,6 +155,14 @@ __device__ __forceinline__ void quant_int4_elem(float x, uint32_t& q, uint16_t& 
     mn = fminf(mn, omn);
     mx = fmaxf(mx, omx);
   }
+  if (mn == 0.0f) {
+    // The scan keeps the first of equal minima, so a zero minimum has the
+    // sign of the group's first zero in dim order (lane order; the stored
+    // binary16 zero point keeps it). All 32 lanes of the group are here.
+    const uint64_t zb = __ballot(x == 0.0f);
+    const int base = (int)__lane_id() & 32;
+    mn = __shfl(x, base + __builtin_ctz((uint32_t)(zb >> base)), 64);
+  }
   const float range = mx - mn;
   const float scale = (range > 0.0f) ? range / 15.0f : 1.0f;
   const _Float16 hs = (_Float16)scale;  // v_cvt_f16_f32, round to nearest even

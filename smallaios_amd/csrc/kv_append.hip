@@ -337,70 +337,110 @@ __global__ __launch_bounds__(kPageThreads<D>) void kv_append_page_int8_kernel(Ap
 // leave in 16-byte stores: K rows of the new slots, V two dims' packed
 // columns per thread with the nibbles of slots outside the appended range
 // kept, and the (scale, zero) pairs of the new slots.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
+// v_min_f32 / v_max_f32 whose first operand is read from another lane of the
+// row by DPP (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror).
+// Their operands are min / max results, never NaN and never signalling, so
+// the quieting step the compiler puts before fminf / fmaxf of a DPP move is
+// not needed. The s_nop covers the wait states between a VALU write of the
+// source (or of EXEC) and its DPP read.
+#define SAI_DPP_OP(name, op, ctrl)                                                   \
+  __device__ __forceinline__ float name(float a) {                                  \
+    float r;                                                                         \
+    asm("s_nop 4\n\t" op " %0, %1, %1 " ctrl " row_mask:0xf bank_mask:0xf"        \
+        : "=v"(r)                                                                    \
+        : "v"(a));                                                                   \
+    return r;                                                                        \
+  }
+SAI_DPP_OP(min_quad1032, "v_min_f32_dpp", "quad_perm:[1,0,3,2]")
+SAI_DPP_OP(max_quad1032, "v_max_f32_dpp", "quad_perm:[1,0,3,2]")
+SAI_DPP_OP(min_quad2301, "v_min_f32_dpp", "quad_perm:[2,3,0,1]")
+SAI_DPP_OP(max_quad2301, "v_max_f32_dpp", "quad_perm:[2,3,0,1]")
+SAI_DPP_OP(min_half_mirror, "v_min_f32_dpp", "row_half_mirror")
+SAI_DPP_OP(max_half_mirror, "v_max_f32_dpp", "row_half_mirror")
+#undef SAI_DPP_OP
 
 // min and max over the 8 aligned lanes of a group (quad swaps, then the other
 // quad of the half-row); exact and order-free
 __device__ __forceinline__ void group8_minmax(float& mn, float& mx) {
-  mn = fminf(mn, dpp_f<0xB1>(mn));
-  mx = fmaxf(mx, dpp_f<0xB1>(mx));
-  mn = fminf(mn, dpp_f<0x4E>(mn));
-  mx = fmaxf(mx, dpp_f<0x4E>(mx));
-  mn = fminf(mn, dpp_f<0x141>(mn));  // row_half_mirror
-  mx = fmaxf(mx, dpp_f<0x141>(mx));
+  mn = min_quad1032(mn);
+  mx = max_quad1032(mx);
+  mn = min_quad2301(mn);
+  mx = max_quad2301(mx);
+  mn = min_half_mirror(mn);
+  mx = max_half_mirror(mx);
 }
 
-// Codes of this lane's 4 elements of a group held by 8 lanes, and the
-// group's binary16 (scale, zero) as one word (scale in the low half).
+// Codes of this lane's 4 elements of a group held by 8 lanes (dims in lane
+// order, then element order), and the group's binary16 (scale, zero) as one
+// word (scale in the low half).
 __device__ __forceinline__ uint32_t quant4_int4(const float (&x)[4], uint32_t& sz) {
 #pragma clang fp contract(off)
-  // NaN never wins a `<` / `>` comparison in the reference loop
-  float mn = INFINITY, mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    mn = fminf(mn, x[j] != x[j] ? INFINITY : x[j]);
-    mx = fmaxf(mx, x[j] != x[j] ? -INFINITY : x[j]);
-  }
+  // The reference scans `if v < min { min = v }` / `if v > max { max = v }`
+  // from +-inf: NaN never wins, as in fminf / fmaxf (the other operand).
+  float mn = fminf(fminf(fminf(x[0], x[1]), fminf(x[2], x[3])), INFINITY);
+  float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), -INFINITY);
   group8_minmax(mn, mx);
+  if (mn == 0.0f) {
+    // The scan keeps the first of equal minima, so a zero minimum has the
+    // sign of the group's first zero in dim order (the stored binary16 zero
+    // point keeps it). All 8 lanes of the group are here.
+    float z = x[3] == 0.0f ? x[3] : 1.0f;
+    z = x[2] == 0.0f ? x[2] : z;
+    z = x[1] == 0.0f ? x[1] : z;
+    z = x[0] == 0.0f ? x[0] : z;
+    const uint64_t has = __ballot(z == 0.0f);
+    const int base = (int)__lane_id() & ~7;
+    mn = __shfl(z, base + __builtin_ctz((uint32_t)(has >> base) & 0xFFu), 64);
+  }
   const float range = mx - mn;
-  const float scale = (range > 0.0f) ? range / 15.0f : 1.0f;
+  // range / 15 correctly rounded, as q0 = range * RN(1/15) corrected once by
+  // its exact fma residual: equal to the IEEE quotient for every positive
+  // finite f32 (checked exhaustively on the CPU).
+  constexpr float kInv15 = 0x1.111112p-4f;  // RN(1/15)
+  const float q0 = range * kInv15;
+  const float q = __builtin_fmaf(__builtin_fmaf(-q0, 15.0f, range), kInv15, q0);
+  // (for range = +inf, q is NaN and fminf gives +inf)
+  const float scale = (range > 0.0f) ? fminf(q, range) : 1.0f;
   const _Float16 hs = (_Float16)scale;  // round to nearest even
   const _Float16 hz = (_Float16)mn;
   const float sf = (float)hs;
   const float zf = (float)hz;
-  // The code round_f32 takes (half away from zero, `as u32`, min 15) is
-  // floor(t + 1/2) clamped to [0, 15] for the correctly rounded quotient
-  // t = (x - z) / s (t <= -1/2 gives 0 either way). y = fma(x - z, rcp(s),
-  // 1/2) is within 3.4e-6 of t + 1/2 for |t| <= 16 (1 ulp of v_rcp_f32, the
-  // division's half ulp, the fma's half ulp), so where y is farther than
-  // 2^-14 from every integer the code is med3(floor(y), 0, 15). Anything else
-  // (near a tie, NaN, inf) takes the reference's own steps below.
+  // The code round_f32 takes (half away from zero, `as u32`, min 15) of the
+  // correctly rounded quotient t = (x - z) / s equals med3(rint(t'), 0, 15)
+  // for t' = (x - z) * rcp(s) wherever t' lies farther than 2^-14 from every
+  // half-integer: for |t| <= 16, t' is within 5e-6 of t (1 ulp of v_rcp_f32,
+  // the product's and the division's half ulps), and farther out both clamp
+  // alike. Anything else (near a tie, NaN, inf, a zero scale) takes the
+  // reference's own steps below, for the whole wave when any lane needs
+  // them. Codes are packed in f32 (exact, < 2^16).
   const float rf = __builtin_amdgcn_rcpf(sf);
-  uint32_t w = 0u;
+  uint64_t slow = __ballot(!(sf > 0.0f));
+  float acc = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t v = 0u;
-    if (sf > 0.0f) {
-      const float d = x[j] - zf;
-      const float y = __builtin_fmaf(d, rf, 0.5f);
-      const float c = floorf(y);
-      const float fr = y - c;  // exact
-      if (fr >= 0x1p-14f && fr <= 1.0f - 0x1p-14f) {  // false for NaN
-        v = (uint32_t)__builtin_amdgcn_fmed3f(c, 0.0f, 15.0f);
-      } else {
+  for (int j = 3; j >= 0; --j) {
+    const float t = (x[j] - zf) * rf;
+    const float r = rintf(t);
+    slow |= __ballot(!(fabsf(t - r) <= 0.5f - 0x1p-14f));  // true for NaN
+    const float c = __builtin_amdgcn_fmed3f(r, 0.0f, 15.0f);
+    acc = j == 3 ? c : __builtin_fmaf(acc, 16.0f, c);
+  }
+  uint32_t w = (uint32_t)acc;  // codes packed LSB first
+  if (slow) {
+    w = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t v = 0u;
+      if (sf > 0.0f) {
         // round_f32 of onnx-rt/src/kv_compression.rs:27-37, then `as u32`
-        const float t = d / sf;
+        const float t = (x[j] - zf) / sf;
         const float tr = (float)sat_i32(t);
-        const float fr2 = t - tr;
-        const float rr = (fr2 >= 0.5f) ? tr + 1.0f : ((fr2 <= -0.5f) ? tr - 1.0f : tr);
+        const float fr = t - tr;
+        const float rr = (fr >= 0.5f) ? tr + 1.0f : ((fr <= -0.5f) ? tr - 1.0f : tr);
         v = sat_u32(rr);
         v = v < 15u ? v : 15u;
       }
+      w |= v << (4 * j);
     }
-    w |= v << (4 * j);  // codes packed LSB first
   }
   sz = (uint32_t)__builtin_bit_cast(uint16_t, hs) | ((uint32_t)__builtin_bit_cast(uint16_t, hz) << 16);
   return w;
@@ -417,8 +457,10 @@ __device__ __forceinline__ uint2 pack_column(const uint4 c) {
   return uint2{pk(c.x, c.y), pk(c.z, c.w)};
 }
 
-template <int D, bool BF16, int ROPE>
-__global__ __launch_bounds__(2 * D) void kv_append_page_int4_kernel(AppendParams p) {
+// HPW kv heads per workgroup (2 D threads each): head_dim 64 and 128 take
+// several, so that a workgroup moves as many bytes as one of head_dim 256.
+template <int D, bool BF16, int ROPE, int HPW>
+__global__ __launch_bounds__(2 * D * HPW) void kv_append_page_int4_kernel(AppendParams p) {
   constexpr int L = D / 8;    // lanes per token
   constexpr int W = D / 32;   // waves: kPageTokens / (64 / L)
   constexpr int HALF = D / 2;
@@ -427,9 +469,10 @@ __global__ __launch_bounds__(2 * D) void kv_append_page_int4_kernel(AppendParams
   constexpr uint32_t ESZ = BF16 ? 2 : 4;
   constexpr int PB = D / 8 < 16 ? D / 8 : 16;  // bytes of a (scale, zero) piece
   constexpr int PPS = (D / 8) / PB;            // pieces per slot
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int sub = __builtin_amdgcn_readfirstlane((int)threadIdx.x / (2 * D));  // head of the workgroup
+  const int tid = (int)threadIdx.x % (2 * D), lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int h = blockIdx.x, b = blockIdx.z;
+  const int h = (int)blockIdx.x * HPW + sub, b = blockIdx.z;
   const int start = p.seq_lens[b];
   const int page_idx = start / kPageTokens + (int)blockIdx.y;
   const int t0 = page_idx * kPageTokens;  // position of slot 0
@@ -495,9 +538,12 @@ __global__ __launch_bounds__(2 * D) void kv_append_page_int4_kernel(AppendParams
   const uint32_t ka = quant4_int4(xa, pka), kb = quant4_int4(xb, pkb);
   const uint32_t qa = quant4_int4(va, pva), qb = quant4_int4(vb, pvb);
 
-  __shared__ __align__(16) uint8_t sm_k[kPageTokens * KS];
-  __shared__ __align__(16) uint8_t sm_v[kPageTokens * D];      // column d at 16 d, one byte per slot
-  __shared__ __align__(16) uint32_t sm_p[2][kPageTokens][NG];  // K, V (scale, zero) per slot
+  __shared__ __align__(16) uint8_t sm_k_all[HPW][kPageTokens * KS];
+  __shared__ __align__(16) uint8_t sm_v_all[HPW][kPageTokens * D];  // column d at 16 d, one byte per slot
+  __shared__ __align__(16) uint32_t sm_p_all[HPW][2][kPageTokens][NG];  // K, V (scale, zero) per slot
+  uint8_t* sm_k = sm_k_all[sub];
+  uint8_t* sm_v = sm_v_all[sub];
+  uint32_t(*sm_p)[kPageTokens][NG] = sm_p_all[sub];
   // K: the 4 codes of dims 4c.. (already nibbles, LSB first) are bytes 2c,
   // 2c + 1 of the row; those of D/2 + 4c.. bytes D/4 + 2c, + 1
   *(uint16_t*)&sm_k[t * KS + 2 * c] = (uint16_t)ka;
@@ -673,14 +719,26 @@ void launch_page_int8(dim3 grid, hipStream_t st, const AppendParams& p, bool bf,
     launch_page_int8_dt<D, false>(grid, st, p, rope);
 }
 
+template <int D, bool BF16, int HPW>
+void launch_page_int4_hpw(dim3 grid, hipStream_t st, const AppendParams& p, int rope) {
+  grid.x /= HPW;
+  const dim3 block(2 * D * HPW);
+  if (rope == 0)
+    hipLaunchKernelGGL((kv_append_page_int4_kernel<D, BF16, 0, HPW>), grid, block, 0, st, p);
+  else if (rope == 1)
+    hipLaunchKernelGGL((kv_append_page_int4_kernel<D, BF16, 1, HPW>), grid, block, 0, st, p);
+  else
+    hipLaunchKernelGGL((kv_append_page_int4_kernel<D, BF16, 2, HPW>), grid, block, 0, st, p);
+}
+
+// 512 threads per workgroup where the kv heads divide evenly
 template <int D, bool BF16>
 void launch_page_int4_dt(dim3 grid, hipStream_t st, const AppendParams& p, int rope) {
-  if (rope == 0)
-    hipLaunchKernelGGL((kv_append_page_int4_kernel<D, BF16, 0>), grid, dim3(2 * D), 0, st, p);
-  else if (rope == 1)
-    hipLaunchKernelGGL((kv_append_page_int4_kernel<D, BF16, 1>), grid, dim3(2 * D), 0, st, p);
+  constexpr int HPW = 256 / D;
+  if (HPW > 1 && p.kv_heads % HPW == 0)
+    launch_page_int4_hpw<D, BF16, HPW>(grid, st, p, rope);
   else
-    hipLaunchKernelGGL((kv_append_page_int4_kernel<D, BF16, 2>), grid, dim3(2 * D), 0, st, p);
+    launch_page_int4_hpw<D, BF16, 1>(grid, st, p, rope);
 }
 
 template <int D>

@@ -115,6 +115,56 @@ def test_append_special_values(rt, quant):
     c.check_codes()
 
 
+def signed_zero_groups(rng, x):
+    """Positive values with groups of 32 whose minimum is zero: +0 before -0 and the
+    reverse, in one lane of the page kernel (dims 4k .. 4k+3) and in different lanes, a
+    lone -0, an all-zero group of mixed signs, and zeros beside a negative minimum."""
+    b, n, hd = x.shape
+    x = (np.abs(x) + np.float32(0.25)).reshape(b, n, hd // 32, 32).copy()
+    pz, nz = np.float32(0.0), np.float32(-0.0)
+    for t in range(n):
+        for g in range(hd // 32):
+            p = (t + 3 * g) % 7
+            row = x[:, t, g]
+            if p == 0:
+                row[:, 3], row[:, 10] = pz, nz
+            elif p == 1:
+                row[:, 2], row[:, 20] = nz, pz
+            elif p == 2:
+                row[:, 31] = nz
+            elif p == 3:
+                row[:, 7], row[:, 5] = nz, pz
+            elif p == 4:
+                row[:, 6], row[:, 4] = pz, nz
+            elif p == 5:
+                row[:] = np.where(np.arange(32) % 2 == 0, nz, pz)
+            else:
+                row[:, 0], row[:, 1], row[:, 9] = pz, nz, np.float32(-1.0)
+    return x.reshape(b, n, hd)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_append_int4_signed_zero_minimum(rt, d, kv_dtype):
+    """A group whose minimum is zero stores the sign of its first zero in dim order as its
+    binary16 zero point: the reference's scan keeps the first of equal minima
+    (kv_compression.rs:227-235). Through the page kernel (30 tokens), the per-pair kernel
+    (3 tokens) and the fused decode step."""
+    log(f"append int4 signed-zero minima d={d} {kv_dtype}")
+    c = Case(rt, 0x5E20 + d, 2, 8, 2, d, [13, 30], 1, quant=S.KV_INT4, kv_dtype=kv_dtype,
+             do_rotary=False, permute_pages=True, extra_tokens=4,
+             k_transform=signed_zero_groups, v_transform=signed_zero_groups)
+    c.check_codes()
+    k, v = c.kv(3)
+    c.append_both(k, v)
+    c.check_codes()
+    c.cache.advance()
+    q = c.query()
+    got = c.step_fused(q)
+    assert_close(got, c.oracle_attend(q), "fused step after signed-zero groups")
+    c.check_codes()
+
+
 def test_append_int4_bit_exact(rt):
     """int4 asym g32 codes and f16 params, K with x20 outlier channels."""
     log("append int4: outlier channels, student-t, odd start positions")

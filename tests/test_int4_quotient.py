@@ -1,18 +1,70 @@
-"""The int4 page append's quotient fast path, checked on the CPU.
+"""The int4 page append's shortcuts past IEEE division, checked on the CPU.
 
-kv_append_page_int4_kernel codes an element as med3(floor(fma(x - z, rcp(s), 1/2)), 0, 15)
-where that value lies at least 2^-14 from every integer, and takes the reference's own
-steps (the correctly rounded quotient, round_f32, `as u32`, min 15;
-onnx-rt/src/kv_compression.rs:27-37 and :223-253) elsewhere. This emulates the fast path
-in numpy: the fma with one rounding, v_rcp_f32 as the correctly rounded reciprocal moved by
--1, 0 or +1 ulp. It checks the fast path against round_f32 of the correctly rounded
-quotient on random groups, with a third of the values placed on the half-integer ties
-z + (k + 1/2) s, where a plausible mistake (floor without the half, a one-sided band, no
-clamp) changes codes.
+kv_append_page_int4_kernel takes two shortcuts, each with the reference's own steps
+as the fallback (onnx-rt/src/kv_compression.rs:27-37 and :223-253):
+
+* the group scale range / 15 as q0 = range * RN(1/15) corrected once by its fma residual,
+  q0 + fma(-q0, 15, range) * RN(1/15); checked against the IEEE quotient for every
+  positive finite f32 (a C program, OpenMP over the 2^31 inputs);
+* the code of an element as med3(rint((x - z) * rcp(s)), 0, 15) where that product lies
+  at least 2^-14 from every half-integer. Emulated in numpy (v_rcp_f32 as the correctly
+  rounded reciprocal moved by -1, 0 or +1 ulp) and checked against round_f32 of the
+  correctly rounded quotient on random groups, with a third of the values placed on the
+  half-integer ties z + (k + 1/2) s, where a plausible mistake (floor instead of rint, a
+  one-sided band, no clamp) changes codes.
 """
+import os
+import subprocess
+
 import numpy as np
+import pytest
 
 F32 = np.float32
+
+DIV15_C = r"""
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+int main(void) {
+  const float c = 0x1.111112p-4f;  /* RN(1/15) */
+  if (c != 1.0f / 15.0f) return 2;
+  unsigned long long bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+  for (long long b = 1; b < 0x7F800000LL; ++b) {
+    const uint32_t u = (uint32_t)b;
+    float r, want, q0, q;
+    memcpy(&r, &u, 4);
+    want = r / 15.0f;
+    q0 = r * c;
+    q = fmaf(fmaf(-q0, 15.0f, r), c, q0);
+    if (memcmp(&q, &want, 4) != 0) ++bad;
+  }
+  printf("%llu\n", bad);
+  return 0;
+}
+"""
+
+
+def test_scale_division_by_15_exhaustive(tmp_path):
+    src = tmp_path / "div15.c"
+    exe = tmp_path / "div15"
+    src.write_text(DIV15_C)
+    subprocess.run(["gcc", "-O2", "-fopenmp", "-o", str(exe), str(src), "-lm"], check=True)
+    env = dict(os.environ, OMP_NUM_THREADS=str(min(8, os.cpu_count() or 1)))
+    out = subprocess.run([str(exe)], check=True, stdout=subprocess.PIPE, text=True, env=env,
+                         timeout=600).stdout
+    assert out.strip() == "0", f"{out.strip()} inputs where the corrected product differs"
+
+
+def test_scale_division_needs_the_correction():
+    """The plain product range * RN(1/15) is not the IEEE quotient everywhere, so the
+    exhaustive check above is what pins the corrected form."""
+    rng = np.random.default_rng(15)
+    r = rng.uniform(1e-3, 1e3, 200_000).astype(F32)
+    want = (r.astype(np.float64) / 15.0).astype(F32)
+    plain = (r * F32(1.0 / 15.0)).astype(F32)
+    assert np.any(plain != want)
 
 
 def reference_codes(x, zf, sf):
@@ -35,33 +87,31 @@ def fast_codes(x, zf, sf, rng):
     dn = np.nextafter(r0, F32(-np.inf)).astype(F32)
     pick = rng.integers(0, 3, len(r0))
     rf = np.where(pick == 0, r0, np.where(pick == 1, up, dn)).astype(F32)
-    y = (d.astype(np.float64) * rf.astype(np.float64) + 0.5).astype(F32)  # fma: one rounding
-    c = np.floor(y).astype(F32)
-    fr = (y - c).astype(F32)
+    t = (d * rf).astype(F32)
+    r = np.rint(t).astype(F32)  # round half to even, as v_rndne_f32
     with np.errstate(invalid="ignore"):
-        decided = (fr >= F32(2.0 ** -14)) & (fr <= F32(1 - 2.0 ** -14))
-    return np.clip(c, 0, 15).astype(np.uint64), decided
+        decided = np.abs((t - r).astype(F32)) <= F32(0.5 - 2.0 ** -14)
+    return np.clip(r, 0, 15).astype(np.uint64), decided
 
 
-def test_int4_quotient_fast_path_matches_round_f32():
-    rng = np.random.default_rng(0x1447)
+@pytest.mark.parametrize("mag", [1e-3, 1.0, 30.0, 1e3])
+def test_int4_quotient_fast_path_matches_round_f32(mag):
+    rng = np.random.default_rng(0x1447 + int(mag * 1000))
     n = 250_000
-    decided_total = 0
-    for mag in (1e-3, 1.0, 30.0, 1e3):
-        mn = (rng.standard_normal(n) * mag).astype(F32)
-        width = (np.abs(rng.standard_normal(n)) * mag + 1e-5).astype(F32)
-        sf = (width / F32(15)).astype(np.float16).astype(F32)
-        zf = mn.astype(np.float16).astype(F32)
-        x = (mn + rng.uniform(-0.02, 1.02, n).astype(F32) * width).astype(F32)
-        k = rng.integers(0, 16, n)
-        ties = rng.random(n) < 0.33
-        x = np.where(ties, (zf + (k + F32(0.5)) * sf).astype(F32), x).astype(F32)
-        keep = (sf > 0) & np.isfinite(sf) & np.isfinite(zf)
-        x, zf, sf = x[keep], zf[keep], sf[keep]
-        codes, decided = fast_codes(x, zf, sf, rng)
-        ref = reference_codes(x, zf, sf)
-        assert np.array_equal(codes[decided], ref[decided]), f"magnitude {mag}"
-        # the band leaves only the elements near a tie to the slow path
-        assert decided.mean() > 0.6
-        decided_total += int(decided.sum())
-    assert decided_total > 600_000
+    mn = (rng.standard_normal(n) * mag).astype(F32)
+    width = (np.abs(rng.standard_normal(n)) * mag + 1e-5).astype(F32)
+    sf = (width / F32(15)).astype(np.float16).astype(F32)
+    zf = mn.astype(np.float16).astype(F32)
+    x = (mn + rng.uniform(-0.02, 1.02, n).astype(F32) * width).astype(F32)
+    k = rng.integers(0, 16, n)
+    ties = rng.random(n) < 0.33
+    x = np.where(ties, (zf + (k + F32(0.5)) * sf).astype(F32), x).astype(F32)
+    keep = (sf > 0) & np.isfinite(sf) & np.isfinite(zf)
+    x, zf, sf = x[keep], zf[keep], sf[keep]
+    codes, decided = fast_codes(x, zf, sf, rng)
+    ref = reference_codes(x, zf, sf)
+    assert np.array_equal(codes[decided], ref[decided]), f"magnitude {mag}"
+    # the band leaves only the elements near a tie to the slow path
+    assert decided.mean() > 0.6
+    # and the ties themselves go there
+    assert decided[ties[keep]].mean() < 0.05

@@ -416,3 +416,19 @@ def test_int4_quant_matches_numpy_and_invariants():
         np.testing.assert_array_equal(deq, q.astype(f32) * sf + zf)
         # error bound: half a step plus the zero point's f16 rounding
         assert (np.abs(deq - x) <= 0.5 * sf + np.abs(zf) * 2 ** -10 + 1e-6 + sf * 1e-3).all()
+
+
+def test_int4_zero_minimum_keeps_first_zero_sign():
+    """The reference's scan (`if v < min { min = v }`, kv_compression.rs:227-235) keeps
+    the first of equal minima, so a zero minimum is stored with the sign of the group's
+    first zero: 0x8000 when -0 comes first, 0x0000 when +0 does. A min() that prefers
+    either sign fails one of the two groups."""
+    x = (np.abs(np.random.default_rng(5).standard_normal(64)) + 0.25).astype(f32)
+    x[3], x[10] = f32(0.0), f32(-0.0)         # group 0: +0 first
+    x[32 + 2], x[32 + 20] = f32(-0.0), f32(0.0)  # group 1: -0 first
+    _, s, z = O.quant_int4_row(x)
+    assert z.tolist() == [0x0000, 0x8000]
+    # both groups keep their scale max / 15 and code zeros as 0
+    p, _, _ = O.quant_int4_row(x)
+    codes = np.stack([p & 15, p >> 4], axis=1).reshape(-1)
+    assert codes[3] == codes[10] == codes[34] == codes[52] == 0
