@@ -457,8 +457,8 @@ __device__ __forceinline__ uint2 pack_column(const uint4 c) {
   return uint2{pk(c.x, c.y), pk(c.z, c.w)};
 }
 
-// HPW kv heads per workgroup (2 D threads each): head_dim 64 and 128 take
-// several, so that a workgroup moves as many bytes as one of head_dim 256.
+// HPW kv heads per workgroup (2 D threads each, up to 1024 threads): fewer,
+// larger workgroups keep more of each CU's loads in flight.
 template <int D, bool BF16, int ROPE, int HPW>
 __global__ __launch_bounds__(2 * D * HPW) void kv_append_page_int4_kernel(AppendParams p) {
   constexpr int L = D / 8;    // lanes per token
@@ -731,14 +731,21 @@ void launch_page_int4_hpw(dim3 grid, hipStream_t st, const AppendParams& p, int 
     hipLaunchKernelGGL((kv_append_page_int4_kernel<D, BF16, 2, HPW>), grid, block, 0, st, p);
 }
 
-// 512 threads per workgroup where the kv heads divide evenly
+// Below head_dim 256, up to 1024 threads per workgroup: the most kv heads (a
+// power of two, at most 512 / D) that divide the kv head count. (Building a
+// 4 x 32768-token cache of 8 kv heads at head_dim 128 from f32 rows: 36.1 us
+// per 131,072 rows with one head per workgroup, 34.8 with two, 32.1 with
+// four; at head_dim 256 two heads measured the same as one.)
 template <int D, bool BF16>
 void launch_page_int4_dt(dim3 grid, hipStream_t st, const AppendParams& p, int rope) {
-  constexpr int HPW = 256 / D;
-  if (HPW > 1 && p.kv_heads % HPW == 0)
-    launch_page_int4_hpw<D, BF16, HPW>(grid, st, p, rope);
-  else
-    launch_page_int4_hpw<D, BF16, 1>(grid, st, p, rope);
+  if constexpr (D <= 64) {
+    if (p.kv_heads % 8 == 0) return launch_page_int4_hpw<D, BF16, 8>(grid, st, p, rope);
+  }
+  if constexpr (D <= 128) {
+    if (p.kv_heads % 4 == 0) return launch_page_int4_hpw<D, BF16, 4>(grid, st, p, rope);
+    if (p.kv_heads % 2 == 0) return launch_page_int4_hpw<D, BF16, 2>(grid, st, p, rope);
+  }
+  launch_page_int4_hpw<D, BF16, 1>(grid, st, p, rope);
 }
 
 template <int D>

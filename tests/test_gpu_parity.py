@@ -45,22 +45,24 @@ def test_append_variants_bit_exact(rt, d, interleaved, rot, kv_dtype):
     c.check_codes()
 
 
+@pytest.mark.parametrize("hkv", [2, 3, 8])
 @pytest.mark.parametrize("quant", [S.KV_INT8, S.KV_INT4])
 @pytest.mark.parametrize("d,interleaved,kv_dtype", [
     (64, False, "f32"), (64, True, "bf16"), (128, False, "bf16"), (128, True, "f32"),
     (256, False, "bf16"), (256, True, "f32")])
-def test_append_page_blocks_bit_exact(rt, d, interleaved, kv_dtype, quant):
+def test_append_page_blocks_bit_exact(rt, d, interleaved, kv_dtype, quant, hkv):
     """Multi-token appends take the page-block kernel (one workgroup per page
     block, 16-byte stores): 20 new tokens from starts 13, 0, 31 and 16 span
     two or three pages, first and last page partial or whole; the slots
     before the start keep their codes (int4: the other nibble of each V
     byte). 3 tokens take the per-row (int4: per-pair) kernel, and the results
     of both meet bit-exact in one cache. K with x20 outlier channels and
-    heavy tails, so the int4 groups' ranges differ widely."""
-    log(f"append page blocks quant={quant} d={d} interleaved={interleaved} {kv_dtype}")
+    heavy tails, so the int4 groups' ranges differ widely. 2, 3 and 8 kv
+    heads: the int4 form puts 1 to 8 kv heads in one workgroup."""
+    log(f"append page blocks quant={quant} d={d} hkv={hkv} interleaved={interleaved} {kv_dtype}")
     from _gpu_util import outlier_keys
-    c = Case(rt, 0xB10C + d, 4, 8, 2, d, [13, 0, 31, 16], 20, theta=5e5, kv_dtype=kv_dtype,
-             permute_pages=True, interleaved=interleaved, extra_tokens=3, quant=quant,
+    c = Case(rt, 0xB10C + d + hkv, 4, 8, hkv, d, [13, 0, 31, 16], 20, theta=5e5,
+             kv_dtype=kv_dtype, permute_pages=True, interleaved=interleaved, extra_tokens=3, quant=quant,
              k_transform=outlier_keys(d, channels=(5, 17, d - 3)))
     c.step_kv()
     c.check_codes()
