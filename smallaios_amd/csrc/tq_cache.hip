@@ -736,36 +736,28 @@ __device__ __forceinline__ int p_slot(int r) {
 }
 
 // Rows sy[g] (the group's outputs in the rotated domain) back to the model's
-// domain: the butterfly's stages over LDS, then * norm and the signs, written
-// to out. All NT threads of the block take part.
-template <int D, int G, int NT>
+// domain: wave g takes row g (lane l: dims l + 64 e) through the butterfly's
+// stages on lane moves and * norm (wave_butterfly, the same stages and
+// roundings as over LDS), then * the signs, written to out. Waves past the
+// group return.
+template <int D, int G, int NW>
 __device__ __forceinline__ void rotate_back(const TqArgs& a, const TqAttendArgs& t, int b,
-                                            int kvh, float (&sy)[G][D]) {
+                                            int kvh, const float (&sy)[G][D]) {
 #pragma clang fp contract(off)
-  constexpr int PER = (G * D + NT - 1) / NT;
-  for (int h = 1; h < D; h *= 2) {
-    float nv[PER];
+  static_assert(G <= NW, "one wave per row of the group");
+  constexpr int E = D / 64;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  if (wave >= G) return;
+  float y[E];
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int e = threadIdx.x + k * NT;
-      if (e < G * D) {
-        const int g = e / D, i = e % D;
-        const float a0 = sy[g][i], a1 = sy[g][i ^ h];
-        nv[k] = (i & h) ? a1 - a0 : a0 + a1;
-      }
-    }
-    __syncthreads();
+  for (int e = 0; e < E; ++e) y[e] = sy[wave][lane + 64 * e];
+  wave_butterfly<D>(y, lane, a.norm);
+  float* o = t.out + ((size_t)b * t.num_heads + kvh * G + wave) * D;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int e = threadIdx.x + k * NT;
-      if (e < G * D) sy[e / D][e % D] = nv[k];
-    }
-    __syncthreads();
-  }
-  for (int e = threadIdx.x; e < G * D; e += NT) {
-    const int g = e / D, i = e % D;
-    t.out[((size_t)b * t.num_heads + kvh * G + g) * D + i] =
-        sy[g][i] * a.norm * (float)a.signs[(size_t)kvh * D + i];
+  for (int e = 0; e < E; ++e) {
+    const int i = lane + 64 * e;
+    o[i] = y[e] * (float)a.signs[(size_t)kvh * D + i];
   }
 }
 
@@ -1233,7 +1225,7 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
     if (threadIdx.x == 0) reset_ticket(counter);
   }
   __syncthreads();
-  rotate_back<D, G, 64 * NW>(a, t, b, kvh, sy);
+  rotate_back<D, G, NW>(a, t, b, kvh, sy);
 }
 
 // Waves per workgroup: 8 (two per SIMD, one workgroup per CU) up to head_dim
