@@ -4,7 +4,7 @@
 draw: numpy default_rng(seed).integers(128, 16385, 64)), 32 query / 8 kv heads,
 head_dim 128, int8 KV in 16-token pages behind a randomly permuted page table,
 one fused decode step (sai_gqa_with_cache) at the automatic split, which cuts
-the longest sequences into up to 8 pieces of 2048 tokens merged by the
+the longest sequences into up to 6 pieces of 3072 tokens merged by the
 8-wide combine. The whole batch runs on the GPU; the shortest, the longest and
 six more sampled sequences are checked against the oracle (a cache holding
 only those sequences, built from the same K/V values), and the shortest and
@@ -92,7 +92,7 @@ def test_decode_ragged_full_lengths(rt):
     n_splits = (lens + split - 1) // split
     log(f"  automatic split {split} tokens, {wg} workgroups, "
         f"up to {int(n_splits.max())} splits per sequence")
-    assert split == 2048 and int(n_splits.max()) == 8 and wg == int(n_splits.sum()) * HKV
+    assert split == 3072 and int(n_splits.max()) == 6 and wg == int(n_splits.sum()) * HKV
 
     oc.append(kn.index_select(0, sel).float().cpu().numpy(),
               vn.index_select(0, sel).float().cpu().numpy(), cos, sin)
