@@ -30,6 +30,8 @@
 
 #include <cstdint>
 
+#include <type_traits>
+
 #include "sai_internal.h"
 
 namespace sai {
@@ -129,9 +131,38 @@ __device__ __forceinline__ Vec<T, N> load_vec(const T* p) {
   return out;
 }
 
+// Two f32 -> two bf16 in one word (a in the low half), rounded to nearest
+// even by v_cvt_pk_bf16_f32 (NaN excepted: see store_vec).
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), bf2));
+}
+
 template <typename T, int N, bool VEC>
 __device__ __forceinline__ void store_vec(T* p, const float (&v)[N]) {
-  if constexpr (VEC) {
+  if constexpr (VEC && std::is_same<T, uint16_t>::value && N % 2 == 0) {
+    // bf16 pairs by the conversion instruction; a vector holding a NaN takes
+    // f32_to_bf16_bits for every element (a quiet NaN keeping the sign and
+    // the high payload bits, as the reference's conversion)
+    typedef typename Raw<N * sizeof(T)>::type R;
+    union {
+      R r;
+      uint32_t w[N / 2];
+    } u;
+    bool nan = false;
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+      u.w[j] = f32x2_to_bf16x2(v[2 * j], v[2 * j + 1]);
+      nan = nan || v[2 * j] != v[2 * j] || v[2 * j + 1] != v[2 * j + 1];
+    }
+    if (nan) {
+#pragma unroll
+      for (int j = 0; j < N / 2; ++j)
+        u.w[j] = (uint32_t)f32_to_bf16_bits(v[2 * j]) | ((uint32_t)f32_to_bf16_bits(v[2 * j + 1]) << 16);
+    }
+    *reinterpret_cast<R*>(p) = u.r;
+  } else if constexpr (VEC) {
     typedef typename Raw<N * sizeof(T)>::type R;
     union {
       R r;

@@ -310,3 +310,45 @@ def test_generated_bf16_tables_drive_the_rotation(rt):
     want = O.apply_rope(x.reshape(2, 4, 16, 128), cf.cpu().numpy(), sf.cpu().numpy(),
                         np.arange(200, 216)).ravel()
     assert np.array_equal(y1.cpu().numpy(), want)
+
+
+def test_rotary_bf16_rounding_patterns(rt):
+    """bf16 outputs round like the reference's f32_to_bf16 (tensor.rs:312-329) on every
+    kind of f32 the rotation can produce: with x = 1 and sin = 0 each output is its cos
+    entry, so the f32 table carries the patterns (262,144 of them): every exponent from
+    denormals to the largest finite binade, low halves exactly at a tie (0x8000, with
+    the kept bit odd and even), one below and above it, 0x0000, 0xFFFF and random, and
+    both signs. (NaN is not among them: a NaN's payload after the rotation's arithmetic
+    is the device's, not the rounding's.)"""
+    import torch
+    rng = np.random.default_rng(0xBF16)
+    s, d = 4096, 128
+    half = d // 2
+    n = s * half
+    sign = rng.integers(0, 2, n, dtype=np.uint32) << 31
+    expo = (np.arange(n, dtype=np.uint32) % 255) << 23
+    high = rng.integers(0, 128, n, dtype=np.uint32) << 16
+    lows = np.array([0x8000, 0x8000, 0x7FFF, 0x8001, 0x0000, 0xFFFF], np.uint32)
+    pick = rng.integers(0, len(lows) + 2, n)
+    low = np.where(pick < len(lows), lows[np.minimum(pick, len(lows) - 1)],
+                   rng.integers(0, 1 << 16, n, dtype=np.uint32))
+    # the kept bit (bit 16) odd for half of the exact ties
+    high = np.where((pick == 1), high | (1 << 16), high)
+    cos = (sign | expo | high | low).view(np.float32).reshape(s, half)
+    sin = np.zeros_like(cos)
+    x = np.ones(s * d, np.float32)
+    xd = to_dev(x, True)
+    yd = to_dev(np.zeros_like(x), True)
+    cd = to_dev(cos, False).reshape(s, half)
+    sd = to_dev(sin, False).reshape(s, half)
+    log("rotary bf16 rounding: 262,144 f32 patterns through the output conversion")
+    rt.rotary_embedding(xd, yd, 1, 1, s, d, cd, sd, start_position=0, layout=S.ROPE_BSHD,
+                        dtype=S.DTYPE_BF16, table_dtype=S.DTYPE_F32)
+    torch.cuda.synchronize()
+    got = from_dev(yd, True)
+    y = oracle_rope(x, 1, 1, s, d, S.ROPE_BSHD, cos, sin, np.arange(s), False, 0)
+    want = O.f32_to_bf16_bits(y)
+    assert np.array_equal(got, want), np.flatnonzero(got != want)[:10]
+    # the patterns reach the conversion unchanged: the first half of each row is
+    # cos - 0 = cos, bit for bit
+    assert np.array_equal(y.reshape(s, d)[:, :half].view(np.uint32), cos.view(np.uint32))
