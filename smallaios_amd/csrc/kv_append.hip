@@ -105,6 +105,16 @@ __device__ __forceinline__ float group_max(float x) {
   return __uint_as_float(v);
 }
 
+// a / 127 correctly rounded for a > 0, as q0 = a * RN(1/127) corrected once
+// by its exact fma residual: equal to the IEEE quotient for every positive
+// finite f32 (checked exhaustively on the CPU); for a = +inf, q is NaN and
+// fminf gives +inf.
+__device__ __forceinline__ float div127(float a) {
+  constexpr float kInv127 = 0x1.020408p-7f;  // RN(1/127)
+  const float q0 = a * kInv127;
+  return fminf(__builtin_fmaf(__builtin_fmaf(-q0, 127.0f, a), kInv127, q0), a);
+}
+
 // The quotient x / s of append_row_int8 (s = fl(m / 127) for the row's
 // maximum m >= |x|), taken without the division. r = 1/s from v_rcp_f32
 // (within 1 ulp) when s is a normal finite float, NaN otherwise. Then
@@ -269,8 +279,8 @@ __global__ __launch_bounds__(kPageThreads<D>) void kv_append_page_int8_kernel(Ap
   }
   ak = group_max<L>(ak);
   av = group_max<L>(av);
-  const float sk = (ak > 0.0f) ? ak / 127.0f : 1.0f;
-  const float sv = (av > 0.0f) ? av / 127.0f : 1.0f;
+  const float sk = (ak > 0.0f) ? div127(ak) : 1.0f;
+  const float sv = (av > 0.0f) ? div127(av) : 1.0f;
   const float rk = (sk >= 0x1p-126f && sk <= 0x1.fffffep127f) ? __builtin_amdgcn_rcpf(sk)
                                                               : __builtin_nanf("");
   const float rv = (sv >= 0x1p-126f && sv <= 0x1.fffffep127f) ? __builtin_amdgcn_rcpf(sv)

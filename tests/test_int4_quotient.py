@@ -21,23 +21,26 @@ import pytest
 
 F32 = np.float32
 
-DIV15_C = r"""
+DIV_C = r"""
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
-int main(void) {
-  const float c = 0x1.111112p-4f;  /* RN(1/15) */
-  if (c != 1.0f / 15.0f) return 2;
+/* argv[1]: the divisor y; argv[2]: the kernel's constant RN(1/y) as a hex float */
+int main(int argc, char** argv) {
+  if (argc != 3) return 3;
+  const float y = strtof(argv[1], NULL), c = strtof(argv[2], NULL);
+  if (c != 1.0f / y) return 2;
   unsigned long long bad = 0;
 #pragma omp parallel for reduction(+ : bad) schedule(static)
   for (long long b = 1; b < 0x7F800000LL; ++b) {
     const uint32_t u = (uint32_t)b;
     float r, want, q0, q;
     memcpy(&r, &u, 4);
-    want = r / 15.0f;
+    want = r / y;
     q0 = r * c;
-    q = fmaf(fmaf(-q0, 15.0f, r), c, q0);
+    q = fmaf(fmaf(-q0, y, r), c, q0);
     if (memcmp(&q, &want, 4) != 0) ++bad;
   }
   printf("%llu\n", bad);
@@ -46,14 +49,22 @@ int main(void) {
 """
 
 
-def test_scale_division_by_15_exhaustive(tmp_path):
-    src = tmp_path / "div15.c"
-    exe = tmp_path / "div15"
-    src.write_text(DIV15_C)
+@pytest.fixture(scope="module")
+def div_exe(tmp_path_factory):
+    d = tmp_path_factory.mktemp("div")
+    src, exe = d / "div.c", d / "div"
+    src.write_text(DIV_C)
     subprocess.run(["gcc", "-O2", "-fopenmp", "-o", str(exe), str(src), "-lm"], check=True)
+    return exe
+
+
+# (divisor, the kernels' constant): the int4 group scale range / 15, and the
+# int8 page append's token scale amax / 127
+@pytest.mark.parametrize("y,c", [("15", "0x1.111112p-4"), ("127", "0x1.020408p-7")])
+def test_scale_division_exhaustive(div_exe, y, c):
     env = dict(os.environ, OMP_NUM_THREADS=str(min(8, os.cpu_count() or 1)))
-    out = subprocess.run([str(exe)], check=True, stdout=subprocess.PIPE, text=True, env=env,
-                         timeout=600).stdout
+    out = subprocess.run([str(div_exe), y, c], check=True, stdout=subprocess.PIPE, text=True,
+                         env=env, timeout=600).stdout
     assert out.strip() == "0", f"{out.strip()} inputs where the corrected product differs"
 
 
