@@ -688,6 +688,38 @@ def test_decode_kernel_timing_ring(rt):
     assert rt.decode_kernel_times(8) == []
 
 
+@pytest.mark.parametrize("quant", [S.KV_INT8, S.KV_INT4])
+def test_split_merge_handoff_repeated(rt, quant):
+    """The in-kernel split merge hands partials between workgroups on different XCDs
+    (agent-scope stores, a wait for their completion, then the ticket; the last
+    ticket's holder loads them). With 64-token splits this 4 x 8k batch makes up to 128
+    splits per (sequence, kv head), 3824 workgroups: 30 launches with the fixed tile order must
+    give the same bits every time (a partial read before its store landed would change
+    an output), and agree with the combine kernel's merge and the oracle within
+    tolerance."""
+    log(f"split merge handoff, 30 launches, split 64, quant {quant}")
+    c = Case(rt, 0x4A4D0FF + quant, 4, 32, 8, 128, [8191, 8191, 6000, 8191], 1, theta=5e5,
+             kv_dtype="bf16", quant=quant)
+    c.step_kv()
+    q = c.query("bf16")
+    prev_r = rt.set_decode_reproducible(1)
+    prev_s, prev_m = rt.set_decode_split(64), rt.set_decode_merge(1)
+    try:
+        outs = [c.gpu_decode(q, "bf16") for _ in range(30)]
+        rt.set_decode_merge(0)
+        comb = c.gpu_decode(q, "bf16")
+    finally:
+        rt.set_decode_reproducible(prev_r)
+        rt.set_decode_split(prev_s)
+        rt.set_decode_merge(prev_m)
+    wg, split = rt.last_decode_shape()
+    assert split == 64 and wg == sum((n + 1 + 63) // 64 for n in c.past_lens) * 8
+    for i, o in enumerate(outs[1:], 1):
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), f"launch {i} differs"
+    assert np.abs(outs[0] - comb).max() <= 1e-4
+    assert_close(outs[0], c.oracle_attend(q), "in-kernel merge of 128 splits")
+
+
 @pytest.mark.parametrize("merge", [1, 0])
 def test_decode_reproducible_tile_order(rt, merge):
     """With the fixed tile order (sai_set_decode_reproducible) repeated decode

@@ -569,3 +569,40 @@ def test_attend_reproducible_tile_order(rt):
         rt.set_decode_reproducible(prev_r)
         rt.set_tq_split(prev_s)
         c.close()
+
+
+def test_attend_split_merge_handoff_repeated(rt):
+    """The attention's in-kernel split merge (agent-scope partial stores, their
+    completion, the ticket, the last holder's loads) over many splits: with the
+    smallest split, 256 positions, three sequences make up to 8 splits each, and 30
+    calls with the fixed tile order give the same bits every time (a partial read
+    before its store landed would change an output)."""
+    import torch
+    log("tq attend: split merge handoff, 256-position splits, 30 calls")
+    rng = np.random.default_rng(0x7A12)
+    d, bits, qjl, group, heads = 128, 4, True, 4, 2
+    lens = [1900, 1500, 77]
+    batch, nh = len(lens), heads * group
+    c = S.TqCache(rt, 1, heads, d, bits, qjl, batch, 2048, seed=SEED)
+    prev_s = rt.set_tq_split(256)
+    prev_r = rt.set_decode_reproducible(1)
+    try:
+        k0 = rng.standard_normal((batch, max(lens), heads * d)).astype(np.float32)
+        v0 = rng.standard_normal((batch, max(lens), heads * d)).astype(np.float32)
+        c.write(0, to_dev(k0, False), to_dev(v0, False), batch, max(lens))
+        c.advance()
+        c.set_lengths(lens)
+        q = to_dev(rng.standard_normal((batch, 1, nh * d)).astype(np.float32), True)
+        outs = []
+        for _ in range(30):
+            out = torch.zeros((batch, 1, nh * d), device="cuda")
+            c.attend(0, q, out, batch, nh)
+            outs.append(out)
+        torch.cuda.synchronize()
+        for i, o in enumerate(outs[1:], 1):
+            assert torch.equal(o, outs[0]), f"call {i} differs"
+        assert torch.isfinite(outs[0]).all()
+    finally:
+        rt.set_decode_reproducible(prev_r)
+        rt.set_tq_split(prev_s)
+        c.close()
