@@ -479,7 +479,8 @@ __global__ __launch_bounds__(2 * D * HPW) void kv_append_page_int4_kernel(Append
   constexpr uint32_t ESZ = BF16 ? 2 : 4;
   constexpr int PB = D / 8 < 16 ? D / 8 : 16;  // bytes of a (scale, zero) piece
   constexpr int PPS = (D / 8) / PB;            // pieces per slot
-  const int sub = __builtin_amdgcn_readfirstlane((int)threadIdx.x / (2 * D));  // head of the workgroup
+  // the workgroup's head of this thread
+  const int sub = __builtin_amdgcn_readfirstlane((int)threadIdx.x / (2 * D));
   const int tid = (int)threadIdx.x % (2 * D), lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = (int)blockIdx.x * HPW + sub, b = blockIdx.z;
@@ -548,9 +549,11 @@ __global__ __launch_bounds__(2 * D * HPW) void kv_append_page_int4_kernel(Append
   const uint32_t ka = quant4_int4(xa, pka), kb = quant4_int4(xb, pkb);
   const uint32_t qa = quant4_int4(va, pva), qb = quant4_int4(vb, pvb);
 
+  // per head: K rows; V column d at 16 d, one byte per slot; K and V (scale,
+  // zero) per slot
   __shared__ __align__(16) uint8_t sm_k_all[HPW][kPageTokens * KS];
-  __shared__ __align__(16) uint8_t sm_v_all[HPW][kPageTokens * D];  // column d at 16 d, one byte per slot
-  __shared__ __align__(16) uint32_t sm_p_all[HPW][2][kPageTokens][NG];  // K, V (scale, zero) per slot
+  __shared__ __align__(16) uint8_t sm_v_all[HPW][kPageTokens * D];
+  __shared__ __align__(16) uint32_t sm_p_all[HPW][2][kPageTokens][NG];
   uint8_t* sm_k = sm_k_all[sub];
   uint8_t* sm_v = sm_v_all[sub];
   uint32_t(*sm_p)[kPageTokens][NG] = sm_p_all[sub];

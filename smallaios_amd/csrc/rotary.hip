@@ -159,7 +159,8 @@ __device__ __forceinline__ void store_vec(T* p, const float (&v)[N]) {
     if (nan) {
 #pragma unroll
       for (int j = 0; j < N / 2; ++j)
-        u.w[j] = (uint32_t)f32_to_bf16_bits(v[2 * j]) | ((uint32_t)f32_to_bf16_bits(v[2 * j + 1]) << 16);
+        u.w[j] = (uint32_t)f32_to_bf16_bits(v[2 * j]) |
+                 ((uint32_t)f32_to_bf16_bits(v[2 * j + 1]) << 16);
     }
     *reinterpret_cast<R*>(p) = u.r;
   } else if constexpr (VEC) {
