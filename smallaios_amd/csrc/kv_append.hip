@@ -347,27 +347,6 @@ __global__ __launch_bounds__(kPageThreads<D>) void kv_append_page_int8_kernel(Ap
 // leave in 16-byte stores: K rows of the new slots, V two dims' packed
 // columns per thread with the nibbles of slots outside the appended range
 // kept, and the (scale, zero) pairs of the new slots.
-// v_min_f32 / v_max_f32 whose first operand is read from another lane of the
-// row by DPP (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror).
-// Their operands are min / max results, never NaN and never signalling, so
-// the quieting step the compiler puts before fminf / fmaxf of a DPP move is
-// not needed. The s_nop covers the wait states between a VALU write of the
-// source (or of EXEC) and its DPP read.
-#define SAI_DPP_OP(name, op, ctrl)                                                   \
-  __device__ __forceinline__ float name(float a) {                                  \
-    float r;                                                                         \
-    asm("s_nop 4\n\t" op " %0, %1, %1 " ctrl " row_mask:0xf bank_mask:0xf"        \
-        : "=v"(r)                                                                    \
-        : "v"(a));                                                                   \
-    return r;                                                                        \
-  }
-SAI_DPP_OP(min_quad1032, "v_min_f32_dpp", "quad_perm:[1,0,3,2]")
-SAI_DPP_OP(max_quad1032, "v_max_f32_dpp", "quad_perm:[1,0,3,2]")
-SAI_DPP_OP(min_quad2301, "v_min_f32_dpp", "quad_perm:[2,3,0,1]")
-SAI_DPP_OP(max_quad2301, "v_max_f32_dpp", "quad_perm:[2,3,0,1]")
-SAI_DPP_OP(min_half_mirror, "v_min_f32_dpp", "row_half_mirror")
-SAI_DPP_OP(max_half_mirror, "v_max_f32_dpp", "row_half_mirror")
-#undef SAI_DPP_OP
 
 // min and max over the 8 aligned lanes of a group (quad swaps, then the other
 // quad of the half-row); exact and order-free

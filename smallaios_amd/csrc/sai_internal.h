@@ -127,6 +127,52 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// v_min_f32 / v_max_f32 whose first operand is read from another lane of the
+// row by DPP (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror). Their operands are values that are never signalling NaNs
+// (results of arithmetic, min or max), so the quieting step the compiler puts
+// before fminf / fmaxf of a DPP move is not needed. The s_nop covers the wait
+// states between a VALU write of the source (or of EXEC) and its DPP read.
+#define SAI_DPP_OP(name, op, ctrl)                                                   \
+  __device__ __forceinline__ float name(float a) {                                  \
+    float r;                                                                         \
+    asm("s_nop 4\n\t" op " %0, %1, %1 " ctrl " row_mask:0xf bank_mask:0xf"        \
+        : "=v"(r)                                                                    \
+        : "v"(a));                                                                   \
+    return r;                                                                        \
+  }
+SAI_DPP_OP(min_quad1032, "v_min_f32_dpp", "quad_perm:[1,0,3,2]")
+SAI_DPP_OP(max_quad1032, "v_max_f32_dpp", "quad_perm:[1,0,3,2]")
+SAI_DPP_OP(min_quad2301, "v_min_f32_dpp", "quad_perm:[2,3,0,1]")
+SAI_DPP_OP(max_quad2301, "v_max_f32_dpp", "quad_perm:[2,3,0,1]")
+SAI_DPP_OP(min_half_mirror, "v_min_f32_dpp", "row_half_mirror")
+SAI_DPP_OP(max_half_mirror, "v_max_f32_dpp", "row_half_mirror")
+SAI_DPP_OP(max_row_mirror, "v_max_f32_dpp", "row_mirror")
+#undef SAI_DPP_OP
+
+// The largest value of the wave, in every lane, for values that are never
+// signalling NaNs. The max is exact, so the order of the steps does not change
+// it: DPP within each row of 16 lanes (the quads, the halves, the row), then
+// the gfx950 row swaps (swap(x, x) leaves the lane's own value in one result
+// and its partner's in the other, so their max needs no select).
+__device__ __forceinline__ float max2_f32(float a, float b) {
+  float r;
+  asm("v_max_f32_e32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float wave_max_rows(float v) {
+  v = max_quad1032(v);
+  v = max_quad2301(v);
+  v = max_half_mirror(v);
+  v = max_row_mirror(v);
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+  v = max2_f32(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+  return max2_f32(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+}
+
 // ---- launch parameters --------------------------------------------------------
 
 struct AppendParams {

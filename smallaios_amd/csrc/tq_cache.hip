@@ -702,14 +702,16 @@ __device__ __forceinline__ int k_operand(const uint32_t (&kc)[KW], int s) {
 // f16 MFMA operand (4 positions of one dim) of V codes, as subnormals
 // code * 2^-24, for value step s. 4-bit: word s/2 gives positions
 // (0, 4, 1, 5) + 8 (s/2) for even s and (2, 6, 3, 7) + 8 (s/2) for odd s;
-// 3- and 8-bit: positions 4s .. 4s+3 in order.
-template <int BITS, int TBW>
+// with MIXED the odd positions' nibbles stay in place, code * 2^-20 (one mask
+// instead of a shift and a mask), and the caller takes the even positions'
+// weights 16x larger. 3- and 8-bit: positions 4s .. 4s+3 in order.
+template <int BITS, int TBW, bool MIXED = false>
 __device__ __forceinline__ half4_t v_operand(const uint32_t (&vc)[TBW], int s) {
   uint32_t lo, hi;
   if constexpr (BITS == 4) {
     const uint32_t w = vc[s >> 1] >> ((s & 1) * 8);
     lo = w & 0x000F000Fu;
-    hi = (w >> 4) & 0x000F000Fu;
+    hi = MIXED ? (w & 0x00F000F0u) : ((w >> 4) & 0x000F000Fu);
   } else if constexpr (BITS == 8) {
     lo = __builtin_amdgcn_perm(0u, vc[s], 0x0C010C00u);
     hi = __builtin_amdgcn_perm(0u, vc[s], 0x0C030C02u);
@@ -1033,7 +1035,7 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
     for (int g = 0; g < G; ++g) {
       alpha[g] = 1.0f;
       if (MODE == 0 && __ballot(lg[g] > m_run[g])) {
-        const float m_new = fmaxf(m_run[g], tq_wave_max(lg[g]));
+        const float m_new = fmaxf(m_run[g], wave_max_rows(lg[g]));
         alpha[g] = fast_exp2(m_run[g] - m_new);
         m_run[g] = m_new;
       }
@@ -1041,11 +1043,17 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
     // weights: P' = f16(p vs / S); the row's whole value (vs code + vz) and
     // the normaliser take the same rounded weight p' = P' S / vs, so the
     // f16 rounding perturbs each weight instead of splitting the row
-    const float vsmax = tq_wave_max(live ? vp.x : 0.0f);
+    const float vsmax = wave_max_rows(live ? vp.x : 0.0f);
+    // 4-bit codes of odd positions enter the values' MFMA at 2^-20 (v_operand's
+    // MIXED form), so the even positions' P' are taken 16x larger (exact; the
+    // softmax weights are <= 1, so P' <= 16). Not for the caller's weights
+    // (MODE 2), whose range binary16 would then shrink 16-fold.
+    constexpr bool kMixed = BITS == 4 && MODE != 2;
+    const float up = (kMixed && (lane & 1) == 0) ? 16.0f : 1.0f;
     // hardware reciprocals (1 ulp) instead of IEEE divisions: the two ratios
     // only need to be each other's inverse far below the f16 rounding of P'
-    const float vsn = vp.x * __builtin_amdgcn_rcpf(vsmax);
-    const float rvsn = vsmax * __builtin_amdgcn_rcpf(vp.x);
+    const float vsn = vp.x * __builtin_amdgcn_rcpf(vsmax) * up;
+    const float rvsn = vsmax * __builtin_amdgcn_rcpf(vp.x) * (1.0f / up);
     const int slot = p_slot<BITS>(lane);
 #pragma unroll
     for (int g = 0; g < NQ * 4; ++g) {
@@ -1078,13 +1086,14 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 2 : 1) void tq_attend_kernel(
       for (int u = 0; u < NQ; ++u) pa[u] = *(const half4_t*)&sp[wave][4 * u + (lane & 3)][4 * s];
 #pragma unroll
       for (int e = 0; e < DH; ++e) {
-        const half4_t vb = v_operand<BITS, TBW>(T.vc[e], s);
+        const half4_t vb = v_operand<BITS, TBW, kMixed>(T.vc[e], s);
 #pragma unroll
         for (int u = 0; u < NQ; ++u)
           mf[u][e] = __builtin_amdgcn_mfma_f32_4x4x4f16(pa[u], vb, mf[u][e], 0, 0, 0);
       }
     }
-    const float sc = vsmax * 16777216.0f;  // 2^24: the codes' subnormal scale
+    // the codes' subnormal scale: 2^24, or 2^20 with the even positions' P' x 16
+    const float sc = vsmax * (kMixed ? 1048576.0f : 16777216.0f);
 #pragma unroll
     for (int u = 0; u < NQ; ++u)
 #pragma unroll
