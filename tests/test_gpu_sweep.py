@@ -12,7 +12,8 @@ names still meet the bar: outputs within 2e-3 abs + 1e-2 rel of the oracle
 bit-exact where a case checks them. The TurboQuant cases draw head_dim, bits,
 QJL, group, lengths, bf16 inputs, the split, the tile order, the scale and the
 fused or separate store, against the oracle's encode and attention at the same
-bar. Each case prints its draw before it runs.
+bar; the append cases, three appends of random sizes after a random past, keep
+every code and scale bit-exact. Each case prints its draw before it runs.
 """
 import numpy as np
 import pytest
@@ -212,3 +213,35 @@ def test_turboquant_attend_sweep(rt, i):
         c.close()
         rt.set_tq_split(prev_split)
         rt.set_decode_reproducible(prev_rep)
+
+
+def _draw_append(i):
+    rng = np.random.default_rng(0xA99E0000 + i)
+    batch = int(rng.integers(1, 5))
+    quant, d, hkv, _ = _shape(rng, 1)
+    return dict(
+        seed=0xA99E0000 + i, quant=quant, d=d, hkv=hkv,
+        past=[int(x) for x in rng.integers(0, _pick(rng, [1, 20, 300]), batch)],
+        steps=[int(_pick(rng, [1, 2, 3, 4, 7, 16, 17, 40, 100])) for _ in range(3)],
+        kv_dtype=_pick(rng, ["f32", "bf16"]), rotary=bool(rng.random() < 0.8),
+        interleaved=bool(rng.random() < 0.3), permute=bool(rng.random() < 0.5),
+        theta=_pick(rng, [1e4, 5e5]))
+
+
+@pytest.mark.parametrize("i", range(48))
+def test_append_sweep(rt, i):
+    """Three appends of random sizes (the row kernel below 4 tokens, the page
+    kernel from 4, partial first and last pages) after a random committed
+    past; every stored code and scale bit-exact against the oracle."""
+    cfg = _draw_append(i)
+    log(f"append sweep {i}: {cfg}")
+    total = sum(cfg["steps"])
+    c = Case(rt, cfg["seed"], len(cfg["past"]), cfg["hkv"], cfg["hkv"], cfg["d"], cfg["past"],
+             0, theta=cfg["theta"], quant=cfg["quant"], kv_dtype=cfg["kv_dtype"],
+             permute_pages=cfg["permute"], do_rotary=cfg["rotary"],
+             interleaved=cfg["interleaved"], extra_tokens=total)
+    for n in cfg["steps"]:
+        k, v = c.kv(n)
+        c.append_both(k, v)
+        c.cache.advance()
+    c.check_codes()
