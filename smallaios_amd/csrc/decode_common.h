@@ -164,6 +164,23 @@ __device__ __forceinline__ void merge_partials(const float* ph, size_t stride, i
   }
 }
 
+// merge_partials with the batch width picked from the split count: all of a
+// (head, dim) entry's splits in one round trip up to 32 splits (each round
+// trip to partials written on other XCDs costs a full memory latency).
+__device__ __forceinline__ void merge_all_splits(const float* ph, size_t stride, int d,
+                                                 int nsplit, float& M, float& Ls, float& O) {
+  if (nsplit <= 2)
+    merge_partials<2>(ph, stride, d, nsplit, -1, M, Ls, O);
+  else if (nsplit <= 4)
+    merge_partials<4>(ph, stride, d, nsplit, -1, M, Ls, O);
+  else if (nsplit <= 8)
+    merge_partials<8>(ph, stride, d, nsplit, -1, M, Ls, O);
+  else if (nsplit <= 16)
+    merge_partials<16>(ph, stride, d, nsplit, -1, M, Ls, O);
+  else
+    merge_partials<32>(ph, stride, d, nsplit, -1, M, Ls, O);
+}
+
 // 16 consecutive elements (f32 or bf16) starting at element `off`; the
 // offset is a multiple of 16 and the row 32-byte aligned.
 __device__ __forceinline__ void load16(const void* base, size_t off, int dtype, float (&x)[16]) {

@@ -725,12 +725,7 @@ __global__ __launch_bounds__(64 * NW, (kInt8OneWavePerSimd<D, G>) ? 1 : 2) void 
     const int hd = t / D, d = t % D;
     float M = -INFINITY, Ls = 0.0f, O = 0.0f;
     const float* ph = p0 + hd * (D + 2);
-    if (nsplit <= 2)
-      merge_partials<2>(ph, stride, d, nsplit, -1, M, Ls, O);
-    else if (nsplit <= 4)
-      merge_partials<4>(ph, stride, d, nsplit, -1, M, Ls, O);
-    else
-      merge_partials<8>(ph, stride, d, nsplit, -1, M, Ls, O);
+    merge_all_splits(ph, stride, d, nsplit, M, Ls, O);
     const int dl = logical_dim<D>(d);
     if (dl >= 0)
       store_out(p.out, ((size_t)b * Hq + kvh * G + hd) * DL + dl, Ls > 0.0f ? O / Ls : 0.0f,

@@ -847,11 +847,14 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
     if (max_len > 2 * mean_len) s = std::min<int64_t>(s, 3072);
     s = ((s + 63) / 64) * 64;
     split = (int32_t)std::max<int64_t>(256, std::min<int64_t>(s, kMaxDecodeSplit));
-    // a batch whose sequences all fit one 512-token split takes one split each
-    // (no merge, no short remainder split): 1 x 512 tokens (8Q/2KV, head_dim
-    // 64) 7.83 -> 7.68 us per step, 16 x 300 (32Q/8KV, 128) 11.66 -> 10.95 us;
-    // longer sequences keep 256 (4 x 1000: 11.5 against 12.9 us at 512)
-    if (split < 512 && max_len <= 512) split = 512;
+    // At the 256-token floor each wave streams one tile. A batch whose
+    // sequences all fit one 512-token split takes one split each (no merge, no
+    // short remainder split): 1 x 512 tokens (8Q/2KV, head_dim 64) 7.83 ->
+    // 7.68 us per step, 16 x 300 (32Q/8KV, 128) 11.66 -> 10.95 us. Sequences
+    // cut into more than 8 such splits take 512 too: 1 x 8192 (32Q/8KV)
+    // 18.5 -> 14.7 us, 2 x 3000 13.8 -> 13.3, 1 x 16384 (8Q/1KV) 38.8 ->
+    // 29.9. Between the two, 256 stays (4 x 1000: 11.5 against 12.9 us).
+    if (split < 512 && (max_len <= 512 || (max_len + 255) / 256 > 8)) split = 512;
   }
   split = std::min(split, kMaxDecodeSplit);
   int64_t work = 0;
