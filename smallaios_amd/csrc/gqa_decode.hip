@@ -216,7 +216,9 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, 
   const int lane = threadIdx.x & 63;
   sm_sc[lane] = T.sk;
   sm_sc[64 + lane] = T.sv;
-  after_qk();
+  // with two passes (group 8) the second pass's QK below still reads this
+  // tile's K codes, so the hook waits for it
+  if constexpr (NP == 1) after_qk();
   __builtin_amdgcn_wave_barrier();  // LDS ops of a wave run in order; keep the compiler from hoisting
   float skv[16], svv[16];
 #pragma unroll
@@ -240,7 +242,10 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D>& T, WaveState<D, 
 #pragma unroll
   for (int ps = 0; ps < NP; ++ps) {
     const bool live = 4 * ps + (r >> 2) < G;
-    if (ps > 0) qk(ps);
+    if (ps > 0) {
+      qk(ps);
+      if (ps == NP - 1) after_qk();
+    }
     float s[16];
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)

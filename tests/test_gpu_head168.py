@@ -127,6 +127,27 @@ def test_decode_d168_windows_interleaved(rt):
                  c.oracle_attend(q, layer_window=4096, mask_window=300), "d=168 both windows")
 
 
+@pytest.mark.parametrize("split,merge", [(512, 0), (1024, 1), (2048, 1)])
+def test_decode_d168_group8_long_splits(rt, split, merge):
+    """Group 8 (two passes of four heads) with two or more tiles per wave: the
+    single tile buffer is refilled with the next tile only after the second
+    pass's QK has read the current one's K codes."""
+    log(f"decode d=168 group 8 split={split} merge={merge}")
+    c = Case(rt, 0x1690 + split, 3, 64, 8, D, [3000, 700, 65], 1, theta=THETA,
+             permute_pages=True, k_transform=outlier_keys(D, (7, 63, 90, 150)))
+    prev_s, prev_m = rt.set_decode_split(split), rt.set_decode_merge(merge)
+    try:
+        c.step_kv()
+        q = c.query("bf16")
+        got = c.gpu_decode(q, "bf16")
+        ref = c.oracle_attend(q)
+        log(f"  worst err/tol {err_tol_ratio(got, ref):.4f}")
+        assert_close(got, ref, f"d=168 group 8 split {split}")
+    finally:
+        rt.set_decode_split(prev_s)
+        rt.set_decode_merge(prev_m)
+
+
 @pytest.mark.parametrize("hq", [32, 64])
 def test_decode_d168_outlier_keys(rt, hq):
     """Student-t keys with x20 outlier channels, fused step."""

@@ -98,7 +98,10 @@ def test_decode_d256_group8(rt, quant):
         return
     q = c.query("bf16")
     ref = c.oracle_attend(q)
-    for split, merge in ((0, 2), (256, 0), (256, 1)):
+    # 512 and 1024: two or more tiles per wave, so the single tile buffer is
+    # refilled with the next tile while the second pass of heads still needs
+    # the current one's K codes
+    for split, merge in ((0, 2), (256, 0), (256, 1), (512, 1), (1024, 0), (1024, 1)):
         prev_s, prev_m = rt.set_decode_split(split), rt.set_decode_merge(merge)
         try:
             got = c.gpu_decode(q, "bf16")
