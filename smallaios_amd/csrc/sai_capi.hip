@@ -854,11 +854,12 @@ sai_status launch_decode(sai_ctx* ctx, sai_kvcache* c, int32_t layer, const void
     // cut into more than 8 such splits take 512 too: 1 x 8192 (32Q/8KV)
     // 18.5 -> 14.7 us, 2 x 3000 13.8 -> 13.3, 1 x 16384 (8Q/1KV) 38.8 ->
     // 29.9. Between the two, 256 stays (4 x 1000: 11.5 against 12.9 us).
-    // int8 only: the int4 kernel's 8-wave workgroups measured the other way
-    // at 16 x 300 (11.0 us at 256 against 11.3) and 2 x 3000 (12.5 against
-    // 13.2), and gained less at 1 x 8192 (14.5 against 13.7).
-    if (c->desc.quant == SAI_KV_INT8 && split < 512 &&
-        (max_len <= 512 || (max_len + 255) / 256 > 8))
+    // The int4 kernel's 8-wave workgroups measured the other way at 16 x 300
+    // (11.0 us at 256 against 11.3) and 2 x 3000 (12.5 against 13.2, twelve
+    // splits), so int4 takes 512 only past 16 splits (1 x 8192: 14.5 -> 13.7).
+    const int64_t splits256 = (max_len + 255) / 256;
+    if (split < 512 && (c->desc.quant == SAI_KV_INT8 ? (max_len <= 512 || splits256 > 8)
+                                                     : splits256 > 16))
       split = 512;
   }
   split = std::min(split, kMaxDecodeSplit);
