@@ -63,7 +63,7 @@ def _draw_decode(i):
         out_dtype=_pick(rng, ["f32", "f32", "bf16"]),
         rotary=bool(rng.random() < 0.8), interleaved=bool(rng.random() < 0.3),
         permute=bool(rng.random() < 0.5), fused=bool(rng.random() < 0.5),
-        split=_pick(rng, [0, 0, 64, 192, 1024]), merge=_pick(rng, [0, 1, 2]),
+        split=_pick(rng, [0, 0, 64, 192, 512, 1024, 2048]), merge=_pick(rng, [0, 1, 2]),
         reproducible=_pick(rng, [0, 1, 2]),
         window=_pick(rng, [0, 0, 0, 1, 37, 500]),
         layer_window=_pick(rng, [0, 0, 0, 64, 300]),
