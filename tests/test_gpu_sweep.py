@@ -245,3 +245,55 @@ def test_append_sweep(rt, i):
         c.append_both(k, v)
         c.cache.advance()
     c.check_codes()
+
+
+def _draw_wide(i):
+    """int8 at head_dim 168 and 256: the decode's single phased tile buffer,
+    with several tiles per wave (long sequences, large splits)."""
+    rng = np.random.default_rng(0x5A560000 + i)
+    batch = int(rng.integers(1, 4))
+    d = _pick(rng, [168, 256])
+    g = _pick(rng, [1, 2, 4, 8])
+    return dict(
+        seed=0x5A560000 + i, quant=S.KV_INT8, d=d, hkv=_pick(rng, [1, 2]), g=g,
+        lens=[int(x) for x in rng.integers(0, 6000, batch)],
+        kv_dtype=_pick(rng, ["f32", "bf16"]), q_dtype=_pick(rng, ["f32", "bf16"]),
+        out_dtype=_pick(rng, ["f32", "bf16"]), rotary=bool(rng.random() < 0.8),
+        interleaved=bool(rng.random() < 0.3), permute=bool(rng.random() < 0.5),
+        fused=bool(rng.random() < 0.5), split=_pick(rng, [0, 512, 1024, 2048, 4096]),
+        merge=_pick(rng, [0, 1, 2]), reproducible=_pick(rng, [0, 1, 2]),
+        window=_pick(rng, [0, 0, 700]), layer_window=_pick(rng, [0, 0, 1024]),
+        theta=1e6)
+
+
+@pytest.mark.parametrize("i", range(32))
+def test_decode_wide_heads_sweep(rt, i):
+    cfg = _draw_wide(i)
+    cfg = dict(cfg, hq=cfg["hkv"] * cfg["g"])
+    log(f"wide-head decode sweep {i}: {cfg}")
+    prev_split = rt.set_decode_split(cfg["split"])
+    prev_merge = rt.set_decode_merge(cfg["merge"])
+    prev_rep = rt.set_decode_reproducible(cfg["reproducible"])
+    try:
+        fused = cfg["fused"]
+        c = Case(rt, cfg["seed"], len(cfg["lens"]), cfg["hq"], cfg["hkv"], cfg["d"], cfg["lens"],
+                 0 if fused else 1, theta=cfg["theta"], quant=cfg["quant"],
+                 kv_dtype=cfg["kv_dtype"], permute_pages=cfg["permute"],
+                 do_rotary=cfg["rotary"], interleaved=cfg["interleaved"],
+                 extra_tokens=1 if fused else 0)
+        c.cache.set_layer_window(0, cfg["layer_window"])
+        q = c.rng.standard_normal((c.batch, 1, c.hq * c.d), dtype=np.float32)
+        if cfg["q_dtype"] == "bf16":
+            q = to_bf16_f32(q)
+        if fused:
+            got = c.step_fused(q, cfg["q_dtype"], window=cfg["window"], out_dtype=cfg["out_dtype"])
+        else:
+            c.step_kv()
+            got = c.gpu_decode(q, cfg["q_dtype"], window=cfg["window"],
+                               out_dtype=cfg["out_dtype"])
+        ref = c.oracle_attend(q, layer_window=cfg["layer_window"], mask_window=cfg["window"])
+        _check(got, ref, cfg["out_dtype"], f"wide-head decode sweep {i}")
+    finally:
+        rt.set_decode_split(prev_split)
+        rt.set_decode_merge(prev_merge)
+        rt.set_decode_reproducible(prev_rep)
