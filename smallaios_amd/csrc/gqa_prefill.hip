@@ -447,7 +447,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
     if (tid == 0) *prec_flag = 0;
   }
   const int n_qt = (p.sq + QT - 1) / QT;
-  const int qtile = n_qt - 1 - (int)blockIdx.x;  // longest rows first
+  const int nks = p.nksplit > 1 ? p.nksplit : 1;
+  const int ksp = (int)blockIdx.x % nks;               // key split
+  const int qtile = n_qt - 1 - (int)blockIdx.x / nks;  // longest rows first
   const int q0 = qtile * QT;
   const int past = p.seq_lens[b];
   const int total = past + p.sq;
@@ -465,6 +467,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   const int W = p.window;
   const int tile_lo = W > 0 ? max(0, past + q0 - W + 1) / 64 : 0;
   const int lo_full = W > 0 ? (max(0, max_pos - W + 1) + 63) / 64 : 0;
+  // this workgroup's tiles [t_first, t_last): the rows' whole range, or its
+  // key split's share of it
+  const int t_first = nks > 1 ? tile_lo + ksp * p.ksplit_tiles : tile_lo;
+  const int t_last = nks > 1 ? min(n_tiles, t_first + p.ksplit_tiles) : n_tiles;
+  // partial of row R (position il, head R % G) of this key split
+  auto partial_of = [&](int il, int hd) {
+    return p.partials +
+           ((((size_t)b * p.sq + il) * nks + ksp) * p.kv_heads + kvh) * (size_t)(G * (D + 2)) +
+           (size_t)hd * (D + 2);
+  };
+  if (nks > 1 && t_first >= t_last) {
+    // a split past the rows' range: empty partials (m = -inf, l = o = 0), which
+    // the merge skips
+    if constexpr (!PREC) {
+      for (int e = tid; e < 16 * RB * NW * (D + 2); e += NT) {
+        const int R = e / (D + 2), k = e % (D + 2);
+        const int il = q0 + R / G;
+        if (il < p.sq) partial_of(il, R % G)[k] = k == 0 ? -INFINITY : 0.0f;
+      }
+    }
+    return;
+  }
 
   // first tile in flight while Q is prepared
   typedef typename std::conditional<INT4, TileStage4<D, NT>, TileStage<D, NT>>::type Stage;
@@ -482,10 +506,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
     else
       stage_store<D, NT>(S, T, t0, total, tid);
   };
-  auto slot = [&](int tile) -> Tile& { return sT[(tile - tile_lo) & (NSLOT - 1)]; };
-  pages.load(pt, tile_lo, last_page, tid);
-  load_stage(tile_lo * 64);
-  pages.load(pt, tile_lo + 1, last_page, tid);
+  auto slot = [&](int tile) -> Tile& { return sT[(tile - t_first) & (NSLOT - 1)]; };
+  pages.load(pt, t_first, last_page, tid);
+  load_stage(t_first * 64);
+  pages.load(pt, t_first + 1, last_page, tid);
 
   // ---- Q^T operand: rows R = wave*32 + rb*16 + r -> (position, head) -------
   // RoPE(q) * scale * log2(e) as an f16 pair hi + lo (~22 bits: a score's
@@ -548,11 +572,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       }
   }
 
-  store_stage(slot(tile_lo), tile_lo * 64);
-  if (PER_BARRIER == 2 && tile_lo + 1 < n_tiles) {
-    load_stage((tile_lo + 1) * 64);
-    pages.load(pt, tile_lo + 2, last_page, tid);
-    store_stage(slot(tile_lo + 1), (tile_lo + 1) * 64);
+  store_stage(slot(t_first), t_first * 64);
+  if (PER_BARRIER == 2 && t_first + 1 < t_last) {
+    load_stage((t_first + 1) * 64);
+    pages.load(pt, t_first + 2, last_page, tid);
+    store_stage(slot(t_first + 1), (t_first + 1) * 64);
   }
   __syncthreads();
 
@@ -859,16 +883,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
   };
   // the loops end early (their bound drops to the current tile) when the fast
   // pass gives up: one loop exit, as without the check
-  int t_stop = n_tiles;
+  int t_stop = t_last;
   if constexpr (NSLOT == 1) {
     // one slot: the next tile's loads are in flight while this one is
     // computed, and it is stored once every wave has finished reading
-    for (int tile = tile_lo; tile < t_stop; ++tile) {
+    for (int tile = t_first; tile < t_stop; ++tile) {
       if (big(sT[0])) {  // every wave sees the same tile
         t_stop = tile;
         break;
       }
-      const bool more = tile + 1 < n_tiles;
+      const bool more = tile + 1 < t_last;
       if (more) {
         load_stage((tile + 1) * 64);
         pages.load(pt, tile + 2, last_page, tid);
@@ -881,10 +905,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       }
     }
   } else {
-    for (int tile = tile_lo; tile < t_stop; tile += PER_BARRIER) {
+    for (int tile = t_first; tile < t_stop; tile += PER_BARRIER) {
       // the tiles of this round are in LDS (the barrier below orders them)
       bool any_big = big(slot(tile));
-      if (PER_BARRIER == 2 && tile + 1 < n_tiles) any_big = any_big || big(slot(tile + 1));
+      if (PER_BARRIER == 2 && tile + 1 < t_last) any_big = any_big || big(slot(tile + 1));
       if (any_big) {
         t_stop = tile;
         break;
@@ -893,9 +917,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
 #pragma nounroll
       for (int h = 0; h < PER_BARRIER; ++h) {
         const int tt = tile + h;
-        if (tt < n_tiles) {
+        if (tt < t_last) {
           const int nxt = tt + PER_BARRIER;
-          const bool more = nxt < n_tiles;
+          const bool more = nxt < t_last;
           if (more) {
             load_stage(nxt * 64);
             pages.load(pt, nxt + 1, last_page, tid);  // consumed by the next stage
@@ -908,7 +932,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
     }
   }
 
-  if (!PREC && t_stop < n_tiles) {
+  if (!PREC && t_stop < t_last) {
     if (tid == 0) *prec_flag = 1;
     return;
   }
@@ -925,6 +949,22 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gqa_prefill_kernel(PrefillPar
       if (il >= p.sq) continue;
       const int hq = kvh * G + R % G;
       const size_t o = (((size_t)b * p.sq + il) * Hq + hq) * DL;
+      if (nks > 1) {
+        // the key split's partial in true units: weights p * 2^m_run summing
+        // to l * 2^m_run, acc * 2^(vexp_run - kPrecLift) in the precise pass;
+        // every stored dim (padding dims hold 0); m = -inf where no key was
+        // visible
+        const float m = __shfl(m_run[rb], row, 64);
+        const float u = __builtin_ldexpf(1.0f, PREC ? vexp_run - kPrecLift : 0);
+        float* part = partial_of(il, R % G);
+        if (r == 0) {
+          part[0] = l > 0.0f ? m : -INFINITY;
+          part[1] = l;
+        }
+#pragma unroll
+        for (int jb = 0; jb < JB; ++jb) part[2 + 16 * jb + r] = acc[rb][jb][e] * u;
+        continue;
+      }
       // acc is in units of 2^(vexp_run - kPrecLift) in the precise pass (exact)
       const float f =
           l > 0.0f ? __builtin_ldexpf(1.0f / l, PREC ? vexp_run - kPrecLift : 0) : 0.0f;
@@ -942,7 +982,8 @@ template <int D, int NW>
 dim3 prefill_grid(const PrefillParams& p, int group) {
   constexpr int RB = D > 128 ? 1 : 2;  // as in the kernel
   const int qt = 16 * RB * NW / group;
-  return dim3((p.sq + qt - 1) / qt, p.kv_heads, p.batch);
+  const int nks = p.nksplit > 1 ? p.nksplit : 1;
+  return dim3((p.sq + qt - 1) / qt * nks, p.kv_heads, p.batch);
 }
 
 template <int D, int NW, int Q, bool PREC>

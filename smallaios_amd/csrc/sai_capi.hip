@@ -1119,11 +1119,46 @@ SAI_API sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* c, int32_t layer, 
   const float sc = has_scale ? scale : sai_default_scale(D);
   p.scale_log2 = sc * 1.4426950408889634f;
   p.window = visible_span(c->layer_window[layer], window);
+  // Key split: a short chunk over a long past has few workgroups (one per
+  // 256 rows and kv head), each streaming the whole visible past. With fewer
+  // than 128 of them and at least 16 tiles to stream, the rows' key range is
+  // cut into splits of at least 4 tiles, to about 256 workgroups, and the
+  // decode's combine kernel merges the partials (each row of the chunk a
+  // sequence of its own).
+  int64_t max_past = 0;
+  for (int b = 0; b < batch; ++b) max_past = std::max<int64_t>(max_past, c->h_seq_lens[b]);
+  const int64_t key_tiles = (max_past + sq + 63) / 64;
+  const int64_t base_wgs = (int64_t)sai::prefill_workgroups(p, D, G);
+  int nks = 1;
+  if (base_wgs < 128 && key_tiles >= 16)
+    nks = (int)std::min<int64_t>((256 + base_wgs - 1) / base_wgs, key_tiles / 4);
+  if (nks > 1) {
+    p.nksplit = nks;
+    p.ksplit_tiles = (int)((key_tiles + nks - 1) / nks);
+    const size_t rows = (size_t)batch * sq;
+    const size_t need =
+        rows * nks * c->desc.num_kv_heads * G * (size_t)(sai::stored_head_dim(D) + 2);
+    st = reserve_workspace(ctx, c->ws, need, 0, 0);
+    if (st != SAI_OK) return st;
+    p.partials = c->ws.partials;
+  }
   st = reserve_prec_flags(ctx, c->ws, sai::prefill_workgroups(p, D, G));
   if (st != SAI_OK) return st;
   p.prec_flags = c->ws.prec_flags;
   hipError_t e = sai::launch_gqa_prefill(p, D, G, c->desc.quant, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gqa_prefill launch");
+  if (nks > 1) {
+    sai::DecodeParams m{};
+    m.out = out;
+    m.out_bf16 = p.out_bf16;
+    m.kv_heads = c->desc.num_kv_heads;
+    m.batch = batch * sq;
+    m.uniform_nsplit = nks;
+    m.max_nsplit = nks;
+    m.partials = c->ws.partials;
+    e = sai::launch_decode_combine(m, D, G, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "gqa_prefill key-split merge");
+  }
   return SAI_OK;
 }
 

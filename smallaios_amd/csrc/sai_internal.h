@@ -254,6 +254,12 @@ struct PrefillParams {
   // one int per workgroup (prefill_workgroups), zero between launches: the
   // int8 fast pass flags the workgroups the precise pass recomputes
   int32_t* prec_flags;
+  // key split (nksplit > 1): each workgroup takes ksplit_tiles 64-token tiles
+  // of its rows' visible range and writes (m, l, o) partials in the decode's
+  // layout (row (b, i) as sequence b * sq + i, nksplit splits each), which the
+  // decode's combine kernel merges
+  int nksplit, ksplit_tiles;
+  float* partials;
 };
 
 // Sliding windows: a query at position L-1 sees keys [L - W, L-1] (W > 0)
