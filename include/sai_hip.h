@@ -246,7 +246,10 @@ sai_status sai_gqa_with_cache_noalloc(sai_ctx* ctx, sai_kvcache* cache, int32_t 
  * q: device [batch, sq, num_heads*D]; out: device [batch, sq, num_heads*D] of
  * out_dtype (F32 or BF16, as for sai_gqa_decode).
  * window and sliding-window layers as for sai_gqa_decode, applied to every
- * query row at its own position (gpu_gqa's mask, attention.rs:79, :111). */
+ * query row at its own position (gpu_gqa's mask, attention.rs:79, :111).
+ * A short chunk over a long past is split over the key range: partials in the
+ * cache's decode workspace, merged by a second kernel on the same stream (the
+ * workspace grows once, synchronously, when a shape needs more). */
 sai_status sai_gqa_prefill(sai_ctx* ctx, sai_kvcache* cache, int32_t layer, const void* q,
                            int32_t dtype, int32_t batch, int32_t sq, int32_t num_heads,
                            const float* cos_cache, const float* sin_cache, int32_t cache_rows,
