@@ -73,7 +73,7 @@ def _draw_decode(i):
 def _draw_prefill(i):
     rng = np.random.default_rng(0x9EF10000 + i)
     batch = int(rng.integers(1, 4))
-    past = [int(x) for x in rng.integers(0, _pick(rng, [1, 200, 1500]), batch)]
+    past = [int(x) for x in rng.integers(0, _pick(rng, [1, 200, 1500, 6000]), batch)]
     new = int(_pick(rng, [1, 5, 64, 130, 300]))
     quant, d, hkv, hq = _shape(rng, batch * (max(past) + new) * 4)
     return dict(
@@ -128,7 +128,7 @@ def test_decode_sweep(rt, i):
         rt.set_decode_reproducible(prev_rep)
 
 
-@pytest.mark.parametrize("i", range(48))
+@pytest.mark.parametrize("i", range(96))
 def test_prefill_sweep(rt, i):
     cfg = _draw_prefill(i)
     log(f"prefill sweep {i}: {cfg}")
