@@ -18,8 +18,9 @@
  * (onnx-rt/src/session.rs:377); callers do the same.
  *
  * Streams: each cache (sai_kvcache, sai_tqcache) owns the device scratch its
- * attention launches use, sized when it is created, so different caches may
- * run on different streams at once. The launches on one cache must be
+ * attention launches use, sized when it is created (a launch that needs more,
+ * such as a prefill chunk's key split, grows it once, synchronously), so
+ * different caches may run on different streams at once. The launches on one cache must be
  * ordered by the caller (one stream, or events between streams), as the
  * cache's contents already require. Calls documented as synchronous wait for
  * all work on the device first.
