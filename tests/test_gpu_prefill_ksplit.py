@@ -1,5 +1,5 @@
 """Prefill of short chunks over long pasts, where the host cuts the rows' key
-range into splits (fewer than 128 workgroups, at least 16 tiles to stream):
+range into splits (fewer than 256 workgroups, at least 16 tiles to stream):
 each workgroup streams its split's tiles and writes (m, l, o) partials, and the
 decode's combine kernel merges them, every row of the chunk as a sequence of
 its own. Against the oracle at the prefill bar (2e-3 abs + 1e-2 rel; bf16
