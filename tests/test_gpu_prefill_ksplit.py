@@ -5,8 +5,9 @@ decode's combine kernel merges them, every row of the chunk as a sequence of
 its own. Against the oracle at the prefill bar (2e-3 abs + 1e-2 rel; bf16
 outputs with bf16's rounding on top; large V against the weighted bound of
 the precise pass), for int8 and int4, head_dim 64/128/168/256, groups 1-8,
-windows, ragged pasts (rows whose visible range ends before a split starts
-write empty partials), and a chunk large enough to keep the plain grid.
+windows, and ragged pasts (rows whose visible range ends before a split
+starts write empty partials). Chunks large enough for the plain grid are the
+other prefill tests' (the c5 chunk among them).
 """
 import numpy as np
 import pytest
@@ -81,10 +82,8 @@ def test_prefill_key_split_large_v(rt, quant, vscale):
 
 def test_prefill_key_split_repeated_and_reused(rt):
     """The same short chunk twice (the precise pass's flags and the partials
-    are reused), then a chunk large enough for the plain grid over the same
-    cache: results equal the oracle each time and the repeated one is
-    bit-identical."""
-    log("prefill key split: repeated, then a plain-grid chunk")
+    are reused): bit-identical results, equal to the oracle's."""
+    log("prefill key split: repeated")
     c = Case(rt, 0x4B7, 2, 32, 8, 128, [6000, 2000], 12, theta=5e5, permute_pages=True)
     c.step_kv()
     q = c.query("f32")
